@@ -1,0 +1,264 @@
+/*
+ * mgauss.h -- C ABI of the gfx950 splatting library (libmgauss.so).
+ *
+ * Every entry point takes raw device pointers, element counts, scalars and a
+ * HIP stream, launches its kernels on that stream, and returns an MG_* status
+ * code. Nothing here allocates device memory: callers pass every output and
+ * every scratch buffer. On failure, mg_last_error() returns a message that
+ * names the entry point and the offending argument (thread-local, valid until
+ * the next failing call on the same thread).
+ *
+ * Each declaration cites the interface of nandometzger/metal-gauss it
+ * replaces, as file:line under that repository. The reference binds these
+ * through a pybind11 module (metal_gauss/csrc/rasterize.mm:518-533); this
+ * library is bound through ctypes by metal-gauss_amd/_lib.py.
+ *
+ * Layout conventions (all fp32 unless stated, all row-major, contiguous):
+ *   means (N,3)  quats (N,4) wxyz  scales (N,3) linear  opacities (N,) in [0,1]
+ *   sh: fused (N,16,3), or split DC (N,1,3) + rest (N,15,3)
+ *   uv (N,2)  conic (N,3) = (c,-b,a)/det of the dilated 2D covariance
+ *   depth (N,)  rxy (N,2)  valid (N,) int32  color (N,3)
+ *   images: rgb (H,W,3), alpha/T (H,W), stop index (H,W) int32
+ */
+#ifndef MGAUSS_H
+#define MGAUSS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* A hipStream_t. NULL selects the null stream. */
+typedef void *mg_stream_t;
+
+enum {
+    MG_OK = 0,
+    MG_ERR_ARG = 1,      /* bad argument: shape, size, pointer, tile */
+    MG_ERR_LAUNCH = 2,   /* a kernel launch failed (hipGetLastError) */
+    MG_ERR_RUNTIME = 3,  /* another HIP runtime call failed */
+    MG_ERR_CAPACITY = 4  /* a caller buffer is smaller than the work needs */
+};
+
+/* ---------------------------------------------------------------- runtime */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *mg_last_error(void);
+
+/* Library version, major*10000 + minor*100 + patch. */
+int32_t mg_version(void);
+
+/* Replaces init(src) (metal_gauss/csrc/rasterize.mm:196, 19-41). The reference
+ * compiles Metal source at run time; here the gfx950 code objects are built
+ * ahead of time, so init only checks that a HIP device is present and that
+ * the code object loads on it. Idempotent. */
+int32_t mg_init(void);
+
+/* Largest tile edge the rasteriser accepts (one workgroup per tile, one
+ * thread per pixel): 32, i.e. 1024 threads. The reference's equivalent check
+ * is rasterize.mm:66-73. */
+int32_t mg_max_tile(void);
+
+/* Kernel timing with HIP events on each launch's own stream, for the bench
+ * harness. No counterpart in the reference (it times phases from Python,
+ * bench/step_profile.py:39-41). While enabled every launch records a pair of
+ * events; mg_timing_query synchronises them and reports the summed duration
+ * and launch count of one kernel by name since the last reset. */
+int32_t mg_timing_enable(int32_t on);
+int32_t mg_timing_reset(void);
+int32_t mg_timing_query(const char *kernel, double *total_ms, int64_t *count);
+
+/* ------------------------------------------------------------- preprocess */
+
+/* Fused projection + EWA covariance + SnugBox extents + validity + SH colour.
+ * Replaces preprocess_forward (metal_gauss/csrc/rasterize.mm:244-284; kernel
+ * preprocess.metal:114-221). viewmat (16 floats, row-major world->camera) and
+ * cam_center (3 floats) are HOST pointers, read at call time, as the reference
+ * reads them on the host (rasterize.mm:226-242). sh_fused != 0 means `sh` is
+ * (N,16,3) and `sh_rest` is ignored; otherwise sh is (N,1,3) and sh_rest is
+ * (N,15,3). sh_degree in 0..3. */
+int32_t mg_preprocess_forward(
+    int64_t N, const float *means, const float *quats, const float *scales,
+    const float *sh, const float *sh_rest, int32_t sh_fused,
+    const float *opacities, const float *viewmat, float fx, float fy,
+    float cx, float cy, int32_t W, int32_t H, float near_plane,
+    float far_plane, float blur, float max_radius, const float *cam_center,
+    int32_t sh_degree, float *uv, float *conic, float *depth, float *rxy,
+    int32_t *valid, float *color, mg_stream_t stream);
+
+/* Analytic backward of mg_preprocess_forward. Replaces preprocess_backward
+ * (metal_gauss/csrc/rasterize.mm:286-327; kernel preprocess.metal:223-411).
+ * d_color may be NULL (explicit-colour callers): the SH branch is skipped and
+ * d_sh / d_sh_rest are not written. In fused mode d_sh is (N,16,3) and
+ * d_sh_rest is ignored (the reference aliases the two, rasterize.mm:300-302). */
+int32_t mg_preprocess_backward(
+    int64_t N, const float *means, const float *quats, const float *scales,
+    const float *sh, const float *sh_rest, int32_t sh_fused,
+    const float *d_uv, const float *d_conic, const float *d_color,
+    const int32_t *valid, const float *viewmat, float fx, float fy, float cx,
+    float cy, int32_t W, int32_t H, float near_plane, float far_plane,
+    float blur, float max_radius, const float *cam_center, int32_t sh_degree,
+    float *d_means, float *d_quats, float *d_scales, float *d_sh,
+    float *d_sh_rest, mg_stream_t stream);
+
+/* ---------------------------------------------------------------- binning */
+
+/* Per-Gaussian count of tiles that pass the exact ellipse-vs-tile test
+ * (conic and opacity NULL: every tile of the uv +- rxy rectangle counts, the
+ * circular-bounds contract of build_tile_lists, metal_backend.py:111-147).
+ * Replaces bin_count (metal_gauss/csrc/rasterize.mm:485-497; kernel
+ * binning.metal:92-104). counts: (N,) int32. */
+int32_t mg_bin_count(int64_t N, const float *uv, const float *rxy,
+                     const float *conic, const float *opacity,
+                     const int32_t *valid, int32_t W, int32_t H, int32_t tile,
+                     int32_t tiles_x, int32_t tiles_y, int32_t *counts,
+                     mg_stream_t stream);
+
+/* Bytes of scratch mg_exclusive_scan_i32 needs for n elements. */
+int64_t mg_scan_workspace_bytes(int64_t n);
+
+/* Exclusive prefix sum of int32 counts into int32 offsets, plus the int64
+ * total written to total_dev (device) and, if total_host is not NULL, copied
+ * to that host address and synchronised. Replaces the torch.cumsum and the
+ * .item() of metal_backend.py:246-248. */
+int32_t mg_exclusive_scan_i32(const int32_t *in, int64_t n, int32_t *out,
+                              int64_t *total_dev, int64_t *total_host,
+                              void *workspace, int64_t workspace_bytes,
+                              mg_stream_t stream);
+
+/* Emits one (key, id) pair per surviving (Gaussian, tile), Gaussian-major,
+ * rows then columns, at offsets[g]: key = (tile_id << 32) | bits(depth).
+ * Replaces bin_write (metal_gauss/csrc/rasterize.mm:499-516; kernel
+ * binning.metal:106-120). keys: (total,) uint64, ids: (total,) int32. */
+int32_t mg_bin_write(int64_t N, const float *uv, const float *rxy,
+                     const float *conic, const float *opacity,
+                     const int32_t *valid, const float *depth,
+                     const int32_t *offsets, int64_t total, int32_t W,
+                     int32_t H, int32_t tile, int32_t tiles_x,
+                     int32_t tiles_y, uint64_t *keys, int32_t *ids,
+                     mg_stream_t stream);
+
+/* Bytes of scratch mg_sort_pairs_u64 needs for n pairs. */
+int64_t mg_sort_workspace_bytes(int64_t n);
+
+/* Stable LSD radix sort of (uint64 key, int32 value) pairs on bits
+ * [begin_bit, end_bit) of the key, 8 bits per pass. Equal keys keep their
+ * input order. Output goes to keys_out/vals_out; keys_in/vals_in are used as
+ * ping-pong buffers and are clobbered. Replaces torch.argsort(keys) plus the
+ * gather of ids (metal_backend.py:256-258). */
+int32_t mg_sort_pairs_u64(uint64_t *keys_in, int32_t *vals_in,
+                          uint64_t *keys_out, int32_t *vals_out, int64_t n,
+                          int32_t begin_bit, int32_t end_bit, void *workspace,
+                          int64_t workspace_bytes, mg_stream_t stream);
+
+/* tile_offsets[t] = first index i with (keys[i] >> 32) >= t, for
+ * t = 0..n_tiles; keys sorted. Replaces keys >> 32 plus torch.searchsorted
+ * (metal_backend.py:257-260). tile_offsets: (n_tiles + 1,) int32. */
+int32_t mg_tile_ranges(const uint64_t *sorted_keys, int64_t n,
+                       int32_t n_tiles, int32_t *tile_offsets,
+                       mg_stream_t stream);
+
+/* -------------------------------------------------------------- rasteriser */
+
+/* Front-to-back compositing, one workgroup per tile, one thread per pixel.
+ * Replaces rasterize_forward (metal_gauss/csrc/rasterize.mm:79-113; kernel
+ * rasterize.metal:61-167). t_min is the per-pixel stop transmittance (the
+ * reference hard-codes 1e-4, rasterize.metal:149); 0 disables early stop.
+ * out_stop holds the stop INDEX into gauss_ids (the reference's n_contrib). */
+int32_t mg_rasterize_forward(
+    int64_t N, const float *uv, const float *conic, const float *opacity,
+    const float *color, const int32_t *gauss_ids, const int32_t *tile_offsets,
+    int32_t W, int32_t H, int32_t tile, int32_t tiles_x, float t_min,
+    float *out_rgb, float *out_alpha, float *out_T, int32_t *out_stop,
+    mg_stream_t stream);
+
+/* Back-to-front replay of mg_rasterize_forward. Replaces rasterize_backward
+ * (metal_gauss/csrc/rasterize.mm:147-194; kernel rasterize.metal:173-340).
+ * Overwrites d_uv (N,2), d_conic (N,3), d_opacity (N,), d_color (N,3); when
+ * d_absuv is not NULL it also overwrites d_absuv (N,) with the per-pixel sum
+ * of |d_uv| (the reference's absgrad statistic). */
+int32_t mg_rasterize_backward(
+    int64_t N, const float *uv, const float *conic, const float *opacity,
+    const float *color, const int32_t *gauss_ids, const int32_t *tile_offsets,
+    const float *final_T, const int32_t *stop, const float *grad_rgb,
+    const float *grad_alpha, int32_t W, int32_t H, int32_t tile,
+    int32_t tiles_x, float *d_uv, float *d_conic, float *d_opacity,
+    float *d_color, float *d_absuv, mg_stream_t stream);
+
+/* ------------------------------------------------------------------- Adam */
+
+/* One Adam step on one flat tensor, torch's formula with eps after the
+ * sqrt(bias_correction2) divide. Replaces adam_step
+ * (metal_gauss/csrc/rasterize.mm:329-360; kernel adam.metal:25-42). */
+int32_t mg_adam_step(float *p, const float *g, float *m, float *v, int64_t n,
+                     float lr, float beta1, float beta2, float eps,
+                     int64_t step, mg_stream_t stream);
+
+/* One Adam step on up to 64 flat tensors in ONE launch. Host arrays of length
+ * count: p/g/m/v pointers, element counts, lr, and each tensor's step count
+ * after this update. eps_inside != 0 selects the p -= lr*sqrt(bc2)/bc1 *
+ * m/(sqrt(v)+eps) placement used by selective_adam.py:206 for dense groups.
+ * Replaces the per-tensor loop of FusedAdam.step (fused_adam.py:31-54). */
+int32_t mg_adam_step_multi(int32_t count, float *const *p,
+                           const float *const *g, float *const *m,
+                           float *const *v, const int64_t *n,
+                           const float *lr, const int64_t *step, float beta1,
+                           float beta2, float eps, int32_t eps_inside,
+                           mg_stream_t stream);
+
+/* Row-masked Adam with a per-row float step count, over up to 64 tensors in
+ * one launch. Tensor k has rows[k] rows of width[k] floats; rows r with
+ * r < n_visible and visible[r] != 0 get steps[r] += 1 and
+ * p -= lr * sqrt(1-b2^k)/(1-b1^k) * m/(sqrt(v)+eps); other rows are left
+ * untouched. visible: (n_visible,) uint8 (torch.bool). The reference has no
+ * kernel for this; it replaces SelectiveAdam._step_indexed / _step_masked
+ * (selective_adam.py:116-187). */
+int32_t mg_selective_adam_step(int32_t count, float *const *p,
+                               const float *const *g, float *const *m,
+                               float *const *v, float *const *steps,
+                               const int64_t *rows, const int32_t *width,
+                               const float *lr, const uint8_t *visible,
+                               int64_t n_visible, float beta1, float beta2,
+                               float eps, mg_stream_t stream);
+
+/* ------------------------------------------------------------------- SSIM */
+
+/* The five SSIM entry points of the reference, same math and layouts
+ * (metal_gauss/csrc/rasterize.mm:383-461; kernels ssim.metal:23-188). x, y
+ * are (H,W,3); stacks are (15,H,W) with channels x,y,xx,yy,xy (x3 colours);
+ * w is the 11-tap window (device, 11 floats). */
+int32_t mg_ssim_stack_blur_h(const float *x, const float *y, const float *w,
+                             int32_t H, int32_t W, float *out,
+                             mg_stream_t stream);
+int32_t mg_ssim_blur15(const float *src, const float *w, int32_t dir,
+                       int32_t H, int32_t W, float *out, mg_stream_t stream);
+int32_t mg_ssim_tail_forward(const float *b, int32_t H, int32_t W,
+                             float *out, mg_stream_t stream);
+int32_t mg_ssim_tail_backward(const float *b, const float *gout, int32_t H,
+                              int32_t W, float *gb, mg_stream_t stream);
+int32_t mg_ssim_chain_backward(const float *x, const float *y,
+                               const float *d_stack, int32_t H, int32_t W,
+                               float *d_x, mg_stream_t stream);
+
+/* Fused SSIM: one pass builds the five moments, blurs both ways in LDS and
+ * evaluates SSIM; it writes the mean SSIM to mean_out (device, 1 float) and
+ * the three unscaled adjoint maps (9,H,W) the backward needs to partials.
+ * No counterpart in the reference, which runs the five kernels above
+ * (train.py:86-105). Scratch: mg_ssim_fused_workspace_bytes(H, W). */
+int64_t mg_ssim_fused_workspace_bytes(int32_t H, int32_t W);
+int32_t mg_ssim_fused_forward(const float *x, const float *y, const float *w,
+                              int32_t H, int32_t W, float *partials,
+                              float *mean_out, void *workspace,
+                              int64_t workspace_bytes, mg_stream_t stream);
+/* d_x = scale * (blur(partials) chained through the moments), scale read
+ * from the device scalar scale_dev (the upstream gradient of the mean). */
+int32_t mg_ssim_fused_backward(const float *x, const float *y, const float *w,
+                               const float *partials, const float *scale_dev,
+                               int32_t H, int32_t W, float *d_x,
+                               mg_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MGAUSS_H */

@@ -1,0 +1,19 @@
+"""metal_gauss_amd: the differentiable 3D Gaussian splatting step of
+nandometzger/metal-gauss, rebuilt as hand-written gfx950 HIP kernels.
+
+Public surface (names of the reference's modules):
+    render                 api.render with backend "hip" (alias "metal")
+    backend                the metal_backend surface: render, build_tile_lists,
+                           build_tile_lists_metal, antialias_scale, ...
+    FusedAdam              fused_adam.FusedAdam
+    SelectiveAdam          selective_adam.SelectiveAdam
+    ssim, gaussian_kernel  the fused SSIM loss used by the training step
+"""
+
+from .api import BACKENDS, render  # noqa: F401
+from .fused_adam import FusedAdam  # noqa: F401
+from .selective_adam import SelectiveAdam  # noqa: F401
+from .ssim import gaussian_kernel, ssim  # noqa: F401
+from . import backend  # noqa: F401
+
+__version__ = "0.1.0"

@@ -1,0 +1,473 @@
+"""HIP backend: the reference's ``metal_backend`` operator surface on gfx950.
+
+Same functions, argument meaning and error behaviour as
+metal_gauss/metal_backend.py, so a caller of the reference's surface can switch
+to this module:
+
+* ``render`` (metal_backend.py:396-559) - projection + SH, binning, raster,
+  background blend; returns (rgb (H,W,3), alpha (H,W), info);
+* ``build_tile_lists`` (metal_backend.py:111-214) and
+  ``build_tile_lists_metal`` (metal_backend.py:217-285) - tile lists, here both
+  on the GPU: count, scan, key emission, radix sort and tile ranges are all
+  HIP kernels (the reference keeps argsort/cumsum/searchsorted in torch);
+* ``_PreprocessMetal`` / ``_RasterizeMetal`` (metal_backend.py:288-364) - the
+  autograd bridges, under the same names;
+* ``antialias_scale`` (metal_backend.py:367-393), ``_load`` (76-108) and
+  ``stale_lock_message`` (37-61).
+
+What changes is underneath: every heavy step is a hand-written HIP kernel in
+libmgauss.so (include/mgauss.h) reached through ``_lib``. Torch is used only
+for allocation, the stream, autograd plumbing and the small elementwise glue
+the reference also leaves in torch (SH zero-padding, antialias compensation,
+background blend).
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from pathlib import Path
+
+import torch
+
+from . import _lib
+
+_HERE = Path(__file__).resolve().parent
+
+# Longer than any build of the library takes; past it, a lock is a leftover.
+_STALE_LOCK_S = 180.0
+
+# The per-pixel stop transmittance of the reference kernel (rasterize.metal:149).
+DEFAULT_T_MIN = 1e-4
+
+
+def stale_lock_message(build_dir, now: float | None = None) -> str | None:
+    """What to say about a lock left in the library's build directory.
+
+    The ahead-of-time build (build.py) holds ``<build_dir>/lock`` while it
+    compiles. Nothing is deleted here: two processes may build at once. Same
+    contract as metal_backend.py:37-61.
+    """
+    try:
+        lock = Path(build_dir) / "lock"
+        age = (now if now is not None else time.time()) - lock.stat().st_mtime
+    except OSError:
+        return None
+    where = f"waiting for the kernel build lock at {lock} ({age:.0f}s old)"
+    if age < _STALE_LOCK_S:
+        return f"{where}; another process is probably compiling."
+    return (f"{where}. A build takes under a minute, so this one is stale -- left by an "
+            f"interrupted build. Delete it to carry on:\n    rm {lock}")
+
+
+def _load():
+    """The native library, loaded and initialised (metal_backend.py:76-108).
+
+    The reference compiles Metal source at first use; libmgauss.so is built
+    ahead of time, so this only loads it. Raises if it is missing.
+    """
+    return _lib.load()
+
+
+def _require_gpu(t: torch.Tensor) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"hip backend requires ROCm (cuda) tensors, got device '{t.device}'. "
+            "Refusing to silently move data or fall back to another backend.")
+
+
+def _tile_grid(W: int, H: int, tile: int) -> tuple[int, int]:
+    return math.ceil(W / tile), math.ceil(H / tile)
+
+
+_pinned_total = None
+
+
+def _host_total() -> torch.Tensor:
+    global _pinned_total
+    if _pinned_total is None:
+        _pinned_total = torch.zeros(1, dtype=torch.int64, pin_memory=True)
+    return _pinned_total
+
+
+def _empty_lists(n_tiles: int, tx: int, device):
+    return (torch.zeros(0, dtype=torch.int32, device=device),
+            torch.zeros(n_tiles + 1, dtype=torch.int32, device=device), tx,
+            torch.zeros(0, dtype=torch.int64, device=device))
+
+
+def _bin(uv, rxy, depth, valid_i, conic, opacity, W, H, tile):
+    """Count -> scan -> emit -> radix sort -> tile ranges, all on the GPU.
+
+    Returns (gauss_ids, tile_offsets, tiles_x, sorted (tile|depth) keys as
+    int64). One device->host read per call: the intersection total that sizes the key
+    buffers (the reference's .item(), metal_backend.py:247-248).
+    """
+    lib = _load()
+    device = uv.device
+    tx, ty = _tile_grid(W, H, tile)
+    n_tiles = tx * ty
+    N = uv.shape[0]
+    if N == 0:
+        return _empty_lists(n_tiles, tx, device)
+    s = _lib.stream(uv)
+    p_uv = _lib.dev_tensor(uv, "uv")
+    p_rxy = _lib.dev_tensor(rxy, "rxy")
+    p_valid = _lib.dev_tensor(valid_i, "valid", torch.int32)
+    p_conic = _lib.dev_tensor(conic, "conic") if conic is not None else None
+    p_op = _lib.dev_tensor(opacity, "opacity") if opacity is not None else None
+    p_depth = _lib.dev_tensor(depth, "depth")
+
+    counts = torch.empty(N, dtype=torch.int32, device=device)
+    _lib.check(lib.mg_bin_count(N, p_uv, p_rxy, p_conic, p_op, p_valid, W, H, tile, tx, ty,
+                                counts.data_ptr(), s))
+    offsets = torch.empty(N, dtype=torch.int32, device=device)
+    scan_ws = torch.empty(lib.mg_scan_workspace_bytes(N), dtype=torch.uint8, device=device)
+    total_dev = torch.empty(1, dtype=torch.int64, device=device)
+    host = _host_total()
+    _lib.check(lib.mg_exclusive_scan_i32(counts.data_ptr(), N, offsets.data_ptr(),
+                                         total_dev.data_ptr(), host.data_ptr(),
+                                         scan_ws.data_ptr(), scan_ws.numel(), s))
+    total = int(host[0])
+    if total == 0:
+        return _empty_lists(n_tiles, tx, device)
+    if total >= 2 ** 31:
+        raise RuntimeError(f"{total} tile intersections exceed the int32 index range")
+
+    keys = torch.empty(2 * total, dtype=torch.int64, device=device)
+    ids = torch.empty(2 * total, dtype=torch.int32, device=device)
+    k_in, k_out = keys[:total], keys[total:]
+    i_in, i_out = ids[:total], ids[total:]
+    _lib.check(lib.mg_bin_write(N, p_uv, p_rxy, p_conic, p_op, p_valid, p_depth,
+                                offsets.data_ptr(), total, W, H, tile, tx, ty,
+                                k_in.data_ptr(), i_in.data_ptr(), s))
+    sort_ws = torch.empty(lib.mg_sort_workspace_bytes(total), dtype=torch.uint8, device=device)
+    end_bit = 32 + max(1, (n_tiles - 1).bit_length())
+    _lib.check(lib.mg_sort_pairs_u64(k_in.data_ptr(), i_in.data_ptr(), k_out.data_ptr(),
+                                     i_out.data_ptr(), total, 0, end_bit, sort_ws.data_ptr(),
+                                     sort_ws.numel(), s))
+    tile_offsets = torch.empty(n_tiles + 1, dtype=torch.int32, device=device)
+    _lib.check(lib.mg_tile_ranges(k_out.data_ptr(), total, n_tiles, tile_offsets.data_ptr(), s))
+    return i_out, tile_offsets, tx, k_out
+
+
+def _cap_per_tile(gauss_ids, tile_offsets, max_per_tile):
+    """Nearest `max_per_tile` per tile (metal_backend.py:262-283); off by default."""
+    n_tiles = tile_offsets.numel() - 1
+    counts = (tile_offsets[1:] - tile_offsets[:-1]).to(torch.int64)
+    tile_of = torch.repeat_interleave(torch.arange(n_tiles, device=gauss_ids.device), counts)
+    rank = torch.arange(gauss_ids.numel(), device=gauss_ids.device) - \
+        tile_offsets[:-1].to(torch.int64)[tile_of]
+    keep = rank < max_per_tile
+    kept = torch.minimum(counts, torch.tensor(max_per_tile, device=counts.device))
+    offs = torch.zeros(n_tiles + 1, dtype=torch.int64, device=counts.device)
+    offs[1:] = torch.cumsum(kept, 0)
+    return gauss_ids[keep].contiguous(), offs.to(torch.int32).contiguous()
+
+
+def build_tile_lists_metal(uv, rxy, depth, valid, conic, opacity, W, H, tile,
+                           max_per_tile: int = 0):
+    """Tile lists with the exact ellipse-vs-tile test (metal_backend.py:217-285).
+
+    Returns (gauss_ids int32 sorted by (tile, depth), tile_offsets int32
+    (n_tiles+1), tiles_x). Equal keys keep emission order (Gaussian, row,
+    column): the radix sort is stable.
+    """
+    _require_gpu(uv)
+    valid_i = valid.to(torch.int32).contiguous()
+    out = _bin(uv.detach().contiguous(), rxy.detach().contiguous(), depth.detach().contiguous(),
+               valid_i, conic.detach().contiguous(), opacity.detach().contiguous(), W, H, tile)
+    gauss_ids, tile_offsets, tx = out[0], out[1], out[2]
+    if max_per_tile > 0 and gauss_ids.numel() > 0:
+        gauss_ids, tile_offsets = _cap_per_tile(gauss_ids, tile_offsets, max_per_tile)
+    return gauss_ids, tile_offsets, tx
+
+
+# The reference's name describes its kernel language; this is the same call.
+build_tile_lists_hip = build_tile_lists_metal
+
+
+def build_tile_lists(uv, radius, depth, valid, W, H, tile, ry=None, conic=None, opacity=None):
+    """Tile lists from rectangular bounds (metal_backend.py:111-214).
+
+    ``radius`` is the x half-extent and ``ry`` the y half-extent (default
+    ``radius``). With ``conic`` and ``opacity`` the exact ellipse test is
+    applied as in build_tile_lists_metal; without them every tile of the
+    rectangle is listed.
+    """
+    _require_gpu(uv)
+    if ry is None:
+        ry = radius
+    rxy = torch.stack([radius.detach(), ry.detach()], dim=-1).to(torch.float32).contiguous()
+    valid_i = valid.to(torch.int32).contiguous()
+    if (conic is None) != (opacity is None):
+        conic = opacity = None
+    out = _bin(uv.detach().contiguous(), rxy, depth.detach().contiguous(), valid_i,
+               None if conic is None else conic.detach().contiguous(),
+               None if opacity is None else opacity.detach().contiguous(), W, H, tile)
+    return out[0], out[1], out[2]
+
+
+def _camera(K, viewmat):
+    K_h = K if K.device.type == "cpu" else K.detach().cpu()
+    fx, fy = float(K_h[0, 0]), float(K_h[1, 1])
+    cx, cy = float(K_h[0, 2]), float(K_h[1, 2])
+    vm_h = viewmat.detach()
+    if vm_h.device.type != "cpu":
+        vm_h = vm_h.cpu()
+    vm_h = vm_h.to(torch.float32).contiguous()
+    cam_center = (-vm_h[:3, :3].T @ vm_h[:3, 3]).contiguous()
+    return fx, fy, cx, cy, vm_h, cam_center
+
+
+class _PreprocessMetal(torch.autograd.Function):
+    """Fused projection + SH colour, forward and analytic backward.
+
+    Same bridge as metal_backend.py:288-333. ``sh_rest is None`` means ``sh``
+    is one (N,16,3) tensor; otherwise sh is the (N,1,3) DC band and sh_rest
+    the (N,15,3) bands 1+. ``sh is None`` is the explicit-colour route: only
+    the projection runs and no colour is returned.
+    """
+
+    @staticmethod
+    def forward(ctx, means, quats, scales, sh, sh_rest, ctx_opac, viewmat, fx, fy, cx, cy,
+                W, H, near, far, blur, max_radius, cam_center, sh_degree):
+        lib = _load()
+        N = means.shape[0]
+        dev = means.device
+        means, quats, scales = (t.contiguous() for t in (means, quats, scales))
+        fused = sh_rest is None
+        if sh is not None:
+            sh = sh.contiguous()
+            rest = None if fused else sh_rest.contiguous()
+            if fused and tuple(sh.shape[1:]) != (16, 3) or (not fused and (
+                    tuple(sh.shape[1:]) != (1, 3) or tuple(rest.shape[1:]) != (15, 3))):
+                raise RuntimeError(
+                    "SH must be either one (N,16,3) tensor or (N,1,3)+(N,15,3); got "
+                    f"{tuple(sh.shape)} and {None if rest is None else tuple(rest.shape)}")
+        else:
+            rest = None
+        opac = ctx_opac.contiguous()
+        uv = torch.empty(N, 2, device=dev)
+        conic = torch.empty(N, 3, device=dev)
+        depth = torch.empty(N, device=dev)
+        rxy = torch.empty(N, 2, device=dev)
+        valid = torch.empty(N, dtype=torch.int32, device=dev)
+        color = torch.empty(N, 3, device=dev) if sh is not None else None
+        vm = _lib.host_f32(viewmat)
+        cc = _lib.host_f32(cam_center)
+        _lib.check(lib.mg_preprocess_forward(
+            N, _lib.dev_tensor(means, "means"), _lib.dev_tensor(quats, "quats"),
+            _lib.dev_tensor(scales, "scales"),
+            None if sh is None else _lib.dev_tensor(sh, "sh"),
+            None if rest is None else _lib.dev_tensor(rest, "sh_rest"), int(fused),
+            _lib.dev_tensor(opac, "opacities"), vm, fx, fy, cx, cy, W, H, near, far, blur,
+            max_radius, cc, sh_degree, uv.data_ptr(), conic.data_ptr(), depth.data_ptr(),
+            rxy.data_ptr(), valid.data_ptr(),
+            None if color is None else color.data_ptr(), _lib.stream(means)))
+        ctx.save_for_backward(means, quats, scales, sh, rest, valid)
+        ctx.fused = fused
+        ctx.has_sh = sh is not None
+        ctx.meta = (viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
+                    sh_degree)
+        ctx.mark_non_differentiable(depth, rxy, valid)
+        if color is None:
+            return uv, conic, depth, rxy, valid
+        return uv, conic, depth, rxy, valid, color
+
+    @staticmethod
+    def backward(ctx, d_uv, d_conic, d_depth, d_rxy, d_valid, d_color=None):
+        lib = _load()
+        means, quats, scales, sh, rest, valid = ctx.saved_tensors
+        viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center, deg = ctx.meta
+        N = means.shape[0]
+        dev = means.device
+        d_means = torch.empty(N, 3, device=dev)
+        d_quats = torch.empty(N, 4, device=dev)
+        d_scales = torch.empty(N, 3, device=dev)
+        d_sh = d_rest = None
+        if ctx.has_sh:
+            d_sh = torch.empty_like(sh)
+            d_rest = None if ctx.fused else torch.empty_like(rest)
+            d_color = torch.zeros(N, 3, device=dev) if d_color is None else d_color.contiguous()
+        d_uv = d_uv.contiguous()
+        d_conic = d_conic.contiguous()
+        _lib.check(lib.mg_preprocess_backward(
+            N, means.data_ptr(), quats.data_ptr(), scales.data_ptr(),
+            None if sh is None else sh.data_ptr(), None if rest is None else rest.data_ptr(),
+            int(ctx.fused), _lib.dev_tensor(d_uv, "d_uv"), _lib.dev_tensor(d_conic, "d_conic"),
+            None if not ctx.has_sh else _lib.dev_tensor(d_color, "d_color"), valid.data_ptr(),
+            _lib.host_f32(viewmat), fx, fy, cx, cy, W, H, near, far, blur, max_radius,
+            _lib.host_f32(cam_center), deg, d_means.data_ptr(), d_quats.data_ptr(),
+            d_scales.data_ptr(), None if d_sh is None else d_sh.data_ptr(),
+            None if d_rest is None else d_rest.data_ptr(), _lib.stream(means)))
+        return (d_means, d_quats, d_scales, d_sh, d_rest) + (None,) * 14
+
+
+class _RasterizeMetal(torch.autograd.Function):
+    """Compositing forward/backward bridge (metal_backend.py:336-364)."""
+
+    @staticmethod
+    def forward(ctx, uv, conic, opacity, color, gauss_ids, tile_offsets, W, H, tile, tiles_x,
+                absgrad_out=None, t_min=DEFAULT_T_MIN):
+        lib = _load()
+        dev = uv.device
+        uv, conic, opacity, color = (t.contiguous() for t in (uv, conic, opacity, color))
+        N = uv.shape[0]
+        rgb = torch.empty(H, W, 3, device=dev)
+        alpha = torch.empty(H, W, device=dev)
+        T = torch.empty(H, W, device=dev)
+        stop = torch.empty(H, W, dtype=torch.int32, device=dev)
+        _lib.check(lib.mg_rasterize_forward(
+            N, _lib.dev_tensor(uv, "uv"), _lib.dev_tensor(conic, "conic"),
+            _lib.dev_tensor(opacity, "opacity"), _lib.dev_tensor(color, "color"),
+            _lib.dev_tensor(gauss_ids, "gauss_ids", torch.int32),
+            _lib.dev_tensor(tile_offsets, "tile_offsets", torch.int32), W, H, tile, tiles_x,
+            float(t_min), rgb.data_ptr(), alpha.data_ptr(), T.data_ptr(), stop.data_ptr(),
+            _lib.stream(uv)))
+        ctx.save_for_backward(uv, conic, opacity, color, gauss_ids, tile_offsets, T, stop)
+        ctx.dims = (W, H, tile, tiles_x)
+        # absgrad is a statistic of the backward, not a gradient: the caller
+        # hands in a buffer and the backward accumulates into it.
+        ctx.absgrad_out = absgrad_out
+        return rgb, alpha
+
+    @staticmethod
+    def backward(ctx, grad_rgb, grad_alpha):
+        lib = _load()
+        uv, conic, opacity, color, gauss_ids, tile_offsets, T, stop = ctx.saved_tensors
+        W, H, tile, tiles_x = ctx.dims
+        N = uv.shape[0]
+        dev = uv.device
+        d_uv = torch.empty(N, 2, device=dev)
+        d_conic = torch.empty(N, 3, device=dev)
+        d_op = torch.empty(N, device=dev)
+        d_col = torch.empty(N, 3, device=dev)
+        d_abs = torch.empty(N, device=dev) if ctx.absgrad_out is not None else None
+        grad_rgb = grad_rgb.contiguous()
+        grad_alpha = grad_alpha.contiguous()
+        _lib.check(lib.mg_rasterize_backward(
+            N, uv.data_ptr(), conic.data_ptr(), opacity.data_ptr(), color.data_ptr(),
+            gauss_ids.data_ptr(), tile_offsets.data_ptr(), T.data_ptr(), stop.data_ptr(),
+            _lib.dev_tensor(grad_rgb, "grad_rgb"), _lib.dev_tensor(grad_alpha, "grad_alpha"),
+            W, H, tile, tiles_x, d_uv.data_ptr(), d_conic.data_ptr(), d_op.data_ptr(),
+            d_col.data_ptr(), None if d_abs is None else d_abs.data_ptr(), _lib.stream(uv)))
+        if ctx.absgrad_out is not None:
+            ctx.absgrad_out[:N] += d_abs
+        return (d_uv, d_conic, d_op, d_col) + (None,) * 8
+
+
+# Names that describe this backend rather than the reference's.
+_PreprocessHIP = _PreprocessMetal
+_RasterizeHIP = _RasterizeMetal
+
+
+def antialias_scale(conic: torch.Tensor, blur: float) -> torch.Tensor:
+    """Mip-Splatting opacity compensation sqrt(det_before / det_after).
+
+    Recovered from the conic, the inverse of the dilated covariance
+    (metal_backend.py:367-393): det_after = 1/det(conic), the dilated
+    covariance is (conic_z, -conic_y, conic_x) * det_after, and the undilated
+    determinant subtracts ``blur`` from the diagonal. Torch autograd carries
+    its gradient into the conic.
+    """
+    cxx, cxy, cyy = conic[:, 0], conic[:, 1], conic[:, 2]
+    det_conic = (cxx * cyy - cxy * cxy).clamp_min(1e-12)
+    det_after = 1.0 / det_conic
+    a = cyy * det_after
+    b = -cxy * det_after
+    c = cxx * det_after
+    det_before = (a - blur) * (c - blur) - b * b
+    return (det_before.clamp_min(0.0) / det_after).clamp(0.0, 1.0).sqrt()
+
+
+def _sh_inputs(sh, sh_rest):
+    """(sh_in, rest_in) for the kernel: fused (N,16,3) with rest None, or the
+    (N,1,3) + (N,15,3) pair; narrower inputs are zero-padded
+    (metal_backend.py:482-497)."""
+    if sh_rest is None:
+        sh_in = sh
+        if sh_in.shape[1] < 16:
+            pad = torch.zeros(sh_in.shape[0], 16 - sh_in.shape[1], 3, device=sh_in.device,
+                              dtype=sh_in.dtype)
+            sh_in = torch.cat([sh_in, pad], dim=1)
+        return sh_in, None
+    if sh.shape[1] != 1:
+        raise ValueError(
+            f"with sh_rest given, sh must be the DC band (N,1,3); got {tuple(sh.shape)}")
+    rest_in = sh_rest
+    if rest_in.shape[1] < 15:
+        pad = torch.zeros(rest_in.shape[0], 15 - rest_in.shape[1], 3, device=rest_in.device,
+                          dtype=rest_in.dtype)
+        rest_in = torch.cat([rest_in, pad], dim=1)
+    return sh, rest_in
+
+
+def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
+           sh_degree: int = 3, tile: int | None = None,
+           near: float = 0.01, far: float = 100.0,
+           background=(0.0, 0.0, 0.0), colors=None, max_radius_frac: float = 1.0,
+           sh_rest=None, antialias: bool = False, absgrad_out=None,
+           min_transmittance: float = DEFAULT_T_MIN, **_ignored):
+    """Render Gaussians from one camera; same signature as the reference's.
+
+    means (N,3) world; quats (N,4) wxyz (need not be normalised); scales (N,3)
+    linear; opacities (N,) in [0,1]; sh (N,B,3) or the (N,1,3) DC band with
+    ``sh_rest`` (N,15,3); K (3,3); viewmat (4,4) world->camera. Returns
+    (rgb (H,W,3), alpha (H,W), info). ``colors`` (N,3) bypasses SH.
+    ``min_transmittance`` is the per-pixel early-stop threshold (the
+    reference's fixed 1e-4); 0 composites every listed Gaussian.
+    """
+    explicit_colors = colors is not None
+    _require_gpu(means)
+    if tile is None:
+        tile = 16
+    W, H, tile = int(W), int(H), int(tile)
+    mt = _lib.open_library().mg_max_tile()
+    if tile * tile > mt * mt:
+        raise RuntimeError(
+            f"tile {tile} needs {tile * tile} threads per threadgroup; rasterize_forward "
+            f"allows at most {mt * mt} on this GPU")
+    fx, fy, cx, cy, vm_h, cam_center = _camera(K, viewmat)
+    max_radius = max_radius_frac * max(W, H)
+
+    if explicit_colors:
+        uv, conic, depth, rxy, valid_i = _PreprocessMetal.apply(
+            means, quats, scales, None, None, opacities.detach(), vm_h, fx, fy, cx, cy, W, H,
+            near, far, 0.3, max_radius, cam_center, sh_degree)
+        colors = colors.contiguous()
+    else:
+        sh_in, rest_in = _sh_inputs(sh, sh_rest)
+        uv, conic, depth, rxy, valid_i, colors = _PreprocessMetal.apply(
+            means, quats, scales, sh_in, rest_in, opacities.detach(), vm_h, fx, fy, cx, cy,
+            W, H, near, far, 0.3, max_radius, cam_center, sh_degree)
+    valid_b = valid_i.bool()
+    if antialias:
+        # Before binning: the compensated opacity gives a tighter, still exact
+        # ellipse bound (metal_backend.py:506-511).
+        opacities = opacities * antialias_scale(conic, 0.3)
+
+    gauss_ids, tile_offsets, tiles_x = build_tile_lists_metal(
+        uv.detach(), rxy.detach(), depth.detach(), valid_i, conic.detach(),
+        opacities.detach(), W, H, tile)
+
+    rgb, alpha = _RasterizeMetal.apply(
+        uv, conic, opacities, colors, gauss_ids, tile_offsets, W, H, tile, tiles_x,
+        absgrad_out, min_transmittance)
+
+    if background is not None:
+        bg = torch.as_tensor(background, device=rgb.device, dtype=rgb.dtype)
+        rgb = rgb + (1.0 - alpha).clamp_min(0)[..., None] * bg
+
+    if uv.requires_grad:
+        uv.retain_grad()
+
+    return rgb, alpha, {
+        "uv": uv,
+        "tiles": int(tile_offsets.numel() - 1),
+        "isect_total": int(gauss_ids.numel()),
+        "isect_dropped": 0,
+        "isect_dropped_frac": 0.0,
+        "valid_mask": valid_b,
+        "backend": "hip",
+    }

@@ -1,0 +1,287 @@
+// Fused Adam and selective (row-masked) Adam.
+//
+// Both are pure streaming kernels: 28 bytes of HBM traffic per parameter
+// element (read p, g, m, v; write p, m, v) and a handful of flops, so the only
+// design goals are full-width coalesced access, enough bytes in flight per CU,
+// and one launch for every parameter group of a step.
+//
+// Formula (torch.optim.Adam, eps after the sqrt(bias_correction2) divide), as
+// in metal_gauss/csrc/adam.metal:34-41 with bc1/sqrt(bc2) formed in double on
+// the host (rasterize.mm:338-342):
+//     m = b1 m + (1-b1) g
+//     v = b2 v + (1-b2) g^2
+//     p -= (lr / bc1) * m / (sqrt(v) / sqrt(bc2) + eps)
+// The selective / dense-auxiliary variant of metal_gauss/selective_adam.py
+// (lines 144-148, 182-186, 201-206) puts eps inside instead:
+//     p -= lr * sqrt(bc2) / bc1 * m / (sqrt(v) + eps)
+#include <cmath>
+
+#include "mg_common.h"
+
+namespace mg {
+
+constexpr int kAdamMaxTensors = 32;
+constexpr int kAdamThreads = 256;
+constexpr int kAdamVec = 4;                       // float4 per thread
+constexpr int kAdamElemsPerBlock = kAdamThreads * kAdamVec * 2;  // 2048
+
+struct AdamTensor {
+    float *p;
+    const float *g;
+    float *m;
+    float *v;
+    int64_t n;
+    int32_t block_begin;   // first workgroup of this tensor
+    int32_t vec_ok;        // all four pointers 16-byte aligned
+    float step_size;       // lr / bc1          (eps_inside: lr*sqrt(bc2)/bc1)
+    float inv_sqrt_bc2;    // 1 / sqrt(bc2)     (eps_inside: 1)
+};
+
+struct AdamTable {
+    AdamTensor t[kAdamMaxTensors];
+    int32_t count;
+    float b1, b2, eps;
+    int32_t eps_inside;
+};
+
+__device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v,
+                                          float b1, float b2, float eps,
+                                          float step_size, float inv_sqrt_bc2,
+                                          bool eps_inside) {
+    m = fmaf(b1, m, (1.0f - b1) * g);
+    v = fmaf(b2, v, (1.0f - b2) * g * g);
+    const float sv = sqrtf(v);
+    const float denom = eps_inside ? (sv + eps) : (sv * inv_sqrt_bc2 + eps);
+    p = p - step_size * m / denom;
+}
+
+__global__ __launch_bounds__(kAdamThreads) void adam_multi_kernel(const AdamTable tab) {
+    // Find this workgroup's tensor: a uniform linear scan over <= 32 entries.
+    int k = 0;
+    const int bid = blockIdx.x;
+    while (k + 1 < tab.count && bid >= tab.t[k + 1].block_begin) ++k;
+    const AdamTensor &T = tab.t[k];
+    const int64_t base = (int64_t)(bid - T.block_begin) * kAdamElemsPerBlock;
+    const bool ei = tab.eps_inside != 0;
+
+    if (T.vec_ok) {
+        // Two float4 per thread, each instruction covering 4 KB contiguous.
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int64_t e = base + ((int64_t)r * kAdamThreads + threadIdx.x) * kAdamVec;
+            if (e + kAdamVec <= T.n) {
+                float4 p = *reinterpret_cast<const float4 *>(T.p + e);
+                const float4 g = *reinterpret_cast<const float4 *>(T.g + e);
+                float4 m = *reinterpret_cast<const float4 *>(T.m + e);
+                float4 v = *reinterpret_cast<const float4 *>(T.v + e);
+                adam_elem(p.x, g.x, m.x, v.x, tab.b1, tab.b2, tab.eps, T.step_size, T.inv_sqrt_bc2, ei);
+                adam_elem(p.y, g.y, m.y, v.y, tab.b1, tab.b2, tab.eps, T.step_size, T.inv_sqrt_bc2, ei);
+                adam_elem(p.z, g.z, m.z, v.z, tab.b1, tab.b2, tab.eps, T.step_size, T.inv_sqrt_bc2, ei);
+                adam_elem(p.w, g.w, m.w, v.w, tab.b1, tab.b2, tab.eps, T.step_size, T.inv_sqrt_bc2, ei);
+                *reinterpret_cast<float4 *>(T.p + e) = p;
+                *reinterpret_cast<float4 *>(T.m + e) = m;
+                *reinterpret_cast<float4 *>(T.v + e) = v;
+            } else {
+                for (int64_t i = e; i < T.n && i < e + kAdamVec; ++i) {
+                    float p = T.p[i], m = T.m[i], v = T.v[i];
+                    adam_elem(p, T.g[i], m, v, tab.b1, tab.b2, tab.eps, T.step_size, T.inv_sqrt_bc2, ei);
+                    T.p[i] = p; T.m[i] = m; T.v[i] = v;
+                }
+            }
+        }
+    } else {
+        for (int r = 0; r < kAdamElemsPerBlock / kAdamThreads; ++r) {
+            const int64_t i = base + (int64_t)r * kAdamThreads + threadIdx.x;
+            if (i < T.n) {
+                float p = T.p[i], m = T.m[i], v = T.v[i];
+                adam_elem(p, T.g[i], m, v, tab.b1, tab.b2, tab.eps, T.step_size, T.inv_sqrt_bc2, ei);
+                T.p[i] = p; T.m[i] = m; T.v[i] = v;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------ selective Adam
+// One workgroup owns kSelRows consecutive rows of one tensor, so the per-row
+// step count can be read, bumped and written back without any other
+// workgroup touching it. Invisible rows issue no loads at all.
+constexpr int kSelRows = 256;
+
+struct SelTensor {
+    float *p;
+    const float *g;
+    float *m;
+    float *v;
+    float *steps;
+    int64_t rows;
+    int32_t width;
+    int32_t block_begin;
+    float lr;
+};
+
+struct SelTable {
+    SelTensor t[kAdamMaxTensors];
+    int32_t count;
+    float b1, b2, eps;
+    const uint8_t *visible;
+    int64_t n_visible;
+};
+
+__global__ __launch_bounds__(kAdamThreads) void selective_adam_kernel(const SelTable tab) {
+    __shared__ float s_step_size[kSelRows];
+    __shared__ uint8_t s_vis[kSelRows];
+
+    int k = 0;
+    const int bid = blockIdx.x;
+    while (k + 1 < tab.count && bid >= tab.t[k + 1].block_begin) ++k;
+    const SelTensor &T = tab.t[k];
+    const int64_t r0 = (int64_t)(bid - T.block_begin) * kSelRows;
+    const int nrows = (int)min((int64_t)kSelRows, T.rows - r0);
+
+    for (int t = threadIdx.x; t < kSelRows; t += kAdamThreads) {
+        const int64_t r = r0 + t;
+        uint8_t vis = 0;
+        if (t < nrows && r < tab.n_visible) vis = tab.visible[r] != 0;
+        float ss = 0.f;
+        if (vis) {
+            // Per-row bias correction in fp32, as torch evaluates
+            // 1 - b ** steps on a float32 tensor; the power itself is taken in
+            // double and rounded once so it is the correctly rounded float.
+            const float kf = T.steps[r] + 1.0f;
+            const float pw1 = (float)pow((double)tab.b1, (double)kf);
+            const float pw2 = (float)pow((double)tab.b2, (double)kf);
+            const float bc1 = 1.0f - pw1;
+            const float bc2 = 1.0f - pw2;
+            ss = T.lr * (sqrtf(bc2) / bc1);
+            T.steps[r] = kf;
+        }
+        s_step_size[t] = ss;
+        s_vis[t] = vis;
+    }
+    __syncthreads();
+
+    const int64_t e0 = r0 * T.width;
+    const int64_t ne = (int64_t)nrows * T.width;
+    const float b1 = tab.b1, b2 = tab.b2, eps = tab.eps;
+    for (int64_t le = threadIdx.x; le < ne; le += kAdamThreads) {
+        const int lr_ = (int)(le / T.width);
+        if (!s_vis[lr_]) continue;
+        const int64_t i = e0 + le;
+        const float g = T.g[i];
+        float m = T.m[i] * b1 + g * (1.0f - b1);
+        float v = T.v[i] * b2 + g * g * (1.0f - b2);
+        T.m[i] = m;
+        T.v[i] = v;
+        T.p[i] = T.p[i] - s_step_size[lr_] * m / (sqrtf(v) + eps);
+    }
+}
+
+}  // namespace mg
+
+using namespace mg;
+
+extern "C" {
+
+int32_t mg_adam_step_multi(int32_t count, float *const *p, const float *const *g,
+                           float *const *m, float *const *v, const int64_t *n,
+                           const float *lr, const int64_t *step, float beta1,
+                           float beta2, float eps, int32_t eps_inside,
+                           mg_stream_t stream) {
+    MG_REQUIRE(count >= 0 && count <= kAdamMaxTensors,
+               "mg_adam_step_multi: %d tensors, at most %d per launch", count,
+               kAdamMaxTensors);
+    AdamTable tab{};
+    tab.b1 = beta1;
+    tab.b2 = beta2;
+    tab.eps = eps;
+    tab.eps_inside = eps_inside;
+    int64_t blocks = 0;
+    int c = 0;
+    for (int i = 0; i < count; ++i) {
+        MG_REQUIRE(n[i] >= 0, "mg_adam_step_multi: tensor %d has negative size", i);
+        if (n[i] == 0) continue;
+        MG_REQUIRE(p[i] && g[i] && m[i] && v[i],
+                   "mg_adam_step_multi: tensor %d has a null pointer", i);
+        MG_REQUIRE(step[i] >= 1, "mg_adam_step_multi: tensor %d step %lld < 1", i,
+                   (long long)step[i]);
+        AdamTensor &T = tab.t[c++];
+        T.p = p[i]; T.g = g[i]; T.m = m[i]; T.v = v[i]; T.n = n[i];
+        T.block_begin = (int32_t)blocks;
+        T.vec_ok = ((((uintptr_t)p[i]) | ((uintptr_t)g[i]) | ((uintptr_t)m[i]) |
+                     ((uintptr_t)v[i])) & 15) == 0;
+        const double bc1 = 1.0 - std::pow((double)beta1, (double)step[i]);
+        const double bc2 = 1.0 - std::pow((double)beta2, (double)step[i]);
+        if (eps_inside) {
+            T.step_size = (float)((double)lr[i] * std::sqrt(bc2) / bc1);
+            T.inv_sqrt_bc2 = 1.0f;
+        } else {
+            T.step_size = (float)((double)lr[i] / bc1);
+            T.inv_sqrt_bc2 = (float)(1.0 / std::sqrt(bc2));
+        }
+        blocks += ceil_div(n[i], kAdamElemsPerBlock);
+    }
+    tab.count = c;
+    if (c == 0) return MG_OK;
+    MG_REQUIRE(blocks < (1LL << 31), "mg_adam_step_multi: too many elements");
+    TimedScope ts("adam_step", as_stream(stream));
+    adam_multi_kernel<<<(unsigned)blocks, kAdamThreads, 0, as_stream(stream)>>>(tab);
+    MG_LAUNCHED("adam_multi_kernel");
+    return MG_OK;
+}
+
+int32_t mg_adam_step(float *p, const float *g, float *m, float *v, int64_t n,
+                     float lr, float beta1, float beta2, float eps, int64_t step,
+                     mg_stream_t stream) {
+    return mg_adam_step_multi(1, &p, &g, &m, &v, &n, &lr, &step, beta1, beta2,
+                              eps, 0, stream);
+}
+
+int32_t mg_selective_adam_step(int32_t count, float *const *p,
+                               const float *const *g, float *const *m,
+                               float *const *v, float *const *steps,
+                               const int64_t *rows, const int32_t *width,
+                               const float *lr, const uint8_t *visible,
+                               int64_t n_visible, float beta1, float beta2,
+                               float eps, mg_stream_t stream) {
+    MG_REQUIRE(count >= 0 && count <= kAdamMaxTensors,
+               "mg_selective_adam_step: %d tensors, at most %d per launch", count,
+               kAdamMaxTensors);
+    MG_REQUIRE(n_visible >= 0 && (n_visible == 0 || visible),
+               "mg_selective_adam_step: null visibility mask");
+    SelTable tab{};
+    tab.b1 = beta1;
+    tab.b2 = beta2;
+    tab.eps = eps;
+    tab.visible = visible;
+    tab.n_visible = n_visible;
+    int64_t blocks = 0;
+    int c = 0;
+    for (int i = 0; i < count; ++i) {
+        MG_REQUIRE(rows[i] >= 0 && width[i] >= 1,
+                   "mg_selective_adam_step: tensor %d has rows %lld width %d", i,
+                   (long long)rows[i], width[i]);
+        MG_REQUIRE(rows[i] >= n_visible,
+                   "mg_selective_adam_step: tensor %d has %lld rows, fewer than the "
+                   "%lld-entry visibility mask", i, (long long)rows[i],
+                   (long long)n_visible);
+        if (rows[i] == 0) continue;
+        MG_REQUIRE(p[i] && g[i] && m[i] && v[i] && steps[i],
+                   "mg_selective_adam_step: tensor %d has a null pointer", i);
+        SelTensor &T = tab.t[c++];
+        T.p = p[i]; T.g = g[i]; T.m = m[i]; T.v = v[i]; T.steps = steps[i];
+        T.rows = rows[i];
+        T.width = width[i];
+        T.lr = lr[i];
+        T.block_begin = (int32_t)blocks;
+        blocks += ceil_div(rows[i], kSelRows);
+    }
+    tab.count = c;
+    if (c == 0) return MG_OK;
+    MG_REQUIRE(blocks < (1LL << 31), "mg_selective_adam_step: too many rows");
+    TimedScope ts("selective_adam_step", as_stream(stream));
+    selective_adam_kernel<<<(unsigned)blocks, kAdamThreads, 0, as_stream(stream)>>>(tab);
+    MG_LAUNCHED("selective_adam_kernel");
+    return MG_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,328 @@
+// Tile binning: per-Gaussian tile count, exclusive scan, (tile|depth) key
+// emission and tile ranges over the sorted keys.
+//
+// Membership follows metal_gauss/csrc/binning.metal:25-90 and
+// metal_backend.py:149-189: a Gaussian claims tile t when the minimum of its
+// conic's quadratic form over the tile rectangle is below 2 ln(255 opacity),
+// which is exactly the rasteriser's alpha >= 1/255 cutoff, so dropped pairs
+// change no pixel. Keys and order are an integer contract that the CPU oracle
+// reproduces bit for bit, so the float work here is written to be
+// reproducible:
+//   * FP contraction is off in min_q_over_rect (no fused multiply-adds), so
+//     every product and sum rounds exactly as a scalar fp32 CPU evaluation of
+//     the same expression does;
+//   * division is IEEE (hipcc's default correctly rounded fp32 divide);
+//   * the threshold is 2 * log(255 op) taken in double and rounded once to
+//     fp32, i.e. the correctly rounded value, rather than a fast fp32 log
+//     whose last bit differs between libraries.
+#include "mg_common.h"
+
+namespace mg {
+
+constexpr int kBinThreads = 256;
+
+__device__ __noinline__ float min_q_over_rect(float mux, float muy, float ca, float cb,
+                                              float cc, float x0, float x1, float y0,
+                                              float y1) {
+#pragma clang fp contract(off)
+    if (mux >= x0 && mux <= x1 && muy >= y0 && muy <= y1) return 0.0f;
+    const float a = fmaxf(ca, 1e-12f), b = cb, c = fmaxf(cc, 1e-12f);
+    float best = __builtin_inff();
+    for (int e = 0; e < 2; ++e) {            // horizontal edges: minimise over x
+        const float yc = e == 0 ? y0 : y1;
+        const float xs = fminf(fmaxf(mux - b * (yc - muy) / a, x0), x1);
+        const float ex = xs - mux, ey = yc - muy;
+        best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
+    }
+    for (int e = 0; e < 2; ++e) {            // vertical edges: minimise over y
+        const float xc = e == 0 ? x0 : x1;
+        const float ys = fminf(fmaxf(muy - b * (xc - mux) / c, y0), y1);
+        const float ex = xc - mux, ey = ys - muy;
+        best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
+    }
+    return best;
+}
+
+// 2 ln(255 op), correctly rounded to fp32; 0 when the Gaussian can never reach
+// alpha 1/255 (it then claims no tiles).
+__device__ __forceinline__ float level_threshold(float op, bool &live) {
+    const float oa = 255.0f * op;
+    live = oa > 1.0f;
+    return live ? (float)(2.0 * log((double)oa)) : 0.0f;
+}
+
+struct BinArgs {
+    int64_t N;
+    const float *uv, *rxy, *conic, *opac, *depth;
+    const int32_t *valid;
+    int32_t W, H, tile, tiles_x, tiles_y;
+};
+
+// The walk shared by both passes: rows of tiles outer, columns inner, so the
+// emission order is (Gaussian, ty, tx) as in binning.metal:74-77.
+template <bool WRITE>
+__device__ __forceinline__ int bin_walk(const BinArgs &A, int64_t g, uint64_t *keys,
+                                        int32_t *ids, int64_t at) {
+    const float ux = A.uv[2 * g], uy = A.uv[2 * g + 1];
+    const float rx = A.rxy[2 * g], ry = A.rxy[2 * g + 1];
+    const float tf = (float)A.tile;
+    int x0 = (int)floorf((ux - rx) / tf), x1 = (int)floorf((ux + rx) / tf);
+    int y0 = (int)floorf((uy - ry) / tf), y1 = (int)floorf((uy + ry) / tf);
+    x0 = min(max(x0, 0), A.tiles_x - 1);
+    x1 = min(max(x1, 0), A.tiles_x - 1);
+    y0 = min(max(y0, 0), A.tiles_y - 1);
+    y1 = min(max(y1, 0), A.tiles_y - 1);
+    // Without a conic (the circular-bounds caller of metal_backend.py:111-147)
+    // every tile of the rectangle is claimed.
+    const bool test = A.conic != nullptr;
+    float thr = 0.f, ca = 0.f, cb = 0.f, cc = 0.f;
+    if (test) {
+        bool live;
+        thr = level_threshold(A.opac[g], live);
+        if (!live) return 0;
+        ca = A.conic[3 * g]; cb = A.conic[3 * g + 1]; cc = A.conic[3 * g + 2];
+    }
+    uint64_t dbits = 0;
+    if (WRITE) dbits = (uint64_t)__float_as_uint(A.depth[g]);
+    int n = 0;
+    for (int ty = y0; ty <= y1; ++ty) {
+        const float ry0 = (float)(ty * A.tile);
+        const float ry1 = fminf((float)((ty + 1) * A.tile), (float)A.H);
+        for (int tx = x0; tx <= x1; ++tx) {
+            const float rx0 = (float)(tx * A.tile);
+            const float rx1 = fminf((float)((tx + 1) * A.tile), (float)A.W);
+            if (test && min_q_over_rect(ux, uy, ca, cb, cc, rx0, rx1, ry0, ry1) >= thr) continue;
+            if (WRITE) {
+                const uint64_t tid = (uint64_t)(ty * A.tiles_x + tx);
+                keys[at + n] = (tid << 32) | dbits;
+                ids[at + n] = (int32_t)g;
+            }
+            ++n;
+        }
+    }
+    return n;
+}
+
+__global__ __launch_bounds__(kBinThreads) void bin_count_kernel(const BinArgs A, int32_t *counts) {
+    const int64_t g = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
+    if (g >= A.N) return;
+    counts[g] = A.valid[g] == 0 ? 0 : bin_walk<false>(A, g, nullptr, nullptr, 0);
+}
+
+__global__ __launch_bounds__(kBinThreads) void bin_write_kernel(const BinArgs A,
+                                                                const int32_t *offsets,
+                                                                uint64_t *keys, int32_t *ids) {
+    const int64_t g = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
+    if (g >= A.N || A.valid[g] == 0) return;
+    bin_walk<true>(A, g, keys, ids, offsets[g]);
+}
+
+// ------------------------------------------------------------------- scan
+// Three launches: per-chunk sums, a single-workgroup scan of those sums, and
+// a downsweep that rescans each chunk and adds its prefix.
+constexpr int kScanThreads = 256;
+constexpr int kScanItems = 8;
+constexpr int kScanChunk = kScanThreads * kScanItems;   // 2048
+
+__device__ __forceinline__ int64_t wave_incl_scan(int64_t v, int lane) {
+    for (int o = 1; o < 64; o <<= 1) {
+        const int64_t t = __shfl_up(v, o, 64);
+        if (lane >= o) v += t;
+    }
+    return v;
+}
+
+// Exclusive scan of one value per thread over a 256-thread workgroup; the
+// workgroup total is returned through *total.
+__device__ __forceinline__ int64_t block_excl_scan(int64_t v, int64_t *s_wave, int64_t *total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t incl = wave_incl_scan(v, lane);
+    if (lane == 63) s_wave[wave] = incl;
+    __syncthreads();
+    int64_t before = 0, all = 0;
+    for (int w = 0; w < kScanThreads / 64; ++w) {
+        if (w < wave) before += s_wave[w];
+        all += s_wave[w];
+    }
+    __syncthreads();
+    *total = all;
+    return before + incl - v;
+}
+
+__global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const int32_t *in, int64_t n,
+                                                                   int64_t *partials) {
+    __shared__ int64_t s_wave[kScanThreads / 64];
+    const int64_t base = (int64_t)blockIdx.x * kScanChunk;
+    int64_t s = 0;
+#pragma unroll
+    for (int r = 0; r < kScanItems; ++r) {
+        const int64_t i = base + (int64_t)r * kScanThreads + threadIdx.x;
+        if (i < n) s += in[i];
+    }
+    int64_t total;
+    block_excl_scan(s, s_wave, &total);
+    if (threadIdx.x == 0) partials[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(kScanThreads) void scan_partials_kernel(int64_t *partials,
+                                                                     int64_t nparts,
+                                                                     int64_t *total_out) {
+    __shared__ int64_t s_wave[kScanThreads / 64];
+    int64_t carry = 0;
+    for (int64_t c0 = 0; c0 < nparts; c0 += kScanThreads) {
+        const int64_t i = c0 + threadIdx.x;
+        const int64_t v = i < nparts ? partials[i] : 0;
+        int64_t tot;
+        const int64_t ex = block_excl_scan(v, s_wave, &tot);
+        if (i < nparts) partials[i] = carry + ex;
+        carry += tot;
+    }
+    if (threadIdx.x == 0) *total_out = carry;
+}
+
+__global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const int32_t *in, int64_t n,
+                                                                 const int64_t *partials,
+                                                                 int32_t *out) {
+    __shared__ int64_t s_wave[kScanThreads / 64];
+    // Blocked arrangement: thread t owns items [t*8, t*8+8) of the chunk, so
+    // one exclusive scan of the per-thread sums orders them correctly.
+    const int64_t base = (int64_t)blockIdx.x * kScanChunk + (int64_t)threadIdx.x * kScanItems;
+    int32_t v[kScanItems];
+    int64_t s = 0;
+#pragma unroll
+    for (int r = 0; r < kScanItems; ++r) {
+        v[r] = (base + r < n) ? in[base + r] : 0;
+        s += v[r];
+    }
+    int64_t tot;
+    int64_t run = block_excl_scan(s, s_wave, &tot) + partials[blockIdx.x];
+#pragma unroll
+    for (int r = 0; r < kScanItems; ++r) {
+        if (base + r < n) out[base + r] = (int32_t)run;
+        run += v[r];
+    }
+}
+
+// -------------------------------------------------------------- tile ranges
+// offsets[t] = first i with tile(keys[i]) >= t. Each boundary between
+// consecutive keys fills the tiles it skips, so empty tiles get the index of
+// the next non-empty one and offsets[n_tiles] = n.
+__global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t *keys, int64_t n,
+                                                          int32_t n_tiles, int32_t *offsets) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i > n) return;
+    const int64_t prev = i == 0 ? -1 : (int64_t)(keys[i - 1] >> 32);
+    const int64_t cur = i == n ? (int64_t)n_tiles : (int64_t)(keys[i] >> 32);
+    for (int64_t t = prev + 1; t <= cur && t <= n_tiles; ++t) offsets[t] = (int32_t)i;
+}
+
+static int32_t check_bin_args(const char *who, int64_t N, const void *uv, const void *rxy,
+                              const void *conic, const void *opac, const void *valid, int W,
+                              int H, int tile, int tiles_x, int tiles_y) {
+    MG_REQUIRE(N >= 0 && N < (1LL << 31), "%s: N = %lld", who, (long long)N);
+    MG_REQUIRE(W > 0 && H > 0 && tile > 0, "%s: image %dx%d tile %d", who, W, H, tile);
+    MG_REQUIRE(tiles_x == (W + tile - 1) / tile && tiles_y == (H + tile - 1) / tile,
+               "%s: tiles %dx%d do not cover %dx%d at tile %d", who, tiles_x, tiles_y, W, H,
+               tile);
+    MG_REQUIRE((int64_t)tiles_x * tiles_y < (1LL << 31), "%s: too many tiles", who);
+    MG_REQUIRE(N == 0 || (uv && rxy && valid), "%s: null tensor pointer", who);
+    MG_REQUIRE((conic == nullptr) == (opac == nullptr),
+               "%s: conic and opacity must be given together (or both omitted)", who);
+    return MG_OK;
+}
+
+}  // namespace mg
+
+using namespace mg;
+
+extern "C" {
+
+int32_t mg_bin_count(int64_t N, const float *uv, const float *rxy, const float *conic,
+                     const float *opacity, const int32_t *valid, int32_t W, int32_t H,
+                     int32_t tile, int32_t tiles_x, int32_t tiles_y, int32_t *counts,
+                     mg_stream_t stream) {
+    int32_t rc = check_bin_args("mg_bin_count", N, uv, rxy, conic, opacity, valid, W, H, tile,
+                                tiles_x, tiles_y);
+    if (rc != MG_OK) return rc;
+    if (N == 0) return MG_OK;
+    MG_REQUIRE(counts, "mg_bin_count: null counts");
+    BinArgs A{N, uv, rxy, conic, opacity, nullptr, valid, W, H, tile, tiles_x, tiles_y};
+    TimedScope ts("bin_count", as_stream(stream));
+    bin_count_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, as_stream(stream)>>>(
+        A, counts);
+    MG_LAUNCHED("bin_count_kernel");
+    return MG_OK;
+}
+
+int64_t mg_scan_workspace_bytes(int64_t n) {
+    return (ceil_div(n > 0 ? n : 1, kScanChunk) + 1) * (int64_t)sizeof(int64_t);
+}
+
+int32_t mg_exclusive_scan_i32(const int32_t *in, int64_t n, int32_t *out, int64_t *total_dev,
+                              int64_t *total_host, void *workspace, int64_t workspace_bytes,
+                              mg_stream_t stream) {
+    MG_REQUIRE(n >= 0, "mg_exclusive_scan_i32: n = %lld", (long long)n);
+    MG_REQUIRE(total_dev, "mg_exclusive_scan_i32: null total_dev");
+    MG_REQUIRE(workspace_bytes >= mg_scan_workspace_bytes(n) && workspace,
+               "mg_exclusive_scan_i32: workspace %lld bytes, need %lld",
+               (long long)workspace_bytes, (long long)mg_scan_workspace_bytes(n));
+    hipStream_t s = as_stream(stream);
+    int64_t *partials = static_cast<int64_t *>(workspace);
+    const int64_t nparts = ceil_div(n > 0 ? n : 1, kScanChunk);
+    {
+        TimedScope ts("exclusive_scan", s);
+        if (n > 0) {
+            MG_REQUIRE(in && out, "mg_exclusive_scan_i32: null input/output");
+            scan_reduce_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(in, n, partials);
+            MG_LAUNCHED("scan_reduce_kernel");
+        } else {
+            // Zero-length input: a single zero partial gives total 0.
+            scan_reduce_kernel<<<1, kScanThreads, 0, s>>>(in, 0, partials);
+            MG_LAUNCHED("scan_reduce_kernel");
+        }
+        scan_partials_kernel<<<1, kScanThreads, 0, s>>>(partials, nparts, total_dev);
+        MG_LAUNCHED("scan_partials_kernel");
+        if (n > 0) {
+            scan_down_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(in, n, partials, out);
+            MG_LAUNCHED("scan_down_kernel");
+        }
+    }
+    if (total_host) {
+        MG_HIP(hipMemcpyAsync(total_host, total_dev, sizeof(int64_t), hipMemcpyDeviceToHost, s));
+        MG_HIP(hipStreamSynchronize(s));
+    }
+    return MG_OK;
+}
+
+int32_t mg_bin_write(int64_t N, const float *uv, const float *rxy, const float *conic,
+                     const float *opacity, const int32_t *valid, const float *depth,
+                     const int32_t *offsets, int64_t total, int32_t W, int32_t H, int32_t tile,
+                     int32_t tiles_x, int32_t tiles_y, uint64_t *keys, int32_t *ids,
+                     mg_stream_t stream) {
+    int32_t rc = check_bin_args("mg_bin_write", N, uv, rxy, conic, opacity, valid, W, H, tile,
+                                tiles_x, tiles_y);
+    if (rc != MG_OK) return rc;
+    MG_REQUIRE(total >= 0 && total < (1LL << 31), "mg_bin_write: total %lld", (long long)total);
+    if (N == 0 || total == 0) return MG_OK;
+    MG_REQUIRE(depth && offsets && keys && ids, "mg_bin_write: null tensor pointer");
+    BinArgs A{N, uv, rxy, conic, opacity, depth, valid, W, H, tile, tiles_x, tiles_y};
+    TimedScope ts("bin_write", as_stream(stream));
+    bin_write_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, as_stream(stream)>>>(
+        A, offsets, keys, ids);
+    MG_LAUNCHED("bin_write_kernel");
+    return MG_OK;
+}
+
+int32_t mg_tile_ranges(const uint64_t *sorted_keys, int64_t n, int32_t n_tiles,
+                       int32_t *tile_offsets, mg_stream_t stream) {
+    MG_REQUIRE(n >= 0 && n < (1LL << 31), "mg_tile_ranges: n = %lld", (long long)n);
+    MG_REQUIRE(n_tiles >= 1 && tile_offsets, "mg_tile_ranges: n_tiles %d", n_tiles);
+    MG_REQUIRE(n == 0 || sorted_keys, "mg_tile_ranges: null keys");
+    TimedScope ts("tile_ranges", as_stream(stream));
+    tile_ranges_kernel<<<(unsigned)ceil_div(n + 1, 256), 256, 0, as_stream(stream)>>>(
+        sorted_keys, n, n_tiles, tile_offsets);
+    MG_LAUNCHED("tile_ranges_kernel");
+    return MG_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,116 @@
+// Shared host + device helpers for libmgauss. Internal header.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mgauss.h"
+
+namespace mg {
+
+// ---------------------------------------------------------------- host side
+
+// Records a printf-style message as the thread's last error.
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+
+// After a launch: maps hipGetLastError to MG_ERR_LAUNCH with the kernel name.
+int32_t check_launch(const char *kernel);
+
+// Event timing around one launch (active only while mg_timing_enable(1)).
+struct TimedScope {
+    TimedScope(const char *kernel, hipStream_t stream);
+    ~TimedScope();
+    const char *kernel_;
+    hipStream_t stream_;
+    int slot_;
+};
+
+inline hipStream_t as_stream(mg_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Number of XCDs workgroups are spread over, round-robin by workgroup id.
+constexpr int kXcds = 8;
+
+#define MG_REQUIRE(cond, ...)                                                  \
+    do {                                                                       \
+        if (!(cond)) {                                                         \
+            ::mg::set_error(__VA_ARGS__);                                      \
+            return MG_ERR_ARG;                                                 \
+        }                                                                      \
+    } while (0)
+
+#define MG_HIP(call)                                                           \
+    do {                                                                       \
+        hipError_t e_ = (call);                                                \
+        if (e_ != hipSuccess) {                                                \
+            ::mg::set_error("%s failed: %s", #call, hipGetErrorString(e_));    \
+            return MG_ERR_RUNTIME;                                             \
+        }                                                                      \
+    } while (0)
+
+#define MG_LAUNCHED(name)                                                      \
+    do {                                                                       \
+        int32_t rc_ = ::mg::check_launch(name);                                \
+        if (rc_ != MG_OK) return rc_;                                          \
+    } while (0)
+
+// -------------------------------------------------------------- device side
+
+// Maps a linear workgroup id onto a work index so that each XCD (which
+// receives every 8th workgroup) processes one contiguous band of the work.
+// Neighbouring tiles share Gaussians, so keeping them on one XCD keeps the
+// shared records in that XCD's L2. `total` is the real work count; the grid
+// has ceil(total/8)*8 workgroups and the surplus ones get -1.
+__device__ __forceinline__ int xcd_band(int bid, int total) {
+    const int per = (total + kXcds - 1) / kXcds;
+    const int w = (bid % kXcds) * per + bid / kXcds;
+    return w < total ? w : -1;
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint64_t ballot(bool p) {
+    return __builtin_amdgcn_ballot_w64(p);
+}
+
+// Lanes below this one that are set in `mask`.
+__device__ __forceinline__ int rank_in(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+}
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                           ROW_MASK, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wave; the total lands in lane 63.
+// Rows of 16 are reduced with row_shr, then rows are combined with the GFX9
+// row broadcasts (lane 15 -> rows 1,3; lane 31 -> rows 2,3).
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+    v += dpp_f<0x111>(v);        // row_shr:1
+    v += dpp_f<0x112>(v);        // row_shr:2
+    v += dpp_f<0x114>(v);        // row_shr:4
+    v += dpp_f<0x118>(v);        // row_shr:8
+    v += dpp_f<0x142, 0xa>(v);   // row_bcast:15
+    v += dpp_f<0x143, 0xc>(v);   // row_bcast:31
+    return v;
+}
+
+__device__ __forceinline__ float wave_min(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+    for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+}  // namespace mg

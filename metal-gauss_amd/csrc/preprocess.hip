@@ -1,0 +1,632 @@
+// Fused projection + EWA 2D covariance + SnugBox extents + SH colour, forward
+// and analytic backward. One thread per Gaussian, no atomics.
+//
+// Follows metal_gauss/torch_ref.py:31-144 (projection, blur 0.3, Jacobian
+// clamp at 1.3x the half field of view, 3-sigma radius), sh.py:24-62 (real SH
+// basis, degree 0..3, +0.5 and clamp at 0) and preprocess.metal:180-195
+// (SnugBox half-extents and the validity test that feeds binning).
+//
+// Memory: the per-Gaussian inputs are AoS rows (12/16/12/4 bytes plus a 192
+// byte SH row). The small rows are read straight from global memory (64 lanes
+// x 12-16 bytes is a contiguous span per instruction). The SH rows would be a
+// 192-byte stride per lane, so each wave stages its 64 rows through LDS with
+// fully coalesced dword loads and reads them back at an odd row pitch (49
+// floats) that keeps the 64 lanes on distinct banks.
+#include "mg_common.h"
+
+namespace mg {
+
+constexpr int kPreThreads = 128;   // two waves: 2 x 12.25 KB of SH staging
+constexpr int kShPitch = 49;       // LDS floats per staged SH row (48 + 1 pad)
+
+struct Cam {
+    float R[9];      // world->camera rotation, row-major
+    float t[3];
+    float fx, fy, cx, cy;
+    float near_p, far_p, blur, max_r;
+    float cc[3];     // camera centre in world space
+    int32_t W, H, deg;
+};
+
+// Real SH constants (sh.py:11-17), the textbook normalisations.
+constexpr float kC0 = 0.28209479177387814f;
+constexpr float kC1 = 0.4886025119029199f;
+constexpr float kC2[5] = {1.0925484305920792f, -1.0925484305920792f, 0.31539156525252005f,
+                          -1.0925484305920792f, 0.5462742152960396f};
+constexpr float kC3[7] = {-0.5900435899266435f, 2.890611442640554f, -0.4570457994644658f,
+                          0.3731763325901154f, -0.4570457994644658f, 1.445305721320277f,
+                          -0.5900435899266435f};
+
+// Basis values for a unit direction (16 entries; only the first (deg+1)^2 are
+// meaningful).
+__device__ __forceinline__ void sh_basis(int deg, float x, float y, float z, float B[16]) {
+    B[0] = kC0;
+    if (deg < 1) return;
+    B[1] = -kC1 * y;
+    B[2] = kC1 * z;
+    B[3] = -kC1 * x;
+    if (deg < 2) return;
+    const float xx = x * x, yy = y * y, zz = z * z;
+    B[4] = kC2[0] * x * y;
+    B[5] = kC2[1] * y * z;
+    B[6] = kC2[2] * (2.0f * zz - xx - yy);
+    B[7] = kC2[3] * x * z;
+    B[8] = kC2[4] * (xx - yy);
+    if (deg < 3) return;
+    B[9] = kC3[0] * y * (3.0f * xx - yy);
+    B[10] = kC3[1] * x * y * z;
+    B[11] = kC3[2] * y * (4.0f * zz - xx - yy);
+    B[12] = kC3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+    B[13] = kC3[4] * x * (4.0f * zz - xx - yy);
+    B[14] = kC3[5] * z * (xx - yy);
+    B[15] = kC3[6] * x * (xx - 3.0f * yy);
+}
+
+// Accumulates sum_b w_b * dB_b/d(x,y,z) into g (the gradient of a weighted sum
+// of basis values with respect to the unnormalised-then-normalised direction).
+__device__ __forceinline__ void sh_basis_vjp(int deg, float x, float y, float z,
+                                             const float w[16], float g[3]) {
+    g[0] = g[1] = g[2] = 0.f;
+    if (deg < 1) return;
+    g[1] += -kC1 * w[1];
+    g[2] += kC1 * w[2];
+    g[0] += -kC1 * w[3];
+    if (deg < 2) return;
+    const float xx = x * x, yy = y * y, zz = z * z;
+    // B4 = c xy ; B5 = c yz ; B6 = c (2zz - xx - yy) ; B7 = c xz ; B8 = c (xx - yy)
+    g[0] += kC2[0] * y * w[4];
+    g[1] += kC2[0] * x * w[4];
+    g[1] += kC2[1] * z * w[5];
+    g[2] += kC2[1] * y * w[5];
+    g[0] += kC2[2] * (-2.0f * x) * w[6];
+    g[1] += kC2[2] * (-2.0f * y) * w[6];
+    g[2] += kC2[2] * (4.0f * z) * w[6];
+    g[0] += kC2[3] * z * w[7];
+    g[2] += kC2[3] * x * w[7];
+    g[0] += kC2[4] * (2.0f * x) * w[8];
+    g[1] += kC2[4] * (-2.0f * y) * w[8];
+    if (deg < 3) return;
+    // B9 = c y (3xx - yy)
+    g[0] += kC3[0] * (6.0f * x * y) * w[9];
+    g[1] += kC3[0] * (3.0f * xx - 3.0f * yy) * w[9];
+    // B10 = c xyz
+    g[0] += kC3[1] * (y * z) * w[10];
+    g[1] += kC3[1] * (x * z) * w[10];
+    g[2] += kC3[1] * (x * y) * w[10];
+    // B11 = c y (4zz - xx - yy)
+    g[0] += kC3[2] * (-2.0f * x * y) * w[11];
+    g[1] += kC3[2] * (4.0f * zz - xx - 3.0f * yy) * w[11];
+    g[2] += kC3[2] * (8.0f * y * z) * w[11];
+    // B12 = c z (2zz - 3xx - 3yy)
+    g[0] += kC3[3] * (-6.0f * x * z) * w[12];
+    g[1] += kC3[3] * (-6.0f * y * z) * w[12];
+    g[2] += kC3[3] * (6.0f * zz - 3.0f * xx - 3.0f * yy) * w[12];
+    // B13 = c x (4zz - xx - yy)
+    g[0] += kC3[4] * (4.0f * zz - 3.0f * xx - yy) * w[13];
+    g[1] += kC3[4] * (-2.0f * x * y) * w[13];
+    g[2] += kC3[4] * (8.0f * x * z) * w[13];
+    // B14 = c z (xx - yy)
+    g[0] += kC3[5] * (2.0f * x * z) * w[14];
+    g[1] += kC3[5] * (-2.0f * y * z) * w[14];
+    g[2] += kC3[5] * (xx - yy) * w[14];
+    // B15 = c x (xx - 3yy)
+    g[0] += kC3[6] * (3.0f * xx - 3.0f * yy) * w[15];
+    g[1] += kC3[6] * (-6.0f * x * y) * w[15];
+}
+
+// Everything the forward derives from one Gaussian, kept so the backward can
+// re-derive it identically.
+struct Proj {
+    float p[3];          // camera-space centre
+    float zc, izc;
+    bool clx, cly;       // Jacobian evaluation point clamped in x / y
+    float tx, ty;        // clamped evaluation point
+    float qn;            // |q|
+    float q[4];          // normalised wxyz
+    float R[9];          // rotation of the Gaussian, row-major
+    float s[3];
+    float M[9];          // R diag(s)
+    float S[6];          // Sigma = M M^T: xx xy xz yy yz zz
+    float T0[3], T1[3];  // rows of J * Rw
+    float a, b, c;       // dilated 2D covariance
+};
+
+__device__ __forceinline__ void project(const Cam &C, float mx, float my, float mz,
+                                        const float qin[4], const float sin_[3], Proj &P) {
+    P.p[0] = C.R[0] * mx + C.R[1] * my + C.R[2] * mz + C.t[0];
+    P.p[1] = C.R[3] * mx + C.R[4] * my + C.R[5] * mz + C.t[1];
+    P.p[2] = C.R[6] * mx + C.R[7] * my + C.R[8] * mz + C.t[2];
+    P.zc = fmaxf(P.p[2], C.near_p);
+    P.izc = 1.0f / P.zc;
+
+    const float lim_x = 1.3f * (0.5f * (float)C.W / C.fx);
+    const float lim_y = 1.3f * (0.5f * (float)C.H / C.fy);
+    const float txn = P.p[0] / P.zc, tyn = P.p[1] / P.zc;
+    P.clx = (txn < -lim_x) || (txn > lim_x);
+    P.cly = (tyn < -lim_y) || (tyn > lim_y);
+    P.tx = fminf(fmaxf(txn, -lim_x), lim_x) * P.zc;
+    P.ty = fminf(fmaxf(tyn, -lim_y), lim_y) * P.zc;
+
+    const float qn = sqrtf(qin[0] * qin[0] + qin[1] * qin[1] + qin[2] * qin[2] + qin[3] * qin[3]);
+    P.qn = qn;
+    const float iq = 1.0f / fmaxf(qn, 1e-12f);
+    const float w = qin[0] * iq, x = qin[1] * iq, y = qin[2] * iq, z = qin[3] * iq;
+    P.q[0] = w; P.q[1] = x; P.q[2] = y; P.q[3] = z;
+    P.R[0] = 1.f - 2.f * (y * y + z * z); P.R[1] = 2.f * (x * y - w * z); P.R[2] = 2.f * (x * z + w * y);
+    P.R[3] = 2.f * (x * y + w * z); P.R[4] = 1.f - 2.f * (x * x + z * z); P.R[5] = 2.f * (y * z - w * x);
+    P.R[6] = 2.f * (x * z - w * y); P.R[7] = 2.f * (y * z + w * x); P.R[8] = 1.f - 2.f * (x * x + y * y);
+    P.s[0] = sin_[0]; P.s[1] = sin_[1]; P.s[2] = sin_[2];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) P.M[3 * i + j] = P.R[3 * i + j] * P.s[j];
+    const float *M = P.M;
+    P.S[0] = M[0] * M[0] + M[1] * M[1] + M[2] * M[2];
+    P.S[1] = M[0] * M[3] + M[1] * M[4] + M[2] * M[5];
+    P.S[2] = M[0] * M[6] + M[1] * M[7] + M[2] * M[8];
+    P.S[3] = M[3] * M[3] + M[4] * M[4] + M[5] * M[5];
+    P.S[4] = M[3] * M[6] + M[4] * M[7] + M[5] * M[8];
+    P.S[5] = M[6] * M[6] + M[7] * M[7] + M[8] * M[8];
+
+    // J rows: (fx/zc, 0, -fx tx/zc^2) and (0, fy/zc, -fy ty/zc^2); T = J Rw.
+    const float izc2 = P.izc * P.izc;
+    const float j0x = C.fx * P.izc, j0z = -C.fx * P.tx * izc2;
+    const float j1y = C.fy * P.izc, j1z = -C.fy * P.ty * izc2;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        P.T0[k] = j0x * C.R[k] + j0z * C.R[6 + k];
+        P.T1[k] = j1y * C.R[3 + k] + j1z * C.R[6 + k];
+    }
+    const float *S = P.S;
+    const float s00 = S[0], s01 = S[1], s02 = S[2], s11 = S[3], s12 = S[4], s22 = S[5];
+    const float ST0x = s00 * P.T0[0] + s01 * P.T0[1] + s02 * P.T0[2];
+    const float ST0y = s01 * P.T0[0] + s11 * P.T0[1] + s12 * P.T0[2];
+    const float ST0z = s02 * P.T0[0] + s12 * P.T0[1] + s22 * P.T0[2];
+    const float ST1x = s00 * P.T1[0] + s01 * P.T1[1] + s02 * P.T1[2];
+    const float ST1y = s01 * P.T1[0] + s11 * P.T1[1] + s12 * P.T1[2];
+    const float ST1z = s02 * P.T1[0] + s12 * P.T1[1] + s22 * P.T1[2];
+    P.a = P.T0[0] * ST0x + P.T0[1] * ST0y + P.T0[2] * ST0z + C.blur;
+    P.b = P.T0[0] * ST1x + P.T0[1] * ST1y + P.T0[2] * ST1z;
+    P.c = P.T1[0] * ST1x + P.T1[1] * ST1y + P.T1[2] * ST1z + C.blur;
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Stages the SH rows of Gaussians [g0, g0+ng) into S[row*kShPitch + 3*basis +
+// channel], only the first 3*nb floats of each row. Wave-collective.
+__device__ __forceinline__ void stage_sh(float *S, const float *sh, const float *rest,
+                                        bool fused, int64_t g0, int ng, int nb, int lane) {
+    const int kmax = 3 * nb;
+    if (fused) {
+        const float *src = sh + g0 * 48;
+        for (int e = lane; e < ng * 48; e += 64) {
+            const int gi = e / 48, k = e - gi * 48;
+            if (k < kmax) S[gi * kShPitch + k] = src[e];
+        }
+    } else {
+        const float *src = sh + g0 * 3;
+        for (int e = lane; e < ng * 3; e += 64) {
+            const int gi = e / 3, k = e - gi * 3;
+            S[gi * kShPitch + k] = src[e];
+        }
+        if (nb > 1) {
+            const float *src2 = rest + g0 * 45;
+            for (int e = lane; e < ng * 45; e += 64) {
+                const int gi = e / 45, k = e - gi * 45;
+                if (k + 3 < kmax) S[gi * kShPitch + 3 + k] = src2[e];
+            }
+        }
+    }
+}
+
+// Writes S rows back to the gradient layout with coalesced stores.
+__device__ __forceinline__ void unstage_sh(const float *S, float *dsh, float *drest, bool fused,
+                                          int64_t g0, int ng, int lane) {
+    if (fused) {
+        float *dst = dsh + g0 * 48;
+        for (int e = lane; e < ng * 48; e += 64) {
+            const int gi = e / 48, k = e - gi * 48;
+            dst[e] = S[gi * kShPitch + k];
+        }
+    } else {
+        float *dst = dsh + g0 * 3;
+        for (int e = lane; e < ng * 3; e += 64) {
+            const int gi = e / 3, k = e - gi * 3;
+            dst[e] = S[gi * kShPitch + k];
+        }
+        float *dst2 = drest + g0 * 45;
+        for (int e = lane; e < ng * 45; e += 64) {
+            const int gi = e / 45, k = e - gi * 45;
+            dst2[e] = S[gi * kShPitch + 3 + k];
+        }
+    }
+}
+
+struct PreFwdArgs {
+    Cam C;
+    int64_t N;
+    const float *means, *quats, *scales, *sh, *rest, *opac;
+    int32_t fused;
+    float *uv, *conic, *depth, *rxy, *color;
+    int32_t *valid;
+};
+
+__global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFwdArgs A) {
+    __shared__ float s_sh[kPreThreads / 64][64 * kShPitch];
+    const Cam &C = A.C;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t g0 = (int64_t)blockIdx.x * kPreThreads + wave * 64;
+    const int64_t g = g0 + lane;
+    const bool in = g < A.N;
+
+    bool ok = false;
+    float u = 0.f, v = 0.f;
+    if (in) {
+        const float mx = A.means[3 * g], my = A.means[3 * g + 1], mz = A.means[3 * g + 2];
+        const float qv[4] = {A.quats[4 * g], A.quats[4 * g + 1], A.quats[4 * g + 2], A.quats[4 * g + 3]};
+        const float sv[3] = {A.scales[3 * g], A.scales[3 * g + 1], A.scales[3 * g + 2]};
+        Proj P;
+        project(C, mx, my, mz, qv, sv, P);
+        const float z = P.p[2];
+        u = C.fx * P.p[0] / P.zc + C.cx;
+        v = C.fy * P.p[1] / P.zc + C.cy;
+        const float det = P.a * P.c - P.b * P.b;
+        const float dets = fmaxf(det, 1e-12f);
+        const float mid = 0.5f * (P.a + P.c);
+        const float disc = sqrtf(fmaxf(mid * mid - dets, 0.0f));
+        const float lam = fmaxf(mid + disc, 1e-12f);
+        const float radius = 3.0f * sqrtf(lam);
+        // SnugBox: the alpha = 1/255 level set has per-axis half-extent
+        // sqrt(2 ln(255 op)) * sqrt(cov_axis), never more than the 3-sigma
+        // circle (preprocess.metal:180-190).
+        const float op = A.opac[g];
+        const float two_l = 2.0f * logf(fmaxf(255.0f * op, 1.0f));
+        const float rs = sqrtf(two_l);
+        const float rx = fminf(rs * sqrtf(fmaxf(P.a, 0.0f)), radius);
+        const float ry = fminf(rs * sqrtf(fmaxf(P.c, 0.0f)), radius);
+        ok = (z > C.near_p) && (z < C.far_p) && (det > 1e-12f) && (radius < C.max_r) &&
+             (rx > 0.0f) && (ry > 0.0f) && (u + rx > 0.0f) && (u - rx < (float)C.W) &&
+             (v + ry > 0.0f) && (v - ry < (float)C.H);
+        A.uv[2 * g] = u;
+        A.uv[2 * g + 1] = v;
+        A.conic[3 * g] = P.c / dets;
+        A.conic[3 * g + 1] = -P.b / dets;
+        A.conic[3 * g + 2] = P.a / dets;
+        A.depth[g] = z;
+        A.rxy[2 * g] = rx;
+        A.rxy[2 * g + 1] = ry;
+        A.valid[g] = ok ? 1 : 0;
+    }
+
+    if (A.sh == nullptr) return;   // explicit-colour callers: no SH, no colour
+    // Wave-uniform: only waves holding at least one valid Gaussian pay for the
+    // SH rows (sh.py is evaluated only where the rasteriser can look).
+    if (ballot(ok) == 0) {
+        if (in) { A.color[3 * g] = 0.f; A.color[3 * g + 1] = 0.f; A.color[3 * g + 2] = 0.f; }
+        return;
+    }
+    const int nb = (C.deg + 1) * (C.deg + 1);
+    const int ng = (int)min((int64_t)64, A.N - g0);
+    float *S = s_sh[wave];
+    stage_sh(S, A.sh, A.rest, A.fused != 0, g0, ng, nb, lane);
+    wave_lds_sync();
+    if (!in) return;
+    if (!ok) {
+        A.color[3 * g] = 0.f; A.color[3 * g + 1] = 0.f; A.color[3 * g + 2] = 0.f;
+        return;
+    }
+    const float dx = A.means[3 * g] - C.cc[0];
+    const float dy = A.means[3 * g + 1] - C.cc[1];
+    const float dz = A.means[3 * g + 2] - C.cc[2];
+    const float inv = 1.0f / fmaxf(sqrtf(dx * dx + dy * dy + dz * dz), 1e-12f);
+    float B[16];
+    sh_basis(C.deg, dx * inv, dy * inv, dz * inv, B);
+    const float *row = S + lane * kShPitch;
+    float r = 0.f, gg = 0.f, bb = 0.f;
+    for (int i = 0; i < nb; ++i) {
+        r += B[i] * row[3 * i];
+        gg += B[i] * row[3 * i + 1];
+        bb += B[i] * row[3 * i + 2];
+    }
+    A.color[3 * g] = fmaxf(r + 0.5f, 0.0f);
+    A.color[3 * g + 1] = fmaxf(gg + 0.5f, 0.0f);
+    A.color[3 * g + 2] = fmaxf(bb + 0.5f, 0.0f);
+}
+
+struct PreBwdArgs {
+    Cam C;
+    int64_t N;
+    const float *means, *quats, *scales, *sh, *rest;
+    int32_t fused;
+    const float *d_uv, *d_conic, *d_color;
+    const int32_t *valid;
+    float *d_means, *d_quats, *d_scales, *d_sh, *d_rest;
+};
+
+__global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBwdArgs A) {
+    __shared__ float s_sh[kPreThreads / 64][64 * kShPitch];
+    const Cam &C = A.C;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t g0 = (int64_t)blockIdx.x * kPreThreads + wave * 64;
+    const int64_t g = g0 + lane;
+    const bool in = g < A.N;
+
+    float mx = 0.f, my = 0.f, mz = 0.f;
+    if (in) { mx = A.means[3 * g]; my = A.means[3 * g + 1]; mz = A.means[3 * g + 2]; }
+    float dmean[3] = {0.f, 0.f, 0.f};
+
+    // ------------------------------------------------------------ SH branch
+    if (A.d_color != nullptr) {
+        float dcol[3] = {0.f, 0.f, 0.f};
+        if (in) { dcol[0] = A.d_color[3 * g]; dcol[1] = A.d_color[3 * g + 1]; dcol[2] = A.d_color[3 * g + 2]; }
+        const bool need = in && (dcol[0] != 0.f || dcol[1] != 0.f || dcol[2] != 0.f);
+        // Wave-uniform row count of this wave's chunk (0 past the end).
+        const int ng = (int)max((int64_t)0, min((int64_t)64, A.N - g0));
+        const int nb = (C.deg + 1) * (C.deg + 1);
+        float *S = s_sh[wave];
+        const bool wave_needs = ballot(need) != 0;
+        if (wave_needs) {
+            stage_sh(S, A.sh, A.rest, A.fused != 0, g0, ng, nb, lane);
+            wave_lds_sync();
+        }
+        float *row = S + lane * kShPitch;
+        if (need) {
+            const float vx = mx - C.cc[0], vy = my - C.cc[1], vz = mz - C.cc[2];
+            const float n = fmaxf(sqrtf(vx * vx + vy * vy + vz * vz), 1e-12f);
+            const float dx = vx / n, dy = vy / n, dz = vz / n;
+            float B[16];
+            sh_basis(C.deg, dx, dy, dz, B);
+            float pre[3] = {0.5f, 0.5f, 0.5f};
+            for (int i = 0; i < nb; ++i) {
+                pre[0] += B[i] * row[3 * i];
+                pre[1] += B[i] * row[3 * i + 1];
+                pre[2] += B[i] * row[3 * i + 2];
+            }
+            // ReLU gate of colour = max(pre, 0) (torch_ref.py:331).
+            const float dp0 = pre[0] > 0.f ? dcol[0] : 0.f;
+            const float dp1 = pre[1] > 0.f ? dcol[1] : 0.f;
+            const float dp2 = pre[2] > 0.f ? dcol[2] : 0.f;
+            float wts[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) wts[i] = 0.f;
+            for (int i = 0; i < nb; ++i)
+                wts[i] = row[3 * i] * dp0 + row[3 * i + 1] * dp1 + row[3 * i + 2] * dp2;
+            float gd[3];
+            sh_basis_vjp(C.deg, dx, dy, dz, wts, gd);
+            // dir = v/|v|: d v = (I - dir dir^T) d dir / |v|
+            const float dd = dx * gd[0] + dy * gd[1] + dz * gd[2];
+            dmean[0] += (gd[0] - dx * dd) / n;
+            dmean[1] += (gd[1] - dy * dd) / n;
+            dmean[2] += (gd[2] - dz * dd) / n;
+            // Overwrite the staged coefficients with their gradient.
+            for (int i = 0; i < 16; ++i) {
+                const float bi = i < nb ? B[i] : 0.f;
+                row[3 * i] = bi * dp0;
+                row[3 * i + 1] = bi * dp1;
+                row[3 * i + 2] = bi * dp2;
+            }
+        } else if (wave_needs) {
+            for (int i = 0; i < 48; ++i) row[i] = 0.f;
+        }
+        if (wave_needs) {
+            wave_lds_sync();
+            unstage_sh(S, A.d_sh, A.d_rest, A.fused != 0, g0, ng, lane);
+        } else if (ng > 0) {
+            // Whole wave had zero colour gradient: coalesced zero fill.
+            if (A.fused) {
+                for (int e = lane; e < ng * 48; e += 64) A.d_sh[g0 * 48 + e] = 0.f;
+            } else {
+                for (int e = lane; e < ng * 3; e += 64) A.d_sh[g0 * 3 + e] = 0.f;
+                for (int e = lane; e < ng * 45; e += 64) A.d_rest[g0 * 45 + e] = 0.f;
+            }
+        }
+    }
+    if (!in) return;
+
+    // --------------------------------------------------- projection branch
+    if (A.valid[g] != 0) {
+        const float qv[4] = {A.quats[4 * g], A.quats[4 * g + 1], A.quats[4 * g + 2], A.quats[4 * g + 3]};
+        const float sv[3] = {A.scales[3 * g], A.scales[3 * g + 1], A.scales[3 * g + 2]};
+        Proj P;
+        project(C, mx, my, mz, qv, sv, P);
+        const float a = P.a, b = P.b, c = P.c;
+        const float det = a * c - b * b;
+        const float id = 1.0f / fmaxf(det, 1e-12f);
+
+        // conic = (c, -b, a) / det
+        const float k0 = A.d_conic[3 * g], k1 = A.d_conic[3 * g + 1], k2 = A.d_conic[3 * g + 2];
+        const float ddet = -(k0 * c - k1 * b + k2 * a) * id * id;
+        float da = k2 * id + ddet * c;
+        float db = -k1 * id - 2.0f * ddet * b;
+        float dc = k0 * id + ddet * a;
+        if (det <= 1e-12f) da = db = dc = 0.f;
+
+        // a = T0 S T0, b = T0 S T1, c = T1 S T1 (S symmetric).
+        const float *S = P.S;
+        const float s00 = S[0], s01 = S[1], s02 = S[2], s11 = S[3], s12 = S[4], s22 = S[5];
+        const float *T0 = P.T0, *T1 = P.T1;
+        float ST0[3], ST1[3];
+        ST0[0] = s00 * T0[0] + s01 * T0[1] + s02 * T0[2];
+        ST0[1] = s01 * T0[0] + s11 * T0[1] + s12 * T0[2];
+        ST0[2] = s02 * T0[0] + s12 * T0[1] + s22 * T0[2];
+        ST1[0] = s00 * T1[0] + s01 * T1[1] + s02 * T1[2];
+        ST1[1] = s01 * T1[0] + s11 * T1[1] + s12 * T1[2];
+        ST1[2] = s02 * T1[0] + s12 * T1[1] + s22 * T1[2];
+        float dT0[3], dT1[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            dT0[k] = 2.0f * da * ST0[k] + db * ST1[k];
+            dT1[k] = 2.0f * dc * ST1[k] + db * ST0[k];
+        }
+        // Symmetric dSigma = da T0T0' + db (T0T1' + T1T0')/2 + dc T1T1'.
+        float dS[9];
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                dS[3 * i + j] = da * T0[i] * T0[j] + 0.5f * db * (T0[i] * T1[j] + T1[i] * T0[j]) +
+                                dc * T1[i] * T1[j];
+
+        // T0 = j0x Rw0 + j0z Rw2 ; T1 = j1y Rw1 + j1z Rw2.
+        const float dj0x = dT0[0] * C.R[0] + dT0[1] * C.R[1] + dT0[2] * C.R[2];
+        const float dj0z = dT0[0] * C.R[6] + dT0[1] * C.R[7] + dT0[2] * C.R[8];
+        const float dj1y = dT1[0] * C.R[3] + dT1[1] * C.R[4] + dT1[2] * C.R[5];
+        const float dj1z = dT1[0] * C.R[6] + dT1[1] * C.R[7] + dT1[2] * C.R[8];
+        const float izc = P.izc, izc2 = izc * izc, izc3 = izc2 * izc;
+        // j0x = fx/zc, j0z = -fx tx/zc^2, j1y = fy/zc, j1z = -fy ty/zc^2
+        const float dtx = -C.fx * izc2 * dj0z;
+        const float dty = -C.fy * izc2 * dj1z;
+        float dzc = -C.fx * izc2 * dj0x - C.fy * izc2 * dj1y +
+                    2.0f * C.fx * P.tx * izc3 * dj0z + 2.0f * C.fy * P.ty * izc3 * dj1z;
+        // u = fx px/zc + cx, v = fy py/zc + cy
+        const float du = A.d_uv[2 * g], dv = A.d_uv[2 * g + 1];
+        float dpx = C.fx * izc * du;
+        float dpy = C.fy * izc * dv;
+        dzc += -C.fx * P.p[0] * izc2 * du - C.fy * P.p[1] * izc2 * dv;
+        // tx = clamp(px/zc) zc: unclamped -> tx == px; clamped -> +-lim zc.
+        if (!P.clx) dpx += dtx; else dzc += dtx * (P.tx * izc);
+        if (!P.cly) dpy += dty; else dzc += dty * (P.ty * izc);
+        const float dpz = (P.p[2] > C.near_p) ? dzc : 0.0f;
+        // p = Rw m + t
+        dmean[0] += C.R[0] * dpx + C.R[3] * dpy + C.R[6] * dpz;
+        dmean[1] += C.R[1] * dpx + C.R[4] * dpy + C.R[7] * dpz;
+        dmean[2] += C.R[2] * dpx + C.R[5] * dpy + C.R[8] * dpz;
+
+        // Sigma = M M^T: dM = 2 dS M.
+        float dM[9];
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                dM[3 * i + j] = 2.0f * (dS[3 * i] * P.M[j] + dS[3 * i + 1] * P.M[3 + j] +
+                                        dS[3 * i + 2] * P.M[6 + j]);
+        // M = R diag(s)
+        float dsc[3], G[9];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            dsc[j] = dM[j] * P.R[j] + dM[3 + j] * P.R[3 + j] + dM[6 + j] * P.R[6 + j];
+            G[j] = dM[j] * P.s[j];
+            G[3 + j] = dM[3 + j] * P.s[j];
+            G[6 + j] = dM[6 + j] * P.s[j];
+        }
+        A.d_scales[3 * g] = dsc[0];
+        A.d_scales[3 * g + 1] = dsc[1];
+        A.d_scales[3 * g + 2] = dsc[2];
+        // R(q) for unit q = (w,x,y,z): d/dq of sum G_ij R_ij.
+        const float w = P.q[0], x = P.q[1], y = P.q[2], z = P.q[3];
+        const float G00 = G[0], G01 = G[1], G02 = G[2], G10 = G[3], G11 = G[4], G12 = G[5],
+                    G20 = G[6], G21 = G[7], G22 = G[8];
+        const float dw = 2.0f * (x * (G21 - G12) + y * (G02 - G20) + z * (G10 - G01));
+        const float dxq = 2.0f * (w * (G21 - G12) + y * (G01 + G10) + z * (G02 + G20) - 2.0f * x * (G11 + G22));
+        const float dyq = 2.0f * (w * (G02 - G20) + x * (G01 + G10) + z * (G12 + G21) - 2.0f * y * (G00 + G22));
+        const float dzq = 2.0f * (w * (G10 - G01) + x * (G02 + G20) + y * (G12 + G21) - 2.0f * z * (G00 + G11));
+        // through q/|q|
+        const float dotq = w * dw + x * dxq + y * dyq + z * dzq;
+        const float iq = 1.0f / fmaxf(P.qn, 1e-12f);
+        A.d_quats[4 * g] = (dw - w * dotq) * iq;
+        A.d_quats[4 * g + 1] = (dxq - x * dotq) * iq;
+        A.d_quats[4 * g + 2] = (dyq - y * dotq) * iq;
+        A.d_quats[4 * g + 3] = (dzq - z * dotq) * iq;
+    } else {
+        A.d_scales[3 * g] = 0.f; A.d_scales[3 * g + 1] = 0.f; A.d_scales[3 * g + 2] = 0.f;
+        A.d_quats[4 * g] = 0.f; A.d_quats[4 * g + 1] = 0.f;
+        A.d_quats[4 * g + 2] = 0.f; A.d_quats[4 * g + 3] = 0.f;
+    }
+    A.d_means[3 * g] = dmean[0];
+    A.d_means[3 * g + 1] = dmean[1];
+    A.d_means[3 * g + 2] = dmean[2];
+}
+
+static int32_t make_cam(Cam &C, const float *viewmat, float fx, float fy, float cx, float cy,
+                        int32_t W, int32_t H, float near_p, float far_p, float blur,
+                        float max_r, const float *cam_center, int32_t deg, const char *who) {
+    MG_REQUIRE(viewmat != nullptr, "%s: viewmat (host, 16 floats) is null", who);
+    MG_REQUIRE(cam_center != nullptr, "%s: cam_center (host, 3 floats) is null", who);
+    MG_REQUIRE(W > 0 && H > 0, "%s: image %dx%d", who, W, H);
+    MG_REQUIRE(deg >= 0 && deg <= 3, "%s: sh_degree %d not in 0..3", who, deg);
+    for (int i = 0; i < 3; ++i) {
+        for (int j = 0; j < 3; ++j) C.R[3 * i + j] = viewmat[4 * i + j];
+        C.t[i] = viewmat[4 * i + 3];
+        C.cc[i] = cam_center[i];
+    }
+    C.fx = fx; C.fy = fy; C.cx = cx; C.cy = cy;
+    C.near_p = near_p; C.far_p = far_p; C.blur = blur; C.max_r = max_r;
+    C.W = W; C.H = H; C.deg = deg;
+    return MG_OK;
+}
+
+}  // namespace mg
+
+using namespace mg;
+
+extern "C" {
+
+int32_t mg_preprocess_forward(int64_t N, const float *means, const float *quats,
+                              const float *scales, const float *sh, const float *sh_rest,
+                              int32_t sh_fused, const float *opacities, const float *viewmat,
+                              float fx, float fy, float cx, float cy, int32_t W, int32_t H,
+                              float near_plane, float far_plane, float blur, float max_radius,
+                              const float *cam_center, int32_t sh_degree, float *uv,
+                              float *conic, float *depth, float *rxy, int32_t *valid,
+                              float *color, mg_stream_t stream) {
+    PreFwdArgs A{};
+    int32_t rc = make_cam(A.C, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane, blur,
+                          max_radius, cam_center, sh_degree, "mg_preprocess_forward");
+    if (rc != MG_OK) return rc;
+    MG_REQUIRE(N >= 0, "mg_preprocess_forward: N = %lld", (long long)N);
+    if (N == 0) return MG_OK;
+    MG_REQUIRE(means && quats && scales && opacities && uv && conic && depth && rxy && valid,
+               "mg_preprocess_forward: null tensor pointer");
+    MG_REQUIRE(sh == nullptr || color != nullptr,
+               "mg_preprocess_forward: SH given but no colour output");
+    MG_REQUIRE(sh == nullptr || sh_fused || sh_rest != nullptr,
+               "SH must be either one (N,16,3) tensor or (N,1,3)+(N,15,3)");
+    A.N = N;
+    A.means = means; A.quats = quats; A.scales = scales; A.sh = sh;
+    A.rest = sh_rest; A.opac = opacities; A.fused = sh_fused;
+    A.uv = uv; A.conic = conic; A.depth = depth; A.rxy = rxy; A.valid = valid; A.color = color;
+    const int64_t blocks = ceil_div(N, kPreThreads);
+    TimedScope ts("preprocess_forward", as_stream(stream));
+    preprocess_fwd_kernel<<<(unsigned)blocks, kPreThreads, 0, as_stream(stream)>>>(A);
+    MG_LAUNCHED("preprocess_fwd_kernel");
+    return MG_OK;
+}
+
+int32_t mg_preprocess_backward(int64_t N, const float *means, const float *quats,
+                               const float *scales, const float *sh, const float *sh_rest,
+                               int32_t sh_fused, const float *d_uv, const float *d_conic,
+                               const float *d_color, const int32_t *valid, const float *viewmat,
+                               float fx, float fy, float cx, float cy, int32_t W, int32_t H,
+                               float near_plane, float far_plane, float blur, float max_radius,
+                               const float *cam_center, int32_t sh_degree, float *d_means,
+                               float *d_quats, float *d_scales, float *d_sh, float *d_sh_rest,
+                               mg_stream_t stream) {
+    PreBwdArgs A{};
+    int32_t rc = make_cam(A.C, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane, blur,
+                          max_radius, cam_center, sh_degree, "mg_preprocess_backward");
+    if (rc != MG_OK) return rc;
+    MG_REQUIRE(N >= 0, "mg_preprocess_backward: N = %lld", (long long)N);
+    if (N == 0) return MG_OK;
+    MG_REQUIRE(means && quats && scales && d_uv && d_conic && valid && d_means && d_quats &&
+                   d_scales, "mg_preprocess_backward: null tensor pointer");
+    if (d_color) {
+        MG_REQUIRE(sh && d_sh && (sh_fused || (sh_rest && d_sh_rest)),
+                   "SH must be either one (N,16,3) tensor or (N,1,3)+(N,15,3)");
+    }
+    A.N = N;
+    A.means = means; A.quats = quats; A.scales = scales; A.sh = sh; A.rest = sh_rest;
+    A.fused = sh_fused; A.d_uv = d_uv; A.d_conic = d_conic; A.d_color = d_color; A.valid = valid;
+    A.d_means = d_means; A.d_quats = d_quats; A.d_scales = d_scales; A.d_sh = d_sh;
+    A.d_rest = d_sh_rest;
+    const int64_t blocks = ceil_div(N, kPreThreads);
+    TimedScope ts("preprocess_backward", as_stream(stream));
+    preprocess_bwd_kernel<<<(unsigned)blocks, kPreThreads, 0, as_stream(stream)>>>(A);
+    MG_LAUNCHED("preprocess_bwd_kernel");
+    return MG_OK;
+}
+
+}  // extern "C"

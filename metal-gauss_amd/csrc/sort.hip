@@ -1,0 +1,274 @@
+// Stable LSD radix sort of (key, int32 value) pairs, 8-bit digits.
+//
+// Each pass is reduce-then-scan, with no inter-workgroup waiting:
+//   1. upsweep   - every workgroup histograms the digit of its 2048-key tile;
+//   2. scan      - one workgroup per digit scans that digit's counts over the
+//                  tiles (digit-major layout), leaving each tile's base;
+//   3. downsweep - every workgroup ranks its keys stably (wave ballots give
+//                  the rank among equal digits inside a wave; LDS counters
+//                  carry ranks across waves and rounds), sorts the tile
+//                  locally in LDS by digit, and writes each digit's run to
+//                  its global slot so stores come out as contiguous runs.
+// Stability holds because items are ranked in their input order: round r,
+// wave w, lane l is item r*256 + w*64 + l of the tile, and tiles are ranked
+// in tile order by the scan.
+#include "mg_common.h"
+
+namespace mg {
+
+constexpr int kSortThreads = 256;
+constexpr int kSortItems = 8;
+constexpr int kSortTile = kSortThreads * kSortItems;   // 2048 keys per tile
+constexpr int kRadix = 256;
+constexpr int kSortWaves = kSortThreads / 64;
+
+template <typename K>
+__device__ __forceinline__ uint32_t digit_of(K key, int shift, uint32_t mask) {
+    return (uint32_t)(key >> shift) & mask;
+}
+
+template <typename K>
+__global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const K *keys, int64_t n,
+                                                                     int shift, uint32_t mask,
+                                                                     uint32_t *hist,
+                                                                     int64_t ntiles) {
+    __shared__ uint32_t s_h[kSortWaves][kRadix];
+    const int wave = threadIdx.x >> 6;
+    for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads) (&s_h[0][0])[i] = 0;
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+#pragma unroll
+    for (int r = 0; r < kSortItems; ++r) {
+        const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
+        if (i < n) atomicAdd(&s_h[wave][digit_of(keys[i], shift, mask)], 1u);
+    }
+    __syncthreads();
+    for (int d = threadIdx.x; d < kRadix; d += kSortThreads) {
+        uint32_t s = 0;
+#pragma unroll
+        for (int w = 0; w < kSortWaves; ++w) s += s_h[w][d];
+        hist[(int64_t)d * ntiles + blockIdx.x] = s;
+    }
+}
+
+// One workgroup per digit: exclusive scan of hist[d][0..ntiles) in place,
+// digit total to totals[d].
+__global__ __launch_bounds__(kSortThreads) void radix_scan_kernel(uint32_t *hist, int64_t ntiles,
+                                                                  uint32_t *totals) {
+    __shared__ uint32_t s_w[kSortWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t *row = hist + (int64_t)blockIdx.x * ntiles;
+    uint32_t carry = 0;
+    for (int64_t c0 = 0; c0 < ntiles; c0 += kSortThreads) {
+        const int64_t i = c0 + threadIdx.x;
+        const uint32_t v = i < ntiles ? row[i] : 0u;
+        uint32_t incl = v;
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t t = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += t;
+        }
+        if (lane == 63) s_w[wave] = incl;
+        __syncthreads();
+        uint32_t before = 0, all = 0;
+#pragma unroll
+        for (int w = 0; w < kSortWaves; ++w) {
+            if (w < wave) before += s_w[w];
+            all += s_w[w];
+        }
+        __syncthreads();
+        if (i < ntiles) row[i] = carry + before + incl - v;
+        carry += all;
+    }
+    if (threadIdx.x == 0) totals[blockIdx.x] = carry;
+}
+
+template <typename K>
+__global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
+    const K *keys_in, const int32_t *vals_in, K *keys_out, int32_t *vals_out, int64_t n,
+    int shift, uint32_t mask, const uint32_t *hist, int64_t ntiles, const uint32_t *totals) {
+    __shared__ K s_keys[kSortTile];
+    __shared__ int32_t s_vals[kSortTile];
+    __shared__ uint32_t s_base[kRadix];     // global slot of this tile's digit run
+    __shared__ uint32_t s_loc[kRadix];      // start of each digit inside the tile
+    __shared__ uint32_t s_run[kRadix];      // items of each digit ranked so far
+    __shared__ uint32_t s_wc[kSortWaves][kRadix];  // (round+1) << 16 | count
+    __shared__ uint32_t s_w[kSortWaves];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    const int nitems = (int)min((int64_t)kSortTile, n - base);
+
+    // Global digit bases: exclusive scan of the digit totals (one digit per
+    // thread), plus this tile's exclusive prefix within the digit.
+    {
+        const uint32_t v = tid < kRadix ? totals[tid] : 0u;
+        uint32_t incl = v;
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t t = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += t;
+        }
+        if (lane == 63) s_w[wave] = incl;
+        __syncthreads();
+        uint32_t before = 0;
+        for (int w = 0; w < wave; ++w) before += s_w[w];
+        if (tid < kRadix) {
+            s_base[tid] = before + incl - v + hist[(int64_t)tid * ntiles + blockIdx.x];
+            s_run[tid] = 0;
+        }
+        for (int i = tid; i < kSortWaves * kRadix; i += kSortThreads) (&s_wc[0][0])[i] = 0;
+    }
+
+    K key[kSortItems];
+    int32_t val[kSortItems];
+    uint32_t rank[kSortItems];
+#pragma unroll
+    for (int r = 0; r < kSortItems; ++r) {
+        const int idx = r * kSortThreads + tid;
+        if (idx < nitems) {
+            key[r] = keys_in[base + idx];
+            val[r] = vals_in[base + idx];
+        } else {
+            key[r] = 0;
+            val[r] = 0;
+        }
+    }
+    __syncthreads();
+
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+    for (int r = 0; r < kSortItems; ++r) {
+        const bool ok = r * kSortThreads + tid < nitems;
+        const uint32_t d = digit_of(key[r], shift, mask);
+        // Lanes of this wave holding the same digit.
+        uint64_t peers = ballot(ok);
+        for (int b = 0; b < 8; ++b) {
+            const bool bit = (d >> b) & 1u;
+            const uint64_t m = ballot(bit);
+            peers &= bit ? m : ~m;
+        }
+        const uint32_t wrank = (uint32_t)__popcll(peers & lt_mask);
+        const uint32_t tag = (uint32_t)(r + 1) << 16;
+        if (ok && wrank == 0) s_wc[wave][d] = tag | (uint32_t)__popcll(peers);
+        __syncthreads();
+        if (ok) {
+            uint32_t before = s_run[d];
+            for (int w = 0; w < wave; ++w) {
+                const uint32_t e = s_wc[w][d];
+                if ((e & 0xffff0000u) == tag) before += e & 0xffffu;
+            }
+            rank[r] = before + wrank;
+        }
+        __syncthreads();
+        for (int dd = tid; dd < kRadix; dd += kSortThreads) {
+            uint32_t add = 0;
+#pragma unroll
+            for (int w = 0; w < kSortWaves; ++w) {
+                const uint32_t e = s_wc[w][dd];
+                if ((e & 0xffff0000u) == tag) add += e & 0xffffu;
+            }
+            s_run[dd] += add;
+        }
+        __syncthreads();
+    }
+
+    // Local digit starts: exclusive scan of the tile's digit counts.
+    {
+        const uint32_t v = tid < kRadix ? s_run[tid] : 0u;
+        uint32_t incl = v;
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t t = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += t;
+        }
+        if (lane == 63) s_w[wave] = incl;
+        __syncthreads();
+        uint32_t before = 0;
+        for (int w = 0; w < wave; ++w) before += s_w[w];
+        if (tid < kRadix) s_loc[tid] = before + incl - v;
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < kSortItems; ++r) {
+        if (r * kSortThreads + tid < nitems) {
+            const uint32_t d = digit_of(key[r], shift, mask);
+            const uint32_t lp = s_loc[d] + rank[r];
+            if (lp < (uint32_t)kSortTile) {
+                s_keys[lp] = key[r];
+                s_vals[lp] = val[r];
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < nitems; i += kSortThreads) {
+        const K k = s_keys[i];
+        const uint32_t d = digit_of(k, shift, mask);
+        const uint32_t dst = s_base[d] + (uint32_t)i - s_loc[d];
+        if ((int64_t)dst < n) {   // always true for a consistent histogram
+            keys_out[dst] = k;
+            vals_out[dst] = s_vals[i];
+        }
+    }
+}
+
+// Workspace: hist (kRadix * ntiles) + totals (kRadix), uint32.
+inline int64_t sort_ws_bytes(int64_t n) {
+    const int64_t ntiles = ceil_div(n > 0 ? n : 1, kSortTile);
+    return (kRadix * ntiles + kRadix) * (int64_t)sizeof(uint32_t);
+}
+
+template <typename K>
+int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *vals_out,
+                         int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
+                         hipStream_t s, const char *who) {
+    MG_REQUIRE(n >= 0 && n < (1LL << 31), "%s: n = %lld", who, (long long)n);
+    MG_REQUIRE(begin_bit >= 0 && end_bit <= (int)(8 * sizeof(K)) && begin_bit <= end_bit,
+               "%s: bit range [%d, %d)", who, begin_bit, end_bit);
+    MG_REQUIRE(ws && ws_bytes >= sort_ws_bytes(n), "%s: workspace %lld bytes, need %lld", who,
+               (long long)ws_bytes, (long long)sort_ws_bytes(n));
+    if (n == 0) return MG_OK;
+    MG_REQUIRE(keys_in && vals_in && keys_out && vals_out, "%s: null buffer", who);
+    const int64_t ntiles = ceil_div(n, kSortTile);
+    uint32_t *hist = static_cast<uint32_t *>(ws);
+    uint32_t *totals = hist + kRadix * ntiles;
+    K *src_k = keys_in, *dst_k = keys_out;
+    int32_t *src_v = vals_in, *dst_v = vals_out;
+    int passes = 0;
+    TimedScope ts("radix_sort", s);
+    for (int b = begin_bit; b < end_bit; b += 8, ++passes) {
+        const int width = min(8, end_bit - b);
+        const uint32_t mask = (1u << width) - 1u;
+        radix_upsweep_kernel<K><<<(unsigned)ntiles, kSortThreads, 0, s>>>(src_k, n, b, mask, hist,
+                                                                         ntiles);
+        MG_LAUNCHED("radix_upsweep_kernel");
+        radix_scan_kernel<<<kRadix, kSortThreads, 0, s>>>(hist, ntiles, totals);
+        MG_LAUNCHED("radix_scan_kernel");
+        radix_downsweep_kernel<K><<<(unsigned)ntiles, kSortThreads, 0, s>>>(
+            src_k, src_v, dst_k, dst_v, n, b, mask, hist, ntiles, totals);
+        MG_LAUNCHED("radix_downsweep_kernel");
+        K *tk = src_k; src_k = dst_k; dst_k = tk;
+        int32_t *tv = src_v; src_v = dst_v; dst_v = tv;
+    }
+    // After the loop src_* holds the sorted data.
+    if (src_k != keys_out) {
+        MG_HIP(hipMemcpyAsync(keys_out, src_k, n * sizeof(K), hipMemcpyDeviceToDevice, s));
+        MG_HIP(hipMemcpyAsync(vals_out, src_v, n * sizeof(int32_t), hipMemcpyDeviceToDevice, s));
+    }
+    return MG_OK;
+}
+
+}  // namespace mg
+
+using namespace mg;
+
+extern "C" {
+
+int64_t mg_sort_workspace_bytes(int64_t n) { return sort_ws_bytes(n); }
+
+int32_t mg_sort_pairs_u64(uint64_t *keys_in, int32_t *vals_in, uint64_t *keys_out,
+                          int32_t *vals_out, int64_t n, int32_t begin_bit, int32_t end_bit,
+                          void *workspace, int64_t workspace_bytes, mg_stream_t stream) {
+    return radix_sort_pairs<uint64_t>(keys_in, vals_in, keys_out, vals_out, n, begin_bit,
+                                      end_bit, workspace, workspace_bytes, as_stream(stream),
+                                      "mg_sort_pairs_u64");
+}
+
+}  // extern "C"

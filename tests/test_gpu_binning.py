@@ -1,0 +1,208 @@
+"""Tile binning on the GPU against the bit-exact numpy oracle
+(oracle/binning_ref.py): per-Gaussian counts, emitted keys and ids in
+emission order, sorted keys, gauss_ids and tile offsets must be IDENTICAL,
+given identical preprocess outputs (the reference's own framing,
+tests/test_metal_binning.py:44-59). Also the scan and sort primitives on their
+own, and the invariants of tests/test_metal_binning.py:62-104."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import binning_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def ref_scene(N=20000, W=240, H=320, seed=1):
+    """tests/test_metal_binning.py:20-31: rotated, elongated splats at z ~ 3."""
+    g = torch.Generator().manual_seed(seed)
+    means = torch.randn(N, 3, generator=g) * 0.5
+    means[:, 2] += 3.0
+    return dict(means=means, quats=torch.randn(N, 4, generator=g),
+                scales=torch.rand(N, 3, generator=g) * 0.08 + 0.005,
+                op=torch.rand(N, generator=g) * 0.9 + 0.05,
+                sh=torch.randn(N, 16, 3, generator=g) * 0.3, W=W, H=H, f=200.0)
+
+
+def gpu_preprocess(s, dev, viewmat=None):
+    from metal_gauss_amd.backend import _PreprocessMetal, _camera
+
+    W, H, f = s["W"], s["H"], s["f"]
+    K = torch.tensor([[f, 0, W / 2], [0, f, H / 2], [0, 0, 1.0]])
+    vm = torch.eye(4) if viewmat is None else viewmat
+    fx, fy, cx, cy, vm_h, cc = _camera(K, vm)
+    with torch.no_grad():
+        return _PreprocessMetal.apply(
+            s["means"].to(dev), s["quats"].to(dev), s["scales"].to(dev), s["sh"].to(dev), None,
+            s["op"].to(dev), vm_h, fx, fy, cx, cy, W, H, 0.01, 100.0, 0.3, float(max(W, H)),
+            cc, 3)
+
+
+def run_both(s, dev, tile, ellipse=True):
+    from metal_gauss_amd.backend import _bin
+
+    uv, conic, depth, rxy, valid, _ = gpu_preprocess(s, dev)
+    op = s["op"].to(dev)
+    gids, offs, tx, skeys = _bin(uv, rxy, depth, valid, conic if ellipse else None,
+                                 op if ellipse else None, s["W"], s["H"], tile)
+    cpu = [t.cpu().numpy() for t in (uv, rxy, conic, op, valid, depth)]
+    rids, roffs, rtx, rkeys = binning_ref.build_tile_lists(
+        cpu[0], cpu[1], cpu[2], cpu[3], cpu[4], cpu[5], s["W"], s["H"], tile, ellipse=ellipse)
+    return (gids.cpu().numpy(), offs.cpu().numpy(), tx, skeys.cpu().numpy().view(np.uint64)), \
+        (rids, roffs, rtx, rkeys)
+
+
+@pytest.mark.parametrize("tile", [8, 12, 16, 32])
+def test_tile_lists_bit_exact(dev, tile):
+    gpu, ref = run_both(ref_scene(), dev, tile)
+    assert gpu[2] == ref[2]
+    assert np.array_equal(gpu[3], ref[3]), "sorted keys differ"
+    assert np.array_equal(gpu[0], ref[0]), "gauss_ids (sorted order incl. ties) differ"
+    assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
+
+
+def test_rect_only_lists_bit_exact_and_longer(dev):
+    s = ref_scene(seed=3)
+    gpu_r, ref_r = run_both(s, dev, 16, ellipse=False)
+    assert np.array_equal(gpu_r[3], ref_r[3]) and np.array_equal(gpu_r[0], ref_r[0])
+    assert np.array_equal(gpu_r[1], ref_r[1])
+    gpu_e, _ = run_both(s, dev, 16, ellipse=True)
+    assert gpu_e[0].size < gpu_r[0].size, "the ellipse test removed nothing"
+
+
+def test_counts_and_emission_order_bit_exact(dev):
+    """The unsorted (key, id) stream in (Gaussian, row, column) order."""
+    from metal_gauss_amd import _lib
+
+    s = ref_scene(seed=2)
+    uv, conic, depth, rxy, valid, _ = gpu_preprocess(s, dev)
+    op = s["op"].to(dev)
+    W, H, tile = s["W"], s["H"], 16
+    tx, ty = math.ceil(W / tile), math.ceil(H / tile)
+    lib = _lib.load()
+    N = uv.shape[0]
+    counts = torch.empty(N, dtype=torch.int32, device=dev)
+    st = _lib.stream(uv)
+    _lib.check(lib.mg_bin_count(N, uv.data_ptr(), rxy.data_ptr(), conic.data_ptr(), op.data_ptr(),
+                                valid.data_ptr(), W, H, tile, tx, ty, counts.data_ptr(), st))
+    offs = torch.empty(N, dtype=torch.int32, device=dev)
+    ws = torch.empty(lib.mg_scan_workspace_bytes(N), dtype=torch.uint8, device=dev)
+    tot = torch.empty(1, dtype=torch.int64, device=dev)
+    _lib.check(lib.mg_exclusive_scan_i32(counts.data_ptr(), N, offs.data_ptr(), tot.data_ptr(),
+                                         None, ws.data_ptr(), ws.numel(), st))
+    total = int(tot.item())
+    keys = torch.empty(total, dtype=torch.int64, device=dev)
+    ids = torch.empty(total, dtype=torch.int32, device=dev)
+    _lib.check(lib.mg_bin_write(N, uv.data_ptr(), rxy.data_ptr(), conic.data_ptr(), op.data_ptr(),
+                                valid.data_ptr(), depth.data_ptr(), offs.data_ptr(), total, W, H,
+                                tile, tx, ty, keys.data_ptr(), ids.data_ptr(), st))
+    cpu = [t.cpu().numpy() for t in (uv, rxy, conic, op, valid, depth)]
+    rkeys, rids, rcounts = binning_ref.emit_pairs(*cpu, W, H, tile)
+    assert np.array_equal(counts.cpu().numpy(), rcounts)
+    assert np.array_equal(offs.cpu().numpy(), np.cumsum(rcounts) - rcounts)
+    assert np.array_equal(keys.cpu().numpy().view(np.uint64), rkeys)
+    assert np.array_equal(ids.cpu().numpy(), rids)
+
+
+def test_offsets_are_monotonic_and_complete(dev):
+    gpu, _ = run_both(ref_scene(seed=2), dev, 16)
+    o = gpu[1].astype(np.int64)
+    assert o[0] == 0 and o[-1] == gpu[0].size and (o[1:] >= o[:-1]).all()
+
+
+def test_all_invalid_scene_gives_empty_lists(dev):
+    """tests/test_metal_binning.py:81-104: everything behind the camera."""
+    N = 128
+    s = dict(means=torch.zeros(N, 3), quats=torch.tensor([[1.0, 0, 0, 0]]).repeat(N, 1),
+             scales=torch.full((N, 3), 0.01), op=torch.full((N,), 0.5),
+             sh=torch.zeros(N, 16, 3), W=64, H=64, f=100.0)
+    s["means"][:, 2] = -5.0
+    gpu, _ = run_both(s, dev, 16)
+    assert gpu[0].size == 0 and int(gpu[1][-1]) == 0 and gpu[1].shape == (17,)
+
+
+def test_config2_scale_bit_exact(dev):
+    """Full BASELINE configs[1] scene and camera: 300k Gaussians at 800x800."""
+    from metal_gauss_amd import scenes
+
+    sc, cam, _ = scenes.config2()
+    m, q, sca, op, sh = sc.activated()
+    s = dict(means=m, quats=q, scales=sca, op=op, sh=sh, W=cam.W, H=cam.H,
+             f=float(cam.K[0, 0]))
+    from metal_gauss_amd.backend import _bin, _camera, _PreprocessMetal
+
+    fx, fy, cx, cy, vm_h, cc = _camera(cam.K, cam.viewmat)
+    with torch.no_grad():
+        uv, conic, depth, rxy, valid, _ = _PreprocessMetal.apply(
+            m.to(dev), q.to(dev), sca.to(dev), sh.to(dev), None, op.to(dev), vm_h, fx, fy, cx, cy,
+            cam.W, cam.H, 0.01, 100.0, 0.3, float(max(cam.W, cam.H)), cc, 3)
+    gids, offs, tx, skeys = _bin(uv, rxy, depth, valid, conic, op.to(dev), cam.W, cam.H, 16)
+    cpu = [t.cpu().numpy() for t in (uv, rxy, conic, op, valid, depth)]
+    rids, roffs, _, rkeys = binning_ref.build_tile_lists(*cpu, cam.W, cam.H, 16)
+    print(f"config 2: {int(valid.sum())} valid of {m.shape[0]}, {rids.size} intersections")
+    assert np.array_equal(skeys.cpu().numpy().view(np.uint64), rkeys)
+    assert np.array_equal(gids.cpu().numpy(), rids)
+    assert np.array_equal(offs.cpu().numpy(), roffs)
+
+
+# ------------------------------------------------------------- primitives
+
+@pytest.mark.parametrize("n", [1, 7, 2047, 2048, 2049, 100_003])
+@pytest.mark.parametrize("bits", [(0, 44), (0, 40), (0, 64), (8, 20)])
+def test_radix_sort_is_stable_and_exact(dev, n, bits):
+    from metal_gauss_amd import _lib
+
+    lib = _lib.load()
+    g = np.random.default_rng(n * 131 + bits[1])
+    # Few distinct values so that ties are everywhere.
+    keys = g.integers(0, 2 ** 63, size=n, dtype=np.int64)
+    keys = np.where(g.random(n) < 0.5, keys % 977, keys)
+    lo, hi = bits
+    mask = np.uint64(((1 << (hi - lo)) - 1) << lo) if hi - lo < 64 else np.uint64(2 ** 64 - 1)
+    want_order = np.argsort(keys.view(np.uint64) & mask, kind="stable")
+    kin = torch.from_numpy(keys).to(dev)
+    vin = torch.arange(n, dtype=torch.int32, device=dev)
+    kout = torch.empty_like(kin)
+    vout = torch.empty_like(vin)
+    ws = torch.empty(lib.mg_sort_workspace_bytes(n), dtype=torch.uint8, device=dev)
+    _lib.check(lib.mg_sort_pairs_u64(kin.data_ptr(), vin.data_ptr(), kout.data_ptr(),
+                                     vout.data_ptr(), n, lo, hi, ws.data_ptr(), ws.numel(),
+                                     _lib.stream(kin)))
+    assert np.array_equal(vout.cpu().numpy(), want_order.astype(np.int32))
+    assert np.array_equal(kout.cpu().numpy(), keys[want_order])
+
+
+@pytest.mark.parametrize("n", [1, 2048, 2049, 1_000_003])
+def test_exclusive_scan(dev, n):
+    from metal_gauss_amd import _lib
+
+    lib = _lib.load()
+    counts = torch.randint(0, 40, (n,), dtype=torch.int32, generator=torch.Generator().manual_seed(n))
+    want = np.cumsum(counts.numpy().astype(np.int64)) - counts.numpy()
+    c = counts.to(dev)
+    out = torch.empty_like(c)
+    tot = torch.empty(1, dtype=torch.int64, device=dev)
+    host = torch.zeros(1, dtype=torch.int64, pin_memory=True)
+    ws = torch.empty(lib.mg_scan_workspace_bytes(n), dtype=torch.uint8, device=dev)
+    _lib.check(lib.mg_exclusive_scan_i32(c.data_ptr(), n, out.data_ptr(), tot.data_ptr(),
+                                         host.data_ptr(), ws.data_ptr(), ws.numel(),
+                                         _lib.stream(c)))
+    assert np.array_equal(out.cpu().numpy(), want.astype(np.int32))
+    assert int(host[0]) == int(counts.sum()) == int(tot.item())
+
+
+def test_tile_ranges_fill_empty_tiles(dev):
+    from metal_gauss_amd import _lib
+
+    lib = _lib.load()
+    tiles = np.array([0, 0, 3, 3, 3, 7, 9, 9], dtype=np.uint64)
+    keys = torch.from_numpy(((tiles << np.uint64(32)) | np.uint64(5)).view(np.int64)).to(dev)
+    offs = torch.empty(12, dtype=torch.int32, device=dev)
+    _lib.check(lib.mg_tile_ranges(keys.data_ptr(), 8, 11, offs.data_ptr(), _lib.stream(keys)))
+    want = np.searchsorted(tiles.astype(np.int64), np.arange(12))
+    assert np.array_equal(offs.cpu().numpy(), want)

@@ -1,0 +1,184 @@
+"""The rasteriser kernels in isolation against the C restatement of their
+per-pixel contract (oracle/raster_seq.c), on identical inputs and tile lists.
+
+Bars: images within 1e-4 max-abs, gradients within
+1e-3 relative L2. Pixels the oracle marks ill-conditioned (an alpha within
+1e-5 relative of the 1/255 cutoff, or the stopping T within 1e-5 of t_min,
+where one ulp of exp flips a discrete decision) are counted and bounded
+separately rather than compared at 1e-4."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import intrinsics, rel_l2, scene
+from oracle import raster_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def prepare(n, seed, W, H, tile, dev, elongate=False, sh=False):
+    from metal_gauss_amd.backend import _PreprocessMetal, _camera, build_tile_lists_metal
+
+    s = scene(n=n, seed=seed)
+    if elongate:
+        s["scales"] = s["scales"] * torch.tensor([4.0, 0.5, 1.0])
+    fx, fy, cx, cy, vm_h, cc = _camera(intrinsics(W, H), torch.eye(4))
+    with torch.no_grad():
+        uv, conic, depth, rxy, valid = _PreprocessMetal.apply(
+            s["means"].to(dev), s["quats"].to(dev), s["scales"].to(dev), None, None,
+            s["opacities"].to(dev), vm_h, fx, fy, cx, cy, W, H, 0.01, 100.0, 0.3,
+            float(max(W, H)), cc, 3)
+        op = s["opacities"].to(dev)
+        col = s["colors"].to(dev)
+        gids, offs, tx = build_tile_lists_metal(uv, rxy, depth, valid, conic, op, W, H, tile)
+    return uv, conic, op, col, gids, offs, tx
+
+
+def gpu_forward(args, W, H, tile, t_min):
+    from metal_gauss_amd import _lib
+
+    uv, conic, op, col, gids, offs, tx = args
+    dev = uv.device
+    rgb = torch.empty(H, W, 3, device=dev)
+    alpha = torch.empty(H, W, device=dev)
+    T = torch.empty(H, W, device=dev)
+    stop = torch.empty(H, W, dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    _lib.check(lib.mg_rasterize_forward(uv.shape[0], uv.data_ptr(), conic.data_ptr(),
+                                        op.data_ptr(), col.data_ptr(), gids.data_ptr(),
+                                        offs.data_ptr(), W, H, tile, tx, t_min, rgb.data_ptr(),
+                                        alpha.data_ptr(), T.data_ptr(), stop.data_ptr(),
+                                        _lib.stream(uv)))
+    return rgb, alpha, T, stop
+
+
+def gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile, absgrad=True):
+    from metal_gauss_amd import _lib
+
+    uv, conic, op, col, gids, offs, tx = args
+    _, _, T, stop = fwd
+    N, dev = uv.shape[0], uv.device
+    outs = [torch.full((N, 2), 7.0, device=dev), torch.full((N, 3), 7.0, device=dev),
+            torch.full((N,), 7.0, device=dev), torch.full((N, 3), 7.0, device=dev),
+            torch.full((N,), 7.0, device=dev) if absgrad else None]
+    lib = _lib.load()
+    _lib.check(lib.mg_rasterize_backward(
+        N, uv.data_ptr(), conic.data_ptr(), op.data_ptr(), col.data_ptr(), gids.data_ptr(),
+        offs.data_ptr(), T.data_ptr(), stop.data_ptr(), grad_rgb.data_ptr(),
+        grad_alpha.data_ptr(), W, H, tile, tx, *[o.data_ptr() if o is not None else None
+                                                   for o in outs], _lib.stream(uv)))
+    return outs
+
+
+def np_(t):
+    return t.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize("t_min", [0.0, 1e-4])
+@pytest.mark.parametrize("tile", [8, 12, 16, 32])
+def test_forward_matches_contract(dev, tile, t_min):
+    W, H = 100, 63
+    args = prepare(600, 17, W, H, tile, dev, elongate=True)
+    rgb, alpha, T, stop = gpu_forward(args, W, H, tile, t_min)
+    r = raster_ref.forward(*[np_(a) for a in args[:6]], W, H, tile, t_min)
+    amb = r[4]
+    ok = ~amb
+    assert amb.mean() < 1e-3, f"{amb.sum()} ill-conditioned pixels"
+    assert np.abs(np_(rgb) - r[0])[ok].max() < 1e-4
+    assert np.abs(np_(alpha) - r[1])[ok].max() < 1e-4
+    assert np.abs(np_(T) - r[2])[ok].max() < 1e-4
+    assert (np_(stop) == r[3])[ok].all(), "stop indices differ"
+
+
+@pytest.mark.parametrize("tile", [8, 12, 16, 32])
+def test_backward_matches_contract(dev, tile):
+    W, H = 100, 63
+    args = prepare(600, 19, W, H, tile, dev, elongate=True)
+    fwd = gpu_forward(args, W, H, tile, 1e-4)
+    g = torch.Generator().manual_seed(3)
+    grad_rgb = torch.randn(H, W, 3, generator=g).to(dev)
+    grad_alpha = torch.randn(H, W, generator=g).to(dev)
+    outs = gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile)
+    ref = raster_ref.backward(*[np_(a) for a in args[:6]], np_(fwd[2]), np_(fwd[3]),
+                              np_(grad_rgb), np_(grad_alpha), W, H, tile)
+    for name, a, b in zip(("d_uv", "d_conic", "d_opacity", "d_color", "d_absuv"), outs, ref):
+        assert torch.isfinite(a).all(), name
+        assert rel_l2(np_(a), b) < 1e-3, f"tile {tile}: {name} rel L2 {rel_l2(np_(a), b):.2e}"
+
+
+def test_absgrad_is_at_least_the_norm_of_the_summed_gradient(dev):
+    """tests/test_absgrad.py:60-76: sum |d_uv_px| >= |sum d_uv_px|."""
+    W, H, tile = 96, 64, 16
+    args = prepare(300, 0, W, H, tile, dev)
+    fwd = gpu_forward(args, W, H, tile, 1e-4)
+    grad_rgb = (2.0 * fwd[0]).contiguous()           # d/drgb of mean(rgb^2) up to 1/n
+    grad_alpha = torch.zeros(H, W, device=dev)
+    d_uv, _, _, _, d_abs = gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile)
+    slack = d_abs - d_uv.norm(dim=1)
+    assert (d_abs >= 0).all() and d_abs.sum() > 0
+    assert (slack >= -1e-4 * d_abs.max()).all()
+    assert (slack > 1e-6 * d_abs.max()).any()
+
+
+def test_gradients_are_overwritten_not_accumulated(dev):
+    """The backward zero-fills its outputs (they arrive holding 7s)."""
+    W, H, tile = 48, 32, 16
+    args = prepare(50, 1, W, H, tile, dev)
+    args = (args[0], args[1], args[2], args[3], args[4][:0].contiguous(),
+            torch.zeros_like(args[5]), args[6])             # empty lists
+    fwd = gpu_forward(args, W, H, tile, 1e-4)
+    assert float(fwd[1].abs().max()) == 0.0 and float(fwd[2].min()) == 1.0
+    outs = gpu_backward(args, fwd, torch.ones(H, W, 3, device=dev), torch.ones(H, W, device=dev),
+                        W, H, tile)
+    for o in outs:
+        assert float(o.abs().max()) == 0.0
+
+
+def test_oversized_tile_is_refused(dev):
+    """tests/test_metal.py:205-213: one tile is one workgroup."""
+    from metal_gauss_amd import render
+
+    s = scene(n=50)
+    with pytest.raises(RuntimeError, match="threads per threadgroup"):
+        render(s["means"].to(dev), s["quats"].to(dev), s["scales"].to(dev),
+               s["opacities"].to(dev), None, intrinsics(96, 64), torch.eye(4), 96, 64,
+               colors=s["colors"].to(dev), tile=64)
+
+
+def test_config2_scale_forward_and_backward(dev):
+    """BASELINE configs[1] at full size: 300k Gaussians, 800x800, SH 3, white
+    background; the raster kernels against the contract on the real lists."""
+    from metal_gauss_amd import scenes
+    from metal_gauss_amd.backend import _PreprocessMetal, _camera, build_tile_lists_metal
+
+    sc, cam, _ = scenes.config2()
+    m, q, sca, op, sh = (t.to(dev) for t in sc.activated())
+    fx, fy, cx, cy, vm_h, cc = _camera(cam.K, cam.viewmat)
+    W, H, tile = cam.W, cam.H, 16
+    with torch.no_grad():
+        uv, conic, depth, rxy, valid, col = _PreprocessMetal.apply(
+            m, q, sca, sh, None, op, vm_h, fx, fy, cx, cy, W, H, 0.01, 100.0, 0.3,
+            float(max(W, H)), cc, 3)
+        gids, offs, tx = build_tile_lists_metal(uv, rxy, depth, valid, conic, op, W, H, tile)
+    args = (uv, conic, op, col, gids, offs, tx)
+    fwd = gpu_forward(args, W, H, tile, 1e-4)
+    r = raster_ref.forward(*[np_(a) for a in args[:6]], W, H, tile, 1e-4)
+    ok = ~r[4]
+    print(f"config 2: {gids.numel()} intersections, {r[4].sum()} ill-conditioned pixels")
+    assert r[4].mean() < 1e-3
+    assert np.abs(np_(fwd[0]) - r[0])[ok].max() < 1e-4
+    assert np.abs(np_(fwd[1]) - r[1])[ok].max() < 1e-4
+    target = scenes.config2_target().to(dev)
+    img = fwd[0] + (1.0 - fwd[1])[..., None]                # white background
+    grad_rgb = (torch.sign(img - target) / img.numel()).contiguous()
+    grad_alpha = (-(grad_rgb.sum(dim=-1))).contiguous()     # through the blend
+    outs = gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile)
+    ref = raster_ref.backward(*[np_(a) for a in args[:6]], np_(fwd[2]), np_(fwd[3]),
+                              np_(grad_rgb), np_(grad_alpha), W, H, tile)
+    for name, a, b in zip(("d_uv", "d_conic", "d_opacity", "d_color"), outs, ref):
+        assert rel_l2(np_(a), b) < 1e-3, f"{name} rel L2 {rel_l2(np_(a), b):.2e}"
