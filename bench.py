@@ -1,0 +1,328 @@
+"""Benchmark: one full training step of the splatting hot path on one MI355X.
+
+Workload ("config 4"): 1,000,000 Gaussians with SH
+degree 3, 800x800 views from 100 seeded cameras on a radius-4 sphere, loss
+0.8 L1 + 0.2 (1 - SSIM) against smooth random targets, then fused Adam over the
+six parameter groups. A step is: activations, render forward (preprocess,
+binning, raster), loss, backward (SSIM, raster, preprocess), Adam. Inputs and
+targets are resident in HBM before timing.
+
+Prints ONE JSON line with the driver's fields plus:
+  roofline      the dominant kernel's algorithmic bytes per launch / its mean
+                launch time (HIP events on its own stream, inside the library)
+                against MI355X's 8 TB/s HBM peak;
+  cpu_baseline  the CPU oracle (oracle/render_ref.py, a restatement of the
+                reference's torch renderer, + torch.optim.Adam) on a bounded
+                sample of the same step, scaled to full-step steps/s;
+  kernels       mean ms per launch of every library kernel in the step.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "train steps/sec & fwd+bwd ms at 1M Gaussians 800×800 SH3; % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+
+# Kernels timed by the library (names used in mg_timing_query).
+KERNELS = ["preprocess_forward", "bin_count", "exclusive_scan", "bin_write", "radix_sort",
+           "tile_ranges", "rasterize_forward", "rasterize_backward", "preprocess_backward",
+           "ssim_fused_forward", "ssim_fused_backward", "adam_step"]
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--gaussians", type=int, default=1_000_000)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-only", action="store_true", help="time only the CPU baseline")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="first copy this many MiB device-to-device 3 times (a plain copy of "
+                         "known size, to calibrate the FETCH_SIZE / WRITE_SIZE counters)")
+    return ap.parse_args()
+
+
+def copy_calibration(mib):
+    import torch
+
+    n = mib * (1 << 18)                       # floats
+    src = torch.ones(n, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+class Step:
+    """The config-4 training step on the GPU."""
+
+    def __init__(self, n, dev):
+        import torch
+
+        from metal_gauss_amd import FusedAdam, gaussian_kernel, scenes
+
+        sc, cams, self.bg = scenes.config4(n)
+        sc = sc.to(dev)
+        self.cams = cams
+        self.p = {k: getattr(sc, k).clone().requires_grad_(True)
+                  for k in ("means", "log_scales", "quats", "logit_opac", "sh_dc", "sh_rest")}
+        lr = {name: l for name, _, l in scenes.config3_groups()}
+        self.opt = FusedAdam([
+            {"params": [self.p["means"]], "lr": lr["means"]},
+            {"params": [self.p["log_scales"]], "lr": lr["scales"]},
+            {"params": [self.p["quats"]], "lr": lr["quats"]},
+            {"params": [self.p["logit_opac"]], "lr": lr["opac"]},
+            {"params": [self.p["sh_dc"]], "lr": lr["sh_dc"]},
+            {"params": [self.p["sh_rest"]], "lr": lr["sh_rest"]},
+        ], eps=1e-15)
+        self.targets = [scenes.config4_target(v).to(dev) for v in range(len(cams))]
+        self.window = gaussian_kernel(device=dev, groups=15)
+        g = torch.Generator().manual_seed(3)
+        self.order = torch.randperm(len(cams), generator=g).tolist()
+        self.k = 0
+        self.last_isect = 0
+
+    def __call__(self, adam=True):
+        import torch
+
+        from metal_gauss_amd import render, ssim
+
+        v = self.order[self.k % len(self.order)]
+        self.k += 1
+        cam, gt, p = self.cams[v], self.targets[v], self.p
+        rgb, alpha, info = render(p["means"], p["quats"], torch.exp(p["log_scales"]),
+                                  torch.sigmoid(p["logit_opac"]), p["sh_dc"], cam.K, cam.viewmat,
+                                  cam.W, cam.H, sh_degree=3, sh_rest=p["sh_rest"],
+                                  background=self.bg)
+        l1 = (rgb - gt).abs().mean()
+        loss = 0.8 * l1 + 0.2 * (1.0 - ssim(rgb, gt, self.window))
+        self.opt.zero_grad(set_to_none=True)
+        loss.backward()
+        if adam:
+            self.opt.step()
+        self.last_isect = info["isect_total"]
+        self.last_valid = info["valid_mask"]
+        return loss
+
+
+def algorithmic_bytes(kernel, N, I, P, T, f_valid, n_floats):
+    """HBM bytes one launch must move, each tensor read or written once."""
+    return {
+        "preprocess_forward": (92 + 192 * f_valid) * N,
+        "preprocess_backward": (308 + 192 * f_valid) * N,
+        "bin_count": 40 * N,
+        "exclusive_scan": 8 * N,
+        "bin_write": 44 * N + 12 * I,
+        "radix_sort": 24 * I,
+        "tile_ranges": 8 * I + 4 * (T + 1),
+        "rasterize_forward": 40 * I + 24 * P + 8 * T,
+        "rasterize_backward": 40 * I + 24 * P + 36 * N,
+        "ssim_fused_forward": 60 * P,
+        "ssim_fused_backward": 72 * P,
+        "adam_step": 28 * n_floats,
+    }[kernel]
+
+
+def gpu_bench(args):
+    import torch
+
+    from metal_gauss_amd import _lib
+
+    dev = torch.device("cuda:0")
+    step = Step(args.gaussians, dev)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # fwd+bwd alone (no optimizer step), fewer iterations.
+    nfb = max(10, args.steps // 4)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(nfb):
+        step(adam=False)
+    torch.cuda.synchronize()
+    fb_ms = (time.perf_counter() - t0) * 1e3 / nfb
+
+    # Per-kernel mean launch time, HIP events recorded inside the library.
+    nt = 10
+    isects = []
+    with _lib.KernelTimer():
+        for _ in range(nt):
+            step()
+            isects.append(step.last_isect)
+        torch.cuda.synchronize()
+        kern = {}
+        for k in KERNELS:
+            tot, cnt = _lib.KernelTimer.query(k)
+            if cnt:
+                kern[k] = (tot / cnt, cnt / nt)      # ms per launch, launches per step
+    N = args.gaussians
+    I = sum(isects) / len(isects)
+    P = 800 * 800
+    T = 50 * 50
+    f_valid = float(step.last_valid.float().mean())
+    n_floats = sum(p.numel() for p in step.p.values())
+    dominant = max(kern, key=lambda k: kern[k][0] * kern[k][1])
+    avg_ms = kern[dominant][0]
+    nbytes = algorithmic_bytes(dominant, N, I, P, T, f_valid, n_floats)
+    achieved = nbytes / (avg_ms * 1e-3) / 1e9
+    rows = {k: {"ms": round(v[0], 4), "per_step": v[1],
+                "GBps": round(algorithmic_bytes(k, N, I, P, T, f_valid, n_floats)
+                              / (v[0] * 1e-3) / 1e9, 1)} for k, v in kern.items()}
+    return dict(ms=ms, fb_ms=fb_ms, kernels=rows, dominant=dominant, achieved=achieved,
+                nbytes=nbytes, I=I, f_valid=f_valid, n_floats=n_floats)
+
+
+def cpu_baseline(n_gaussians=1_000_000, crop=96):
+    """The CPU oracle on a bounded sample of the config-4 step, scaled.
+
+    Sample: the full config-4 scene (all N Gaussians projected, SH evaluated,
+    and differentiated), rasterised forward+backward over a crop x crop window
+    at the image centre, loss on the crop, and torch.optim.Adam over all 59N
+    parameters. Full-step time = projection + Adam + (raster + loss on the
+    crop) x (800^2 / crop^2); reported as steps/s.
+    """
+    import torch
+
+    from metal_gauss_amd import scenes
+    from oracle import render_ref as R
+    from oracle import ssim_ref
+
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    sc, cams, _ = scenes.config4(n_gaussians)
+    cam = cams[0]
+    W = H = 800
+    x0 = y0 = (W - crop) // 2
+    K = cam.K.clone()
+    K[0, 2] -= x0
+    K[1, 2] -= y0
+    leaves = {k: getattr(sc, k).clone().requires_grad_(True)
+              for k in ("means", "log_scales", "quats", "logit_opac", "sh_dc", "sh_rest")}
+    gt = scenes.config4_target(0)[y0:y0 + crop, x0:x0 + crop].contiguous()
+    vm = cam.viewmat
+    fx, fy, cx, cy = float(K[0, 0]), float(K[1, 1]), float(K[0, 2]), float(K[1, 2])
+
+    def project_part():
+        scales = torch.exp(leaves["log_scales"])
+        op = torch.sigmoid(leaves["logit_opac"])
+        sh = torch.cat([leaves["sh_dc"], leaves["sh_rest"]], dim=1)
+        cov = R.build_cov3d(leaves["quats"], scales)
+        uv, conic, depth, radius, valid, _ = R.project(leaves["means"], cov, vm, fx, fy, cx, cy,
+                                                       crop, crop, 0.01, 100.0,
+                                                       max_radius_frac=W / crop)
+        cc = -vm[:3, :3].T @ vm[:3, 3]
+        d = leaves["means"] - cc
+        d = d / d.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+        col = (R.eval_sh(3, sh, d) + 0.5).clamp_min(0.0)
+        return uv, conic, op, col, depth, radius, valid
+
+    # Projection of all N (forward + backward through a dummy reduction of the
+    # same outputs the rasteriser consumes).
+    t0 = time.perf_counter()
+    uv, conic, op, col, depth, radius, valid = project_part()
+    (uv.sum() + conic.sum() + col.sum() + op.sum()).backward()
+    t_proj = time.perf_counter() - t0
+    for t in leaves.values():
+        t.grad = None
+    # Raster + loss on the crop (the projection repeated outside the timer).
+    uv, conic, op, col, depth, radius, valid = project_part()
+    t0 = time.perf_counter()
+    rgb, alpha, info = R.rasterize(uv, conic, op, col, depth, radius, valid, crop, crop, tile=16,
+                                   background=(0.0, 0.0, 0.0))
+    loss = 0.8 * (rgb - gt).abs().mean() + 0.2 * (1.0 - ssim_ref.ssim(rgb, gt))
+    loss.backward()
+    t_crop = time.perf_counter() - t0
+    # Adam over all parameters.
+    opt = torch.optim.Adam(list(leaves.values()), lr=1e-3, eps=1e-15)
+    for t in leaves.values():
+        t.grad = torch.zeros_like(t)
+    t0 = time.perf_counter()
+    opt.step()
+    t_adam = time.perf_counter() - t0
+    scale = (W * H) / (crop * crop)
+    t_step = t_proj + t_adam + t_crop * scale
+    return {
+        "value": round(1.0 / t_step, 6), "unit": "steps/s", "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"config-4 step, CPU oracle (torch_ref restatement): projection+SH fwd+bwd of "
+                   f"all {n_gaussians} Gaussians {t_proj:.2f}s + Adam over all params "
+                   f"{t_adam:.2f}s + raster/loss fwd+bwd on a {crop}x{crop} centre crop "
+                   f"{t_crop:.2f}s x {scale:.1f} (pixel ratio); {info['isect_total']} crop "
+                   f"intersections; os.cpu_count()={cores}"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported by this build "
+              f"(the splatting step has no multi-GPU path here).", file=sys.stderr)
+        sys.exit(2)
+    if args.cpu_only:
+        print(json.dumps(cpu_baseline(args.gaussians)))
+        return
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        sys.exit(2)
+    if args.copy_mib:
+        copy_calibration(args.copy_mib)
+    r = gpu_bench(args)
+    out = {
+        "metric": METRIC,
+        "value": round(1000.0 / r["ms"], 3),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms"], 4),
+        "fwd_bwd_ms": round(r["fb_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": ("config 4: 1M Gaussians SH3, 800x800, 100 seeded views, "
+                         "fwd + bwd + FusedAdam, loss 0.8 L1 + 0.2 (1-SSIM)"),
+            "n_gaussians": args.gaussians, "width": 800, "height": 800, "sh_degree": 3,
+            "tile": 16, "mean_intersections": int(r["I"]),
+            "valid_fraction": round(r["f_valid"], 4),
+        },
+        "roofline": {
+            "bound": "hbm", "kernel": r["dominant"], "achieved": round(r["achieved"], 2),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(r["achieved"] / HBM_PEAK_GBS, 5), "traffic": None,
+            "algorithmic_bytes_per_launch": int(r["nbytes"]),
+        },
+        "kernels": r["kernels"],
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.gaussians)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -191,22 +191,25 @@ int32_t mg_rasterize_backward(
  * sqrt(bias_correction2) divide. Replaces adam_step
  * (metal_gauss/csrc/rasterize.mm:329-360; kernel adam.metal:25-42). */
 int32_t mg_adam_step(float *p, const float *g, float *m, float *v, int64_t n,
-                     float lr, float beta1, float beta2, float eps,
+                     double lr, double beta1, double beta2, double eps,
                      int64_t step, mg_stream_t stream);
 
-/* One Adam step on up to 64 flat tensors in ONE launch. Host arrays of length
+/* One Adam step on up to 32 flat tensors in ONE launch. Host arrays of length
  * count: p/g/m/v pointers, element counts, lr, and each tensor's step count
- * after this update. eps_inside != 0 selects the p -= lr*sqrt(bc2)/bc1 *
- * m/(sqrt(v)+eps) placement used by selective_adam.py:206 for dense groups.
- * Replaces the per-tensor loop of FusedAdam.step (fused_adam.py:31-54). */
+ * after this update. Hyperparameters are doubles: the bias corrections and
+ * step sizes are formed in double on the host (rasterize.mm:338-342); the
+ * moment updates use fp32 betas. eps_inside != 0 selects the
+ * p -= lr*sqrt(bc2)/bc1 * m/(sqrt(v)+eps) placement used by
+ * selective_adam.py:206 for dense groups. Replaces the per-tensor loop of
+ * FusedAdam.step (fused_adam.py:31-54). */
 int32_t mg_adam_step_multi(int32_t count, float *const *p,
                            const float *const *g, float *const *m,
                            float *const *v, const int64_t *n,
-                           const float *lr, const int64_t *step, float beta1,
-                           float beta2, float eps, int32_t eps_inside,
+                           const double *lr, const int64_t *step, double beta1,
+                           double beta2, double eps, int32_t eps_inside,
                            mg_stream_t stream);
 
-/* Row-masked Adam with a per-row float step count, over up to 64 tensors in
+/* Row-masked Adam with a per-row float step count, over up to 32 tensors in
  * one launch. Tensor k has rows[k] rows of width[k] floats; rows r with
  * r < n_visible and visible[r] != 0 get steps[r] += 1 and
  * p -= lr * sqrt(1-b2^k)/(1-b1^k) * m/(sqrt(v)+eps); other rows are left

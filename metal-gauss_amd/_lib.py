@@ -25,6 +25,7 @@ _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
+_f64 = ctypes.c_double
 _pp = ctypes.POINTER(ctypes.c_void_p)
 
 _SIGNATURES = {
@@ -55,9 +56,9 @@ _SIGNATURES = {
                                     _f32, _vp, _vp, _vp, _vp, _vp]),
     "mg_rasterize_backward": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                      _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "mg_adam_step": (_i32, [_vp, _vp, _vp, _vp, _i64, _f32, _f32, _f32, _f32, _i64, _vp]),
+    "mg_adam_step": (_i32, [_vp, _vp, _vp, _vp, _i64, _f64, _f64, _f64, _f64, _i64, _vp]),
     "mg_adam_step_multi": (_i32, [_i32, _pp, _pp, _pp, _pp, ctypes.POINTER(_i64),
-                                  ctypes.POINTER(_f32), ctypes.POINTER(_i64), _f32, _f32, _f32,
+                                  ctypes.POINTER(_f64), ctypes.POINTER(_i64), _f64, _f64, _f64,
                                   _i32, _vp]),
     "mg_selective_adam_step": (_i32, [_i32, _pp, _pp, _pp, _pp, _pp, ctypes.POINTER(_i64),
                                       ctypes.POINTER(_i32), ctypes.POINTER(_f32), _vp, _i64,
@@ -143,6 +144,10 @@ def i32_array(xs):
 
 def f32_array(xs):
     return (_f32 * max(1, len(xs)))(*xs)
+
+
+def f64_array(xs):
+    return (_f64 * max(1, len(xs)))(*xs)
 
 
 def host_f32(t: torch.Tensor) -> ctypes.Array:

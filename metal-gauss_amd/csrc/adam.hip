@@ -184,16 +184,19 @@ extern "C" {
 
 int32_t mg_adam_step_multi(int32_t count, float *const *p, const float *const *g,
                            float *const *m, float *const *v, const int64_t *n,
-                           const float *lr, const int64_t *step, float beta1,
-                           float beta2, float eps, int32_t eps_inside,
+                           const double *lr, const int64_t *step, double beta1,
+                           double beta2, double eps, int32_t eps_inside,
                            mg_stream_t stream) {
     MG_REQUIRE(count >= 0 && count <= kAdamMaxTensors,
                "mg_adam_step_multi: %d tensors, at most %d per launch", count,
                kAdamMaxTensors);
+    // The moments use fp32 betas (as the reference kernel, adam.metal:35-36);
+    // the bias corrections and step size are formed in double from the exact
+    // hyperparameters, as torch and rasterize.mm:338-342 do.
     AdamTable tab{};
-    tab.b1 = beta1;
-    tab.b2 = beta2;
-    tab.eps = eps;
+    tab.b1 = (float)beta1;
+    tab.b2 = (float)beta2;
+    tab.eps = (float)eps;
     tab.eps_inside = eps_inside;
     int64_t blocks = 0;
     int c = 0;
@@ -212,10 +215,10 @@ int32_t mg_adam_step_multi(int32_t count, float *const *p, const float *const *g
         const double bc1 = 1.0 - std::pow((double)beta1, (double)step[i]);
         const double bc2 = 1.0 - std::pow((double)beta2, (double)step[i]);
         if (eps_inside) {
-            T.step_size = (float)((double)lr[i] * std::sqrt(bc2) / bc1);
+            T.step_size = (float)(lr[i] * std::sqrt(bc2) / bc1);
             T.inv_sqrt_bc2 = 1.0f;
         } else {
-            T.step_size = (float)((double)lr[i] / bc1);
+            T.step_size = (float)(lr[i] / bc1);
             T.inv_sqrt_bc2 = (float)(1.0 / std::sqrt(bc2));
         }
         blocks += ceil_div(n[i], kAdamElemsPerBlock);
@@ -230,7 +233,7 @@ int32_t mg_adam_step_multi(int32_t count, float *const *p, const float *const *g
 }
 
 int32_t mg_adam_step(float *p, const float *g, float *m, float *v, int64_t n,
-                     float lr, float beta1, float beta2, float eps, int64_t step,
+                     double lr, double beta1, double beta2, double eps, int64_t step,
                      mg_stream_t stream) {
     return mg_adam_step_multi(1, &p, &g, &m, &v, &n, &lr, &step, beta1, beta2,
                               eps, 0, stream);

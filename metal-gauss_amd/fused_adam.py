@@ -68,7 +68,7 @@ class FusedAdam(torch.optim.Optimizer):
                         _lib.ptr_array([it[2].data_ptr() for it in chunk]),
                         _lib.ptr_array([it[3].data_ptr() for it in chunk]),
                         _lib.i64_array([it[0].numel() for it in chunk]),
-                        _lib.f32_array([it[4] for it in chunk]),
+                        _lib.f64_array([it[4] for it in chunk]),
                         _lib.i64_array([it[5] for it in chunk]),
                         b1, b2, eps, 0, s))
                     # Gradients made contiguous above must outlive the launch.

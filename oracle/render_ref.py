@@ -249,7 +249,7 @@ def rasterize(uv, conic, opacity, color, depth, radius, valid, W, H, tile: int =
                 present = ids >= 0
                 if not bool(present.any()):
                     break
-                if float(T.max()) < min_transmittance:
+                if float(T.detach().max()) < min_transmittance:
                     break
                 g = ids.clamp_min(0)
                 d = pix[:, None] - uv[g][:, :, None, :]

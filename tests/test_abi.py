@@ -66,7 +66,7 @@ def test_bad_arguments_fail_before_any_launch():
     lib = _lib.open_library()
     arr = (ctypes.c_void_p * 1)(None)
     n = (ctypes.c_int64 * 1)(1)
-    assert lib.mg_adam_step_multi(99, arr, arr, arr, arr, n, (ctypes.c_float * 1)(1.0),
+    assert lib.mg_adam_step_multi(99, arr, arr, arr, arr, n, (ctypes.c_double * 1)(1.0),
                                   n, 0.9, 0.999, 1e-15, 0, None) == 1
     assert "at most 32" in lib.mg_last_error().decode()
     # tiles that do not cover the image

@@ -24,8 +24,11 @@ def _params(n, seed, dev):
 
 
 def _max_rel_step(got, want, start):
-    step = np.abs(want - start).max()
-    return np.abs(got - want).max() / max(step, 1e-30)
+    """max |got - want| relative to the largest parameter magnitude, the
+    reference's metric (tests/test_fused_adam.py:37). A last-bit difference in
+    an fp32 parameter is ~1e-7 of its magnitude; measured against the step
+    size (~1e-4 of it) the same bit would read as ~1e-3."""
+    return np.abs(got - want).max() / max(np.abs(want).max(), 1e-30)
 
 
 @pytest.mark.parametrize("steps", [1, 30, 101])
@@ -70,10 +73,9 @@ def test_fused_adam_matches_torch_adam_over_many_steps(dev):
             t.grad = gr.clone()
         oa.step()
         ob.step()
-    for a, b, t0 in zip(A, B, init):
-        moved = (a.detach().cpu() - t0).abs().max()
-        rel = ((a - b).abs().max().cpu() / moved).item()
-        assert rel < 1e-5, f"diverged from torch Adam: {rel:.2e} of the step"
+    for a, b in zip(A, B):
+        rel = ((a - b).abs().max() / a.abs().max()).item()
+        assert rel < 1e-6, f"diverged from torch Adam: rel {rel:.2e}"
 
 
 def test_first_step_closed_form_at_config3_size(dev):
@@ -94,8 +96,10 @@ def test_first_step_closed_form_at_config3_size(dev):
         g = p.grad.double()
         want = -lr * g / (g.abs() + 1e-15)
         got = (p.detach() - s).double()
-        err = ((got - want).abs().max() / lr).item()
-        assert err < 2e-6, f"step-1 closed form off by {err:.2e} of lr"
+        # The stored parameter is rounded to fp32: allow one ulp of it.
+        ulp = torch.finfo(torch.float32).eps * p.detach().abs().double()
+        err = ((got - want).abs() - ulp).clamp_min(0).max().item() / lr
+        assert err < 1e-6, f"step-1 closed form off by {err:.2e} of lr"
 
 
 def test_state_layout_matches_torch(dev):

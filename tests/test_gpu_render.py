@@ -244,7 +244,7 @@ def test_no_discontinuity_across_boundaries(dev, lo, hi):
     op = torch.tensor([0.99], device=dev)
     es = []
     for u in np.arange(lo, hi, 0.05):
-        m = torch.tensor([[(u - W / 2) * Z / F, 0.0, Z]], device=dev)
+        m = torch.tensor([[(u - W / 2) * Z / F, 0.0, Z]], device=dev, dtype=torch.float32)
         rgb, _, _ = render(m, q, sc, op, sh, K, torch.eye(4), W, H, tile=32)
         es.append(float(rgb.sum()))
     steps = np.abs(np.diff(es))
