@@ -158,6 +158,43 @@ int32_t mg_tile_ranges(const uint64_t *sorted_keys, int64_t n,
                        int32_t n_tiles, int32_t *tile_offsets,
                        mg_stream_t stream);
 
+/* Depth-first tile lists: the whole of build_tile_lists_metal
+ * (metal_backend.py:217-285) in two calls around the one host read of the
+ * intersection total.
+ *
+ * begin: per-Gaussian tile counts (the exact ellipse test, as mg_bin_count),
+ * a stable 32-bit radix sort of all Gaussians by depth (invalid last), and
+ * the exclusive scan of the counts in depth order; the total goes to
+ * total_host (host; the stream is synchronised) when not NULL. The
+ * workspace (mg_bin_lists_workspace_bytes(N)) carries state to finish and
+ * must not be touched in between.
+ *
+ * finish: emits each Gaussian's (tile id, Gaussian id) pairs in depth order,
+ * stably radix-sorts them by tile id on ceil(log2(tiles_x*tiles_y)) bits and
+ * writes gauss_ids (total,) and tile_offsets (tiles_x*tiles_y + 1,). The
+ * result equals a stable sort of the (tile << 32 | depth bits) keys of
+ * mg_bin_write by mg_sort_pairs_u64: order (tile, depth, Gaussian id).
+ * Same arguments as begin, plus its workspace, the total, and a scratch of
+ * mg_bin_lists_finish_workspace_bytes(total). */
+int64_t mg_bin_lists_workspace_bytes(int64_t N);
+int64_t mg_bin_lists_finish_workspace_bytes(int64_t total);
+int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy,
+                           const float *conic, const float *opacity,
+                           const int32_t *valid, const float *depth, int32_t W,
+                           int32_t H, int32_t tile, int32_t tiles_x,
+                           int32_t tiles_y, void *workspace,
+                           int64_t workspace_bytes, int64_t *total_host,
+                           mg_stream_t stream);
+int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy,
+                            const float *conic, const float *opacity,
+                            const int32_t *valid, const float *depth, int32_t W,
+                            int32_t H, int32_t tile, int32_t tiles_x,
+                            int32_t tiles_y, const void *workspace,
+                            int64_t workspace_bytes, int64_t total,
+                            int32_t *gauss_ids, int32_t *tile_offsets,
+                            void *finish_workspace,
+                            int64_t finish_workspace_bytes, mg_stream_t stream);
+
 /* -------------------------------------------------------------- rasteriser */
 
 /* Front-to-back compositing, one workgroup per tile, one thread per pixel.
@@ -221,8 +258,8 @@ int32_t mg_selective_adam_step(int32_t count, float *const *p,
                                float *const *v, float *const *steps,
                                const int64_t *rows, const int32_t *width,
                                const float *lr, const uint8_t *visible,
-                               int64_t n_visible, float beta1, float beta2,
-                               float eps, mg_stream_t stream);
+                               int64_t n_visible, double beta1, double beta2,
+                               double eps, mg_stream_t stream);
 
 /* ------------------------------------------------------------------- SSIM */
 

@@ -52,6 +52,12 @@ _SIGNATURES = {
     "mg_sort_workspace_bytes": (_i64, [_i64]),
     "mg_sort_pairs_u64": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _i64, _vp]),
     "mg_tile_ranges": (_i32, [_vp, _i64, _i32, _vp, _vp]),
+    "mg_bin_lists_workspace_bytes": (_i64, [_i64]),
+    "mg_bin_lists_finish_workspace_bytes": (_i64, [_i64]),
+    "mg_bin_lists_begin": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
+                                  _i32, _vp, _i64, _vp, _vp]),
+    "mg_bin_lists_finish": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
+                                   _i32, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
     "mg_rasterize_forward": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                     _f32, _vp, _vp, _vp, _vp, _vp]),
     "mg_rasterize_backward": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -62,7 +68,7 @@ _SIGNATURES = {
                                   _i32, _vp]),
     "mg_selective_adam_step": (_i32, [_i32, _pp, _pp, _pp, _pp, _pp, ctypes.POINTER(_i64),
                                       ctypes.POINTER(_i32), ctypes.POINTER(_f32), _vp, _i64,
-                                      _f32, _f32, _f32, _vp]),
+                                      _f64, _f64, _f64, _vp]),
     "mg_ssim_stack_blur_h": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "mg_ssim_blur15": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp]),
     "mg_ssim_tail_forward": (_i32, [_vp, _i32, _i32, _vp, _vp]),

@@ -92,16 +92,18 @@ def _host_total() -> torch.Tensor:
 
 def _empty_lists(n_tiles: int, tx: int, device):
     return (torch.zeros(0, dtype=torch.int32, device=device),
-            torch.zeros(n_tiles + 1, dtype=torch.int32, device=device), tx,
-            torch.zeros(0, dtype=torch.int64, device=device))
+            torch.zeros(n_tiles + 1, dtype=torch.int32, device=device), tx)
 
 
 def _bin(uv, rxy, depth, valid_i, conic, opacity, W, H, tile):
-    """Count -> scan -> emit -> radix sort -> tile ranges, all on the GPU.
+    """Tile lists on the GPU, depth-first (mg_bin_lists_begin / _finish).
 
-    Returns (gauss_ids, tile_offsets, tiles_x, sorted (tile|depth) keys as
-    int64). One device->host read per call: the intersection total that sizes the key
-    buffers (the reference's .item(), metal_backend.py:247-248).
+    Counts with the exact ellipse test, one 32-bit radix sort of the
+    Gaussians by depth, the scan in that order, then emission in depth order
+    and a stable sort of the pairs by tile id alone. Returns (gauss_ids,
+    tile_offsets, tiles_x). One device->host read per call: the intersection
+    total that sizes the pair buffers (the reference's .item(),
+    metal_backend.py:247-248).
     """
     lib = _load()
     device = uv.device
@@ -110,6 +112,41 @@ def _bin(uv, rxy, depth, valid_i, conic, opacity, W, H, tile):
     N = uv.shape[0]
     if N == 0:
         return _empty_lists(n_tiles, tx, device)
+    s = _lib.stream(uv)
+    ptrs = (N, _lib.dev_tensor(uv, "uv"), _lib.dev_tensor(rxy, "rxy"),
+            _lib.dev_tensor(conic, "conic") if conic is not None else None,
+            _lib.dev_tensor(opacity, "opacity") if opacity is not None else None,
+            _lib.dev_tensor(valid_i, "valid", torch.int32), _lib.dev_tensor(depth, "depth"),
+            W, H, tile, tx, ty)
+    ws = torch.empty(lib.mg_bin_lists_workspace_bytes(N), dtype=torch.uint8, device=device)
+    host = _host_total()
+    _lib.check(lib.mg_bin_lists_begin(*ptrs, ws.data_ptr(), ws.numel(), host.data_ptr(), s))
+    total = int(host[0])
+    if total >= 2 ** 31:
+        raise RuntimeError(f"{total} tile intersections exceed the int32 index range")
+    gauss_ids = torch.empty(total, dtype=torch.int32, device=device)
+    tile_offsets = torch.empty(n_tiles + 1, dtype=torch.int32, device=device)
+    fws = torch.empty(lib.mg_bin_lists_finish_workspace_bytes(total), dtype=torch.uint8,
+                      device=device)
+    _lib.check(lib.mg_bin_lists_finish(*ptrs, ws.data_ptr(), ws.numel(), total,
+                                       gauss_ids.data_ptr() if total else None,
+                                       tile_offsets.data_ptr(), fws.data_ptr(), fws.numel(), s))
+    return gauss_ids, tile_offsets, tx
+
+
+def _bin_keys64(uv, rxy, depth, valid_i, conic, opacity, W, H, tile):
+    """The same lists through the reference's ABI pipeline: mg_bin_count ->
+    mg_exclusive_scan_i32 -> mg_bin_write (64-bit (tile|depth) keys) ->
+    mg_sort_pairs_u64 -> mg_tile_ranges. Returns (gauss_ids, tile_offsets,
+    tiles_x, sorted keys as int64)."""
+    lib = _load()
+    device = uv.device
+    tx, ty = _tile_grid(W, H, tile)
+    n_tiles = tx * ty
+    N = uv.shape[0]
+    if N == 0:
+        return _empty_lists(n_tiles, tx, device) + (torch.zeros(0, dtype=torch.int64,
+                                                                device=device),)
     s = _lib.stream(uv)
     p_uv = _lib.dev_tensor(uv, "uv")
     p_rxy = _lib.dev_tensor(rxy, "rxy")
@@ -130,7 +167,8 @@ def _bin(uv, rxy, depth, valid_i, conic, opacity, W, H, tile):
                                          scan_ws.data_ptr(), scan_ws.numel(), s))
     total = int(host[0])
     if total == 0:
-        return _empty_lists(n_tiles, tx, device)
+        return _empty_lists(n_tiles, tx, device) + (torch.zeros(0, dtype=torch.int64,
+                                                                device=device),)
     if total >= 2 ** 31:
         raise RuntimeError(f"{total} tile intersections exceed the int32 index range")
 

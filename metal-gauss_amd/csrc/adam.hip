@@ -40,16 +40,16 @@ struct AdamTensor {
 struct AdamTable {
     AdamTensor t[kAdamMaxTensors];
     int32_t count;
-    float b1, b2, eps;
+    float b1, b2, omb1, omb2, eps;   // omb = 1 - beta, formed in double
     int32_t eps_inside;
 };
 
 __device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v,
-                                          float b1, float b2, float eps,
-                                          float step_size, float inv_sqrt_bc2,
-                                          bool eps_inside) {
-    m = fmaf(b1, m, (1.0f - b1) * g);
-    v = fmaf(b2, v, (1.0f - b2) * g * g);
+                                          const AdamTable &tab, float step_size,
+                                          float inv_sqrt_bc2, bool eps_inside) {
+    const float eps = tab.eps;
+    m = fmaf(tab.b1, m, tab.omb1 * g);
+    v = fmaf(tab.b2, v, tab.omb2 * g * g);
     const float sv = sqrtf(v);
     const float denom = eps_inside ? (sv + eps) : (sv * inv_sqrt_bc2 + eps);
     p = p - step_size * m / denom;
@@ -74,17 +74,17 @@ __global__ __launch_bounds__(kAdamThreads) void adam_multi_kernel(const AdamTabl
                 const float4 g = *reinterpret_cast<const float4 *>(T.g + e);
                 float4 m = *reinterpret_cast<const float4 *>(T.m + e);
                 float4 v = *reinterpret_cast<const float4 *>(T.v + e);
-                adam_elem(p.x, g.x, m.x, v.x, tab.b1, tab.b2, tab.eps, T.step_size, T.inv_sqrt_bc2, ei);
-                adam_elem(p.y, g.y, m.y, v.y, tab.b1, tab.b2, tab.eps, T.step_size, T.inv_sqrt_bc2, ei);
-                adam_elem(p.z, g.z, m.z, v.z, tab.b1, tab.b2, tab.eps, T.step_size, T.inv_sqrt_bc2, ei);
-                adam_elem(p.w, g.w, m.w, v.w, tab.b1, tab.b2, tab.eps, T.step_size, T.inv_sqrt_bc2, ei);
+                adam_elem(p.x, g.x, m.x, v.x, tab, T.step_size, T.inv_sqrt_bc2, ei);
+                adam_elem(p.y, g.y, m.y, v.y, tab, T.step_size, T.inv_sqrt_bc2, ei);
+                adam_elem(p.z, g.z, m.z, v.z, tab, T.step_size, T.inv_sqrt_bc2, ei);
+                adam_elem(p.w, g.w, m.w, v.w, tab, T.step_size, T.inv_sqrt_bc2, ei);
                 *reinterpret_cast<float4 *>(T.p + e) = p;
                 *reinterpret_cast<float4 *>(T.m + e) = m;
                 *reinterpret_cast<float4 *>(T.v + e) = v;
             } else {
                 for (int64_t i = e; i < T.n && i < e + kAdamVec; ++i) {
                     float p = T.p[i], m = T.m[i], v = T.v[i];
-                    adam_elem(p, T.g[i], m, v, tab.b1, tab.b2, tab.eps, T.step_size, T.inv_sqrt_bc2, ei);
+                    adam_elem(p, T.g[i], m, v, tab, T.step_size, T.inv_sqrt_bc2, ei);
                     T.p[i] = p; T.m[i] = m; T.v[i] = v;
                 }
             }
@@ -94,7 +94,7 @@ __global__ __launch_bounds__(kAdamThreads) void adam_multi_kernel(const AdamTabl
             const int64_t i = base + (int64_t)r * kAdamThreads + threadIdx.x;
             if (i < T.n) {
                 float p = T.p[i], m = T.m[i], v = T.v[i];
-                adam_elem(p, T.g[i], m, v, tab.b1, tab.b2, tab.eps, T.step_size, T.inv_sqrt_bc2, ei);
+                adam_elem(p, T.g[i], m, v, tab, T.step_size, T.inv_sqrt_bc2, ei);
                 T.p[i] = p; T.m[i] = m; T.v[i] = v;
             }
         }
@@ -122,7 +122,7 @@ struct SelTensor {
 struct SelTable {
     SelTensor t[kAdamMaxTensors];
     int32_t count;
-    float b1, b2, eps;
+    float b1, b2, omb1, omb2, eps;   // omb = 1 - beta, formed in double
     const uint8_t *visible;
     int64_t n_visible;
 };
@@ -162,14 +162,14 @@ __global__ __launch_bounds__(kAdamThreads) void selective_adam_kernel(const SelT
 
     const int64_t e0 = r0 * T.width;
     const int64_t ne = (int64_t)nrows * T.width;
-    const float b1 = tab.b1, b2 = tab.b2, eps = tab.eps;
+    const float b1 = tab.b1, b2 = tab.b2, omb1 = tab.omb1, omb2 = tab.omb2, eps = tab.eps;
     for (int64_t le = threadIdx.x; le < ne; le += kAdamThreads) {
         const int lr_ = (int)(le / T.width);
         if (!s_vis[lr_]) continue;
         const int64_t i = e0 + le;
         const float g = T.g[i];
-        float m = T.m[i] * b1 + g * (1.0f - b1);
-        float v = T.v[i] * b2 + g * g * (1.0f - b2);
+        float m = T.m[i] * b1 + g * omb1;
+        float v = T.v[i] * b2 + g * g * omb2;
         T.m[i] = m;
         T.v[i] = v;
         T.p[i] = T.p[i] - s_step_size[lr_] * m / (sqrtf(v) + eps);
@@ -196,6 +196,8 @@ int32_t mg_adam_step_multi(int32_t count, float *const *p, const float *const *g
     AdamTable tab{};
     tab.b1 = (float)beta1;
     tab.b2 = (float)beta2;
+    tab.omb1 = (float)(1.0 - beta1);   // torch's lerp weight / addcmul value
+    tab.omb2 = (float)(1.0 - beta2);
     tab.eps = (float)eps;
     tab.eps_inside = eps_inside;
     int64_t blocks = 0;
@@ -244,8 +246,8 @@ int32_t mg_selective_adam_step(int32_t count, float *const *p,
                                float *const *v, float *const *steps,
                                const int64_t *rows, const int32_t *width,
                                const float *lr, const uint8_t *visible,
-                               int64_t n_visible, float beta1, float beta2,
-                               float eps, mg_stream_t stream) {
+                               int64_t n_visible, double beta1, double beta2,
+                               double eps, mg_stream_t stream) {
     MG_REQUIRE(count >= 0 && count <= kAdamMaxTensors,
                "mg_selective_adam_step: %d tensors, at most %d per launch", count,
                kAdamMaxTensors);
@@ -254,6 +256,8 @@ int32_t mg_selective_adam_step(int32_t count, float *const *p,
     SelTable tab{};
     tab.b1 = beta1;
     tab.b2 = beta2;
+    tab.omb1 = (float)(1.0 - (double)beta1);
+    tab.omb2 = (float)(1.0 - (double)beta2);
     tab.eps = eps;
     tab.visible = visible;
     tab.n_visible = n_visible;

@@ -16,6 +16,7 @@
 //     fp32, i.e. the correctly rounded value, rather than a fast fp32 log
 //     whose last bit differs between libraries.
 #include "mg_common.h"
+#include "mg_sort.h"
 
 namespace mg {
 
@@ -149,7 +150,8 @@ __device__ __forceinline__ int64_t block_excl_scan(int64_t v, int64_t *s_wave, i
     return before + incl - v;
 }
 
-__global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const int32_t *in, int64_t n,
+__global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const int32_t *in,
+                                                                   const int32_t *idx, int64_t n,
                                                                    int64_t *partials) {
     __shared__ int64_t s_wave[kScanThreads / 64];
     const int64_t base = (int64_t)blockIdx.x * kScanChunk;
@@ -157,7 +159,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const int32_t
 #pragma unroll
     for (int r = 0; r < kScanItems; ++r) {
         const int64_t i = base + (int64_t)r * kScanThreads + threadIdx.x;
-        if (i < n) s += in[i];
+        if (i < n) s += in[idx ? idx[i] : i];
     }
     int64_t total;
     block_excl_scan(s, s_wave, &total);
@@ -180,7 +182,8 @@ __global__ __launch_bounds__(kScanThreads) void scan_partials_kernel(int64_t *pa
     if (threadIdx.x == 0) *total_out = carry;
 }
 
-__global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const int32_t *in, int64_t n,
+__global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const int32_t *in,
+                                                                 const int32_t *idx, int64_t n,
                                                                  const int64_t *partials,
                                                                  int32_t *out) {
     __shared__ int64_t s_wave[kScanThreads / 64];
@@ -191,7 +194,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const int32_t *
     int64_t s = 0;
 #pragma unroll
     for (int r = 0; r < kScanItems; ++r) {
-        v[r] = (base + r < n) ? in[base + r] : 0;
+        v[r] = (base + r < n) ? in[idx ? idx[base + r] : base + r] : 0;
         s += v[r];
     }
     int64_t tot;
@@ -214,6 +217,133 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint64_t *keys, 
     const int64_t prev = i == 0 ? -1 : (int64_t)(keys[i - 1] >> 32);
     const int64_t cur = i == n ? (int64_t)n_tiles : (int64_t)(keys[i] >> 32);
     for (int64_t t = prev + 1; t <= cur && t <= n_tiles; ++t) offsets[t] = (int32_t)i;
+}
+
+int64_t scan_ws_bytes(int64_t n) {
+    return (ceil_div(n > 0 ? n : 1, kScanChunk) + 1) * (int64_t)sizeof(int64_t);
+}
+
+int32_t exclusive_scan(const int32_t *in, const int32_t *idx, int64_t n, int32_t *out,
+                       int64_t *total_dev, void *ws, int64_t ws_bytes, hipStream_t s) {
+    MG_REQUIRE(ws && ws_bytes >= scan_ws_bytes(n), "exclusive scan: workspace %lld bytes, need %lld",
+               (long long)ws_bytes, (long long)scan_ws_bytes(n));
+    int64_t *partials = static_cast<int64_t *>(ws);
+    const int64_t nparts = ceil_div(n > 0 ? n : 1, kScanChunk);
+    TimedScope ts("exclusive_scan", s);
+    // A zero-length input still runs one reduce block so the total is 0.
+    scan_reduce_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(in, idx, n, partials);
+    MG_LAUNCHED("scan_reduce_kernel");
+    scan_partials_kernel<<<1, kScanThreads, 0, s>>>(partials, nparts, total_dev);
+    MG_LAUNCHED("scan_partials_kernel");
+    if (n > 0) {
+        scan_down_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(in, idx, n, partials, out);
+        MG_LAUNCHED("scan_down_kernel");
+    }
+    return MG_OK;
+}
+
+// ------------------------------------------------- depth-first tile lists
+// The (tile << 32 | depth) order is built in two cheaper sorts: all N
+// Gaussians by depth once (32-bit keys; invalid ones get 0xFFFFFFFF and sort
+// last), then the intersections, emitted in that depth order, by tile id
+// alone (ceil(log2 n_tiles) bits). The tile sort is stable, so inside a tile
+// the order is (depth bits, Gaussian id) - the same total order as one stable
+// sort of the 64-bit keys emitted Gaussian by Gaussian.
+__global__ __launch_bounds__(256) void depth_keys_kernel(const float *depth, const int32_t *valid,
+                                                         int64_t n, uint32_t *keys,
+                                                         int32_t *vals) {
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (g >= n) return;
+    keys[g] = valid[g] ? __float_as_uint(depth[g]) : 0xFFFFFFFFu;
+    vals[g] = (int32_t)g;
+}
+
+// Thread k emits the pairs of the k-th Gaussian in depth order: tile id keys
+// (32-bit) and Gaussian ids, at the scanned offset of position k.
+__global__ __launch_bounds__(kBinThreads) void bin_write_ordered_kernel(
+    const BinArgs A, const int32_t *order, const int32_t *offsets, uint32_t *tkeys,
+    int32_t *ids) {
+    const int64_t k = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
+    if (k >= A.N) return;
+    const int64_t g = order[k];
+    if (A.valid[g] == 0) return;
+    const float ux = A.uv[2 * g], uy = A.uv[2 * g + 1];
+    const float rx = A.rxy[2 * g], ry = A.rxy[2 * g + 1];
+    const float tf = (float)A.tile;
+    int x0 = (int)floorf((ux - rx) / tf), x1 = (int)floorf((ux + rx) / tf);
+    int y0 = (int)floorf((uy - ry) / tf), y1 = (int)floorf((uy + ry) / tf);
+    x0 = min(max(x0, 0), A.tiles_x - 1);
+    x1 = min(max(x1, 0), A.tiles_x - 1);
+    y0 = min(max(y0, 0), A.tiles_y - 1);
+    y1 = min(max(y1, 0), A.tiles_y - 1);
+    const bool test = A.conic != nullptr;
+    float thr = 0.f, ca = 0.f, cb = 0.f, cc = 0.f;
+    if (test) {
+        bool live;
+        thr = level_threshold(A.opac[g], live);
+        if (!live) return;
+        ca = A.conic[3 * g]; cb = A.conic[3 * g + 1]; cc = A.conic[3 * g + 2];
+    }
+    int64_t at = offsets[k];
+    for (int ty = y0; ty <= y1; ++ty) {
+        const float ry0 = (float)(ty * A.tile);
+        const float ry1 = fminf((float)((ty + 1) * A.tile), (float)A.H);
+        for (int tx = x0; tx <= x1; ++tx) {
+            const float rx0 = (float)(tx * A.tile);
+            const float rx1 = fminf((float)((tx + 1) * A.tile), (float)A.W);
+            if (test && min_q_over_rect(ux, uy, ca, cb, cc, rx0, rx1, ry0, ry1) >= thr) continue;
+            tkeys[at] = (uint32_t)(ty * A.tiles_x + tx);
+            ids[at] = (int32_t)g;
+            ++at;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void tile_ranges_u32_kernel(const uint32_t *tiles, int64_t n,
+                                                              int32_t n_tiles, int32_t *offsets) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i > n) return;
+    const int64_t prev = i == 0 ? -1 : (int64_t)tiles[i - 1];
+    const int64_t cur = i == n ? (int64_t)n_tiles : (int64_t)tiles[i];
+    for (int64_t t = prev + 1; t <= cur && t <= n_tiles; ++t) offsets[t] = (int32_t)i;
+}
+
+constexpr int kDepthBits = 32;
+
+inline int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
+
+// Carves the begin/finish workspace identically on both calls.
+struct BeginWs {
+    int32_t *counts, *perm_a, *perm_b, *offsets;
+    uint32_t *dkey_a, *dkey_b;
+    int64_t *total;
+    void *scan_ws, *sort_ws;
+    int64_t scan_bytes, sort_bytes, bytes;
+    BeginWs(void *base, int64_t N) {
+        char *p = static_cast<char *>(base);
+        int64_t off = 0;
+        auto take = [&](int64_t b) { char *q = p ? p + off : nullptr; off += align256(b); return q; };
+        counts = (int32_t *)take(4 * N);
+        perm_a = (int32_t *)take(4 * N);
+        perm_b = (int32_t *)take(4 * N);
+        offsets = (int32_t *)take(4 * N);
+        dkey_a = (uint32_t *)take(4 * N);
+        dkey_b = (uint32_t *)take(4 * N);
+        total = (int64_t *)take(8);
+        scan_bytes = scan_ws_bytes(N);
+        scan_ws = take(scan_bytes);
+        sort_bytes = sort_ws_bytes(N);
+        sort_ws = take(sort_bytes);
+        bytes = off;
+    }
+    // The depth sort runs ceil(32/8) = 4 passes, so its result is in slot a.
+    int32_t *perm() const { return ((kDepthBits + 7) / 8) % 2 == 0 ? perm_a : perm_b; }
+};
+
+inline int tile_bits(int n_tiles) {
+    int b = 1;
+    while ((1LL << b) < n_tiles) ++b;
+    return b;
 }
 
 static int32_t check_bin_args(const char *who, int64_t N, const void *uv, const void *rxy,
@@ -254,39 +384,17 @@ int32_t mg_bin_count(int64_t N, const float *uv, const float *rxy, const float *
     return MG_OK;
 }
 
-int64_t mg_scan_workspace_bytes(int64_t n) {
-    return (ceil_div(n > 0 ? n : 1, kScanChunk) + 1) * (int64_t)sizeof(int64_t);
-}
+int64_t mg_scan_workspace_bytes(int64_t n) { return scan_ws_bytes(n); }
 
 int32_t mg_exclusive_scan_i32(const int32_t *in, int64_t n, int32_t *out, int64_t *total_dev,
                               int64_t *total_host, void *workspace, int64_t workspace_bytes,
                               mg_stream_t stream) {
     MG_REQUIRE(n >= 0, "mg_exclusive_scan_i32: n = %lld", (long long)n);
     MG_REQUIRE(total_dev, "mg_exclusive_scan_i32: null total_dev");
-    MG_REQUIRE(workspace_bytes >= mg_scan_workspace_bytes(n) && workspace,
-               "mg_exclusive_scan_i32: workspace %lld bytes, need %lld",
-               (long long)workspace_bytes, (long long)mg_scan_workspace_bytes(n));
+    MG_REQUIRE(n == 0 || (in && out), "mg_exclusive_scan_i32: null input/output");
     hipStream_t s = as_stream(stream);
-    int64_t *partials = static_cast<int64_t *>(workspace);
-    const int64_t nparts = ceil_div(n > 0 ? n : 1, kScanChunk);
-    {
-        TimedScope ts("exclusive_scan", s);
-        if (n > 0) {
-            MG_REQUIRE(in && out, "mg_exclusive_scan_i32: null input/output");
-            scan_reduce_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(in, n, partials);
-            MG_LAUNCHED("scan_reduce_kernel");
-        } else {
-            // Zero-length input: a single zero partial gives total 0.
-            scan_reduce_kernel<<<1, kScanThreads, 0, s>>>(in, 0, partials);
-            MG_LAUNCHED("scan_reduce_kernel");
-        }
-        scan_partials_kernel<<<1, kScanThreads, 0, s>>>(partials, nparts, total_dev);
-        MG_LAUNCHED("scan_partials_kernel");
-        if (n > 0) {
-            scan_down_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(in, n, partials, out);
-            MG_LAUNCHED("scan_down_kernel");
-        }
-    }
+    int32_t rc = exclusive_scan(in, nullptr, n, out, total_dev, workspace, workspace_bytes, s);
+    if (rc != MG_OK) return rc;
     if (total_host) {
         MG_HIP(hipMemcpyAsync(total_host, total_dev, sizeof(int64_t), hipMemcpyDeviceToHost, s));
         MG_HIP(hipStreamSynchronize(s));
@@ -322,6 +430,113 @@ int32_t mg_tile_ranges(const uint64_t *sorted_keys, int64_t n, int32_t n_tiles,
     tile_ranges_kernel<<<(unsigned)ceil_div(n + 1, 256), 256, 0, as_stream(stream)>>>(
         sorted_keys, n, n_tiles, tile_offsets);
     MG_LAUNCHED("tile_ranges_kernel");
+    return MG_OK;
+}
+
+int64_t mg_bin_lists_workspace_bytes(int64_t N) { return BeginWs(nullptr, N > 0 ? N : 1).bytes; }
+
+int64_t mg_bin_lists_finish_workspace_bytes(int64_t total) {
+    const int64_t T = total > 0 ? total : 1;
+    return 3 * align256(4 * T) + align256(sort_ws_bytes(T));
+}
+
+int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy, const float *conic,
+                           const float *opacity, const int32_t *valid, const float *depth,
+                           int32_t W, int32_t H, int32_t tile, int32_t tiles_x, int32_t tiles_y,
+                           void *workspace, int64_t workspace_bytes, int64_t *total_host,
+                           mg_stream_t stream) {
+    int32_t rc = check_bin_args("mg_bin_lists_begin", N, uv, rxy, conic, opacity, valid, W, H,
+                                tile, tiles_x, tiles_y);
+    if (rc != MG_OK) return rc;
+    MG_REQUIRE(depth || N == 0, "mg_bin_lists_begin: null depth");
+    BeginWs ws(workspace, N > 0 ? N : 1);
+    MG_REQUIRE(workspace && workspace_bytes >= ws.bytes,
+               "mg_bin_lists_begin: workspace %lld bytes, need %lld", (long long)workspace_bytes,
+               (long long)ws.bytes);
+    hipStream_t s = as_stream(stream);
+    BinArgs A{N, uv, rxy, conic, opacity, depth, valid, W, H, tile, tiles_x, tiles_y};
+    if (N > 0) {
+        {
+            TimedScope ts("bin_count", s);
+            bin_count_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(A, ws.counts);
+            MG_LAUNCHED("bin_count_kernel");
+        }
+        depth_keys_kernel<<<(unsigned)ceil_div(N, 256), 256, 0, s>>>(depth, valid, N, ws.dkey_a,
+                                                                      ws.perm_a);
+        MG_LAUNCHED("depth_keys_kernel");
+        uint32_t *rk;
+        int32_t *rv;
+        rc = radix_sort_passes<uint32_t>(ws.dkey_a, ws.perm_a, ws.dkey_b, ws.perm_b, N, 0,
+                                         kDepthBits, ws.sort_ws, ws.sort_bytes, s, "depth_sort",
+                                         &rk, &rv);
+        if (rc != MG_OK) return rc;
+        MG_REQUIRE(rv == ws.perm(), "mg_bin_lists_begin: depth order landed in the wrong buffer");
+    }
+    rc = exclusive_scan(ws.counts, ws.perm(), N, ws.offsets, ws.total, ws.scan_ws, ws.scan_bytes, s);
+    if (rc != MG_OK) return rc;
+    if (total_host) {
+        MG_HIP(hipMemcpyAsync(total_host, ws.total, sizeof(int64_t), hipMemcpyDeviceToHost, s));
+        MG_HIP(hipStreamSynchronize(s));
+    }
+    return MG_OK;
+}
+
+int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy, const float *conic,
+                            const float *opacity, const int32_t *valid, const float *depth,
+                            int32_t W, int32_t H, int32_t tile, int32_t tiles_x, int32_t tiles_y,
+                            const void *workspace, int64_t workspace_bytes, int64_t total,
+                            int32_t *gauss_ids, int32_t *tile_offsets, void *finish_workspace,
+                            int64_t finish_workspace_bytes, mg_stream_t stream) {
+    int32_t rc = check_bin_args("mg_bin_lists_finish", N, uv, rxy, conic, opacity, valid, W, H,
+                                tile, tiles_x, tiles_y);
+    if (rc != MG_OK) return rc;
+    MG_REQUIRE(total >= 0 && total < (1LL << 31), "mg_bin_lists_finish: total %lld",
+               (long long)total);
+    MG_REQUIRE(tile_offsets, "mg_bin_lists_finish: null tile_offsets");
+    BeginWs ws(const_cast<void *>(workspace), N > 0 ? N : 1);
+    MG_REQUIRE(workspace && workspace_bytes >= ws.bytes,
+               "mg_bin_lists_finish: begin workspace %lld bytes, need %lld",
+               (long long)workspace_bytes, (long long)ws.bytes);
+    MG_REQUIRE(finish_workspace &&
+                   finish_workspace_bytes >= mg_bin_lists_finish_workspace_bytes(total),
+               "mg_bin_lists_finish: workspace %lld bytes, need %lld",
+               (long long)finish_workspace_bytes,
+               (long long)mg_bin_lists_finish_workspace_bytes(total));
+    hipStream_t s = as_stream(stream);
+    const int n_tiles = tiles_x * tiles_y;
+    const int64_t T = total > 0 ? total : 1;
+    char *f = static_cast<char *>(finish_workspace);
+    uint32_t *tk_a = (uint32_t *)f;
+    uint32_t *tk_b = (uint32_t *)(f + align256(4 * T));
+    int32_t *ids_tmp = (int32_t *)(f + 2 * align256(4 * T));
+    void *sort_ws = f + 3 * align256(4 * T);
+    const int64_t sort_bytes = align256(sort_ws_bytes(T));
+    uint32_t *res_tiles = tk_a;
+    if (total > 0) {
+        MG_REQUIRE(gauss_ids, "mg_bin_lists_finish: null gauss_ids");
+        // Emit into the id buffer the last sort pass will NOT write, so the
+        // sorted ids end in gauss_ids whatever the pass count's parity.
+        const int bits = tile_bits(n_tiles);
+        const bool even = ((bits + 7) / 8) % 2 == 0;
+        int32_t *ids_a = even ? gauss_ids : ids_tmp;
+        int32_t *ids_b = even ? ids_tmp : gauss_ids;
+        BinArgs A{N, uv, rxy, conic, opacity, depth, valid, W, H, tile, tiles_x, tiles_y};
+        {
+            TimedScope ts("bin_write", s);
+            bin_write_ordered_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(
+                A, ws.perm(), ws.offsets, tk_a, ids_a);
+            MG_LAUNCHED("bin_write_ordered_kernel");
+        }
+        int32_t *rv;
+        rc = radix_sort_passes<uint32_t>(tk_a, ids_a, tk_b, ids_b, total, 0, bits, sort_ws,
+                                         sort_bytes, s, "tile_sort", &res_tiles, &rv);
+        if (rc != MG_OK) return rc;
+        MG_REQUIRE(rv == gauss_ids, "mg_bin_lists_finish: ids landed in the wrong buffer");
+    }
+    TimedScope ts("tile_ranges", s);
+    tile_ranges_u32_kernel<<<(unsigned)ceil_div(total + 1, 256), 256, 0, s>>>(res_tiles, total,
+                                                                              n_tiles, tile_offsets);
+    MG_LAUNCHED("tile_ranges_u32_kernel");
     return MG_OK;
 }
 

@@ -19,9 +19,13 @@
 //   when all its waves are.
 // Backward (rasterize.metal:173-340 contract): back to front from the
 //   largest stop index of the wave, T recovered by dividing out (1 - alpha),
-//   colour/alpha suffix sums, gradients to colour, uv, conic and opacity;
-//   the 9 (10 with absgrad) per-Gaussian sums are reduced across the 64
-//   lanes with DPP and one lane issues the global float atomics.
+//   colour/alpha suffix sums, gradients to colour, uv, conic and opacity.
+//   The 9 (10 with absgrad) per-Gaussian sums are reduced across the 64
+//   lanes with DPP and added into a per-batch LDS accumulator (LDS float
+//   atomics: several waves may hold the same Gaussian); after the batch one
+//   thread per Gaussian issues the global float atomics. Global atomics go
+//   to a coherence point shared by all XCDs and cost HBM write traffic, so
+//   there is one set per (Gaussian, tile) rather than per (Gaussian, wave).
 #include "mg_common.h"
 
 namespace mg {
@@ -84,18 +88,28 @@ __device__ __forceinline__ float rect_min_q(float mux, float muy, float ca, floa
     return best;
 }
 
+// LDS of one workgroup; MAXW bounds the waves per tile (4 up to 16x16).
+template <int MAXW>
 struct Stage {
     float4 geo[kBatch];       // u, v, opacity, unused
     float4 con[kBatch];       // conic a, b, c, unused
     float4 col[kBatch];       // r, g, b, unused
     int32_t id[kBatch];
     uint32_t live[kBatch];    // bit w: wave w may be touched
-    uint16_t list[kMaxWaves][kBatch];
-    float4 rect[kMaxWaves];   // x_lo, x_hi, y_lo, y_hi of pixel centres
-    int32_t flag[kMaxWaves];
+    uint16_t list[MAXW][kBatch];
+    float4 rect[MAXW];        // x_lo, x_hi, y_lo, y_hi of pixel centres
+    int32_t flag[MAXW];
 };
 
-__device__ __forceinline__ void stage_batch(Stage &S, const RasterArgs &A, int base, int n,
+constexpr int kGradSlots = 10;   // colour 3, uv 2, conic 3, opacity, |uv|
+
+template <int MAXW>
+struct StageBwd : Stage<MAXW> {
+    float grad[kGradSlots][kBatch];   // per batch entry, summed over waves
+};
+
+template <class S_>
+__device__ __forceinline__ void stage_batch(S_ &S, const RasterArgs &A, int base, int n,
                                             int nwaves) {
     for (int t = threadIdx.x; t < n; t += blockDim.x) {
         const int g = A.ids[base + t];
@@ -125,7 +139,8 @@ __device__ __forceinline__ void wave_sync_lds() {
 
 // Builds this wave's ordered list of batch entries j < lim that are live for
 // it. Returns the count (wave-uniform).
-__device__ __forceinline__ int compact_live(Stage &S, int n, int lim, int wave, int lane) {
+template <class S_>
+__device__ __forceinline__ int compact_live(S_ &S, int n, int lim, int wave, int lane) {
     int cnt = 0;
     for (int c = 0; c < n; c += 64) {
         const int j = c + lane;
@@ -138,7 +153,8 @@ __device__ __forceinline__ int compact_live(Stage &S, int n, int lim, int wave, 
     return cnt;
 }
 
-__device__ __forceinline__ void publish_rect(Stage &S, bool inimg, float fx, float fy, int wave,
+template <class S_>
+__device__ __forceinline__ void publish_rect(S_ &S, bool inimg, float fx, float fy, int wave,
                                              int lane) {
     const float inf = __builtin_inff();
     const float x0 = wave_min(inimg ? fx : inf), x1 = wave_max(inimg ? fx : -inf);
@@ -149,10 +165,11 @@ __device__ __forceinline__ void publish_rect(Stage &S, bool inimg, float fx, flo
     }
 }
 
-__global__ __launch_bounds__(1024) void raster_fwd_kernel(const RasterArgs A, float *out_rgb,
-                                                          float *out_alpha, float *out_T,
-                                                          int32_t *out_stop) {
-    __shared__ Stage S;
+template <int MAXW>
+__global__ __launch_bounds__(MAXW * 64) void raster_fwd_kernel(const RasterArgs A, float *out_rgb,
+                                                               float *out_alpha, float *out_T,
+                                                               int32_t *out_stop) {
+    __shared__ Stage<MAXW> S;
     const int tile_id = xcd_band(blockIdx.x, A.n_tiles);
     if (tile_id < 0) return;   // whole workgroup
     const int tx = tile_id % A.tiles_x, ty = tile_id / A.tiles_x;
@@ -226,8 +243,10 @@ struct RasterGrads {
     float *d_uv, *d_conic, *d_op, *d_col, *d_abs;
 };
 
-__global__ __launch_bounds__(1024) void raster_bwd_kernel(const RasterArgs A, const RasterGrads G) {
-    __shared__ Stage S;
+template <int MAXW>
+__global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs A,
+                                                               const RasterGrads G) {
+    __shared__ StageBwd<MAXW> S;
     const int tile_id = xcd_band(blockIdx.x, A.n_tiles);
     if (tile_id < 0) return;
     const int tx = tile_id % A.tiles_x, ty = tile_id / A.tiles_x;
@@ -263,8 +282,10 @@ __global__ __launch_bounds__(1024) void raster_bwd_kernel(const RasterArgs A, co
     for (int bi = nbatch - 1; bi >= 0; --bi) {
         const int base = start + bi * kBatch;
         const int n = min(kBatch, bstop - base);
-        __syncthreads();
+        __syncthreads();   // the previous batch's flush has read S.grad
         stage_batch(S, A, base, n, nwaves);
+        for (int t = threadIdx.x; t < kGradSlots * kBatch; t += blockDim.x)
+            (&S.grad[0][0])[t] = 0.f;
         __syncthreads();
         const int cnt = compact_live(S, n, wstop - base, wave, lane);
         for (int k = cnt - 1; k >= 0; --k) {
@@ -280,17 +301,18 @@ __global__ __launch_bounds__(1024) void raster_bwd_kernel(const RasterArgs A, co
             const float alpha = fminf(kAlphaMax, alpha_raw);
             const bool active = inimg && i < my_stop && power <= 0.0f && alpha >= kAlphaMin;
             if (ballot(active) == 0) continue;
-            float vcr = 0.f, vcg = 0.f, vcb = 0.f, vu = 0.f, vv = 0.f;
-            float vka = 0.f, vkb = 0.f, vkc = 0.f, vop = 0.f, vabs = 0.f;
+            float v[kGradSlots];
+#pragma unroll
+            for (int q = 0; q < kGradSlots; ++q) v[q] = 0.f;
             if (active) {
                 const float4 col = S.col[j];
                 const float om = fmaxf(1.0f - alpha, 1e-8f);
                 T = T / om;
                 const float iom = 1.0f / om;
                 const float w = alpha * T;
-                vcr = w * gr;
-                vcg = w * gg;
-                vcb = w * gb;
+                v[0] = w * gr;
+                v[1] = w * gg;
+                v[2] = w * gb;
                 const float dal = gr * (T * col.x - sr * iom) + gg * (T * col.y - sg * iom) +
                                   gb * (T * col.z - sb * iom) + ga * (T - sa * iom);
                 sr = fmaf(w, col.x, sr);
@@ -298,39 +320,43 @@ __global__ __launch_bounds__(1024) void raster_bwd_kernel(const RasterArgs A, co
                 sb = fmaf(w, col.z, sb);
                 sa += w;
                 if (alpha_raw <= kAlphaMax) {
-                    vop = dal * gauss;
+                    v[8] = dal * gauss;
                     const float dpow = dal * op * gauss;
-                    vu = dpow * (con.x * dx + con.y * dy);
-                    vv = dpow * (con.y * dx + con.z * dy);
-                    vka = -0.5f * dpow * dx * dx;
-                    vkb = -dpow * dx * dy;
-                    vkc = -0.5f * dpow * dy * dy;
-                    if (want_abs) vabs = sqrtf(vu * vu + vv * vv);
+                    v[3] = dpow * (con.x * dx + con.y * dy);
+                    v[4] = dpow * (con.y * dx + con.z * dy);
+                    v[5] = -0.5f * dpow * dx * dx;
+                    v[6] = -dpow * dx * dy;
+                    v[7] = -0.5f * dpow * dy * dy;
+                    if (want_abs) v[9] = sqrtf(v[3] * v[3] + v[4] * v[4]);
                 }
             }
-            vcr = wave_sum_to_lane63(vcr);
-            vcg = wave_sum_to_lane63(vcg);
-            vcb = wave_sum_to_lane63(vcb);
-            vu = wave_sum_to_lane63(vu);
-            vv = wave_sum_to_lane63(vv);
-            vka = wave_sum_to_lane63(vka);
-            vkb = wave_sum_to_lane63(vkb);
-            vkc = wave_sum_to_lane63(vkc);
-            vop = wave_sum_to_lane63(vop);
-            if (want_abs) vabs = wave_sum_to_lane63(vabs);
+            const int nq = want_abs ? kGradSlots : kGradSlots - 1;
+#pragma unroll
+            for (int q = 0; q < kGradSlots; ++q)
+                if (q < nq) v[q] = wave_sum_to_lane63(v[q]);
             if (lane == 63) {
-                const int g = S.id[j];
-                if (vcr != 0.f) unsafeAtomicAdd(G.d_col + 3 * g, vcr);
-                if (vcg != 0.f) unsafeAtomicAdd(G.d_col + 3 * g + 1, vcg);
-                if (vcb != 0.f) unsafeAtomicAdd(G.d_col + 3 * g + 2, vcb);
-                if (vu != 0.f) unsafeAtomicAdd(G.d_uv + 2 * g, vu);
-                if (vv != 0.f) unsafeAtomicAdd(G.d_uv + 2 * g + 1, vv);
-                if (vka != 0.f) unsafeAtomicAdd(G.d_conic + 3 * g, vka);
-                if (vkb != 0.f) unsafeAtomicAdd(G.d_conic + 3 * g + 1, vkb);
-                if (vkc != 0.f) unsafeAtomicAdd(G.d_conic + 3 * g + 2, vkc);
-                if (vop != 0.f) unsafeAtomicAdd(G.d_op + g, vop);
-                if (want_abs && vabs != 0.f) unsafeAtomicAdd(G.d_abs + g, vabs);
+#pragma unroll
+                for (int q = 0; q < kGradSlots; ++q)
+                    if (q < nq && v[q] != 0.f) atomicAdd(&S.grad[q][j], v[q]);
             }
+        }
+        __syncthreads();
+        // One thread per batch entry publishes the tile's sums.
+        for (int t = threadIdx.x; t < n; t += blockDim.x) {
+            const int g = S.id[t];
+            float s[kGradSlots];
+#pragma unroll
+            for (int q = 0; q < kGradSlots; ++q) s[q] = S.grad[q][t];
+            if (s[0] != 0.f) unsafeAtomicAdd(G.d_col + 3 * g, s[0]);
+            if (s[1] != 0.f) unsafeAtomicAdd(G.d_col + 3 * g + 1, s[1]);
+            if (s[2] != 0.f) unsafeAtomicAdd(G.d_col + 3 * g + 2, s[2]);
+            if (s[3] != 0.f) unsafeAtomicAdd(G.d_uv + 2 * g, s[3]);
+            if (s[4] != 0.f) unsafeAtomicAdd(G.d_uv + 2 * g + 1, s[4]);
+            if (s[5] != 0.f) unsafeAtomicAdd(G.d_conic + 3 * g, s[5]);
+            if (s[6] != 0.f) unsafeAtomicAdd(G.d_conic + 3 * g + 1, s[6]);
+            if (s[7] != 0.f) unsafeAtomicAdd(G.d_conic + 3 * g + 2, s[7]);
+            if (s[8] != 0.f) unsafeAtomicAdd(G.d_op + g, s[8]);
+            if (want_abs && s[9] != 0.f) unsafeAtomicAdd(G.d_abs + g, s[9]);
         }
     }
 }
@@ -389,8 +415,12 @@ int32_t mg_rasterize_forward(int64_t N, const float *uv, const float *conic, con
     const int threads = ((tile * tile + 63) / 64) * 64;
     const int grid = (int)ceil_div(A.n_tiles, kXcds) * kXcds;
     TimedScope ts("rasterize_forward", as_stream(stream));
-    raster_fwd_kernel<<<grid, threads, 0, as_stream(stream)>>>(A, out_rgb, out_alpha, out_T,
-                                                               out_stop);
+    if (threads <= 4 * 64)
+        raster_fwd_kernel<4><<<grid, threads, 0, as_stream(stream)>>>(A, out_rgb, out_alpha,
+                                                                       out_T, out_stop);
+    else
+        raster_fwd_kernel<kMaxWaves><<<grid, threads, 0, as_stream(stream)>>>(
+            A, out_rgb, out_alpha, out_T, out_stop);
     MG_LAUNCHED("raster_fwd_kernel");
     return MG_OK;
 }
@@ -423,7 +453,10 @@ int32_t mg_rasterize_backward(int64_t N, const float *uv, const float *conic,
     const int threads = ((tile * tile + 63) / 64) * 64;
     const int grid = (int)ceil_div(A.n_tiles, kXcds) * kXcds;
     TimedScope ts("rasterize_backward", s);
-    raster_bwd_kernel<<<grid, threads, 0, s>>>(A, Gr);
+    if (threads <= 4 * 64)
+        raster_bwd_kernel<4><<<grid, threads, 0, s>>>(A, Gr);
+    else
+        raster_bwd_kernel<kMaxWaves><<<grid, threads, 0, s>>>(A, Gr);
     MG_LAUNCHED("raster_bwd_kernel");
     return MG_OK;
 }

@@ -13,6 +13,7 @@
 // wave w, lane l is item r*256 + w*64 + l of the tile, and tiles are ranked
 // in tile order by the scan.
 #include "mg_common.h"
+#include "mg_sort.h"
 
 namespace mg {
 
@@ -210,20 +211,24 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
 }
 
 // Workspace: hist (kRadix * ntiles) + totals (kRadix), uint32.
-inline int64_t sort_ws_bytes(int64_t n) {
+int64_t sort_ws_bytes(int64_t n) {
     const int64_t ntiles = ceil_div(n > 0 ? n : 1, kSortTile);
     return (kRadix * ntiles + kRadix) * (int64_t)sizeof(uint32_t);
 }
 
+// Runs the passes; on return *res_k / *res_v point at whichever ping-pong
+// buffer holds the sorted data (keys_out when the pass count is odd).
 template <typename K>
-int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *vals_out,
-                         int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
-                         hipStream_t s, const char *who) {
+int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *vals_out,
+                          int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
+                          hipStream_t s, const char *who, K **res_k, int32_t **res_v) {
     MG_REQUIRE(n >= 0 && n < (1LL << 31), "%s: n = %lld", who, (long long)n);
     MG_REQUIRE(begin_bit >= 0 && end_bit <= (int)(8 * sizeof(K)) && begin_bit <= end_bit,
                "%s: bit range [%d, %d)", who, begin_bit, end_bit);
     MG_REQUIRE(ws && ws_bytes >= sort_ws_bytes(n), "%s: workspace %lld bytes, need %lld", who,
                (long long)ws_bytes, (long long)sort_ws_bytes(n));
+    *res_k = keys_in;
+    *res_v = vals_in;
     if (n == 0) return MG_OK;
     MG_REQUIRE(keys_in && vals_in && keys_out && vals_out, "%s: null buffer", who);
     const int64_t ntiles = ceil_div(n, kSortTile);
@@ -231,9 +236,8 @@ int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *val
     uint32_t *totals = hist + kRadix * ntiles;
     K *src_k = keys_in, *dst_k = keys_out;
     int32_t *src_v = vals_in, *dst_v = vals_out;
-    int passes = 0;
-    TimedScope ts("radix_sort", s);
-    for (int b = begin_bit; b < end_bit; b += 8, ++passes) {
+    TimedScope ts(who, s);
+    for (int b = begin_bit; b < end_bit; b += 8) {
         const int width = min(8, end_bit - b);
         const uint32_t mask = (1u << width) - 1u;
         radix_upsweep_kernel<K><<<(unsigned)ntiles, kSortThreads, 0, s>>>(src_k, n, b, mask, hist,
@@ -247,13 +251,34 @@ int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *val
         K *tk = src_k; src_k = dst_k; dst_k = tk;
         int32_t *tv = src_v; src_v = dst_v; dst_v = tv;
     }
-    // After the loop src_* holds the sorted data.
-    if (src_k != keys_out) {
-        MG_HIP(hipMemcpyAsync(keys_out, src_k, n * sizeof(K), hipMemcpyDeviceToDevice, s));
-        MG_HIP(hipMemcpyAsync(vals_out, src_v, n * sizeof(int32_t), hipMemcpyDeviceToDevice, s));
+    *res_k = src_k;      // after the last swap src_* holds the sorted data
+    *res_v = src_v;
+    return MG_OK;
+}
+
+template <typename K>
+int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *vals_out,
+                         int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
+                         hipStream_t s, const char *who) {
+    K *rk;
+    int32_t *rv;
+    int32_t rc = radix_sort_passes<K>(keys_in, vals_in, keys_out, vals_out, n, begin_bit,
+                                      end_bit, ws, ws_bytes, s, who, &rk, &rv);
+    if (rc != MG_OK) return rc;
+    if (n > 0 && rk != keys_out) {
+        MG_HIP(hipMemcpyAsync(keys_out, rk, n * sizeof(K), hipMemcpyDeviceToDevice, s));
+        MG_HIP(hipMemcpyAsync(vals_out, rv, n * sizeof(int32_t), hipMemcpyDeviceToDevice, s));
     }
     return MG_OK;
 }
+
+template int32_t radix_sort_pairs<uint32_t>(uint32_t *, int32_t *, uint32_t *, int32_t *, int64_t,
+                                            int, int, void *, int64_t, hipStream_t, const char *);
+template int32_t radix_sort_pairs<uint64_t>(uint64_t *, int32_t *, uint64_t *, int32_t *, int64_t,
+                                            int, int, void *, int64_t, hipStream_t, const char *);
+template int32_t radix_sort_passes<uint32_t>(uint32_t *, int32_t *, uint32_t *, int32_t *,
+                                             int64_t, int, int, void *, int64_t, hipStream_t,
+                                             const char *, uint32_t **, int32_t **);
 
 }  // namespace mg
 
@@ -268,7 +293,7 @@ int32_t mg_sort_pairs_u64(uint64_t *keys_in, int32_t *vals_in, uint64_t *keys_ou
                           void *workspace, int64_t workspace_bytes, mg_stream_t stream) {
     return radix_sort_pairs<uint64_t>(keys_in, vals_in, keys_out, vals_out, n, begin_bit,
                                       end_bit, workspace, workspace_bytes, as_stream(stream),
-                                      "mg_sort_pairs_u64");
+                                      "radix_sort");
 }
 
 }  // extern "C"

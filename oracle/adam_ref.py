@@ -34,8 +34,10 @@ def adam_step(p, g, m, v, lr, b1, b2, eps, step):
     step_size = f32(lr / bc1)
     inv_sqrt_bc2 = f32(1.0 / math.sqrt(bc2))
     b1f, b2f = f32(b1), f32(b2)
-    m[:] = b1f * m + (f32(1.0) - b1f) * g
-    v[:] = b2f * v + (f32(1.0) - b2f) * g * g
+    # torch scales the gradient by (1 - beta) formed in double (lerp weight,
+    # addcmul value), not by 1 - fp32(beta).
+    m[:] = b1f * m + f32(1.0 - b1) * g
+    v[:] = b2f * v + f32(1.0 - b2) * g * g
     p[:] = p - step_size * m / (np.sqrt(v) * inv_sqrt_bc2 + f32(eps))
 
 
@@ -44,8 +46,8 @@ def dense_eps_inside_step(p, g, m, v, lr, b1, b2, eps, step):
     bc2 = 1.0 - math.pow(b2, step)
     step_size = f32(lr * math.sqrt(bc2) / bc1)
     b1f, b2f = f32(b1), f32(b2)
-    m[:] = b1f * m + (f32(1.0) - b1f) * g
-    v[:] = b2f * v + (f32(1.0) - b2f) * g * g
+    m[:] = b1f * m + f32(1.0 - b1) * g
+    v[:] = b2f * v + f32(1.0 - b2) * g * g
     p[:] = p - step_size * m / (np.sqrt(v) + f32(eps))
 
 
@@ -66,8 +68,8 @@ def selective_adam_step(p, g, m, v, steps, visible, lr, b1, b2, eps):
     step_size = f32(lr) * (np.sqrt(f32(1.0) - pw2) / (f32(1.0) - pw1))
     shape = (-1,) + (1,) * (p.ndim - 1)
     gs = g[idx]
-    mm = m[idx] * b1f + gs * (f32(1.0) - b1f)
-    vv = v[idx] * b2f + gs * gs * (f32(1.0) - b2f)
+    mm = m[idx] * b1f + gs * f32(1.0 - b1)
+    vv = v[idx] * b2f + gs * gs * f32(1.0 - b2)
     m[idx] = mm
     v[idx] = vv
     p[idx] = p[idx] - step_size.reshape(shape) * mm / (np.sqrt(vv) + f32(eps))

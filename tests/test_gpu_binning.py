@@ -43,18 +43,31 @@ def gpu_preprocess(s, dev, viewmat=None):
             cc, 3)
 
 
+def keys_of(gids, offs, depth):
+    """Sorted 64-bit keys implied by a list: (tile << 32) | bits(depth[id])."""
+    tiles = np.repeat(np.arange(offs.size - 1, dtype=np.uint64), np.diff(offs))
+    dbits = depth.astype(np.float32).view(np.uint32).astype(np.uint64)[gids]
+    return (tiles << np.uint64(32)) | dbits
+
+
 def run_both(s, dev, tile, ellipse=True):
-    from metal_gauss_amd.backend import _bin
+    """GPU lists from both pipelines (depth-first, and the 64-bit-key ABI
+    chain) and the oracle's; the two GPU pipelines must agree exactly."""
+    from metal_gauss_amd.backend import _bin, _bin_keys64
 
     uv, conic, depth, rxy, valid, _ = gpu_preprocess(s, dev)
     op = s["op"].to(dev)
-    gids, offs, tx, skeys = _bin(uv, rxy, depth, valid, conic if ellipse else None,
-                                 op if ellipse else None, s["W"], s["H"], tile)
+    args = (uv, rxy, depth, valid, conic if ellipse else None, op if ellipse else None,
+            s["W"], s["H"], tile)
+    gids, offs, tx = (t.cpu().numpy() if hasattr(t, "cpu") else t for t in _bin(*args))
+    g64, o64, _, k64 = _bin_keys64(*args)
     cpu = [t.cpu().numpy() for t in (uv, rxy, conic, op, valid, depth)]
+    skeys = keys_of(gids, offs, cpu[5])
+    assert np.array_equal(g64.cpu().numpy(), gids) and np.array_equal(o64.cpu().numpy(), offs)
+    assert np.array_equal(k64.cpu().numpy().view(np.uint64), skeys)
     rids, roffs, rtx, rkeys = binning_ref.build_tile_lists(
         cpu[0], cpu[1], cpu[2], cpu[3], cpu[4], cpu[5], s["W"], s["H"], tile, ellipse=ellipse)
-    return (gids.cpu().numpy(), offs.cpu().numpy(), tx, skeys.cpu().numpy().view(np.uint64)), \
-        (rids, roffs, rtx, rkeys)
+    return (gids, offs, tx, skeys), (rids, roffs, rtx, rkeys)
 
 
 @pytest.mark.parametrize("tile", [8, 12, 16, 32])
@@ -141,13 +154,14 @@ def test_config2_scale_bit_exact(dev):
         uv, conic, depth, rxy, valid, _ = _PreprocessMetal.apply(
             m.to(dev), q.to(dev), sca.to(dev), sh.to(dev), None, op.to(dev), vm_h, fx, fy, cx, cy,
             cam.W, cam.H, 0.01, 100.0, 0.3, float(max(cam.W, cam.H)), cc, 3)
-    gids, offs, tx, skeys = _bin(uv, rxy, depth, valid, conic, op.to(dev), cam.W, cam.H, 16)
+    gids, offs, tx = _bin(uv, rxy, depth, valid, conic, op.to(dev), cam.W, cam.H, 16)
     cpu = [t.cpu().numpy() for t in (uv, rxy, conic, op, valid, depth)]
     rids, roffs, _, rkeys = binning_ref.build_tile_lists(*cpu, cam.W, cam.H, 16)
     print(f"config 2: {int(valid.sum())} valid of {m.shape[0]}, {rids.size} intersections")
-    assert np.array_equal(skeys.cpu().numpy().view(np.uint64), rkeys)
-    assert np.array_equal(gids.cpu().numpy(), rids)
-    assert np.array_equal(offs.cpu().numpy(), roffs)
+    gids, offs = gids.cpu().numpy(), offs.cpu().numpy()
+    assert np.array_equal(keys_of(gids, offs, cpu[5]), rkeys)
+    assert np.array_equal(gids, rids)
+    assert np.array_equal(offs, roffs)
 
 
 # ------------------------------------------------------------- primitives
