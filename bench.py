@@ -36,9 +36,20 @@ METRIC = "train steps/sec & fwd+bwd ms at 1M Gaussians 800×800 SH3; % HBM roofl
 HBM_PEAK_GBS = 8000.0
 
 # Kernels timed by the library (names used in mg_timing_query).
-KERNELS = ["preprocess_forward", "bin_count", "exclusive_scan", "bin_write", "radix_sort",
-           "tile_ranges", "rasterize_forward", "rasterize_backward", "preprocess_backward",
-           "ssim_fused_forward", "ssim_fused_backward", "adam_step"]
+KERNELS = ["preprocess_forward", "bin_count", "depth_sort", "exclusive_scan", "bin_write",
+           "tile_sort", "tile_ranges", "rasterize_forward", "rasterize_backward",
+           "preprocess_backward", "ssim_fused_forward", "ssim_fused_backward", "adam_step"]
+
+# Library timing label -> the kernel name rocprofv3 reports for it (the sorts
+# run three kernels per pass and are left out of the counter summary).
+PROF_NAMES = {
+    "preprocess_forward": "preprocess_fwd_kernel", "preprocess_backward": "preprocess_bwd_kernel",
+    "bin_count": "bin_count_rec_kernel", "bin_write": "bin_write_rec_kernel",
+    "tile_ranges": "tile_ranges_u32_kernel", "rasterize_forward": "raster_fwd_kernel",
+    "rasterize_backward": "raster_bwd_kernel", "ssim_fused_forward": "ssim_fused_fwd_kernel",
+    "ssim_fused_backward": "ssim_fused_bwd_kernel", "adam_step": "adam_multi_kernel",
+}
+TRAFFIC_FILE = ROOT / "profiles" / "pmc_traffic_config4.txt"
 
 
 def parse():
@@ -49,6 +60,10 @@ def parse():
     ap.add_argument("--gaussians", type=int, default=1_000_000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-only", action="store_true", help="time only the CPU baseline")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print the HBM traffic summary of two rocprofv3 --pmc runs and exit")
+    ap.add_argument("--stats-summary", metavar="KERNEL_STATS_CSV",
+                    help="print a rocprofv3 kernel-stats summary and exit")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first copy this many MiB device-to-device 3 times (a plain copy of "
                          "known size, to calibrate the FETCH_SIZE / WRITE_SIZE counters)")
@@ -125,11 +140,12 @@ def algorithmic_bytes(kernel, N, I, P, T, f_valid, n_floats):
     return {
         "preprocess_forward": (92 + 192 * f_valid) * N,
         "preprocess_backward": (308 + 192 * f_valid) * N,
-        "bin_count": 40 * N,
-        "exclusive_scan": 8 * N,
-        "bin_write": 44 * N + 12 * I,
-        "radix_sort": 24 * I,
-        "tile_ranges": 8 * I + 4 * (T + 1),
+        "bin_count": 84 * N,                      # 40 B read; count, key, id, 32 B record
+        "depth_sort": 3 * 20 * N,                 # 3 passes (24 varying depth bits at config 4)
+        "exclusive_scan": 12 * N,                 # counts + order read, offsets written
+        "bin_write": 40 * N + 8 * I,              # order, offset, record; key + id per pair
+        "tile_sort": 2 * 20 * I,                  # 2 passes at 50x50 tiles
+        "tile_ranges": 4 * I + 4 * (T + 1),
         "rasterize_forward": 40 * I + 24 * P + 8 * T,
         "rasterize_backward": 40 * I + 24 * P + 36 * N,
         "ssim_fused_forward": 60 * P,
@@ -191,6 +207,102 @@ def gpu_bench(args):
                               / (v[0] * 1e-3) / 1e9, 1)} for k, v in kern.items()}
     return dict(ms=ms, fb_ms=fb_ms, kernels=rows, dominant=dominant, achieved=achieved,
                 nbytes=nbytes, I=I, f_valid=f_valid, n_floats=n_floats)
+
+
+PMC_REGEX = ("raster_bwd|raster_fwd|adam_multi|preprocess_fwd|preprocess_bwd|radix_|scan_|"
+             "bin_write|bin_count|copyBuffer")
+
+
+def _counter_rows(d):
+    import csv
+
+    files = sorted(Path(d).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    with open(files[0], newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _per_kernel(rows):
+    acc = {}
+    for r in rows:
+        acc.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return acc
+
+
+def pmc_summary(fetch_dir, write_dir, copy_mib):
+    """Text summary of HBM traffic per launch from two rocprofv3 --pmc runs.
+
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are each scaled by what they
+    read for the run's own plain copy of copy_mib MiB (its largest
+    __amd_rocclr_copyBuffer dispatch), which reads and writes exactly that
+    many bytes.
+    """
+    fetch = _per_kernel(_counter_rows(fetch_dir))
+    write = _per_kernel(_counter_rows(write_dir))
+    nbytes = copy_mib * (1 << 20)
+    cf = nbytes / (max(fetch["__amd_rocclr_copyBuffer"]) * 1024)
+    cw = nbytes / (max(write["__amd_rocclr_copyBuffer"]) * 1024)
+    lines = [
+        "# HBM traffic per launch, config-4 step (1M Gaussians SH3, 800x800, tile 16), MI355X",
+        "# made by (from the repository root, TMPDIR=/tmp):",
+        f"#   rocprofv3 --pmc FETCH_SIZE --kernel-include-regex '{PMC_REGEX}' -f csv -T "
+        "-d F -o pmc -- python -u bench.py --steps 3 --warmup 2 --no-cpu-baseline "
+        f"--copy-mib {copy_mib}",
+        "#   (the same with --pmc WRITE_SIZE -d W)",
+        f"#   python bench.py --pmc-summary F W --copy-mib {copy_mib}",
+        f"# calibration: a {copy_mib} MiB device copy reads FETCH_SIZE "
+        f"{max(fetch['__amd_rocclr_copyBuffer']):.0f} KiB (factor {cf:.3f}) and WRITE_SIZE "
+        f"{max(write['__amd_rocclr_copyBuffer']):.0f} KiB (factor {cw:.3f})",
+        "# traffic_bytes = factor_f * FETCH_SIZE + factor_w * WRITE_SIZE, mean per dispatch",
+        f"{'kernel':28s} {'dispatches':>10s} {'FETCH_KiB':>12s} {'WRITE_KiB':>12s} "
+        f"{'read_MB':>9s} {'write_MB':>9s} {'traffic_bytes':>14s}",
+    ]
+    for name in sorted(fetch):
+        if name == "__amd_rocclr_copyBuffer" or name not in write:
+            continue
+        fk = sum(fetch[name]) / len(fetch[name])
+        wk = sum(write[name]) / len(write[name])
+        rd, wr = cf * fk * 1024, cw * wk * 1024
+        lines.append(f"{name:28s} {len(fetch[name]):10d} {fk:12.1f} {wk:12.1f} "
+                     f"{rd / 1e6:9.2f} {wr / 1e6:9.2f} {int(rd + wr):14d}")
+    return "\n".join(lines)
+
+
+def stats_summary(stats_csv, steps):
+    """Text summary of a rocprofv3 --kernel-trace --stats kernel_stats.csv."""
+    import csv
+
+    with open(stats_csv, newline="") as f:
+        rows = list(csv.DictReader(f))
+    total = sum(float(r["TotalDurationNs"]) for r in rows)
+    lines = [
+        "# rocprofv3 kernel statistics, config-4 step (1M Gaussians SH3, 800x800, tile 16), MI355X",
+        "# made by (from the repository root, TMPDIR=/tmp):",
+        "#   rocprofv3 --kernel-trace --stats -f csv -T -d P -o kt -- python -u bench.py "
+        f"--steps {steps} --warmup 5 --no-cpu-baseline",
+        "#   python bench.py --stats-summary P/kt_kernel_stats.csv",
+        "# The run covers warmup + timed steps + the fwd+bwd-only loop + 10 per-kernel timing "
+        "steps.",
+        f"{'kernel':36s} {'calls':>7s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'share_%':>8s}",
+    ]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        lines.append(f"{r['Name'][:36]:36s} {int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.1f} "
+                     f"{float(r['MinNs']) / 1e3:9.1f} {float(r['MaxNs']) / 1e3:9.1f} "
+                     f"{100 * float(r['TotalDurationNs']) / total:8.2f}")
+    return "\n".join(lines)
+
+
+def committed_traffic(label):
+    """HBM bytes per launch of a kernel from the committed PMC summary, or None."""
+    name = PROF_NAMES.get(label)
+    if name is None or not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        parts = line.split()
+        if parts and parts[0] == name and not line.startswith("#"):
+            return int(parts[-1])
+    return None
 
 
 def cpu_baseline(n_gaussians=1_000_000, crop=96):
@@ -279,6 +391,12 @@ def main():
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported by this build "
               f"(the splatting step has no multi-GPU path here).", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_summary:
+        print(pmc_summary(*args.pmc_summary, args.copy_mib or 1024))
+        return
+    if args.stats_summary:
+        print(stats_summary(args.stats_summary, 20))
+        return
     if args.cpu_only:
         print(json.dumps(cpu_baseline(args.gaussians)))
         return
@@ -314,7 +432,8 @@ def main():
         "roofline": {
             "bound": "hbm", "kernel": r["dominant"], "achieved": round(r["achieved"], 2),
             "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(r["achieved"] / HBM_PEAK_GBS, 5), "traffic": None,
+            "frac": round(r["achieved"] / HBM_PEAK_GBS, 5),
+            "traffic": committed_traffic(r["dominant"]),
             "algorithmic_bytes_per_launch": int(r["nbytes"]),
         },
         "kernels": r["kernels"],

@@ -163,11 +163,13 @@ int32_t mg_tile_ranges(const uint64_t *sorted_keys, int64_t n,
  * intersection total.
  *
  * begin: per-Gaussian tile counts (the exact ellipse test, as mg_bin_count),
- * a stable 32-bit radix sort of all Gaussians by depth (invalid last), and
- * the exclusive scan of the counts in depth order; the total goes to
- * total_host (host; the stream is synchronised) when not NULL. The
- * workspace (mg_bin_lists_workspace_bytes(N)) carries state to finish and
- * must not be touched in between.
+ * then one synchronous host read of the intersection total and of the depth
+ * range of the Gaussians that claim a tile, then a stable 32-bit radix sort
+ * of all Gaussians by depth on only the bits in which those depths differ,
+ * and the exclusive scan of the counts in depth order. The total goes to
+ * total_host (host) when not NULL; the stream is always synchronised once.
+ * The workspace (mg_bin_lists_workspace_bytes(N)) carries state to finish
+ * and must not be touched in between.
  *
  * finish: emits each Gaussian's (tile id, Gaussian id) pairs in depth order,
  * stably radix-sorts them by tile id on ceil(log2(tiles_x*tiles_y)) bits and

@@ -1,5 +1,7 @@
 // Tile binning: per-Gaussian tile count, exclusive scan, (tile|depth) key
-// emission and tile ranges over the sorted keys.
+// emission and tile ranges over the sorted keys, plus the depth-first
+// pipeline (mg_bin_lists_begin/finish) that builds the same lists with two
+// cheaper sorts.
 //
 // Membership follows metal_gauss/csrc/binning.metal:25-90 and
 // metal_backend.py:149-189: a Gaussian claims tile t when the minimum of its
@@ -8,7 +10,7 @@
 // change no pixel. Keys and order are an integer contract that the CPU oracle
 // reproduces bit for bit, so the float work here is written to be
 // reproducible:
-//   * FP contraction is off in min_q_over_rect (no fused multiply-adds), so
+//   * FP contraction is off in the tile walk (no fused multiply-adds), so
 //     every product and sum rounds exactly as a scalar fp32 CPU evaluation of
 //     the same expression does;
 //   * division is IEEE (hipcc's default correctly rounded fp32 divide);
@@ -21,28 +23,6 @@
 namespace mg {
 
 constexpr int kBinThreads = 256;
-
-__device__ __noinline__ float min_q_over_rect(float mux, float muy, float ca, float cb,
-                                              float cc, float x0, float x1, float y0,
-                                              float y1) {
-#pragma clang fp contract(off)
-    if (mux >= x0 && mux <= x1 && muy >= y0 && muy <= y1) return 0.0f;
-    const float a = fmaxf(ca, 1e-12f), b = cb, c = fmaxf(cc, 1e-12f);
-    float best = __builtin_inff();
-    for (int e = 0; e < 2; ++e) {            // horizontal edges: minimise over x
-        const float yc = e == 0 ? y0 : y1;
-        const float xs = fminf(fmaxf(mux - b * (yc - muy) / a, x0), x1);
-        const float ex = xs - mux, ey = yc - muy;
-        best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
-    }
-    for (int e = 0; e < 2; ++e) {            // vertical edges: minimise over y
-        const float xc = e == 0 ? x0 : x1;
-        const float ys = fminf(fmaxf(muy - b * (xc - mux) / c, y0), y1);
-        const float ex = xc - mux, ey = ys - muy;
-        best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
-    }
-    return best;
-}
 
 // 2 ln(255 op), correctly rounded to fp32; 0 when the Gaussian can never reach
 // alpha 1/255 (it then claims no tiles).
@@ -59,11 +39,21 @@ struct BinArgs {
     int32_t W, H, tile, tiles_x, tiles_y;
 };
 
-// The walk shared by both passes: rows of tiles outer, columns inner, so the
-// emission order is (Gaussian, ty, tx) as in binning.metal:74-77.
-template <bool WRITE>
-__device__ __forceinline__ int bin_walk(const BinArgs &A, int64_t g, uint64_t *keys,
-                                        int32_t *ids, int64_t at) {
+// Everything the tile walk needs for one Gaussian, in one 32-byte sector:
+// the centre, the conic with its diagonal clamped at 1e-12, the level
+// threshold and the clamped tile rectangle (x0 | x1 << 16, y0 | y1 << 16).
+// The count pass writes it in Gaussian order; the write pass gathers it in
+// depth order, one sector per Gaussian instead of six scattered arrays.
+struct __align__(16) BinRec {
+    float ux, uy, a, b;
+    float c, thr;
+    uint32_t xs, ys;
+};
+
+// False when the Gaussian claims no tile (invalid, or alpha below 1/255 at
+// every point).
+__device__ __forceinline__ bool make_rec(const BinArgs &A, int64_t g, BinRec &r) {
+    if (A.valid[g] == 0) return false;
     const float ux = A.uv[2 * g], uy = A.uv[2 * g + 1];
     const float rx = A.rxy[2 * g], ry = A.rxy[2 * g + 1];
     const float tf = (float)A.tile;
@@ -73,33 +63,82 @@ __device__ __forceinline__ int bin_walk(const BinArgs &A, int64_t g, uint64_t *k
     x1 = min(max(x1, 0), A.tiles_x - 1);
     y0 = min(max(y0, 0), A.tiles_y - 1);
     y1 = min(max(y1, 0), A.tiles_y - 1);
+    r.ux = ux;
+    r.uy = uy;
+    r.xs = (uint32_t)x0 | ((uint32_t)x1 << 16);
+    r.ys = (uint32_t)y0 | ((uint32_t)y1 << 16);
+    r.a = r.b = r.c = r.thr = 0.0f;
     // Without a conic (the circular-bounds caller of metal_backend.py:111-147)
     // every tile of the rectangle is claimed.
-    const bool test = A.conic != nullptr;
-    float thr = 0.f, ca = 0.f, cb = 0.f, cc = 0.f;
-    if (test) {
+    if (A.conic != nullptr) {
         bool live;
-        thr = level_threshold(A.opac[g], live);
-        if (!live) return 0;
-        ca = A.conic[3 * g]; cb = A.conic[3 * g + 1]; cc = A.conic[3 * g + 2];
+        r.thr = level_threshold(A.opac[g], live);
+        if (!live) return false;
+        r.a = fmaxf(A.conic[3 * g], 1e-12f);
+        r.b = A.conic[3 * g + 1];
+        r.c = fmaxf(A.conic[3 * g + 2], 1e-12f);
     }
-    uint64_t dbits = 0;
-    if (WRITE) dbits = (uint64_t)__float_as_uint(A.depth[g]);
+    return true;
+}
+
+// Walks the rectangle, rows outer and columns inner (binning.metal:74-77),
+// calling emit(n, tile_id) for the n-th claimed tile; returns the count.
+//
+// A tile is claimed when the minimum over the tile rectangle of
+// q(d) = a dx^2 + 2 b dx dy + c dy^2 is below the threshold. The minimum is 0
+// when the centre lies inside; otherwise it lies on an edge. On a horizontal
+// edge y = yc the unconstrained minimiser is x = ux - b (yc - uy) / a,
+// clamped to the edge; on a vertical edge x = xc it is
+// y = uy - b (xc - ux) / c. That minimiser depends on the edge line alone,
+// so it is computed once per row boundary and once per column boundary and
+// shared by the tiles on either side. Every value is the same fp32
+// expression the oracle evaluates per tile, so each decision is bit-exact.
+// FP contraction is off: every product and sum rounds separately.
+template <typename Emit>
+__device__ __forceinline__ int rec_walk(const BinRec &r, bool test, int tile, int W, int H,
+                                        int tiles_x, Emit emit) {
+#pragma clang fp contract(off)
+    const int x0 = (int)(r.xs & 0xffffu), x1 = (int)(r.xs >> 16);
+    const int y0 = (int)(r.ys & 0xffffu), y1 = (int)(r.ys >> 16);
     int n = 0;
+    if (!test) {
+        for (int ty = y0; ty <= y1; ++ty)
+            for (int tx = x0; tx <= x1; ++tx) emit(n++, (uint32_t)(ty * tiles_x + tx));
+        return n;
+    }
+    const float mux = r.ux, muy = r.uy, a = r.a, b = r.b, c = r.c;
+    float ry0 = (float)(y0 * tile);
+    float u0 = mux - b * (ry0 - muy) / a;
     for (int ty = y0; ty <= y1; ++ty) {
-        const float ry0 = (float)(ty * A.tile);
-        const float ry1 = fminf((float)((ty + 1) * A.tile), (float)A.H);
+        const float ry1 = fminf((float)((ty + 1) * tile), (float)H);
+        const float u1 = mux - b * (ry1 - muy) / a;
+        const float ey0 = ry0 - muy, ey1 = ry1 - muy;
+        const bool yin = muy >= ry0 && muy <= ry1;
+        float rx0 = (float)(x0 * tile);
+        float v0 = muy - b * (rx0 - mux) / c;
         for (int tx = x0; tx <= x1; ++tx) {
-            const float rx0 = (float)(tx * A.tile);
-            const float rx1 = fminf((float)((tx + 1) * A.tile), (float)A.W);
-            if (test && min_q_over_rect(ux, uy, ca, cb, cc, rx0, rx1, ry0, ry1) >= thr) continue;
-            if (WRITE) {
-                const uint64_t tid = (uint64_t)(ty * A.tiles_x + tx);
-                keys[at + n] = (tid << 32) | dbits;
-                ids[at + n] = (int32_t)g;
+            const float rx1 = fminf((float)((tx + 1) * tile), (float)W);
+            const float v1 = muy - b * (rx1 - mux) / c;
+            bool claim = yin && mux >= rx0 && mux <= rx1;
+            if (!claim) {
+                float ex = fminf(fmaxf(u0, rx0), rx1) - mux;
+                float best = a * ex * ex + 2.0f * b * ex * ey0 + c * ey0 * ey0;
+                ex = fminf(fmaxf(u1, rx0), rx1) - mux;
+                best = fminf(best, a * ex * ex + 2.0f * b * ex * ey1 + c * ey1 * ey1);
+                float ey = fminf(fmaxf(v0, ry0), ry1) - muy;
+                ex = rx0 - mux;
+                best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
+                ey = fminf(fmaxf(v1, ry0), ry1) - muy;
+                ex = rx1 - mux;
+                best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
+                claim = best < r.thr;
             }
-            ++n;
+            if (claim) emit(n++, (uint32_t)(ty * tiles_x + tx));
+            rx0 = rx1;      // equal to (tx + 1) * tile unless this is the last column
+            v0 = v1;
         }
+        ry0 = ry1;          // likewise for rows
+        u0 = u1;
     }
     return n;
 }
@@ -107,15 +146,26 @@ __device__ __forceinline__ int bin_walk(const BinArgs &A, int64_t g, uint64_t *k
 __global__ __launch_bounds__(kBinThreads) void bin_count_kernel(const BinArgs A, int32_t *counts) {
     const int64_t g = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
     if (g >= A.N) return;
-    counts[g] = A.valid[g] == 0 ? 0 : bin_walk<false>(A, g, nullptr, nullptr, 0);
+    BinRec r;
+    int n = 0;
+    if (make_rec(A, g, r))
+        n = rec_walk(r, A.conic != nullptr, A.tile, A.W, A.H, A.tiles_x, [](int, uint32_t) {});
+    counts[g] = n;
 }
 
 __global__ __launch_bounds__(kBinThreads) void bin_write_kernel(const BinArgs A,
                                                                 const int32_t *offsets,
                                                                 uint64_t *keys, int32_t *ids) {
     const int64_t g = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
-    if (g >= A.N || A.valid[g] == 0) return;
-    bin_walk<true>(A, g, keys, ids, offsets[g]);
+    if (g >= A.N) return;
+    BinRec r;
+    if (!make_rec(A, g, r)) return;
+    const uint64_t dbits = (uint64_t)__float_as_uint(A.depth[g]);
+    const int64_t at = offsets[g];
+    rec_walk(r, A.conic != nullptr, A.tile, A.W, A.H, A.tiles_x, [&](int n, uint32_t t) {
+        keys[at + n] = ((uint64_t)t << 32) | dbits;
+        ids[at + n] = (int32_t)g;
+    });
 }
 
 // ------------------------------------------------------------------- scan
@@ -150,16 +200,23 @@ __device__ __forceinline__ int64_t block_excl_scan(int64_t v, int64_t *s_wave, i
     return before + incl - v;
 }
 
+// With idx, in[idx[i]] is gathered once and stored to gathered[i], which the
+// downsweep then reads in order.
 __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const int32_t *in,
                                                                    const int32_t *idx, int64_t n,
-                                                                   int64_t *partials) {
+                                                                   int64_t *partials,
+                                                                   int32_t *gathered) {
     __shared__ int64_t s_wave[kScanThreads / 64];
     const int64_t base = (int64_t)blockIdx.x * kScanChunk;
     int64_t s = 0;
 #pragma unroll
     for (int r = 0; r < kScanItems; ++r) {
         const int64_t i = base + (int64_t)r * kScanThreads + threadIdx.x;
-        if (i < n) s += in[idx ? idx[i] : i];
+        if (i < n) {
+            const int32_t v = in[idx ? idx[i] : i];
+            if (idx) gathered[i] = v;
+            s += v;
+        }
     }
     int64_t total;
     block_excl_scan(s, s_wave, &total);
@@ -182,8 +239,9 @@ __global__ __launch_bounds__(kScanThreads) void scan_partials_kernel(int64_t *pa
     if (threadIdx.x == 0) *total_out = carry;
 }
 
-__global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const int32_t *in,
-                                                                 const int32_t *idx, int64_t n,
+// May run in place (in == out): each thread reads its items before writing
+// them and touches no other thread's.
+__global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const int32_t *in, int64_t n,
                                                                  const int64_t *partials,
                                                                  int32_t *out) {
     __shared__ int64_t s_wave[kScanThreads / 64];
@@ -194,7 +252,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const int32_t *
     int64_t s = 0;
 #pragma unroll
     for (int r = 0; r < kScanItems; ++r) {
-        v[r] = (base + r < n) ? in[idx ? idx[base + r] : base + r] : 0;
+        v[r] = (base + r < n) ? in[base + r] : 0;
         s += v[r];
     }
     int64_t tot;
@@ -231,70 +289,169 @@ int32_t exclusive_scan(const int32_t *in, const int32_t *idx, int64_t n, int32_t
     const int64_t nparts = ceil_div(n > 0 ? n : 1, kScanChunk);
     TimedScope ts("exclusive_scan", s);
     // A zero-length input still runs one reduce block so the total is 0.
-    scan_reduce_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(in, idx, n, partials);
+    scan_reduce_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(in, idx, n, partials,
+                                                                  idx ? out : nullptr);
     MG_LAUNCHED("scan_reduce_kernel");
     scan_partials_kernel<<<1, kScanThreads, 0, s>>>(partials, nparts, total_dev);
     MG_LAUNCHED("scan_partials_kernel");
     if (n > 0) {
-        scan_down_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(in, idx, n, partials, out);
+        scan_down_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(idx ? out : in, n, partials,
+                                                                    out);
         MG_LAUNCHED("scan_down_kernel");
     }
     return MG_OK;
 }
 
 // ------------------------------------------------- depth-first tile lists
-// The (tile << 32 | depth) order is built in two cheaper sorts: all N
-// Gaussians by depth once (32-bit keys; invalid ones get 0xFFFFFFFF and sort
-// last), then the intersections, emitted in that depth order, by tile id
-// alone (ceil(log2 n_tiles) bits). The tile sort is stable, so inside a tile
-// the order is (depth bits, Gaussian id) - the same total order as one stable
-// sort of the 64-bit keys emitted Gaussian by Gaussian.
-__global__ __launch_bounds__(256) void depth_keys_kernel(const float *depth, const int32_t *valid,
-                                                         int64_t n, uint32_t *keys,
-                                                         int32_t *vals) {
-    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (g >= n) return;
-    keys[g] = valid[g] ? __float_as_uint(depth[g]) : 0xFFFFFFFFu;
-    vals[g] = (int32_t)g;
+// The (tile << 32 | depth) order is built in two cheaper sorts: the N
+// Gaussians by depth once (32-bit keys), then the intersections, emitted in
+// that depth order, by tile id alone (ceil(log2 n_tiles) bits). The tile sort
+// is stable, so inside a tile the order is (depth bits, Gaussian id) - the
+// same total order as one stable sort of the 64-bit keys emitted Gaussian by
+// Gaussian. Gaussians that claim no tile never appear in the lists, so their
+// place in the depth order is free.
+
+struct BinStats {
+    unsigned long long total;       // intersections
+    uint32_t kmin, kmax;            // depth-key range of Gaussians with a tile
+    unsigned long long scan_total;  // the scan's own total (same value)
+};
+
+// One per count workgroup, reduced by bin_stats_kernel. (Same-address
+// atomics from every wave would serialise at the memory side: the eight
+// XCDs' L2s are not coherent with each other, so device-scope atomics are
+// performed there.)
+struct BinPart {
+    unsigned long long total;
+    uint32_t kmin, kmax;
+};
+
+// Count pass in Gaussian order (coalesced reads): the tile count, the walk
+// record, and the depth sort's key (0xFFFFFFFF for a Gaussian with no tile)
+// and identity value; per workgroup the intersection total and key range.
+__global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArgs A,
+                                                                    int32_t *counts, BinRec *recs,
+                                                                    uint32_t *dkeys,
+                                                                    int32_t *perm, BinPart *parts) {
+    __shared__ BinPart s_p[kBinThreads / 64];
+    const int64_t g = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
+    int n = 0;
+    uint32_t key = 0xFFFFFFFFu;
+    if (g < A.N) {
+        BinRec r;
+        if (make_rec(A, g, r)) {
+            n = rec_walk(r, A.conic != nullptr, A.tile, A.W, A.H, A.tiles_x,
+                         [](int, uint32_t) {});
+            recs[g] = r;
+        }
+        if (n > 0) key = __float_as_uint(A.depth[g]);
+        counts[g] = n;
+        dkeys[g] = key;
+        perm[g] = (int32_t)g;
+    }
+    unsigned long long tot = (unsigned long long)n;
+    uint32_t kmin = key, kmax = n > 0 ? key : 0u;
+    for (int o = 32; o >= 1; o >>= 1) {
+        tot += __shfl_xor(tot, o, 64);
+        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
+        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
+    }
+    if ((threadIdx.x & 63) == 0) s_p[threadIdx.x >> 6] = BinPart{tot, kmin, kmax};
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        BinPart b = s_p[0];
+        for (int w = 1; w < kBinThreads / 64; ++w) {
+            b.total += s_p[w].total;
+            b.kmin = min(b.kmin, s_p[w].kmin);
+            b.kmax = max(b.kmax, s_p[w].kmax);
+        }
+        parts[blockIdx.x] = b;
+    }
 }
 
-// Thread k emits the pairs of the k-th Gaussian in depth order: tile id keys
-// (32-bit) and Gaussian ids, at the scanned offset of position k.
-__global__ __launch_bounds__(kBinThreads) void bin_write_ordered_kernel(
-    const BinArgs A, const int32_t *order, const int32_t *offsets, uint32_t *tkeys,
-    int32_t *ids) {
-    const int64_t k = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
-    if (k >= A.N) return;
-    const int64_t g = order[k];
-    if (A.valid[g] == 0) return;
-    const float ux = A.uv[2 * g], uy = A.uv[2 * g + 1];
-    const float rx = A.rxy[2 * g], ry = A.rxy[2 * g + 1];
-    const float tf = (float)A.tile;
-    int x0 = (int)floorf((ux - rx) / tf), x1 = (int)floorf((ux + rx) / tf);
-    int y0 = (int)floorf((uy - ry) / tf), y1 = (int)floorf((uy + ry) / tf);
-    x0 = min(max(x0, 0), A.tiles_x - 1);
-    x1 = min(max(x1, 0), A.tiles_x - 1);
-    y0 = min(max(y0, 0), A.tiles_y - 1);
-    y1 = min(max(y1, 0), A.tiles_y - 1);
-    const bool test = A.conic != nullptr;
-    float thr = 0.f, ca = 0.f, cb = 0.f, cc = 0.f;
-    if (test) {
-        bool live;
-        thr = level_threshold(A.opac[g], live);
-        if (!live) return;
-        ca = A.conic[3 * g]; cb = A.conic[3 * g + 1]; cc = A.conic[3 * g + 2];
+// One workgroup folds the count pass's per-workgroup partials into *st.
+__global__ __launch_bounds__(256) void bin_stats_kernel(const BinPart *parts, int64_t nparts,
+                                                        BinStats *st) {
+    __shared__ BinPart s_p[4];
+    unsigned long long tot = 0;
+    uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+    for (int64_t i = threadIdx.x; i < nparts; i += 256) {
+        const BinPart b = parts[i];
+        tot += b.total;
+        kmin = min(kmin, b.kmin);
+        kmax = max(kmax, b.kmax);
     }
-    int64_t at = offsets[k];
-    for (int ty = y0; ty <= y1; ++ty) {
-        const float ry0 = (float)(ty * A.tile);
-        const float ry1 = fminf((float)((ty + 1) * A.tile), (float)A.H);
-        for (int tx = x0; tx <= x1; ++tx) {
-            const float rx0 = (float)(tx * A.tile);
-            const float rx1 = fminf((float)((tx + 1) * A.tile), (float)A.W);
-            if (test && min_q_over_rect(ux, uy, ca, cb, cc, rx0, rx1, ry0, ry1) >= thr) continue;
-            tkeys[at] = (uint32_t)(ty * A.tiles_x + tx);
-            ids[at] = (int32_t)g;
-            ++at;
+    for (int o = 32; o >= 1; o >>= 1) {
+        tot += __shfl_xor(tot, o, 64);
+        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
+        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
+    }
+    if ((threadIdx.x & 63) == 0) s_p[threadIdx.x >> 6] = BinPart{tot, kmin, kmax};
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        BinPart b = s_p[0];
+        for (int w = 1; w < 4; ++w) {
+            b.total += s_p[w].total;
+            b.kmin = min(b.kmin, s_p[w].kmin);
+            b.kmax = max(b.kmax, s_p[w].kmax);
+        }
+        st->total = b.total;
+        st->kmin = b.kmin;
+        st->kmax = b.kmax;
+        st->scan_total = 0;
+    }
+}
+
+// Pairs staged in LDS per workgroup before the coalesced store.
+constexpr int kBinStage = 2048;
+
+// Thread k emits the pairs of the k-th Gaussian in depth order (tile id key,
+// Gaussian id) at the scanned offset of position k. The workgroup's 256
+// Gaussians own one contiguous output range; when it fits in LDS the pairs
+// are assembled there and stored with consecutive lanes on consecutive
+// addresses, otherwise each thread stores its own run.
+__global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
+    const BinRec *recs, const int32_t *order, const int32_t *offsets, int64_t N, int64_t total,
+    int tile, int W, int H, int tiles_x, int test, uint32_t *tkeys, int32_t *ids) {
+    __shared__ uint32_t s_k[kBinStage];
+    __shared__ int32_t s_i[kBinStage];
+    const int64_t k0 = (int64_t)blockIdx.x * kBinThreads;
+    const int64_t k = k0 + threadIdx.x;
+    const int64_t kend = min(k0 + kBinThreads, N);
+    const int64_t base = offsets[k0];
+    const int64_t stop = kend < N ? (int64_t)offsets[kend] : total;
+    const bool staged = stop - base <= kBinStage;    // uniform over the workgroup
+    if (k < N) {
+        const int64_t at = offsets[k];
+        const int64_t nxt = k + 1 < N ? (int64_t)offsets[k + 1] : total;
+        const int cap = (int)(nxt - at);
+        if (cap > 0) {
+            const int32_t g = order[k];
+            const BinRec r = recs[g];
+            if (staged) {
+                const int o = (int)(at - base);
+                rec_walk(r, test != 0, tile, W, H, tiles_x, [&](int n, uint32_t t) {
+                    if (n < cap) {
+                        s_k[o + n] = t;
+                        s_i[o + n] = g;
+                    }
+                });
+            } else {
+                rec_walk(r, test != 0, tile, W, H, tiles_x, [&](int n, uint32_t t) {
+                    if (n < cap) {
+                        tkeys[at + n] = t;
+                        ids[at + n] = g;
+                    }
+                });
+            }
+        }
+    }
+    if (staged) {
+        __syncthreads();
+        const int cnt = (int)(stop - base);
+        for (int i = threadIdx.x; i < cnt; i += kBinThreads) {
+            tkeys[base + i] = s_k[i];
+            ids[base + i] = s_i[i];
         }
     }
 }
@@ -308,15 +465,17 @@ __global__ __launch_bounds__(256) void tile_ranges_u32_kernel(const uint32_t *ti
     for (int64_t t = prev + 1; t <= cur && t <= n_tiles; ++t) offsets[t] = (int32_t)i;
 }
 
-constexpr int kDepthBits = 32;
-
 inline int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
 
-// Carves the begin/finish workspace identically on both calls.
+// Carves the begin/finish workspace identically on both calls. After begin,
+// perm_a holds the depth order, offsets the scanned counts in that order and
+// recs the walk records.
 struct BeginWs {
     int32_t *counts, *perm_a, *perm_b, *offsets;
     uint32_t *dkey_a, *dkey_b;
-    int64_t *total;
+    BinRec *recs;
+    BinPart *parts;
+    BinStats *stats;
     void *scan_ws, *sort_ws;
     int64_t scan_bytes, sort_bytes, bytes;
     BeginWs(void *base, int64_t N) {
@@ -329,16 +488,18 @@ struct BeginWs {
         offsets = (int32_t *)take(4 * N);
         dkey_a = (uint32_t *)take(4 * N);
         dkey_b = (uint32_t *)take(4 * N);
-        total = (int64_t *)take(8);
+        recs = (BinRec *)take((int64_t)sizeof(BinRec) * N);
+        parts = (BinPart *)take((int64_t)sizeof(BinPart) * ceil_div(N, kBinThreads));
+        stats = (BinStats *)take(sizeof(BinStats));
         scan_bytes = scan_ws_bytes(N);
         scan_ws = take(scan_bytes);
         sort_bytes = sort_ws_bytes(N);
         sort_ws = take(sort_bytes);
         bytes = off;
     }
-    // The depth sort runs ceil(32/8) = 4 passes, so its result is in slot a.
-    int32_t *perm() const { return ((kDepthBits + 7) / 8) % 2 == 0 ? perm_a : perm_b; }
 };
+
+inline int bit_width(uint32_t v) { return v == 0 ? 0 : 32 - __builtin_clz(v); }
 
 inline int tile_bits(int n_tiles) {
     int b = 1;
@@ -354,7 +515,8 @@ static int32_t check_bin_args(const char *who, int64_t N, const void *uv, const 
     MG_REQUIRE(tiles_x == (W + tile - 1) / tile && tiles_y == (H + tile - 1) / tile,
                "%s: tiles %dx%d do not cover %dx%d at tile %d", who, tiles_x, tiles_y, W, H,
                tile);
-    MG_REQUIRE((int64_t)tiles_x * tiles_y < (1LL << 31), "%s: too many tiles", who);
+    MG_REQUIRE((int64_t)tiles_x * tiles_y < (1LL << 31) && tiles_x < 65536 && tiles_y < 65536,
+               "%s: too many tiles (%d x %d)", who, tiles_x, tiles_y);
     MG_REQUIRE(N == 0 || (uv && rxy && valid), "%s: null tensor pointer", who);
     MG_REQUIRE((conic == nullptr) == (opac == nullptr),
                "%s: conic and opacity must be given together (or both omitted)", who);
@@ -455,30 +617,37 @@ int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy, const f
                (long long)ws.bytes);
     hipStream_t s = as_stream(stream);
     BinArgs A{N, uv, rxy, conic, opacity, depth, valid, W, H, tile, tiles_x, tiles_y};
+    const int64_t nparts = N > 0 ? ceil_div(N, kBinThreads) : 0;
     if (N > 0) {
-        {
-            TimedScope ts("bin_count", s);
-            bin_count_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(A, ws.counts);
-            MG_LAUNCHED("bin_count_kernel");
-        }
-        depth_keys_kernel<<<(unsigned)ceil_div(N, 256), 256, 0, s>>>(depth, valid, N, ws.dkey_a,
-                                                                      ws.perm_a);
-        MG_LAUNCHED("depth_keys_kernel");
-        uint32_t *rk;
-        int32_t *rv;
-        rc = radix_sort_passes<uint32_t>(ws.dkey_a, ws.perm_a, ws.dkey_b, ws.perm_b, N, 0,
-                                         kDepthBits, ws.sort_ws, ws.sort_bytes, s, "depth_sort",
-                                         &rk, &rv);
-        if (rc != MG_OK) return rc;
-        MG_REQUIRE(rv == ws.perm(), "mg_bin_lists_begin: depth order landed in the wrong buffer");
+        TimedScope ts("bin_count", s);
+        bin_count_rec_kernel<<<(unsigned)nparts, kBinThreads, 0, s>>>(
+            A, ws.counts, ws.recs, ws.dkey_a, ws.perm_a, ws.parts);
+        MG_LAUNCHED("bin_count_rec_kernel");
     }
-    rc = exclusive_scan(ws.counts, ws.perm(), N, ws.offsets, ws.total, ws.scan_ws, ws.scan_bytes, s);
+    bin_stats_kernel<<<1, 256, 0, s>>>(ws.parts, nparts, ws.stats);
+    MG_LAUNCHED("bin_stats_kernel");
+    // The one host read: the total sizes the caller's id buffer, the key
+    // range sets the depth sort's pass count.
+    BinStats st;
+    MG_HIP(hipMemcpyAsync(&st, ws.stats, sizeof(st), hipMemcpyDeviceToHost, s));
+    MG_HIP(hipStreamSynchronize(s));
+    MG_REQUIRE(st.total < (1ULL << 31), "mg_bin_lists_begin: %llu intersections exceed int32",
+               st.total);
+    if (total_host) *total_host = (int64_t)st.total;
+    if (st.total == 0) return MG_OK;
+    // Keys of Gaussians with tiles lie in [kmin, kmax]; the others clamp to
+    // kmax and sort among the farthest, which changes no list.
+    const int bits = bit_width(st.kmax - st.kmin);
+    uint32_t *rk;
+    int32_t *rv;
+    rc = radix_sort_passes<uint32_t>(ws.dkey_a, ws.perm_a, ws.dkey_b, ws.perm_b, N, 0, bits,
+                                     ws.sort_ws, ws.sort_bytes, s, "depth_sort", &rk, &rv,
+                                     st.kmin, st.kmax);
     if (rc != MG_OK) return rc;
-    if (total_host) {
-        MG_HIP(hipMemcpyAsync(total_host, ws.total, sizeof(int64_t), hipMemcpyDeviceToHost, s));
-        MG_HIP(hipStreamSynchronize(s));
-    }
-    return MG_OK;
+    if (rv != ws.perm_a)
+        MG_HIP(hipMemcpyAsync(ws.perm_a, rv, 4 * N, hipMemcpyDeviceToDevice, s));
+    return exclusive_scan(ws.counts, ws.perm_a, N, ws.offsets, (int64_t *)&ws.stats->scan_total,
+                          ws.scan_ws, ws.scan_bytes, s);
 }
 
 int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy, const float *conic,
@@ -514,22 +683,25 @@ int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy, const 
     uint32_t *res_tiles = tk_a;
     if (total > 0) {
         MG_REQUIRE(gauss_ids, "mg_bin_lists_finish: null gauss_ids");
+        MG_REQUIRE(N > 0, "mg_bin_lists_finish: %lld intersections from no Gaussians",
+                   (long long)total);
         // Emit into the id buffer the last sort pass will NOT write, so the
         // sorted ids end in gauss_ids whatever the pass count's parity.
         const int bits = tile_bits(n_tiles);
         const bool even = ((bits + 7) / 8) % 2 == 0;
         int32_t *ids_a = even ? gauss_ids : ids_tmp;
         int32_t *ids_b = even ? ids_tmp : gauss_ids;
-        BinArgs A{N, uv, rxy, conic, opacity, depth, valid, W, H, tile, tiles_x, tiles_y};
         {
             TimedScope ts("bin_write", s);
-            bin_write_ordered_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(
-                A, ws.perm(), ws.offsets, tk_a, ids_a);
-            MG_LAUNCHED("bin_write_ordered_kernel");
+            bin_write_rec_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(
+                ws.recs, ws.perm_a, ws.offsets, N, total, tile, W, H, tiles_x,
+                conic != nullptr ? 1 : 0, tk_a, ids_a);
+            MG_LAUNCHED("bin_write_rec_kernel");
         }
         int32_t *rv;
         rc = radix_sort_passes<uint32_t>(tk_a, ids_a, tk_b, ids_b, total, 0, bits, sort_ws,
-                                         sort_bytes, s, "tile_sort", &res_tiles, &rv);
+                                         sort_bytes, s, "tile_sort", &res_tiles, &rv, 0u,
+                                         0xFFFFFFFFu);
         if (rc != MG_OK) return rc;
         MG_REQUIRE(rv == gauss_ids, "mg_bin_lists_finish: ids landed in the wrong buffer");
     }

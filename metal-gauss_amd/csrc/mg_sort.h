@@ -19,16 +19,21 @@ int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *val
 
 // The passes only: the sorted data stays in whichever ping-pong buffer the
 // last pass wrote (*res_k, *res_v), saving the final copy when the pass count
-// is even. Instantiated for uint32_t keys.
+// is even. Digits come from min(key, hi) - lo, so keys known to lie in
+// [lo, hi] sort on bits [0, bit_width(hi - lo)) alone. Instantiated for
+// uint32_t keys.
 template <typename K>
 int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *vals_out,
                           int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
-                          hipStream_t s, const char *who, K **res_k, int32_t **res_v);
+                          hipStream_t s, const char *who, K **res_k, int32_t **res_v, K lo,
+                          K hi);
 
 // Workspace bytes for an exclusive scan of n int32 values.
 int64_t scan_ws_bytes(int64_t n);
 
 // out[i] = sum_{j<i} in[idx ? idx[j] : j]; total to total_dev (device int64).
+// With idx the values are gathered once (into out, which the second kernel
+// then scans in place).
 int32_t exclusive_scan(const int32_t *in, const int32_t *idx, int64_t n, int32_t *out,
                        int64_t *total_dev, void *ws, int64_t ws_bytes, hipStream_t s);
 

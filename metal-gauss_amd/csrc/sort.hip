@@ -12,6 +12,11 @@
 // Stability holds because items are ranked in their input order: round r,
 // wave w, lane l is item r*256 + w*64 + l of the tile, and tiles are ranked
 // in tile order by the scan.
+//
+// Digits are taken from min(key, hi) - lo. With lo/hi the smallest and
+// largest key that matters, this order-preserving shift lets a caller sort
+// only the bits in which its keys differ (fewer passes); keys above hi tie
+// with hi. The identity window is lo = 0, hi = all ones.
 #include "mg_common.h"
 #include "mg_sort.h"
 
@@ -24,14 +29,19 @@ constexpr int kRadix = 256;
 constexpr int kSortWaves = kSortThreads / 64;
 
 template <typename K>
-__device__ __forceinline__ uint32_t digit_of(K key, int shift, uint32_t mask) {
-    return (uint32_t)(key >> shift) & mask;
+struct KeyWin {
+    K lo, hi;
+};
+
+template <typename K>
+__device__ __forceinline__ uint32_t digit_of(K key, int shift, uint32_t mask, KeyWin<K> w) {
+    return (uint32_t)(((key < w.hi ? key : w.hi) - w.lo) >> shift) & mask;
 }
 
 template <typename K>
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const K *keys, int64_t n,
                                                                      int shift, uint32_t mask,
-                                                                     uint32_t *hist,
+                                                                     KeyWin<K> win, uint32_t *hist,
                                                                      int64_t ntiles) {
     __shared__ uint32_t s_h[kSortWaves][kRadix];
     const int wave = threadIdx.x >> 6;
@@ -41,7 +51,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const K *ke
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
         const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
-        if (i < n) atomicAdd(&s_h[wave][digit_of(keys[i], shift, mask)], 1u);
+        if (i < n) atomicAdd(&s_h[wave][digit_of(keys[i], shift, mask, win)], 1u);
     }
     __syncthreads();
     for (int d = threadIdx.x; d < kRadix; d += kSortThreads) {
@@ -86,7 +96,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_scan_kernel(uint32_t *hist
 template <typename K>
 __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     const K *keys_in, const int32_t *vals_in, K *keys_out, int32_t *vals_out, int64_t n,
-    int shift, uint32_t mask, const uint32_t *hist, int64_t ntiles, const uint32_t *totals) {
+    int shift, uint32_t mask, KeyWin<K> win, const uint32_t *hist, int64_t ntiles,
+    const uint32_t *totals) {
     __shared__ K s_keys[kSortTile];
     __shared__ int32_t s_vals[kSortTile];
     __shared__ uint32_t s_base[kRadix];     // global slot of this tile's digit run
@@ -139,7 +150,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
         const bool ok = r * kSortThreads + tid < nitems;
-        const uint32_t d = digit_of(key[r], shift, mask);
+        const uint32_t d = digit_of(key[r], shift, mask, win);
         // Lanes of this wave holding the same digit.
         uint64_t peers = ballot(ok);
         for (int b = 0; b < 8; ++b) {
@@ -190,7 +201,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
         if (r * kSortThreads + tid < nitems) {
-            const uint32_t d = digit_of(key[r], shift, mask);
+            const uint32_t d = digit_of(key[r], shift, mask, win);
             const uint32_t lp = s_loc[d] + rank[r];
             if (lp < (uint32_t)kSortTile) {
                 s_keys[lp] = key[r];
@@ -201,7 +212,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     __syncthreads();
     for (int i = tid; i < nitems; i += kSortThreads) {
         const K k = s_keys[i];
-        const uint32_t d = digit_of(k, shift, mask);
+        const uint32_t d = digit_of(k, shift, mask, win);
         const uint32_t dst = s_base[d] + (uint32_t)i - s_loc[d];
         if ((int64_t)dst < n) {   // always true for a consistent histogram
             keys_out[dst] = k;
@@ -221,7 +232,8 @@ int64_t sort_ws_bytes(int64_t n) {
 template <typename K>
 int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *vals_out,
                           int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
-                          hipStream_t s, const char *who, K **res_k, int32_t **res_v) {
+                          hipStream_t s, const char *who, K **res_k, int32_t **res_v, K lo,
+                          K hi) {
     MG_REQUIRE(n >= 0 && n < (1LL << 31), "%s: n = %lld", who, (long long)n);
     MG_REQUIRE(begin_bit >= 0 && end_bit <= (int)(8 * sizeof(K)) && begin_bit <= end_bit,
                "%s: bit range [%d, %d)", who, begin_bit, end_bit);
@@ -236,17 +248,19 @@ int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *va
     uint32_t *totals = hist + kRadix * ntiles;
     K *src_k = keys_in, *dst_k = keys_out;
     int32_t *src_v = vals_in, *dst_v = vals_out;
+    MG_REQUIRE(lo <= hi, "%s: empty key window", who);
+    const KeyWin<K> win{lo, hi};
     TimedScope ts(who, s);
     for (int b = begin_bit; b < end_bit; b += 8) {
         const int width = min(8, end_bit - b);
         const uint32_t mask = (1u << width) - 1u;
-        radix_upsweep_kernel<K><<<(unsigned)ntiles, kSortThreads, 0, s>>>(src_k, n, b, mask, hist,
-                                                                         ntiles);
+        radix_upsweep_kernel<K><<<(unsigned)ntiles, kSortThreads, 0, s>>>(src_k, n, b, mask, win,
+                                                                         hist, ntiles);
         MG_LAUNCHED("radix_upsweep_kernel");
         radix_scan_kernel<<<kRadix, kSortThreads, 0, s>>>(hist, ntiles, totals);
         MG_LAUNCHED("radix_scan_kernel");
         radix_downsweep_kernel<K><<<(unsigned)ntiles, kSortThreads, 0, s>>>(
-            src_k, src_v, dst_k, dst_v, n, b, mask, hist, ntiles, totals);
+            src_k, src_v, dst_k, dst_v, n, b, mask, win, hist, ntiles, totals);
         MG_LAUNCHED("radix_downsweep_kernel");
         K *tk = src_k; src_k = dst_k; dst_k = tk;
         int32_t *tv = src_v; src_v = dst_v; dst_v = tv;
@@ -263,7 +277,7 @@ int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *val
     K *rk;
     int32_t *rv;
     int32_t rc = radix_sort_passes<K>(keys_in, vals_in, keys_out, vals_out, n, begin_bit,
-                                      end_bit, ws, ws_bytes, s, who, &rk, &rv);
+                                      end_bit, ws, ws_bytes, s, who, &rk, &rv, K(0), ~K(0));
     if (rc != MG_OK) return rc;
     if (n > 0 && rk != keys_out) {
         MG_HIP(hipMemcpyAsync(keys_out, rk, n * sizeof(K), hipMemcpyDeviceToDevice, s));
@@ -278,7 +292,8 @@ template int32_t radix_sort_pairs<uint64_t>(uint64_t *, int32_t *, uint64_t *, i
                                             int, int, void *, int64_t, hipStream_t, const char *);
 template int32_t radix_sort_passes<uint32_t>(uint32_t *, int32_t *, uint32_t *, int32_t *,
                                              int64_t, int, int, void *, int64_t, hipStream_t,
-                                             const char *, uint32_t **, int32_t **);
+                                             const char *, uint32_t **, int32_t **, uint32_t,
+                                             uint32_t);
 
 }  // namespace mg
 
