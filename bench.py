@@ -4,7 +4,8 @@ Workload ("config 4"): 1,000,000 Gaussians with SH
 degree 3, 800x800 views from 100 seeded cameras on a radius-4 sphere, loss
 0.8 L1 + 0.2 (1 - SSIM) against smooth random targets, then fused Adam over the
 six parameter groups. A step is: activations, render forward (preprocess,
-binning, raster), loss, backward (SSIM, raster, preprocess), Adam. Inputs and
+binning, raster with the background blend), the fused L1 + SSIM loss,
+backward (loss, raster, preprocess), Adam. Inputs and
 targets are resident in HBM before timing.
 
 Prints ONE JSON line with the driver's fields plus:
@@ -115,7 +116,7 @@ class Step:
     def __call__(self, adam=True):
         import torch
 
-        from metal_gauss_amd import render, ssim
+        from metal_gauss_amd import photometric_loss, render
 
         v = self.order[self.k % len(self.order)]
         self.k += 1
@@ -124,8 +125,8 @@ class Step:
                                   torch.sigmoid(p["logit_opac"]), p["sh_dc"], cam.K, cam.viewmat,
                                   cam.W, cam.H, sh_degree=3, sh_rest=p["sh_rest"],
                                   background=self.bg)
-        l1 = (rgb - gt).abs().mean()
-        loss = 0.8 * l1 + 0.2 * (1.0 - ssim(rgb, gt, self.window))
+        # 0.8 * |rgb - gt|.mean() + 0.2 * (1 - ssim(rgb, gt)) (train.py:389-390), fused.
+        loss, _ = photometric_loss(rgb, gt, self.window, 0.2)
         self.opt.zero_grad(set_to_none=True)
         loss.backward()
         if adam:

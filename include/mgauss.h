@@ -203,26 +203,33 @@ int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy,
  * Replaces rasterize_forward (metal_gauss/csrc/rasterize.mm:79-113; kernel
  * rasterize.metal:61-167). t_min is the per-pixel stop transmittance (the
  * reference hard-codes 1e-4, rasterize.metal:149); 0 disables early stop.
- * out_stop holds the stop INDEX into gauss_ids (the reference's n_contrib). */
+ * out_stop holds the stop INDEX into gauss_ids (the reference's n_contrib).
+ * background (host, 3 floats, or NULL) blends the colour in the kernel:
+ * rgb += max(1 - alpha, 0) * background, the torch glue of
+ * metal_backend.py:539-541 (out_alpha stays the coverage). */
 int32_t mg_rasterize_forward(
     int64_t N, const float *uv, const float *conic, const float *opacity,
     const float *color, const int32_t *gauss_ids, const int32_t *tile_offsets,
     int32_t W, int32_t H, int32_t tile, int32_t tiles_x, float t_min,
-    float *out_rgb, float *out_alpha, float *out_T, int32_t *out_stop,
-    mg_stream_t stream);
+    const float *background, float *out_rgb, float *out_alpha, float *out_T,
+    int32_t *out_stop, mg_stream_t stream);
 
 /* Back-to-front replay of mg_rasterize_forward. Replaces rasterize_backward
  * (metal_gauss/csrc/rasterize.mm:147-194; kernel rasterize.metal:173-340).
  * Overwrites d_uv (N,2), d_conic (N,3), d_opacity (N,), d_color (N,3); when
  * d_absuv is not NULL it also overwrites d_absuv (N,) with the per-pixel sum
- * of |d_uv| (the reference's absgrad statistic). */
+ * of |d_uv| (the reference's absgrad statistic). With the forward's
+ * background (host, or NULL), grad_rgb is the gradient of the blended colour
+ * and alpha (the forward's out_alpha, device) adds the blend's share to
+ * grad_alpha. */
 int32_t mg_rasterize_backward(
     int64_t N, const float *uv, const float *conic, const float *opacity,
     const float *color, const int32_t *gauss_ids, const int32_t *tile_offsets,
     const float *final_T, const int32_t *stop, const float *grad_rgb,
-    const float *grad_alpha, int32_t W, int32_t H, int32_t tile,
-    int32_t tiles_x, float *d_uv, float *d_conic, float *d_opacity,
-    float *d_color, float *d_absuv, mg_stream_t stream);
+    const float *grad_alpha, const float *alpha, const float *background,
+    int32_t W, int32_t H, int32_t tile, int32_t tiles_x, float *d_uv,
+    float *d_conic, float *d_opacity, float *d_color, float *d_absuv,
+    mg_stream_t stream);
 
 /* ------------------------------------------------------------------- Adam */
 
@@ -298,6 +305,26 @@ int32_t mg_ssim_fused_backward(const float *x, const float *y, const float *w,
                                const float *partials, const float *scale_dev,
                                int32_t H, int32_t W, float *d_x,
                                mg_stream_t stream);
+
+/* The trainer's photometric loss in the fused SSIM pass: replaces
+ * l1 = (rgb - gt).abs().mean(); loss = 0.8 * l1 + 0.2 * (1 - ssim(rgb, gt))
+ * (metal_gauss/train.py:389-390), with ssim_weight the 0.2. The forward
+ * writes out[0] = loss, out[1] = the L1 mean, out[2] = the SSIM mean (device,
+ * 3 floats) and the same partials as mg_ssim_fused_forward; its workspace is
+ * mg_ssim_fused_workspace_bytes(H, W). The backward writes d_x = grad_dev[0] *
+ * d loss / d x, with the L1 term's derivative sign(x - y) taken as 0 where
+ * x == y (torch's abs). */
+int32_t mg_photometric_loss_forward(const float *x, const float *y,
+                                    const float *w, int32_t H, int32_t W,
+                                    float ssim_weight, float *partials,
+                                    float *out, void *workspace,
+                                    int64_t workspace_bytes,
+                                    mg_stream_t stream);
+int32_t mg_photometric_loss_backward(const float *x, const float *y,
+                                     const float *w, const float *partials,
+                                     const float *grad_dev, int32_t H,
+                                     int32_t W, float ssim_weight, float *d_x,
+                                     mg_stream_t stream);
 
 #ifdef __cplusplus
 }

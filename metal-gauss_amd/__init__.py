@@ -13,7 +13,7 @@ Public surface (names of the reference's modules):
 from .api import BACKENDS, render  # noqa: F401
 from .fused_adam import FusedAdam  # noqa: F401
 from .selective_adam import SelectiveAdam  # noqa: F401
-from .ssim import gaussian_kernel, ssim  # noqa: F401
+from .ssim import gaussian_kernel, photometric_loss, ssim  # noqa: F401
 from . import backend  # noqa: F401
 
 __version__ = "0.1.0"

@@ -347,7 +347,10 @@ class _RasterizeMetal(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, uv, conic, opacity, color, gauss_ids, tile_offsets, W, H, tile, tiles_x,
-                absgrad_out=None, t_min=DEFAULT_T_MIN):
+                absgrad_out=None, t_min=DEFAULT_T_MIN, background=None):
+        """``background`` is None or three host floats blended in the kernel
+        (rgb + max(1 - alpha, 0) * background); the backward then carries the
+        blend's gradient too."""
         lib = _load()
         dev = uv.device
         uv, conic, opacity, color = (t.contiguous() for t in (uv, conic, opacity, color))
@@ -361,10 +364,12 @@ class _RasterizeMetal(torch.autograd.Function):
             _lib.dev_tensor(opacity, "opacity"), _lib.dev_tensor(color, "color"),
             _lib.dev_tensor(gauss_ids, "gauss_ids", torch.int32),
             _lib.dev_tensor(tile_offsets, "tile_offsets", torch.int32), W, H, tile, tiles_x,
-            float(t_min), rgb.data_ptr(), alpha.data_ptr(), T.data_ptr(), stop.data_ptr(),
-            _lib.stream(uv)))
-        ctx.save_for_backward(uv, conic, opacity, color, gauss_ids, tile_offsets, T, stop)
+            float(t_min), None if background is None else _lib.f32_array(background),
+            rgb.data_ptr(), alpha.data_ptr(), T.data_ptr(), stop.data_ptr(), _lib.stream(uv)))
+        ctx.save_for_backward(uv, conic, opacity, color, gauss_ids, tile_offsets, T, stop,
+                              alpha if background is not None else None)
         ctx.dims = (W, H, tile, tiles_x)
+        ctx.background = background
         # absgrad is a statistic of the backward, not a gradient: the caller
         # hands in a buffer and the backward accumulates into it.
         ctx.absgrad_out = absgrad_out
@@ -373,8 +378,9 @@ class _RasterizeMetal(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_rgb, grad_alpha):
         lib = _load()
-        uv, conic, opacity, color, gauss_ids, tile_offsets, T, stop = ctx.saved_tensors
+        uv, conic, opacity, color, gauss_ids, tile_offsets, T, stop, alpha = ctx.saved_tensors
         W, H, tile, tiles_x = ctx.dims
+        bg = ctx.background
         N = uv.shape[0]
         dev = uv.device
         d_uv = torch.empty(N, 2, device=dev)
@@ -388,16 +394,34 @@ class _RasterizeMetal(torch.autograd.Function):
             N, uv.data_ptr(), conic.data_ptr(), opacity.data_ptr(), color.data_ptr(),
             gauss_ids.data_ptr(), tile_offsets.data_ptr(), T.data_ptr(), stop.data_ptr(),
             _lib.dev_tensor(grad_rgb, "grad_rgb"), _lib.dev_tensor(grad_alpha, "grad_alpha"),
+            None if bg is None else alpha.data_ptr(), None if bg is None else _lib.f32_array(bg),
             W, H, tile, tiles_x, d_uv.data_ptr(), d_conic.data_ptr(), d_op.data_ptr(),
             d_col.data_ptr(), None if d_abs is None else d_abs.data_ptr(), _lib.stream(uv)))
         if ctx.absgrad_out is not None:
             ctx.absgrad_out[:N] += d_abs
-        return (d_uv, d_conic, d_op, d_col) + (None,) * 8
+        return (d_uv, d_conic, d_op, d_col) + (None,) * 9
 
 
 # Names that describe this backend rather than the reference's.
 _PreprocessHIP = _PreprocessMetal
 _RasterizeHIP = _RasterizeMetal
+
+
+def _host_background(background):
+    """Three host floats for the in-kernel blend, or None when the torch
+    expression must do it (no background, a device tensor, or one that
+    requires grad)."""
+    if background is None:
+        return None
+    if isinstance(background, torch.Tensor):
+        if background.device.type != "cpu" or background.requires_grad:
+            return None
+        vals = background.detach().to(torch.float32).reshape(-1).tolist()
+    else:
+        vals = [float(v) for v in background]
+    if len(vals) != 3:
+        return None
+    return tuple(vals)
 
 
 def antialias_scale(conic: torch.Tensor, blur: float) -> torch.Tensor:
@@ -489,11 +513,15 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
         uv.detach(), rxy.detach(), depth.detach(), valid_i, conic.detach(),
         opacities.detach(), W, H, tile)
 
+    # A constant background (tuple, list or CPU tensor without grad) is
+    # blended inside the raster kernels; a device or trainable one by the
+    # reference's torch expression (metal_backend.py:539-541).
+    bg_host = _host_background(background)
     rgb, alpha = _RasterizeMetal.apply(
         uv, conic, opacities, colors, gauss_ids, tile_offsets, W, H, tile, tiles_x,
-        absgrad_out, min_transmittance)
+        absgrad_out, min_transmittance, bg_host)
 
-    if background is not None:
+    if background is not None and bg_host is None:
         bg = torch.as_tensor(background, device=rgb.device, dtype=rgb.dtype)
         rgb = rgb + (1.0 - alpha).clamp_min(0)[..., None] * bg
 

@@ -40,6 +40,9 @@ struct RasterArgs {
     const int32_t *ids, *offsets;
     int32_t W, H, tile, tiles_x, n_tiles;
     float t_min;
+    // Optional background: rgb += max(1 - alpha, 0) * bg (has_bg != 0).
+    int32_t has_bg;
+    float bg[3];
 };
 
 __device__ __forceinline__ void tile_pixel(int tid, int tile, int &lx, int &ly, bool &inblk) {
@@ -228,6 +231,14 @@ __global__ __launch_bounds__(MAXW * 64) void raster_fwd_kernel(const RasterArgs 
     }
     if (!inimg) return;
     const int64_t o = (int64_t)py * A.W + px;
+    if (A.has_bg) {
+        // Rounded as the separate torch ops of metal_backend.py's blend
+        // (rgb + (1 - alpha).clamp_min(0) * bg): no fused multiply-add.
+        const float r = fmaxf(1.0f - acc, 0.0f);
+        cr = __fadd_rn(cr, __fmul_rn(r, A.bg[0]));
+        cg = __fadd_rn(cg, __fmul_rn(r, A.bg[1]));
+        cb = __fadd_rn(cb, __fmul_rn(r, A.bg[2]));
+    }
     out_rgb[3 * o] = cr;
     out_rgb[3 * o + 1] = cg;
     out_rgb[3 * o + 2] = cb;
@@ -240,6 +251,7 @@ struct RasterGrads {
     const float *final_T;
     const int32_t *stop;
     const float *grad_rgb, *grad_alpha;
+    const float *alpha;   // the forward's alpha; read only with a background
     float *d_uv, *d_conic, *d_op, *d_col, *d_abs;
 };
 
@@ -267,7 +279,11 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
     const float gr = inimg ? G.grad_rgb[3 * o] : 0.f;
     const float gg = inimg ? G.grad_rgb[3 * o + 1] : 0.f;
     const float gb = inimg ? G.grad_rgb[3 * o + 2] : 0.f;
-    const float ga = inimg ? G.grad_alpha[o] : 0.f;
+    float ga = inimg ? G.grad_alpha[o] : 0.f;
+    // The background blend's share: d rgb_out / d alpha = -bg where
+    // 1 - alpha >= 0 (torch's clamp_min passes the gradient at the bound).
+    if (A.has_bg && inimg && 1.0f - G.alpha[o] >= 0.0f)
+        ga -= gr * A.bg[0] + gg * A.bg[1] + gb * A.bg[2];
     const bool want_abs = G.d_abs != nullptr;
 
     // Nothing at or past a pixel's stop index contributed to it.
@@ -403,15 +419,18 @@ extern "C" {
 int32_t mg_rasterize_forward(int64_t N, const float *uv, const float *conic, const float *opacity,
                              const float *color, const int32_t *gauss_ids,
                              const int32_t *tile_offsets, int32_t W, int32_t H, int32_t tile,
-                             int32_t tiles_x, float t_min, float *out_rgb, float *out_alpha,
-                             float *out_T, int32_t *out_stop, mg_stream_t stream) {
+                             int32_t tiles_x, float t_min, const float *background,
+                             float *out_rgb, float *out_alpha, float *out_T, int32_t *out_stop,
+                             mg_stream_t stream) {
     int32_t rc = check_raster("rasterize_forward", N, uv, conic, opacity, color, gauss_ids,
                               tile_offsets, W, H, tile, tiles_x);
     if (rc != MG_OK) return rc;
     MG_REQUIRE(out_rgb && out_alpha && out_T && out_stop, "rasterize_forward: null output");
     const int tiles_y = (H + tile - 1) / tile;
     RasterArgs A{uv, conic, opacity, color, gauss_ids, tile_offsets, W, H, tile, tiles_x,
-                 tiles_x * tiles_y, t_min};
+                 tiles_x * tiles_y, t_min, background != nullptr,
+                 {background ? background[0] : 0.f, background ? background[1] : 0.f,
+                  background ? background[2] : 0.f}};
     const int threads = ((tile * tile + 63) / 64) * 64;
     const int grid = (int)ceil_div(A.n_tiles, kXcds) * kXcds;
     TimedScope ts("rasterize_forward", as_stream(stream));
@@ -429,13 +448,15 @@ int32_t mg_rasterize_backward(int64_t N, const float *uv, const float *conic,
                               const float *opacity, const float *color,
                               const int32_t *gauss_ids, const int32_t *tile_offsets,
                               const float *final_T, const int32_t *stop, const float *grad_rgb,
-                              const float *grad_alpha, int32_t W, int32_t H, int32_t tile,
+                              const float *grad_alpha, const float *alpha,
+                              const float *background, int32_t W, int32_t H, int32_t tile,
                               int32_t tiles_x, float *d_uv, float *d_conic, float *d_opacity,
                               float *d_color, float *d_absuv, mg_stream_t stream) {
     int32_t rc = check_raster("rasterize_backward", N, uv, conic, opacity, color, gauss_ids,
                               tile_offsets, W, H, tile, tiles_x);
     if (rc != MG_OK) return rc;
     MG_REQUIRE(final_T && stop && grad_rgb && grad_alpha, "rasterize_backward: null input");
+    MG_REQUIRE(!background || alpha, "rasterize_backward: a background needs the forward's alpha");
     MG_REQUIRE(N == 0 || (d_uv && d_conic && d_opacity && d_color),
                "rasterize_backward: null gradient output");
     hipStream_t s = as_stream(stream);
@@ -448,8 +469,11 @@ int32_t mg_rasterize_backward(int64_t N, const float *uv, const float *conic,
     }
     const int tiles_y = (H + tile - 1) / tile;
     RasterArgs A{uv, conic, opacity, color, gauss_ids, tile_offsets, W, H, tile, tiles_x,
-                 tiles_x * tiles_y, 0.0f};
-    RasterGrads Gr{final_T, stop, grad_rgb, grad_alpha, d_uv, d_conic, d_opacity, d_color, d_absuv};
+                 tiles_x * tiles_y, 0.0f, background != nullptr,
+                 {background ? background[0] : 0.f, background ? background[1] : 0.f,
+                  background ? background[2] : 0.f}};
+    RasterGrads Gr{final_T, stop, grad_rgb, grad_alpha, alpha, d_uv, d_conic, d_opacity, d_color,
+                   d_absuv};
     const int threads = ((tile * tile + 63) / 64) * 64;
     const int grid = (int)ceil_div(A.n_tiles, kXcds) * kXcds;
     TimedScope ts("rasterize_backward", s);

@@ -131,13 +131,15 @@ constexpr int kTW = 32, kTH = 16;                 // output tile
 constexpr int kIW = kTW + 2 * kR, kIH = kTH + 2 * kR;   // 42 x 26 with halo
 constexpr int kSsimThreads = 256;
 
+// block_sums[b] gets the block's SSIM sum; with l1_sums, l1_sums[b] gets its
+// sum of |x - y| over the same pixels and channel.
 __global__ __launch_bounds__(kSsimThreads) void ssim_fused_fwd_kernel(
     const float *x, const float *y, const float *w, int H, int W, float *partials,
-    float *block_sums) {
+    float *block_sums, float *l1_sums) {
     __shared__ float s_x[kIH][kIW], s_y[kIH][kIW];
     __shared__ float s_h[5][kIH][kTW];
     __shared__ float s_w[2 * kR + 1];
-    __shared__ float s_red[kSsimThreads / 64];
+    __shared__ float s_red[2][kSsimThreads / 64];
     const int c = blockIdx.z;
     const int x0 = blockIdx.x * kTW - kR, y0 = blockIdx.y * kTH - kR;
     const int tid = threadIdx.x;
@@ -178,11 +180,12 @@ __global__ __launch_bounds__(kSsimThreads) void ssim_fused_fwd_kernel(
     __syncthreads();
     // Vertical pass and the SSIM tail at the tile's own pixels.
     const int64_t N = (int64_t)W * H;
-    float local = 0.f;
+    float local = 0.f, local_l1 = 0.f;
     for (int i = tid; i < kTH * kTW; i += kSsimThreads) {
         const int ly = i / kTW, lx = i - ly * kTW;
         const int gx = blockIdx.x * kTW + lx, gy = blockIdx.y * kTH + ly;
         if (gx >= W || gy >= H) continue;
+        local_l1 += fabsf(s_x[ly + kR][lx + kR] - s_y[ly + kR][lx + kR]);
         float m[5] = {0, 0, 0, 0, 0};
 #pragma unroll
         for (int k = 0; k <= 2 * kR; ++k) {
@@ -198,16 +201,26 @@ __global__ __launch_bounds__(kSsimThreads) void ssim_fused_fwd_kernel(
         partials[(3 + c) * N + o] = pxx;
         partials[(6 + c) * N + o] = pxy;
     }
-    // Deterministic per-block sum (fixed reduction order).
-    for (int off = 32; off >= 1; off >>= 1) local += __shfl_xor(local, off, 64);
-    if ((tid & 63) == 0) s_red[tid >> 6] = local;
+    // Deterministic per-block sums (fixed reduction order).
+    for (int off = 32; off >= 1; off >>= 1) {
+        local += __shfl_xor(local, off, 64);
+        local_l1 += __shfl_xor(local_l1, off, 64);
+    }
+    if ((tid & 63) == 0) {
+        s_red[0][tid >> 6] = local;
+        s_red[1][tid >> 6] = local_l1;
+    }
     __syncthreads();
     if (tid == 0) {
-        float s = 0.f;
-        for (int k = 0; k < kSsimThreads / 64; ++k) s += s_red[k];
+        float s = 0.f, s1 = 0.f;
+        for (int k = 0; k < kSsimThreads / 64; ++k) {
+            s += s_red[0][k];
+            s1 += s_red[1][k];
+        }
         const int64_t bid =
             ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
         block_sums[bid] = s;
+        if (l1_sums) l1_sums[bid] = s1;
     }
 }
 
@@ -222,9 +235,43 @@ __global__ __launch_bounds__(256) void ssim_mean_kernel(const float *block_sums,
     if (threadIdx.x == 0) mean_out[0] = (float)((s_red[0] + s_red[1] + s_red[2] + s_red[3]) / (double)count);
 }
 
+// out[0] = (1 - lam) * mean|x - y| + lam * (1 - mean SSIM), out[1] = the L1
+// mean, out[2] = the SSIM mean; sums in double.
+__global__ __launch_bounds__(256) void photometric_loss_kernel(const float *ssim_sums,
+                                                               const float *l1_sums, int64_t nb,
+                                                               int64_t count, float lam,
+                                                               float *out) {
+    __shared__ double s_red[2][4];
+    double s = 0.0, s1 = 0.0;
+    for (int64_t i = threadIdx.x; i < nb; i += 256) {
+        s += (double)ssim_sums[i];
+        s1 += (double)l1_sums[i];
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        s += __shfl_xor(s, off, 64);
+        s1 += __shfl_xor(s1, off, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        s_red[0][threadIdx.x >> 6] = s;
+        s_red[1][threadIdx.x >> 6] = s1;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const double ss = (s_red[0][0] + s_red[0][1] + s_red[0][2] + s_red[0][3]) / (double)count;
+        const double l1 = (s_red[1][0] + s_red[1][1] + s_red[1][2] + s_red[1][3]) / (double)count;
+        const double l = (double)lam;
+        out[0] = (float)((1.0 - l) * l1 + l * (1.0 - ss));
+        out[1] = (float)l1;
+        out[2] = (float)ss;
+    }
+}
+
+// dx = g / (3N) * (a_ssim * dSSIM_sum/dx + a_l1 * sign(x - y)), g = scale_dev[0]:
+// a_ssim = 1, a_l1 = 0 is the gradient of the SSIM mean; a_ssim = -lam,
+// a_l1 = 1 - lam that of the photometric loss.
 __global__ __launch_bounds__(kSsimThreads) void ssim_fused_bwd_kernel(
     const float *x, const float *y, const float *w, const float *partials, const float *scale_dev,
-    int H, int W, float *dx) {
+    int H, int W, float a_ssim, float a_l1, float *dx) {
     __shared__ float s_p[3][kIH][kIW];
     __shared__ float s_h[3][kIH][kTW];
     __shared__ float s_w[2 * kR + 1];
@@ -277,7 +324,14 @@ __global__ __launch_bounds__(kSsimThreads) void ssim_fused_bwd_kernel(
             b2 += wk * s_h[2][ly + k][lx];
         }
         const int64_t o = ((int64_t)gy * W + gx) * 3 + c;
-        dx[o] = scale * (b0 + 2.0f * x[o] * b1 + y[o] * b2);
+        const float xv = x[o], yv = y[o];
+        float d = a_ssim * (b0 + 2.0f * xv * b1 + yv * b2);
+        if (a_l1 != 0.0f) {
+            // torch's abs backward: sign, with 0 at x == y.
+            const float sg = xv > yv ? 1.0f : (xv < yv ? -1.0f : 0.0f);
+            d += a_l1 * sg;
+        }
+        dx[o] = scale * d;
     }
 }
 
@@ -345,7 +399,7 @@ int32_t mg_ssim_chain_backward(const float *x, const float *y, const float *d_st
 
 int64_t mg_ssim_fused_workspace_bytes(int32_t H, int32_t W) {
     if (H <= 0 || W <= 0) return 0;
-    return ssim_blocks(H, W) * (int64_t)sizeof(float);
+    return 2 * ssim_blocks(H, W) * (int64_t)sizeof(float);   // SSIM and L1 block sums
 }
 
 int32_t mg_ssim_fused_forward(const float *x, const float *y, const float *w, int32_t H, int32_t W,
@@ -360,7 +414,7 @@ int32_t mg_ssim_fused_forward(const float *x, const float *y, const float *w, in
     dim3 grid((unsigned)ceil_div(W, kTW), (unsigned)ceil_div(H, kTH), 3);
     float *sums = static_cast<float *>(workspace);
     TimedScope ts("ssim_fused_forward", s);
-    ssim_fused_fwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, H, W, partials, sums);
+    ssim_fused_fwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, H, W, partials, sums, nullptr);
     MG_LAUNCHED("ssim_fused_fwd_kernel");
     ssim_mean_kernel<<<1, 256, 0, s>>>(sums, ssim_blocks(H, W), 3LL * H * W, mean_out);
     MG_LAUNCHED("ssim_mean_kernel");
@@ -375,7 +429,49 @@ int32_t mg_ssim_fused_backward(const float *x, const float *y, const float *w,
     hipStream_t s = as_stream(stream);
     dim3 grid((unsigned)ceil_div(W, kTW), (unsigned)ceil_div(H, kTH), 3);
     TimedScope ts("ssim_fused_backward", s);
-    ssim_fused_bwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, partials, scale_dev, H, W, d_x);
+    ssim_fused_bwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, partials, scale_dev, H, W, 1.0f,
+                                                        0.0f, d_x);
+    MG_LAUNCHED("ssim_fused_bwd_kernel");
+    return MG_OK;
+}
+
+int32_t mg_photometric_loss_forward(const float *x, const float *y, const float *w, int32_t H,
+                                    int32_t W, float ssim_weight, float *partials, float *out,
+                                    void *workspace, int64_t workspace_bytes,
+                                    mg_stream_t stream) {
+    MG_REQUIRE(H > 0 && W > 0 && x && y && w && partials && out,
+               "mg_photometric_loss_forward: bad arguments");
+    MG_REQUIRE(ssim_weight >= 0.0f && ssim_weight <= 1.0f,
+               "mg_photometric_loss_forward: ssim_weight %g outside [0, 1]", (double)ssim_weight);
+    MG_REQUIRE(workspace && workspace_bytes >= mg_ssim_fused_workspace_bytes(H, W),
+               "mg_photometric_loss_forward: workspace %lld bytes, need %lld",
+               (long long)workspace_bytes, (long long)mg_ssim_fused_workspace_bytes(H, W));
+    hipStream_t s = as_stream(stream);
+    dim3 grid((unsigned)ceil_div(W, kTW), (unsigned)ceil_div(H, kTH), 3);
+    const int64_t nb = ssim_blocks(H, W);
+    float *sums = static_cast<float *>(workspace);
+    TimedScope ts("ssim_fused_forward", s);
+    ssim_fused_fwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, H, W, partials, sums, sums + nb);
+    MG_LAUNCHED("ssim_fused_fwd_kernel");
+    photometric_loss_kernel<<<1, 256, 0, s>>>(sums, sums + nb, nb, 3LL * H * W, ssim_weight, out);
+    MG_LAUNCHED("photometric_loss_kernel");
+    return MG_OK;
+}
+
+int32_t mg_photometric_loss_backward(const float *x, const float *y, const float *w,
+                                     const float *partials, const float *grad_dev, int32_t H,
+                                     int32_t W, float ssim_weight, float *d_x,
+                                     mg_stream_t stream) {
+    MG_REQUIRE(H > 0 && W > 0 && x && y && w && partials && grad_dev && d_x,
+               "mg_photometric_loss_backward: bad arguments");
+    MG_REQUIRE(ssim_weight >= 0.0f && ssim_weight <= 1.0f,
+               "mg_photometric_loss_backward: ssim_weight %g outside [0, 1]",
+               (double)ssim_weight);
+    hipStream_t s = as_stream(stream);
+    dim3 grid((unsigned)ceil_div(W, kTW), (unsigned)ceil_div(H, kTH), 3);
+    TimedScope ts("ssim_fused_backward", s);
+    ssim_fused_bwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, partials, grad_dev, H, W,
+                                                        -ssim_weight, 1.0f - ssim_weight, d_x);
     MG_LAUNCHED("ssim_fused_bwd_kernel");
     return MG_OK;
 }

@@ -72,6 +72,60 @@ class _SSIMFused(torch.autograd.Function):
         return d_a, None, None
 
 
+class _PhotometricLoss(torch.autograd.Function):
+    """[loss, L1 mean, SSIM mean] with loss = (1 - w) * mean|a - b| +
+    w * (1 - mean SSIM(a, b)). Only the loss entry carries a gradient (to
+    ``a``); the wrapper detaches the other two."""
+
+    @staticmethod
+    def forward(ctx, a, b, win, ssim_weight):
+        lib = _lib.load()
+        _check_image(a, "render")
+        _check_image(b, "target")
+        a, b = a.contiguous(), b.contiguous()
+        win = win.reshape(-1).contiguous().to(torch.float32)
+        if win.numel() != 11:
+            raise ValueError(f"SSIM window must have 11 taps, got {win.numel()}")
+        H, W = a.shape[0], a.shape[1]
+        partials = torch.empty(9, H, W, device=a.device)
+        out = torch.empty(3, device=a.device)
+        ws = torch.empty(lib.mg_ssim_fused_workspace_bytes(H, W), dtype=torch.uint8,
+                         device=a.device)
+        _lib.check(lib.mg_photometric_loss_forward(
+            _lib.dev_tensor(a, "render"), _lib.dev_tensor(b, "target"),
+            _lib.dev_tensor(win, "window"), H, W, float(ssim_weight), partials.data_ptr(),
+            out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(a)))
+        ctx.save_for_backward(a, b, win, partials)
+        ctx.ssim_weight = float(ssim_weight)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        lib = _lib.load()
+        a, b, win, partials = ctx.saved_tensors
+        H, W = a.shape[0], a.shape[1]
+        g = grad_out.detach().to(torch.float32).reshape(-1)[:1].contiguous()
+        d_a = torch.empty_like(a)
+        _lib.check(lib.mg_photometric_loss_backward(
+            a.data_ptr(), b.data_ptr(), win.data_ptr(), partials.data_ptr(),
+            _lib.dev_tensor(g, "grad"), H, W, ctx.ssim_weight, d_a.data_ptr(), _lib.stream(a)))
+        return d_a, None, None, None
+
+
+def photometric_loss(a: torch.Tensor, b: torch.Tensor, kernel: torch.Tensor,
+                     ssim_weight: float = 0.2):
+    """The trainer's loss (train.py:389-390) in one fused pass:
+    ``(1 - ssim_weight) * (a - b).abs().mean() + ssim_weight * (1 - ssim(a, b))``.
+
+    Returns (loss, parts), where parts is a detached device tensor holding
+    [L1 mean, SSIM mean]. Differentiable w.r.t. ``a`` only. The value and the
+    gradient equal the two-term torch expression up to float rounding.
+    """
+    w = kernel.reshape(-1, kernel.shape[-1])[0] if kernel.dim() > 1 else kernel
+    out = _PhotometricLoss.apply(a, b, w, ssim_weight)
+    return out[0], out[1:].detach()
+
+
 def ssim(a: torch.Tensor, b: torch.Tensor, kernel: torch.Tensor) -> torch.Tensor:
     """Mean SSIM of a, b (H,W,3) in [0,1]; differentiable w.r.t. ``a`` only.
 

@@ -55,7 +55,7 @@ def test_oversized_tile_is_refused_with_the_reference_message():
 
     lib = _lib.open_library()
     rc = lib.mg_rasterize_forward(0, None, None, None, None, None, 1, 96, 64, 64, 2, 1e-4,
-                                  1, 1, 1, 1, None)
+                                  None, 1, 1, 1, 1, None)
     assert rc == 1
     assert "threads per threadgroup" in lib.mg_last_error().decode()
 
@@ -100,7 +100,7 @@ def test_workspace_size_queries_are_pure():
     assert lib.mg_scan_workspace_bytes(0) > 0
     assert lib.mg_scan_workspace_bytes(1 << 20) >= 8 * ((1 << 20) // 2048)
     assert lib.mg_sort_workspace_bytes(3_500_000) >= 4 * 256 * (3_500_000 // 2048)
-    assert lib.mg_ssim_fused_workspace_bytes(800, 800) == 4 * 25 * 50 * 3
+    assert lib.mg_ssim_fused_workspace_bytes(800, 800) == 2 * 4 * 25 * 50 * 3   # SSIM + L1 sums
 
 
 @pytest.mark.parametrize("missing", [True])

@@ -39,7 +39,7 @@ def prepare(n, seed, W, H, tile, dev, elongate=False, sh=False):
     return uv, conic, op, col, gids, offs, tx
 
 
-def gpu_forward(args, W, H, tile, t_min):
+def gpu_forward(args, W, H, tile, t_min, background=None):
     from metal_gauss_amd import _lib
 
     uv, conic, op, col, gids, offs, tx = args
@@ -51,17 +51,19 @@ def gpu_forward(args, W, H, tile, t_min):
     lib = _lib.load()
     _lib.check(lib.mg_rasterize_forward(uv.shape[0], uv.data_ptr(), conic.data_ptr(),
                                         op.data_ptr(), col.data_ptr(), gids.data_ptr(),
-                                        offs.data_ptr(), W, H, tile, tx, t_min, rgb.data_ptr(),
+                                        offs.data_ptr(), W, H, tile, tx, t_min,
+                                        None if background is None else
+                                        _lib.f32_array(background), rgb.data_ptr(),
                                         alpha.data_ptr(), T.data_ptr(), stop.data_ptr(),
                                         _lib.stream(uv)))
     return rgb, alpha, T, stop
 
 
-def gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile, absgrad=True):
+def gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile, absgrad=True, background=None):
     from metal_gauss_amd import _lib
 
     uv, conic, op, col, gids, offs, tx = args
-    _, _, T, stop = fwd
+    _, alpha, T, stop = fwd
     N, dev = uv.shape[0], uv.device
     outs = [torch.full((N, 2), 7.0, device=dev), torch.full((N, 3), 7.0, device=dev),
             torch.full((N,), 7.0, device=dev), torch.full((N, 3), 7.0, device=dev),
@@ -70,8 +72,9 @@ def gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile, absgrad=True):
     _lib.check(lib.mg_rasterize_backward(
         N, uv.data_ptr(), conic.data_ptr(), op.data_ptr(), col.data_ptr(), gids.data_ptr(),
         offs.data_ptr(), T.data_ptr(), stop.data_ptr(), grad_rgb.data_ptr(),
-        grad_alpha.data_ptr(), W, H, tile, tx, *[o.data_ptr() if o is not None else None
-                                                   for o in outs], _lib.stream(uv)))
+        grad_alpha.data_ptr(), alpha.data_ptr() if background is not None else None,
+        None if background is None else _lib.f32_array(background), W, H, tile, tx,
+        *[o.data_ptr() if o is not None else None for o in outs], _lib.stream(uv)))
     return outs
 
 
@@ -182,3 +185,29 @@ def test_config2_scale_forward_and_backward(dev):
                               np_(grad_rgb), np_(grad_alpha), W, H, tile)
     for name, a, b in zip(("d_uv", "d_conic", "d_opacity", "d_color"), outs, ref):
         assert rel_l2(np_(a), b) < 1e-3, f"{name} rel L2 {rel_l2(np_(a), b):.2e}"
+
+
+def test_background_blend_in_kernel(dev):
+    """The in-kernel blend equals the reference's torch expression
+    rgb + (1 - alpha).clamp_min(0) * bg (metal_backend.py:539-541), and its
+    backward equals the plain backward with grad_alpha reduced by grad_rgb . bg
+    (clamp_min passes the gradient wherever 1 - alpha >= 0)."""
+    W, H, tile = 100, 63, 16
+    bg = (0.25, 0.5, 1.0)
+    args = prepare(600, 23, W, H, tile, dev, elongate=True)
+    plain = gpu_forward(args, W, H, tile, 1e-4)
+    blended = gpu_forward(args, W, H, tile, 1e-4, background=bg)
+    bgt = torch.tensor(bg, device=dev)
+    want = plain[0] + (1.0 - plain[1]).clamp_min(0)[..., None] * bgt
+    assert torch.equal(blended[0], want)
+    for a, b in zip(plain[1:], blended[1:]):
+        assert torch.equal(a, b)
+    g = torch.Generator().manual_seed(5)
+    grad_rgb = torch.randn(H, W, 3, generator=g).to(dev)
+    grad_alpha = torch.randn(H, W, generator=g).to(dev)
+    got = gpu_backward(args, blended, grad_rgb, grad_alpha, W, H, tile, background=bg)
+    ga = grad_alpha - torch.where(1.0 - plain[1] >= 0, (grad_rgb * bgt).sum(-1),
+                                  torch.zeros_like(grad_alpha))
+    ref = gpu_backward(args, plain, grad_rgb, ga.contiguous(), W, H, tile)
+    for a, b in zip(got, ref):
+        assert rel_l2(a.cpu(), b.cpu()) < 1e-5

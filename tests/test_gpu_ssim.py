@@ -75,3 +75,43 @@ def test_reference_abi_kernels(dev):
     a2 = a.double().requires_grad_(True)
     g2, = torch.autograd.grad(ssim_ref.ssim(a2, b.double(), ssim_ref.window(dtype=torch.float64)), a2)
     assert ((dx.cpu().double() - g2).abs().max() / g2.abs().max()).item() < 1e-4
+
+
+@pytest.mark.parametrize("H,W,lam", [(64, 64, 0.2), (97, 131, 0.2), (800, 800, 0.2),
+                                     (50, 70, 0.0), (50, 70, 1.0)])
+def test_photometric_loss_matches_the_trainer_expression(dev, H, W, lam):
+    """photometric_loss equals (1 - lam) * |a - b|.mean() + lam * (1 - ssim)
+    (train.py:389-390), with the SSIM term from the float64 conv2d oracle.
+    Value within 1e-6; gradient max error within 1e-4 of its magnitude. Some
+    pixels have a == b exactly, so the L1 term's sign(0) = 0 is exercised."""
+    from metal_gauss_amd import gaussian_kernel, photometric_loss
+
+    g = torch.Generator().manual_seed(H + W)
+    a = torch.rand(H, W, 3, generator=g)
+    b = torch.rand(H, W, 3, generator=g)
+    b[: H // 4] = a[: H // 4]
+    ag = a.to(dev).requires_grad_(True)
+    loss, parts = photometric_loss(ag, b.to(dev), gaussian_kernel(device=dev, groups=15), lam)
+    g1, = torch.autograd.grad(loss, ag)
+    a2 = a.double().requires_grad_(True)
+    l1 = (a2 - b.double()).abs().mean()
+    s2 = ssim_ref.ssim(a2, b.double(), ssim_ref.window(dtype=torch.float64))
+    want = (1.0 - lam) * l1 + lam * (1.0 - s2)
+    g2, = torch.autograd.grad(want, a2)
+    assert abs(loss.item() - want.item()) < 1e-6
+    assert abs(parts[0].item() - l1.item()) < 1e-6
+    assert abs(parts[1].item() - s2.item()) < 1e-6
+    err = ((g1.cpu().double() - g2).abs().max() / g2.abs().max()).item()
+    assert err < 1e-4, f"gradient rel err {err:.2e}"
+
+
+def test_photometric_loss_upstream_gradient(dev):
+    from metal_gauss_amd import gaussian_kernel, photometric_loss
+
+    g = torch.Generator().manual_seed(8)
+    a = torch.rand(40, 60, 3, generator=g).to(dev).requires_grad_(True)
+    b = torch.rand(40, 60, 3, generator=g).to(dev)
+    w = gaussian_kernel(device=dev)
+    g1, = torch.autograd.grad(photometric_loss(a, b, w)[0], a)
+    g2, = torch.autograd.grad(2.5 * photometric_loss(a, b, w)[0], a)
+    assert torch.allclose(g2, 2.5 * g1, rtol=1e-5, atol=1e-12)
