@@ -7,17 +7,21 @@
 // (SnugBox half-extents and the validity test that feeds binning).
 //
 // Memory: the per-Gaussian inputs are AoS rows (12/16/12/4 bytes plus a 192
-// byte SH row). The small rows are read straight from global memory (64 lanes
-// x 12-16 bytes is a contiguous span per instruction). The SH rows would be a
-// 192-byte stride per lane, so each wave stages its 64 rows through LDS with
-// fully coalesced dword loads and reads them back at an odd row pitch (49
-// floats) that keeps the 64 lanes on distinct banks.
+// byte SH row). Each kernel runs in two phases over a wave's 64 Gaussians:
+//   * projection: one lane per Gaussian; the small rows are contiguous spans
+//     of 64 x 12-16 bytes per load instruction;
+//   * SH colour: four lanes per Gaussian (a quad), in four rounds of 16
+//     Gaussians. Lane q of a quad owns bases 4q..4q+3, i.e. 48 contiguous
+//     bytes of the row, so a round reads (and the backward writes) 16 whole
+//     rows as 16-byte accesses with no LDS. Partial sums are combined with
+//     quad DPP swizzles; per-Gaussian values cross between the phases by wave
+//     shuffles. Quads of Gaussians that are not visible skip their row.
+// No LDS is used, so occupancy is limited by registers alone.
 #include "mg_common.h"
 
 namespace mg {
 
-constexpr int kPreThreads = 128;   // two waves: 2 x 12.25 KB of SH staging
-constexpr int kShPitch = 49;       // LDS floats per staged SH row (48 + 1 pad)
+constexpr int kPreThreads = 256;
 
 struct Cam {
     float R[9];      // world->camera rotation, row-major
@@ -190,58 +194,77 @@ __device__ __forceinline__ void project(const Cam &C, float mx, float my, float 
     P.c = P.T1[0] * ST1x + P.T1[1] * ST1y + P.T1[2] * ST1z + C.blur;
 }
 
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+// ------------------------------------------------------------ quad SH phase
+// In round r lane L works on the wave's Gaussian 16 r + L / 4, bases
+// 4 (L % 4) .. 4 (L % 4) + 3.
+
+// Sum over the four lanes of a quad, in every lane of it.
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    return v;
 }
 
-// Stages the SH rows of Gaussians [g0, g0+ng) into S[row*kShPitch + 3*basis +
-// channel], only the first 3*nb floats of each row. Wave-collective.
-__device__ __forceinline__ void stage_sh(float *S, const float *sh, const float *rest,
-                                        bool fused, int64_t g0, int ng, int nb, int lane) {
-    const int kmax = 3 * nb;
-    if (fused) {
-        const float *src = sh + g0 * 48;
-        for (int e = lane; e < ng * 48; e += 64) {
-            const int gi = e / 48, k = e - gi * 48;
-            if (k < kmax) S[gi * kShPitch + k] = src[e];
-        }
-    } else {
-        const float *src = sh + g0 * 3;
-        for (int e = lane; e < ng * 3; e += 64) {
-            const int gi = e / 3, k = e - gi * 3;
-            S[gi * kShPitch + k] = src[e];
-        }
-        if (nb > 1) {
-            const float *src2 = rest + g0 * 45;
-            for (int e = lane; e < ng * 45; e += 64) {
-                const int gi = e / 45, k = e - gi * 45;
-                if (k + 3 < kmax) S[gi * kShPitch + 3 + k] = src2[e];
+// This lane's four basis values out of the sixteen (q = lane % 4), without
+// dynamic register indexing.
+__device__ __forceinline__ void pick4(const float B[16], int q, float b[4]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        b[k] = q == 0 ? B[k] : (q == 1 ? B[4 + k] : (q == 2 ? B[8 + k] : B[12 + k]));
+}
+
+struct ShRows {
+    const float *sh, *rest;   // fused (N,16,3) in sh, or DC (N,1,3) + rest (N,15,3)
+    int fused, vec4;          // vec4: fused, 16-byte aligned and degree 3
+};
+
+// Loads coefficients c[k][ch] of bases 4q+k (k < 4) of Gaussian G; bases at
+// or past nb read as 0.
+__device__ __forceinline__ void load_bases(const ShRows &R, int64_t G, int q, int nb,
+                                           float c[4][3]) {
+    if (R.vec4) {
+        const float4 *src = reinterpret_cast<const float4 *>(R.sh + G * 48 + 12 * q);
+        const float4 a = src[0], b = src[1], d = src[2];
+        c[0][0] = a.x; c[0][1] = a.y; c[0][2] = a.z;
+        c[1][0] = a.w; c[1][1] = b.x; c[1][2] = b.y;
+        c[2][0] = b.z; c[2][1] = b.w; c[2][2] = d.x;
+        c[3][0] = d.y; c[3][1] = d.z; c[3][2] = d.w;
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = 4 * q + k;
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) {
+            float v = 0.f;
+            if (i < nb) {
+                if (R.fused) v = R.sh[G * 48 + 3 * i + ch];
+                else v = i == 0 ? R.sh[G * 3 + ch] : R.rest[G * 45 + 3 * (i - 1) + ch];
             }
+            c[k][ch] = v;
         }
     }
 }
 
-// Writes S rows back to the gradient layout with coalesced stores.
-__device__ __forceinline__ void unstage_sh(const float *S, float *dsh, float *drest, bool fused,
-                                          int64_t g0, int ng, int lane) {
-    if (fused) {
-        float *dst = dsh + g0 * 48;
-        for (int e = lane; e < ng * 48; e += 64) {
-            const int gi = e / 48, k = e - gi * 48;
-            dst[e] = S[gi * kShPitch + k];
-        }
-    } else {
-        float *dst = dsh + g0 * 3;
-        for (int e = lane; e < ng * 3; e += 64) {
-            const int gi = e / 3, k = e - gi * 3;
-            dst[e] = S[gi * kShPitch + k];
-        }
-        float *dst2 = drest + g0 * 45;
-        for (int e = lane; e < ng * 45; e += 64) {
-            const int gi = e / 45, k = e - gi * 45;
-            dst2[e] = S[gi * kShPitch + 3 + k];
+// Stores d[k][ch] as the gradient of bases 4q+k of Gaussian G (all 16 bases
+// are written; the caller passes zeros past the degree).
+__device__ __forceinline__ void store_bases(float *dsh, float *drest, int fused, int vec4,
+                                            int64_t G, int q, const float d[4][3]) {
+    if (vec4) {
+        float4 *dst = reinterpret_cast<float4 *>(dsh + G * 48 + 12 * q);
+        dst[0] = make_float4(d[0][0], d[0][1], d[0][2], d[1][0]);
+        dst[1] = make_float4(d[1][1], d[1][2], d[2][0], d[2][1]);
+        dst[2] = make_float4(d[2][2], d[3][0], d[3][1], d[3][2]);
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = 4 * q + k;
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) {
+            if (fused) dsh[G * 48 + 3 * i + ch] = d[k][ch];
+            else if (i == 0) dsh[G * 3 + ch] = d[k][ch];
+            else drest[G * 45 + 3 * (i - 1) + ch] = d[k][ch];
         }
     }
 }
@@ -250,30 +273,30 @@ struct PreFwdArgs {
     Cam C;
     int64_t N;
     const float *means, *quats, *scales, *sh, *rest, *opac;
-    int32_t fused;
+    int32_t fused, vec4;
     float *uv, *conic, *depth, *rxy, *color;
     int32_t *valid;
 };
 
 __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFwdArgs A) {
-    __shared__ float s_sh[kPreThreads / 64][64 * kShPitch];
     const Cam &C = A.C;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t g0 = (int64_t)blockIdx.x * kPreThreads + wave * 64;
     const int64_t g = g0 + lane;
     const bool in = g < A.N;
 
+    // ------------------------------------------ projection: lane = Gaussian
     bool ok = false;
-    float u = 0.f, v = 0.f;
+    float mx = 0.f, my = 0.f, mz = 0.f;
     if (in) {
-        const float mx = A.means[3 * g], my = A.means[3 * g + 1], mz = A.means[3 * g + 2];
+        mx = A.means[3 * g]; my = A.means[3 * g + 1]; mz = A.means[3 * g + 2];
         const float qv[4] = {A.quats[4 * g], A.quats[4 * g + 1], A.quats[4 * g + 2], A.quats[4 * g + 3]};
         const float sv[3] = {A.scales[3 * g], A.scales[3 * g + 1], A.scales[3 * g + 2]};
         Proj P;
         project(C, mx, my, mz, qv, sv, P);
         const float z = P.p[2];
-        u = C.fx * P.p[0] / P.zc + C.cx;
-        v = C.fy * P.p[1] / P.zc + C.cy;
+        const float u = C.fx * P.p[0] / P.zc + C.cx;
+        const float v = C.fy * P.p[1] / P.zc + C.cy;
         const float det = P.a * P.c - P.b * P.b;
         const float dets = fmaxf(det, 1e-12f);
         const float mid = 0.5f * (P.a + P.c);
@@ -303,52 +326,60 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFw
     }
 
     if (A.sh == nullptr) return;   // explicit-colour callers: no SH, no colour
-    // Wave-uniform: only waves holding at least one valid Gaussian pay for the
-    // SH rows (sh.py is evaluated only where the rasteriser can look).
+    // Colour is evaluated only where the rasteriser can look (sh.py at the
+    // visible Gaussians); the rest get 0.
     if (ballot(ok) == 0) {
         if (in) { A.color[3 * g] = 0.f; A.color[3 * g + 1] = 0.f; A.color[3 * g + 2] = 0.f; }
         return;
     }
+    float ux = 0.f, uy = 0.f, uz = 0.f;   // unit view direction
+    if (ok) {
+        const float dx = mx - C.cc[0], dy = my - C.cc[1], dz = mz - C.cc[2];
+        const float inv = 1.0f / fmaxf(sqrtf(dx * dx + dy * dy + dz * dz), 1e-12f);
+        ux = dx * inv; uy = dy * inv; uz = dz * inv;
+    }
+
+    // ---------------------------------------------- SH colour: quad = Gaussian
     const int nb = (C.deg + 1) * (C.deg + 1);
-    const int ng = (int)min((int64_t)64, A.N - g0);
-    float *S = s_sh[wave];
-    stage_sh(S, A.sh, A.rest, A.fused != 0, g0, ng, nb, lane);
-    wave_lds_sync();
-    if (!in) return;
-    if (!ok) {
-        A.color[3 * g] = 0.f; A.color[3 * g + 1] = 0.f; A.color[3 * g + 2] = 0.f;
-        return;
+    const ShRows R{A.sh, A.rest, A.fused, A.vec4};
+    const int q = lane & 3;
+#pragma unroll 1
+    for (int r = 0; r < 4; ++r) {
+        const int gl = 16 * r + (lane >> 2);
+        const int64_t G = g0 + gl;
+        const bool okq = __shfl((int)ok, gl, 64) != 0;     // false past the end
+        const float x = __shfl(ux, gl, 64), y = __shfl(uy, gl, 64), z = __shfl(uz, gl, 64);
+        float part[3] = {0.f, 0.f, 0.f};
+        if (okq) {
+            float c[4][3], b[4];
+            load_bases(R, G, q, nb, c);
+            float B[16] = {};
+            sh_basis(C.deg, x, y, z, B);
+            pick4(B, q, b);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int ch = 0; ch < 3; ++ch) part[ch] += b[k] * c[k][ch];
+        }
+        const float s0 = quad_sum(part[0]), s1 = quad_sum(part[1]), s2 = quad_sum(part[2]);
+        if (G < A.N && q < 3) {
+            const float sv = q == 0 ? s0 : (q == 1 ? s1 : s2);
+            A.color[3 * G + q] = okq ? fmaxf(sv + 0.5f, 0.0f) : 0.0f;
+        }
     }
-    const float dx = A.means[3 * g] - C.cc[0];
-    const float dy = A.means[3 * g + 1] - C.cc[1];
-    const float dz = A.means[3 * g + 2] - C.cc[2];
-    const float inv = 1.0f / fmaxf(sqrtf(dx * dx + dy * dy + dz * dz), 1e-12f);
-    float B[16];
-    sh_basis(C.deg, dx * inv, dy * inv, dz * inv, B);
-    const float *row = S + lane * kShPitch;
-    float r = 0.f, gg = 0.f, bb = 0.f;
-    for (int i = 0; i < nb; ++i) {
-        r += B[i] * row[3 * i];
-        gg += B[i] * row[3 * i + 1];
-        bb += B[i] * row[3 * i + 2];
-    }
-    A.color[3 * g] = fmaxf(r + 0.5f, 0.0f);
-    A.color[3 * g + 1] = fmaxf(gg + 0.5f, 0.0f);
-    A.color[3 * g + 2] = fmaxf(bb + 0.5f, 0.0f);
 }
 
 struct PreBwdArgs {
     Cam C;
     int64_t N;
     const float *means, *quats, *scales, *sh, *rest;
-    int32_t fused;
+    int32_t fused, vec4, st_vec4;
     const float *d_uv, *d_conic, *d_color;
     const int32_t *valid;
     float *d_means, *d_quats, *d_scales, *d_sh, *d_rest;
 };
 
 __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBwdArgs A) {
-    __shared__ float s_sh[kPreThreads / 64][64 * kShPitch];
     const Cam &C = A.C;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t g0 = (int64_t)blockIdx.x * kPreThreads + wave * 64;
@@ -356,79 +387,98 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
     const bool in = g < A.N;
 
     float mx = 0.f, my = 0.f, mz = 0.f;
-    if (in) { mx = A.means[3 * g]; my = A.means[3 * g + 1]; mz = A.means[3 * g + 2]; }
+    int vld = 0;
+    if (in) {
+        mx = A.means[3 * g]; my = A.means[3 * g + 1]; mz = A.means[3 * g + 2];
+        vld = A.valid[g];
+    }
     float dmean[3] = {0.f, 0.f, 0.f};
 
-    // ------------------------------------------------------------ SH branch
+    // ------------------------------------------------ SH: quad = Gaussian
     if (A.d_color != nullptr) {
         float dcol[3] = {0.f, 0.f, 0.f};
         if (in) { dcol[0] = A.d_color[3 * g]; dcol[1] = A.d_color[3 * g + 1]; dcol[2] = A.d_color[3 * g + 2]; }
-        const bool need = in && (dcol[0] != 0.f || dcol[1] != 0.f || dcol[2] != 0.f);
-        // Wave-uniform row count of this wave's chunk (0 past the end).
+        // The colour of a Gaussian that is not visible is the constant 0, so
+        // its coefficients get no gradient.
+        const bool need = vld != 0 && (dcol[0] != 0.f || dcol[1] != 0.f || dcol[2] != 0.f);
         const int ng = (int)max((int64_t)0, min((int64_t)64, A.N - g0));
-        const int nb = (C.deg + 1) * (C.deg + 1);
-        float *S = s_sh[wave];
-        const bool wave_needs = ballot(need) != 0;
-        if (wave_needs) {
-            stage_sh(S, A.sh, A.rest, A.fused != 0, g0, ng, nb, lane);
-            wave_lds_sync();
-        }
-        float *row = S + lane * kShPitch;
-        if (need) {
-            const float vx = mx - C.cc[0], vy = my - C.cc[1], vz = mz - C.cc[2];
-            const float n = fmaxf(sqrtf(vx * vx + vy * vy + vz * vz), 1e-12f);
-            const float dx = vx / n, dy = vy / n, dz = vz / n;
-            float B[16];
-            sh_basis(C.deg, dx, dy, dz, B);
-            float pre[3] = {0.5f, 0.5f, 0.5f};
-            for (int i = 0; i < nb; ++i) {
-                pre[0] += B[i] * row[3 * i];
-                pre[1] += B[i] * row[3 * i + 1];
-                pre[2] += B[i] * row[3 * i + 2];
-            }
-            // ReLU gate of colour = max(pre, 0) (torch_ref.py:331).
-            const float dp0 = pre[0] > 0.f ? dcol[0] : 0.f;
-            const float dp1 = pre[1] > 0.f ? dcol[1] : 0.f;
-            const float dp2 = pre[2] > 0.f ? dcol[2] : 0.f;
-            float wts[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) wts[i] = 0.f;
-            for (int i = 0; i < nb; ++i)
-                wts[i] = row[3 * i] * dp0 + row[3 * i + 1] * dp1 + row[3 * i + 2] * dp2;
-            float gd[3];
-            sh_basis_vjp(C.deg, dx, dy, dz, wts, gd);
-            // dir = v/|v|: d v = (I - dir dir^T) d dir / |v|
-            const float dd = dx * gd[0] + dy * gd[1] + dz * gd[2];
-            dmean[0] += (gd[0] - dx * dd) / n;
-            dmean[1] += (gd[1] - dy * dd) / n;
-            dmean[2] += (gd[2] - dz * dd) / n;
-            // Overwrite the staged coefficients with their gradient.
-            for (int i = 0; i < 16; ++i) {
-                const float bi = i < nb ? B[i] : 0.f;
-                row[3 * i] = bi * dp0;
-                row[3 * i + 1] = bi * dp1;
-                row[3 * i + 2] = bi * dp2;
-            }
-        } else if (wave_needs) {
-            for (int i = 0; i < 48; ++i) row[i] = 0.f;
-        }
-        if (wave_needs) {
-            wave_lds_sync();
-            unstage_sh(S, A.d_sh, A.d_rest, A.fused != 0, g0, ng, lane);
-        } else if (ng > 0) {
-            // Whole wave had zero colour gradient: coalesced zero fill.
+        if (ballot(need) == 0) {
+            // Coalesced zero fill of the wave's rows.
             if (A.fused) {
                 for (int e = lane; e < ng * 48; e += 64) A.d_sh[g0 * 48 + e] = 0.f;
             } else {
                 for (int e = lane; e < ng * 3; e += 64) A.d_sh[g0 * 3 + e] = 0.f;
                 for (int e = lane; e < ng * 45; e += 64) A.d_rest[g0 * 45 + e] = 0.f;
             }
+        } else {
+            float ux = 0.f, uy = 0.f, uz = 0.f, un = 1.f;
+            if (need) {
+                const float vx = mx - C.cc[0], vy = my - C.cc[1], vz = mz - C.cc[2];
+                un = fmaxf(sqrtf(vx * vx + vy * vy + vz * vz), 1e-12f);
+                ux = vx / un; uy = vy / un; uz = vz / un;
+            }
+            const int nb = (C.deg + 1) * (C.deg + 1);
+            const ShRows R{A.sh, A.rest, A.fused, A.vec4};
+            const int q = lane & 3;
+#pragma unroll 1
+            for (int r = 0; r < 4; ++r) {
+                const int gl = 16 * r + (lane >> 2);
+                const int64_t G = g0 + gl;
+                const bool nq = __shfl((int)need, gl, 64) != 0;
+                const float x = __shfl(ux, gl, 64), y = __shfl(uy, gl, 64);
+                const float z = __shfl(uz, gl, 64), n = __shfl(un, gl, 64);
+                const float d0 = __shfl(dcol[0], gl, 64), d1 = __shfl(dcol[1], gl, 64);
+                const float d2 = __shfl(dcol[2], gl, 64);
+                float c[4][3] = {}, b[4] = {0.f, 0.f, 0.f, 0.f};
+                float pre[3] = {0.f, 0.f, 0.f};
+                if (nq) {
+                    load_bases(R, G, q, nb, c);
+                    float B[16] = {};
+                    sh_basis(C.deg, x, y, z, B);
+                    pick4(B, q, b);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+#pragma unroll
+                        for (int ch = 0; ch < 3; ++ch) pre[ch] += b[k] * c[k][ch];
+                }
+                const float p0 = quad_sum(pre[0]) + 0.5f, p1 = quad_sum(pre[1]) + 0.5f;
+                const float p2 = quad_sum(pre[2]) + 0.5f;
+                // ReLU gate of colour = max(pre, 0) (torch_ref.py:331).
+                const float dp0 = p0 > 0.f ? d0 : 0.f, dp1 = p1 > 0.f ? d1 : 0.f;
+                const float dp2 = p2 > 0.f ? d2 : 0.f;
+                float dsh[4][3];
+                float w16[16];
+                float wk[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    dsh[k][0] = nq ? b[k] * dp0 : 0.f;
+                    dsh[k][1] = nq ? b[k] * dp1 : 0.f;
+                    dsh[k][2] = nq ? b[k] * dp2 : 0.f;
+                    wk[k] = c[k][0] * dp0 + c[k][1] * dp1 + c[k][2] * dp2;
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) w16[i] = (i >> 2) == q && nq ? wk[i & 3] : 0.f;
+                if (G < A.N) store_bases(A.d_sh, A.d_rest, A.fused, A.st_vec4, G, q, dsh);
+                float gp[3] = {0.f, 0.f, 0.f};
+                if (nq) sh_basis_vjp(C.deg, x, y, z, w16, gp);
+                const float g0s = quad_sum(gp[0]), g1s = quad_sum(gp[1]), g2s = quad_sum(gp[2]);
+                // dir = v/|v|: d v = (I - dir dir^T) d dir / |v|
+                const float dd = x * g0s + y * g1s + z * g2s;
+                const float m0 = nq ? (g0s - x * dd) / n : 0.f;
+                const float m1 = nq ? (g1s - y * dd) / n : 0.f;
+                const float m2 = nq ? (g2s - z * dd) / n : 0.f;
+                // Back to the lane that owns the Gaussian.
+                const int src = 4 * (lane & 15);
+                const float v0 = __shfl(m0, src, 64), v1 = __shfl(m1, src, 64);
+                const float v2 = __shfl(m2, src, 64);
+                if ((lane >> 4) == r) { dmean[0] += v0; dmean[1] += v1; dmean[2] += v2; }
+            }
         }
     }
     if (!in) return;
 
-    // --------------------------------------------------- projection branch
-    if (A.valid[g] != 0) {
+    // ------------------------------------------ projection: lane = Gaussian
+    if (vld != 0) {
         const float qv[4] = {A.quats[4 * g], A.quats[4 * g + 1], A.quats[4 * g + 2], A.quats[4 * g + 3]};
         const float sv[3] = {A.scales[3 * g], A.scales[3 * g + 1], A.scales[3 * g + 2]};
         Proj P;
@@ -589,6 +639,7 @@ int32_t mg_preprocess_forward(int64_t N, const float *means, const float *quats,
     A.means = means; A.quats = quats; A.scales = scales; A.sh = sh;
     A.rest = sh_rest; A.opac = opacities; A.fused = sh_fused;
     A.uv = uv; A.conic = conic; A.depth = depth; A.rxy = rxy; A.valid = valid; A.color = color;
+    A.vec4 = sh && sh_fused && sh_degree == 3 && ((uintptr_t)sh & 15) == 0;
     const int64_t blocks = ceil_div(N, kPreThreads);
     TimedScope ts("preprocess_forward", as_stream(stream));
     preprocess_fwd_kernel<<<(unsigned)blocks, kPreThreads, 0, as_stream(stream)>>>(A);
@@ -622,6 +673,8 @@ int32_t mg_preprocess_backward(int64_t N, const float *means, const float *quats
     A.fused = sh_fused; A.d_uv = d_uv; A.d_conic = d_conic; A.d_color = d_color; A.valid = valid;
     A.d_means = d_means; A.d_quats = d_quats; A.d_scales = d_scales; A.d_sh = d_sh;
     A.d_rest = d_sh_rest;
+    A.vec4 = sh && sh_fused && sh_degree == 3 && ((uintptr_t)sh & 15) == 0;
+    A.st_vec4 = d_sh && sh_fused && sh_degree == 3 && ((uintptr_t)d_sh & 15) == 0;
     const int64_t blocks = ceil_div(N, kPreThreads);
     TimedScope ts("preprocess_backward", as_stream(stream));
     preprocess_bwd_kernel<<<(unsigned)blocks, kPreThreads, 0, as_stream(stream)>>>(A);
