@@ -106,6 +106,46 @@ struct Stage {
 
 constexpr int kGradSlots = 10;   // colour 3, uv 2, conic 3, opacity, |uv|
 
+// Pairwise wave-wide sums by lane swaps. v_permlane32_swap a, b swaps lanes
+// 32-63 of a with lanes 0-31 of b, leaving (a[0:32], b[0:32]) in a and
+// (a[32:64], b[32:64]) in b, so a + b holds a's half-sums in lanes 0-31 and
+// b's in lanes 32-63. v_permlane16_swap does the same between rows 0/1 and
+// 2/3. Issued as inline assembly: this compiler folds the two results of the
+// __builtin_amdgcn_permlane*_swap builtins into one register (r[0] + r[1]
+// comes out as r[0] + r[0]). The s_nop gives the two wait states a swap
+// needs after a VALU write of its operands.
+__device__ __forceinline__ float swap32_sum(float a, float b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+__device__ __forceinline__ float swap16_sum(float a, float b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+// Sum over the 16 lanes of each row, in every lane of the row.
+__device__ __forceinline__ float row_allsum(float x) {
+    x += dpp_f<0x128>(x);   // row_ror:8
+    x += dpp_f<0x124>(x);   // row_ror:4
+    x += dpp_f<0x122>(x);   // row_ror:2
+    x += dpp_f<0x121>(x);   // row_ror:1
+    return x;
+}
+// Wave sums of ten values in 28 VALU operations instead of ten separate
+// reductions: after the 32- and 16-lane swap stages each row of 16 lanes
+// carries one value's partials, which a row reduction finishes. Rows of q0
+// hold the sums of v0, v2, v1, v3; of q1 v4, v6, v5, v7; of q2 v8, -, v9, -.
+__device__ __forceinline__ void reduce10_to_rows(const float v[10], float &q0, float &q1,
+                                                 float &q2) {
+    const float p0 = swap32_sum(v[0], v[1]);
+    const float p1 = swap32_sum(v[2], v[3]);
+    const float p2 = swap32_sum(v[4], v[5]);
+    const float p3 = swap32_sum(v[6], v[7]);
+    const float p4 = swap32_sum(v[8], v[9]);
+    q0 = row_allsum(swap16_sum(p0, p1));
+    q1 = row_allsum(swap16_sum(p2, p3));
+    q2 = row_allsum(swap16_sum(p4, 0.0f));
+}
+
 template <int MAXW>
 struct StageBwd : Stage<MAXW> {
     float grad[kGradSlots][kBatch];   // per batch entry, summed over waves
@@ -346,14 +386,19 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
                     if (want_abs) v[9] = sqrtf(v[3] * v[3] + v[4] * v[4]);
                 }
             }
-            const int nq = want_abs ? kGradSlots : kGradSlots - 1;
-#pragma unroll
-            for (int q = 0; q < kGradSlots; ++q)
-                if (q < nq) v[q] = wave_sum_to_lane63(v[q]);
-            if (lane == 63) {
-#pragma unroll
-                for (int q = 0; q < kGradSlots; ++q)
-                    if (q < nq && v[q] != 0.f) atomicAdd(&S.grad[q][j], v[q]);
+            // Sums over the wave of v[0..9], deposited into S.grad[.][j]
+            // with four lanes per LDS atomic (see reduce10_to_rows).
+            float q0, q1, q2;
+            reduce10_to_rows(v, q0, q1, q2);
+            if ((lane & 15) == 0) {
+                const int row = lane >> 4;
+                // Row r of Q0 holds slot {0,2,1,3}[r], of Q1 {4,6,5,7}[r],
+                // of Q2 {8,-,9,-}[r].
+                const int s0 = (row & 1) * 2 + (row >> 1);
+                if (q0 != 0.f) atomicAdd(&S.grad[s0][j], q0);
+                if (q1 != 0.f) atomicAdd(&S.grad[4 + s0][j], q1);
+                if ((row & 1) == 0 && q2 != 0.f && (row == 0 || want_abs))
+                    atomicAdd(&S.grad[8 + (row >> 1)][j], q2);
             }
         }
         __syncthreads();
