@@ -206,12 +206,22 @@ int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy,
  * out_stop holds the stop INDEX into gauss_ids (the reference's n_contrib).
  * background (host, 3 floats, or NULL) blends the colour in the kernel:
  * rgb += max(1 - alpha, 0) * background, the torch glue of
- * metal_backend.py:539-541 (out_alpha stays the coverage). */
+ * metal_backend.py:539-541 (out_alpha stays the coverage).
+ *
+ * chunk_ws (device, or NULL) enables the chunked backward: the forward plans
+ * one backward work unit per 512 list entries of each tile and records each
+ * pixel's state at every unit's end, so mg_rasterize_backward can run the
+ * units in parallel instead of one long chain per tile. Size it with
+ * mg_rasterize_chunk_workspace_bytes(n_isect, tiles, tile), where n_isect
+ * is the length of gauss_ids, and pass it unchanged to the backward. */
+int64_t mg_rasterize_chunk_workspace_bytes(int64_t n_isect, int32_t n_tiles,
+                                           int32_t tile);
 int32_t mg_rasterize_forward(
     int64_t N, const float *uv, const float *conic, const float *opacity,
     const float *color, const int32_t *gauss_ids, const int32_t *tile_offsets,
     int32_t W, int32_t H, int32_t tile, int32_t tiles_x, float t_min,
-    const float *background, float *out_rgb, float *out_alpha, float *out_T,
+    const float *background, int64_t n_isect, void *chunk_ws,
+    int64_t chunk_ws_bytes, float *out_rgb, float *out_alpha, float *out_T,
     int32_t *out_stop, mg_stream_t stream);
 
 /* Back-to-front replay of mg_rasterize_forward. Replaces rasterize_backward
@@ -221,15 +231,16 @@ int32_t mg_rasterize_forward(
  * of |d_uv| (the reference's absgrad statistic). With the forward's
  * background (host, or NULL), grad_rgb is the gradient of the blended colour
  * and alpha (the forward's out_alpha, device) adds the blend's share to
- * grad_alpha. */
+ * grad_alpha. n_isect / chunk_ws / chunk_ws_bytes are the forward's (chunk_ws
+ * NULL: one workgroup per tile). */
 int32_t mg_rasterize_backward(
     int64_t N, const float *uv, const float *conic, const float *opacity,
     const float *color, const int32_t *gauss_ids, const int32_t *tile_offsets,
     const float *final_T, const int32_t *stop, const float *grad_rgb,
     const float *grad_alpha, const float *alpha, const float *background,
-    int32_t W, int32_t H, int32_t tile, int32_t tiles_x, float *d_uv,
-    float *d_conic, float *d_opacity, float *d_color, float *d_absuv,
-    mg_stream_t stream);
+    int64_t n_isect, const void *chunk_ws, int64_t chunk_ws_bytes, int32_t W,
+    int32_t H, int32_t tile, int32_t tiles_x, float *d_uv, float *d_conic,
+    float *d_opacity, float *d_color, float *d_absuv, mg_stream_t stream);
 
 /* ------------------------------------------------------------------- Adam */
 

@@ -347,10 +347,12 @@ class _RasterizeMetal(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, uv, conic, opacity, color, gauss_ids, tile_offsets, W, H, tile, tiles_x,
-                absgrad_out=None, t_min=DEFAULT_T_MIN, background=None):
+                absgrad_out=None, t_min=DEFAULT_T_MIN, background=None, chunked=False):
         """``background`` is None or three host floats blended in the kernel
         (rgb + max(1 - alpha, 0) * background); the backward then carries the
-        blend's gradient too."""
+        blend's gradient too. ``chunked`` runs the backward as independent
+        512-entry units per tile from checkpoints the forward records, which
+        pays when a few tiles hold most of the intersections."""
         lib = _load()
         dev = uv.device
         uv, conic, opacity, color = (t.contiguous() for t in (uv, conic, opacity, color))
@@ -359,15 +361,22 @@ class _RasterizeMetal(torch.autograd.Function):
         alpha = torch.empty(H, W, device=dev)
         T = torch.empty(H, W, device=dev)
         stop = torch.empty(H, W, dtype=torch.int32, device=dev)
+        # Plan + per-chunk pixel states for the chunked backward.
+        n_isect = gauss_ids.numel()
+        chunk_ws = torch.empty(
+            lib.mg_rasterize_chunk_workspace_bytes(n_isect, tile_offsets.numel() - 1, tile)
+            if chunked else 0, dtype=torch.uint8, device=dev)
         _lib.check(lib.mg_rasterize_forward(
             N, _lib.dev_tensor(uv, "uv"), _lib.dev_tensor(conic, "conic"),
             _lib.dev_tensor(opacity, "opacity"), _lib.dev_tensor(color, "color"),
             _lib.dev_tensor(gauss_ids, "gauss_ids", torch.int32),
             _lib.dev_tensor(tile_offsets, "tile_offsets", torch.int32), W, H, tile, tiles_x,
             float(t_min), None if background is None else _lib.f32_array(background),
-            rgb.data_ptr(), alpha.data_ptr(), T.data_ptr(), stop.data_ptr(), _lib.stream(uv)))
+            n_isect, chunk_ws.data_ptr() if chunked else None, chunk_ws.numel(), rgb.data_ptr(),
+            alpha.data_ptr(),
+            T.data_ptr(), stop.data_ptr(), _lib.stream(uv)))
         ctx.save_for_backward(uv, conic, opacity, color, gauss_ids, tile_offsets, T, stop,
-                              alpha if background is not None else None)
+                              alpha if background is not None else None, chunk_ws)
         ctx.dims = (W, H, tile, tiles_x)
         ctx.background = background
         # absgrad is a statistic of the backward, not a gradient: the caller
@@ -378,7 +387,8 @@ class _RasterizeMetal(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_rgb, grad_alpha):
         lib = _load()
-        uv, conic, opacity, color, gauss_ids, tile_offsets, T, stop, alpha = ctx.saved_tensors
+        (uv, conic, opacity, color, gauss_ids, tile_offsets, T, stop, alpha,
+         chunk_ws) = ctx.saved_tensors
         W, H, tile, tiles_x = ctx.dims
         bg = ctx.background
         N = uv.shape[0]
@@ -395,11 +405,13 @@ class _RasterizeMetal(torch.autograd.Function):
             gauss_ids.data_ptr(), tile_offsets.data_ptr(), T.data_ptr(), stop.data_ptr(),
             _lib.dev_tensor(grad_rgb, "grad_rgb"), _lib.dev_tensor(grad_alpha, "grad_alpha"),
             None if bg is None else alpha.data_ptr(), None if bg is None else _lib.f32_array(bg),
-            W, H, tile, tiles_x, d_uv.data_ptr(), d_conic.data_ptr(), d_op.data_ptr(),
+            gauss_ids.numel(), chunk_ws.data_ptr() if chunk_ws.numel() else None,
+            chunk_ws.numel(), W, H, tile, tiles_x,
+            d_uv.data_ptr(), d_conic.data_ptr(), d_op.data_ptr(),
             d_col.data_ptr(), None if d_abs is None else d_abs.data_ptr(), _lib.stream(uv)))
         if ctx.absgrad_out is not None:
             ctx.absgrad_out[:N] += d_abs
-        return (d_uv, d_conic, d_op, d_col) + (None,) * 9
+        return (d_uv, d_conic, d_op, d_col) + (None,) * 10
 
 
 # Names that describe this backend rather than the reference's.
@@ -470,7 +482,8 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
            near: float = 0.01, far: float = 100.0,
            background=(0.0, 0.0, 0.0), colors=None, max_radius_frac: float = 1.0,
            sh_rest=None, antialias: bool = False, absgrad_out=None,
-           min_transmittance: float = DEFAULT_T_MIN, **_ignored):
+           min_transmittance: float = DEFAULT_T_MIN, chunked_backward: bool = False,
+           **_ignored):
     """Render Gaussians from one camera; same signature as the reference's.
 
     means (N,3) world; quats (N,4) wxyz (need not be normalised); scales (N,3)
@@ -479,6 +492,9 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     (rgb (H,W,3), alpha (H,W), info). ``colors`` (N,3) bypasses SH.
     ``min_transmittance`` is the per-pixel early-stop threshold (the
     reference's fixed 1e-4); 0 composites every listed Gaussian.
+    ``chunked_backward`` splits each tile's backward into 512-entry units run
+    in parallel (same gradients up to rounding); it helps when a few tiles hold
+    most of the intersections.
     """
     explicit_colors = colors is not None
     _require_gpu(means)
@@ -519,7 +535,7 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     bg_host = _host_background(background)
     rgb, alpha = _RasterizeMetal.apply(
         uv, conic, opacities, colors, gauss_ids, tile_offsets, W, H, tile, tiles_x,
-        absgrad_out, min_transmittance, bg_host)
+        absgrad_out, min_transmittance, bg_host, chunked_backward)
 
     if background is not None and bg_host is None:
         bg = torch.as_tensor(background, device=rgb.device, dtype=rgb.dtype)

@@ -465,8 +465,6 @@ __global__ __launch_bounds__(256) void tile_ranges_u32_kernel(const uint32_t *ti
     for (int64_t t = prev + 1; t <= cur && t <= n_tiles; ++t) offsets[t] = (int32_t)i;
 }
 
-inline int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
-
 // Carves the begin/finish workspace identically on both calls. After begin,
 // perm_a holds the depth order, offsets the scanned counts in that order and
 // recs the walk records.

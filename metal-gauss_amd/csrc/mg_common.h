@@ -29,6 +29,9 @@ inline hipStream_t as_stream(mg_stream_t s) { return reinterpret_cast<hipStream_
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Workspace carving: every sub-buffer starts on a 256-byte boundary.
+inline int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
+
 // Number of XCDs workgroups are spread over, round-robin by workgroup id.
 constexpr int kXcds = 8;
 
@@ -56,17 +59,6 @@ constexpr int kXcds = 8;
     } while (0)
 
 // -------------------------------------------------------------- device side
-
-// Maps a linear workgroup id onto a work index so that each XCD (which
-// receives every 8th workgroup) processes one contiguous band of the work.
-// Neighbouring tiles share Gaussians, so keeping them on one XCD keeps the
-// shared records in that XCD's L2. `total` is the real work count; the grid
-// has ceil(total/8)*8 workgroups and the surplus ones get -1.
-__device__ __forceinline__ int xcd_band(int bid, int total) {
-    const int per = (total + kXcds - 1) / kXcds;
-    const int w = (bid % kXcds) * per + bid / kXcds;
-    return w < total ? w : -1;
-}
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 

@@ -58,6 +58,31 @@ __device__ __forceinline__ void tile_pixel(int tid, int tile, int &lx, int &ly, 
     }
 }
 
+// Workgroup -> tile. The dispatcher deals workgroup b to XCD b % 8, as that
+// XCD's (b / 8)-th. Tiles are grouped into kSuper x kSuper super-tiles, and
+// the super-tiles are dealt round-robin to the XCDs. Neighbouring tiles share
+// many Gaussians, so each super-tile's 16 tiles run on one XCD and hit its
+// L2. Every XCD gets super-tiles from all over the image, so the dense
+// centre is spread over all eight. Slots outside the image get -1.
+constexpr int kSuper = 4;
+
+inline int raster_grid(int tiles_x, int tiles_y) {
+    const int n_super = ((tiles_x + kSuper - 1) / kSuper) * ((tiles_y + kSuper - 1) / kSuper);
+    return ((n_super + kXcds - 1) / kXcds) * kXcds * kSuper * kSuper;
+}
+
+__device__ __forceinline__ int tile_of_block(int bid, int tiles_x, int tiles_y) {
+    const int xcd = bid % kXcds, k = bid / kXcds;
+    const int per = kSuper * kSuper;
+    const int sup = (k / per) * kXcds + xcd;
+    const int sx = (tiles_x + kSuper - 1) / kSuper, sy = (tiles_y + kSuper - 1) / kSuper;
+    if (sup >= sx * sy) return -1;
+    const int local = k % per;
+    const int tx = (sup % sx) * kSuper + local % kSuper;
+    const int ty = (sup / sx) * kSuper + local / kSuper;
+    return tx < tiles_x && ty < tiles_y ? ty * tiles_x + tx : -1;
+}
+
 // The exponent of the splat at offset (dx, dy). Written with explicit fmas so
 // the forward and the backward round identically: the backward divides the
 // forward's (1 - alpha) back out and must see the same alpha bit for bit.
@@ -208,12 +233,86 @@ __device__ __forceinline__ void publish_rect(S_ &S, bool inimg, float fx, float 
     }
 }
 
+// ------------------------------------------------- chunked backward plan
+// The backward walks a tile's list back to front, so a tile is one long
+// dependent chain and the longest list bounds the whole kernel. With a chunk
+// workspace the forward records, every kChunk list entries, each pixel's
+// transmittance and accumulated colour (a checkpoint at the chunk's end), and
+// the backward runs one workgroup per (tile, chunk): it starts from the
+// chunk's end checkpoint, takes the colour behind it as final minus prefix,
+// and walks only its kChunk entries. Each entry still belongs to exactly one
+// workgroup, so the gradient atomics are unchanged.
+constexpr int kChunk = 2 * kBatch;   // entries per backward unit
+
+struct ChunkPlan {
+    int32_t *base;        // n_tiles + 1: first unit of each tile; base[n_tiles] = units
+    int32_t *unit_tile;   // unit -> tile
+    float4 *ckpt;         // unit * tile^2 + pixel: (T, r, g, b) at the chunk's end
+    int32_t cap;          // units the workspace holds
+};
+
+inline int64_t chunk_units_cap(int64_t n_isect, int n_tiles) {
+    return (n_isect + kChunk - 1) / kChunk + n_tiles;
+}
+
+inline int64_t chunk_ws_bytes(int64_t n_isect, int n_tiles, int tile) {
+    const int64_t cap = chunk_units_cap(n_isect, n_tiles);
+    return align256(4 * ((int64_t)n_tiles + 1)) + align256(4 * cap) +
+           cap * (int64_t)tile * tile * (int64_t)sizeof(float4);
+}
+
+inline ChunkPlan chunk_plan_of(void *ws, int64_t n_isect, int n_tiles) {
+    char *p = static_cast<char *>(ws);
+    const int64_t cap = chunk_units_cap(n_isect, n_tiles);
+    ChunkPlan P;
+    P.base = (int32_t *)p;
+    P.unit_tile = (int32_t *)(p + align256(4 * ((int64_t)n_tiles + 1)));
+    P.ckpt = (float4 *)(p + align256(4 * ((int64_t)n_tiles + 1)) + align256(4 * cap));
+    P.cap = (int32_t)cap;
+    return P;
+}
+
+// One workgroup: units per tile ceil(len / kChunk), their exclusive scan into
+// base, and unit_tile.
+__global__ __launch_bounds__(1024) void chunk_plan_kernel(const int32_t *offsets, int n_tiles,
+                                                          ChunkPlan P) {
+    __shared__ int32_t s_w[16];
+    __shared__ int32_t s_carry;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (threadIdx.x == 0) s_carry = 0;
+    __syncthreads();
+    for (int t0 = 0; t0 < n_tiles; t0 += 1024) {
+        const int t = t0 + (int)threadIdx.x;
+        const int len = t < n_tiles ? offsets[t + 1] - offsets[t] : 0;
+        const int nck = (len + kChunk - 1) / kChunk;
+        int incl = nck;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += v;
+        }
+        if (lane == 63) s_w[wave] = incl;
+        __syncthreads();
+        int before = s_carry;
+        for (int w = 0; w < wave; ++w) before += s_w[w];
+        const int b = before + incl - nck;
+        if (t < n_tiles) {
+            P.base[t] = b;
+            for (int k = 0; k < nck; ++k) P.unit_tile[b + k] = t;
+        }
+        __syncthreads();
+        if (threadIdx.x == 1023) s_carry = b + nck;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) P.base[n_tiles] = s_carry;
+}
+
 template <int MAXW>
 __global__ __launch_bounds__(MAXW * 64) void raster_fwd_kernel(const RasterArgs A, float *out_rgb,
                                                                float *out_alpha, float *out_T,
-                                                               int32_t *out_stop) {
+                                                               int32_t *out_stop,
+                                                               const ChunkPlan P) {
     __shared__ Stage<MAXW> S;
-    const int tile_id = xcd_band(blockIdx.x, A.n_tiles);
+    const int tile_id = tile_of_block(blockIdx.x, A.tiles_x, A.n_tiles / A.tiles_x);
     if (tile_id < 0) return;   // whole workgroup
     const int tx = tile_id % A.tiles_x, ty = tile_id / A.tiles_x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -230,6 +329,11 @@ __global__ __launch_bounds__(MAXW * 64) void raster_fwd_kernel(const RasterArgs 
     float T = 1.0f, cr = 0.f, cg = 0.f, cb = 0.f, acc = 0.f;
     int stop = start;
     bool done = !inimg;
+    // Checkpoints: pixel slot inside the tile, next unit to record.
+    const int tile2 = A.tile * A.tile;
+    const int pslot = ly * A.tile + lx;
+    int unit = P.ckpt ? P.base[tile_id] : 0;
+    const int unit_end = P.ckpt ? unit + (end - start + kChunk - 1) / kChunk : 0;
 
     for (int base = start; base < end; base += kBatch) {
         __syncthreads();
@@ -268,7 +372,15 @@ __global__ __launch_bounds__(MAXW * 64) void raster_fwd_kernel(const RasterArgs 
         }
         const bool wave_done = ballot(!done) == 0;
         if (lane == 0) S.flag[wave] = wave_done ? 1 : 0;
+        const int bend = min(base + kBatch, end);
+        if (unit < unit_end && ((bend - start) % kChunk == 0 || bend == end)) {
+            if (inimg) P.ckpt[(int64_t)unit * tile2 + pslot] = make_float4(T, cr, cg, cb);
+            ++unit;
+        }
     }
+    // A tile that turned opaque early: its later chunks end in the final state.
+    for (; unit < unit_end; ++unit)
+        if (inimg) P.ckpt[(int64_t)unit * tile2 + pslot] = make_float4(T, cr, cg, cb);
     if (!inimg) return;
     const int64_t o = (int64_t)py * A.W + px;
     if (A.has_bg) {
@@ -297,10 +409,25 @@ struct RasterGrads {
 
 template <int MAXW>
 __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs A,
-                                                               const RasterGrads G) {
+                                                               const RasterGrads G,
+                                                               const ChunkPlan P) {
     __shared__ StageBwd<MAXW> S;
-    const int tile_id = xcd_band(blockIdx.x, A.n_tiles);
-    if (tile_id < 0) return;
+    // Without a plan a workgroup takes a whole tile; with one, one chunk.
+    int tile_id, chunk = 0;
+    if (P.ckpt) {
+        // Range checks keep a workspace that did not come from the forward
+        // from indexing outside it (the whole workgroup returns).
+        const int u = (int)blockIdx.x;
+        if (u >= min(P.base[A.n_tiles], P.cap)) return;
+        tile_id = P.unit_tile[u];
+        if (tile_id < 0 || tile_id >= A.n_tiles) return;
+        chunk = u - P.base[tile_id];
+        const int nck = (A.offsets[tile_id + 1] - A.offsets[tile_id] + kChunk - 1) / kChunk;
+        if (chunk < 0 || chunk >= nck || P.base[tile_id] + nck > P.cap) return;
+    } else {
+        tile_id = tile_of_block(blockIdx.x, A.tiles_x, A.n_tiles / A.tiles_x);
+        if (tile_id < 0) return;
+    }
     const int tx = tile_id % A.tiles_x, ty = tile_id / A.tiles_x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nwaves = blockDim.x >> 6;
@@ -312,10 +439,26 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
     const float fx = (float)px + 0.5f, fy = (float)py + 0.5f;
     publish_rect(S, inimg, fx, fy, wave, lane);
 
-    const int start = A.offsets[tile_id];
+    const int tile_start = A.offsets[tile_id], tile_end = A.offsets[tile_id + 1];
+    const int start = tile_start + chunk * kChunk;   // this workgroup's entries
+    const int cend = P.ckpt ? min(start + kChunk, tile_end) : tile_end;
     const int64_t o = inimg ? (int64_t)py * A.W + px : 0;
     float T = inimg ? G.final_T[o] : 1.0f;
-    const int my_stop = inimg ? G.stop[o] : start;
+    // Colour and coverage composited behind this chunk (the suffix sums).
+    float sr = 0.f, sg = 0.f, sb = 0.f, sa = 0.f;
+    if (P.ckpt && inimg) {
+        const int tile2 = A.tile * A.tile, pslot = ly * A.tile + lx;
+        const int u0 = P.base[tile_id];
+        const int nck = (tile_end - tile_start + kChunk - 1) / kChunk;
+        const float4 e = P.ckpt[(int64_t)(u0 + chunk) * tile2 + pslot];
+        const float4 f = P.ckpt[(int64_t)(u0 + nck - 1) * tile2 + pslot];
+        T = e.x;
+        sr = f.y - e.y;
+        sg = f.z - e.z;
+        sb = f.w - e.w;
+        sa = e.x - f.x;      // sum of the weights behind = T_end - T_final
+    }
+    const int my_stop = inimg ? min(G.stop[o], cend) : start;
     const float gr = inimg ? G.grad_rgb[3 * o] : 0.f;
     const float gg = inimg ? G.grad_rgb[3 * o + 1] : 0.f;
     const float gb = inimg ? G.grad_rgb[3 * o + 2] : 0.f;
@@ -333,7 +476,6 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
     int bstop = start;
     for (int w = 0; w < nwaves; ++w) bstop = max(bstop, S.flag[w]);
 
-    float sr = 0.f, sg = 0.f, sb = 0.f, sa = 0.f;
     const int nbatch = (bstop - start + kBatch - 1) / kBatch;
     for (int bi = nbatch - 1; bi >= 0; --bi) {
         const int base = start + bi * kBatch;
@@ -357,35 +499,37 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
             const float alpha = fminf(kAlphaMax, alpha_raw);
             const bool active = inimg && i < my_stop && power <= 0.0f && alpha >= kAlphaMin;
             if (ballot(active) == 0) continue;
+            // Branchless: inactive lanes compute on finite values and select
+            // zeros (never multiply by 0, which would keep an inf as NaN).
+            // T before this entry is recovered as T / (1 - alpha) with a
+            // 1-ulp reciprocal; the forward's rounding of T (1 - alpha)
+            // already makes the recovery approximate.
+            const float4 col = S.col[j];
+            const float om = fmaxf(1.0f - alpha, 1e-8f);
+            const float iom = __builtin_amdgcn_rcpf(om);
+            const float Tn = T * iom;
+            const float w = active ? alpha * Tn : 0.0f;
+            const float dal = gr * (Tn * col.x - sr * iom) + gg * (Tn * col.y - sg * iom) +
+                              gb * (Tn * col.z - sb * iom) + ga * (Tn - sa * iom);
+            T = active ? Tn : T;
+            sr = fmaf(w, col.x, sr);
+            sg = fmaf(w, col.y, sg);
+            sb = fmaf(w, col.z, sb);
+            sa += w;
+            // Past the 0.999 clamp alpha no longer depends on the splat.
+            const float dg = active && alpha_raw <= kAlphaMax ? dal * gauss : 0.0f;
+            const float dpow = dg * op;
             float v[kGradSlots];
-#pragma unroll
-            for (int q = 0; q < kGradSlots; ++q) v[q] = 0.f;
-            if (active) {
-                const float4 col = S.col[j];
-                const float om = fmaxf(1.0f - alpha, 1e-8f);
-                T = T / om;
-                const float iom = 1.0f / om;
-                const float w = alpha * T;
-                v[0] = w * gr;
-                v[1] = w * gg;
-                v[2] = w * gb;
-                const float dal = gr * (T * col.x - sr * iom) + gg * (T * col.y - sg * iom) +
-                                  gb * (T * col.z - sb * iom) + ga * (T - sa * iom);
-                sr = fmaf(w, col.x, sr);
-                sg = fmaf(w, col.y, sg);
-                sb = fmaf(w, col.z, sb);
-                sa += w;
-                if (alpha_raw <= kAlphaMax) {
-                    v[8] = dal * gauss;
-                    const float dpow = dal * op * gauss;
-                    v[3] = dpow * (con.x * dx + con.y * dy);
-                    v[4] = dpow * (con.y * dx + con.z * dy);
-                    v[5] = -0.5f * dpow * dx * dx;
-                    v[6] = -dpow * dx * dy;
-                    v[7] = -0.5f * dpow * dy * dy;
-                    if (want_abs) v[9] = sqrtf(v[3] * v[3] + v[4] * v[4]);
-                }
-            }
+            v[0] = w * gr;
+            v[1] = w * gg;
+            v[2] = w * gb;
+            v[3] = dpow * (con.x * dx + con.y * dy);
+            v[4] = dpow * (con.y * dx + con.z * dy);
+            v[5] = -0.5f * dpow * dx * dx;
+            v[6] = -dpow * dx * dy;
+            v[7] = -0.5f * dpow * dy * dy;
+            v[8] = dg;
+            v[9] = want_abs ? __builtin_amdgcn_sqrtf(v[3] * v[3] + v[4] * v[4]) : 0.0f;
             // Sums over the wave of v[0..9], deposited into S.grad[.][j]
             // with four lanes per LDS atomic (see reduce10_to_rows).
             float q0, q1, q2;
@@ -461,10 +605,16 @@ using namespace mg;
 
 extern "C" {
 
+int64_t mg_rasterize_chunk_workspace_bytes(int64_t n_isect, int32_t n_tiles, int32_t tile) {
+    if (n_isect < 0 || n_tiles < 1 || tile < 1) return 0;
+    return chunk_ws_bytes(n_isect, n_tiles, tile);
+}
+
 int32_t mg_rasterize_forward(int64_t N, const float *uv, const float *conic, const float *opacity,
                              const float *color, const int32_t *gauss_ids,
                              const int32_t *tile_offsets, int32_t W, int32_t H, int32_t tile,
                              int32_t tiles_x, float t_min, const float *background,
+                             int64_t n_isect, void *chunk_ws, int64_t chunk_ws_size,
                              float *out_rgb, float *out_alpha, float *out_T, int32_t *out_stop,
                              mg_stream_t stream) {
     int32_t rc = check_raster("rasterize_forward", N, uv, conic, opacity, color, gauss_ids,
@@ -476,15 +626,25 @@ int32_t mg_rasterize_forward(int64_t N, const float *uv, const float *conic, con
                  tiles_x * tiles_y, t_min, background != nullptr,
                  {background ? background[0] : 0.f, background ? background[1] : 0.f,
                   background ? background[2] : 0.f}};
+    hipStream_t s = as_stream(stream);
+    ChunkPlan P{nullptr, nullptr, nullptr, 0};
+    if (chunk_ws) {
+        MG_REQUIRE(n_isect >= 0 && chunk_ws_size >= chunk_ws_bytes(n_isect, A.n_tiles, tile),
+                   "rasterize_forward: chunk workspace %lld bytes, need %lld for %lld "
+                   "intersections", (long long)chunk_ws_size,
+                   (long long)chunk_ws_bytes(n_isect, A.n_tiles, tile), (long long)n_isect);
+        P = chunk_plan_of(chunk_ws, n_isect, A.n_tiles);
+        chunk_plan_kernel<<<1, 1024, 0, s>>>(tile_offsets, A.n_tiles, P);
+        MG_LAUNCHED("chunk_plan_kernel");
+    }
     const int threads = ((tile * tile + 63) / 64) * 64;
-    const int grid = (int)ceil_div(A.n_tiles, kXcds) * kXcds;
-    TimedScope ts("rasterize_forward", as_stream(stream));
+    const int grid = raster_grid(tiles_x, tiles_y);
+    TimedScope ts("rasterize_forward", s);
     if (threads <= 4 * 64)
-        raster_fwd_kernel<4><<<grid, threads, 0, as_stream(stream)>>>(A, out_rgb, out_alpha,
-                                                                       out_T, out_stop);
+        raster_fwd_kernel<4><<<grid, threads, 0, s>>>(A, out_rgb, out_alpha, out_T, out_stop, P);
     else
-        raster_fwd_kernel<kMaxWaves><<<grid, threads, 0, as_stream(stream)>>>(
-            A, out_rgb, out_alpha, out_T, out_stop);
+        raster_fwd_kernel<kMaxWaves><<<grid, threads, 0, s>>>(A, out_rgb, out_alpha, out_T,
+                                                              out_stop, P);
     MG_LAUNCHED("raster_fwd_kernel");
     return MG_OK;
 }
@@ -494,7 +654,8 @@ int32_t mg_rasterize_backward(int64_t N, const float *uv, const float *conic,
                               const int32_t *gauss_ids, const int32_t *tile_offsets,
                               const float *final_T, const int32_t *stop, const float *grad_rgb,
                               const float *grad_alpha, const float *alpha,
-                              const float *background, int32_t W, int32_t H, int32_t tile,
+                              const float *background, int64_t n_isect, const void *chunk_ws,
+                              int64_t chunk_ws_size, int32_t W, int32_t H, int32_t tile,
                               int32_t tiles_x, float *d_uv, float *d_conic, float *d_opacity,
                               float *d_color, float *d_absuv, mg_stream_t stream) {
     int32_t rc = check_raster("rasterize_backward", N, uv, conic, opacity, color, gauss_ids,
@@ -519,14 +680,26 @@ int32_t mg_rasterize_backward(int64_t N, const float *uv, const float *conic,
                   background ? background[2] : 0.f}};
     RasterGrads Gr{final_T, stop, grad_rgb, grad_alpha, alpha, d_uv, d_conic, d_opacity, d_color,
                    d_absuv};
+    ChunkPlan P{nullptr, nullptr, nullptr, 0};
+    int grid = raster_grid(tiles_x, tiles_y);
+    if (chunk_ws) {
+        // The plan and checkpoints the forward wrote into this workspace.
+        MG_REQUIRE(n_isect >= 0 && chunk_ws_size >= chunk_ws_bytes(n_isect, A.n_tiles, tile),
+                   "rasterize_backward: chunk workspace %lld bytes, need %lld for %lld "
+                   "intersections", (long long)chunk_ws_size,
+                   (long long)chunk_ws_bytes(n_isect, A.n_tiles, tile), (long long)n_isect);
+        P = chunk_plan_of(const_cast<void *>(chunk_ws), n_isect, A.n_tiles);
+        grid = P.cap;
+    }
     const int threads = ((tile * tile + 63) / 64) * 64;
-    const int grid = (int)ceil_div(A.n_tiles, kXcds) * kXcds;
     TimedScope ts("rasterize_backward", s);
-    if (threads <= 4 * 64)
-        raster_bwd_kernel<4><<<grid, threads, 0, s>>>(A, Gr);
-    else
-        raster_bwd_kernel<kMaxWaves><<<grid, threads, 0, s>>>(A, Gr);
-    MG_LAUNCHED("raster_bwd_kernel");
+    if (grid > 0) {
+        if (threads <= 4 * 64)
+            raster_bwd_kernel<4><<<grid, threads, 0, s>>>(A, Gr, P);
+        else
+            raster_bwd_kernel<kMaxWaves><<<grid, threads, 0, s>>>(A, Gr, P);
+        MG_LAUNCHED("raster_bwd_kernel");
+    }
     return MG_OK;
 }
 

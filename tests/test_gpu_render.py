@@ -249,3 +249,27 @@ def test_no_discontinuity_across_boundaries(dev, lo, hi):
         es.append(float(rgb.sum()))
     steps = np.abs(np.diff(es))
     assert steps.max() <= 8 * max(np.median(steps), 1e-9)
+
+
+def test_chunked_backward_matches_single_chain(dev):
+    """render(chunked_backward=True) runs the raster backward as 512-entry
+    units per tile from forward checkpoints; same image, same gradients up to
+    rounding (both recover T by division, from different starting points)."""
+    from metal_gauss_amd import render
+
+    s = scene(n=5000, seed=12, sh=True)
+    W, H = 64, 48
+    grads = []
+    for chunked in (False, True):
+        leaves = {k: s[k].clone().to(dev).requires_grad_(True)
+                  for k in ("means", "quats", "scales", "opacities", "sh")}
+        rgb, alpha, info = render(leaves["means"], leaves["quats"], leaves["scales"],
+                                  leaves["opacities"], leaves["sh"], intrinsics(W, H),
+                                  torch.eye(4), W, H, sh_degree=3, background=(1.0, 1.0, 1.0),
+                                  chunked_backward=chunked)
+        (rgb.square().mean() + 0.1 * alpha.square().mean()).backward()
+        grads.append((rgb.detach(), {k: v.grad.detach().clone() for k, v in leaves.items()}))
+    assert torch.equal(grads[0][0], grads[1][0])
+    for k in grads[0][1]:
+        e = rel_l2(grads[1][1][k].cpu(), grads[0][1][k].cpu())
+        assert e < 1e-4, (k, e)
