@@ -215,20 +215,51 @@ __device__ __forceinline__ void pick4(const float B[16], int q, float b[4]) {
 
 struct ShRows {
     const float *sh, *rest;   // fused (N,16,3) in sh, or DC (N,1,3) + rest (N,15,3)
-    int fused, vec4;          // vec4: fused, 16-byte aligned and degree 3
+    int fused, vec4;          // vec4: degree 3 (and, when fused, 16-byte aligned)
 };
+
+// 16- and 12-byte accesses that need only 4-byte alignment (gfx9 global
+// memory accepts dword-aligned multi-dword accesses): the split layout's
+// 180-byte rest rows start on any dword.
+typedef float v4u __attribute__((ext_vector_type(4), aligned(4)));
+typedef float v3u __attribute__((ext_vector_type(3), aligned(4)));
 
 // Loads coefficients c[k][ch] of bases 4q+k (k < 4) of Gaussian G; bases at
 // or past nb read as 0.
 __device__ __forceinline__ void load_bases(const ShRows &R, int64_t G, int q, int nb,
                                            float c[4][3]) {
-    if (R.vec4) {
+    if (R.vec4 && R.fused) {
         const float4 *src = reinterpret_cast<const float4 *>(R.sh + G * 48 + 12 * q);
         const float4 a = src[0], b = src[1], d = src[2];
         c[0][0] = a.x; c[0][1] = a.y; c[0][2] = a.z;
         c[1][0] = a.w; c[1][1] = b.x; c[1][2] = b.y;
         c[2][0] = b.z; c[2][1] = b.w; c[2][2] = d.x;
         c[3][0] = d.y; c[3][1] = d.z; c[3][2] = d.w;
+        return;
+    }
+    if (R.vec4) {   // split layout, degree 3: the quad reads the 180-byte rest row
+        float f[12];
+        if (q == 0) {
+            const v3u d = *reinterpret_cast<const v3u *>(R.sh + G * 3);
+            const float *r = R.rest + G * 45;
+            const v4u a = *reinterpret_cast<const v4u *>(r);
+            const v4u b = *reinterpret_cast<const v4u *>(r + 4);
+            f[0] = d.x; f[1] = d.y; f[2] = d.z;
+            f[3] = a.x; f[4] = a.y; f[5] = a.z; f[6] = a.w;
+            f[7] = b.x; f[8] = b.y; f[9] = b.z; f[10] = b.w; f[11] = r[8];
+        } else {
+            const float *r = R.rest + G * 45 + 12 * q - 3;
+            const v4u a = *reinterpret_cast<const v4u *>(r);
+            const v4u b = *reinterpret_cast<const v4u *>(r + 4);
+            const v4u d = *reinterpret_cast<const v4u *>(r + 8);
+            f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+            f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+            f[8] = d.x; f[9] = d.y; f[10] = d.z; f[11] = d.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int ch = 0; ch < 3; ++ch) c[k][ch] = f[3 * k + ch];
         return;
     }
 #pragma unroll
@@ -250,11 +281,31 @@ __device__ __forceinline__ void load_bases(const ShRows &R, int64_t G, int q, in
 // are written; the caller passes zeros past the degree).
 __device__ __forceinline__ void store_bases(float *dsh, float *drest, int fused, int vec4,
                                             int64_t G, int q, const float d[4][3]) {
-    if (vec4) {
+    if (vec4 && fused) {
         float4 *dst = reinterpret_cast<float4 *>(dsh + G * 48 + 12 * q);
         dst[0] = make_float4(d[0][0], d[0][1], d[0][2], d[1][0]);
         dst[1] = make_float4(d[1][1], d[1][2], d[2][0], d[2][1]);
         dst[2] = make_float4(d[2][2], d[3][0], d[3][1], d[3][2]);
+        return;
+    }
+    if (vec4) {     // split layout (the fused case returned above)
+        float f[12];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int ch = 0; ch < 3; ++ch) f[3 * k + ch] = d[k][ch];
+        if (q == 0) {
+            *reinterpret_cast<v3u *>(dsh + G * 3) = v3u{f[0], f[1], f[2]};
+            float *r = drest + G * 45;
+            *reinterpret_cast<v4u *>(r) = v4u{f[3], f[4], f[5], f[6]};
+            *reinterpret_cast<v4u *>(r + 4) = v4u{f[7], f[8], f[9], f[10]};
+            r[8] = f[11];
+        } else {
+            float *r = drest + G * 45 + 12 * q - 3;
+            *reinterpret_cast<v4u *>(r) = v4u{f[0], f[1], f[2], f[3]};
+            *reinterpret_cast<v4u *>(r + 4) = v4u{f[4], f[5], f[6], f[7]};
+            *reinterpret_cast<v4u *>(r + 8) = v4u{f[8], f[9], f[10], f[11]};
+        }
         return;
     }
 #pragma unroll
@@ -639,7 +690,7 @@ int32_t mg_preprocess_forward(int64_t N, const float *means, const float *quats,
     A.means = means; A.quats = quats; A.scales = scales; A.sh = sh;
     A.rest = sh_rest; A.opac = opacities; A.fused = sh_fused;
     A.uv = uv; A.conic = conic; A.depth = depth; A.rxy = rxy; A.valid = valid; A.color = color;
-    A.vec4 = sh && sh_fused && sh_degree == 3 && ((uintptr_t)sh & 15) == 0;
+    A.vec4 = sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)sh & 15) == 0);
     const int64_t blocks = ceil_div(N, kPreThreads);
     TimedScope ts("preprocess_forward", as_stream(stream));
     preprocess_fwd_kernel<<<(unsigned)blocks, kPreThreads, 0, as_stream(stream)>>>(A);
@@ -673,8 +724,8 @@ int32_t mg_preprocess_backward(int64_t N, const float *means, const float *quats
     A.fused = sh_fused; A.d_uv = d_uv; A.d_conic = d_conic; A.d_color = d_color; A.valid = valid;
     A.d_means = d_means; A.d_quats = d_quats; A.d_scales = d_scales; A.d_sh = d_sh;
     A.d_rest = d_sh_rest;
-    A.vec4 = sh && sh_fused && sh_degree == 3 && ((uintptr_t)sh & 15) == 0;
-    A.st_vec4 = d_sh && sh_fused && sh_degree == 3 && ((uintptr_t)d_sh & 15) == 0;
+    A.vec4 = sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)sh & 15) == 0);
+    A.st_vec4 = d_sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)d_sh & 15) == 0);
     const int64_t blocks = ceil_div(N, kPreThreads);
     TimedScope ts("preprocess_backward", as_stream(stream));
     preprocess_bwd_kernel<<<(unsigned)blocks, kPreThreads, 0, as_stream(stream)>>>(A);
