@@ -486,11 +486,19 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
             (&S.grad[0][0])[t] = 0.f;
         __syncthreads();
         const int cnt = compact_live(S, n, wstop - base, wave, lane);
+        // The next entry's LDS reads are issued before this entry's math.
+        int jn = cnt > 0 ? S.list[wave][cnt - 1] : 0;
+        float4 geo_n = S.geo[jn], con_n = S.con[jn], col_n = S.col[jn];
         for (int k = cnt - 1; k >= 0; --k) {
-            const int j = S.list[wave][k];
+            const int j = jn;
+            const float4 geo = geo_n, con = con_n, col = col_n;
+            if (k > 0) {
+                jn = S.list[wave][k - 1];
+                geo_n = S.geo[jn];
+                con_n = S.con[jn];
+                col_n = S.col[jn];
+            }
             const int i = base + j;
-            const float4 geo = S.geo[j];
-            const float4 con = S.con[j];
             const float dx = fx - geo.x, dy = fy - geo.y;
             const float power = splat_power(dx, dy, con.x, con.y, con.z);
             const float gauss = __expf(power);
@@ -504,7 +512,6 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
             // T before this entry is recovered as T / (1 - alpha) with a
             // 1-ulp reciprocal; the forward's rounding of T (1 - alpha)
             // already makes the recovery approximate.
-            const float4 col = S.col[j];
             const float om = fmaxf(1.0f - alpha, 1e-8f);
             const float iom = __builtin_amdgcn_rcpf(om);
             const float Tn = T * iom;
