@@ -60,6 +60,12 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--gaussians", type=int, default=1_000_000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--variant", default="base", choices=["base", "mip", "mip-torch"],
+                    help="base: the config-4 step; mip: with Mip-Splatting's 3D filter and "
+                         "the 2D antialias compensation folded into the projection kernel "
+                         "(render(filter_3d=, antialias=True)); mip-torch: the same step with "
+                         "the 3D filter applied as the reference's torch reparameterisation "
+                         "(apply_3d_filter, train.py:223-227) before render")
     ap.add_argument("--cpu-only", action="store_true", help="time only the CPU baseline")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the HBM traffic summary of two rocprofv3 --pmc runs and exit")
@@ -87,7 +93,7 @@ def copy_calibration(mib):
 class Step:
     """The config-4 training step on the GPU."""
 
-    def __init__(self, n, dev):
+    def __init__(self, n, dev, variant="base"):
         import torch
 
         from metal_gauss_amd import FusedAdam, gaussian_kernel, scenes
@@ -112,6 +118,30 @@ class Step:
         self.order = torch.randperm(len(cams), generator=g).tolist()
         self.k = 0
         self.last_isect = 0
+        self.variant = variant
+        self.f3d = None
+        self.f3d_ms = None
+        if variant != "base":
+            self.f3d_ms = self.refresh_filter()
+
+    def refresh_filter(self):
+        """Mip 3D filter sizes over all views (compute_3d_filter), as the
+        reference's trainer recomputes them every 100 steps; returns ms."""
+        import torch
+
+        from metal_gauss_amd import compute_3d_filter
+
+        class _V:
+            def __init__(self, c):
+                self.K, self.viewmat = c.K, c.viewmat
+                self.image = torch.empty(c.H, c.W, 0)
+
+        views = [_V(c) for c in self.cams]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        self.f3d = compute_3d_filter(self.p["means"], views)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3
 
     def __call__(self, adam=True):
         import torch
@@ -121,10 +151,17 @@ class Step:
         v = self.order[self.k % len(self.order)]
         self.k += 1
         cam, gt, p = self.cams[v], self.targets[v], self.p
-        rgb, alpha, info = render(p["means"], p["quats"], torch.exp(p["log_scales"]),
-                                  torch.sigmoid(p["logit_opac"]), p["sh_dc"], cam.K, cam.viewmat,
-                                  cam.W, cam.H, sh_degree=3, sh_rest=p["sh_rest"],
-                                  background=self.bg)
+        scales, opac = torch.exp(p["log_scales"]), torch.sigmoid(p["logit_opac"])
+        kw = {}
+        if self.variant == "mip":
+            kw = dict(filter_3d=self.f3d, antialias=True)
+        elif self.variant == "mip-torch":
+            from metal_gauss_amd import apply_3d_filter
+            scales, opac = apply_3d_filter(scales, opac, self.f3d)
+            kw = dict(antialias=True)
+        rgb, alpha, info = render(p["means"], p["quats"], scales, opac, p["sh_dc"], cam.K,
+                                  cam.viewmat, cam.W, cam.H, sh_degree=3, sh_rest=p["sh_rest"],
+                                  background=self.bg, **kw)
         # 0.8 * |rgb - gt|.mean() + 0.2 * (1 - ssim(rgb, gt)) (train.py:389-390), fused.
         loss, _ = photometric_loss(rgb, gt, self.window, 0.2)
         self.opt.zero_grad(set_to_none=True)
@@ -161,7 +198,7 @@ def gpu_bench(args):
     from metal_gauss_amd import _lib
 
     dev = torch.device("cuda:0")
-    step = Step(args.gaussians, dev)
+    step = Step(args.gaussians, dev, args.variant)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -206,8 +243,14 @@ def gpu_bench(args):
     rows = {k: {"ms": round(v[0], 4), "per_step": v[1],
                 "GBps": round(algorithmic_bytes(k, N, I, P, T, f_valid, n_floats)
                               / (v[0] * 1e-3) / 1e9, 1)} for k, v in kern.items()}
+    f3d_ms = None
+    if args.variant != "base":
+        with _lib.KernelTimer():
+            wall = step.refresh_filter()
+            tot, cnt = _lib.KernelTimer.query("compute_3d_filter")
+        f3d_ms = (tot / max(cnt, 1), wall)
     return dict(ms=ms, fb_ms=fb_ms, kernels=rows, dominant=dominant, achieved=achieved,
-                nbytes=nbytes, I=I, f_valid=f_valid, n_floats=n_floats)
+                nbytes=nbytes, I=I, f_valid=f_valid, n_floats=n_floats, f3d_ms=f3d_ms)
 
 
 PMC_REGEX = ("raster_bwd|raster_fwd|adam_multi|preprocess_fwd|preprocess_bwd|radix_|scan_|"
@@ -270,19 +313,23 @@ def pmc_summary(fetch_dir, write_dir, copy_mib):
     return "\n".join(lines)
 
 
-def stats_summary(stats_csv, steps):
+def stats_summary(stats_csv, steps, variant="base"):
     """Text summary of a rocprofv3 --kernel-trace --stats kernel_stats.csv."""
     import csv
 
     with open(stats_csv, newline="") as f:
         rows = list(csv.DictReader(f))
     total = sum(float(r["TotalDurationNs"]) for r in rows)
+    vflag = "" if variant == "base" else f" --variant {variant}"
+    what = {"base": "", "mip": ", Mip 3D filter + 2D antialias in the projection kernel",
+            "mip-torch": ", Mip 3D filter as torch reparameterisation"}[variant]
     lines = [
-        "# rocprofv3 kernel statistics, config-4 step (1M Gaussians SH3, 800x800, tile 16), MI355X",
+        "# rocprofv3 kernel statistics, config-4 step (1M Gaussians SH3, 800x800, tile 16"
+        f"{what}), MI355X",
         "# made by (from the repository root, TMPDIR=/tmp):",
         "#   rocprofv3 --kernel-trace --stats -f csv -T -d P -o kt -- python -u bench.py "
-        f"--steps {steps} --warmup 5 --no-cpu-baseline",
-        "#   python bench.py --stats-summary P/kt_kernel_stats.csv",
+        f"--steps {steps} --warmup 5 --no-cpu-baseline{vflag}",
+        f"#   python bench.py --stats-summary P/kt_kernel_stats.csv{vflag}",
         "# The run covers warmup + timed steps + the fwd+bwd-only loop + 10 per-kernel timing "
         "steps.",
         f"{'kernel':36s} {'calls':>7s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'share_%':>8s}",
@@ -306,14 +353,19 @@ def committed_traffic(label):
     return None
 
 
-def cpu_baseline(n_gaussians=1_000_000, crop=96):
-    """The CPU oracle on a bounded sample of the config-4 step, scaled.
+def cpu_baseline(n_gaussians=1_000_000, crop=800):
+    """The CPU oracle on one config-4 step.
 
-    Sample: the full config-4 scene (all N Gaussians projected, SH evaluated,
-    and differentiated), rasterised forward+backward over a crop x crop window
-    at the image centre, loss on the crop, and torch.optim.Adam over all 59N
-    parameters. Full-step time = projection + Adam + (raster + loss on the
-    crop) x (800^2 / crop^2); reported as steps/s.
+    The full config-4 scene (all N Gaussians projected, SH evaluated, and
+    differentiated), rasterised forward+backward over a crop x crop window at
+    the image centre (by default the whole 800x800 view, so nothing is
+    extrapolated), the loss on it, and torch.optim.Adam over all 59N
+    parameters; reported as steps/s. With a smaller crop, whose centre is
+    denser than the frame, the crop's time is scaled by the ratio of the
+    oracle's own intersection counts (3-sigma boxes at tile 16,
+    render_ref.tile_lists) over the full view and over the crop. The
+    projection is run once untimed first (allocator and thread-pool warm-up).
+    The whole view needs about 40 GB of host memory.
     """
     import torch
 
@@ -350,8 +402,20 @@ def cpu_baseline(n_gaussians=1_000_000, crop=96):
         col = (R.eval_sh(3, sh, d) + 0.5).clamp_min(0.0)
         return uv, conic, op, col, depth, radius, valid
 
+    def isect_count(Kc, w, h):
+        with torch.no_grad():
+            cov = R.build_cov3d(leaves["quats"], torch.exp(leaves["log_scales"]))
+            uvc, _, dc, rc, vc, _ = R.project(leaves["means"], cov, vm, float(Kc[0, 0]),
+                                              float(Kc[1, 1]), float(Kc[0, 2]), float(Kc[1, 2]),
+                                              w, h, 0.01, 100.0, max_radius_frac=W / w)
+            return R.tile_lists(uvc, rc, vc, dc, w, h, 16)[3]
+
     # Projection of all N (forward + backward through a dummy reduction of the
-    # same outputs the rasteriser consumes).
+    # same outputs the rasteriser consumes); once untimed, then timed.
+    for t in (project_part(),):
+        (t[0].sum() + t[1].sum() + t[3].sum() + t[2].sum()).backward()
+    for t in leaves.values():
+        t.grad = None
     t0 = time.perf_counter()
     uv, conic, op, col, depth, radius, valid = project_part()
     (uv.sum() + conic.sum() + col.sum() + op.sum()).backward()
@@ -373,7 +437,8 @@ def cpu_baseline(n_gaussians=1_000_000, crop=96):
     t0 = time.perf_counter()
     opt.step()
     t_adam = time.perf_counter() - t0
-    scale = (W * H) / (crop * crop)
+    i_full = isect_count(cam.K, W, H) if crop < W else info["isect_total"]
+    scale = i_full / max(1, info["isect_total"])
     t_step = t_proj + t_adam + t_crop * scale
     return {
         "value": round(1.0 / t_step, 6), "unit": "steps/s", "cores": torch.get_num_threads(),
@@ -381,9 +446,20 @@ def cpu_baseline(n_gaussians=1_000_000, crop=96):
         "sample": (f"config-4 step, CPU oracle (torch_ref restatement): projection+SH fwd+bwd of "
                    f"all {n_gaussians} Gaussians {t_proj:.2f}s + Adam over all params "
                    f"{t_adam:.2f}s + raster/loss fwd+bwd on a {crop}x{crop} centre crop "
-                   f"{t_crop:.2f}s x {scale:.1f} (pixel ratio); {info['isect_total']} crop "
-                   f"intersections; os.cpu_count()={cores}"),
+                   f"{t_crop:.2f}s x {scale:.2f} (oracle intersections, full view "
+                   f"{i_full} / crop {info['isect_total']}); os.cpu_count()={cores}"),
     }
+
+
+def _cpu_crop():
+    """The whole view when the host has room for the oracle's slab tensors
+    (about 40 GB), else a 384x384 centre crop scaled by intersections."""
+    try:
+        import psutil
+        avail = psutil.virtual_memory().available
+    except Exception:
+        avail = 0
+    return 800 if avail > 96 * (1 << 30) else 384
 
 
 def main():
@@ -396,10 +472,10 @@ def main():
         print(pmc_summary(*args.pmc_summary, args.copy_mib or 1024))
         return
     if args.stats_summary:
-        print(stats_summary(args.stats_summary, 20))
+        print(stats_summary(args.stats_summary, 20, args.variant))
         return
     if args.cpu_only:
-        print(json.dumps(cpu_baseline(args.gaussians)))
+        print(json.dumps(cpu_baseline(args.gaussians, crop=_cpu_crop())))
         return
     import torch
 
@@ -439,8 +515,18 @@ def main():
         },
         "kernels": r["kernels"],
     }
+    if args.variant != "base":
+        out["config"]["workload"] += {
+            "mip": "; Mip 3D filter + 2D antialias in the projection kernel",
+            "mip-torch": "; Mip 3D filter as torch reparameterisation, 2D antialias in kernel",
+        }[args.variant]
+        out["config"]["variant"] = args.variant
+        # Once per densify interval in the reference's trainer, not per step:
+        # the kernel alone, and with building the per-view table on the host.
+        out["compute_3d_filter_ms"] = {"kernel": round(r["f3d_ms"][0], 4),
+                                       "with_host_views": round(r["f3d_ms"][1], 3)}
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(args.gaussians)
+        out["cpu_baseline"] = cpu_baseline(args.gaussians, crop=_cpu_crop())
     print(json.dumps(out))
 
 

@@ -101,6 +101,59 @@ int32_t mg_preprocess_backward(
     float *d_means, float *d_quats, float *d_scales, float *d_sh,
     float *d_sh_rest, mg_stream_t stream);
 
+/* Mip-Splatting's filters folded into the projection: the same work as
+ * mg_preprocess_forward, plus
+ *   - filter_3d (N,) or NULL: the 3D low-pass of apply_3d_filter
+ *     (metal_gauss/mipfilter.py:76-93), scales' = sqrt(scales^2 + f^2) and
+ *     opacity * sqrt(prod scales^2 / prod scales'^2), which the reference's
+ *     trainer applies in torch before render (train.py:223-227);
+ *   - antialias != 0: the 2D compensation opacity * sqrt(det0 / det) of the
+ *     blurred covariance, which the reference recomputes from the conic in
+ *     torch (antialias_scale, metal_gauss/metal_backend.py:367-393, applied
+ *     at 506-511; torch_ref.py:100-124).
+ * opacity_eff (N,) receives the opacity binning and compositing use. rxy and
+ * valid see the opacity after the 3D filter and before the 2D one, as in the
+ * reference. */
+int32_t mg_preprocess_forward_mip(
+    int64_t N, const float *means, const float *quats, const float *scales,
+    const float *sh, const float *sh_rest, int32_t sh_fused,
+    const float *opacities, const float *viewmat, float fx, float fy,
+    float cx, float cy, int32_t W, int32_t H, float near_plane,
+    float far_plane, float blur, float max_radius, const float *cam_center,
+    int32_t sh_degree, const float *filter_3d, int32_t antialias, float *uv,
+    float *conic, float *depth, float *rxy, int32_t *valid, float *color,
+    float *opacity_eff, mg_stream_t stream);
+
+/* Analytic backward of mg_preprocess_forward_mip. d_opacity_eff is the
+ * gradient of opacity_eff; d_opacities (N,) receives the gradient of the
+ * unfiltered opacities, and the filters' share of the scale and covariance
+ * gradients is folded into d_scales, d_quats and d_means. The reference gets
+ * these from torch autograd of the same expressions. */
+int32_t mg_preprocess_backward_mip(
+    int64_t N, const float *means, const float *quats, const float *scales,
+    const float *sh, const float *sh_rest, int32_t sh_fused,
+    const float *d_uv, const float *d_conic, const float *d_color,
+    const int32_t *valid, const float *viewmat, float fx, float fy, float cx,
+    float cy, int32_t W, int32_t H, float near_plane, float far_plane,
+    float blur, float max_radius, const float *cam_center, int32_t sh_degree,
+    const float *opacities, const float *filter_3d, int32_t antialias,
+    const float *d_opacity_eff, float *d_means, float *d_quats,
+    float *d_scales, float *d_sh, float *d_sh_rest, float *d_opacities,
+    mg_stream_t stream);
+
+/* Per-Gaussian 3D filter size. Replaces compute_3d_filter
+ * (metal_gauss/mipfilter.py:29-73). views: (n_views, 20) device floats per
+ * view: world->camera R (9, row-major), t (3), fx, fy, cx, cy, and the
+ * frame's bounds with the margin, -margin*W, (1+margin)*W, -margin*H,
+ * (1+margin)*H. focal is the largest fx or fy over the views (<= 0 means 1).
+ * scratch: one device int32. filter_3d (N,) receives
+ * (min seen depth / focal) * sqrt(0.2); unseen Gaussians take the largest
+ * seen depth, and with none seen every depth is 1. */
+int32_t mg_compute_3d_filter(int64_t N, const float *means, int32_t n_views,
+                             const float *views, float focal,
+                             float near_plane, float *filter_3d,
+                             int32_t *scratch, mg_stream_t stream);
+
 /* ---------------------------------------------------------------- binning */
 
 /* Per-Gaussian count of tiles that pass the exact ellipse-vs-tile test

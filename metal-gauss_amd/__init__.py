@@ -8,12 +8,15 @@ Public surface (names of the reference's modules):
     FusedAdam              fused_adam.FusedAdam
     SelectiveAdam          selective_adam.SelectiveAdam
     ssim, gaussian_kernel  the fused SSIM loss used by the training step
+    compute_3d_filter,     mipfilter: Mip-Splatting's 3D filter (also folded
+    apply_3d_filter        into render's projection kernel via filter_3d=)
 """
 
 from .api import BACKENDS, render  # noqa: F401
 from .fused_adam import FusedAdam  # noqa: F401
 from .selective_adam import SelectiveAdam  # noqa: F401
 from .ssim import gaussian_kernel, photometric_loss, ssim  # noqa: F401
+from .mipfilter import apply_3d_filter, compute_3d_filter  # noqa: F401
 from . import backend  # noqa: F401
 
 __version__ = "0.1.0"

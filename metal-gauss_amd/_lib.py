@@ -43,6 +43,14 @@ _SIGNATURES = {
     "mg_preprocess_backward": (_i32, [
         _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _f32,
         _i32, _i32, _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "mg_preprocess_forward_mip": (_i32, [
+        _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _f32, _f32, _i32, _i32,
+        _f32, _f32, _f32, _f32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "mg_preprocess_backward_mip": (_i32, [
+        _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _f32,
+        _i32, _i32, _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
+        _vp, _vp, _vp]),
+    "mg_compute_3d_filter": (_i32, [_i64, _vp, _i32, _vp, _f32, _f32, _vp, _vp, _vp]),
     "mg_bin_count": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp,
                             _vp]),
     "mg_scan_workspace_bytes": (_i64, [_i64]),

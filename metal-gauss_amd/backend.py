@@ -18,8 +18,11 @@ to this module:
 What changes is underneath: every heavy step is a hand-written HIP kernel in
 libmgauss.so (include/mgauss.h) reached through ``_lib``. Torch is used only
 for allocation, the stream, autograd plumbing and the small elementwise glue
-the reference also leaves in torch (SH zero-padding, antialias compensation,
-background blend).
+the reference also leaves in torch (SH zero-padding, a background given as a
+device tensor). The antialias compensation and Mip-Splatting's 3D filter,
+which the reference computes in torch, run inside the projection kernel
+(``_PreprocessMip``); ``antialias_scale`` is kept for callers that use it
+directly.
 """
 
 from __future__ import annotations
@@ -414,6 +417,105 @@ class _RasterizeMetal(torch.autograd.Function):
         return (d_uv, d_conic, d_op, d_col) + (None,) * 10
 
 
+class _PreprocessMip(torch.autograd.Function):
+    """Preprocess with Mip-Splatting's filters folded into the kernel.
+
+    The reference applies the 3D filter as a torch reparameterisation of
+    scales and opacity before render (train.py:214-229, mipfilter.py:76-93)
+    and the 2D antialias compensation as torch ops on the conic after
+    preprocess (metal_backend.py:367-393, 506-511). Here both run inside the
+    projection kernel: it takes the unfiltered scales and opacity (and
+    ``filter_3d`` as a constant) and returns, after the usual outputs, the
+    opacity binning and compositing use. The backward carries that opacity's
+    gradient to the opacity, the scales and the projected covariance.
+    """
+
+    @staticmethod
+    def forward(ctx, means, quats, scales, opacities, sh, sh_rest, filter_3d, antialias,
+                viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
+                sh_degree):
+        lib = _load()
+        N = means.shape[0]
+        dev = means.device
+        means, quats, scales, opacities = (t.contiguous() for t in
+                                           (means, quats, scales, opacities))
+        fused = sh_rest is None
+        if sh is not None:
+            sh = sh.contiguous()
+            rest = None if fused else sh_rest.contiguous()
+        else:
+            rest = None
+        filt = None
+        if filter_3d is not None:
+            filt = filter_3d.detach().to(torch.float32).contiguous()
+            if filt.shape != (N,):
+                raise ValueError(f"filter_3d must be ({N},), got {tuple(filt.shape)}")
+        uv = torch.empty(N, 2, device=dev)
+        conic = torch.empty(N, 3, device=dev)
+        depth = torch.empty(N, device=dev)
+        rxy = torch.empty(N, 2, device=dev)
+        valid = torch.empty(N, dtype=torch.int32, device=dev)
+        color = torch.empty(N, 3, device=dev) if sh is not None else None
+        op_eff = torch.empty(N, device=dev)
+        _lib.check(lib.mg_preprocess_forward_mip(
+            N, _lib.dev_tensor(means, "means"), _lib.dev_tensor(quats, "quats"),
+            _lib.dev_tensor(scales, "scales"),
+            None if sh is None else _lib.dev_tensor(sh, "sh"),
+            None if rest is None else _lib.dev_tensor(rest, "sh_rest"), int(fused),
+            _lib.dev_tensor(opacities, "opacities"), _lib.host_f32(viewmat), fx, fy, cx, cy,
+            W, H, near, far, blur, max_radius, _lib.host_f32(cam_center), sh_degree,
+            None if filt is None else _lib.dev_tensor(filt, "filter_3d"), int(bool(antialias)),
+            uv.data_ptr(), conic.data_ptr(), depth.data_ptr(), rxy.data_ptr(), valid.data_ptr(),
+            None if color is None else color.data_ptr(), op_eff.data_ptr(),
+            _lib.stream(means)))
+        ctx.save_for_backward(means, quats, scales, opacities, sh, rest, filt, valid)
+        ctx.fused = fused
+        ctx.has_sh = sh is not None
+        ctx.antialias = bool(antialias)
+        ctx.meta = (viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
+                    sh_degree)
+        ctx.mark_non_differentiable(depth, rxy, valid)
+        if color is None:
+            return uv, conic, depth, rxy, valid, op_eff
+        return uv, conic, depth, rxy, valid, color, op_eff
+
+    @staticmethod
+    def backward(ctx, d_uv, d_conic, d_depth, d_rxy, d_valid, *rest_grads):
+        lib = _load()
+        means, quats, scales, opacities, sh, rest, filt, valid = ctx.saved_tensors
+        viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center, deg = ctx.meta
+        if ctx.has_sh:
+            d_color, d_oe = rest_grads
+        else:
+            d_color, (d_oe,) = None, rest_grads
+        N = means.shape[0]
+        dev = means.device
+        d_means = torch.empty(N, 3, device=dev)
+        d_quats = torch.empty(N, 4, device=dev)
+        d_scales = torch.empty(N, 3, device=dev)
+        d_op = torch.empty(N, device=dev)
+        d_sh = d_rest = None
+        if ctx.has_sh:
+            d_sh = torch.empty_like(sh)
+            d_rest = None if ctx.fused else torch.empty_like(rest)
+            d_color = torch.zeros(N, 3, device=dev) if d_color is None else d_color.contiguous()
+        d_oe = torch.zeros(N, device=dev) if d_oe is None else d_oe.contiguous()
+        d_uv = torch.zeros(N, 2, device=dev) if d_uv is None else d_uv.contiguous()
+        d_conic = torch.zeros(N, 3, device=dev) if d_conic is None else d_conic.contiguous()
+        _lib.check(lib.mg_preprocess_backward_mip(
+            N, means.data_ptr(), quats.data_ptr(), scales.data_ptr(),
+            None if sh is None else sh.data_ptr(), None if rest is None else rest.data_ptr(),
+            int(ctx.fused), _lib.dev_tensor(d_uv, "d_uv"), _lib.dev_tensor(d_conic, "d_conic"),
+            None if not ctx.has_sh else _lib.dev_tensor(d_color, "d_color"), valid.data_ptr(),
+            _lib.host_f32(viewmat), fx, fy, cx, cy, W, H, near, far, blur, max_radius,
+            _lib.host_f32(cam_center), deg, opacities.data_ptr(),
+            None if filt is None else filt.data_ptr(), int(ctx.antialias),
+            _lib.dev_tensor(d_oe, "d_opacity"), d_means.data_ptr(), d_quats.data_ptr(),
+            d_scales.data_ptr(), None if d_sh is None else d_sh.data_ptr(),
+            None if d_rest is None else d_rest.data_ptr(), d_op.data_ptr(), _lib.stream(means)))
+        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 15
+
+
 # Names that describe this backend rather than the reference's.
 _PreprocessHIP = _PreprocessMetal
 _RasterizeHIP = _RasterizeMetal
@@ -483,7 +585,7 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
            background=(0.0, 0.0, 0.0), colors=None, max_radius_frac: float = 1.0,
            sh_rest=None, antialias: bool = False, absgrad_out=None,
            min_transmittance: float = DEFAULT_T_MIN, chunked_backward: bool = False,
-           **_ignored):
+           filter_3d=None, **_ignored):
     """Render Gaussians from one camera; same signature as the reference's.
 
     means (N,3) world; quats (N,4) wxyz (need not be normalised); scales (N,3)
@@ -495,6 +597,11 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     ``chunked_backward`` splits each tile's backward into 512-entry units run
     in parallel (same gradients up to rounding); it helps when a few tiles hold
     most of the intersections.
+    ``filter_3d`` (N,) applies Mip-Splatting's 3D filter inside the
+    projection kernel: the result equals rendering
+    ``apply_3d_filter(scales, opacities, filter_3d)`` (what the reference's
+    trainer does in torch, train.py:223-227), with the filter a constant.
+    ``antialias`` likewise runs in the kernel.
     """
     explicit_colors = colors is not None
     _require_gpu(means)
@@ -509,7 +616,21 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     fx, fy, cx, cy, vm_h, cam_center = _camera(K, viewmat)
     max_radius = max_radius_frac * max(W, H)
 
-    if explicit_colors:
+    if filter_3d is not None or antialias:
+        # Both filters in the projection kernel; the compensated opacity is
+        # binned too, which gives a tighter, still exact, ellipse bound
+        # (metal_backend.py:506-511).
+        if explicit_colors:
+            uv, conic, depth, rxy, valid_i, opacities = _PreprocessMip.apply(
+                means, quats, scales, opacities, None, None, filter_3d, antialias, vm_h, fx,
+                fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree)
+            colors = colors.contiguous()
+        else:
+            sh_in, rest_in = _sh_inputs(sh, sh_rest)
+            uv, conic, depth, rxy, valid_i, colors, opacities = _PreprocessMip.apply(
+                means, quats, scales, opacities, sh_in, rest_in, filter_3d, antialias, vm_h,
+                fx, fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree)
+    elif explicit_colors:
         uv, conic, depth, rxy, valid_i = _PreprocessMetal.apply(
             means, quats, scales, None, None, opacities.detach(), vm_h, fx, fy, cx, cy, W, H,
             near, far, 0.3, max_radius, cam_center, sh_degree)
@@ -520,10 +641,6 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
             means, quats, scales, sh_in, rest_in, opacities.detach(), vm_h, fx, fy, cx, cy,
             W, H, near, far, 0.3, max_radius, cam_center, sh_degree)
     valid_b = valid_i.bool()
-    if antialias:
-        # Before binning: the compensated opacity gives a tighter, still exact
-        # ellipse bound (metal_backend.py:506-511).
-        opacities = opacities * antialias_scale(conic, 0.3)
 
     gauss_ids, tile_offsets, tiles_x = build_tile_lists_metal(
         uv.detach(), rxy.detach(), depth.detach(), valid_i, conic.detach(),

@@ -132,6 +132,7 @@ struct Proj {
     float M[9];          // R diag(s)
     float S[6];          // Sigma = M M^T: xx xy xz yy yz zz
     float T0[3], T1[3];  // rows of J * Rw
+    float a0, c0;        // diagonal of the undilated 2D covariance
     float a, b, c;       // dilated 2D covariance
 };
 
@@ -189,9 +190,49 @@ __device__ __forceinline__ void project(const Cam &C, float mx, float my, float 
     const float ST1x = s00 * P.T1[0] + s01 * P.T1[1] + s02 * P.T1[2];
     const float ST1y = s01 * P.T1[0] + s11 * P.T1[1] + s12 * P.T1[2];
     const float ST1z = s02 * P.T1[0] + s12 * P.T1[1] + s22 * P.T1[2];
-    P.a = P.T0[0] * ST0x + P.T0[1] * ST0y + P.T0[2] * ST0z + C.blur;
+    P.a0 = P.T0[0] * ST0x + P.T0[1] * ST0y + P.T0[2] * ST0z;
     P.b = P.T0[0] * ST1x + P.T0[1] * ST1y + P.T0[2] * ST1z;
-    P.c = P.T1[0] * ST1x + P.T1[1] * ST1y + P.T1[2] * ST1z + C.blur;
+    P.c0 = P.T1[0] * ST1x + P.T1[1] * ST1y + P.T1[2] * ST1z;
+    P.a = P.a0 + C.blur;
+    P.c = P.c0 + C.blur;
+}
+
+// ------------------------------------------------------------ mip filters
+// Mip-Splatting's two low-pass filters, folded into the projection.
+//
+// 3D (mipfilter.py:76-93): per-Gaussian filter size f widens every axis,
+// s' = sqrt(s^2 + f^2), and dims the Gaussian by
+// coef3 = sqrt(clamp(prod s^2 / prod s'^2, 0, 1)) so the total density is
+// kept. The covariance is built from s'.
+// 2D (torch_ref.py:100-124, metal_backend.py:367-393): the blur added to the
+// projected covariance is compensated by coef2 = sqrt(clamp(max(det0, 0) /
+// max(det, 1e-12), 0, 1)), det0 and det the determinants before and after the
+// blur. The SnugBox extents and the validity test see the opacity after the
+// 3D filter and before the 2D one, as the reference's kernel does (it is
+// handed the filtered opacity and the antialias factor is applied after it,
+// metal_backend.py:498-511); binning and compositing see both.
+struct Mip3 {
+    float s2[3], s2f[3];   // s^2 and s^2 + f^2
+    float coef;            // 1 without a filter
+};
+
+__device__ __forceinline__ void mip3_apply(float f, float s[3], Mip3 &M) {
+    const float f2 = f * f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        M.s2[i] = s[i] * s[i];
+        M.s2f[i] = M.s2[i] + f2;
+        s[i] = sqrtf(M.s2f[i]);
+    }
+    const float r = (M.s2[0] * M.s2[1] * M.s2[2]) / (M.s2f[0] * M.s2f[1] * M.s2f[2]);
+    M.coef = sqrtf(fminf(fmaxf(r, 0.0f), 1.0f));
+}
+
+__device__ __forceinline__ float mip2_coef(const Proj &P) {
+    const float det0 = P.a0 * P.c0 - P.b * P.b;
+    const float det = P.a * P.c - P.b * P.b;
+    const float r = fmaxf(det0, 0.0f) / fmaxf(det, 1e-12f);
+    return sqrtf(fminf(fmaxf(r, 0.0f), 1.0f));
 }
 
 // ------------------------------------------------------------ quad SH phase
@@ -327,8 +368,14 @@ struct PreFwdArgs {
     int32_t fused, vec4;
     float *uv, *conic, *depth, *rxy, *color;
     int32_t *valid;
+    // Mip filters (MIP kernels only): per-Gaussian 3D filter size or null,
+    // the 2D compensation flag, and the opacity binning and compositing use.
+    const float *filt;
+    int32_t aa;
+    float *op_eff;
 };
 
+template <bool MIP>
 __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFwdArgs A) {
     const Cam &C = A.C;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -342,7 +389,13 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFw
     if (in) {
         mx = A.means[3 * g]; my = A.means[3 * g + 1]; mz = A.means[3 * g + 2];
         const float qv[4] = {A.quats[4 * g], A.quats[4 * g + 1], A.quats[4 * g + 2], A.quats[4 * g + 3]};
-        const float sv[3] = {A.scales[3 * g], A.scales[3 * g + 1], A.scales[3 * g + 2]};
+        float sv[3] = {A.scales[3 * g], A.scales[3 * g + 1], A.scales[3 * g + 2]};
+        float op = A.opac[g];
+        if (MIP && A.filt) {
+            Mip3 M3;
+            mip3_apply(A.filt[g], sv, M3);
+            op *= M3.coef;
+        }
         Proj P;
         project(C, mx, my, mz, qv, sv, P);
         const float z = P.p[2];
@@ -357,7 +410,6 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFw
         // SnugBox: the alpha = 1/255 level set has per-axis half-extent
         // sqrt(2 ln(255 op)) * sqrt(cov_axis), never more than the 3-sigma
         // circle (preprocess.metal:180-190).
-        const float op = A.opac[g];
         const float two_l = 2.0f * logf(fmaxf(255.0f * op, 1.0f));
         const float rs = sqrtf(two_l);
         const float rx = fminf(rs * sqrtf(fmaxf(P.a, 0.0f)), radius);
@@ -374,6 +426,7 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFw
         A.rxy[2 * g] = rx;
         A.rxy[2 * g + 1] = ry;
         A.valid[g] = ok ? 1 : 0;
+        if (MIP) A.op_eff[g] = A.aa ? op * mip2_coef(P) : op;
     }
 
     if (A.sh == nullptr) return;   // explicit-colour callers: no SH, no colour
@@ -428,8 +481,15 @@ struct PreBwdArgs {
     const float *d_uv, *d_conic, *d_color;
     const int32_t *valid;
     float *d_means, *d_quats, *d_scales, *d_sh, *d_rest;
+    // Mip filters (MIP kernels only): the unfiltered opacity, the 3D filter
+    // size or null, the 2D flag, the gradient of the effective opacity, and
+    // the opacity gradient written back.
+    const float *opac, *filt, *d_oe;
+    int32_t aa;
+    float *d_op;
 };
 
+template <bool MIP>
 __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBwdArgs A) {
     const Cam &C = A.C;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -531,7 +591,15 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
     // ------------------------------------------ projection: lane = Gaussian
     if (vld != 0) {
         const float qv[4] = {A.quats[4 * g], A.quats[4 * g + 1], A.quats[4 * g + 2], A.quats[4 * g + 3]};
-        const float sv[3] = {A.scales[3 * g], A.scales[3 * g + 1], A.scales[3 * g + 2]};
+        const float sraw[3] = {A.scales[3 * g], A.scales[3 * g + 1], A.scales[3 * g + 2]};
+        float sv[3] = {sraw[0], sraw[1], sraw[2]};
+        Mip3 M3;
+        M3.coef = 1.0f;
+        float f3 = 0.0f;
+        if (MIP && A.filt) {
+            f3 = A.filt[g];
+            mip3_apply(f3, sv, M3);
+        }
         Proj P;
         project(C, mx, my, mz, qv, sv, P);
         const float a = P.a, b = P.b, c = P.c;
@@ -545,6 +613,32 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
         float db = -k1 * id - 2.0f * ddet * b;
         float dc = k0 * id + ddet * a;
         if (det <= 1e-12f) da = db = dc = 0.f;
+
+        // Effective opacity oe = op coef3 coef2: its gradient reaches the
+        // opacity, the 2D covariance (through coef2) and the scales (through
+        // coef3, below).
+        float d_op1 = 0.0f;
+        if (MIP) {
+            const float d_oe = A.d_oe[g];
+            d_op1 = d_oe;
+            if (A.aa) {
+                const float op1 = A.opac[g] * M3.coef;
+                const float det0 = P.a0 * P.c0 - b * b;
+                const float r = fmaxf(det0, 0.0f) / fmaxf(det, 1e-12f);
+                const float coef2 = sqrtf(fminf(fmaxf(r, 0.0f), 1.0f));
+                d_op1 = d_oe * coef2;
+                // coef2 = sqrt(det0 / det) where 0 < r <= 1 (the clamps pass
+                // the gradient there; sqrt has none to give at r = 0).
+                if (r > 0.0f && r <= 1.0f && det > 1e-12f) {
+                    const float dr = 0.5f * d_oe * op1 / coef2;
+                    const float ddet0 = dr / det;
+                    const float ddet = -dr * r / det;
+                    da += ddet0 * P.c0 + ddet * c;
+                    dc += ddet0 * P.a0 + ddet * a;
+                    db += -2.0f * b * (ddet0 + ddet);
+                }
+            }
+        }
 
         // a = T0 S T0, b = T0 S T1, c = T1 S T1 (S symmetric).
         const float *S = P.S;
@@ -614,6 +708,22 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
             G[3 + j] = dM[3 + j] * P.s[j];
             G[6 + j] = dM[6 + j] * P.s[j];
         }
+        if (MIP) {
+            if (A.filt) {
+                // s' = sqrt(s^2 + f^2): ds = ds' s / s'. coef3^2 = prod s^2 /
+                // prod (s^2 + f^2): d coef3 / d s_j = coef3 f^2 / (s_j (s_j^2 + f^2)).
+                const float dcoef3 = d_op1 * A.opac[g];
+                const float f2 = f3 * f3;
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    const float chain = sv[j] > 0.0f ? dsc[j] * sraw[j] / sv[j] : 0.0f;
+                    const float dimm = sraw[j] > 0.0f
+                        ? dcoef3 * M3.coef * f2 / (sraw[j] * M3.s2f[j]) : 0.0f;
+                    dsc[j] = chain + dimm;
+                }
+            }
+            A.d_op[g] = d_op1 * M3.coef;
+        }
         A.d_scales[3 * g] = dsc[0];
         A.d_scales[3 * g + 1] = dsc[1];
         A.d_scales[3 * g + 2] = dsc[2];
@@ -633,6 +743,7 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
         A.d_quats[4 * g + 2] = (dyq - y * dotq) * iq;
         A.d_quats[4 * g + 3] = (dzq - z * dotq) * iq;
     } else {
+        if (MIP) A.d_op[g] = 0.f;
         A.d_scales[3 * g] = 0.f; A.d_scales[3 * g + 1] = 0.f; A.d_scales[3 * g + 2] = 0.f;
         A.d_quats[4 * g] = 0.f; A.d_quats[4 * g + 1] = 0.f;
         A.d_quats[4 * g + 2] = 0.f; A.d_quats[4 * g + 3] = 0.f;
@@ -660,6 +771,88 @@ static int32_t make_cam(Cam &C, const float *viewmat, float fx, float fy, float 
     return MG_OK;
 }
 
+static int32_t preprocess_fwd(int64_t N, const float *means, const float *quats,
+                              const float *scales, const float *sh, const float *sh_rest,
+                              int32_t sh_fused, const float *opacities, const float *viewmat,
+                              float fx, float fy, float cx, float cy, int32_t W, int32_t H,
+                              float near_plane, float far_plane, float blur, float max_radius,
+                              const float *cam_center, int32_t sh_degree, bool mip,
+                              const float *filter_3d, int32_t antialias, float *uv,
+                              float *conic, float *depth, float *rxy, int32_t *valid,
+                              float *color, float *opacity_eff, mg_stream_t stream,
+                              const char *who) {
+    PreFwdArgs A{};
+    int32_t rc = make_cam(A.C, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane, blur,
+                          max_radius, cam_center, sh_degree, who);
+    if (rc != MG_OK) return rc;
+    MG_REQUIRE(N >= 0, "%s: N = %lld", who, (long long)N);
+    if (N == 0) return MG_OK;
+    MG_REQUIRE(means && quats && scales && opacities && uv && conic && depth && rxy && valid,
+               "%s: null tensor pointer", who);
+    MG_REQUIRE(sh == nullptr || color != nullptr, "%s: SH given but no colour output", who);
+    MG_REQUIRE(sh == nullptr || sh_fused || sh_rest != nullptr,
+               "SH must be either one (N,16,3) tensor or (N,1,3)+(N,15,3)");
+    MG_REQUIRE(!mip || opacity_eff != nullptr, "%s: null effective-opacity output", who);
+    A.N = N;
+    A.means = means; A.quats = quats; A.scales = scales; A.sh = sh;
+    A.rest = sh_rest; A.opac = opacities; A.fused = sh_fused;
+    A.uv = uv; A.conic = conic; A.depth = depth; A.rxy = rxy; A.valid = valid; A.color = color;
+    A.filt = filter_3d; A.aa = antialias; A.op_eff = opacity_eff;
+    A.vec4 = sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)sh & 15) == 0);
+    const int64_t blocks = ceil_div(N, kPreThreads);
+    TimedScope ts("preprocess_forward", as_stream(stream));
+    if (mip)
+        preprocess_fwd_kernel<true><<<(unsigned)blocks, kPreThreads, 0, as_stream(stream)>>>(A);
+    else
+        preprocess_fwd_kernel<false><<<(unsigned)blocks, kPreThreads, 0, as_stream(stream)>>>(A);
+    MG_LAUNCHED("preprocess_fwd_kernel");
+    return MG_OK;
+}
+
+static int32_t preprocess_bwd(int64_t N, const float *means, const float *quats,
+                              const float *scales, const float *sh, const float *sh_rest,
+                              int32_t sh_fused, const float *d_uv, const float *d_conic,
+                              const float *d_color, const int32_t *valid, const float *viewmat,
+                              float fx, float fy, float cx, float cy, int32_t W, int32_t H,
+                              float near_plane, float far_plane, float blur, float max_radius,
+                              const float *cam_center, int32_t sh_degree, bool mip,
+                              const float *opacities, const float *filter_3d, int32_t antialias,
+                              const float *d_opacity_eff, float *d_means, float *d_quats,
+                              float *d_scales, float *d_sh, float *d_sh_rest,
+                              float *d_opacities, mg_stream_t stream, const char *who) {
+    PreBwdArgs A{};
+    int32_t rc = make_cam(A.C, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane, blur,
+                          max_radius, cam_center, sh_degree, who);
+    if (rc != MG_OK) return rc;
+    MG_REQUIRE(N >= 0, "%s: N = %lld", who, (long long)N);
+    if (N == 0) return MG_OK;
+    MG_REQUIRE(means && quats && scales && d_uv && d_conic && valid && d_means && d_quats &&
+                   d_scales, "%s: null tensor pointer", who);
+    if (d_color) {
+        MG_REQUIRE(sh && d_sh && (sh_fused || (sh_rest && d_sh_rest)),
+                   "SH must be either one (N,16,3) tensor or (N,1,3)+(N,15,3)");
+    }
+    MG_REQUIRE(!mip || (opacities && d_opacity_eff && d_opacities),
+               "%s: null opacity pointer", who);
+    A.N = N;
+    A.means = means; A.quats = quats; A.scales = scales; A.sh = sh; A.rest = sh_rest;
+    A.fused = sh_fused; A.d_uv = d_uv; A.d_conic = d_conic; A.d_color = d_color; A.valid = valid;
+    A.d_means = d_means; A.d_quats = d_quats; A.d_scales = d_scales; A.d_sh = d_sh;
+    A.d_rest = d_sh_rest;
+    A.opac = opacities; A.filt = filter_3d; A.aa = antialias; A.d_oe = d_opacity_eff;
+    A.d_op = d_opacities;
+    A.vec4 = sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)sh & 15) == 0);
+    A.st_vec4 = d_sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)d_sh & 15) == 0);
+    const int64_t blocks = ceil_div(N, kPreThreads);
+    TimedScope ts("preprocess_backward", as_stream(stream));
+    if (mip)
+        preprocess_bwd_kernel<true><<<(unsigned)blocks, kPreThreads, 0, as_stream(stream)>>>(A);
+    else
+        preprocess_bwd_kernel<false><<<(unsigned)blocks, kPreThreads, 0, as_stream(stream)>>>(A);
+    MG_LAUNCHED("preprocess_bwd_kernel");
+    return MG_OK;
+}
+
 }  // namespace mg
 
 using namespace mg;
@@ -674,28 +867,26 @@ int32_t mg_preprocess_forward(int64_t N, const float *means, const float *quats,
                               const float *cam_center, int32_t sh_degree, float *uv,
                               float *conic, float *depth, float *rxy, int32_t *valid,
                               float *color, mg_stream_t stream) {
-    PreFwdArgs A{};
-    int32_t rc = make_cam(A.C, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane, blur,
-                          max_radius, cam_center, sh_degree, "mg_preprocess_forward");
-    if (rc != MG_OK) return rc;
-    MG_REQUIRE(N >= 0, "mg_preprocess_forward: N = %lld", (long long)N);
-    if (N == 0) return MG_OK;
-    MG_REQUIRE(means && quats && scales && opacities && uv && conic && depth && rxy && valid,
-               "mg_preprocess_forward: null tensor pointer");
-    MG_REQUIRE(sh == nullptr || color != nullptr,
-               "mg_preprocess_forward: SH given but no colour output");
-    MG_REQUIRE(sh == nullptr || sh_fused || sh_rest != nullptr,
-               "SH must be either one (N,16,3) tensor or (N,1,3)+(N,15,3)");
-    A.N = N;
-    A.means = means; A.quats = quats; A.scales = scales; A.sh = sh;
-    A.rest = sh_rest; A.opac = opacities; A.fused = sh_fused;
-    A.uv = uv; A.conic = conic; A.depth = depth; A.rxy = rxy; A.valid = valid; A.color = color;
-    A.vec4 = sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)sh & 15) == 0);
-    const int64_t blocks = ceil_div(N, kPreThreads);
-    TimedScope ts("preprocess_forward", as_stream(stream));
-    preprocess_fwd_kernel<<<(unsigned)blocks, kPreThreads, 0, as_stream(stream)>>>(A);
-    MG_LAUNCHED("preprocess_fwd_kernel");
-    return MG_OK;
+    return preprocess_fwd(N, means, quats, scales, sh, sh_rest, sh_fused, opacities, viewmat,
+                          fx, fy, cx, cy, W, H, near_plane, far_plane, blur, max_radius,
+                          cam_center, sh_degree, false, nullptr, 0, uv, conic, depth, rxy,
+                          valid, color, nullptr, stream, "mg_preprocess_forward");
+}
+
+int32_t mg_preprocess_forward_mip(int64_t N, const float *means, const float *quats,
+                                  const float *scales, const float *sh, const float *sh_rest,
+                                  int32_t sh_fused, const float *opacities,
+                                  const float *viewmat, float fx, float fy, float cx, float cy,
+                                  int32_t W, int32_t H, float near_plane, float far_plane,
+                                  float blur, float max_radius, const float *cam_center,
+                                  int32_t sh_degree, const float *filter_3d, int32_t antialias,
+                                  float *uv, float *conic, float *depth, float *rxy,
+                                  int32_t *valid, float *color, float *opacity_eff,
+                                  mg_stream_t stream) {
+    return preprocess_fwd(N, means, quats, scales, sh, sh_rest, sh_fused, opacities, viewmat,
+                          fx, fy, cx, cy, W, H, near_plane, far_plane, blur, max_radius,
+                          cam_center, sh_degree, true, filter_3d, antialias, uv, conic, depth,
+                          rxy, valid, color, opacity_eff, stream, "mg_preprocess_forward_mip");
 }
 
 int32_t mg_preprocess_backward(int64_t N, const float *means, const float *quats,
@@ -707,30 +898,30 @@ int32_t mg_preprocess_backward(int64_t N, const float *means, const float *quats
                                const float *cam_center, int32_t sh_degree, float *d_means,
                                float *d_quats, float *d_scales, float *d_sh, float *d_sh_rest,
                                mg_stream_t stream) {
-    PreBwdArgs A{};
-    int32_t rc = make_cam(A.C, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane, blur,
-                          max_radius, cam_center, sh_degree, "mg_preprocess_backward");
-    if (rc != MG_OK) return rc;
-    MG_REQUIRE(N >= 0, "mg_preprocess_backward: N = %lld", (long long)N);
-    if (N == 0) return MG_OK;
-    MG_REQUIRE(means && quats && scales && d_uv && d_conic && valid && d_means && d_quats &&
-                   d_scales, "mg_preprocess_backward: null tensor pointer");
-    if (d_color) {
-        MG_REQUIRE(sh && d_sh && (sh_fused || (sh_rest && d_sh_rest)),
-                   "SH must be either one (N,16,3) tensor or (N,1,3)+(N,15,3)");
-    }
-    A.N = N;
-    A.means = means; A.quats = quats; A.scales = scales; A.sh = sh; A.rest = sh_rest;
-    A.fused = sh_fused; A.d_uv = d_uv; A.d_conic = d_conic; A.d_color = d_color; A.valid = valid;
-    A.d_means = d_means; A.d_quats = d_quats; A.d_scales = d_scales; A.d_sh = d_sh;
-    A.d_rest = d_sh_rest;
-    A.vec4 = sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)sh & 15) == 0);
-    A.st_vec4 = d_sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)d_sh & 15) == 0);
-    const int64_t blocks = ceil_div(N, kPreThreads);
-    TimedScope ts("preprocess_backward", as_stream(stream));
-    preprocess_bwd_kernel<<<(unsigned)blocks, kPreThreads, 0, as_stream(stream)>>>(A);
-    MG_LAUNCHED("preprocess_bwd_kernel");
-    return MG_OK;
+    return preprocess_bwd(N, means, quats, scales, sh, sh_rest, sh_fused, d_uv, d_conic,
+                          d_color, valid, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane,
+                          blur, max_radius, cam_center, sh_degree, false, nullptr, nullptr, 0,
+                          nullptr, d_means, d_quats, d_scales, d_sh, d_sh_rest, nullptr, stream,
+                          "mg_preprocess_backward");
+}
+
+int32_t mg_preprocess_backward_mip(int64_t N, const float *means, const float *quats,
+                                   const float *scales, const float *sh, const float *sh_rest,
+                                   int32_t sh_fused, const float *d_uv, const float *d_conic,
+                                   const float *d_color, const int32_t *valid,
+                                   const float *viewmat, float fx, float fy, float cx, float cy,
+                                   int32_t W, int32_t H, float near_plane, float far_plane,
+                                   float blur, float max_radius, const float *cam_center,
+                                   int32_t sh_degree, const float *opacities,
+                                   const float *filter_3d, int32_t antialias,
+                                   const float *d_opacity_eff, float *d_means, float *d_quats,
+                                   float *d_scales, float *d_sh, float *d_sh_rest,
+                                   float *d_opacities, mg_stream_t stream) {
+    return preprocess_bwd(N, means, quats, scales, sh, sh_rest, sh_fused, d_uv, d_conic,
+                          d_color, valid, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane,
+                          blur, max_radius, cam_center, sh_degree, true, opacities, filter_3d,
+                          antialias, d_opacity_eff, d_means, d_quats, d_scales, d_sh, d_sh_rest,
+                          d_opacities, stream, "mg_preprocess_backward_mip");
 }
 
 }  // extern "C"
