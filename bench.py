@@ -67,6 +67,9 @@ def parse():
                          "the 3D filter applied as the reference's torch reparameterisation "
                          "(apply_3d_filter, train.py:223-227) before render")
     ap.add_argument("--cpu-only", action="store_true", help="time only the CPU baseline")
+    ap.add_argument("--mcmc", action="store_true",
+                    help="time the MCMC densification kernels (add_noise, relocate, grow) on the "
+                         "config-4 parameters instead of the step")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the HBM traffic summary of two rocprofv3 --pmc runs and exit")
     ap.add_argument("--stats-summary", metavar="KERNEL_STATS_CSV",
@@ -253,6 +256,73 @@ def gpu_bench(args):
                 nbytes=nbytes, I=I, f_valid=f_valid, n_floats=n_floats, f3d_ms=f3d_ms)
 
 
+def mcmc_bench(args):
+    """MCMC densification at config 4: the 1M-Gaussian parameter dict with
+    FusedAdam state, as the reference's trainer holds it between steps.
+
+    add_noise runs every step in the reference's trainer (train.py:417);
+    relocate and grow every 100 steps (train.py:450-457). relocate is timed
+    with a stated 5% of rows made dead (logit -8, a seeded choice) before each
+    call; grow from 900k to 1M active rows. Wall times include the one host
+    sync each of relocate and grow makes; kernel times are HIP events.
+    """
+    import torch
+
+    from metal_gauss_amd import _lib, mcmc
+
+    dev = torch.device("cuda:0")
+    step = Step(args.gaussians, dev)
+    step()                                  # optimizer state exists
+    torch.cuda.synchronize()
+    p = {k: v for k, v in step.p.items()}
+    N = args.gaussians
+    g = torch.Generator().manual_seed(7)
+    dead = torch.randperm(N, generator=g)[: N // 20].to(dev)
+    keep_logit = p["logit_opac"].detach().clone()
+    out = {}
+
+    def timed(fn, reps, label, prep=None):
+        walls = []
+        with _lib.KernelTimer():
+            for r in range(reps):
+                if prep is not None:
+                    prep()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                walls.append(time.perf_counter() - t0)
+            kern = {}
+            for k in label:
+                tot, cnt = _lib.KernelTimer.query(k)
+                if cnt:
+                    kern[k] = round(tot / cnt, 4)
+        walls.sort()
+        return round(1e3 * walls[len(walls) // 2], 4), kern
+
+    with torch.no_grad():
+        for _ in range(10):
+            mcmc.add_noise(p, lr_means=1.6e-4)
+        wall, kern = timed(lambda: mcmc.add_noise(p, lr_means=1.6e-4), 100, ["add_noise"])
+        out["add_noise"] = {"wall_ms": wall, "kernel_ms": kern.get("add_noise"),
+                            "GBps": round(56 * N / (kern["add_noise"] * 1e-3) / 1e9, 1)}
+
+        def kill():
+            p["logit_opac"].copy_(keep_logit)
+            p["logit_opac"][dead] = -8.0
+
+        moved = []
+        wall, kern = timed(lambda: moved.append(mcmc.relocate(p, opt=step.opt)), 10,
+                           ["mcmc_weights", "mcmc_apply"], prep=kill)
+        out["relocate"] = {"wall_ms": wall, "kernel_ms": kern, "moved": moved[-1],
+                           "dead_fraction": 0.05}
+        p["logit_opac"].copy_(keep_logit)
+        wall, kern = timed(lambda: mcmc.grow(p, target=N, active=N - N // 10, opt=step.opt), 10,
+                           ["mcmc_weights", "mcmc_apply"])
+        out["grow"] = {"wall_ms": wall, "kernel_ms": kern, "added": N // 10}
+    return out
+
+
 PMC_REGEX = ("raster_bwd|raster_fwd|adam_multi|preprocess_fwd|preprocess_bwd|radix_|scan_|"
              "bin_write|bin_count|copyBuffer")
 
@@ -313,25 +383,39 @@ def pmc_summary(fetch_dir, write_dir, copy_mib):
     return "\n".join(lines)
 
 
-def stats_summary(stats_csv, steps, variant="base"):
+def stats_summary(stats_csv, steps, variant="base", mcmc=False):
     """Text summary of a rocprofv3 --kernel-trace --stats kernel_stats.csv."""
     import csv
 
     with open(stats_csv, newline="") as f:
         rows = list(csv.DictReader(f))
     total = sum(float(r["TotalDurationNs"]) for r in rows)
-    vflag = "" if variant == "base" else f" --variant {variant}"
-    what = {"base": "", "mip": ", Mip 3D filter + 2D antialias in the projection kernel",
-            "mip-torch": ", Mip 3D filter as torch reparameterisation"}[variant]
-    lines = [
-        "# rocprofv3 kernel statistics, config-4 step (1M Gaussians SH3, 800x800, tile 16"
-        f"{what}), MI355X",
-        "# made by (from the repository root, TMPDIR=/tmp):",
-        "#   rocprofv3 --kernel-trace --stats -f csv -T -d P -o kt -- python -u bench.py "
-        f"--steps {steps} --warmup 5 --no-cpu-baseline{vflag}",
-        f"#   python bench.py --stats-summary P/kt_kernel_stats.csv{vflag}",
-        "# The run covers warmup + timed steps + the fwd+bwd-only loop + 10 per-kernel timing "
-        "steps.",
+    if mcmc:
+        lines = [
+            "# rocprofv3 kernel statistics, MCMC densification on the config-4 parameters "
+            "(1M Gaussians, 59 floats each, FusedAdam state), MI355X",
+            "# made by (from the repository root, TMPDIR=/tmp):",
+            "#   rocprofv3 --kernel-trace --stats -f csv -T -d P -o kt -- python -u bench.py "
+            "--mcmc",
+            "#   python bench.py --stats-summary P/kt_kernel_stats.csv --mcmc",
+            "# The run covers one config-4 step (to create optimizer state), 110 add_noise "
+            "calls, 10 relocates (5% dead rows) and 10 grows (900k -> 1M).",
+        ]
+    else:
+        vflag = "" if variant == "base" else f" --variant {variant}"
+        what = {"base": "", "mip": ", Mip 3D filter + 2D antialias in the projection kernel",
+                "mip-torch": ", Mip 3D filter as torch reparameterisation"}[variant]
+        lines = [
+            "# rocprofv3 kernel statistics, config-4 step (1M Gaussians SH3, 800x800, tile 16"
+            f"{what}), MI355X",
+            "# made by (from the repository root, TMPDIR=/tmp):",
+            "#   rocprofv3 --kernel-trace --stats -f csv -T -d P -o kt -- python -u bench.py "
+            f"--steps {steps} --warmup 5 --no-cpu-baseline{vflag}",
+            f"#   python bench.py --stats-summary P/kt_kernel_stats.csv{vflag}",
+            "# The run covers warmup + timed steps + the fwd+bwd-only loop + 10 per-kernel "
+            "timing steps.",
+        ]
+    lines += [
         f"{'kernel':36s} {'calls':>7s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'share_%':>8s}",
     ]
     for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
@@ -472,7 +556,7 @@ def main():
         print(pmc_summary(*args.pmc_summary, args.copy_mib or 1024))
         return
     if args.stats_summary:
-        print(stats_summary(args.stats_summary, 20, args.variant))
+        print(stats_summary(args.stats_summary, 20, args.variant, args.mcmc))
         return
     if args.cpu_only:
         print(json.dumps(cpu_baseline(args.gaussians, crop=_cpu_crop())))
@@ -484,6 +568,17 @@ def main():
         sys.exit(2)
     if args.copy_mib:
         copy_calibration(args.copy_mib)
+    if args.mcmc:
+        print(json.dumps({
+            "metric": "MCMC densification ms at 1M Gaussians (config-4 parameters + FusedAdam "
+                      "state)",
+            "unit": "ms", "n_gpus": 1, "higher_is_better": False, "dtype": "f32",
+            "data": "synthetic",
+            "config": {"workload": "config-4 parameter set, 59 floats per Gaussian, "
+                                   "relocate with 5% dead rows, grow 900k -> 1M",
+                       "n_gaussians": args.gaussians},
+            "mcmc": mcmc_bench(args)}))
+        return
     r = gpu_bench(args)
     out = {
         "metric": METRIC,

@@ -154,6 +154,54 @@ int32_t mg_compute_3d_filter(int64_t N, const float *means, int32_t n_views,
                              float near_plane, float *filter_3d,
                              int32_t *scratch, mg_stream_t stream);
 
+/* ------------------------------------------------------------------- MCMC */
+
+/* SGLD exploration of the means of near-transparent Gaussians. Replaces
+ * add_noise (metal_gauss/mcmc.py:164-192): means[i] += R(q_i) (z_i *
+ * exp(log_scales_i)) * sigmoid(-100 (sigmoid(logit_i) - opacity_gate)) *
+ * lr_means * weight for rows i < n. z are standard normals: eps (n,3) when
+ * given, else drawn in the kernel (Philox4x64-10 keyed by `seed`, counter =
+ * row, Box-Muller), so a seed fixes the draw. */
+int32_t mg_add_noise(int64_t n, float *means, const float *log_scales,
+                     const float *quats, const float *logit_opac,
+                     const float *eps, float lr_means, float weight,
+                     float opacity_gate, uint64_t seed, mg_stream_t stream);
+
+/* Bytes of scratch relocate / grow need over n_rows candidate rows with
+ * n_draw draw slots (relocate: n_draw = n_rows). */
+int64_t mg_mcmc_workspace_bytes(int64_t n_rows, int64_t n_draw);
+
+/* First half of relocate (metal_gauss/mcmc.py:52-104) or grow (124-161):
+ * candidate weights over rows < n (weights (n,) or NULL for the opacity
+ * sigmoid(logit); relocate: rows with opacity < thresh are dead and weigh 0;
+ * grow != 0: every row is a candidate and drawn weights are floored at
+ * 1e-8), their block sums, and the multiplicity counters cleared. Copies
+ * five totals to totals_host after synchronising the stream (the
+ * reference's nonzero / multinomial syncs too): [sum of weights, sum of the
+ * opacity fallback, dead rows, any weight inf or nan, any weight > 0]. */
+int32_t mg_mcmc_weights(int64_t n, const float *logit_opac, const float *weights,
+                        float thresh, int32_t grow, void *ws, int64_t ws_size,
+                        int64_t n_draw, double *totals_host, mg_stream_t stream);
+
+/* Second half: draws with replacement in proportion to the weights (or the
+ * opacity when use_opacity != 0, the reference's fallback), by inverse CDF
+ * with Philox uniforms keyed by `seed`; relocate: one draw per dead row,
+ * which becomes its destination; grow: n_draw draws with destinations
+ * dst0 .. dst0 + n_draw - 1. Every destination gets its source's row of each
+ * tensor, with the source's opacity split N ways (N = clamp(draws of the
+ * source, 1, 51), plus 1 for grow) and its log-scales shrunk to match; every
+ * drawn source gets the same split; both have their optimizer-state rows
+ * zeroed (mcmc.py:107-121). tensors: n_tensors device pointers, each with
+ * `widths[t]` floats per row and kinds[t] 0 = copied parameter, 1 =
+ * log-scales, 2 = logit opacity (width 1), 3 = optimizer state (zeroed).
+ * n_dest = dead rows (relocate) or n_draw (grow), from mg_mcmc_weights. */
+int32_t mg_mcmc_apply(int64_t n, const float *logit_opac, const float *weights,
+                      float thresh, int32_t grow, int32_t use_opacity, void *ws,
+                      int64_t ws_size, int64_t n_draw, int64_t n_dest, int64_t dst0,
+                      uint64_t seed, int32_t n_tensors, float *const *tensors,
+                      const int32_t *widths, const int32_t *kinds,
+                      mg_stream_t stream);
+
 /* ---------------------------------------------------------------- binning */
 
 /* Per-Gaussian count of tiles that pass the exact ellipse-vs-tile test

@@ -26,6 +26,7 @@ _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
 _f64 = ctypes.c_double
+_u64 = ctypes.c_uint64
 _pp = ctypes.POINTER(ctypes.c_void_p)
 
 _SIGNATURES = {
@@ -51,6 +52,12 @@ _SIGNATURES = {
         _i32, _i32, _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
         _vp, _vp, _vp]),
     "mg_compute_3d_filter": (_i32, [_i64, _vp, _i32, _vp, _f32, _f32, _vp, _vp, _vp]),
+    "mg_add_noise": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _u64, _vp]),
+    "mg_mcmc_workspace_bytes": (_i64, [_i64, _i64]),
+    "mg_mcmc_weights": (_i32, [_i64, _vp, _vp, _f32, _i32, _vp, _i64, _i64,
+                               ctypes.POINTER(_f64), _vp]),
+    "mg_mcmc_apply": (_i32, [_i64, _vp, _vp, _f32, _i32, _i32, _vp, _i64, _i64, _i64, _i64,
+                             _u64, _i32, _pp, ctypes.POINTER(_i32), ctypes.POINTER(_i32), _vp]),
     "mg_bin_count": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp,
                             _vp]),
     "mg_scan_workspace_bytes": (_i64, [_i64]),

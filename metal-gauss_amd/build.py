@@ -22,7 +22,7 @@ BUILD = PKG / "_build"
 LIB = PKG / "libmgauss.so"
 ARCH = "gfx950"
 
-SOURCES = ["runtime.hip", "adam.hip", "preprocess.hip", "mip.hip", "binning.hip", "sort.hip",
+SOURCES = ["runtime.hip", "adam.hip", "preprocess.hip", "mip.hip", "mcmc.hip", "binning.hip", "sort.hip",
            "rasterize.hip", "ssim.hip"]
 
 # -packed-fp32-ops keeps the compiler from emitting packed fp32 VALU forms;
