@@ -67,6 +67,10 @@ def parse():
                          "the 3D filter applied as the reference's torch reparameterisation "
                          "(apply_3d_filter, train.py:223-227) before render")
     ap.add_argument("--cpu-only", action="store_true", help="time only the CPU baseline")
+    ap.add_argument("--config", type=int, choices=[1, 2, 3, 5], default=None,
+                    help="time another BASELINE configuration instead of the config-4 step: "
+                         "1 forward at 10k/256^2; 2 fwd+bwd at 300k/800^2; 3 FusedAdam and "
+                         "SelectiveAdam over 1M Gaussians; 5 fwd+bwd at 3M/1920x1080")
     ap.add_argument("--mcmc", action="store_true",
                     help="time the MCMC densification kernels (add_noise, relocate, grow) on the "
                          "config-4 parameters instead of the step")
@@ -323,6 +327,146 @@ def mcmc_bench(args):
     return out
 
 
+def _timed_ms(fn, reps, warm=3):
+    """Median wall ms of `reps` synchronised calls after `warm` untimed ones."""
+    import torch
+
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return 1e3 * ts[len(ts) // 2]
+
+
+def _kernel_means(fn, reps, labels):
+    """Mean ms per launch of each library kernel over `reps` calls of fn."""
+    import torch
+
+    from metal_gauss_amd import _lib
+
+    with _lib.KernelTimer():
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        out = {}
+        for k in labels:
+            tot, cnt = _lib.KernelTimer.query(k)
+            if cnt:
+                out[k] = {"ms": round(tot / cnt, 4), "per_call": cnt / reps}
+    return out
+
+
+def render_config(which, reps):
+    """Configs 1, 2 and 5 ([1], [4]): one view, render
+    forward (config 1) or forward + L1 loss + backward (2, 5), on the
+    configuration's seeded scene and camera."""
+    import torch
+
+    from metal_gauss_amd import render, scenes
+
+    dev = torch.device("cuda:0")
+    if which == 1:
+        sc, cam, bg = scenes.config1()
+        target = None
+    elif which == 2:
+        sc, cam, bg = scenes.config2()
+        target = scenes.config2_target(cam.H, cam.W).to(dev)
+    else:
+        sc, cam, bg = scenes.config5()
+        target = torch.zeros(cam.H, cam.W, 3, device=dev)
+    sc = sc.to(dev)
+    leaves = {k: getattr(sc, k).clone().requires_grad_(which != 1)
+              for k in ("means", "log_scales", "quats", "logit_opac", "sh_dc", "sh_rest")}
+    info = {}
+
+    def fwd():
+        L = leaves
+        rgb, alpha, inf = render(L["means"], L["quats"], torch.exp(L["log_scales"]),
+                                 torch.sigmoid(L["logit_opac"]), L["sh_dc"], cam.K, cam.viewmat,
+                                 cam.W, cam.H, sh_degree=sc.sh_degree, sh_rest=L["sh_rest"],
+                                 background=bg)
+        info.update(inf)
+        return rgb
+
+    def fwd_bwd():
+        for t in leaves.values():
+            t.grad = None
+        (fwd() - target).abs().mean().backward()
+
+    with torch.no_grad():
+        fwd_ms = _timed_ms(fwd, reps)
+    out = {"fwd_ms": round(fwd_ms, 4)}
+    step = fwd if which == 1 else fwd_bwd
+    if which != 1:
+        out["fwd_bwd_ms"] = round(_timed_ms(fwd_bwd, reps), 4)
+    out["kernels"] = _kernel_means(step, 5, KERNELS)
+    gids_len = None
+    with torch.no_grad():
+        from metal_gauss_amd.backend import _PreprocessMetal, _camera, build_tile_lists_metal
+
+        fx, fy, cx, cy, vm_h, cc = _camera(cam.K, cam.viewmat)
+        m, q, s_, o, sh = sc.activated()
+        uv, conic, depth, rxy, valid, _ = _PreprocessMetal.apply(
+            m, q, s_, sh, None, o, vm_h, fx, fy, cx, cy, cam.W, cam.H, 0.01, 100.0, 0.3,
+            float(max(cam.W, cam.H)), cc, sc.sh_degree)
+        gids, offs, _ = build_tile_lists_metal(uv, rxy, depth, valid, conic, o, cam.W, cam.H, 16)
+        lens = (offs[1:] - offs[:-1]).cpu()
+        gids_len = int(gids.numel())
+    out.update({"intersections": gids_len, "max_tile_list": int(lens.max()),
+                "mean_tile_list": round(float(lens.float().mean()), 1),
+                "tiles_over_10k": int((lens > 10_000).sum()),
+                "valid": int(valid.sum()), "n_gaussians": sc.n,
+                "width": cam.W, "height": cam.H})
+    return out
+
+
+def adam_config(reps):
+    """Config 3: 1M Gaussians x 59 floats in the six
+    trainer groups, gradients N(0, 1e-3); FusedAdam one step then 100 steps,
+    and SelectiveAdam with a Bernoulli(0.6) visibility mask."""
+    import torch
+
+    from metal_gauss_amd import FusedAdam, SelectiveAdam, scenes
+
+    dev = torch.device("cuda:0")
+    N = 1_000_000
+    g = torch.Generator().manual_seed(2)
+    groups = scenes.config3_groups(N)
+    params = [torch.randn(N, w, generator=g).to(dev).requires_grad_(True) for _, w, _ in groups]
+    grads = [(torch.randn(N, w, generator=g) * 1e-3).to(dev) for _, w, _ in groups]
+    vis = (torch.rand(N, generator=g) < 0.6).to(dev)
+    n_floats = sum(p.numel() for p in params)
+
+    def run(opt_cls, selective):
+        ps = [p.detach().clone().requires_grad_(True) for p in params]
+        opt = opt_cls([{"params": [p], "lr": lr} for p, (_, _, lr) in zip(ps, groups)],
+                      eps=1e-15)
+        for p, gr in zip(ps, grads):
+            p.grad = gr
+        stepf = (lambda: opt.step(vis)) if selective else opt.step
+        first = _timed_ms(stepf, 1, warm=0)
+        ms = _timed_ms(stepf, 100, warm=3)
+        return first, ms
+
+    f_first, f_ms = run(FusedAdam, False)
+    s_first, s_ms = run(SelectiveAdam, True)
+    f_vis = float(vis.float().mean())
+    fused_bytes = 28 * n_floats
+    sel_bytes = (28 * n_floats + 4 * 2 * 6 * N) * f_vis + N      # + per-row steps r/w, mask
+    return {"fused": {"first_step_ms": round(f_first, 4), "ms_per_step": round(f_ms, 4),
+                      "GBps": round(fused_bytes / (f_ms * 1e-3) / 1e9, 1)},
+            "selective": {"first_step_ms": round(s_first, 4), "ms_per_step": round(s_ms, 4),
+                          "visible_fraction": round(f_vis, 4),
+                          "GBps": round(sel_bytes / (s_ms * 1e-3) / 1e9, 1)},
+            "n_floats": n_floats}
+
+
 PMC_REGEX = ("raster_bwd|raster_fwd|adam_multi|preprocess_fwd|preprocess_bwd|radix_|scan_|"
              "bin_write|bin_count|copyBuffer")
 
@@ -383,14 +527,26 @@ def pmc_summary(fetch_dir, write_dir, copy_mib):
     return "\n".join(lines)
 
 
-def stats_summary(stats_csv, steps, variant="base", mcmc=False):
+def stats_summary(stats_csv, steps, variant="base", mcmc=False, config=None):
     """Text summary of a rocprofv3 --kernel-trace --stats kernel_stats.csv."""
     import csv
 
     with open(stats_csv, newline="") as f:
         rows = list(csv.DictReader(f))
     total = sum(float(r["TotalDurationNs"]) for r in rows)
-    if mcmc:
+    if config is not None:
+        what = {1: "config 1: forward, 10k Gaussians SH0, 256x256",
+                2: "config 2: forward + L1 + backward, 300k Gaussians SH3, 800x800",
+                3: "config 3: FusedAdam and SelectiveAdam over 1M Gaussians x 59 floats",
+                5: "config 5: forward + L1 + backward, 3M Gaussians SH3, 1920x1080"}[config]
+        lines = [
+            f"# rocprofv3 kernel statistics, {what}, MI355X",
+            "# made by (from the repository root, TMPDIR=/tmp):",
+            "#   rocprofv3 --kernel-trace --stats -f csv -T -d P -o kt -- python -u bench.py "
+            f"--config {config} --steps {steps}",
+            f"#   python bench.py --stats-summary P/kt_kernel_stats.csv --config {config}",
+        ]
+    elif mcmc:
         lines = [
             "# rocprofv3 kernel statistics, MCMC densification on the config-4 parameters "
             "(1M Gaussians, 59 floats each, FusedAdam state), MI355X",
@@ -556,7 +712,8 @@ def main():
         print(pmc_summary(*args.pmc_summary, args.copy_mib or 1024))
         return
     if args.stats_summary:
-        print(stats_summary(args.stats_summary, 20, args.variant, args.mcmc))
+        print(stats_summary(args.stats_summary, args.steps if args.config else 20,
+                            args.variant, args.mcmc, args.config))
         return
     if args.cpu_only:
         print(json.dumps(cpu_baseline(args.gaussians, crop=_cpu_crop())))
@@ -568,6 +725,20 @@ def main():
         sys.exit(2)
     if args.copy_mib:
         copy_calibration(args.copy_mib)
+    if args.config is not None:
+        c = args.config
+        res = adam_config(args.steps) if c == 3 else render_config(c, min(args.steps, 50))
+        metric = {1: "forward ms at 10k Gaussians 256x256 SH0",
+                  2: "fwd+bwd ms at 300k Gaussians 800x800 SH3",
+                  3: "Adam ms per step over 1M Gaussians x 59 floats",
+                  5: "fwd+bwd ms at 3M Gaussians 1920x1080 SH3"}[c]
+        value = (res["fused"]["ms_per_step"] if c == 3 else
+                 res["fwd_ms"] if c == 1 else res["fwd_bwd_ms"])
+        print(json.dumps({"metric": metric, "value": value, "unit": "ms", "n_gpus": 1,
+                          "higher_is_better": False, "dtype": "f32", "data": "synthetic",
+                          "config": {"workload": f"BASELINE configs[{c - 1}] (config {c})"},
+                          "result": res}))
+        return
     if args.mcmc:
         print(json.dumps({
             "metric": "MCMC densification ms at 1M Gaussians (config-4 parameters + FusedAdam "

@@ -143,6 +143,133 @@ __device__ __forceinline__ int rec_walk(const BinRec &r, bool test, int tile, in
     return n;
 }
 
+// One tile's decision, with exactly the expressions rec_walk evaluates for it
+// (its shared edge minimisers are the same expressions of the same edge
+// lines), so a wave that splits a rectangle over its lanes decides every
+// tile as the walk does, bit for bit.
+__device__ __forceinline__ bool tile_claim(const BinRec &r, bool test, int tx, int ty, int tile,
+                                           int W, int H) {
+#pragma clang fp contract(off)
+    if (!test) return true;
+    const float mux = r.ux, muy = r.uy, a = r.a, b = r.b, c = r.c;
+    const float ry0 = (float)(ty * tile), ry1 = fminf((float)((ty + 1) * tile), (float)H);
+    const float rx0 = (float)(tx * tile), rx1 = fminf((float)((tx + 1) * tile), (float)W);
+    if (muy >= ry0 && muy <= ry1 && mux >= rx0 && mux <= rx1) return true;
+    const float u0 = mux - b * (ry0 - muy) / a;
+    const float u1 = mux - b * (ry1 - muy) / a;
+    const float v0 = muy - b * (rx0 - mux) / c;
+    const float v1 = muy - b * (rx1 - mux) / c;
+    const float ey0 = ry0 - muy, ey1 = ry1 - muy;
+    float ex = fminf(fmaxf(u0, rx0), rx1) - mux;
+    float best = a * ex * ex + 2.0f * b * ex * ey0 + c * ey0 * ey0;
+    ex = fminf(fmaxf(u1, rx0), rx1) - mux;
+    best = fminf(best, a * ex * ex + 2.0f * b * ex * ey1 + c * ey1 * ey1);
+    float ey = fminf(fmaxf(v0, ry0), ry1) - muy;
+    ex = rx0 - mux;
+    best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
+    ey = fminf(fmaxf(v1, ry0), ry1) - muy;
+    ex = rx1 - mux;
+    best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
+    return best < r.thr;
+}
+
+// Rectangles larger than this many tiles are walked by a whole wave (64
+// tiles a step) instead of one thread: near-camera Gaussians can cover
+// thousands of tiles, and one thread walking them holds up its workgroup.
+constexpr int kWaveWalkArea = 32;
+
+// A wave's walk of one large rectangle. The edge minimisers of every row
+// boundary (u, h + 1 of them) and column boundary (v, w + 1) are computed
+// once into the wave's LDS slice, with the walk's own expressions, and each
+// lane then tests its tiles from them; lanes step through the row-major tile
+// order without integer division. Rectangles whose boundaries do not fit the
+// slice test each tile from scratch (tile_claim).
+constexpr int kEdgeSlots = 256;
+
+struct WaveWalk {
+    const BinRec *r;
+    const float *u, *v;     // LDS: row / column boundary minimisers, or null
+    int x0, y0, w, h;
+    bool test;
+    int tile, W, H;
+
+    __device__ __forceinline__ bool claim(int row, int col) const {
+#pragma clang fp contract(off)
+        if (!test) return true;
+        if (u == nullptr) return tile_claim(*r, true, x0 + col, y0 + row, tile, W, H);
+        const int tx = x0 + col, ty = y0 + row;
+        const float mux = r->ux, muy = r->uy, a = r->a, b = r->b, c = r->c;
+        const float ry0 = (float)(ty * tile), ry1 = fminf((float)((ty + 1) * tile), (float)H);
+        const float rx0 = (float)(tx * tile), rx1 = fminf((float)((tx + 1) * tile), (float)W);
+        if (muy >= ry0 && muy <= ry1 && mux >= rx0 && mux <= rx1) return true;
+        const float u0 = u[row], u1 = u[row + 1], v0 = v[col], v1 = v[col + 1];
+        const float ey0 = ry0 - muy, ey1 = ry1 - muy;
+        float ex = fminf(fmaxf(u0, rx0), rx1) - mux;
+        float best = a * ex * ex + 2.0f * b * ex * ey0 + c * ey0 * ey0;
+        ex = fminf(fmaxf(u1, rx0), rx1) - mux;
+        best = fminf(best, a * ex * ex + 2.0f * b * ex * ey1 + c * ey1 * ey1);
+        float ey = fminf(fmaxf(v0, ry0), ry1) - muy;
+        ex = rx0 - mux;
+        best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
+        ey = fminf(fmaxf(v1, ry0), ry1) - muy;
+        ex = rx1 - mux;
+        best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
+        return best < r->thr;
+    }
+};
+
+// Fills the wave's edge slice for rectangle r (all 64 lanes call it) and
+// returns the walk.
+__device__ __forceinline__ WaveWalk wave_walk_setup(const BinRec &r, bool test, int tile, int W,
+                                                    int H, float *slice, int lane) {
+#pragma clang fp contract(off)
+    WaveWalk k;
+    k.r = &r;
+    k.x0 = (int)(r.xs & 0xffffu);
+    k.y0 = (int)(r.ys & 0xffffu);
+    k.w = (int)(r.xs >> 16) - k.x0 + 1;
+    k.h = (int)(r.ys >> 16) - k.y0 + 1;
+    k.test = test;
+    k.tile = tile;
+    k.W = W;
+    k.H = H;
+    k.u = k.v = nullptr;
+    if (test && k.h + 1 + k.w + 1 <= kEdgeSlots) {
+        const float mux = r.ux, muy = r.uy, a = r.a, b = r.b, c = r.c;
+        for (int i = lane; i <= k.h; i += 64) {
+            // Row boundary of row y0 + i: its top edge; the last is the
+            // bottom of row y1, clamped to the image as the walk clamps it.
+            const int ty = k.y0 + i;
+            const float ry = i == 0 ? (float)(ty * tile) : fminf((float)(ty * tile), (float)H);
+            slice[i] = mux - b * (ry - muy) / a;
+        }
+        for (int j = lane; j <= k.w; j += 64) {
+            const int tx = k.x0 + j;
+            const float rx = j == 0 ? (float)(tx * tile) : fminf((float)(tx * tile), (float)W);
+            slice[k.h + 1 + j] = muy - b * (rx - mux) / c;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        k.u = slice;
+        k.v = slice + k.h + 1;
+    }
+    return k;
+}
+
+__device__ __forceinline__ int rec_area(const BinRec &r) {
+    return ((int)(r.xs >> 16) - (int)(r.xs & 0xffffu) + 1) *
+           ((int)(r.ys >> 16) - (int)(r.ys & 0xffffu) + 1);
+}
+
+// Tile t (row-major) of a rectangle of width w starting at (x0, y0).
+__device__ __forceinline__ void rect_tile(const BinRec &r, int t, int &tx, int &ty) {
+    const int x0 = (int)(r.xs & 0xffffu), y0 = (int)(r.ys & 0xffffu);
+    const int w = (int)(r.xs >> 16) - x0 + 1;
+    ty = y0 + t / w;
+    tx = x0 + t % w;
+}
+
 __global__ __launch_bounds__(kBinThreads) void bin_count_kernel(const BinArgs A, int32_t *counts) {
     const int64_t g = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
     if (g >= A.N) return;
@@ -334,16 +461,60 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
                                                                     uint32_t *dkeys,
                                                                     int32_t *perm, BinPart *parts) {
     __shared__ BinPart s_p[kBinThreads / 64];
-    const int64_t g = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
+    __shared__ BinRec s_rec[kBinThreads];
+    __shared__ int32_t s_big[kBinThreads], s_cnt[kBinThreads];
+    __shared__ int32_t s_nbig;
+    __shared__ float s_edge[kBinThreads / 64][kEdgeSlots];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t g = (int64_t)blockIdx.x * kBinThreads + tid;
+    const bool test = A.conic != nullptr;
+    if (tid == 0) s_nbig = 0;
+    __syncthreads();
     int n = 0;
-    uint32_t key = 0xFFFFFFFFu;
+    bool big = false;
     if (g < A.N) {
         BinRec r;
         if (make_rec(A, g, r)) {
-            n = rec_walk(r, A.conic != nullptr, A.tile, A.W, A.H, A.tiles_x,
-                         [](int, uint32_t) {});
             recs[g] = r;
+            if (rec_area(r) > kWaveWalkArea) {
+                big = true;
+                s_rec[tid] = r;
+            } else {
+                n = rec_walk(r, test, A.tile, A.W, A.H, A.tiles_x, [](int, uint32_t) {});
+            }
         }
+    }
+    // Large rectangles: compacted in LDS, one wave each.
+    const uint64_t m = ballot(big);
+    int at = 0;
+    if (lane == 0 && m) at = atomicAdd(&s_nbig, __popcll(m));
+    at = __shfl(at, 0, 64);
+    if (big) s_big[at + rank_in(m)] = tid;
+    __syncthreads();
+    for (int e = wave; e < s_nbig; e += kBinThreads / 64) {
+        const int j = s_big[e];
+        const BinRec r = s_rec[j];
+        const WaveWalk k = wave_walk_setup(r, test, A.tile, A.W, A.H, s_edge[wave], lane);
+        const int area = k.w * k.h;
+        // Lane l starts at tile l of the row-major order and steps by 64.
+        int row = lane / k.w, col = lane % k.w;
+        const int drow = 64 / k.w, dcol = 64 % k.w;
+        int cnt = 0;
+        for (int t = lane; t < area; t += 64) {
+            cnt += k.claim(row, col) ? 1 : 0;
+            row += drow;
+            col += dcol;
+            if (col >= k.w) { col -= k.w; ++row; }
+        }
+        for (int o = 32; o >= 1; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
+        if (lane == 0) s_cnt[j] = cnt;
+        // The slice is rewritten for the wave's next rectangle.
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    uint32_t key = 0xFFFFFFFFu;
+    if (g < A.N) {
+        if (big) n = s_cnt[tid];
         if (n > 0) key = __float_as_uint(A.depth[g]);
         counts[g] = n;
         dkeys[g] = key;
@@ -406,53 +577,124 @@ __global__ __launch_bounds__(256) void bin_stats_kernel(const BinPart *parts, in
 constexpr int kBinStage = 2048;
 
 // Thread k emits the pairs of the k-th Gaussian in depth order (tile id key,
-// Gaussian id) at the scanned offset of position k. The workgroup's 256
-// Gaussians own one contiguous output range; when it fits in LDS the pairs
-// are assembled there and stored with consecutive lanes on consecutive
-// addresses, otherwise each thread stores its own run.
+// Gaussian id) at the scanned offset of position k; the workgroup's 256
+// Gaussians own one contiguous output range.
+//   * Small rectangles (walked by their own thread) go through LDS: their
+//     runs are numbered by a workgroup prefix scan of their counts (at most
+//     256 x 32 pairs) and staged in windows of kBinStage slots, each slot
+//     with its position in the range, then stored by consecutive lanes, so
+//     adjacent runs land as coalesced stores.
+//   * Large rectangles (more than kWaveWalkArea tiles) are walked by a wave,
+//     64 tiles a step in row-major order; the claimed tiles of a step take
+//     consecutive positions by lane rank (the walk's emission order), and
+//     the wave stores them directly, consecutive lanes on consecutive
+//     addresses.
 __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
     const BinRec *recs, const int32_t *order, const int32_t *offsets, int64_t N, int64_t total,
     int tile, int W, int H, int tiles_x, int test, uint32_t *tkeys, int32_t *ids) {
     __shared__ uint32_t s_k[kBinStage];
     __shared__ int32_t s_i[kBinStage];
+    __shared__ int32_t s_off[kBinStage];
+    __shared__ BinRec s_rec[kBinThreads];
+    __shared__ int32_t s_big[kBinThreads], s_g[kBinThreads];
+    __shared__ int32_t s_nbig, s_wsum[kBinThreads / 64];
+    __shared__ float s_edge[kBinThreads / 64][kEdgeSlots];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t k0 = (int64_t)blockIdx.x * kBinThreads;
-    const int64_t k = k0 + threadIdx.x;
-    const int64_t kend = min(k0 + kBinThreads, N);
+    const int64_t k = k0 + tid;
     const int64_t base = offsets[k0];
-    const int64_t stop = kend < N ? (int64_t)offsets[kend] : total;
-    const bool staged = stop - base <= kBinStage;    // uniform over the workgroup
+    if (tid == 0) s_nbig = 0;
+    __syncthreads();
+    bool big = false;
+    int small_cap = 0;        // pairs this thread stages (0 unless a small rectangle)
+    int64_t at = 0;
+    int32_t g = 0;
+    BinRec r{};
     if (k < N) {
-        const int64_t at = offsets[k];
+        at = offsets[k];
         const int64_t nxt = k + 1 < N ? (int64_t)offsets[k + 1] : total;
         const int cap = (int)(nxt - at);
         if (cap > 0) {
-            const int32_t g = order[k];
-            const BinRec r = recs[g];
-            if (staged) {
-                const int o = (int)(at - base);
-                rec_walk(r, test != 0, tile, W, H, tiles_x, [&](int n, uint32_t t) {
-                    if (n < cap) {
-                        s_k[o + n] = t;
-                        s_i[o + n] = g;
-                    }
-                });
+            g = order[k];
+            r = recs[g];
+            if (rec_area(r) > kWaveWalkArea) {
+                big = true;
+                s_rec[tid] = r;
+                s_g[tid] = g;
             } else {
-                rec_walk(r, test != 0, tile, W, H, tiles_x, [&](int n, uint32_t t) {
-                    if (n < cap) {
-                        tkeys[at + n] = t;
-                        ids[at + n] = g;
-                    }
-                });
+                small_cap = cap;
             }
         }
     }
-    if (staged) {
-        __syncthreads();
-        const int cnt = (int)(stop - base);
-        for (int i = threadIdx.x; i < cnt; i += kBinThreads) {
-            tkeys[base + i] = s_k[i];
-            ids[base + i] = s_i[i];
+    // Big rectangles, compacted; small runs, numbered (exclusive scan).
+    const uint64_t m = ballot(big);
+    int slot = 0;
+    if (lane == 0 && m) slot = atomicAdd(&s_nbig, __popcll(m));
+    slot = __shfl(slot, 0, 64);
+    if (big) s_big[slot + rank_in(m)] = tid;
+    int incl = small_cap;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
+    }
+    if (lane == 63) s_wsum[wave] = incl;
+    __syncthreads();
+    int first = incl - small_cap, n_small = 0;
+    for (int w = 0; w < kBinThreads / 64; ++w) {
+        if (w < wave) first += s_wsum[w];
+        n_small += s_wsum[w];
+    }
+    // Large rectangles: direct stores.
+    for (int e = wave; e < s_nbig; e += kBinThreads / 64) {
+        const int j = s_big[e];
+        const BinRec rb = s_rec[j];
+        const int32_t gb = s_g[j];
+        const int64_t kj = k0 + j;
+        const int64_t atb = offsets[kj];
+        const int64_t nxt = kj + 1 < N ? (int64_t)offsets[kj + 1] : total;
+        const int cap = (int)(nxt - atb);
+        const WaveWalk wk = wave_walk_setup(rb, test != 0, tile, W, H, s_edge[wave], lane);
+        const int area = wk.w * wk.h;
+        int row = lane / wk.w, col = lane % wk.w;
+        const int drow = 64 / wk.w, dcol = 64 % wk.w;
+        int emitted = 0;
+        for (int t0 = 0; t0 < area; t0 += 64) {
+            const bool claim = t0 + lane < area && wk.claim(row, col);
+            const int tx = wk.x0 + col, ty = wk.y0 + row;
+            row += drow;
+            col += dcol;
+            if (col >= wk.w) { col -= wk.w; ++row; }
+            const uint64_t cm = ballot(claim);
+            const int pos = emitted + rank_in(cm);
+            if (claim && pos < cap) {
+                tkeys[atb + pos] = (uint32_t)(ty * tiles_x + tx);
+                ids[atb + pos] = gb;
+            }
+            emitted += __popcll(cm);
         }
+        __builtin_amdgcn_wave_barrier();
+    }
+    // Small rectangles: LDS windows over the numbered runs.
+    const int off0 = (int)(at - base);
+    for (int w0 = 0; w0 < n_small; w0 += kBinStage) {
+        const int w1 = min(w0 + kBinStage, n_small);
+        if (small_cap > 0 && first < w1 && first + small_cap > w0) {
+            rec_walk(r, test != 0, tile, W, H, tiles_x, [&](int n, uint32_t t) {
+                const int sl = first + n;
+                if (n < small_cap && sl >= w0 && sl < w1) {
+                    s_k[sl - w0] = t;
+                    s_i[sl - w0] = g;
+                    s_off[sl - w0] = off0 + n;
+                }
+            });
+        }
+        __syncthreads();
+        for (int i = tid; i < w1 - w0; i += kBinThreads) {
+            const int64_t pos = base + s_off[i];
+            tkeys[pos] = s_k[i];
+            ids[pos] = s_i[i];
+        }
+        __syncthreads();
     }
 }
 

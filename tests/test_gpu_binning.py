@@ -79,6 +79,28 @@ def test_tile_lists_bit_exact(dev, tile):
     assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
 
 
+@pytest.mark.parametrize("tile", [8, 16])
+@pytest.mark.parametrize("ellipse", [True, False])
+def test_large_rectangles_bit_exact(dev, tile, ellipse):
+    """Near, wide splats whose rectangles span tens to hundreds of tiles take
+    the wave-parallel walk (more than 32 tiles); mixed with small ones, the
+    lists must still equal the oracle's, emission order included."""
+    s = ref_scene(N=6000, seed=11)
+    g = torch.Generator().manual_seed(12)
+    k = 600
+    s["means"][:k, 2] = torch.rand(k, generator=g) * 1.5 + 1.2
+    s["scales"][:k] = torch.rand(k, 3, generator=g) * 0.3 + 0.02
+    gpu, ref = run_both(s, dev, tile, ellipse=ellipse)
+    uv, conic, depth, rxy, valid, _ = gpu_preprocess(s, dev)
+    rxy = rxy.cpu().numpy()
+    big = ((2 * rxy[:, 0] / tile + 1) * (2 * rxy[:, 1] / tile + 1) > 32) & \
+        (valid.cpu().numpy() != 0)
+    assert big.sum() > 100, big.sum()
+    assert np.array_equal(gpu[3], ref[3]), "sorted keys differ"
+    assert np.array_equal(gpu[0], ref[0]), "gauss_ids differ"
+    assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
+
+
 def test_rect_only_lists_bit_exact_and_longer(dev):
     s = ref_scene(seed=3)
     gpu_r, ref_r = run_both(s, dev, 16, ellipse=False)
