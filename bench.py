@@ -71,6 +71,9 @@ def parse():
                     help="time another BASELINE configuration instead of the config-4 step: "
                          "1 forward at 10k/256^2; 2 fwd+bwd at 300k/800^2; 3 FusedAdam and "
                          "SelectiveAdam over 1M Gaussians; 5 fwd+bwd at 3M/1920x1080")
+    ap.add_argument("--render-fps", action="store_true",
+                    help="forward-only frames per second at the reference's published points "
+                         "(bench/render_fps.py, README.md:145-148)")
     ap.add_argument("--mcmc", action="store_true",
                     help="time the MCMC densification kernels (add_noise, relocate, grow) on the "
                          "config-4 parameters instead of the step")
@@ -426,6 +429,54 @@ def render_config(which, reps):
     return out
 
 
+# The reference's published forward-only rates on an Apple M5 (README.md:145-148,
+# bench/results/render_fps.json): (splats, resolution) -> frames per second.
+REF_FPS = {(100_000, 256): 508.2, (100_000, 384): 481.3, (100_000, 512): 377.0,
+           (100_000, 768): 256.5, (600_000, 512): 91.0, (600_000, 768): 69.0}
+
+
+def render_fps(ramp_s=1.0, k=21):
+    """Forward-only render rate, timed like bench/render_fps.py:30-44: a ramp
+    of continuous frames, then the median of k synchronised frames (trimmed),
+    with a constant black background and no autograd."""
+    import torch
+
+    from metal_gauss_amd import render, scenes
+
+    dev = torch.device("cuda:0")
+    rows = []
+    for n in (100_000, 300_000, 600_000):
+        sc = scenes.fps_scene(n).to(dev)
+        m, q, sca, op, sh = sc.activated()
+        for res in (256, 384, 512, 768):
+            K = scenes.intrinsics(res, res, 45.0)
+            vm = torch.eye(4)
+
+            def frame():
+                return render(m, q, sca, op, sh, K, vm, res, res, sh_degree=3)
+
+            with torch.no_grad():
+                end = time.perf_counter() + ramp_s
+                while time.perf_counter() < end:
+                    frame()
+                torch.cuda.synchronize()
+                ts = []
+                for _ in range(k):
+                    t0 = time.perf_counter()
+                    _, _, info = frame()
+                    torch.cuda.synchronize()
+                    ts.append(time.perf_counter() - t0)
+            ts.sort()
+            ms = 1e3 * float(sum(ts[1:-1]) / len(ts[1:-1])) if k > 2 else 1e3 * ts[0]
+            med = 1e3 * ts[len(ts) // 2]
+            row = {"splats": n, "res": res, "ms": round(med, 4), "fps": round(1e3 / med, 1),
+                   "trimmed_mean_ms": round(ms, 4), "intersections": info["isect_total"]}
+            if (n, res) in REF_FPS:
+                row["reference_m5_fps"] = REF_FPS[(n, res)]
+            rows.append(row)
+    return rows
+
+
 def adam_config(reps):
     """Config 3: 1M Gaussians x 59 floats in the six
     trainer groups, gradients N(0, 1e-3); FusedAdam one step then 100 steps,
@@ -725,6 +776,17 @@ def main():
         sys.exit(2)
     if args.copy_mib:
         copy_calibration(args.copy_mib)
+    if args.render_fps:
+        rows = render_fps()
+        head = next(r for r in rows if r["splats"] == 600_000 and r["res"] == 768)
+        print(json.dumps({"metric": "forward-only render frames/s (600k Gaussians SH3, 768^2)",
+                          "value": head["fps"], "unit": "frames/s", "n_gpus": 1,
+                          "higher_is_better": True, "dtype": "f32",
+                          "data": "synthetic (seeded frustum scene; the reference renders a ply)",
+                          "config": {"workload": "forward-only render, fixed view, fov 45 deg"},
+                          "vs_reference_m5": round(head["fps"] / REF_FPS[(600_000, 768)], 2),
+                          "rows": rows}))
+        return
     if args.config is not None:
         c = args.config
         res = adam_config(args.steps) if c == 3 else render_config(c, min(args.steps, 50))

@@ -1,17 +1,20 @@
-// Stable LSD radix sort of (key, int32 value) pairs, 8-bit digits.
+// Stable LSD radix sort of (key, int32 value) pairs, 8-bit digits, tiles of
+// 1024 to 4096 keys (large sorts use 4096, so a tile's run of one digit
+// averages 16 keys: 64-byte stores).
 //
 // Each pass is reduce-then-scan, with no inter-workgroup waiting:
-//   1. upsweep   - every workgroup histograms the digit of its 2048-key tile;
+//   1. upsweep   - every workgroup histograms the digit of its tile;
 //   2. scan      - one workgroup per digit scans that digit's counts over the
 //                  tiles (digit-major layout), leaving each tile's base;
-//   3. downsweep - every workgroup ranks its keys stably (wave ballots give
-//                  the rank among equal digits inside a wave; LDS counters
-//                  carry ranks across waves and rounds), sorts the tile
-//                  locally in LDS by digit, and writes each digit's run to
-//                  its global slot so stores come out as contiguous runs.
-// Stability holds because items are ranked in their input order: round r,
-// wave w, lane l is item r*256 + w*64 + l of the tile, and tiles are ranked
-// in tile order by the scan.
+//   3. downsweep - every workgroup ranks its keys stably (each wave ranks its
+//                  own contiguous chunk with ballots against a wave-private
+//                  LDS histogram; a prefix over the waves joins them), sorts
+//                  the tile locally in LDS by digit, and writes each digit's
+//                  run to its global slot so stores come out as contiguous
+//                  runs.
+// Stability holds because items are ranked in their input order (wave w,
+// round r, lane l is item c w + 64 r + l of the tile, c the keys per wave),
+// and tiles are ranked in tile order by the scan.
 //
 // Digits are taken from min(key, hi) - lo. With lo/hi the smallest and
 // largest key that matters, this order-preserving shift lets a caller sort
@@ -23,9 +26,19 @@
 namespace mg {
 
 constexpr int kSortThreads = 256;
-constexpr int kSortItems = 8;
-constexpr int kSortTile = kSortThreads * kSortItems;   // 2048 keys per tile
+// Keys per thread: 4, 8 or 16 (tiles of 1024, 2048 or 4096 keys). Large
+// sorts (from ~4M keys) take 4096-key tiles for long digit runs; mid-sized
+// ones (from ~256k) 2048, small ones 1024 to spread over the CUs. Measured
+// at config 4: the 1M-key depth sort is fastest at 2048 (67 vs 74 us at 1024
+// and 80 at 4096), the 5M-pair tile sort at 4096 (102 vs 109 at 2048).
+constexpr int kSortTileMin = kSortThreads * 4;
 constexpr int kRadix = 256;
+
+inline int sort_items_for(int64_t n) {
+    if (n >= (int64_t)kSortThreads * 16 * 1024) return 16;
+    if (n >= (int64_t)kSortThreads * 8 * 128) return 8;
+    return 4;
+}
 constexpr int kSortWaves = kSortThreads / 64;
 
 template <typename K>
@@ -38,7 +51,7 @@ __device__ __forceinline__ uint32_t digit_of(K key, int shift, uint32_t mask, Ke
     return (uint32_t)(((key < w.hi ? key : w.hi) - w.lo) >> shift) & mask;
 }
 
-template <typename K>
+template <typename K, int kSortItems>
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const K *keys, int64_t n,
                                                                      int shift, uint32_t mask,
                                                                      KeyWin<K> win, uint32_t *hist,
@@ -47,6 +60,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const K *ke
     const int wave = threadIdx.x >> 6;
     for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads) (&s_h[0][0])[i] = 0;
     __syncthreads();
+    constexpr int kSortTile = kSortThreads * kSortItems;
     const int64_t base = (int64_t)blockIdx.x * kSortTile;
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
@@ -93,22 +107,38 @@ __global__ __launch_bounds__(kSortThreads) void radix_scan_kernel(uint32_t *hist
     if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
-template <typename K>
+// Downsweep: rank the tile's keys stably by digit, sort the tile in LDS,
+// store each digit's run at its global slot.
+//
+// Wave w owns the contiguous chunk [c w, c w + c) of the tile (c = 64 x keys
+// per thread), loaded in rounds of 64 consecutive keys. Within a round, lanes holding the same
+// digit find each other with one ballot per live digit bit; the lowest such
+// lane adds the group's size to the wave's own LDS digit histogram, which
+// every lane of the group read first, so an item's rank within its wave is
+// (earlier rounds' count of its digit) + (earlier lanes of its group). No
+// workgroup barrier is needed while ranking. Afterwards each digit's wave
+// counts become an exclusive prefix over the waves, and the tile's digit
+// starts an exclusive scan over digits; position in the tile = digit start
+// + wave prefix + rank in wave. Items are thus ranked in tile order (wave,
+// round, lane), which makes every pass stable.
+template <typename K, int kSortItems>
 __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     const K *keys_in, const int32_t *vals_in, K *keys_out, int32_t *vals_out, int64_t n,
     int shift, uint32_t mask, KeyWin<K> win, const uint32_t *hist, int64_t ntiles,
     const uint32_t *totals) {
+    constexpr int kSortTile = kSortThreads * kSortItems;
+    constexpr int kChunk = kSortTile / kSortWaves;       // keys per wave
     __shared__ K s_keys[kSortTile];
     __shared__ int32_t s_vals[kSortTile];
     __shared__ uint32_t s_base[kRadix];     // global slot of this tile's digit run
     __shared__ uint32_t s_loc[kRadix];      // start of each digit inside the tile
-    __shared__ uint32_t s_run[kRadix];      // items of each digit ranked so far
-    __shared__ uint32_t s_wc[kSortWaves][kRadix];  // (round+1) << 16 | count
+    __shared__ uint32_t s_wh[kSortWaves][kRadix];   // per-wave digit counts
     __shared__ uint32_t s_w[kSortWaves];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t base = (int64_t)blockIdx.x * kSortTile;
     const int nitems = (int)min((int64_t)kSortTile, n - base);
+    const int nbits = 32 - __builtin_clz(mask);          // live digit bits (mask = 2^b - 1)
 
     // Global digit bases: exclusive scan of the digit totals (one digit per
     // thread), plus this tile's exclusive prefix within the digit.
@@ -123,19 +153,18 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
         __syncthreads();
         uint32_t before = 0;
         for (int w = 0; w < wave; ++w) before += s_w[w];
-        if (tid < kRadix) {
+        if (tid < kRadix)
             s_base[tid] = before + incl - v + hist[(int64_t)tid * ntiles + blockIdx.x];
-            s_run[tid] = 0;
-        }
-        for (int i = tid; i < kSortWaves * kRadix; i += kSortThreads) (&s_wc[0][0])[i] = 0;
     }
+    for (int i = lane; i < kRadix; i += 64) s_wh[wave][i] = 0;
 
     K key[kSortItems];
     int32_t val[kSortItems];
     uint32_t rank[kSortItems];
+    const int c0 = wave * kChunk;
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
-        const int idx = r * kSortThreads + tid;
+        const int idx = c0 + r * 64 + lane;
         if (idx < nitems) {
             key[r] = keys_in[base + idx];
             val[r] = vals_in[base + idx];
@@ -144,65 +173,65 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
             val[r] = 0;
         }
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    uint32_t *wh = s_wh[wave];
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
-        const bool ok = r * kSortThreads + tid < nitems;
+        const bool ok = c0 + r * 64 + lane < nitems;
         const uint32_t d = digit_of(key[r], shift, mask, win);
-        // Lanes of this wave holding the same digit.
         uint64_t peers = ballot(ok);
-        for (int b = 0; b < 8; ++b) {
+        for (int b = 0; b < nbits; ++b) {
             const bool bit = (d >> b) & 1u;
             const uint64_t m = ballot(bit);
             peers &= bit ? m : ~m;
         }
         const uint32_t wrank = (uint32_t)__popcll(peers & lt_mask);
-        const uint32_t tag = (uint32_t)(r + 1) << 16;
-        if (ok && wrank == 0) s_wc[wave][d] = tag | (uint32_t)__popcll(peers);
-        __syncthreads();
-        if (ok) {
-            uint32_t before = s_run[d];
-            for (int w = 0; w < wave; ++w) {
-                const uint32_t e = s_wc[w][d];
-                if ((e & 0xffff0000u) == tag) before += e & 0xffffu;
-            }
-            rank[r] = before + wrank;
-        }
-        __syncthreads();
-        for (int dd = tid; dd < kRadix; dd += kSortThreads) {
-            uint32_t add = 0;
+        const uint32_t prior = ok ? wh[d] : 0u;
+        rank[r] = prior + wrank;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (ok && wrank == 0) wh[d] = prior + (uint32_t)__popcll(peers);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    __syncthreads();
+
+    // Per digit: wave counts -> exclusive prefix over the waves; the tile's
+    // digit count, scanned over digits, gives the digit starts.
+    {
+        uint32_t cnt = 0;
+        if (tid < kRadix) {
 #pragma unroll
             for (int w = 0; w < kSortWaves; ++w) {
-                const uint32_t e = s_wc[w][dd];
-                if ((e & 0xffff0000u) == tag) add += e & 0xffffu;
+                const uint32_t t = s_wh[w][tid];
+                s_wh[w][tid] = cnt;
+                cnt += t;
             }
-            s_run[dd] += add;
         }
-        __syncthreads();
-    }
-
-    // Local digit starts: exclusive scan of the tile's digit counts.
-    {
-        const uint32_t v = tid < kRadix ? s_run[tid] : 0u;
-        uint32_t incl = v;
+        uint32_t incl = cnt;
         for (int o = 1; o < 64; o <<= 1) {
             const uint32_t t = __shfl_up(incl, o, 64);
             if (lane >= o) incl += t;
         }
+        __syncthreads();                     // s_w is reused
         if (lane == 63) s_w[wave] = incl;
         __syncthreads();
         uint32_t before = 0;
         for (int w = 0; w < wave; ++w) before += s_w[w];
-        if (tid < kRadix) s_loc[tid] = before + incl - v;
+        if (tid < kRadix) s_loc[tid] = before + incl - cnt;
         __syncthreads();
     }
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
-        if (r * kSortThreads + tid < nitems) {
+        if (c0 + r * 64 + lane < nitems) {
             const uint32_t d = digit_of(key[r], shift, mask, win);
-            const uint32_t lp = s_loc[d] + rank[r];
+            const uint32_t lp = s_loc[d] + s_wh[wave][d] + rank[r];
             if (lp < (uint32_t)kSortTile) {
                 s_keys[lp] = key[r];
                 s_vals[lp] = val[r];
@@ -221,9 +250,10 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     }
 }
 
-// Workspace: hist (kRadix * ntiles) + totals (kRadix), uint32.
+// Workspace: hist (kRadix * ntiles) + totals (kRadix), uint32, sized for the
+// smallest tile.
 int64_t sort_ws_bytes(int64_t n) {
-    const int64_t ntiles = ceil_div(n > 0 ? n : 1, kSortTile);
+    const int64_t ntiles = ceil_div(n > 0 ? n : 1, kSortTileMin);
     return (kRadix * ntiles + kRadix) * (int64_t)sizeof(uint32_t);
 }
 
@@ -243,7 +273,8 @@ int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *va
     *res_v = vals_in;
     if (n == 0) return MG_OK;
     MG_REQUIRE(keys_in && vals_in && keys_out && vals_out, "%s: null buffer", who);
-    const int64_t ntiles = ceil_div(n, kSortTile);
+    const int items = sort_items_for(n);
+    const int64_t ntiles = ceil_div(n, (int64_t)kSortThreads * items);
     uint32_t *hist = static_cast<uint32_t *>(ws);
     uint32_t *totals = hist + kRadix * ntiles;
     K *src_k = keys_in, *dst_k = keys_out;
@@ -254,14 +285,19 @@ int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *va
     for (int b = begin_bit; b < end_bit; b += 8) {
         const int width = min(8, end_bit - b);
         const uint32_t mask = (1u << width) - 1u;
-        radix_upsweep_kernel<K><<<(unsigned)ntiles, kSortThreads, 0, s>>>(src_k, n, b, mask, win,
-                                                                         hist, ntiles);
-        MG_LAUNCHED("radix_upsweep_kernel");
-        radix_scan_kernel<<<kRadix, kSortThreads, 0, s>>>(hist, ntiles, totals);
-        MG_LAUNCHED("radix_scan_kernel");
-        radix_downsweep_kernel<K><<<(unsigned)ntiles, kSortThreads, 0, s>>>(
-            src_k, src_v, dst_k, dst_v, n, b, mask, win, hist, ntiles, totals);
-        MG_LAUNCHED("radix_downsweep_kernel");
+#define MG_SORT_PASS(IT)                                                                   \
+    radix_upsweep_kernel<K, IT><<<(unsigned)ntiles, kSortThreads, 0, s>>>(src_k, n, b, mask, \
+                                                                          win, hist, ntiles); \
+    MG_LAUNCHED("radix_upsweep_kernel");                                                   \
+    radix_scan_kernel<<<kRadix, kSortThreads, 0, s>>>(hist, ntiles, totals);               \
+    MG_LAUNCHED("radix_scan_kernel");                                                      \
+    radix_downsweep_kernel<K, IT><<<(unsigned)ntiles, kSortThreads, 0, s>>>(               \
+        src_k, src_v, dst_k, dst_v, n, b, mask, win, hist, ntiles, totals);                \
+    MG_LAUNCHED("radix_downsweep_kernel");
+        if (items == 16) { MG_SORT_PASS(16) }
+        else if (items == 8) { MG_SORT_PASS(8) }
+        else { MG_SORT_PASS(4) }
+#undef MG_SORT_PASS
         K *tk = src_k; src_k = dst_k; dst_k = tk;
         int32_t *tv = src_v; src_v = dst_v; dst_v = tv;
     }

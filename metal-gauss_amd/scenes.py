@@ -164,6 +164,24 @@ def config4_target(view: int, H=800, W=800):
     return t[0].permute(1, 2, 0).contiguous()
 
 
+def fps_scene(n, seed=7):
+    """Forward-only render workload (the reference's bench/render_fps.py renders a
+    loaded ply from one fixed view; this is a seeded stand-in of the same
+    size): n Gaussians with SH 3 filling the view frustum of a camera at the
+    origin looking down +z (identity world->camera), depths U[1.5, 6],
+    log-scales N(-4.5, 0.5), opacity logits N(0, 1.5)."""
+    g = torch.Generator().manual_seed(seed)
+    z = torch.rand(n, generator=g) * 4.5 + 1.5
+    xy = (torch.rand(n, 2, generator=g) * 2.0 - 1.0) * 0.45 * z[:, None]
+    means = torch.cat([xy, z[:, None]], dim=1)
+    log_scales = torch.randn(n, 3, generator=g) * 0.5 - 4.5
+    quats = torch.randn(n, 4, generator=g)
+    logit = torch.randn(n, generator=g) * 1.5
+    dc = torch.randn(n, 1, 3, generator=g) * 0.3
+    rest = torch.randn(n, 15, 3, generator=g) * 0.05
+    return Scene(means, log_scales, quats, logit, dc, rest, 3)
+
+
 def config5(n=3_000_000):
     s = _scene(n, 4, -2.0, 2.0, -5.0, 0.7, 0.5, 1.5, 3, heavy_tail=True)
     cam = Camera(intrinsics(1920, 1080, 60.0, horizontal=True),

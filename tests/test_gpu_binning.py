@@ -188,6 +188,14 @@ def test_config2_scale_bit_exact(dev):
 
 # ------------------------------------------------------------- primitives
 
+@pytest.mark.parametrize("n,bits", [(2_500_001, (0, 44)), (5_000_003, (0, 44)),
+                                    (5_000_003, (8, 20))])
+def test_radix_sort_large_tiles(dev, n, bits):
+    """Sizes that take the 2048- and 4096-key tiles (the small ones above
+    take 1024)."""
+    test_radix_sort_is_stable_and_exact(dev, n, bits)
+
+
 @pytest.mark.parametrize("n", [1, 7, 2047, 2048, 2049, 100_003])
 @pytest.mark.parametrize("bits", [(0, 44), (0, 40), (0, 64), (8, 20)])
 def test_radix_sort_is_stable_and_exact(dev, n, bits):

@@ -273,3 +273,31 @@ def test_chunked_backward_matches_single_chain(dev):
     for k in grads[0][1]:
         e = rel_l2(grads[1][1][k].cpu(), grads[0][1][k].cpu())
         assert e < 1e-4, (k, e)
+
+
+@pytest.mark.parametrize("use_sh", [False, True])
+def test_preview_renders_exactly_what_training_renders(dev, use_sh):
+    """tests/test_trainer.py:410-439: a forward-only render (no autograd, as
+    the viewer and the video renderer call it) gives the same pixels, bit for
+    bit, as the training render, here with the Mip 3D filter, antialias and a
+    white background all on."""
+    from metal_gauss_amd import render
+
+    W, H = 128, 96
+    s = scene(n=3000, seed=5, scale=(0.004, 0.05))
+    g = torch.Generator().manual_seed(6)
+    f3d = (torch.rand(3000, generator=g) * 0.01).to(dev)
+    K = intrinsics(W, H)
+    vm = torch.eye(4)
+    names = ["means", "quats", "scales", "opacities"] + (["sh"] if use_sh else ["colors"])
+    leaves = {k: s[k].clone().to(dev).requires_grad_(True) for k in names}
+    kw = dict(antialias=True, filter_3d=f3d, background=(1.0, 1.0, 1.0))
+    trained, a_t, _ = render(leaves["means"], leaves["quats"], leaves["scales"],
+                             leaves["opacities"], leaves.get("sh"), K, vm, W, H,
+                             colors=leaves.get("colors"), **kw)
+    with torch.no_grad():
+        previewed, a_p, _ = render(*(leaves[k].detach() for k in names[:4]),
+                                   leaves["sh"].detach() if use_sh else None, K, vm, W, H,
+                                   colors=None if use_sh else leaves["colors"].detach(), **kw)
+    assert torch.equal(trained.detach(), previewed)
+    assert torch.equal(a_t.detach(), a_p)
