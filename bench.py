@@ -74,6 +74,9 @@ def parse():
     ap.add_argument("--render-fps", action="store_true",
                     help="forward-only frames per second at the reference's published points "
                          "(bench/render_fps.py, README.md:145-148)")
+    ap.add_argument("--ply", action="store_true",
+                    help="time writing and reading a 1M-Gaussian SH3 .ply (export_ply from the "
+                         "GPU, load_ply to the GPU and to the CPU)")
     ap.add_argument("--mcmc", action="store_true",
                     help="time the MCMC densification kernels (add_noise, relocate, grow) on the "
                          "config-4 parameters instead of the step")
@@ -429,6 +432,39 @@ def render_config(which, reps):
     return out
 
 
+def ply_bench(n=1_000_000):
+    """PLY I/O at config-4 size: export_ply of the trainer's parameters from the
+    GPU (one encode kernel, one copy to the host, one file write), load_ply to
+    the GPU (file read, one upload, one decode kernel) and to the CPU (numpy).
+    Files go to a temporary directory (page cache warm after the write)."""
+    import tempfile
+
+    import torch
+
+    from metal_gauss_amd import _lib, scenes
+    from metal_gauss_amd.io import export_ply, load_ply
+
+    dev = torch.device("cuda:0")
+    sc = scenes.config4(n)[0].to(dev)
+    p = {k: getattr(sc, k) for k in ("means", "log_scales", "quats", "logit_opac", "sh_dc",
+                                     "sh_rest")}
+    out = {}
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "scene.ply")
+        out["export_ms"] = round(_timed_ms(lambda: export_ply(p, path), 5, warm=1), 2)
+        size = os.path.getsize(path)
+        out["file_MB"] = round(size / 1e6, 1)
+        out["load_gpu_ms"] = round(_timed_ms(lambda: load_ply(path, device="cuda"), 5, warm=1), 2)
+        out["load_cpu_ms"] = round(_timed_ms(lambda: load_ply(path), 3, warm=1), 2)
+        k = _kernel_means(lambda: (export_ply(p, path), load_ply(path, device="cuda")), 3,
+                          ["ply_encode", "ply_decode"])
+        out["kernels"] = k
+        for name in ("ply_encode", "ply_decode"):
+            if name in k:
+                out[name + "_GBps"] = round(2 * size / (k[name]["ms"] * 1e-3) / 1e9, 1)
+    return out
+
+
 # The reference's published forward-only rates on an Apple M5 (README.md:145-148,
 # bench/results/render_fps.json): (splats, resolution) -> frames per second.
 REF_FPS = {(100_000, 256): 508.2, (100_000, 384): 481.3, (100_000, 512): 377.0,
@@ -776,6 +812,16 @@ def main():
         sys.exit(2)
     if args.copy_mib:
         copy_calibration(args.copy_mib)
+    if args.ply:
+        r = ply_bench(args.gaussians)
+        print(json.dumps({"metric": "PLY export + load ms at 1M Gaussians SH3",
+                          "value": round(r["export_ms"] + r["load_gpu_ms"], 2), "unit": "ms",
+                          "n_gpus": 1, "higher_is_better": False, "dtype": "f32",
+                          "data": "synthetic (config-4 parameters)",
+                          "config": {"workload": "export_ply from the GPU, load_ply to the GPU "
+                                                 "and to the CPU", "n_gaussians": args.gaussians},
+                          "result": r}))
+        return
     if args.render_fps:
         rows = render_fps()
         head = next(r for r in rows if r["splats"] == 600_000 and r["res"] == 768)

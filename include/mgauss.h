@@ -202,6 +202,34 @@ int32_t mg_mcmc_apply(int64_t n, const float *logit_opac, const float *weights,
                       const int32_t *widths, const int32_t *kinds,
                       mg_stream_t stream);
 
+/* -------------------------------------------------------------------- PLY */
+
+/* De-parameterise INRIA 3DGS .ply records on the device. Replaces the
+ * arithmetic of load_ply (metal_gauss/io.py:89-123; the reference parses the
+ * file with plyfile and computes in numpy). records: (n, stride) float32 as
+ * they lie in the file. columns: 14 + 3*per_channel column indices, in the
+ * order x y z rot_0..3 scale_0..2 opacity f_dc_0..2 f_rest_0..3P-1.
+ * Writes means (n,3), quats (n,4) normalised, scales (n,3) = exp, opacities
+ * (n,) = sigmoid, sh (n, 1+P, 3) (f_rest channel-major: f_rest_[c*P + b-1]
+ * is sh[:, b, c]). */
+int32_t mg_ply_decode(int64_t n, const float *records, int32_t stride,
+                      const int32_t *columns, int32_t per_channel, float *means,
+                      float *quats, float *scales, float *opacities, float *sh,
+                      mg_stream_t stream);
+
+/* Build INRIA records from the trainer's parameters. Replaces the arithmetic
+ * of export_ply (metal_gauss/train.py:582-624): pre-activation values as
+ * they are; SH from `sh` (n, sh_bases, 3) or from sh_dc (n,1,3) + sh_rest
+ * (n, sh_bases-1, 3); with filter_3d (n,) the Mip 3D filter baked into the
+ * log-scales and logit opacity. columns and per_channel as in
+ * mg_ply_decode; records: (n, stride) float32. */
+int32_t mg_ply_encode(int64_t n, const float *means, const float *quats,
+                      const float *log_scales, const float *logit_opac,
+                      const float *sh_dc, const float *sh_rest, const float *sh,
+                      int32_t sh_bases, const float *filter_3d, int32_t stride,
+                      const int32_t *columns, int32_t per_channel, float *records,
+                      mg_stream_t stream);
+
 /* ---------------------------------------------------------------- binning */
 
 /* Per-Gaussian count of tiles that pass the exact ellipse-vs-tile test

@@ -10,6 +10,8 @@ Public surface (names of the reference's modules):
     ssim, gaussian_kernel  the fused SSIM loss used by the training step
     compute_3d_filter,     mipfilter: Mip-Splatting's 3D filter (also folded
     apply_3d_filter        into render's projection kernel via filter_3d=)
+    mcmc                   relocate / grow / add_noise / reset_adam_state
+    io                     Splats, load_ply, save_ply, export_ply
 """
 
 from .api import BACKENDS, render  # noqa: F401

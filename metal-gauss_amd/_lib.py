@@ -58,6 +58,10 @@ _SIGNATURES = {
                                ctypes.POINTER(_f64), _vp]),
     "mg_mcmc_apply": (_i32, [_i64, _vp, _vp, _f32, _i32, _i32, _vp, _i64, _i64, _i64, _i64,
                              _u64, _i32, _pp, ctypes.POINTER(_i32), ctypes.POINTER(_i32), _vp]),
+    "mg_ply_decode": (_i32, [_i64, _vp, _i32, ctypes.POINTER(_i32), _i32, _vp, _vp, _vp, _vp,
+                             _vp, _vp]),
+    "mg_ply_encode": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32,
+                             ctypes.POINTER(_i32), _i32, _vp, _vp]),
     "mg_bin_count": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp,
                             _vp]),
     "mg_scan_workspace_bytes": (_i64, [_i64]),

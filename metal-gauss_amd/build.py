@@ -23,7 +23,7 @@ LIB = PKG / "libmgauss.so"
 ARCH = "gfx950"
 
 SOURCES = ["runtime.hip", "adam.hip", "preprocess.hip", "mip.hip", "mcmc.hip", "binning.hip", "sort.hip",
-           "rasterize.hip", "ssim.hip"]
+           "rasterize.hip", "ssim.hip", "ply.hip"]
 
 # -packed-fp32-ops keeps the compiler from emitting packed fp32 VALU forms;
 # hardware float atomics are requested explicitly (the gradient buffers are
