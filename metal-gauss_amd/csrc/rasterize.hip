@@ -20,12 +20,20 @@
 // Backward (rasterize.metal:173-340 contract): back to front from the
 //   largest stop index of the wave, T recovered by dividing out (1 - alpha),
 //   colour/alpha suffix sums, gradients to colour, uv, conic and opacity.
-//   The 9 (10 with absgrad) per-Gaussian sums are reduced across the 64
-//   lanes with DPP and added into a per-batch LDS accumulator (LDS float
-//   atomics: several waves may hold the same Gaussian); after the batch one
-//   thread per Gaussian issues the global float atomics. Global atomics go
-//   to a coherence point shared by all XCDs and cost HBM write traffic, so
-//   there is one set per (Gaussian, tile) rather than per (Gaussian, wave).
+//   Per pixel the backward keeps T and one running scalar, the suffix sum
+//   of the output gradient dotted with the colour composited behind,
+//   G = gr sr + gg sg + gb sb + ga sa, which is all that dL/dalpha needs:
+//   dL/dalpha = (T (g . c + ga) - G) / (1 - alpha). The 9 (10 with absgrad)
+//   per-Gaussian sums are the colour weights and the moments of
+//   dg = dL/dgauss over the pixels (sum dg, dg dx, dg dy, dg dx^2, dg dx dy,
+//   dg dy^2), reduced across the 64 lanes with lane swaps and DPP and added
+//   into a per-batch LDS accumulator (LDS float atomics: several waves may
+//   hold the same Gaussian). After the batch one thread per Gaussian turns
+//   the moments into the uv, conic and opacity gradients with the
+//   Gaussian's own opacity and conic, and issues the global float atomics.
+//   Global atomics go to a coherence point shared by all XCDs and cost HBM
+//   write traffic, so there is one set per (Gaussian, tile) rather than per
+//   (Gaussian, wave).
 #include "mg_common.h"
 
 namespace mg {
@@ -129,25 +137,23 @@ struct Stage {
     int32_t flag[MAXW];
 };
 
-constexpr int kGradSlots = 10;   // colour 3, uv 2, conic 3, opacity, |uv|
+constexpr int kGradSlots = 10;   // colour 3, moments 5, sum dg, |d uv|
 
-// Pairwise wave-wide sums by lane swaps. v_permlane32_swap a, b swaps lanes
+// Wave sums of ten values by lane swaps. v_permlane32_swap a, b swaps lanes
 // 32-63 of a with lanes 0-31 of b, leaving (a[0:32], b[0:32]) in a and
 // (a[32:64], b[32:64]) in b, so a + b holds a's half-sums in lanes 0-31 and
 // b's in lanes 32-63. v_permlane16_swap does the same between rows 0/1 and
-// 2/3. Issued as inline assembly: this compiler folds the two results of the
+// 2/3. After the two swap stages each row of 16 lanes carries one value's
+// partials, which a row reduction finishes: rows of q0 hold the sums of v0,
+// v2, v1, v3; of q1 v4, v6, v5, v7; of q2 v8, -, v9, -. 26 VALU operations
+// for ten sums.
+//
+// The swaps are inline assembly: this compiler folds the two results of the
 // __builtin_amdgcn_permlane*_swap builtins into one register (r[0] + r[1]
-// comes out as r[0] + r[0]). The s_nop gives the two wait states a swap
-// needs after a VALU write of its operands.
-__device__ __forceinline__ float swap32_sum(float a, float b) {
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return a + b;
-}
-__device__ __forceinline__ float swap16_sum(float a, float b) {
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return a + b;
-}
-// Sum over the 16 lanes of each row, in every lane of the row.
+// comes out as r[0] + r[0]). A swap needs two wait states after a VALU write
+// of its operands; each stage's swaps read only registers written before the
+// stage and write disjoint pairs, so one s_nop 1 at the head of a stage
+// covers all of them.
 __device__ __forceinline__ float row_allsum(float x) {
     x += dpp_f<0x128>(x);   // row_ror:8
     x += dpp_f<0x124>(x);   // row_ror:4
@@ -155,20 +161,30 @@ __device__ __forceinline__ float row_allsum(float x) {
     x += dpp_f<0x121>(x);   // row_ror:1
     return x;
 }
-// Wave sums of ten values in 28 VALU operations instead of ten separate
-// reductions: after the 32- and 16-lane swap stages each row of 16 lanes
-// carries one value's partials, which a row reduction finishes. Rows of q0
-// hold the sums of v0, v2, v1, v3; of q1 v4, v6, v5, v7; of q2 v8, -, v9, -.
 __device__ __forceinline__ void reduce10_to_rows(const float v[10], float &q0, float &q1,
                                                  float &q2) {
-    const float p0 = swap32_sum(v[0], v[1]);
-    const float p1 = swap32_sum(v[2], v[3]);
-    const float p2 = swap32_sum(v[4], v[5]);
-    const float p3 = swap32_sum(v[6], v[7]);
-    const float p4 = swap32_sum(v[8], v[9]);
-    q0 = row_allsum(swap16_sum(p0, p1));
-    q1 = row_allsum(swap16_sum(p2, p3));
-    q2 = row_allsum(swap16_sum(p4, 0.0f));
+    float a0 = v[0], b0 = v[1], a1 = v[2], b1 = v[3], a2 = v[4], b2 = v[5];
+    float a3 = v[6], b3 = v[7], a4 = v[8], b4 = v[9];
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_permlane32_swap_b32 %0, %1\n\t"
+        "v_permlane32_swap_b32 %2, %3\n\t"
+        "v_permlane32_swap_b32 %4, %5\n\t"
+        "v_permlane32_swap_b32 %6, %7\n\t"
+        "v_permlane32_swap_b32 %8, %9"
+        : "+v"(a0), "+v"(b0), "+v"(a1), "+v"(b1), "+v"(a2), "+v"(b2), "+v"(a3), "+v"(b3),
+          "+v"(a4), "+v"(b4));
+    float p0 = a0 + b0, p1 = a1 + b1, p2 = a2 + b2, p3 = a3 + b3, p4 = a4 + b4;
+    float z = 0.0f;
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_permlane16_swap_b32 %0, %1\n\t"
+        "v_permlane16_swap_b32 %2, %3\n\t"
+        "v_permlane16_swap_b32 %4, %5"
+        : "+v"(p0), "+v"(p1), "+v"(p2), "+v"(p3), "+v"(p4), "+v"(z));
+    q0 = row_allsum(p0 + p1);
+    q1 = row_allsum(p2 + p3);
+    q2 = row_allsum(p4 + z);
 }
 
 template <int MAXW>
@@ -176,27 +192,53 @@ struct StageBwd : Stage<MAXW> {
     float grad[kGradSlots][kBatch];   // per batch entry, summed over waves
 };
 
+// One list entry's record, gathered from the per-Gaussian arrays.
+struct Rec {
+    float4 geo;   // u, v, opacity
+    float4 con;   // conic a, b, c
+    float4 col;   // r, g, b
+    int32_t id;
+};
+
+__device__ __forceinline__ Rec gather_rec(const RasterArgs &A, int g) {
+    Rec r;
+    r.id = g;
+    r.geo = make_float4(A.uv[2 * g], A.uv[2 * g + 1], A.opac[g], 0.f);
+    r.con = make_float4(A.conic[3 * g], A.conic[3 * g + 1], A.conic[3 * g + 2], 0.f);
+    r.col = make_float4(A.color[3 * g], A.color[3 * g + 1], A.color[3 * g + 2], 0.f);
+    return r;
+}
+
+// Writes entry t's record to LDS with its per-wave cull bits.
+template <class S_>
+__device__ __forceinline__ void put_rec(S_ &S, int t, const Rec &r, int nwaves) {
+    S.geo[t] = r.geo;
+    S.con[t] = r.con;
+    S.col[t] = r.col;
+    S.id[t] = r.id;
+    const float thr = 2.0f * __logf(fmaxf(255.0f * r.geo.z, 1.0f));
+    const float thr_m = thr * 1.0001f + 1e-4f;
+    uint32_t m = 0;
+    for (int w = 0; w < nwaves; ++w) {
+        const float4 q = S.rect[w];
+        if (q.x <= q.y &&
+            rect_min_q(r.geo.x, r.geo.y, r.con.x, r.con.y, r.con.z, q.x, q.y, q.z, q.w) < thr_m)
+            m |= 1u << w;
+    }
+    S.live[t] = m;
+}
+
 template <class S_>
 __device__ __forceinline__ void stage_batch(S_ &S, const RasterArgs &A, int base, int n,
                                             int nwaves) {
-    for (int t = threadIdx.x; t < n; t += blockDim.x) {
-        const int g = A.ids[base + t];
-        const float u = A.uv[2 * g], v = A.uv[2 * g + 1];
-        const float op = A.opac[g];
-        const float ca = A.conic[3 * g], cb = A.conic[3 * g + 1], cc = A.conic[3 * g + 2];
-        S.geo[t] = make_float4(u, v, op, 0.f);
-        S.con[t] = make_float4(ca, cb, cc, 0.f);
-        S.col[t] = make_float4(A.color[3 * g], A.color[3 * g + 1], A.color[3 * g + 2], 0.f);
-        S.id[t] = g;
-        const float thr = 2.0f * __logf(fmaxf(255.0f * op, 1.0f));
-        const float thr_m = thr * 1.0001f + 1e-4f;
-        uint32_t m = 0;
-        for (int w = 0; w < nwaves; ++w) {
-            const float4 r = S.rect[w];
-            if (r.x <= r.y && rect_min_q(u, v, ca, cb, cc, r.x, r.y, r.z, r.w) < thr_m) m |= 1u << w;
-        }
-        S.live[t] = m;
-    }
+    for (int t = threadIdx.x; t < n; t += blockDim.x)
+        put_rec(S, t, gather_rec(A, A.ids[base + t]), nwaves);
+}
+
+// Forces the values to have arrived (the compiler waits for their loads
+// here rather than at a first use inside a loop).
+__device__ __forceinline__ void settle(float a, float b, float c, float d) {
+    asm volatile("" ::"v"(a), "v"(b), "v"(c), "v"(d));
 }
 
 __device__ __forceinline__ void wave_sync_lds() {
@@ -407,13 +449,13 @@ struct RasterGrads {
     float *d_uv, *d_conic, *d_op, *d_col, *d_abs;
 };
 
-template <int MAXW>
+template <int MAXW, bool ABS, bool PIPE>
 __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs A,
                                                                const RasterGrads G,
                                                                const ChunkPlan P) {
     __shared__ StageBwd<MAXW> S;
     // Without a plan a workgroup takes a whole tile; with one, one chunk.
-    int tile_id, chunk = 0;
+    int tile_id, chunk = 0, tile_start, tile_end;
     if (P.ckpt) {
         // Range checks keep a workspace that did not come from the forward
         // from indexing outside it (the whole workgroup returns).
@@ -422,11 +464,15 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
         tile_id = P.unit_tile[u];
         if (tile_id < 0 || tile_id >= A.n_tiles) return;
         chunk = u - P.base[tile_id];
-        const int nck = (A.offsets[tile_id + 1] - A.offsets[tile_id] + kChunk - 1) / kChunk;
+        tile_start = A.offsets[tile_id];
+        tile_end = A.offsets[tile_id + 1];
+        const int nck = (tile_end - tile_start + kChunk - 1) / kChunk;
         if (chunk < 0 || chunk >= nck || P.base[tile_id] + nck > P.cap) return;
     } else {
         tile_id = tile_of_block(blockIdx.x, A.tiles_x, A.n_tiles / A.tiles_x);
         if (tile_id < 0) return;
+        tile_start = A.offsets[tile_id];
+        tile_end = A.offsets[tile_id + 1];
     }
     const int tx = tile_id % A.tiles_x, ty = tile_id / A.tiles_x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -439,25 +485,9 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
     const float fx = (float)px + 0.5f, fy = (float)py + 0.5f;
     publish_rect(S, inimg, fx, fy, wave, lane);
 
-    const int tile_start = A.offsets[tile_id], tile_end = A.offsets[tile_id + 1];
     const int start = tile_start + chunk * kChunk;   // this workgroup's entries
     const int cend = P.ckpt ? min(start + kChunk, tile_end) : tile_end;
     const int64_t o = inimg ? (int64_t)py * A.W + px : 0;
-    float T = inimg ? G.final_T[o] : 1.0f;
-    // Colour and coverage composited behind this chunk (the suffix sums).
-    float sr = 0.f, sg = 0.f, sb = 0.f, sa = 0.f;
-    if (P.ckpt && inimg) {
-        const int tile2 = A.tile * A.tile, pslot = ly * A.tile + lx;
-        const int u0 = P.base[tile_id];
-        const int nck = (tile_end - tile_start + kChunk - 1) / kChunk;
-        const float4 e = P.ckpt[(int64_t)(u0 + chunk) * tile2 + pslot];
-        const float4 f = P.ckpt[(int64_t)(u0 + nck - 1) * tile2 + pslot];
-        T = e.x;
-        sr = f.y - e.y;
-        sg = f.z - e.z;
-        sb = f.w - e.w;
-        sa = e.x - f.x;      // sum of the weights behind = T_end - T_final
-    }
     const int my_stop = inimg ? min(G.stop[o], cend) : start;
     const float gr = inimg ? G.grad_rgb[3 * o] : 0.f;
     const float gg = inimg ? G.grad_rgb[3 * o + 1] : 0.f;
@@ -467,7 +497,21 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
     // 1 - alpha >= 0 (torch's clamp_min passes the gradient at the bound).
     if (A.has_bg && inimg && 1.0f - G.alpha[o] >= 0.0f)
         ga -= gr * A.bg[0] + gg * A.bg[1] + gb * A.bg[2];
-    const bool want_abs = G.d_abs != nullptr;
+    float T = inimg ? G.final_T[o] : 1.0f;
+    // Gs = gr sr + gg sg + gb sb + ga sa over the colour (sr, sg, sb) and
+    // coverage sa composited behind the current entry. With a chunk plan the
+    // walk starts at the chunk's end: colour behind = final - prefix there,
+    // coverage behind = T_end - T_final.
+    float Gs = 0.f;
+    if (P.ckpt && inimg) {
+        const int tile2 = A.tile * A.tile, pslot = ly * A.tile + lx;
+        const int u0 = P.base[tile_id];
+        const int nck = (tile_end - tile_start + kChunk - 1) / kChunk;
+        const float4 e = P.ckpt[(int64_t)(u0 + chunk) * tile2 + pslot];
+        const float4 f = P.ckpt[(int64_t)(u0 + nck - 1) * tile2 + pslot];
+        T = e.x;
+        Gs = gr * (f.y - e.y) + gg * (f.z - e.z) + gb * (f.w - e.w) + ga * (e.x - f.x);
+    }
 
     // Nothing at or past a pixel's stop index contributed to it.
     const int wstop = wave_max_i(my_stop);
@@ -476,101 +520,187 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
     int bstop = start;
     for (int w = 0; w < nwaves; ++w) bstop = max(bstop, S.flag[w]);
 
+    // One list entry: the pixel's update and the wave's sums into S.grad.
+    auto entry = [&](const int j, const int i, const float4 geo, const float4 con,
+                     const float4 col) {
+        const float dx = fx - geo.x, dy = fy - geo.y;
+        const float power = splat_power(dx, dy, con.x, con.y, con.z);
+        const float gauss = __expf(power);
+        const float op = geo.z;
+        const float alpha_raw = op * gauss;
+        const float alpha = fminf(kAlphaMax, alpha_raw);
+        const bool active = inimg && i < my_stop && power <= 0.0f && alpha >= kAlphaMin;
+        if (ballot(active) == 0) return;
+        // Branchless: inactive lanes compute on finite values and select
+        // zeros (never multiply by 0, which would keep an inf as NaN). T
+        // before this entry is recovered as T / (1 - alpha) with a 1-ulp
+        // reciprocal; the forward's rounding of T (1 - alpha) already makes
+        // the recovery approximate.
+        const float om = fmaxf(1.0f - alpha, 1e-8f);
+        const float iom = __builtin_amdgcn_rcpf(om);
+        const float gc = fmaf(gb, col.z, fmaf(gg, col.y, fmaf(gr, col.x, ga)));
+        const float dal = (T * gc - Gs) * iom;
+        const float Tn = T * iom;
+        const float w = active ? alpha * Tn : 0.0f;
+        T = active ? Tn : T;
+        Gs = fmaf(w, gc, Gs);
+        // Past the 0.999 clamp alpha no longer depends on the splat.
+        const float dg = active && alpha_raw <= kAlphaMax ? dal * gauss : 0.0f;
+        float v[kGradSlots];
+        v[0] = w * gr;
+        v[1] = w * gg;
+        v[2] = w * gb;
+        const float mx = dg * dx, my = dg * dy;
+        v[3] = mx;
+        v[4] = my;
+        v[5] = mx * dx;
+        v[6] = mx * dy;
+        v[7] = my * dy;
+        v[8] = dg;
+        if (ABS) {
+            // |d uv| of this pixel over op: |dg| |(a dx + b dy, b dx + c dy)|.
+            const float ex = fmaf(con.x, dx, con.y * dy), ey = fmaf(con.y, dx, con.z * dy);
+            v[9] = fabsf(dg) * __builtin_amdgcn_sqrtf(fmaf(ex, ex, ey * ey));
+        } else {
+            v[9] = 0.0f;
+        }
+        // Sums over the wave of v[0..9], deposited into S.grad[.][j] with
+        // four lanes per LDS atomic (see reduce10_to_rows).
+        float q0, q1, q2;
+        reduce10_to_rows(v, q0, q1, q2);
+        if ((lane & 15) == 0) {
+            const int row = lane >> 4;
+            // Row r of q0 holds slot {0,2,1,3}[r], of q1 {4,6,5,7}[r], of
+            // q2 {8,0,9,0}[r]: rows 1 and 3 of q2 are sums of zeros and add
+            // nothing, so all four lanes deposit it (to slots 8, 8, 9, 9; a
+            // lane-dependent address, which the compiler does not turn into
+            // a wave-aggregation loop as it does a single lane's).
+            const int s0 = (row & 1) * 2 + (row >> 1);
+            atomicAdd(&S.grad[s0][j], q0);
+            atomicAdd(&S.grad[4 + s0][j], q1);
+            atomicAdd(&S.grad[8 + (row >> 1)][j], q2);
+        }
+    };
+
+    // A finished entry's gradients: the tile's sums turned into d_col,
+    // d_uv = op (a Sx + b Sy, b Sx + c Sy), d_conic = -op (Sxx / 2, Sxy,
+    // Syy / 2), d_op = S1 and d_abs = op Sabs.
+    struct Flush {
+        int g;
+        float v[kGradSlots];
+    };
+    auto take = [&](const int t, Flush &f) {
+        f.g = S.id[t];
+        float s[kGradSlots];
+#pragma unroll
+        for (int q = 0; q < kGradSlots; ++q) s[q] = S.grad[q][t];
+        const float op = S.geo[t].z;
+        const float4 con = S.con[t];
+        f.v[0] = s[0];
+        f.v[1] = s[1];
+        f.v[2] = s[2];
+        f.v[3] = op * fmaf(con.x, s[3], con.y * s[4]);
+        f.v[4] = op * fmaf(con.y, s[3], con.z * s[4]);
+        f.v[5] = -0.5f * op * s[5];
+        f.v[6] = -op * s[6];
+        f.v[7] = -0.5f * op * s[7];
+        f.v[8] = s[8];
+        f.v[9] = op * s[9];
+    };
+    auto publish = [&](const Flush &f) {
+        const int g = f.g;
+        if (f.v[0] != 0.f) unsafeAtomicAdd(G.d_col + 3 * g, f.v[0]);
+        if (f.v[1] != 0.f) unsafeAtomicAdd(G.d_col + 3 * g + 1, f.v[1]);
+        if (f.v[2] != 0.f) unsafeAtomicAdd(G.d_col + 3 * g + 2, f.v[2]);
+        if (f.v[3] != 0.f) unsafeAtomicAdd(G.d_uv + 2 * g, f.v[3]);
+        if (f.v[4] != 0.f) unsafeAtomicAdd(G.d_uv + 2 * g + 1, f.v[4]);
+        if (f.v[5] != 0.f) unsafeAtomicAdd(G.d_conic + 3 * g, f.v[5]);
+        if (f.v[6] != 0.f) unsafeAtomicAdd(G.d_conic + 3 * g + 1, f.v[6]);
+        if (f.v[7] != 0.f) unsafeAtomicAdd(G.d_conic + 3 * g + 2, f.v[7]);
+        if (f.v[8] != 0.f) unsafeAtomicAdd(G.d_op + g, f.v[8]);
+        if (ABS && f.v[9] != 0.f) unsafeAtomicAdd(G.d_abs + g, f.v[9]);
+    };
+
+    // PIPE (one batch entry per thread): the batches are software-pipelined.
+    // Vector-memory completions are counted in order with stores and
+    // atomics, so a load issued after a batch's gradient atomics cannot be
+    // waited for without waiting for the atomics. Each batch therefore
+    // issues, before its atomics, the gather of the next batch's records and
+    // the load of the ids of the one after; the walk then covers both, and
+    // the atomics of a batch go out after the next batch is staged.
+    const int t = threadIdx.x;
+    Rec rec{};
+    int nid = 0;
+    Flush fl;
+    fl.g = -1;
     const int nbatch = (bstop - start + kBatch - 1) / kBatch;
+    if (PIPE && nbatch > 0) {
+        const int b0 = start + (nbatch - 1) * kBatch;
+        if (t < bstop - b0) rec = gather_rec(A, A.ids[b0 + t]);
+        if (nbatch > 1 && t < kBatch) nid = A.ids[b0 - kBatch + t];
+    }
+    // The pixel's own inputs have arrived before the first walk.
+    settle(gr, gg, gb, ga);
+    settle(T, Gs, __int_as_float(my_stop), fx);
     for (int bi = nbatch - 1; bi >= 0; --bi) {
         const int base = start + bi * kBatch;
         const int n = min(kBatch, bstop - base);
-        __syncthreads();   // the previous batch's flush has read S.grad
-        stage_batch(S, A, base, n, nwaves);
-        for (int t = threadIdx.x; t < kGradSlots * kBatch; t += blockDim.x)
-            (&S.grad[0][0])[t] = 0.f;
+        __syncthreads();   // the previous batch's walk and sums are read
+        if (PIPE) {
+            if (t < n) put_rec(S, t, rec, nwaves);
+        } else {
+            stage_batch(S, A, base, n, nwaves);
+        }
+        for (int q = t; q < kGradSlots * kBatch; q += blockDim.x) (&S.grad[0][0])[q] = 0.f;
         __syncthreads();
+        if (PIPE) {
+            // Batches below the first are full.
+            if (bi > 0 && t < kBatch) rec = gather_rec(A, nid);
+            if (bi > 1 && t < kBatch) nid = A.ids[base - 2 * kBatch + t];
+            if (fl.g >= 0) publish(fl);
+        }
         const int cnt = compact_live(S, n, wstop - base, wave, lane);
-        // The next entry's LDS reads are issued before this entry's math.
-        int jn = cnt > 0 ? S.list[wave][cnt - 1] : 0;
-        float4 geo_n = S.geo[jn], con_n = S.con[jn], col_n = S.col[jn];
-        for (int k = cnt - 1; k >= 0; --k) {
-            const int j = jn;
-            const float4 geo = geo_n, con = con_n, col = col_n;
-            if (k > 0) {
-                jn = S.list[wave][k - 1];
-                geo_n = S.geo[jn];
-                con_n = S.con[jn];
-                col_n = S.col[jn];
-            }
-            const int i = base + j;
-            const float dx = fx - geo.x, dy = fy - geo.y;
-            const float power = splat_power(dx, dy, con.x, con.y, con.z);
-            const float gauss = __expf(power);
-            const float op = geo.z;
-            const float alpha_raw = op * gauss;
-            const float alpha = fminf(kAlphaMax, alpha_raw);
-            const bool active = inimg && i < my_stop && power <= 0.0f && alpha >= kAlphaMin;
-            if (ballot(active) == 0) continue;
-            // Branchless: inactive lanes compute on finite values and select
-            // zeros (never multiply by 0, which would keep an inf as NaN).
-            // T before this entry is recovered as T / (1 - alpha) with a
-            // 1-ulp reciprocal; the forward's rounding of T (1 - alpha)
-            // already makes the recovery approximate.
-            const float om = fmaxf(1.0f - alpha, 1e-8f);
-            const float iom = __builtin_amdgcn_rcpf(om);
-            const float Tn = T * iom;
-            const float w = active ? alpha * Tn : 0.0f;
-            const float dal = gr * (Tn * col.x - sr * iom) + gg * (Tn * col.y - sg * iom) +
-                              gb * (Tn * col.z - sb * iom) + ga * (Tn - sa * iom);
-            T = active ? Tn : T;
-            sr = fmaf(w, col.x, sr);
-            sg = fmaf(w, col.y, sg);
-            sb = fmaf(w, col.z, sb);
-            sa += w;
-            // Past the 0.999 clamp alpha no longer depends on the splat.
-            const float dg = active && alpha_raw <= kAlphaMax ? dal * gauss : 0.0f;
-            const float dpow = dg * op;
-            float v[kGradSlots];
-            v[0] = w * gr;
-            v[1] = w * gg;
-            v[2] = w * gb;
-            v[3] = dpow * (con.x * dx + con.y * dy);
-            v[4] = dpow * (con.y * dx + con.z * dy);
-            v[5] = -0.5f * dpow * dx * dx;
-            v[6] = -dpow * dx * dy;
-            v[7] = -0.5f * dpow * dy * dy;
-            v[8] = dg;
-            v[9] = want_abs ? __builtin_amdgcn_sqrtf(v[3] * v[3] + v[4] * v[4]) : 0.0f;
-            // Sums over the wave of v[0..9], deposited into S.grad[.][j]
-            // with four lanes per LDS atomic (see reduce10_to_rows).
-            float q0, q1, q2;
-            reduce10_to_rows(v, q0, q1, q2);
-            if ((lane & 15) == 0) {
-                const int row = lane >> 4;
-                // Row r of Q0 holds slot {0,2,1,3}[r], of Q1 {4,6,5,7}[r],
-                // of Q2 {8,-,9,-}[r].
-                const int s0 = (row & 1) * 2 + (row >> 1);
-                if (q0 != 0.f) atomicAdd(&S.grad[s0][j], q0);
-                if (q1 != 0.f) atomicAdd(&S.grad[4 + s0][j], q1);
-                if ((row & 1) == 0 && q2 != 0.f && (row == 0 || want_abs))
-                    atomicAdd(&S.grad[8 + (row >> 1)][j], q2);
+        // Walk the wave's list back to front, two entries per iteration with
+        // the records of the next entry read before this one's math. The
+        // list is read 64 indices at a time into a register and the entry's
+        // index taken from it with a lane read, so it is wave-uniform.
+        if (cnt > 0) {
+            int k = cnt - 1;
+            int lreg = S.list[wave][(k & ~63) + lane];
+            int ja = __builtin_amdgcn_readlane(lreg, k & 63);
+            float4 geo_a = S.geo[ja], con_a = S.con[ja], col_a = S.col[ja];
+            for (;;) {
+                // Entry k - 1 (or k again at the end) into the b registers.
+                const int kb = max(k - 1, 0);
+                if ((kb & 63) == 63) lreg = S.list[wave][(kb & ~63) + lane];
+                const int jb = __builtin_amdgcn_readlane(lreg, kb & 63);
+                const float4 geo_b = S.geo[jb], con_b = S.con[jb], col_b = S.col[jb];
+                entry(ja, base + ja, geo_a, con_a, col_a);
+                if (--k < 0) break;
+                const int kc = max(k - 1, 0);
+                if ((kc & 63) == 63) lreg = S.list[wave][(kc & ~63) + lane];
+                ja = __builtin_amdgcn_readlane(lreg, kc & 63);
+                geo_a = S.geo[ja];
+                con_a = S.con[ja];
+                col_a = S.col[ja];
+                entry(jb, base + jb, geo_b, con_b, col_b);
+                if (--k < 0) break;
             }
         }
         __syncthreads();
-        // One thread per batch entry publishes the tile's sums.
-        for (int t = threadIdx.x; t < n; t += blockDim.x) {
-            const int g = S.id[t];
-            float s[kGradSlots];
-#pragma unroll
-            for (int q = 0; q < kGradSlots; ++q) s[q] = S.grad[q][t];
-            if (s[0] != 0.f) unsafeAtomicAdd(G.d_col + 3 * g, s[0]);
-            if (s[1] != 0.f) unsafeAtomicAdd(G.d_col + 3 * g + 1, s[1]);
-            if (s[2] != 0.f) unsafeAtomicAdd(G.d_col + 3 * g + 2, s[2]);
-            if (s[3] != 0.f) unsafeAtomicAdd(G.d_uv + 2 * g, s[3]);
-            if (s[4] != 0.f) unsafeAtomicAdd(G.d_uv + 2 * g + 1, s[4]);
-            if (s[5] != 0.f) unsafeAtomicAdd(G.d_conic + 3 * g, s[5]);
-            if (s[6] != 0.f) unsafeAtomicAdd(G.d_conic + 3 * g + 1, s[6]);
-            if (s[7] != 0.f) unsafeAtomicAdd(G.d_conic + 3 * g + 2, s[7]);
-            if (s[8] != 0.f) unsafeAtomicAdd(G.d_op + g, s[8]);
-            if (want_abs && s[9] != 0.f) unsafeAtomicAdd(G.d_abs + g, s[9]);
+        // One thread per batch entry takes the tile's sums.
+        if (PIPE) {
+            fl.g = -1;
+            if (t < n) take(t, fl);
+        } else {
+            for (int e = t; e < n; e += blockDim.x) {
+                Flush f;
+                take(e, f);
+                publish(f);
+            }
         }
     }
+    if (PIPE && fl.g >= 0) publish(fl);
 }
 
 // Zero-fills up to five float buffers in one launch (gradient accumulators).
@@ -701,10 +831,21 @@ int32_t mg_rasterize_backward(int64_t N, const float *uv, const float *conic,
     const int threads = ((tile * tile + 63) / 64) * 64;
     TimedScope ts("rasterize_backward", s);
     if (grid > 0) {
-        if (threads <= 4 * 64)
-            raster_bwd_kernel<4><<<grid, threads, 0, s>>>(A, Gr, P);
-        else
-            raster_bwd_kernel<kMaxWaves><<<grid, threads, 0, s>>>(A, Gr, P);
+        // One batch entry per thread (tile 16 and up) takes the pipelined
+        // batch loop.
+        const bool abs = d_absuv != nullptr, pipe = threads >= kBatch;
+        if (threads <= 4 * 64) {
+            if (pipe) {
+                if (abs) raster_bwd_kernel<4, true, true><<<grid, threads, 0, s>>>(A, Gr, P);
+                else raster_bwd_kernel<4, false, true><<<grid, threads, 0, s>>>(A, Gr, P);
+            } else {
+                if (abs) raster_bwd_kernel<4, true, false><<<grid, threads, 0, s>>>(A, Gr, P);
+                else raster_bwd_kernel<4, false, false><<<grid, threads, 0, s>>>(A, Gr, P);
+            }
+        } else {
+            if (abs) raster_bwd_kernel<kMaxWaves, true, true><<<grid, threads, 0, s>>>(A, Gr, P);
+            else raster_bwd_kernel<kMaxWaves, false, true><<<grid, threads, 0, s>>>(A, Gr, P);
+        }
         MG_LAUNCHED("raster_bwd_kernel");
     }
     return MG_OK;
