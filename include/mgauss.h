@@ -357,7 +357,8 @@ int32_t mg_rasterize_forward(
  * (metal_gauss/csrc/rasterize.mm:147-194; kernel rasterize.metal:173-340).
  * Overwrites d_uv (N,2), d_conic (N,3), d_opacity (N,), d_color (N,3); when
  * d_absuv is not NULL it also overwrites d_absuv (N,) with the per-pixel sum
- * of |d_uv| (the reference's absgrad statistic). With the forward's
+ * of |d_uv| (the reference's absgrad statistic). grad_alpha may be NULL
+ * (a zero gradient, when the coverage is not used). With the forward's
  * background (host, or NULL), grad_rgb is the gradient of the blended colour
  * and alpha (the forward's out_alpha, device) adds the blend's share to
  * grad_alpha. n_isect / chunk_ws / chunk_ws_bytes are the forward's (chunk_ws

@@ -307,6 +307,9 @@ class _PreprocessMetal(torch.autograd.Function):
             rxy.data_ptr(), valid.data_ptr(),
             None if color is None else color.data_ptr(), _lib.stream(means)))
         ctx.save_for_backward(means, quats, scales, sh, rest, valid)
+        # depth, rxy and valid carry no gradient: no zeros are materialised
+        # for them (or for an unused output) in the backward.
+        ctx.set_materialize_grads(False)
         ctx.fused = fused
         ctx.has_sh = sh is not None
         ctx.meta = (viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
@@ -331,8 +334,8 @@ class _PreprocessMetal(torch.autograd.Function):
             d_sh = torch.empty_like(sh)
             d_rest = None if ctx.fused else torch.empty_like(rest)
             d_color = torch.zeros(N, 3, device=dev) if d_color is None else d_color.contiguous()
-        d_uv = d_uv.contiguous()
-        d_conic = d_conic.contiguous()
+        d_uv = torch.zeros(N, 2, device=dev) if d_uv is None else d_uv.contiguous()
+        d_conic = torch.zeros(N, 3, device=dev) if d_conic is None else d_conic.contiguous()
         _lib.check(lib.mg_preprocess_backward(
             N, means.data_ptr(), quats.data_ptr(), scales.data_ptr(),
             None if sh is None else sh.data_ptr(), None if rest is None else rest.data_ptr(),
@@ -382,6 +385,9 @@ class _RasterizeMetal(torch.autograd.Function):
                               alpha if background is not None else None, chunk_ws)
         ctx.dims = (W, H, tile, tiles_x)
         ctx.background = background
+        # An output nobody differentiates (alpha, most often) gets no
+        # materialised zeros: the kernel reads a missing grad_alpha as 0.
+        ctx.set_materialize_grads(False)
         # absgrad is a statistic of the backward, not a gradient: the caller
         # hands in a buffer and the backward accumulates into it.
         ctx.absgrad_out = absgrad_out
@@ -401,12 +407,15 @@ class _RasterizeMetal(torch.autograd.Function):
         d_op = torch.empty(N, device=dev)
         d_col = torch.empty(N, 3, device=dev)
         d_abs = torch.empty(N, device=dev) if ctx.absgrad_out is not None else None
-        grad_rgb = grad_rgb.contiguous()
-        grad_alpha = grad_alpha.contiguous()
+        if grad_rgb is None and grad_alpha is None:
+            return (None,) * 14
+        grad_rgb = torch.zeros(H, W, 3, device=dev) if grad_rgb is None else grad_rgb.contiguous()
+        grad_alpha = None if grad_alpha is None else grad_alpha.contiguous()
         _lib.check(lib.mg_rasterize_backward(
             N, uv.data_ptr(), conic.data_ptr(), opacity.data_ptr(), color.data_ptr(),
             gauss_ids.data_ptr(), tile_offsets.data_ptr(), T.data_ptr(), stop.data_ptr(),
-            _lib.dev_tensor(grad_rgb, "grad_rgb"), _lib.dev_tensor(grad_alpha, "grad_alpha"),
+            _lib.dev_tensor(grad_rgb, "grad_rgb"),
+            None if grad_alpha is None else _lib.dev_tensor(grad_alpha, "grad_alpha"),
             None if bg is None else alpha.data_ptr(), None if bg is None else _lib.f32_array(bg),
             gauss_ids.numel(), chunk_ws.data_ptr() if chunk_ws.numel() else None,
             chunk_ws.numel(), W, H, tile, tiles_x,
@@ -469,6 +478,7 @@ class _PreprocessMip(torch.autograd.Function):
             None if color is None else color.data_ptr(), op_eff.data_ptr(),
             _lib.stream(means)))
         ctx.save_for_backward(means, quats, scales, opacities, sh, rest, filt, valid)
+        ctx.set_materialize_grads(False)
         ctx.fused = fused
         ctx.has_sh = sh is not None
         ctx.antialias = bool(antialias)

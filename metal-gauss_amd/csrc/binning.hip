@@ -442,6 +442,7 @@ struct BinStats {
     unsigned long long total;       // intersections
     uint32_t kmin, kmax;            // depth-key range of Gaussians with a tile
     unsigned long long scan_total;  // the scan's own total (same value)
+    DevWin<uint32_t> win;           // the depth sort's window: [kmin, kmax], its bit width
 };
 
 // One per count workgroup, reduced by bin_stats_kernel. (Same-address
@@ -570,6 +571,14 @@ __global__ __launch_bounds__(256) void bin_stats_kernel(const BinPart *parts, in
         st->kmin = b.kmin;
         st->kmax = b.kmax;
         st->scan_total = 0;
+        // Keys of Gaussians with tiles lie in [kmin, kmax]; the others clamp
+        // to kmax and sort among the farthest, which changes no list. No
+        // tiles at all: every pass copies.
+        const bool any = b.kmin <= b.kmax;
+        const uint32_t span = any ? b.kmax - b.kmin : 0u;
+        st->win.lo = any ? b.kmin : 0u;
+        st->win.hi = any ? b.kmax : 0u;
+        st->win.bits = span == 0u ? 0 : 32 - __builtin_clz(span);
     }
 }
 
@@ -739,8 +748,6 @@ struct BeginWs {
     }
 };
 
-inline int bit_width(uint32_t v) { return v == 0 ? 0 : 32 - __builtin_clz(v); }
-
 inline int tile_bits(int n_tiles) {
     int b = 1;
     while ((1LL << b) < n_tiles) ++b;
@@ -866,28 +873,34 @@ int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy, const f
     }
     bin_stats_kernel<<<1, 256, 0, s>>>(ws.parts, nparts, ws.stats);
     MG_LAUNCHED("bin_stats_kernel");
-    // The one host read: the total sizes the caller's id buffer, the key
-    // range sets the depth sort's pass count.
-    BinStats st;
-    MG_HIP(hipMemcpyAsync(&st, ws.stats, sizeof(st), hipMemcpyDeviceToHost, s));
-    MG_HIP(hipStreamSynchronize(s));
-    MG_REQUIRE(st.total < (1ULL << 31), "mg_bin_lists_begin: %llu intersections exceed int32",
-               st.total);
-    if (total_host) *total_host = (int64_t)st.total;
-    if (st.total == 0) return MG_OK;
-    // Keys of Gaussians with tiles lie in [kmin, kmax]; the others clamp to
-    // kmax and sort among the farthest, which changes no list.
-    const int bits = bit_width(st.kmax - st.kmin);
-    uint32_t *rk;
-    int32_t *rv;
-    rc = radix_sort_passes<uint32_t>(ws.dkey_a, ws.perm_a, ws.dkey_b, ws.perm_b, N, 0, bits,
-                                     ws.sort_ws, ws.sort_bytes, s, "depth_sort", &rk, &rv,
-                                     st.kmin, st.kmax);
-    if (rc != MG_OK) return rc;
-    if (rv != ws.perm_a)
-        MG_HIP(hipMemcpyAsync(ws.perm_a, rv, 4 * N, hipMemcpyDeviceToDevice, s));
-    return exclusive_scan(ws.counts, ws.perm_a, N, ws.offsets, (int64_t *)&ws.stats->scan_total,
-                          ws.scan_ws, ws.scan_bytes, s);
+    // The one host read: the total sizes the caller's id buffer. It is copied
+    // into a pinned word behind an event, and the depth sort and the scan are
+    // queued before the host waits, so the GPU keeps working meanwhile. The
+    // sort reads its key window and live bit count on the device: all four
+    // 8-bit passes are queued, those above the live bits only copy, and the
+    // even pass count leaves the order in perm_a.
+    HostReadback rb;
+    if (!rb.ok()) return MG_ERR_RUNTIME;
+    MG_HIP(hipMemcpyAsync(rb.slot, &ws.stats->total, sizeof(int64_t), hipMemcpyDeviceToHost, s));
+    MG_HIP(hipEventRecord(rb.ev, s));
+    if (N > 0) {
+        uint32_t *rk;
+        int32_t *rv;
+        rc = radix_sort_passes<uint32_t>(ws.dkey_a, ws.perm_a, ws.dkey_b, ws.perm_b, N, 0, 32,
+                                         ws.sort_ws, ws.sort_bytes, s, "depth_sort", &rk, &rv,
+                                         0u, 0xFFFFFFFFu, &ws.stats->win);
+        if (rc != MG_OK) return rc;
+        MG_REQUIRE(rv == ws.perm_a, "mg_bin_lists_begin: depth order in the wrong buffer");
+        rc = exclusive_scan(ws.counts, ws.perm_a, N, ws.offsets,
+                            (int64_t *)&ws.stats->scan_total, ws.scan_ws, ws.scan_bytes, s);
+        if (rc != MG_OK) return rc;
+    }
+    MG_HIP(hipEventSynchronize(rb.ev));
+    const int64_t total = *rb.slot;
+    MG_REQUIRE(total >= 0 && total < (1LL << 31),
+               "mg_bin_lists_begin: %lld intersections exceed int32", (long long)total);
+    if (total_host) *total_host = total;
+    return MG_OK;
 }
 
 int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy, const float *conic,
@@ -941,7 +954,7 @@ int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy, const 
         int32_t *rv;
         rc = radix_sort_passes<uint32_t>(tk_a, ids_a, tk_b, ids_b, total, 0, bits, sort_ws,
                                          sort_bytes, s, "tile_sort", &res_tiles, &rv, 0u,
-                                         0xFFFFFFFFu);
+                                         0xFFFFFFFFu, nullptr);
         if (rc != MG_OK) return rc;
         MG_REQUIRE(rv == gauss_ids, "mg_bin_lists_finish: ids landed in the wrong buffer");
     }

@@ -25,6 +25,24 @@ struct TimedScope {
     int slot_;
 };
 
+// A pinned host word and an event of the current device, held (locked) for
+// the life of the object: a host read that must not stall the stream copies
+// its value into `slot`, records `ev`, queues further work, and only then
+// waits on `ev`. ok() is false (with the error set) if allocation failed.
+class HostReadback {
+  public:
+    HostReadback();
+    ~HostReadback();
+    HostReadback(const HostReadback &) = delete;
+    HostReadback &operator=(const HostReadback &) = delete;
+    bool ok() const { return slot != nullptr; }
+    int64_t *slot = nullptr;
+    hipEvent_t ev = nullptr;
+
+  private:
+    void *lock_;
+};
+
 inline hipStream_t as_stream(mg_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -9,6 +9,15 @@ namespace mg {
 // Workspace bytes for sorting n pairs.
 int64_t sort_ws_bytes(int64_t n);
 
+// A key window in device memory, for sorts queued before the host knows the
+// key range: digits come from min(key, hi) - lo, and passes at or above
+// `bits` only copy (their digits are all 0).
+template <typename K>
+struct DevWin {
+    K lo, hi;
+    int32_t bits;
+};
+
 // Stable LSD sort of (key, int32 value) pairs on key bits [begin_bit,
 // end_bit), 8 bits per pass. Result in keys_out/vals_out; the inputs are
 // clobbered (ping-pong). Instantiated for uint32_t and uint64_t keys.
@@ -20,13 +29,14 @@ int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *val
 // The passes only: the sorted data stays in whichever ping-pong buffer the
 // last pass wrote (*res_k, *res_v), saving the final copy when the pass count
 // is even. Digits come from min(key, hi) - lo, so keys known to lie in
-// [lo, hi] sort on bits [0, bit_width(hi - lo)) alone. Instantiated for
-// uint32_t keys.
+// [lo, hi] sort on bits [0, bit_width(hi - lo)) alone. With dw (device) the
+// window and live bit count are read on the device instead of lo/hi, and
+// passes at or above dw->bits copy. Instantiated for uint32_t keys.
 template <typename K>
 int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *vals_out,
                           int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
                           hipStream_t s, const char *who, K **res_k, int32_t **res_v, K lo,
-                          K hi);
+                          K hi, const DevWin<K> *dw);
 
 // Workspace bytes for an exclusive scan of n int32 values.
 int64_t scan_ws_bytes(int64_t n);

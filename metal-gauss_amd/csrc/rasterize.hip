@@ -492,7 +492,7 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
     const float gr = inimg ? G.grad_rgb[3 * o] : 0.f;
     const float gg = inimg ? G.grad_rgb[3 * o + 1] : 0.f;
     const float gb = inimg ? G.grad_rgb[3 * o + 2] : 0.f;
-    float ga = inimg ? G.grad_alpha[o] : 0.f;
+    float ga = inimg && G.grad_alpha ? G.grad_alpha[o] : 0.f;
     // The background blend's share: d rgb_out / d alpha = -bg where
     // 1 - alpha >= 0 (torch's clamp_min passes the gradient at the bound).
     if (A.has_bg && inimg && 1.0f - G.alpha[o] >= 0.0f)
@@ -798,7 +798,7 @@ int32_t mg_rasterize_backward(int64_t N, const float *uv, const float *conic,
     int32_t rc = check_raster("rasterize_backward", N, uv, conic, opacity, color, gauss_ids,
                               tile_offsets, W, H, tile, tiles_x);
     if (rc != MG_OK) return rc;
-    MG_REQUIRE(final_T && stop && grad_rgb && grad_alpha, "rasterize_backward: null input");
+    MG_REQUIRE(final_T && stop && grad_rgb, "rasterize_backward: null input");
     MG_REQUIRE(!background || alpha, "rasterize_backward: a background needs the forward's alpha");
     MG_REQUIRE(N == 0 || (d_uv && d_conic && d_opacity && d_color),
                "rasterize_backward: null gradient output");

@@ -92,6 +92,52 @@ TimedScope::~TimedScope() {
     (void)hipEventRecord(g_pending[slot_].b, stream_);
 }
 
+// ---------------------------------------------------------- host readback
+namespace {
+struct ReadbackSlot {
+    int64_t *slot = nullptr;
+    hipEvent_t ev = nullptr;
+    std::mutex mu;
+};
+std::mutex g_rbmu;
+std::unordered_map<int, ReadbackSlot *> g_rb;   // per device, kept until exit
+}  // namespace
+
+HostReadback::HostReadback() : lock_(nullptr) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        set_error("host readback: hipGetDevice failed");
+        return;
+    }
+    ReadbackSlot *r;
+    {
+        std::lock_guard<std::mutex> lk(g_rbmu);
+        auto it = g_rb.find(dev);
+        if (it == g_rb.end()) it = g_rb.emplace(dev, new ReadbackSlot).first;
+        r = it->second;
+    }
+    r->mu.lock();
+    lock_ = r;
+    if (!r->slot) {
+        void *p = nullptr;
+        if (hipHostMalloc(&p, 256, hipHostMallocDefault) != hipSuccess) {
+            set_error("host readback: hipHostMalloc failed");
+            return;
+        }
+        r->slot = static_cast<int64_t *>(p);
+    }
+    if (!r->ev && hipEventCreateWithFlags(&r->ev, hipEventDisableTiming) != hipSuccess) {
+        set_error("host readback: hipEventCreateWithFlags failed");
+        return;
+    }
+    slot = r->slot;
+    ev = r->ev;
+}
+
+HostReadback::~HostReadback() {
+    if (lock_) static_cast<ReadbackSlot *>(lock_)->mu.unlock();
+}
+
 }  // namespace mg
 
 extern "C" {

@@ -51,12 +51,29 @@ __device__ __forceinline__ uint32_t digit_of(K key, int shift, uint32_t mask, Ke
     return (uint32_t)(((key < w.hi ? key : w.hi) - w.lo) >> shift) & mask;
 }
 
+// The window a pass uses: the by-value one, or the device-resident one
+// (dw != NULL), whose bit count also marks passes at or above it as plain
+// copies (all their digits are 0, so a stable pass would not move a key).
+template <typename K>
+__device__ __forceinline__ KeyWin<K> pass_window(KeyWin<K> win, const DevWin<K> *dw, int shift,
+                                                 bool &copy) {
+    copy = false;
+    if (dw == nullptr) return win;
+    copy = shift >= dw->bits;
+    return KeyWin<K>{dw->lo, dw->hi};
+}
+
 template <typename K, int kSortItems>
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const K *keys, int64_t n,
                                                                      int shift, uint32_t mask,
-                                                                     KeyWin<K> win, uint32_t *hist,
+                                                                     KeyWin<K> win0,
+                                                                     const DevWin<K> *dw,
+                                                                     uint32_t *hist,
                                                                      int64_t ntiles) {
     __shared__ uint32_t s_h[kSortWaves][kRadix];
+    bool copy;
+    const KeyWin<K> win = pass_window(win0, dw, shift, copy);
+    if (copy) return;   // whole workgroup
     const int wave = threadIdx.x >> 6;
     for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads) (&s_h[0][0])[i] = 0;
     __syncthreads();
@@ -79,8 +96,10 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const K *ke
 // One workgroup per digit: exclusive scan of hist[d][0..ntiles) in place,
 // digit total to totals[d].
 __global__ __launch_bounds__(kSortThreads) void radix_scan_kernel(uint32_t *hist, int64_t ntiles,
-                                                                  uint32_t *totals) {
+                                                                  uint32_t *totals, int shift,
+                                                                  const int32_t *dbits) {
     __shared__ uint32_t s_w[kSortWaves];
+    if (dbits && shift >= *dbits) return;   // a copy pass: nothing to scan
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     uint32_t *row = hist + (int64_t)blockIdx.x * ntiles;
     uint32_t carry = 0;
@@ -124,8 +143,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_scan_kernel(uint32_t *hist
 template <typename K, int kSortItems>
 __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     const K *keys_in, const int32_t *vals_in, K *keys_out, int32_t *vals_out, int64_t n,
-    int shift, uint32_t mask, KeyWin<K> win, const uint32_t *hist, int64_t ntiles,
-    const uint32_t *totals) {
+    int shift, uint32_t mask, KeyWin<K> win0, const DevWin<K> *dw, const uint32_t *hist,
+    int64_t ntiles, const uint32_t *totals) {
     constexpr int kSortTile = kSortThreads * kSortItems;
     constexpr int kChunk = kSortTile / kSortWaves;       // keys per wave
     __shared__ K s_keys[kSortTile];
@@ -139,6 +158,16 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     const int64_t base = (int64_t)blockIdx.x * kSortTile;
     const int nitems = (int)min((int64_t)kSortTile, n - base);
     const int nbits = 32 - __builtin_clz(mask);          // live digit bits (mask = 2^b - 1)
+    bool copy;
+    const KeyWin<K> win = pass_window(win0, dw, shift, copy);
+    if (copy) {
+        // Every digit of this pass is 0: the stable order is the input order.
+        for (int i = tid; i < nitems; i += kSortThreads) {
+            keys_out[base + i] = keys_in[base + i];
+            vals_out[base + i] = vals_in[base + i];
+        }
+        return;
+    }
 
     // Global digit bases: exclusive scan of the digit totals (one digit per
     // thread), plus this tile's exclusive prefix within the digit.
@@ -263,7 +292,7 @@ template <typename K>
 int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *vals_out,
                           int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
                           hipStream_t s, const char *who, K **res_k, int32_t **res_v, K lo,
-                          K hi) {
+                          K hi, const DevWin<K> *dw) {
     MG_REQUIRE(n >= 0 && n < (1LL << 31), "%s: n = %lld", who, (long long)n);
     MG_REQUIRE(begin_bit >= 0 && end_bit <= (int)(8 * sizeof(K)) && begin_bit <= end_bit,
                "%s: bit range [%d, %d)", who, begin_bit, end_bit);
@@ -286,13 +315,14 @@ int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *va
         const int width = min(8, end_bit - b);
         const uint32_t mask = (1u << width) - 1u;
 #define MG_SORT_PASS(IT)                                                                   \
-    radix_upsweep_kernel<K, IT><<<(unsigned)ntiles, kSortThreads, 0, s>>>(src_k, n, b, mask, \
-                                                                          win, hist, ntiles); \
+    radix_upsweep_kernel<K, IT><<<(unsigned)ntiles, kSortThreads, 0, s>>>(                 \
+        src_k, n, b, mask, win, dw, hist, ntiles);                                         \
     MG_LAUNCHED("radix_upsweep_kernel");                                                   \
-    radix_scan_kernel<<<kRadix, kSortThreads, 0, s>>>(hist, ntiles, totals);               \
+    radix_scan_kernel<<<kRadix, kSortThreads, 0, s>>>(hist, ntiles, totals, b,             \
+                                                      dw ? &dw->bits : nullptr);           \
     MG_LAUNCHED("radix_scan_kernel");                                                      \
     radix_downsweep_kernel<K, IT><<<(unsigned)ntiles, kSortThreads, 0, s>>>(               \
-        src_k, src_v, dst_k, dst_v, n, b, mask, win, hist, ntiles, totals);                \
+        src_k, src_v, dst_k, dst_v, n, b, mask, win, dw, hist, ntiles, totals);            \
     MG_LAUNCHED("radix_downsweep_kernel");
         if (items == 16) { MG_SORT_PASS(16) }
         else if (items == 8) { MG_SORT_PASS(8) }
@@ -313,7 +343,8 @@ int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *val
     K *rk;
     int32_t *rv;
     int32_t rc = radix_sort_passes<K>(keys_in, vals_in, keys_out, vals_out, n, begin_bit,
-                                      end_bit, ws, ws_bytes, s, who, &rk, &rv, K(0), ~K(0));
+                                      end_bit, ws, ws_bytes, s, who, &rk, &rv, K(0), ~K(0),
+                                      nullptr);
     if (rc != MG_OK) return rc;
     if (n > 0 && rk != keys_out) {
         MG_HIP(hipMemcpyAsync(keys_out, rk, n * sizeof(K), hipMemcpyDeviceToDevice, s));
@@ -329,7 +360,7 @@ template int32_t radix_sort_pairs<uint64_t>(uint64_t *, int32_t *, uint64_t *, i
 template int32_t radix_sort_passes<uint32_t>(uint32_t *, int32_t *, uint32_t *, int32_t *,
                                              int64_t, int, int, void *, int64_t, hipStream_t,
                                              const char *, uint32_t **, int32_t **, uint32_t,
-                                             uint32_t);
+                                             uint32_t, const DevWin<uint32_t> *);
 
 }  // namespace mg
 

@@ -73,9 +73,10 @@ class _SSIMFused(torch.autograd.Function):
 
 
 class _PhotometricLoss(torch.autograd.Function):
-    """[loss, L1 mean, SSIM mean] with loss = (1 - w) * mean|a - b| +
-    w * (1 - mean SSIM(a, b)). Only the loss entry carries a gradient (to
-    ``a``); the wrapper detaches the other two."""
+    """(loss, [L1 mean, SSIM mean]) with loss = (1 - w) * mean|a - b| +
+    w * (1 - mean SSIM(a, b)). Only the loss carries a gradient (to ``a``);
+    the parts are non-differentiable, and no zero gradient is materialised
+    for them."""
 
     @staticmethod
     def forward(ctx, a, b, win, ssim_weight):
@@ -97,14 +98,19 @@ class _PhotometricLoss(torch.autograd.Function):
             out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(a)))
         ctx.save_for_backward(a, b, win, partials)
         ctx.ssim_weight = float(ssim_weight)
-        return out
+        ctx.set_materialize_grads(False)
+        loss, parts = out[0], out[1:]
+        ctx.mark_non_differentiable(parts)
+        return loss, parts
 
     @staticmethod
-    def backward(ctx, grad_out):
+    def backward(ctx, grad_loss, grad_parts):
+        if grad_loss is None:
+            return None, None, None, None
         lib = _lib.load()
         a, b, win, partials = ctx.saved_tensors
         H, W = a.shape[0], a.shape[1]
-        g = grad_out.detach().to(torch.float32).reshape(-1)[:1].contiguous()
+        g = grad_loss.detach().to(torch.float32).reshape(1).contiguous()
         d_a = torch.empty_like(a)
         _lib.check(lib.mg_photometric_loss_backward(
             a.data_ptr(), b.data_ptr(), win.data_ptr(), partials.data_ptr(),
@@ -122,8 +128,7 @@ def photometric_loss(a: torch.Tensor, b: torch.Tensor, kernel: torch.Tensor,
     gradient equal the two-term torch expression up to float rounding.
     """
     w = kernel.reshape(-1, kernel.shape[-1])[0] if kernel.dim() > 1 else kernel
-    out = _PhotometricLoss.apply(a, b, w, ssim_weight)
-    return out[0], out[1:].detach()
+    return _PhotometricLoss.apply(a, b, w, ssim_weight)
 
 
 def ssim(a: torch.Tensor, b: torch.Tensor, kernel: torch.Tensor) -> torch.Tensor:

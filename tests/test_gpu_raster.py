@@ -80,7 +80,8 @@ def gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile, absgrad=True, back
     _lib.check(lib.mg_rasterize_backward(
         N, uv.data_ptr(), conic.data_ptr(), op.data_ptr(), col.data_ptr(), gids.data_ptr(),
         offs.data_ptr(), T.data_ptr(), stop.data_ptr(), grad_rgb.data_ptr(),
-        grad_alpha.data_ptr(), alpha.data_ptr() if background is not None else None,
+        None if grad_alpha is None else grad_alpha.data_ptr(),
+        alpha.data_ptr() if background is not None else None,
         None if background is None else _lib.f32_array(background), gids.numel(),
         None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), W, H, tile, tx,
         *[o.data_ptr() if o is not None else None for o in outs], _lib.stream(uv)))
@@ -251,3 +252,17 @@ def test_chunked_backward_on_long_lists(dev, tile, t_min):
         assert torch.isfinite(a).all(), name
         assert rel_l2(np_(a), c) < 1e-3, f"{name} vs contract {rel_l2(np_(a), c):.2e}"
         assert rel_l2(a.cpu(), b.cpu()) < 1e-4, f"{name} chunked vs whole {rel_l2(a.cpu(), b.cpu()):.2e}"
+
+
+def test_missing_alpha_gradient_reads_as_zero(dev):
+    """grad_alpha NULL (the coverage feeds no loss; render's autograd passes
+    no materialised zeros) equals an explicit zero gradient."""
+    W, H, tile = 100, 63, 16
+    args = prepare(600, 37, W, H, tile, dev, elongate=True)
+    fwd = gpu_forward(args, W, H, tile, 1e-4, chunked=False)
+    g = torch.Generator().manual_seed(9)
+    grad_rgb = torch.randn(H, W, 3, generator=g).to(dev)
+    none = gpu_backward(args, fwd, grad_rgb, None, W, H, tile)
+    zero = gpu_backward(args, fwd, grad_rgb, torch.zeros(H, W, device=dev), W, H, tile)
+    for a, b in zip(none, zero):
+        assert rel_l2(a.cpu(), b.cpu()) < 1e-6
