@@ -239,19 +239,19 @@ __device__ __forceinline__ float mip2_coef(const Proj &P) {
 // In round r lane L works on the wave's Gaussian 16 r + L / 4, bases
 // 4 (L % 4) .. 4 (L % 4) + 3.
 
+// Orders a wave's LDS writes before its following LDS reads (lanes read what
+// other lanes of the same wave wrote).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Sum over the four lanes of a quad, in every lane of it.
 __device__ __forceinline__ float quad_sum(float v) {
     v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
     v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
     return v;
-}
-
-// This lane's four basis values out of the sixteen (q = lane % 4), without
-// dynamic register indexing.
-__device__ __forceinline__ void pick4(const float B[16], int q, float b[4]) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        b[k] = q == 0 ? B[k] : (q == 1 ? B[4 + k] : (q == 2 ? B[8 + k] : B[12 + k]));
 }
 
 struct ShRows {
@@ -436,40 +436,60 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFw
         if (in) { A.color[3 * g] = 0.f; A.color[3 * g + 1] = 0.f; A.color[3 * g + 2] = 0.f; }
         return;
     }
-    float ux = 0.f, uy = 0.f, uz = 0.f;   // unit view direction
-    if (ok) {
-        const float dx = mx - C.cc[0], dy = my - C.cc[1], dz = mz - C.cc[2];
-        const float inv = 1.0f / fmaxf(sqrtf(dx * dx + dy * dy + dz * dz), 1e-12f);
-        ux = dx * inv; uy = dy * inv; uz = dz * inv;
+    // Basis values once per Gaussian (lane = Gaussian), parked in LDS for
+    // the quads.
+    __shared__ float s_b[kPreThreads / 64][64 * 16];
+    float *bw = s_b[wave];
+    {
+        float B[16] = {};
+        if (ok) {
+            const float dx = mx - C.cc[0], dy = my - C.cc[1], dz = mz - C.cc[2];
+            const float inv = 1.0f / fmaxf(sqrtf(dx * dx + dy * dy + dz * dz), 1e-12f);
+            sh_basis(C.deg, dx * inv, dy * inv, dz * inv, B);
+        }
+        float4 *dst = reinterpret_cast<float4 *>(bw + 16 * lane);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            dst[k] = make_float4(B[4 * k], B[4 * k + 1], B[4 * k + 2], B[4 * k + 3]);
     }
+    wave_lds_sync();
 
     // ---------------------------------------------- SH colour: quad = Gaussian
+    // Four rounds of 16 Gaussians; each round requests the next one's
+    // coefficients before its own arithmetic.
     const int nb = (C.deg + 1) * (C.deg + 1);
     const ShRows R{A.sh, A.rest, A.fused, A.vec4};
     const int q = lane & 3;
+    float c[4][3] = {};
+    bool okq = __shfl((int)ok, lane >> 2, 64) != 0;     // false past the end
+    if (okq) load_bases(R, g0 + (lane >> 2), q, nb, c);
 #pragma unroll 1
     for (int r = 0; r < 4; ++r) {
         const int gl = 16 * r + (lane >> 2);
         const int64_t G = g0 + gl;
-        const bool okq = __shfl((int)ok, gl, 64) != 0;     // false past the end
-        const float x = __shfl(ux, gl, 64), y = __shfl(uy, gl, 64), z = __shfl(uz, gl, 64);
-        float part[3] = {0.f, 0.f, 0.f};
-        if (okq) {
-            float c[4][3], b[4];
-            load_bases(R, G, q, nb, c);
-            float B[16] = {};
-            sh_basis(C.deg, x, y, z, B);
-            pick4(B, q, b);
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-#pragma unroll
-                for (int ch = 0; ch < 3; ++ch) part[ch] += b[k] * c[k][ch];
+        float cn[4][3] = {};
+        bool okn = false;
+        if (r < 3) {
+            okn = __shfl((int)ok, gl + 16, 64) != 0;
+            if (okn) load_bases(R, G + 16, q, nb, cn);
         }
+        const float4 bq = *reinterpret_cast<const float4 *>(bw + 16 * gl + 4 * q);
+        const float b[4] = {bq.x, bq.y, bq.z, bq.w};
+        float part[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int ch = 0; ch < 3; ++ch) part[ch] += b[k] * c[k][ch];
         const float s0 = quad_sum(part[0]), s1 = quad_sum(part[1]), s2 = quad_sum(part[2]);
         if (G < A.N && q < 3) {
             const float sv = q == 0 ? s0 : (q == 1 ? s1 : s2);
             A.color[3 * G + q] = okq ? fmaxf(sv + 0.5f, 0.0f) : 0.0f;
         }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int ch = 0; ch < 3; ++ch) c[k][ch] = cn[k][ch];
+        okq = okn;
     }
 }
 
@@ -504,8 +524,28 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
         vld = A.valid[g];
     }
     float dmean[3] = {0.f, 0.f, 0.f};
+    // The projection's inputs, requested now so they arrive during the SH
+    // phase.
+    float qv[4] = {0.f, 0.f, 0.f, 0.f}, sraw[3] = {0.f, 0.f, 0.f};
+    float k0 = 0.f, k1 = 0.f, k2 = 0.f, du = 0.f, dv = 0.f;
+    if (in) {
+        qv[0] = A.quats[4 * g]; qv[1] = A.quats[4 * g + 1];
+        qv[2] = A.quats[4 * g + 2]; qv[3] = A.quats[4 * g + 3];
+        sraw[0] = A.scales[3 * g]; sraw[1] = A.scales[3 * g + 1]; sraw[2] = A.scales[3 * g + 2];
+        k0 = A.d_conic[3 * g]; k1 = A.d_conic[3 * g + 1]; k2 = A.d_conic[3 * g + 2];
+        du = A.d_uv[2 * g]; dv = A.d_uv[2 * g + 1];
+    }
 
-    // ------------------------------------------------ SH: quad = Gaussian
+    // --------------------------------------------------------------- SH
+    // A (lane = Gaussian): view direction and the 16 basis values, parked in
+    //   LDS. B (quad = Gaussian, four rounds of 16, the next round's
+    //   coefficients loaded during this one): the quad's four bases and
+    //   coefficients give the colour for the ReLU gate, d_sh, and the four
+    //   per-basis weights w_b = c_b . dcolour, which overwrite those bases in
+    //   LDS. C (lane = Gaussian): one VJP of the 16 bases with those weights
+    //   gives the direction gradient. The basis values and the VJP are thus
+    //   evaluated once per Gaussian rather than once per quad lane.
+    __shared__ float s_bw[kPreThreads / 64][64 * 16];
     if (A.d_color != nullptr) {
         float dcol[3] = {0.f, 0.f, 0.f};
         if (in) { dcol[0] = A.d_color[3 * g]; dcol[1] = A.d_color[3 * g + 1]; dcol[2] = A.d_color[3 * g + 2]; }
@@ -522,67 +562,87 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
                 for (int e = lane; e < ng * 45; e += 64) A.d_rest[g0 * 45 + e] = 0.f;
             }
         } else {
+            float *bw = s_bw[wave];
             float ux = 0.f, uy = 0.f, uz = 0.f, un = 1.f;
-            if (need) {
-                const float vx = mx - C.cc[0], vy = my - C.cc[1], vz = mz - C.cc[2];
-                un = fmaxf(sqrtf(vx * vx + vy * vy + vz * vz), 1e-12f);
-                ux = vx / un; uy = vy / un; uz = vz / un;
+            {
+                float B[16] = {};
+                if (need) {
+                    const float vx = mx - C.cc[0], vy = my - C.cc[1], vz = mz - C.cc[2];
+                    un = fmaxf(sqrtf(vx * vx + vy * vy + vz * vz), 1e-12f);
+                    ux = vx / un; uy = vy / un; uz = vz / un;
+                    sh_basis(C.deg, ux, uy, uz, B);
+                }
+                float4 *dst = reinterpret_cast<float4 *>(bw + 16 * lane);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    dst[k] = make_float4(B[4 * k], B[4 * k + 1], B[4 * k + 2], B[4 * k + 3]);
             }
+            wave_lds_sync();
             const int nb = (C.deg + 1) * (C.deg + 1);
             const ShRows R{A.sh, A.rest, A.fused, A.vec4};
             const int q = lane & 3;
+            // Round 0's coefficients; each round then requests the next one's.
+            float c[4][3] = {};
+            bool nq = __shfl((int)need, lane >> 2, 64) != 0;
+            if (nq) load_bases(R, g0 + (lane >> 2), q, nb, c);
 #pragma unroll 1
             for (int r = 0; r < 4; ++r) {
                 const int gl = 16 * r + (lane >> 2);
                 const int64_t G = g0 + gl;
-                const bool nq = __shfl((int)need, gl, 64) != 0;
-                const float x = __shfl(ux, gl, 64), y = __shfl(uy, gl, 64);
-                const float z = __shfl(uz, gl, 64), n = __shfl(un, gl, 64);
+                float cn[4][3] = {};
+                bool nqn = false;
+                if (r < 3) {
+                    nqn = __shfl((int)need, gl + 16, 64) != 0;
+                    if (nqn) load_bases(R, G + 16, q, nb, cn);
+                }
                 const float d0 = __shfl(dcol[0], gl, 64), d1 = __shfl(dcol[1], gl, 64);
                 const float d2 = __shfl(dcol[2], gl, 64);
-                float c[4][3] = {}, b[4] = {0.f, 0.f, 0.f, 0.f};
+                const float4 bq = *reinterpret_cast<const float4 *>(bw + 16 * gl + 4 * q);
+                const float b[4] = {bq.x, bq.y, bq.z, bq.w};
                 float pre[3] = {0.f, 0.f, 0.f};
-                if (nq) {
-                    load_bases(R, G, q, nb, c);
-                    float B[16] = {};
-                    sh_basis(C.deg, x, y, z, B);
-                    pick4(B, q, b);
 #pragma unroll
-                    for (int k = 0; k < 4; ++k)
+                for (int k = 0; k < 4; ++k)
 #pragma unroll
-                        for (int ch = 0; ch < 3; ++ch) pre[ch] += b[k] * c[k][ch];
-                }
+                    for (int ch = 0; ch < 3; ++ch) pre[ch] += b[k] * c[k][ch];
                 const float p0 = quad_sum(pre[0]) + 0.5f, p1 = quad_sum(pre[1]) + 0.5f;
                 const float p2 = quad_sum(pre[2]) + 0.5f;
                 // ReLU gate of colour = max(pre, 0) (torch_ref.py:331).
                 const float dp0 = p0 > 0.f ? d0 : 0.f, dp1 = p1 > 0.f ? d1 : 0.f;
                 const float dp2 = p2 > 0.f ? d2 : 0.f;
                 float dsh[4][3];
-                float w16[16];
                 float wk[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     dsh[k][0] = nq ? b[k] * dp0 : 0.f;
                     dsh[k][1] = nq ? b[k] * dp1 : 0.f;
                     dsh[k][2] = nq ? b[k] * dp2 : 0.f;
-                    wk[k] = c[k][0] * dp0 + c[k][1] * dp1 + c[k][2] * dp2;
+                    wk[k] = nq ? c[k][0] * dp0 + c[k][1] * dp1 + c[k][2] * dp2 : 0.f;
                 }
-#pragma unroll
-                for (int i = 0; i < 16; ++i) w16[i] = (i >> 2) == q && nq ? wk[i & 3] : 0.f;
                 if (G < A.N) store_bases(A.d_sh, A.d_rest, A.fused, A.st_vec4, G, q, dsh);
-                float gp[3] = {0.f, 0.f, 0.f};
-                if (nq) sh_basis_vjp(C.deg, x, y, z, w16, gp);
-                const float g0s = quad_sum(gp[0]), g1s = quad_sum(gp[1]), g2s = quad_sum(gp[2]);
+                *reinterpret_cast<float4 *>(bw + 16 * gl + 4 * q) =
+                    make_float4(wk[0], wk[1], wk[2], wk[3]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+#pragma unroll
+                    for (int ch = 0; ch < 3; ++ch) c[k][ch] = cn[k][ch];
+                nq = nqn;
+            }
+            wave_lds_sync();
+            if (need) {
+                float w16[16];
+                const float4 *src = reinterpret_cast<const float4 *>(bw + 16 * lane);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float4 v = src[k];
+                    w16[4 * k] = v.x; w16[4 * k + 1] = v.y; w16[4 * k + 2] = v.z; w16[4 * k + 3] = v.w;
+                }
+                float gp[3];
+                sh_basis_vjp(C.deg, ux, uy, uz, w16, gp);
                 // dir = v/|v|: d v = (I - dir dir^T) d dir / |v|
-                const float dd = x * g0s + y * g1s + z * g2s;
-                const float m0 = nq ? (g0s - x * dd) / n : 0.f;
-                const float m1 = nq ? (g1s - y * dd) / n : 0.f;
-                const float m2 = nq ? (g2s - z * dd) / n : 0.f;
-                // Back to the lane that owns the Gaussian.
-                const int src = 4 * (lane & 15);
-                const float v0 = __shfl(m0, src, 64), v1 = __shfl(m1, src, 64);
-                const float v2 = __shfl(m2, src, 64);
-                if ((lane >> 4) == r) { dmean[0] += v0; dmean[1] += v1; dmean[2] += v2; }
+                const float dd = ux * gp[0] + uy * gp[1] + uz * gp[2];
+                dmean[0] += (gp[0] - ux * dd) / un;
+                dmean[1] += (gp[1] - uy * dd) / un;
+                dmean[2] += (gp[2] - uz * dd) / un;
             }
         }
     }
@@ -590,8 +650,6 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
 
     // ------------------------------------------ projection: lane = Gaussian
     if (vld != 0) {
-        const float qv[4] = {A.quats[4 * g], A.quats[4 * g + 1], A.quats[4 * g + 2], A.quats[4 * g + 3]};
-        const float sraw[3] = {A.scales[3 * g], A.scales[3 * g + 1], A.scales[3 * g + 2]};
         float sv[3] = {sraw[0], sraw[1], sraw[2]};
         Mip3 M3;
         M3.coef = 1.0f;
@@ -607,7 +665,6 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
         const float id = 1.0f / fmaxf(det, 1e-12f);
 
         // conic = (c, -b, a) / det
-        const float k0 = A.d_conic[3 * g], k1 = A.d_conic[3 * g + 1], k2 = A.d_conic[3 * g + 2];
         const float ddet = -(k0 * c - k1 * b + k2 * a) * id * id;
         float da = k2 * id + ddet * c;
         float db = -k1 * id - 2.0f * ddet * b;
@@ -678,7 +735,6 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
         float dzc = -C.fx * izc2 * dj0x - C.fy * izc2 * dj1y +
                     2.0f * C.fx * P.tx * izc3 * dj0z + 2.0f * C.fy * P.ty * izc3 * dj1z;
         // u = fx px/zc + cx, v = fy py/zc + cy
-        const float du = A.d_uv[2 * g], dv = A.d_uv[2 * g + 1];
         float dpx = C.fx * izc * du;
         float dpy = C.fy * izc * dv;
         dzc += -C.fx * P.p[0] * izc2 * du - C.fy * P.p[1] * izc2 * dv;
