@@ -90,12 +90,16 @@ int32_t mg_preprocess_forward(
  * (metal_gauss/csrc/rasterize.mm:286-327; kernel preprocess.metal:223-411).
  * d_color may be NULL (explicit-colour callers): the SH branch is skipped and
  * d_sh / d_sh_rest are not written. In fused mode d_sh is (N,16,3) and
- * d_sh_rest is ignored (the reference aliases the two, rasterize.mm:300-302). */
+ * d_sh_rest is ignored (the reference aliases the two, rasterize.mm:300-302).
+ * grad_stride 0: d_uv (N,2), d_conic (N,3), d_color (N,3) are separate
+ * arrays; otherwise all three (and d_opacity_eff below) are read at
+ * pointer + i * grad_stride floats for Gaussian i, e.g. slots 0, 2, 6 (and 5)
+ * of mg_rasterize_backward's gradient records with grad_stride 10. */
 int32_t mg_preprocess_backward(
     int64_t N, const float *means, const float *quats, const float *scales,
     const float *sh, const float *sh_rest, int32_t sh_fused,
     const float *d_uv, const float *d_conic, const float *d_color,
-    const int32_t *valid, const float *viewmat, float fx, float fy, float cx,
+    int32_t grad_stride, const int32_t *valid, const float *viewmat, float fx, float fy, float cx,
     float cy, int32_t W, int32_t H, float near_plane, float far_plane,
     float blur, float max_radius, const float *cam_center, int32_t sh_degree,
     float *d_means, float *d_quats, float *d_scales, float *d_sh,
@@ -133,7 +137,7 @@ int32_t mg_preprocess_backward_mip(
     int64_t N, const float *means, const float *quats, const float *scales,
     const float *sh, const float *sh_rest, int32_t sh_fused,
     const float *d_uv, const float *d_conic, const float *d_color,
-    const int32_t *valid, const float *viewmat, float fx, float fy, float cx,
+    int32_t grad_stride, const int32_t *valid, const float *viewmat, float fx, float fy, float cx,
     float cy, int32_t W, int32_t H, float near_plane, float far_plane,
     float blur, float max_radius, const float *cam_center, int32_t sh_degree,
     const float *opacities, const float *filter_3d, int32_t antialias,
@@ -354,10 +358,14 @@ int32_t mg_rasterize_forward(
     int32_t *out_stop, mg_stream_t stream);
 
 /* Back-to-front replay of mg_rasterize_forward. Replaces rasterize_backward
- * (metal_gauss/csrc/rasterize.mm:147-194; kernel rasterize.metal:173-340).
- * Overwrites d_uv (N,2), d_conic (N,3), d_opacity (N,), d_color (N,3); when
- * d_absuv is not NULL it also overwrites d_absuv (N,) with the per-pixel sum
- * of |d_uv| (the reference's absgrad statistic). grad_alpha may be NULL
+ * (metal_gauss/csrc/rasterize.mm:147-194; kernel rasterize.metal:173-340),
+ * whose five gradient tensors come back here as one record of 10 floats per
+ * Gaussian in d_grads (N,10), overwritten: d_uv (slots 0-1), d_conic (2-4),
+ * d_opacity (5), d_color (6-8) and, when absgrad != 0, the per-pixel sum of
+ * |d_uv| (9; the reference's absgrad statistic; 0 otherwise). The record
+ * layout lets the kernel's cross-tile float atomics update one record with
+ * consecutive lanes; strided views give the five tensors (see
+ * mg_preprocess_backward's grad_stride). grad_alpha may be NULL
  * (a zero gradient, when the coverage is not used). With the forward's
  * background (host, or NULL), grad_rgb is the gradient of the blended colour
  * and alpha (the forward's out_alpha, device) adds the blend's share to
@@ -369,8 +377,8 @@ int32_t mg_rasterize_backward(
     const float *final_T, const int32_t *stop, const float *grad_rgb,
     const float *grad_alpha, const float *alpha, const float *background,
     int64_t n_isect, const void *chunk_ws, int64_t chunk_ws_bytes, int32_t W,
-    int32_t H, int32_t tile, int32_t tiles_x, float *d_uv, float *d_conic,
-    float *d_opacity, float *d_color, float *d_absuv, mg_stream_t stream);
+    int32_t H, int32_t tile, int32_t tiles_x, float *d_grads, int32_t absgrad,
+    mg_stream_t stream);
 
 /* ------------------------------------------------------------------- Adam */
 

@@ -261,6 +261,40 @@ def _camera(K, viewmat):
     return fx, fy, cx, cy, vm_h, cam_center
 
 
+# Slots of the rasteriser backward's per-Gaussian gradient record
+# (mg_rasterize_backward): d_uv 0-1, d_conic 2-4, d_opacity 5, d_color 6-8,
+# sum |d_uv| 9.
+_REC = 10
+
+
+def _grad_inputs(N, dev, d_uv, d_conic, d_color, d_oe, want_color, want_oe):
+    """Pointers and record stride for the preprocess backward's incoming
+    gradients. Row views of one gradient record (what the raster backward
+    hands autograd) are read in place with the record's stride; anything else
+    becomes separate contiguous arrays (zeros for a missing gradient)."""
+    mats = [d_uv, d_conic] + ([d_color] if want_color else [])
+    ts = mats + ([d_oe] if want_oe else [])
+    if all(t is not None and t.device.type == "cuda" and t.dtype == torch.float32 for t in ts):
+        k = d_uv.stride(0)
+        ok = k >= 3 and all(t.dim() == 2 and t.shape[0] == N and t.stride(0) == k and
+                            t.stride(1) == 1 for t in mats)
+        if want_oe:
+            ok = ok and d_oe.dim() == 1 and d_oe.shape[0] == N and d_oe.stride(0) == k
+        if ok:
+            return ([d_uv.data_ptr(), d_conic.data_ptr(),
+                     d_color.data_ptr() if want_color else None,
+                     d_oe.data_ptr() if want_oe else None], k, ())
+
+    def dense(t, shape):
+        return torch.zeros(*shape, device=dev) if t is None else t.contiguous()
+    keep = (dense(d_uv, (N, 2)), dense(d_conic, (N, 3)),
+            dense(d_color, (N, 3)) if want_color else None,
+            dense(d_oe, (N,)) if want_oe else None)
+    ptrs = [None if t is None else _lib.dev_tensor(t, what)
+            for t, what in zip(keep, ("d_uv", "d_conic", "d_color", "d_opacity"))]
+    return ptrs, 0, keep
+
+
 class _PreprocessMetal(torch.autograd.Function):
     """Fused projection + SH colour, forward and analytic backward.
 
@@ -333,14 +367,12 @@ class _PreprocessMetal(torch.autograd.Function):
         if ctx.has_sh:
             d_sh = torch.empty_like(sh)
             d_rest = None if ctx.fused else torch.empty_like(rest)
-            d_color = torch.zeros(N, 3, device=dev) if d_color is None else d_color.contiguous()
-        d_uv = torch.zeros(N, 2, device=dev) if d_uv is None else d_uv.contiguous()
-        d_conic = torch.zeros(N, 3, device=dev) if d_conic is None else d_conic.contiguous()
+        (p_uv, p_conic, p_color, _), stride, keep = _grad_inputs(
+            N, dev, d_uv, d_conic, d_color, None, ctx.has_sh, False)
         _lib.check(lib.mg_preprocess_backward(
             N, means.data_ptr(), quats.data_ptr(), scales.data_ptr(),
             None if sh is None else sh.data_ptr(), None if rest is None else rest.data_ptr(),
-            int(ctx.fused), _lib.dev_tensor(d_uv, "d_uv"), _lib.dev_tensor(d_conic, "d_conic"),
-            None if not ctx.has_sh else _lib.dev_tensor(d_color, "d_color"), valid.data_ptr(),
+            int(ctx.fused), p_uv, p_conic, p_color, stride, valid.data_ptr(),
             _lib.host_f32(viewmat), fx, fy, cx, cy, W, H, near, far, blur, max_radius,
             _lib.host_f32(cam_center), deg, d_means.data_ptr(), d_quats.data_ptr(),
             d_scales.data_ptr(), None if d_sh is None else d_sh.data_ptr(),
@@ -402,11 +434,8 @@ class _RasterizeMetal(torch.autograd.Function):
         bg = ctx.background
         N = uv.shape[0]
         dev = uv.device
-        d_uv = torch.empty(N, 2, device=dev)
-        d_conic = torch.empty(N, 3, device=dev)
-        d_op = torch.empty(N, device=dev)
-        d_col = torch.empty(N, 3, device=dev)
-        d_abs = torch.empty(N, device=dev) if ctx.absgrad_out is not None else None
+        # One gradient record per Gaussian; autograd gets row views of it.
+        rec = torch.empty(N, _REC, device=dev)
         if grad_rgb is None and grad_alpha is None:
             return (None,) * 14
         grad_rgb = torch.zeros(H, W, 3, device=dev) if grad_rgb is None else grad_rgb.contiguous()
@@ -418,12 +447,11 @@ class _RasterizeMetal(torch.autograd.Function):
             None if grad_alpha is None else _lib.dev_tensor(grad_alpha, "grad_alpha"),
             None if bg is None else alpha.data_ptr(), None if bg is None else _lib.f32_array(bg),
             gauss_ids.numel(), chunk_ws.data_ptr() if chunk_ws.numel() else None,
-            chunk_ws.numel(), W, H, tile, tiles_x,
-            d_uv.data_ptr(), d_conic.data_ptr(), d_op.data_ptr(),
-            d_col.data_ptr(), None if d_abs is None else d_abs.data_ptr(), _lib.stream(uv)))
+            chunk_ws.numel(), W, H, tile, tiles_x, rec.data_ptr(),
+            int(ctx.absgrad_out is not None), _lib.stream(uv)))
         if ctx.absgrad_out is not None:
-            ctx.absgrad_out[:N] += d_abs
-        return (d_uv, d_conic, d_op, d_col) + (None,) * 10
+            ctx.absgrad_out[:N] += rec[:, 9]
+        return (rec[:, 0:2], rec[:, 2:5], rec[:, 5], rec[:, 6:9]) + (None,) * 10
 
 
 class _PreprocessMip(torch.autograd.Function):
@@ -508,19 +536,16 @@ class _PreprocessMip(torch.autograd.Function):
         if ctx.has_sh:
             d_sh = torch.empty_like(sh)
             d_rest = None if ctx.fused else torch.empty_like(rest)
-            d_color = torch.zeros(N, 3, device=dev) if d_color is None else d_color.contiguous()
-        d_oe = torch.zeros(N, device=dev) if d_oe is None else d_oe.contiguous()
-        d_uv = torch.zeros(N, 2, device=dev) if d_uv is None else d_uv.contiguous()
-        d_conic = torch.zeros(N, 3, device=dev) if d_conic is None else d_conic.contiguous()
+        (p_uv, p_conic, p_color, p_oe), stride, keep = _grad_inputs(
+            N, dev, d_uv, d_conic, d_color, d_oe, ctx.has_sh, True)
         _lib.check(lib.mg_preprocess_backward_mip(
             N, means.data_ptr(), quats.data_ptr(), scales.data_ptr(),
             None if sh is None else sh.data_ptr(), None if rest is None else rest.data_ptr(),
-            int(ctx.fused), _lib.dev_tensor(d_uv, "d_uv"), _lib.dev_tensor(d_conic, "d_conic"),
-            None if not ctx.has_sh else _lib.dev_tensor(d_color, "d_color"), valid.data_ptr(),
+            int(ctx.fused), p_uv, p_conic, p_color, stride, valid.data_ptr(),
             _lib.host_f32(viewmat), fx, fy, cx, cy, W, H, near, far, blur, max_radius,
             _lib.host_f32(cam_center), deg, opacities.data_ptr(),
             None if filt is None else filt.data_ptr(), int(ctx.antialias),
-            _lib.dev_tensor(d_oe, "d_opacity"), d_means.data_ptr(), d_quats.data_ptr(),
+            p_oe, d_means.data_ptr(), d_quats.data_ptr(),
             d_scales.data_ptr(), None if d_sh is None else d_sh.data_ptr(),
             None if d_rest is None else d_rest.data_ptr(), d_op.data_ptr(), _lib.stream(means)))
         return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 15

@@ -31,7 +31,8 @@ int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *val
 // is even. Digits come from min(key, hi) - lo, so keys known to lie in
 // [lo, hi] sort on bits [0, bit_width(hi - lo)) alone. With dw (device) the
 // window and live bit count are read on the device instead of lo/hi, and
-// passes at or above dw->bits copy. Instantiated for uint32_t keys.
+// passes at or above dw->bits copy the values only: the sorted values are
+// the result, the keys are left unspecified. Instantiated for uint32_t keys.
 template <typename K>
 int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *vals_out,
                           int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,

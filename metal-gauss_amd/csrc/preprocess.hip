@@ -499,6 +499,9 @@ struct PreBwdArgs {
     const float *means, *quats, *scales, *sh, *rest;
     int32_t fused, vec4, st_vec4;
     const float *d_uv, *d_conic, *d_color;
+    // Floats per Gaussian between consecutive d_uv, d_conic, d_color and d_oe
+    // entries: 2, 3, 3, 1 for separate arrays, one record stride otherwise.
+    int32_t su, sk, sc, so;
     const int32_t *valid;
     float *d_means, *d_quats, *d_scales, *d_sh, *d_rest;
     // Mip filters (MIP kernels only): the unfiltered opacity, the 3D filter
@@ -532,8 +535,9 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
         qv[0] = A.quats[4 * g]; qv[1] = A.quats[4 * g + 1];
         qv[2] = A.quats[4 * g + 2]; qv[3] = A.quats[4 * g + 3];
         sraw[0] = A.scales[3 * g]; sraw[1] = A.scales[3 * g + 1]; sraw[2] = A.scales[3 * g + 2];
-        k0 = A.d_conic[3 * g]; k1 = A.d_conic[3 * g + 1]; k2 = A.d_conic[3 * g + 2];
-        du = A.d_uv[2 * g]; dv = A.d_uv[2 * g + 1];
+        const float *kc = A.d_conic + (int64_t)A.sk * g, *ku = A.d_uv + (int64_t)A.su * g;
+        k0 = kc[0]; k1 = kc[1]; k2 = kc[2];
+        du = ku[0]; dv = ku[1];
     }
 
     // --------------------------------------------------------------- SH
@@ -548,7 +552,10 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
     __shared__ float s_bw[kPreThreads / 64][64 * 16];
     if (A.d_color != nullptr) {
         float dcol[3] = {0.f, 0.f, 0.f};
-        if (in) { dcol[0] = A.d_color[3 * g]; dcol[1] = A.d_color[3 * g + 1]; dcol[2] = A.d_color[3 * g + 2]; }
+        if (in) {
+            const float *kd = A.d_color + (int64_t)A.sc * g;
+            dcol[0] = kd[0]; dcol[1] = kd[1]; dcol[2] = kd[2];
+        }
         // The colour of a Gaussian that is not visible is the constant 0, so
         // its coefficients get no gradient.
         const bool need = vld != 0 && (dcol[0] != 0.f || dcol[1] != 0.f || dcol[2] != 0.f);
@@ -676,7 +683,7 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
         // coef3, below).
         float d_op1 = 0.0f;
         if (MIP) {
-            const float d_oe = A.d_oe[g];
+            const float d_oe = A.d_oe[(int64_t)A.so * g];
             d_op1 = d_oe;
             if (A.aa) {
                 const float op1 = A.opac[g] * M3.coef;
@@ -868,10 +875,11 @@ static int32_t preprocess_fwd(int64_t N, const float *means, const float *quats,
 static int32_t preprocess_bwd(int64_t N, const float *means, const float *quats,
                               const float *scales, const float *sh, const float *sh_rest,
                               int32_t sh_fused, const float *d_uv, const float *d_conic,
-                              const float *d_color, const int32_t *valid, const float *viewmat,
-                              float fx, float fy, float cx, float cy, int32_t W, int32_t H,
-                              float near_plane, float far_plane, float blur, float max_radius,
-                              const float *cam_center, int32_t sh_degree, bool mip,
+                              const float *d_color, int32_t grad_stride, const int32_t *valid,
+                              const float *viewmat, float fx, float fy, float cx, float cy,
+                              int32_t W, int32_t H, float near_plane, float far_plane,
+                              float blur, float max_radius, const float *cam_center,
+                              int32_t sh_degree, bool mip,
                               const float *opacities, const float *filter_3d, int32_t antialias,
                               const float *d_opacity_eff, float *d_means, float *d_quats,
                               float *d_scales, float *d_sh, float *d_sh_rest,
@@ -890,6 +898,12 @@ static int32_t preprocess_bwd(int64_t N, const float *means, const float *quats,
     }
     MG_REQUIRE(!mip || (opacities && d_opacity_eff && d_opacities),
                "%s: null opacity pointer", who);
+    MG_REQUIRE(grad_stride == 0 || grad_stride >= 3, "%s: gradient record stride %d", who,
+               grad_stride);
+    A.su = grad_stride ? grad_stride : 2;
+    A.sk = grad_stride ? grad_stride : 3;
+    A.sc = grad_stride ? grad_stride : 3;
+    A.so = grad_stride ? grad_stride : 1;
     A.N = N;
     A.means = means; A.quats = quats; A.scales = scales; A.sh = sh; A.rest = sh_rest;
     A.fused = sh_fused; A.d_uv = d_uv; A.d_conic = d_conic; A.d_color = d_color; A.valid = valid;
@@ -948,15 +962,17 @@ int32_t mg_preprocess_forward_mip(int64_t N, const float *means, const float *qu
 int32_t mg_preprocess_backward(int64_t N, const float *means, const float *quats,
                                const float *scales, const float *sh, const float *sh_rest,
                                int32_t sh_fused, const float *d_uv, const float *d_conic,
-                               const float *d_color, const int32_t *valid, const float *viewmat,
+                               const float *d_color, int32_t grad_stride, const int32_t *valid,
+                               const float *viewmat,
                                float fx, float fy, float cx, float cy, int32_t W, int32_t H,
                                float near_plane, float far_plane, float blur, float max_radius,
                                const float *cam_center, int32_t sh_degree, float *d_means,
                                float *d_quats, float *d_scales, float *d_sh, float *d_sh_rest,
                                mg_stream_t stream) {
     return preprocess_bwd(N, means, quats, scales, sh, sh_rest, sh_fused, d_uv, d_conic,
-                          d_color, valid, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane,
-                          blur, max_radius, cam_center, sh_degree, false, nullptr, nullptr, 0,
+                          d_color, grad_stride, valid, viewmat, fx, fy, cx, cy, W, H, near_plane,
+                          far_plane, blur, max_radius, cam_center, sh_degree, false, nullptr,
+                          nullptr, 0,
                           nullptr, d_means, d_quats, d_scales, d_sh, d_sh_rest, nullptr, stream,
                           "mg_preprocess_backward");
 }
@@ -964,8 +980,9 @@ int32_t mg_preprocess_backward(int64_t N, const float *means, const float *quats
 int32_t mg_preprocess_backward_mip(int64_t N, const float *means, const float *quats,
                                    const float *scales, const float *sh, const float *sh_rest,
                                    int32_t sh_fused, const float *d_uv, const float *d_conic,
-                                   const float *d_color, const int32_t *valid,
-                                   const float *viewmat, float fx, float fy, float cx, float cy,
+                                   const float *d_color, int32_t grad_stride,
+                                   const int32_t *valid, const float *viewmat, float fx, float fy,
+                                   float cx, float cy,
                                    int32_t W, int32_t H, float near_plane, float far_plane,
                                    float blur, float max_radius, const float *cam_center,
                                    int32_t sh_degree, const float *opacities,
@@ -974,8 +991,9 @@ int32_t mg_preprocess_backward_mip(int64_t N, const float *means, const float *q
                                    float *d_scales, float *d_sh, float *d_sh_rest,
                                    float *d_opacities, mg_stream_t stream) {
     return preprocess_bwd(N, means, quats, scales, sh, sh_rest, sh_fused, d_uv, d_conic,
-                          d_color, valid, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane,
-                          blur, max_radius, cam_center, sh_degree, true, opacities, filter_3d,
+                          d_color, grad_stride, valid, viewmat, fx, fy, cx, cy, W, H,
+                          near_plane, far_plane, blur, max_radius, cam_center, sh_degree, true,
+                          opacities, filter_3d,
                           antialias, d_opacity_eff, d_means, d_quats, d_scales, d_sh, d_sh_rest,
                           d_opacities, stream, "mg_preprocess_backward_mip");
 }

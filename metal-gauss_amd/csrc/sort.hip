@@ -162,10 +162,9 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     const KeyWin<K> win = pass_window(win0, dw, shift, copy);
     if (copy) {
         // Every digit of this pass is 0: the stable order is the input order.
-        for (int i = tid; i < nitems; i += kSortThreads) {
-            keys_out[base + i] = keys_in[base + i];
-            vals_out[base + i] = vals_in[base + i];
-        }
+        // Only the values move; later passes are copies too, so the keys are
+        // not read again (and are unspecified after a device-window sort).
+        for (int i = tid; i < nitems; i += kSortThreads) vals_out[base + i] = vals_in[base + i];
         return;
     }
 

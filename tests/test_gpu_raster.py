@@ -73,9 +73,7 @@ def gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile, absgrad=True, back
     uv, conic, op, col, gids, offs, tx = args
     _, alpha, T, stop, ws = fwd
     N, dev = uv.shape[0], uv.device
-    outs = [torch.full((N, 2), 7.0, device=dev), torch.full((N, 3), 7.0, device=dev),
-            torch.full((N,), 7.0, device=dev), torch.full((N, 3), 7.0, device=dev),
-            torch.full((N,), 7.0, device=dev) if absgrad else None]
+    rec = torch.full((N, 10), 7.0, device=dev)     # overwritten by the kernel
     lib = _lib.load()
     _lib.check(lib.mg_rasterize_backward(
         N, uv.data_ptr(), conic.data_ptr(), op.data_ptr(), col.data_ptr(), gids.data_ptr(),
@@ -84,8 +82,9 @@ def gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile, absgrad=True, back
         alpha.data_ptr() if background is not None else None,
         None if background is None else _lib.f32_array(background), gids.numel(),
         None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), W, H, tile, tx,
-        *[o.data_ptr() if o is not None else None for o in outs], _lib.stream(uv)))
-    return outs
+        rec.data_ptr(), int(absgrad), _lib.stream(uv)))
+    # The record's slots as the reference's five tensors.
+    return [rec[:, 0:2], rec[:, 2:5], rec[:, 5], rec[:, 6:9], rec[:, 9] if absgrad else None]
 
 
 def np_(t):
