@@ -79,8 +79,35 @@ __global__ __launch_bounds__(kAdamThreads) void adam_multi_kernel(const AdamTabl
     const int64_t base = (int64_t)(bid - T.block_begin) * kAdamElemsPerBlock;
     const bool ei = tab.eps_inside != 0;
 
-    if (T.vec_ok) {
-        // Two float4 per thread, each instruction covering 4 KB contiguous.
+    const int64_t e0 = base + (int64_t)threadIdx.x * kAdamVec;
+    const int64_t e1 = e0 + (int64_t)kAdamThreads * kAdamVec;
+    if (T.vec_ok && e1 + kAdamVec <= T.n) {
+        // Both float4 of the thread (each instruction covering 4 KB
+        // contiguous) are requested before any arithmetic or store: the
+        // stores could alias later loads, so the compiler would not hoist
+        // them itself, and eight loads in flight per thread instead of four
+        // keep more of HBM busy.
+        float4 p0 = ld_stream(T.p + e0), p1 = ld_stream(T.p + e1);
+        const float4 g0 = ld_stream(T.g + e0), g1 = ld_stream(T.g + e1);
+        float4 m0 = ld_stream(T.m + e0), m1 = ld_stream(T.m + e1);
+        float4 v0 = ld_stream(T.v + e0), v1 = ld_stream(T.v + e1);
+        const float ss = T.step_size, ib = T.inv_sqrt_bc2;
+        adam_elem(p0.x, g0.x, m0.x, v0.x, tab, ss, ib, ei);
+        adam_elem(p0.y, g0.y, m0.y, v0.y, tab, ss, ib, ei);
+        adam_elem(p0.z, g0.z, m0.z, v0.z, tab, ss, ib, ei);
+        adam_elem(p0.w, g0.w, m0.w, v0.w, tab, ss, ib, ei);
+        adam_elem(p1.x, g1.x, m1.x, v1.x, tab, ss, ib, ei);
+        adam_elem(p1.y, g1.y, m1.y, v1.y, tab, ss, ib, ei);
+        adam_elem(p1.z, g1.z, m1.z, v1.z, tab, ss, ib, ei);
+        adam_elem(p1.w, g1.w, m1.w, v1.w, tab, ss, ib, ei);
+        st_stream(T.p + e0, p0);
+        st_stream(T.p + e1, p1);
+        st_stream(T.m + e0, m0);
+        st_stream(T.m + e1, m1);
+        st_stream(T.v + e0, v0);
+        st_stream(T.v + e1, v1);
+    } else if (T.vec_ok) {
+        // The tensor's last workgroup.
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             const int64_t e = base + ((int64_t)r * kAdamThreads + threadIdx.x) * kAdamVec;
