@@ -84,7 +84,7 @@ int32_t mg_preprocess_forward(
     float cx, float cy, int32_t W, int32_t H, float near_plane,
     float far_plane, float blur, float max_radius, const float *cam_center,
     int32_t sh_degree, float *uv, float *conic, float *depth, float *rxy,
-    int32_t *valid, float *color, mg_stream_t stream);
+    int32_t *valid, uint8_t *valid_mask, float *color, mg_stream_t stream);
 
 /* Analytic backward of mg_preprocess_forward. Replaces preprocess_backward
  * (metal_gauss/csrc/rasterize.mm:286-327; kernel preprocess.metal:223-411).
@@ -125,7 +125,8 @@ int32_t mg_preprocess_forward_mip(
     float cx, float cy, int32_t W, int32_t H, float near_plane,
     float far_plane, float blur, float max_radius, const float *cam_center,
     int32_t sh_degree, const float *filter_3d, int32_t antialias, float *uv,
-    float *conic, float *depth, float *rxy, int32_t *valid, float *color,
+    float *conic, float *depth, float *rxy, int32_t *valid, uint8_t *valid_mask,
+    float *color,
     float *opacity_eff, mg_stream_t stream);
 
 /* Analytic backward of mg_preprocess_forward_mip. d_opacity_eff is the

@@ -40,13 +40,14 @@ _SIGNATURES = {
                                ctypes.POINTER(_i64)]),
     "mg_preprocess_forward": (_i32, [
         _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _f32, _f32, _i32, _i32,
-        _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+        _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mg_preprocess_backward": (_i32, [
         _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _f32,
         _f32, _i32, _i32, _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mg_preprocess_forward_mip": (_i32, [
         _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _f32, _f32, _i32, _i32,
-        _f32, _f32, _f32, _f32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+        _f32, _f32, _f32, _f32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+        _vp]),
     "mg_preprocess_backward_mip": (_i32, [
         _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _f32,
         _f32, _i32, _i32, _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp,

@@ -306,7 +306,9 @@ class _PreprocessMetal(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, means, quats, scales, sh, sh_rest, ctx_opac, viewmat, fx, fy, cx, cy,
-                W, H, near, far, blur, max_radius, cam_center, sh_degree):
+                W, H, near, far, blur, max_radius, cam_center, sh_degree, valid_mask=None):
+        # valid_mask: an optional (N,) bool buffer the kernel also fills with
+        # the visibility flags (render's info["valid_mask"]).
         lib = _load()
         N = means.shape[0]
         dev = means.device
@@ -339,6 +341,7 @@ class _PreprocessMetal(torch.autograd.Function):
             _lib.dev_tensor(opac, "opacities"), vm, fx, fy, cx, cy, W, H, near, far, blur,
             max_radius, cc, sh_degree, uv.data_ptr(), conic.data_ptr(), depth.data_ptr(),
             rxy.data_ptr(), valid.data_ptr(),
+            None if valid_mask is None else _lib.dev_tensor(valid_mask, "valid_mask", torch.bool),
             None if color is None else color.data_ptr(), _lib.stream(means)))
         ctx.save_for_backward(means, quats, scales, sh, rest, valid)
         # depth, rxy and valid carry no gradient: no zeros are materialised
@@ -377,7 +380,7 @@ class _PreprocessMetal(torch.autograd.Function):
             _lib.host_f32(cam_center), deg, d_means.data_ptr(), d_quats.data_ptr(),
             d_scales.data_ptr(), None if d_sh is None else d_sh.data_ptr(),
             None if d_rest is None else d_rest.data_ptr(), _lib.stream(means)))
-        return (d_means, d_quats, d_scales, d_sh, d_rest) + (None,) * 14
+        return (d_means, d_quats, d_scales, d_sh, d_rest) + (None,) * 15
 
 
 class _RasterizeMetal(torch.autograd.Function):
@@ -470,7 +473,7 @@ class _PreprocessMip(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means, quats, scales, opacities, sh, sh_rest, filter_3d, antialias,
                 viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
-                sh_degree):
+                sh_degree, valid_mask=None):
         lib = _load()
         N = means.shape[0]
         dev = means.device
@@ -503,6 +506,7 @@ class _PreprocessMip(torch.autograd.Function):
             W, H, near, far, blur, max_radius, _lib.host_f32(cam_center), sh_degree,
             None if filt is None else _lib.dev_tensor(filt, "filter_3d"), int(bool(antialias)),
             uv.data_ptr(), conic.data_ptr(), depth.data_ptr(), rxy.data_ptr(), valid.data_ptr(),
+            None if valid_mask is None else _lib.dev_tensor(valid_mask, "valid_mask", torch.bool),
             None if color is None else color.data_ptr(), op_eff.data_ptr(),
             _lib.stream(means)))
         ctx.save_for_backward(means, quats, scales, opacities, sh, rest, filt, valid)
@@ -548,7 +552,7 @@ class _PreprocessMip(torch.autograd.Function):
             p_oe, d_means.data_ptr(), d_quats.data_ptr(),
             d_scales.data_ptr(), None if d_sh is None else d_sh.data_ptr(),
             None if d_rest is None else d_rest.data_ptr(), d_op.data_ptr(), _lib.stream(means)))
-        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 15
+        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 16
 
 
 # Names that describe this backend rather than the reference's.
@@ -650,6 +654,8 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
             f"allows at most {mt * mt} on this GPU")
     fx, fy, cx, cy, vm_h, cam_center = _camera(K, viewmat)
     max_radius = max_radius_frac * max(W, H)
+    # info["valid_mask"], written by the projection kernel itself.
+    valid_b = torch.empty(means.shape[0], dtype=torch.bool, device=means.device)
 
     if filter_3d is not None or antialias:
         # Both filters in the projection kernel; the compensated opacity is
@@ -658,24 +664,24 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
         if explicit_colors:
             uv, conic, depth, rxy, valid_i, opacities = _PreprocessMip.apply(
                 means, quats, scales, opacities, None, None, filter_3d, antialias, vm_h, fx,
-                fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree)
+                fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree, valid_b)
             colors = colors.contiguous()
         else:
             sh_in, rest_in = _sh_inputs(sh, sh_rest)
             uv, conic, depth, rxy, valid_i, colors, opacities = _PreprocessMip.apply(
                 means, quats, scales, opacities, sh_in, rest_in, filter_3d, antialias, vm_h,
-                fx, fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree)
+                fx, fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree,
+                valid_b)
     elif explicit_colors:
         uv, conic, depth, rxy, valid_i = _PreprocessMetal.apply(
             means, quats, scales, None, None, opacities.detach(), vm_h, fx, fy, cx, cy, W, H,
-            near, far, 0.3, max_radius, cam_center, sh_degree)
+            near, far, 0.3, max_radius, cam_center, sh_degree, valid_b)
         colors = colors.contiguous()
     else:
         sh_in, rest_in = _sh_inputs(sh, sh_rest)
         uv, conic, depth, rxy, valid_i, colors = _PreprocessMetal.apply(
             means, quats, scales, sh_in, rest_in, opacities.detach(), vm_h, fx, fy, cx, cy,
-            W, H, near, far, 0.3, max_radius, cam_center, sh_degree)
-    valid_b = valid_i.bool()
+            W, H, near, far, 0.3, max_radius, cam_center, sh_degree, valid_b)
 
     gauss_ids, tile_offsets, tiles_x = build_tile_lists_metal(
         uv.detach(), rxy.detach(), depth.detach(), valid_i, conic.detach(),

@@ -368,6 +368,7 @@ struct PreFwdArgs {
     int32_t fused, vec4;
     float *uv, *conic, *depth, *rxy, *color;
     int32_t *valid;
+    uint8_t *valid_mask;   // optional: the same flag as one byte (a torch bool mask)
     // Mip filters (MIP kernels only): per-Gaussian 3D filter size or null,
     // the 2D compensation flag, and the opacity binning and compositing use.
     const float *filt;
@@ -426,6 +427,7 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFw
         A.rxy[2 * g] = rx;
         A.rxy[2 * g + 1] = ry;
         A.valid[g] = ok ? 1 : 0;
+        if (A.valid_mask) A.valid_mask[g] = ok ? 1 : 0;
         if (MIP) A.op_eff[g] = A.aa ? op * mip2_coef(P) : op;
     }
 
@@ -842,8 +844,8 @@ static int32_t preprocess_fwd(int64_t N, const float *means, const float *quats,
                               const float *cam_center, int32_t sh_degree, bool mip,
                               const float *filter_3d, int32_t antialias, float *uv,
                               float *conic, float *depth, float *rxy, int32_t *valid,
-                              float *color, float *opacity_eff, mg_stream_t stream,
-                              const char *who) {
+                              uint8_t *valid_mask, float *color, float *opacity_eff,
+                              mg_stream_t stream, const char *who) {
     PreFwdArgs A{};
     int32_t rc = make_cam(A.C, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane, blur,
                           max_radius, cam_center, sh_degree, who);
@@ -860,6 +862,7 @@ static int32_t preprocess_fwd(int64_t N, const float *means, const float *quats,
     A.means = means; A.quats = quats; A.scales = scales; A.sh = sh;
     A.rest = sh_rest; A.opac = opacities; A.fused = sh_fused;
     A.uv = uv; A.conic = conic; A.depth = depth; A.rxy = rxy; A.valid = valid; A.color = color;
+    A.valid_mask = valid_mask;
     A.filt = filter_3d; A.aa = antialias; A.op_eff = opacity_eff;
     A.vec4 = sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)sh & 15) == 0);
     const int64_t blocks = ceil_div(N, kPreThreads);
@@ -936,11 +939,11 @@ int32_t mg_preprocess_forward(int64_t N, const float *means, const float *quats,
                               float near_plane, float far_plane, float blur, float max_radius,
                               const float *cam_center, int32_t sh_degree, float *uv,
                               float *conic, float *depth, float *rxy, int32_t *valid,
-                              float *color, mg_stream_t stream) {
+                              uint8_t *valid_mask, float *color, mg_stream_t stream) {
     return preprocess_fwd(N, means, quats, scales, sh, sh_rest, sh_fused, opacities, viewmat,
                           fx, fy, cx, cy, W, H, near_plane, far_plane, blur, max_radius,
                           cam_center, sh_degree, false, nullptr, 0, uv, conic, depth, rxy,
-                          valid, color, nullptr, stream, "mg_preprocess_forward");
+                          valid, valid_mask, color, nullptr, stream, "mg_preprocess_forward");
 }
 
 int32_t mg_preprocess_forward_mip(int64_t N, const float *means, const float *quats,
@@ -951,12 +954,13 @@ int32_t mg_preprocess_forward_mip(int64_t N, const float *means, const float *qu
                                   float blur, float max_radius, const float *cam_center,
                                   int32_t sh_degree, const float *filter_3d, int32_t antialias,
                                   float *uv, float *conic, float *depth, float *rxy,
-                                  int32_t *valid, float *color, float *opacity_eff,
-                                  mg_stream_t stream) {
+                                  int32_t *valid, uint8_t *valid_mask, float *color,
+                                  float *opacity_eff, mg_stream_t stream) {
     return preprocess_fwd(N, means, quats, scales, sh, sh_rest, sh_fused, opacities, viewmat,
                           fx, fy, cx, cy, W, H, near_plane, far_plane, blur, max_radius,
                           cam_center, sh_degree, true, filter_3d, antialias, uv, conic, depth,
-                          rxy, valid, color, opacity_eff, stream, "mg_preprocess_forward_mip");
+                          rxy, valid, valid_mask, color, opacity_eff, stream,
+                          "mg_preprocess_forward_mip");
 }
 
 int32_t mg_preprocess_backward(int64_t N, const float *means, const float *quats,

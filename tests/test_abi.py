@@ -85,11 +85,12 @@ def test_bad_arguments_fail_before_any_launch():
     vm = (ctypes.c_float * 16)(*([0.0] * 16))
     cc = (ctypes.c_float * 3)(0.0, 0.0, 0.0)
     rc = lib.mg_preprocess_forward(4, 1, 1, 1, 1, None, 0, 1, vm, 1.0, 1.0, 0.0, 0.0, 8, 8,
-                                   0.01, 100.0, 0.3, 8.0, cc, 3, 1, 1, 1, 1, 1, 1, None)
+                                   0.01, 100.0, 0.3, 8.0, cc, 3, 1, 1, 1, 1, 1, None, 1, None)
     assert rc == 1
     assert "(N,16,3)" in lib.mg_last_error().decode()
     rc = lib.mg_preprocess_forward(4, 1, 1, 1, None, None, 1, 1, vm, 1.0, 1.0, 0.0, 0.0, 8, 8,
-                                   0.01, 100.0, 0.3, 8.0, cc, 4, 1, 1, 1, 1, 1, None, None)
+                                   0.01, 100.0, 0.3, 8.0, cc, 4, 1, 1, 1, 1, 1, None, None,
+                                   None)
     assert rc == 1 and "sh_degree" in lib.mg_last_error().decode()
 
 
