@@ -60,12 +60,16 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--gaussians", type=int, default=1_000_000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--variant", default="base", choices=["base", "mip", "mip-torch"],
-                    help="base: the config-4 step; mip: with Mip-Splatting's 3D filter and "
-                         "the 2D antialias compensation folded into the projection kernel "
+    ap.add_argument("--variant", default="base",
+                    choices=["base", "torch-act", "mip", "mip-torch"],
+                    help="base: the config-4 step, exp/sigmoid of the parameters inside the "
+                         "projection kernel (render(activations=True)); torch-act: the same "
+                         "step with exp/sigmoid in torch before render (train.py:221-222); "
+                         "mip: with Mip-Splatting's 3D filter and the 2D antialias "
+                         "compensation folded into the projection kernel "
                          "(render(filter_3d=, antialias=True)); mip-torch: the same step with "
-                         "the 3D filter applied as the reference's torch reparameterisation "
-                         "(apply_3d_filter, train.py:223-227) before render")
+                         "the activations and the 3D filter applied as the reference's torch "
+                         "reparameterisation (apply_3d_filter, train.py:223-227) before render")
     ap.add_argument("--cpu-only", action="store_true", help="time only the CPU baseline")
     ap.add_argument("--config", type=int, choices=[1, 2, 3, 5], default=None,
                     help="time another BASELINE configuration instead of the config-4 step: "
@@ -134,7 +138,7 @@ class Step:
         self.variant = variant
         self.f3d = None
         self.f3d_ms = None
-        if variant != "base":
+        if variant in ("mip", "mip-torch"):
             self.f3d_ms = self.refresh_filter()
 
     def refresh_filter(self):
@@ -164,13 +168,19 @@ class Step:
         v = self.order[self.k % len(self.order)]
         self.k += 1
         cam, gt, p = self.cams[v], self.targets[v], self.p
-        scales, opac = torch.exp(p["log_scales"]), torch.sigmoid(p["logit_opac"])
-        kw = {}
+        # exp(log_scales) and sigmoid(logit_opac) (train.py:221-222) run inside
+        # the projection kernel and its backward; the "-torch" variants take
+        # them in torch as the reference's trainer does.
+        scales, opac = p["log_scales"], p["logit_opac"]
+        kw = dict(activations=True)
         if self.variant == "mip":
-            kw = dict(filter_3d=self.f3d, antialias=True)
+            kw = dict(filter_3d=self.f3d, antialias=True, activations=True)
+        elif self.variant == "torch-act":
+            scales, opac = torch.exp(scales), torch.sigmoid(opac)
+            kw = {}
         elif self.variant == "mip-torch":
             from metal_gauss_amd import apply_3d_filter
-            scales, opac = apply_3d_filter(scales, opac, self.f3d)
+            scales, opac = apply_3d_filter(torch.exp(scales), torch.sigmoid(opac), self.f3d)
             kw = dict(antialias=True)
         rgb, alpha, info = render(p["means"], p["quats"], scales, opac, p["sh_dc"], cam.K,
                                   cam.viewmat, cam.W, cam.H, sh_degree=3, sh_rest=p["sh_rest"],
@@ -189,13 +199,15 @@ class Step:
 def algorithmic_bytes(kernel, N, I, P, T, f_valid, n_floats):
     """HBM bytes one launch must move, each tensor read or written once."""
     return {
-        "preprocess_forward": (92 + 192 * f_valid) * N,
-        "preprocess_backward": (308 + 192 * f_valid) * N,
-        "bin_count": 84 * N,                      # 40 B read; count, key, id, 32 B record
-        "depth_sort": 3 * 20 * N,                 # 3 passes (24 varying depth bits at config 4)
-        "exclusive_scan": 12 * N,                 # counts + order read, offsets written
-        "bin_write": 40 * N + 8 * I,              # order, offset, record; key + id per pair
-        "tile_sort": 2 * 20 * I,                  # 2 passes at 50x50 tiles
+        # + the activated opacity written (forward); the logit read, its
+        # record gradient read and the logit gradient written (backward).
+        "preprocess_forward": (96 + 192 * f_valid) * N,
+        "preprocess_backward": (320 + 192 * f_valid) * N,
+        "bin_count": 76 * N,                      # 40 B read; count, 32 B record
+        "exclusive_scan": 8 * N,                  # counts read, offsets written
+        "bin_write": 36 * N + 8 * I,              # offset, record; key + id per pair
+        "tile_sort": 16 * I,                      # one counting pass: tiles read twice, ids once, ids written
+        "depth_sort": 12 * I,                     # per tile list: ids read, depths gathered, ids written
         "tile_ranges": 4 * I + 4 * (T + 1),
         "rasterize_forward": 40 * I + 24 * P + 8 * T,
         "rasterize_backward": 40 * I + 24 * P + 36 * N,
@@ -257,7 +269,7 @@ def gpu_bench(args):
                 "GBps": round(algorithmic_bytes(k, N, I, P, T, f_valid, n_floats)
                               / (v[0] * 1e-3) / 1e9, 1)} for k, v in kern.items()}
     f3d_ms = None
-    if args.variant != "base":
+    if args.variant in ("mip", "mip-torch"):
         with _lib.KernelTimer():
             wall = step.refresh_filter()
             tot, cnt = _lib.KernelTimer.query("compute_3d_filter")
@@ -555,7 +567,7 @@ def adam_config(reps):
 
 
 PMC_REGEX = ("raster_bwd|raster_fwd|adam_multi|preprocess_fwd|preprocess_bwd|radix_|scan_|"
-             "bin_write|bin_count|copyBuffer")
+             "bin_write|bin_count|tile_hist|tile_scatter|ssim_fused|copyBuffer")
 
 
 def _counter_rows(d):
@@ -646,7 +658,8 @@ def stats_summary(stats_csv, steps, variant="base", mcmc=False, config=None):
         ]
     else:
         vflag = "" if variant == "base" else f" --variant {variant}"
-        what = {"base": "", "mip": ", Mip 3D filter + 2D antialias in the projection kernel",
+        what = {"base": "", "torch-act": ", exp/sigmoid of the parameters in torch",
+                "mip": ", Mip 3D filter + 2D antialias in the projection kernel",
                 "mip-torch": ", Mip 3D filter as torch reparameterisation"}[variant]
         lines = [
             "# rocprofv3 kernel statistics, config-4 step (1M Gaussians SH3, 800x800, tile 16"
@@ -891,10 +904,12 @@ def main():
     }
     if args.variant != "base":
         out["config"]["workload"] += {
+            "torch-act": "; exp/sigmoid of the parameters in torch before render",
             "mip": "; Mip 3D filter + 2D antialias in the projection kernel",
             "mip-torch": "; Mip 3D filter as torch reparameterisation, 2D antialias in kernel",
         }[args.variant]
         out["config"]["variant"] = args.variant
+    if args.variant in ("mip", "mip-torch"):
         # Once per densify interval in the reference's trainer, not per step:
         # the kernel alone, and with building the per-view table on the host.
         out["compute_3d_filter_ms"] = {"kernel": round(r["f3d_ms"][0], 4),

@@ -115,6 +115,11 @@ int32_t mg_preprocess_backward(
  *     blurred covariance, which the reference recomputes from the conic in
  *     torch (antialias_scale, metal_gauss/metal_backend.py:367-393, applied
  *     at 506-511; torch_ref.py:100-124).
+ *   - activations: bit 0 set, scales holds log scales and the kernel takes
+ *     their exp; bit 1 set, opacities holds logits and the kernel takes their
+ *     sigmoid 1 / (1 + exp(-x)). These are the torch.exp and torch.sigmoid
+ *     the reference's trainer applies before render (train.py:221-222); 0
+ *     takes scales and opacities as given.
  * opacity_eff (N,) receives the opacity binning and compositing use. rxy and
  * valid see the opacity after the 3D filter and before the 2D one, as in the
  * reference. */
@@ -124,16 +129,19 @@ int32_t mg_preprocess_forward_mip(
     const float *opacities, const float *viewmat, float fx, float fy,
     float cx, float cy, int32_t W, int32_t H, float near_plane,
     float far_plane, float blur, float max_radius, const float *cam_center,
-    int32_t sh_degree, const float *filter_3d, int32_t antialias, float *uv,
-    float *conic, float *depth, float *rxy, int32_t *valid, uint8_t *valid_mask,
-    float *color,
-    float *opacity_eff, mg_stream_t stream);
+    int32_t sh_degree, const float *filter_3d, int32_t antialias,
+    int32_t activations, float *uv, float *conic, float *depth, float *rxy,
+    int32_t *valid, uint8_t *valid_mask, float *color, float *opacity_eff,
+    mg_stream_t stream);
 
 /* Analytic backward of mg_preprocess_forward_mip. d_opacity_eff is the
  * gradient of opacity_eff; d_opacities (N,) receives the gradient of the
  * unfiltered opacities, and the filters' share of the scale and covariance
- * gradients is folded into d_scales, d_quats and d_means. The reference gets
- * these from torch autograd of the same expressions. */
+ * gradients is folded into d_scales, d_quats and d_means. With activations
+ * (the forward's), d_scales and d_opacities are the gradients of the log
+ * scales and the logits: times exp(log scale), and times (1 - y) y for
+ * y = sigmoid(logit), as torch's backward of exp and sigmoid. The reference
+ * gets these from torch autograd of the same expressions. */
 int32_t mg_preprocess_backward_mip(
     int64_t N, const float *means, const float *quats, const float *scales,
     const float *sh, const float *sh_rest, int32_t sh_fused,
@@ -142,7 +150,7 @@ int32_t mg_preprocess_backward_mip(
     float cy, int32_t W, int32_t H, float near_plane, float far_plane,
     float blur, float max_radius, const float *cam_center, int32_t sh_degree,
     const float *opacities, const float *filter_3d, int32_t antialias,
-    const float *d_opacity_eff, float *d_means, float *d_quats,
+    int32_t activations, const float *d_opacity_eff, float *d_means, float *d_quats,
     float *d_scales, float *d_sh, float *d_sh_rest, float *d_opacities,
     mg_stream_t stream);
 
@@ -285,6 +293,24 @@ int32_t mg_sort_pairs_u64(uint64_t *keys_in, int32_t *vals_in,
                           int32_t begin_bit, int32_t end_bit, void *workspace,
                           int64_t workspace_bytes, mg_stream_t stream);
 
+/* Bytes of scratch mg_sort_pairs_by_tile needs for n pairs over n_tiles. */
+int64_t mg_sort_pairs_by_tile_workspace_bytes(int64_t n, int32_t n_tiles);
+
+/* Stable counting sort of n (tile, id) pairs by tile, 0 < n < 2^31,
+ * 1 <= n_tiles <= 4096: ids_out gets the ids in (tile, input position) order
+ * and tile_offsets (n_tiles + 1,) the start of each tile's run, the last
+ * entry the count of pairs with tile < n_tiles (pairs with a larger tile are
+ * dropped). tiles must be 16-byte aligned. One pass over the pairs; the
+ * tile-id sort of mg_bin_lists_finish.
+ * With pairs emitted in depth order it replaces the argsort of the 64-bit
+ * (tile << 32 | depth) keys and the searchsorted of the tile ranges
+ * (metal_backend.py:256-260). */
+int32_t mg_sort_pairs_by_tile(int64_t n, const uint32_t *tiles,
+                              const int32_t *ids, int32_t n_tiles,
+                              int32_t *ids_out, int32_t *tile_offsets,
+                              void *workspace, int64_t workspace_bytes,
+                              mg_stream_t stream);
+
 /* tile_offsets[t] = first index i with (keys[i] >> 32) >= t, for
  * t = 0..n_tiles; keys sorted. Replaces keys >> 32 plus torch.searchsorted
  * (metal_backend.py:257-260). tile_offsets: (n_tiles + 1,) int32. */
@@ -292,26 +318,25 @@ int32_t mg_tile_ranges(const uint64_t *sorted_keys, int64_t n,
                        int32_t n_tiles, int32_t *tile_offsets,
                        mg_stream_t stream);
 
-/* Depth-first tile lists: the whole of build_tile_lists_metal
- * (metal_backend.py:217-285) in two calls around the one host read of the
- * intersection total.
+/* Tile lists: the whole of build_tile_lists_metal (metal_backend.py:217-285)
+ * in two calls around the one host read of the intersection total.
  *
- * begin: per-Gaussian tile counts (the exact ellipse test, as mg_bin_count),
- * then one synchronous host read of the intersection total and of the depth
- * range of the Gaussians that claim a tile, then a stable 32-bit radix sort
- * of all Gaussians by depth on only the bits in which those depths differ,
- * and the exclusive scan of the counts in depth order. The total goes to
- * total_host (host) when not NULL; the stream is always synchronised once.
- * The workspace (mg_bin_lists_workspace_bytes(N)) carries state to finish
- * and must not be touched in between.
+ * begin: per-Gaussian tile counts (the exact ellipse test, as mg_bin_count)
+ * and their exclusive scan, then one synchronous host read of the
+ * intersection total, which goes to total_host (host) when not NULL; the
+ * stream is always synchronised once. The workspace
+ * (mg_bin_lists_workspace_bytes(N)) carries state to finish and must not be
+ * touched in between.
  *
- * finish: emits each Gaussian's (tile id, Gaussian id) pairs in depth order,
- * stably radix-sorts them by tile id on ceil(log2(tiles_x*tiles_y)) bits and
- * writes gauss_ids (total,) and tile_offsets (tiles_x*tiles_y + 1,). The
- * result equals a stable sort of the (tile << 32 | depth bits) keys of
- * mg_bin_write by mg_sort_pairs_u64: order (tile, depth, Gaussian id).
- * Same arguments as begin, plus its workspace, the total, and a scratch of
- * mg_bin_lists_finish_workspace_bytes(total). */
+ * finish: emits each Gaussian's (tile id, Gaussian id) pairs, Gaussian by
+ * Gaussian, sorts them stably by tile id (up to 4096 tiles a one-pass
+ * counting sort, as mg_sort_pairs_by_tile; beyond, radix passes on
+ * ceil(log2(tiles_x*tiles_y)) bits), then sorts every tile's list stably by
+ * the depth's float bits, and writes gauss_ids (total,) and tile_offsets
+ * (tiles_x*tiles_y + 1,). The result equals a stable sort of the
+ * (tile << 32 | depth bits) keys of mg_bin_write by mg_sort_pairs_u64: order
+ * (tile, depth, Gaussian id). Same arguments as begin, plus its workspace,
+ * the total, and a scratch of mg_bin_lists_finish_workspace_bytes(total). */
 int64_t mg_bin_lists_workspace_bytes(int64_t N);
 int64_t mg_bin_lists_finish_workspace_bytes(int64_t total);
 int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy,

@@ -46,12 +46,12 @@ _SIGNATURES = {
         _f32, _i32, _i32, _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mg_preprocess_forward_mip": (_i32, [
         _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _f32, _f32, _i32, _i32,
-        _f32, _f32, _f32, _f32, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-        _vp]),
+        _f32, _f32, _f32, _f32, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+        _vp, _vp]),
     "mg_preprocess_backward_mip": (_i32, [
         _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _f32,
-        _f32, _i32, _i32, _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp,
-        _vp, _vp, _vp, _vp]),
+        _f32, _i32, _i32, _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp,
+        _vp, _vp, _vp, _vp, _vp, _vp]),
     "mg_compute_3d_filter": (_i32, [_i64, _vp, _i32, _vp, _f32, _f32, _vp, _vp, _vp]),
     "mg_add_noise": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _u64, _vp]),
     "mg_mcmc_workspace_bytes": (_i64, [_i64, _i64]),
@@ -72,6 +72,8 @@ _SIGNATURES = {
     "mg_sort_workspace_bytes": (_i64, [_i64]),
     "mg_sort_pairs_u64": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _i64, _vp]),
     "mg_tile_ranges": (_i32, [_vp, _i64, _i32, _vp, _vp]),
+    "mg_sort_pairs_by_tile_workspace_bytes": (_i64, [_i64, _i32]),
+    "mg_sort_pairs_by_tile": (_i32, [_i64, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _vp]),
     "mg_bin_lists_workspace_bytes": (_i64, [_i64]),
     "mg_bin_lists_finish_workspace_bytes": (_i64, [_i64]),
     "mg_bin_lists_begin": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,

@@ -468,12 +468,16 @@ class _PreprocessMip(torch.autograd.Function):
     ``filter_3d`` as a constant) and returns, after the usual outputs, the
     opacity binning and compositing use. The backward carries that opacity's
     gradient to the opacity, the scales and the projected covariance.
+    ``activations`` (bit 0: scales are log scales, bit 1: opacities are
+    logits) moves the trainer's torch.exp / torch.sigmoid (train.py:221-222)
+    into the same kernels; the gradients then land on the log scales and
+    logits.
     """
 
     @staticmethod
     def forward(ctx, means, quats, scales, opacities, sh, sh_rest, filter_3d, antialias,
                 viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
-                sh_degree, valid_mask=None):
+                sh_degree, valid_mask=None, activations=0):
         lib = _load()
         N = means.shape[0]
         dev = means.device
@@ -505,7 +509,7 @@ class _PreprocessMip(torch.autograd.Function):
             _lib.dev_tensor(opacities, "opacities"), _lib.host_f32(viewmat), fx, fy, cx, cy,
             W, H, near, far, blur, max_radius, _lib.host_f32(cam_center), sh_degree,
             None if filt is None else _lib.dev_tensor(filt, "filter_3d"), int(bool(antialias)),
-            uv.data_ptr(), conic.data_ptr(), depth.data_ptr(), rxy.data_ptr(), valid.data_ptr(),
+            int(activations), uv.data_ptr(), conic.data_ptr(), depth.data_ptr(), rxy.data_ptr(), valid.data_ptr(),
             None if valid_mask is None else _lib.dev_tensor(valid_mask, "valid_mask", torch.bool),
             None if color is None else color.data_ptr(), op_eff.data_ptr(),
             _lib.stream(means)))
@@ -514,6 +518,7 @@ class _PreprocessMip(torch.autograd.Function):
         ctx.fused = fused
         ctx.has_sh = sh is not None
         ctx.antialias = bool(antialias)
+        ctx.activations = int(activations)
         ctx.meta = (viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
                     sh_degree)
         ctx.mark_non_differentiable(depth, rxy, valid)
@@ -548,11 +553,11 @@ class _PreprocessMip(torch.autograd.Function):
             int(ctx.fused), p_uv, p_conic, p_color, stride, valid.data_ptr(),
             _lib.host_f32(viewmat), fx, fy, cx, cy, W, H, near, far, blur, max_radius,
             _lib.host_f32(cam_center), deg, opacities.data_ptr(),
-            None if filt is None else filt.data_ptr(), int(ctx.antialias),
+            None if filt is None else filt.data_ptr(), int(ctx.antialias), ctx.activations,
             p_oe, d_means.data_ptr(), d_quats.data_ptr(),
             d_scales.data_ptr(), None if d_sh is None else d_sh.data_ptr(),
             None if d_rest is None else d_rest.data_ptr(), d_op.data_ptr(), _lib.stream(means)))
-        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 16
+        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 17
 
 
 # Names that describe this backend rather than the reference's.
@@ -624,7 +629,7 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
            background=(0.0, 0.0, 0.0), colors=None, max_radius_frac: float = 1.0,
            sh_rest=None, antialias: bool = False, absgrad_out=None,
            min_transmittance: float = DEFAULT_T_MIN, chunked_backward: bool = False,
-           filter_3d=None, **_ignored):
+           filter_3d=None, activations: bool = False, **_ignored):
     """Render Gaussians from one camera; same signature as the reference's.
 
     means (N,3) world; quats (N,4) wxyz (need not be normalised); scales (N,3)
@@ -641,6 +646,12 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     ``apply_3d_filter(scales, opacities, filter_3d)`` (what the reference's
     trainer does in torch, train.py:223-227), with the filter a constant.
     ``antialias`` likewise runs in the kernel.
+    ``activations=True`` takes ``scales`` as log scales and ``opacities`` as
+    logits: the exp and sigmoid the reference's trainer applies in torch
+    before render (train.py:221-222) run inside the projection kernel and
+    their derivatives in its backward, so the gradients land on the log
+    scales and logits (the same values as torch.exp / torch.sigmoid in
+    front of ``render``).
     """
     explicit_colors = colors is not None
     _require_gpu(means)
@@ -657,21 +668,23 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     # info["valid_mask"], written by the projection kernel itself.
     valid_b = torch.empty(means.shape[0], dtype=torch.bool, device=means.device)
 
-    if filter_3d is not None or antialias:
-        # Both filters in the projection kernel; the compensated opacity is
-        # binned too, which gives a tighter, still exact, ellipse bound
-        # (metal_backend.py:506-511).
+    if filter_3d is not None or antialias or activations:
+        # Both filters (and the activations) in the projection kernel; the
+        # compensated opacity is binned too, which gives a tighter, still
+        # exact, ellipse bound (metal_backend.py:506-511).
+        act = 3 if activations else 0
         if explicit_colors:
             uv, conic, depth, rxy, valid_i, opacities = _PreprocessMip.apply(
                 means, quats, scales, opacities, None, None, filter_3d, antialias, vm_h, fx,
-                fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree, valid_b)
+                fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree, valid_b,
+                act)
             colors = colors.contiguous()
         else:
             sh_in, rest_in = _sh_inputs(sh, sh_rest)
             uv, conic, depth, rxy, valid_i, colors, opacities = _PreprocessMip.apply(
                 means, quats, scales, opacities, sh_in, rest_in, filter_3d, antialias, vm_h,
                 fx, fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree,
-                valid_b)
+                valid_b, act)
     elif explicit_colors:
         uv, conic, depth, rxy, valid_i = _PreprocessMetal.apply(
             means, quats, scales, None, None, opacities.detach(), vm_h, fx, fy, cx, cy, W, H,

@@ -327,13 +327,14 @@ __device__ __forceinline__ int64_t block_excl_scan(int64_t v, int64_t *s_wave, i
     return before + incl - v;
 }
 
-// With idx, in[idx[i]] is gathered once and stored to gathered[i], which the
-// downsweep then reads in order.
-__global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const int32_t *in,
-                                                                   const int32_t *idx, int64_t n,
-                                                                   int64_t *partials,
-                                                                   int32_t *gathered) {
+// With idx (or *idx_dev, an index array chosen on the device), in[idx[i]] is
+// gathered once and stored to gathered[i], which the downsweep then reads in
+// order.
+__global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(
+    const int32_t *in, const int32_t *idx, const int32_t *const *idx_dev, int64_t n,
+    int64_t *partials, int32_t *gathered) {
     __shared__ int64_t s_wave[kScanThreads / 64];
+    if (idx_dev) idx = *idx_dev;
     const int64_t base = (int64_t)blockIdx.x * kScanChunk;
     int64_t s = 0;
 #pragma unroll
@@ -409,40 +410,39 @@ int64_t scan_ws_bytes(int64_t n) {
 }
 
 int32_t exclusive_scan(const int32_t *in, const int32_t *idx, int64_t n, int32_t *out,
-                       int64_t *total_dev, void *ws, int64_t ws_bytes, hipStream_t s) {
+                       int64_t *total_dev, void *ws, int64_t ws_bytes, hipStream_t s,
+                       const int32_t *const *idx_dev) {
+    const bool gather = idx != nullptr || idx_dev != nullptr;
     MG_REQUIRE(ws && ws_bytes >= scan_ws_bytes(n), "exclusive scan: workspace %lld bytes, need %lld",
                (long long)ws_bytes, (long long)scan_ws_bytes(n));
     int64_t *partials = static_cast<int64_t *>(ws);
     const int64_t nparts = ceil_div(n > 0 ? n : 1, kScanChunk);
     TimedScope ts("exclusive_scan", s);
     // A zero-length input still runs one reduce block so the total is 0.
-    scan_reduce_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(in, idx, n, partials,
-                                                                  idx ? out : nullptr);
+    scan_reduce_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(in, idx, idx_dev, n, partials,
+                                                                  gather ? out : nullptr);
     MG_LAUNCHED("scan_reduce_kernel");
     scan_partials_kernel<<<1, kScanThreads, 0, s>>>(partials, nparts, total_dev);
     MG_LAUNCHED("scan_partials_kernel");
     if (n > 0) {
-        scan_down_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(idx ? out : in, n, partials,
-                                                                    out);
+        scan_down_kernel<<<(unsigned)nparts, kScanThreads, 0, s>>>(gather ? out : in, n,
+                                                                    partials, out);
         MG_LAUNCHED("scan_down_kernel");
     }
     return MG_OK;
 }
 
-// ------------------------------------------------- depth-first tile lists
-// The (tile << 32 | depth) order is built in two cheaper sorts: the N
-// Gaussians by depth once (32-bit keys), then the intersections, emitted in
-// that depth order, by tile id alone (ceil(log2 n_tiles) bits). The tile sort
-// is stable, so inside a tile the order is (depth bits, Gaussian id) - the
-// same total order as one stable sort of the 64-bit keys emitted Gaussian by
-// Gaussian. Gaussians that claim no tile never appear in the lists, so their
-// place in the depth order is free.
+// ------------------------------------------------------ tile-major lists
+// The (tile << 32 | depth) order is built without a global depth sort: the
+// intersections are emitted Gaussian by Gaussian (ids ascending), grouped by
+// tile id with a stable counting sort (ids stay ascending inside a tile),
+// and each tile's list is then sorted stably by its depth bits alone, in LDS
+// by one workgroup per tile. Inside a tile the order is thus (depth bits,
+// Gaussian id): the same total order as one stable sort of the 64-bit keys.
 
 struct BinStats {
     unsigned long long total;       // intersections
-    uint32_t kmin, kmax;            // depth-key range of Gaussians with a tile
     unsigned long long scan_total;  // the scan's own total (same value)
-    DevWin<uint32_t> win;           // the depth sort's window: [kmin, kmax], its bit width
 };
 
 // One per count workgroup, reduced by bin_stats_kernel. (Same-address
@@ -451,16 +451,13 @@ struct BinStats {
 // performed there.)
 struct BinPart {
     unsigned long long total;
-    uint32_t kmin, kmax;
 };
 
-// Count pass in Gaussian order (coalesced reads): the tile count, the walk
-// record, and the depth sort's key (0xFFFFFFFF for a Gaussian with no tile)
-// and identity value; per workgroup the intersection total and key range.
+// Count pass in Gaussian order (coalesced reads): the tile count and the
+// walk record; per workgroup the intersection total.
 __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArgs A,
                                                                     int32_t *counts, BinRec *recs,
-                                                                    uint32_t *dkeys,
-                                                                    int32_t *perm, BinPart *parts) {
+                                                                    BinPart *parts) {
     __shared__ BinPart s_p[kBinThreads / 64];
     __shared__ BinRec s_rec[kBinThreads];
     __shared__ int32_t s_big[kBinThreads], s_cnt[kBinThreads];
@@ -513,81 +510,43 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
         __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
-    uint32_t key = 0xFFFFFFFFu;
     if (g < A.N) {
         if (big) n = s_cnt[tid];
-        if (n > 0) key = __float_as_uint(A.depth[g]);
         counts[g] = n;
-        dkeys[g] = key;
-        perm[g] = (int32_t)g;
     }
     unsigned long long tot = (unsigned long long)n;
-    uint32_t kmin = key, kmax = n > 0 ? key : 0u;
-    for (int o = 32; o >= 1; o >>= 1) {
-        tot += __shfl_xor(tot, o, 64);
-        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
-        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
-    }
-    if ((threadIdx.x & 63) == 0) s_p[threadIdx.x >> 6] = BinPart{tot, kmin, kmax};
+    for (int o = 32; o >= 1; o >>= 1) tot += __shfl_xor(tot, o, 64);
+    if ((threadIdx.x & 63) == 0) s_p[threadIdx.x >> 6] = BinPart{tot};
     __syncthreads();
     if (threadIdx.x == 0) {
         BinPart b = s_p[0];
-        for (int w = 1; w < kBinThreads / 64; ++w) {
-            b.total += s_p[w].total;
-            b.kmin = min(b.kmin, s_p[w].kmin);
-            b.kmax = max(b.kmax, s_p[w].kmax);
-        }
+        for (int w = 1; w < kBinThreads / 64; ++w) b.total += s_p[w].total;
         parts[blockIdx.x] = b;
     }
 }
 
 // One workgroup folds the count pass's per-workgroup partials into *st.
+// One workgroup folds the count pass's per-workgroup partials into *st.
 __global__ __launch_bounds__(256) void bin_stats_kernel(const BinPart *parts, int64_t nparts,
                                                         BinStats *st) {
-    __shared__ BinPart s_p[4];
+    __shared__ unsigned long long s_p[4];
     unsigned long long tot = 0;
-    uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
-    for (int64_t i = threadIdx.x; i < nparts; i += 256) {
-        const BinPart b = parts[i];
-        tot += b.total;
-        kmin = min(kmin, b.kmin);
-        kmax = max(kmax, b.kmax);
-    }
-    for (int o = 32; o >= 1; o >>= 1) {
-        tot += __shfl_xor(tot, o, 64);
-        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
-        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
-    }
-    if ((threadIdx.x & 63) == 0) s_p[threadIdx.x >> 6] = BinPart{tot, kmin, kmax};
+    for (int64_t i = threadIdx.x; i < nparts; i += 256) tot += parts[i].total;
+    for (int o = 32; o >= 1; o >>= 1) tot += __shfl_xor(tot, o, 64);
+    if ((threadIdx.x & 63) == 0) s_p[threadIdx.x >> 6] = tot;
     __syncthreads();
     if (threadIdx.x == 0) {
-        BinPart b = s_p[0];
-        for (int w = 1; w < 4; ++w) {
-            b.total += s_p[w].total;
-            b.kmin = min(b.kmin, s_p[w].kmin);
-            b.kmax = max(b.kmax, s_p[w].kmax);
-        }
-        st->total = b.total;
-        st->kmin = b.kmin;
-        st->kmax = b.kmax;
+        st->total = s_p[0] + s_p[1] + s_p[2] + s_p[3];
         st->scan_total = 0;
-        // Keys of Gaussians with tiles lie in [kmin, kmax]; the others clamp
-        // to kmax and sort among the farthest, which changes no list. No
-        // tiles at all: every pass copies.
-        const bool any = b.kmin <= b.kmax;
-        const uint32_t span = any ? b.kmax - b.kmin : 0u;
-        st->win.lo = any ? b.kmin : 0u;
-        st->win.hi = any ? b.kmax : 0u;
-        st->win.bits = span == 0u ? 0 : 32 - __builtin_clz(span);
     }
 }
 
 // Pairs staged in LDS per workgroup before the coalesced store.
 constexpr int kBinStage = 2048;
 
-// Thread k emits the pairs of the k-th Gaussian in depth order (tile id key,
-// Gaussian id) at the scanned offset of position k; the workgroup's 256
-// Gaussians own one contiguous output range.
+// Thread k emits the pairs of Gaussian k (tile id key, Gaussian id) at its
+// scanned offset; the workgroup's 256 Gaussians own one contiguous output
+// range.
 //   * Small rectangles (walked by their own thread) go through LDS: their
 //     runs are numbered by a workgroup prefix scan of their counts (at most
 //     256 x 32 pairs) and staged in windows of kBinStage slots, each slot
@@ -598,9 +557,11 @@ constexpr int kBinStage = 2048;
 //     consecutive positions by lane rank (the walk's emission order), and
 //     the wave stores them directly, consecutive lanes on consecutive
 //     addresses.
+// With pairs (and depth) the value of a pair is {Gaussian id, its depth's
+// float bits} in one 8-byte store instead of the id alone in ids.
 __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
-    const BinRec *recs, const int32_t *order, const int32_t *offsets, int64_t N, int64_t total,
-    int tile, int W, int H, int tiles_x, int test, uint32_t *tkeys, int32_t *ids) {
+    const BinRec *recs, const int32_t *offsets, int64_t N, int64_t total, int tile, int W, int H,
+    int tiles_x, int test, uint32_t *tkeys, int32_t *ids, const float *depth, uint2 *pairs) {
     __shared__ uint32_t s_k[kBinStage];
     __shared__ int32_t s_i[kBinStage];
     __shared__ int32_t s_off[kBinStage];
@@ -608,10 +569,12 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
     __shared__ int32_t s_big[kBinThreads], s_g[kBinThreads];
     __shared__ int32_t s_nbig, s_wsum[kBinThreads / 64];
     __shared__ float s_edge[kBinThreads / 64][kEdgeSlots];
+    __shared__ uint32_t s_dk[kBinThreads];   // depth bits of the workgroup's Gaussians
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t k0 = (int64_t)blockIdx.x * kBinThreads;
     const int64_t k = k0 + tid;
     const int64_t base = offsets[k0];
+    if (pairs) s_dk[tid] = k < N ? __float_as_uint(depth[k]) : 0u;
     if (tid == 0) s_nbig = 0;
     __syncthreads();
     bool big = false;
@@ -624,7 +587,7 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
         const int64_t nxt = k + 1 < N ? (int64_t)offsets[k + 1] : total;
         const int cap = (int)(nxt - at);
         if (cap > 0) {
-            g = order[k];
+            g = (int32_t)k;
             r = recs[g];
             if (rec_area(r) > kWaveWalkArea) {
                 big = true;
@@ -677,7 +640,10 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
             const int pos = emitted + rank_in(cm);
             if (claim && pos < cap) {
                 tkeys[atb + pos] = (uint32_t)(ty * tiles_x + tx);
-                ids[atb + pos] = gb;
+                if (pairs)
+                    pairs[atb + pos] = make_uint2((uint32_t)gb, s_dk[j]);
+                else
+                    ids[atb + pos] = gb;
             }
             emitted += __popcll(cm);
         }
@@ -701,7 +667,10 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
         for (int i = tid; i < w1 - w0; i += kBinThreads) {
             const int64_t pos = base + s_off[i];
             tkeys[pos] = s_k[i];
-            ids[pos] = s_i[i];
+            if (pairs)
+                pairs[pos] = make_uint2((uint32_t)s_i[i], s_dk[s_i[i] - k0]);
+            else
+                ids[pos] = s_i[i];
         }
         __syncthreads();
     }
@@ -716,43 +685,610 @@ __global__ __launch_bounds__(256) void tile_ranges_u32_kernel(const uint32_t *ti
     for (int64_t t = prev + 1; t <= cur && t <= n_tiles; ++t) offsets[t] = (int32_t)i;
 }
 
-// Carves the begin/finish workspace identically on both calls. After begin,
-// perm_a holds the depth order, offsets the scanned counts in that order and
-// recs the walk records.
-struct BeginWs {
-    int32_t *counts, *perm_a, *perm_b, *offsets;
-    uint32_t *dkey_a, *dkey_b;
-    BinRec *recs;
-    BinPart *parts;
-    BinStats *stats;
-    void *scan_ws, *sort_ws;
-    int64_t scan_bytes, sort_bytes, bytes;
-    BeginWs(void *base, int64_t N) {
-        char *p = static_cast<char *>(base);
-        int64_t off = 0;
-        auto take = [&](int64_t b) { char *q = p ? p + off : nullptr; off += align256(b); return q; };
-        counts = (int32_t *)take(4 * N);
-        perm_a = (int32_t *)take(4 * N);
-        perm_b = (int32_t *)take(4 * N);
-        offsets = (int32_t *)take(4 * N);
-        dkey_a = (uint32_t *)take(4 * N);
-        dkey_b = (uint32_t *)take(4 * N);
-        recs = (BinRec *)take((int64_t)sizeof(BinRec) * N);
-        parts = (BinPart *)take((int64_t)sizeof(BinPart) * ceil_div(N, kBinThreads));
-        stats = (BinStats *)take(sizeof(BinStats));
-        scan_bytes = scan_ws_bytes(N);
-        scan_ws = take(scan_bytes);
-        sort_bytes = sort_ws_bytes(N);
-        sort_ws = take(sort_bytes);
-        bytes = off;
-    }
-};
-
 inline int tile_bits(int n_tiles) {
     int b = 1;
     while ((1LL << b) < n_tiles) ++b;
     return b;
 }
+
+// ------------------------------------------------------------ tile sort
+// Stable counting sort of the (tile, id) pairs by tile, in one pass over the
+// pairs, for up to kCsBuckets tiles (more take the radix sort). The pairs are
+// cut into chunks of 256 * per consecutive pairs, one workgroup each, dealt
+// to the XCDs in contiguous runs:
+//   1. count_hist    - chunk c's count of each tile -> hist[c][t];
+//   2. count_colscan - per tile, exclusive scan of its counts over the chunks
+//                      (in place) and the tile's total;
+//   3. count_scatter - each workgroup holds its chunk in registers, one
+//                      contiguous part of 64 * per pairs per wave, counts
+//                      each part into a wave-private LDS histogram, forms the
+//                      tile starts (exclusive scan of the totals) and from
+//                      them each wave's first slot per tile, then walks its
+//                      part in input order, ranking pairs of one tile by
+//                      ballots over the tile bits, and stores each id at its
+//                      slot.
+// A pair's slot is start(t) + the pairs of tile t in earlier chunks, in
+// earlier waves' parts and earlier in its own part: the input order within
+// each tile, i.e. the stable order. The tile starts double as the list
+// offsets. Pairs with a tile >= n_tiles are dropped.
+constexpr int kCsBuckets = 4096;
+constexpr int kCsThreads = 256, kCsWaves = kCsThreads / 64;
+constexpr int64_t kCsMaxChunks = 512;   // about two workgroups per CU
+constexpr int kColWaves = 16;           // waves of the column scan's workgroups
+
+struct CsPlan {
+    int per;        // pairs per lane (a chunk is 256 * per pairs)
+    int64_t nchunks;
+};
+
+// The smallest chunk that needs no more than kCsMaxChunks workgroups.
+inline CsPlan cs_plan(int64_t n) {
+    static const int kPers[] = {8, 16, 24, 32, 48, 64};
+    for (int p : kPers) {
+        const int64_t nc = ceil_div(n, (int64_t)kCsThreads * p);
+        if (nc <= kCsMaxChunks || p == 64) return {p, nc};
+    }
+    return {64, ceil_div(n, (int64_t)kCsThreads * 64)};
+}
+
+inline int64_t tile_sort_ws_bytes(int64_t n, int nb) {
+    return align256(4 * (int64_t)nb * cs_plan(n).nchunks) + align256(4 * (int64_t)nb);
+}
+
+// V is the value moved with each tile key: an int32 id, or a uint2
+// {id, depth bits}.
+template <typename V>
+struct CsPass {
+    const uint32_t *tiles;
+    const V *ids;
+    int64_t n;
+    int nb, nbits;                  // tiles; bits that tell them apart
+    V *out;
+    int32_t *offsets;               // tile starts, nb + 1
+    uint32_t *hist, *tot;           // hist[nchunks][nb], tot[nb]
+};
+
+// A chunk's tiles as kPer / 4 16-byte loads per thread, all in flight at once
+// (chunk starts are multiples of 2048 pairs, so 16-byte aligned); ~0 past n.
+template <int kPer>
+__device__ __forceinline__ void load_chunk_tiles(const uint32_t *tiles, int64_t n, int64_t b,
+                                                 uint32_t (&t)[kPer]) {
+#pragma unroll
+    for (int j = 0; j < kPer / 4; ++j) {
+        const int64_t i = b + 4 * ((int64_t)threadIdx.x + (int64_t)kCsThreads * j);
+        if (i + 4 <= n) {
+            const uint4 q = *reinterpret_cast<const uint4 *>(tiles + i);
+            t[4 * j] = q.x;
+            t[4 * j + 1] = q.y;
+            t[4 * j + 2] = q.z;
+            t[4 * j + 3] = q.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t[4 * j + e] = i + e < n ? tiles[i + e] : 0xFFFFFFFFu;
+        }
+    }
+}
+
+template <int kPer, typename V>
+__global__ __launch_bounds__(kCsThreads) void count_hist_kernel(const CsPass<V> P) {
+    __shared__ uint32_t s_h[kCsBuckets];
+    const int64_t c = xcd_contiguous(blockIdx.x, gridDim.x);
+    uint32_t t[kPer];
+    load_chunk_tiles<kPer>(P.tiles, P.n, c * kCsThreads * kPer, t);
+    for (int i = threadIdx.x; i < P.nb; i += kCsThreads) s_h[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kPer; ++r)
+        if (t[r] < (uint32_t)P.nb) atomicAdd(&s_h[t[r]], 1u);
+    __syncthreads();
+    uint32_t *row = P.hist + c * P.nb;
+    for (int i = threadIdx.x; i < P.nb; i += kCsThreads) row[i] = s_h[i];
+}
+
+// One workgroup per 64 tiles, lane = tile; each of its 16 waves scans a
+// sixteenth of the chunks (coalesced rows), the waves' sums are joined
+// through LDS, and each wave writes its running exclusive prefixes.
+template <typename V>
+__global__ __launch_bounds__(64 * kColWaves) void count_colscan_kernel(const CsPass<V> P,
+                                                                       int64_t nchunks) {
+    __shared__ uint32_t s_sum[kColWaves][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int bkt = blockIdx.x * 64 + lane;
+    const bool in = bkt < P.nb;
+    const int64_t q = (nchunks + kColWaves - 1) / kColWaves;
+    const int64_t c0 = wave * q, c1 = min(nchunks, c0 + q);
+    uint32_t sum = 0;
+#pragma unroll 8
+    for (int64_t c = c0; c < c1; ++c) sum += in ? P.hist[c * P.nb + bkt] : 0u;
+    s_sum[wave][lane] = sum;
+    __syncthreads();
+    uint32_t run = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kColWaves; ++w) {
+        const uint32_t v = s_sum[w][lane];
+        run += w < wave ? v : 0u;
+        all += v;
+    }
+    if (in) {
+#pragma unroll 8
+        for (int64_t c = c0; c < c1; ++c) {
+            uint32_t *h = P.hist + c * P.nb + bkt;
+            const uint32_t v = *h;
+            *h = run;
+            run += v;
+        }
+        if (wave == 0) P.tot[bkt] = all;
+    }
+}
+
+template <int kPer, typename V>
+__global__ __launch_bounds__(kCsThreads) void count_scatter_kernel(const CsPass<V> P) {
+    constexpr int64_t kChunk = (int64_t)kCsThreads * kPer, kPart = 64 * kPer;
+    constexpr int kTPer = kCsBuckets / kCsThreads;   // tiles owned per thread
+    __shared__ uint32_t s_wh[kCsWaves][kCsBuckets];   // per wave: count, then next slot
+    __shared__ uint32_t s_part[kCsWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t c = xcd_contiguous(blockIdx.x, gridDim.x);
+    const int64_t pb = c * kChunk + wave * kPart;
+    const int64_t n = P.n;
+    const int nb = P.nb;
+    // The wave's part: pair pb + 64 r + lane is (tile t[r], id v[r]); a tile
+    // of nb or more marks a dropped or absent pair.
+    uint32_t t[kPer];
+    V v[kPer];
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int64_t i = pb + 64 * r + lane;
+        t[r] = i < n ? P.tiles[i] : 0xFFFFFFFFu;
+        v[r] = i < n ? P.ids[i] : V{};
+    }
+    // Thread tid owns tiles [tid * kTPer, tid * kTPer + kTPer): their totals
+    // and this chunk's prefix, requested with the pairs.
+    const int t0 = tid * kTPer;
+    uint32_t tv[kTPer], hv[kTPer];
+#pragma unroll
+    for (int j = 0; j < kTPer; ++j) {
+        const bool in = t0 + j < nb;
+        tv[j] = in ? P.tot[t0 + j] : 0u;
+        hv[j] = in ? P.hist[c * nb + t0 + j] : 0u;
+    }
+    for (int i = tid; i < nb; i += kCsThreads) {
+#pragma unroll
+        for (int w = 0; w < kCsWaves; ++w) s_wh[w][i] = 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kPer; ++r)
+        if (t[r] < (uint32_t)nb) atomicAdd(&s_wh[wave][t[r]], 1u);
+    __syncthreads();
+    uint32_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < kTPer; ++j) sum += tv[j];
+    uint32_t incl = sum;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t u = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += u;
+    }
+    if (lane == 63) s_part[wave] = incl;
+    __syncthreads();
+    uint32_t start = incl - sum;
+    for (int w = 0; w < wave; ++w) start += s_part[w];
+#pragma unroll
+    for (int j = 0; j < kTPer; ++j) {
+        const int tt = t0 + j;
+        if (tt < nb) {
+            if (c == 0) P.offsets[tt] = (int32_t)start;
+            uint32_t slot = start + hv[j];
+#pragma unroll
+            for (int w = 0; w < kCsWaves; ++w) {
+                const uint32_t cnt = s_wh[w][tt];
+                s_wh[w][tt] = slot;
+                slot += cnt;
+            }
+        }
+        start += tv[j];
+    }
+    // The last thread's running start has passed every tile: the total.
+    if (c == 0 && tid == kCsThreads - 1) P.offsets[nb] = (int32_t)start;
+    __syncthreads();
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    uint32_t *wh = s_wh[wave];
+    // Lanes whose pair is in the same tile (kept pairs only): one ballot per
+    // tile bit, kept where the bit agrees; x is -1 where this lane's bit is 0.
+    auto peers_of = [&](uint32_t tt) {
+        uint64_t pm = ballot(tt < (uint32_t)nb);
+        const int32_t nt = (int32_t)~tt;
+        for (int b = 0; b < P.nbits; ++b) {
+            const int32_t x = __builtin_amdgcn_sbfe(nt, b, 1);
+            pm &= ballot(x == 0) ^ (uint64_t)(int64_t)x;
+        }
+        return pm;
+    };
+    uint64_t next = peers_of(t[0]);
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const bool ok = t[r] < (uint32_t)nb;
+        const uint64_t peers = next;
+        const uint32_t wr = (uint32_t)__popcll(peers & lt);
+        const uint32_t prior = ok ? wh[t[r]] : 0u;
+        // The next round's ballots overlap this round's LDS read.
+        if (r + 1 < kPer) next = peers_of(t[r + 1]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (ok && wr == 0) wh[t[r]] = prior + (uint32_t)__popcll(peers);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const uint32_t pos = prior + wr;
+        if (ok && (int64_t)pos < n) P.out[pos] = v[r];
+    }
+}
+
+// Sorts n (tile, value) pairs stably by tile into out, and writes the list
+// offsets (n_tiles + 1). Needs n_tiles <= kCsBuckets and n < 2^31.
+template <typename V>
+static int32_t tile_count_sort(const uint32_t *tiles, const V *ids, int64_t n, int n_tiles,
+                               V *out, int32_t *tile_offsets, void *ws, int64_t ws_bytes,
+                               hipStream_t s) {
+    MG_REQUIRE(n > 0 && n < (1LL << 31) && n_tiles >= 1 && n_tiles <= kCsBuckets,
+               "tile sort: %lld pairs over %d tiles", (long long)n, n_tiles);
+    MG_REQUIRE(ws && ws_bytes >= tile_sort_ws_bytes(n, n_tiles),
+               "tile sort: workspace %lld bytes, need %lld", (long long)ws_bytes,
+               (long long)tile_sort_ws_bytes(n, n_tiles));
+    const CsPlan plan = cs_plan(n);
+    CsPass<V> P{};
+    P.tiles = tiles;
+    P.ids = ids;
+    P.n = n;
+    P.nb = n_tiles;
+    P.nbits = tile_bits(n_tiles);
+    P.out = out;
+    P.offsets = tile_offsets;
+    P.hist = static_cast<uint32_t *>(ws);
+    P.tot = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) +
+                                         align256(4 * (int64_t)n_tiles * plan.nchunks));
+    const unsigned grid = (unsigned)plan.nchunks;
+    TimedScope ts("tile_sort", s);
+#define MG_CS(PER)                                                                     \
+    case PER:                                                                          \
+        count_hist_kernel<PER, V><<<grid, kCsThreads, 0, s>>>(P);                      \
+        MG_LAUNCHED("count_hist_kernel");                                              \
+        count_colscan_kernel<V><<<(unsigned)ceil_div(n_tiles, 64), 64 * kColWaves, 0, s>>>( \
+            P, plan.nchunks);                                                          \
+        MG_LAUNCHED("count_colscan_kernel");                                           \
+        count_scatter_kernel<PER, V><<<grid, kCsThreads, 0, s>>>(P);                   \
+        MG_LAUNCHED("count_scatter_kernel");                                           \
+        break;
+    switch (plan.per) {
+        MG_CS(8)
+        MG_CS(16)
+        MG_CS(24)
+        MG_CS(32)
+        MG_CS(48)
+        MG_CS(64)
+        default: MG_REQUIRE(false, "tile sort: %d pairs per lane", plan.per);
+    }
+#undef MG_CS
+    return MG_OK;
+}
+
+// ------------------------------------------------------ per-tile depth sort
+// One workgroup per tile sorts the tile's list [offsets[t], offsets[t+1]) of
+// {id, depth bits} pairs stably by the depth's float bits (positive depths
+// order as their bits), on only the bits in which the list's keys differ:
+// LSD passes of 8 bits. The list arrives in ascending id, so ties keep id
+// order. The ids are written to gauss_ids.
+//   * Up to kTdCap entries: the list lives in registers, each wave holding
+//     one contiguous quarter (rounded up to 64 entries); each pass ranks
+//     every wave's quarter against a wave-private LDS histogram, joins the
+//     waves through a digit scan, and exchanges the entries through LDS into
+//     their new order.
+//   * Longer lists: the same pass over chunks of kTdCap, in order, with the
+//     digit starts carried from chunk to chunk, ping-ponging between the
+//     input pairs and scratch of the list's own range.
+// Lanes of a round holding the same digit find each other through a 64-bit
+// LDS mask per digit: each ORs in its lane bit, then reads the mask back.
+constexpr int kTdThreads = 256, kTdWaves = kTdThreads / 64, kTdPer = 16;
+constexpr int kTdCap = kTdThreads * kTdPer;
+
+struct TdArgs {
+    const int32_t *offsets;
+    uint2 *pairs;                     // {id, depth bits}, grouped by tile (clobbered)
+    uint2 *pairs_b;                   // scratch for lists longer than kTdCap
+    int32_t *ids;                     // gauss_ids
+};
+
+struct TdShared {
+    uint32_t key[kTdCap];
+    int32_t id[kTdCap];
+    uint32_t wh[kTdWaves][256];               // per wave: digit counts, then slots
+    unsigned long long mask[kTdWaves][256];   // per wave: lanes of a round per digit
+    uint32_t run[256], tot[256];
+    uint32_t red[2 * kTdWaves];
+};
+
+// Workgroup min and max of the keys.
+__device__ __forceinline__ void td_minmax(uint32_t &kmin, uint32_t &kmax, uint32_t *red) {
+    for (int o = 32; o >= 1; o >>= 1) {
+        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, 64));
+        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, 64));
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) {
+        red[wave] = kmin;
+        red[kTdWaves + wave] = kmax;
+    }
+    __syncthreads();
+    kmin = red[0];
+    kmax = red[kTdWaves];
+#pragma unroll
+    for (int w = 1; w < kTdWaves; ++w) {
+        kmin = min(kmin, red[w]);
+        kmax = max(kmax, red[kTdWaves + w]);
+    }
+}
+
+// Ranks the entries this lane holds in rounds [0, rounds) (bit r of valid
+// marks a real entry) by digit d[r]: rank[r] = entries of digit d[r] before
+// it in the wave's part. Counts accumulate in wh (zeroed by the caller); wm
+// is zero on entry and on exit.
+__device__ __forceinline__ void td_rank(const uint32_t (&d)[kTdPer], uint32_t valid, int rounds,
+                                        uint32_t (&rank)[kTdPer], uint32_t *wh,
+                                        unsigned long long *wm) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+    for (int r = 0; r < kTdPer; ++r) {
+        if (r < rounds) {   // wave-uniform
+            const bool ok = (valid >> r) & 1u;
+            if (ok) atomicOr(&wm[d[r]], 1ull << lane);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const uint64_t pm = ok ? wm[d[r]] : 0ull;
+            const uint32_t prior = ok ? wh[d[r]] : 0u;
+            const uint32_t wr = (uint32_t)__popcll(pm & lt);
+            rank[r] = prior + wr;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (ok && wr == 0) {
+                wh[d[r]] = prior + (uint32_t)__popcll(pm);
+                wm[d[r]] = 0ull;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    }
+}
+
+// After td_rank: wh[w][dg] becomes the slot of wave w's first entry of digit
+// dg: the digit's start plus the entries of that digit in earlier waves. The
+// digit starts are an exclusive scan of the digit totals, or with base
+// (chunked lists) base[dg], the running start carried from earlier chunks.
+// tot (may be null) gets the digit totals. One digit per thread.
+__device__ __forceinline__ void td_slots(TdShared &S, uint32_t *tot, const uint32_t *base) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t cnt = 0, c[kTdWaves];
+#pragma unroll
+    for (int w = 0; w < kTdWaves; ++w) {
+        c[w] = S.wh[w][tid];
+        cnt += c[w];
+    }
+    uint32_t start;
+    if (base) {
+        start = base[tid];
+    } else {
+        uint32_t incl = cnt;
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t u = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += u;
+        }
+        if (lane == 63) S.red[wave] = incl;
+        __syncthreads();
+        start = incl - cnt;
+        for (int w = 0; w < wave; ++w) start += S.red[w];
+    }
+#pragma unroll
+    for (int w = 0; w < kTdWaves; ++w) {
+        S.wh[w][tid] = start;
+        start += c[w];
+    }
+    if (tot) tot[tid] = cnt;
+}
+
+// Entries per wave part for a list (or chunk) of len: a quarter, rounded up
+// to whole rounds of 64.
+__device__ __forceinline__ int td_part(int len) { return ((len + 4 * 64 - 1) / (4 * 64)) * 64; }
+
+__global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArgs A) {
+    __shared__ TdShared S;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t = (int)xcd_contiguous(blockIdx.x, gridDim.x);
+    const int64_t s0 = A.offsets[t];
+    const int64_t len = (int64_t)A.offsets[t + 1] - s0;
+    if (len <= 0) return;   // workgroup-uniform
+    const uint2 *in = A.pairs + s0;
+    if (len == 1) {
+        if (tid == 0) A.ids[s0] = (int32_t)in[0].x;
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) S.mask[wave][lane + 64 * j] = 0ull;
+
+    if (len <= kTdCap) {
+        const int part = td_part((int)len), rounds = part / 64;
+        const int pb = wave * part + lane;   // entry of round r: pb + 64 r
+        uint32_t k[kTdPer], d[kTdPer], rank[kTdPer];
+        int32_t v[kTdPer];
+        uint32_t valid = 0, kmin = 0xFFFFFFFFu, kmax = 0u;
+#pragma unroll
+        for (int r = 0; r < kTdPer; ++r) {
+            const int i = pb + 64 * r;
+            const bool ok = r < rounds && i < len && 64 * r < part;
+            uint2 q = make_uint2(0u, 0u);
+            if (ok) q = in[i];
+            v[r] = (int32_t)q.x;
+            k[r] = q.y;
+            if (ok) {
+                valid |= 1u << r;
+                kmin = min(kmin, k[r]);
+                kmax = max(kmax, k[r]);
+            }
+        }
+        td_minmax(kmin, kmax, S.red);
+        const uint32_t span = kmax - kmin;
+        const int bits = span == 0u ? 0 : 32 - __builtin_clz(span);
+        for (int shift = 0; shift < bits; shift += 8) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) S.wh[wave][lane + 64 * j] = 0;
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < kTdPer; ++r) d[r] = ((k[r] - kmin) >> shift) & 255u;
+            td_rank(d, valid, rounds, rank, S.wh[wave], S.mask[wave]);
+            __syncthreads();
+            td_slots(S, nullptr, nullptr);
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < kTdPer; ++r) {
+                if ((valid >> r) & 1u) {
+                    const uint32_t pos = S.wh[wave][d[r]] + rank[r];
+                    S.key[pos] = k[r];
+                    S.id[pos] = v[r];
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < kTdPer; ++r) {
+                if ((valid >> r) & 1u) {
+                    const int i = pb + 64 * r;
+                    k[r] = S.key[i];
+                    v[r] = S.id[i];
+                }
+            }
+            // The next pass rewrites wh and red only after its barrier.
+        }
+#pragma unroll
+        for (int r = 0; r < kTdPer; ++r)
+            if ((valid >> r) & 1u) A.ids[s0 + pb + 64 * r] = v[r];
+        return;
+    }
+
+    // Longer lists: key range, then passes over chunks of kTdCap in order,
+    // ping-ponging between the input pairs and pairs_b.
+    uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+    for (int64_t i = tid; i < len; i += kTdThreads) {
+        const uint32_t kk = in[i].y;
+        kmin = min(kmin, kk);
+        kmax = max(kmax, kk);
+    }
+    td_minmax(kmin, kmax, S.red);
+    const uint32_t span = kmax - kmin;
+    const int bits = span == 0u ? 0 : 32 - __builtin_clz(span);
+    uint2 *pin = A.pairs + s0, *pout = A.pairs_b + s0;
+    for (int shift = 0; shift < bits; shift += 8) {
+        // Digit totals over the list -> the running digit starts S.run.
+        S.tot[tid] = 0;
+        __syncthreads();
+        for (int64_t i = tid; i < len; i += kTdThreads)
+            atomicAdd(&S.tot[((pin[i].y - kmin) >> shift) & 255u], 1u);
+        __syncthreads();
+        {
+            const uint32_t cnt = S.tot[tid];
+            uint32_t incl = cnt;
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t u = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += u;
+            }
+            if (lane == 63) S.red[wave] = incl;
+            __syncthreads();
+            uint32_t start = incl - cnt;
+            for (int w = 0; w < wave; ++w) start += S.red[w];
+            S.run[tid] = start;
+        }
+        for (int64_t c0 = 0; c0 < len; c0 += kTdCap) {
+            const int cl = (int)min((int64_t)kTdCap, len - c0);
+            const int part = td_part(cl), rounds = part / 64;
+            const int pb = wave * part + lane;
+            uint32_t k[kTdPer], d[kTdPer], rank[kTdPer];
+            int32_t v[kTdPer];
+            uint32_t valid = 0;
+#pragma unroll
+            for (int r = 0; r < kTdPer; ++r) {
+                const int i = pb + 64 * r;
+                const bool ok = r < rounds && i < cl && 64 * r < part;
+                uint2 q = make_uint2(0u, 0u);
+                if (ok) q = pin[c0 + i];
+                v[r] = (int32_t)q.x;
+                k[r] = q.y;
+                valid |= ok ? 1u << r : 0u;
+                d[r] = ((k[r] - kmin) >> shift) & 255u;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) S.wh[wave][lane + 64 * j] = 0;
+            __syncthreads();
+            td_rank(d, valid, rounds, rank, S.wh[wave], S.mask[wave]);
+            __syncthreads();
+            td_slots(S, S.tot, S.run);
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < kTdPer; ++r) {
+                if ((valid >> r) & 1u) {
+                    const uint32_t pos = S.wh[wave][d[r]] + rank[r];
+                    pout[pos] = make_uint2((uint32_t)v[r], k[r]);
+                }
+            }
+            S.run[tid] += S.tot[tid];   // this chunk's entries of digit tid
+            __syncthreads();
+        }
+        // This pass's stores reach the next pass's loads: same workgroup,
+        // ordered by the barrier's release and acquire.
+        __syncthreads();
+        uint2 *tp = pin;
+        pin = pout;
+        pout = tp;
+    }
+    for (int64_t i = tid; i < len; i += kTdThreads) A.ids[s0 + i] = (int32_t)pin[i].x;
+}
+
+// {id, depth bits} pairs from ids and the depth array (the radix route, for
+// more tiles than the counting sort takes).
+__global__ __launch_bounds__(256) void gather_depth_pairs_kernel(const int32_t *ids,
+                                                                 const float *depth, int64_t n,
+                                                                 uint2 *pairs) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int32_t g = ids[i];
+    pairs[i] = make_uint2((uint32_t)g, __float_as_uint(depth[g]));
+}
+
+// Carves the begin/finish workspace identically on both calls. After begin,
+// counts and offsets hold each Gaussian's tile count and its exclusive scan,
+// recs the walk records.
+struct BeginWs {
+    int32_t *counts, *offsets;
+    BinRec *recs;
+    BinPart *parts;
+    BinStats *stats;
+    void *scan_ws;
+    int64_t scan_bytes, bytes;
+    BeginWs(void *base, int64_t N) {
+        char *p = static_cast<char *>(base);
+        int64_t off = 0;
+        auto take = [&](int64_t b) { char *q = p ? p + off : nullptr; off += align256(b); return q; };
+        counts = (int32_t *)take(4 * N);
+        offsets = (int32_t *)take(4 * N);
+        recs = (BinRec *)take((int64_t)sizeof(BinRec) * N);
+        parts = (BinPart *)take((int64_t)sizeof(BinPart) * ceil_div(N, kBinThreads));
+        stats = (BinStats *)take(sizeof(BinStats));
+        scan_bytes = scan_ws_bytes(N);
+        scan_ws = take(scan_bytes);
+        bytes = off;
+    }
+};
 
 static int32_t check_bin_args(const char *who, int64_t N, const void *uv, const void *rxy,
                               const void *conic, const void *opac, const void *valid, int W,
@@ -802,7 +1338,8 @@ int32_t mg_exclusive_scan_i32(const int32_t *in, int64_t n, int32_t *out, int64_
     MG_REQUIRE(total_dev, "mg_exclusive_scan_i32: null total_dev");
     MG_REQUIRE(n == 0 || (in && out), "mg_exclusive_scan_i32: null input/output");
     hipStream_t s = as_stream(stream);
-    int32_t rc = exclusive_scan(in, nullptr, n, out, total_dev, workspace, workspace_bytes, s);
+    int32_t rc =
+        exclusive_scan(in, nullptr, n, out, total_dev, workspace, workspace_bytes, s, nullptr);
     if (rc != MG_OK) return rc;
     if (total_host) {
         MG_HIP(hipMemcpyAsync(total_host, total_dev, sizeof(int64_t), hipMemcpyDeviceToHost, s));
@@ -842,11 +1379,39 @@ int32_t mg_tile_ranges(const uint64_t *sorted_keys, int64_t n, int32_t n_tiles,
     return MG_OK;
 }
 
+int64_t mg_sort_pairs_by_tile_workspace_bytes(int64_t n, int32_t n_tiles) {
+    if (n <= 0 || n_tiles < 1) return 0;
+    return tile_sort_ws_bytes(n, n_tiles);
+}
+
+int32_t mg_sort_pairs_by_tile(int64_t n, const uint32_t *tiles, const int32_t *ids,
+                              int32_t n_tiles, int32_t *ids_out, int32_t *tile_offsets,
+                              void *workspace, int64_t workspace_bytes, mg_stream_t stream) {
+    MG_REQUIRE(n > 0 && n < (1LL << 31), "mg_sort_pairs_by_tile: n = %lld", (long long)n);
+    MG_REQUIRE(n_tiles >= 1 && n_tiles <= kCsBuckets, "mg_sort_pairs_by_tile: %d tiles (1..%d)",
+               n_tiles, kCsBuckets);
+    MG_REQUIRE(tiles && ids && ids_out && tile_offsets, "mg_sort_pairs_by_tile: null pointer");
+    MG_REQUIRE(ids_out != ids, "mg_sort_pairs_by_tile: ids_out must not alias ids");
+    MG_REQUIRE(((uintptr_t)tiles & 15) == 0, "mg_sort_pairs_by_tile: tiles not 16-byte aligned");
+    return tile_count_sort(tiles, ids, n, n_tiles, ids_out, tile_offsets, workspace,
+                           workspace_bytes, as_stream(stream));
+}
+
 int64_t mg_bin_lists_workspace_bytes(int64_t N) { return BeginWs(nullptr, N > 0 ? N : 1).bytes; }
 
+// Scratch of either tile sort: the radix passes' histograms, or the counting
+// sort's per-chunk counts at its largest tile count.
+static int64_t finish_sort_bytes(int64_t T) {
+    return align256(std::max(sort_ws_bytes(T), tile_sort_ws_bytes(T, kCsBuckets)));
+}
+
+// Two regions of 8 bytes per pair (the pairs' {id, depth bits} values, and
+// the tile-sorted copy), the pairs' tile keys, then the sort scratch. The
+// radix route (more than kCsBuckets tiles) keeps its second key buffer and
+// id buffer in the first region.
 int64_t mg_bin_lists_finish_workspace_bytes(int64_t total) {
     const int64_t T = total > 0 ? total : 1;
-    return 3 * align256(4 * T) + align256(sort_ws_bytes(T));
+    return 5 * align256(4 * T) + finish_sort_bytes(T);
 }
 
 int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy, const float *conic,
@@ -867,32 +1432,22 @@ int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy, const f
     const int64_t nparts = N > 0 ? ceil_div(N, kBinThreads) : 0;
     if (N > 0) {
         TimedScope ts("bin_count", s);
-        bin_count_rec_kernel<<<(unsigned)nparts, kBinThreads, 0, s>>>(
-            A, ws.counts, ws.recs, ws.dkey_a, ws.perm_a, ws.parts);
+        bin_count_rec_kernel<<<(unsigned)nparts, kBinThreads, 0, s>>>(A, ws.counts, ws.recs,
+                                                                       ws.parts);
         MG_LAUNCHED("bin_count_rec_kernel");
     }
     bin_stats_kernel<<<1, 256, 0, s>>>(ws.parts, nparts, ws.stats);
     MG_LAUNCHED("bin_stats_kernel");
     // The one host read: the total sizes the caller's id buffer. It is copied
-    // into a pinned word behind an event, and the depth sort and the scan are
-    // queued before the host waits, so the GPU keeps working meanwhile. The
-    // sort reads its key window and live bit count on the device: all four
-    // 8-bit passes are queued, those above the live bits only copy, and the
-    // even pass count leaves the order in perm_a.
+    // into a pinned word behind an event, and the scan is queued before the
+    // host waits, so the GPU keeps working meanwhile.
     HostReadback rb;
     if (!rb.ok()) return MG_ERR_RUNTIME;
     MG_HIP(hipMemcpyAsync(rb.slot, &ws.stats->total, sizeof(int64_t), hipMemcpyDeviceToHost, s));
     MG_HIP(hipEventRecord(rb.ev, s));
     if (N > 0) {
-        uint32_t *rk;
-        int32_t *rv;
-        rc = radix_sort_passes<uint32_t>(ws.dkey_a, ws.perm_a, ws.dkey_b, ws.perm_b, N, 0, 32,
-                                         ws.sort_ws, ws.sort_bytes, s, "depth_sort", &rk, &rv,
-                                         0u, 0xFFFFFFFFu, &ws.stats->win);
-        if (rc != MG_OK) return rc;
-        MG_REQUIRE(rv == ws.perm_a, "mg_bin_lists_begin: depth order in the wrong buffer");
-        rc = exclusive_scan(ws.counts, ws.perm_a, N, ws.offsets,
-                            (int64_t *)&ws.stats->scan_total, ws.scan_ws, ws.scan_bytes, s);
+        rc = exclusive_scan(ws.counts, nullptr, N, ws.offsets, (int64_t *)&ws.stats->scan_total,
+                            ws.scan_ws, ws.scan_bytes, s, nullptr);
         if (rc != MG_OK) return rc;
     }
     MG_HIP(hipEventSynchronize(rb.ev));
@@ -927,36 +1482,66 @@ int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy, const 
     hipStream_t s = as_stream(stream);
     const int n_tiles = tiles_x * tiles_y;
     const int64_t T = total > 0 ? total : 1;
+    const int64_t T4 = align256(4 * T);
     char *f = static_cast<char *>(finish_workspace);
-    uint32_t *tk_a = (uint32_t *)f;
-    uint32_t *tk_b = (uint32_t *)(f + align256(4 * T));
-    int32_t *ids_tmp = (int32_t *)(f + 2 * align256(4 * T));
-    void *sort_ws = f + 3 * align256(4 * T);
-    const int64_t sort_bytes = align256(sort_ws_bytes(T));
+    uint2 *pairs_a = (uint2 *)f;                      // region A: 2 * T4 bytes
+    uint2 *pairs_b = (uint2 *)(f + 2 * T4);           // region B: 2 * T4 bytes
+    uint32_t *tk_a = (uint32_t *)(f + 4 * T4);
+    void *sort_ws = f + 5 * T4;
+    const int64_t sort_bytes = finish_sort_bytes(T);
     uint32_t *res_tiles = tk_a;
     if (total > 0) {
         MG_REQUIRE(gauss_ids, "mg_bin_lists_finish: null gauss_ids");
         MG_REQUIRE(N > 0, "mg_bin_lists_finish: %lld intersections from no Gaussians",
                    (long long)total);
-        // Emit into the id buffer the last sort pass will NOT write, so the
-        // sorted ids end in gauss_ids whatever the pass count's parity.
+        MG_REQUIRE(depth, "mg_bin_lists_finish: null depth");
+        // Pairs in Gaussian order, grouped by tile, then each tile's list
+        // sorted by depth. Up to kCsBuckets tiles, bin_write emits {id, depth
+        // bits} values that the one-pass counting sort carries (and it writes
+        // the offsets). Otherwise bin_write emits ids, radix passes sort them
+        // into gauss_ids (from the id buffer their last pass will NOT write,
+        // so they end there whatever the pass count's parity), tile_ranges
+        // writes the offsets, and the depth bits are gathered afterwards.
+        const bool counting = n_tiles <= kCsBuckets;
         const int bits = tile_bits(n_tiles);
         const bool even = ((bits + 7) / 8) % 2 == 0;
+        uint32_t *tk_b = (uint32_t *)pairs_a;
+        int32_t *ids_tmp = (int32_t *)((char *)pairs_a + T4);
         int32_t *ids_a = even ? gauss_ids : ids_tmp;
         int32_t *ids_b = even ? ids_tmp : gauss_ids;
         {
             TimedScope ts("bin_write", s);
             bin_write_rec_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(
-                ws.recs, ws.perm_a, ws.offsets, N, total, tile, W, H, tiles_x,
-                conic != nullptr ? 1 : 0, tk_a, ids_a);
+                ws.recs, ws.offsets, N, total, tile, W, H, tiles_x, conic != nullptr ? 1 : 0,
+                tk_a, counting ? nullptr : ids_a, depth, counting ? pairs_a : nullptr);
             MG_LAUNCHED("bin_write_rec_kernel");
         }
-        int32_t *rv;
-        rc = radix_sort_passes<uint32_t>(tk_a, ids_a, tk_b, ids_b, total, 0, bits, sort_ws,
-                                         sort_bytes, s, "tile_sort", &res_tiles, &rv, 0u,
-                                         0xFFFFFFFFu, nullptr);
-        if (rc != MG_OK) return rc;
-        MG_REQUIRE(rv == gauss_ids, "mg_bin_lists_finish: ids landed in the wrong buffer");
+        if (counting) {
+            rc = tile_count_sort<uint2>(tk_a, pairs_a, total, n_tiles, pairs_b, tile_offsets,
+                                        sort_ws, sort_bytes, s);
+            if (rc != MG_OK) return rc;
+        } else {
+            int32_t *rv;
+            rc = radix_sort_passes<uint32_t>(tk_a, ids_a, tk_b, ids_b, total, 0, bits, sort_ws,
+                                             sort_bytes, s, "tile_sort", &res_tiles, &rv, 0u,
+                                             0xFFFFFFFFu, nullptr);
+            if (rc != MG_OK) return rc;
+            MG_REQUIRE(rv == gauss_ids, "mg_bin_lists_finish: ids landed in the wrong buffer");
+            {
+                TimedScope ts("tile_ranges", s);
+                tile_ranges_u32_kernel<<<(unsigned)ceil_div(total + 1, 256), 256, 0, s>>>(
+                    res_tiles, total, n_tiles, tile_offsets);
+                MG_LAUNCHED("tile_ranges_u32_kernel");
+            }
+            gather_depth_pairs_kernel<<<(unsigned)ceil_div(total, 256), 256, 0, s>>>(
+                gauss_ids, depth, total, pairs_b);
+            MG_LAUNCHED("gather_depth_pairs_kernel");
+        }
+        TdArgs D{tile_offsets, pairs_b, pairs_a, gauss_ids};
+        TimedScope ts("depth_sort", s);
+        tile_depth_sort_kernel<<<(unsigned)n_tiles, kTdThreads, 0, s>>>(D);
+        MG_LAUNCHED("tile_depth_sort_kernel");
+        return MG_OK;
     }
     TimedScope ts("tile_ranges", s);
     tile_ranges_u32_kernel<<<(unsigned)ceil_div(total + 1, 256), 256, 0, s>>>(res_tiles, total,

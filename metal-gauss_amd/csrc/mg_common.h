@@ -53,6 +53,15 @@ inline int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
 // Number of XCDs workgroups are spread over, round-robin by workgroup id.
 constexpr int kXcds = 8;
 
+// Work item of workgroup b out of nb such that each XCD runs one contiguous
+// run of items (XCD k the k-th run, the first nb % 8 runs one item longer):
+// neighbouring items then share an L2. A bijection of [0, nb).
+__device__ __forceinline__ int64_t xcd_contiguous(int64_t b, int64_t nb) {
+    const int64_t q = nb / kXcds, r = nb - q * kXcds;
+    const int64_t xcd = b % kXcds, idx = b / kXcds;
+    return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+}
+
 #define MG_REQUIRE(cond, ...)                                                  \
     do {                                                                       \
         if (!(cond)) {                                                         \

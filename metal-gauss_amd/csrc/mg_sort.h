@@ -44,8 +44,10 @@ int64_t scan_ws_bytes(int64_t n);
 
 // out[i] = sum_{j<i} in[idx ? idx[j] : j]; total to total_dev (device int64).
 // With idx the values are gathered once (into out, which the second kernel
-// then scans in place).
+// then scans in place). idx_dev (device, may be null) supplies idx on the
+// device instead, for an index buffer chosen by an earlier kernel.
 int32_t exclusive_scan(const int32_t *in, const int32_t *idx, int64_t n, int32_t *out,
-                       int64_t *total_dev, void *ws, int64_t ws_bytes, hipStream_t s);
+                       int64_t *total_dev, void *ws, int64_t ws_bytes, hipStream_t s,
+                       const int32_t *const *idx_dev);
 
 }  // namespace mg

@@ -23,6 +23,13 @@ namespace mg {
 
 constexpr int kPreThreads = 256;
 
+// Activations taken inside the projection (train.py:221-222 takes them in
+// torch before render): the scales argument holds log scales (exp), the
+// opacity argument logits (sigmoid). The effective-opacity kernels only.
+constexpr int32_t kActLogScale = 1, kActLogitOpac = 2;
+
+__device__ __forceinline__ float act_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
 struct Cam {
     float R[9];      // world->camera rotation, row-major
     float t[3];
@@ -374,6 +381,7 @@ struct PreFwdArgs {
     const float *filt;
     int32_t aa;
     float *op_eff;
+    int32_t act;   // kActLogScale | kActLogitOpac (effective-opacity kernel only)
 };
 
 template <bool MIP>
@@ -392,6 +400,12 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFw
         const float qv[4] = {A.quats[4 * g], A.quats[4 * g + 1], A.quats[4 * g + 2], A.quats[4 * g + 3]};
         float sv[3] = {A.scales[3 * g], A.scales[3 * g + 1], A.scales[3 * g + 2]};
         float op = A.opac[g];
+        if (MIP && (A.act & kActLogScale)) {
+            sv[0] = expf(sv[0]);
+            sv[1] = expf(sv[1]);
+            sv[2] = expf(sv[2]);
+        }
+        if (MIP && (A.act & kActLogitOpac)) op = act_sigmoid(op);
         if (MIP && A.filt) {
             Mip3 M3;
             mip3_apply(A.filt[g], sv, M3);
@@ -512,6 +526,7 @@ struct PreBwdArgs {
     const float *opac, *filt, *d_oe;
     int32_t aa;
     float *d_op;
+    int32_t act;   // kActLogScale | kActLogitOpac (effective-opacity kernel only)
 };
 
 template <bool MIP>
@@ -659,7 +674,20 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
 
     // ------------------------------------------ projection: lane = Gaussian
     if (vld != 0) {
-        float sv[3] = {sraw[0], sraw[1], sraw[2]};
+        // s0: the activated scales before the 3D filter; op0: the activated
+        // opacity.
+        float s0[3] = {sraw[0], sraw[1], sraw[2]};
+        float op0 = 0.0f;
+        if (MIP) {
+            if (A.act & kActLogScale) {
+                s0[0] = expf(s0[0]);
+                s0[1] = expf(s0[1]);
+                s0[2] = expf(s0[2]);
+            }
+            op0 = A.opac[g];
+            if (A.act & kActLogitOpac) op0 = act_sigmoid(op0);
+        }
+        float sv[3] = {s0[0], s0[1], s0[2]};
         Mip3 M3;
         M3.coef = 1.0f;
         float f3 = 0.0f;
@@ -688,7 +716,7 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
             const float d_oe = A.d_oe[(int64_t)A.so * g];
             d_op1 = d_oe;
             if (A.aa) {
-                const float op1 = A.opac[g] * M3.coef;
+                const float op1 = op0 * M3.coef;
                 const float det0 = P.a0 * P.c0 - b * b;
                 const float r = fmaxf(det0, 0.0f) / fmaxf(det, 1e-12f);
                 const float coef2 = sqrtf(fminf(fmaxf(r, 0.0f), 1.0f));
@@ -777,17 +805,26 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_bwd_kernel(const PreBw
             if (A.filt) {
                 // s' = sqrt(s^2 + f^2): ds = ds' s / s'. coef3^2 = prod s^2 /
                 // prod (s^2 + f^2): d coef3 / d s_j = coef3 f^2 / (s_j (s_j^2 + f^2)).
-                const float dcoef3 = d_op1 * A.opac[g];
+                const float dcoef3 = d_op1 * op0;
                 const float f2 = f3 * f3;
 #pragma unroll
                 for (int j = 0; j < 3; ++j) {
-                    const float chain = sv[j] > 0.0f ? dsc[j] * sraw[j] / sv[j] : 0.0f;
-                    const float dimm = sraw[j] > 0.0f
-                        ? dcoef3 * M3.coef * f2 / (sraw[j] * M3.s2f[j]) : 0.0f;
+                    const float chain = sv[j] > 0.0f ? dsc[j] * s0[j] / sv[j] : 0.0f;
+                    const float dimm = s0[j] > 0.0f
+                        ? dcoef3 * M3.coef * f2 / (s0[j] * M3.s2f[j]) : 0.0f;
                     dsc[j] = chain + dimm;
                 }
             }
-            A.d_op[g] = d_op1 * M3.coef;
+            float dop = d_op1 * M3.coef;
+            // Through the activations, as torch's backward of exp (grad *
+            // result) and of sigmoid (grad * (1 - y) * y).
+            if (A.act & kActLogitOpac) dop = dop * (1.0f - op0) * op0;
+            A.d_op[g] = dop;
+            if (A.act & kActLogScale) {
+                dsc[0] = dsc[0] * s0[0];
+                dsc[1] = dsc[1] * s0[1];
+                dsc[2] = dsc[2] * s0[2];
+            }
         }
         A.d_scales[3 * g] = dsc[0];
         A.d_scales[3 * g + 1] = dsc[1];
@@ -842,10 +879,10 @@ static int32_t preprocess_fwd(int64_t N, const float *means, const float *quats,
                               float fx, float fy, float cx, float cy, int32_t W, int32_t H,
                               float near_plane, float far_plane, float blur, float max_radius,
                               const float *cam_center, int32_t sh_degree, bool mip,
-                              const float *filter_3d, int32_t antialias, float *uv,
-                              float *conic, float *depth, float *rxy, int32_t *valid,
-                              uint8_t *valid_mask, float *color, float *opacity_eff,
-                              mg_stream_t stream, const char *who) {
+                              const float *filter_3d, int32_t antialias, int32_t activations,
+                              float *uv, float *conic, float *depth, float *rxy,
+                              int32_t *valid, uint8_t *valid_mask, float *color,
+                              float *opacity_eff, mg_stream_t stream, const char *who) {
     PreFwdArgs A{};
     int32_t rc = make_cam(A.C, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane, blur,
                           max_radius, cam_center, sh_degree, who);
@@ -858,12 +895,15 @@ static int32_t preprocess_fwd(int64_t N, const float *means, const float *quats,
     MG_REQUIRE(sh == nullptr || sh_fused || sh_rest != nullptr,
                "SH must be either one (N,16,3) tensor or (N,1,3)+(N,15,3)");
     MG_REQUIRE(!mip || opacity_eff != nullptr, "%s: null effective-opacity output", who);
+    MG_REQUIRE((activations & ~(kActLogScale | kActLogitOpac)) == 0 && (mip || activations == 0),
+               "%s: activations %d (bit 0: log scales, bit 1: logit opacities)", who,
+               activations);
     A.N = N;
     A.means = means; A.quats = quats; A.scales = scales; A.sh = sh;
     A.rest = sh_rest; A.opac = opacities; A.fused = sh_fused;
     A.uv = uv; A.conic = conic; A.depth = depth; A.rxy = rxy; A.valid = valid; A.color = color;
     A.valid_mask = valid_mask;
-    A.filt = filter_3d; A.aa = antialias; A.op_eff = opacity_eff;
+    A.filt = filter_3d; A.aa = antialias; A.op_eff = opacity_eff; A.act = activations;
     A.vec4 = sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)sh & 15) == 0);
     const int64_t blocks = ceil_div(N, kPreThreads);
     TimedScope ts("preprocess_forward", as_stream(stream));
@@ -884,6 +924,7 @@ static int32_t preprocess_bwd(int64_t N, const float *means, const float *quats,
                               float blur, float max_radius, const float *cam_center,
                               int32_t sh_degree, bool mip,
                               const float *opacities, const float *filter_3d, int32_t antialias,
+                              int32_t activations,
                               const float *d_opacity_eff, float *d_means, float *d_quats,
                               float *d_scales, float *d_sh, float *d_sh_rest,
                               float *d_opacities, mg_stream_t stream, const char *who) {
@@ -903,6 +944,9 @@ static int32_t preprocess_bwd(int64_t N, const float *means, const float *quats,
                "%s: null opacity pointer", who);
     MG_REQUIRE(grad_stride == 0 || grad_stride >= 3, "%s: gradient record stride %d", who,
                grad_stride);
+    MG_REQUIRE((activations & ~(kActLogScale | kActLogitOpac)) == 0 && (mip || activations == 0),
+               "%s: activations %d (bit 0: log scales, bit 1: logit opacities)", who,
+               activations);
     A.su = grad_stride ? grad_stride : 2;
     A.sk = grad_stride ? grad_stride : 3;
     A.sc = grad_stride ? grad_stride : 3;
@@ -913,7 +957,7 @@ static int32_t preprocess_bwd(int64_t N, const float *means, const float *quats,
     A.d_means = d_means; A.d_quats = d_quats; A.d_scales = d_scales; A.d_sh = d_sh;
     A.d_rest = d_sh_rest;
     A.opac = opacities; A.filt = filter_3d; A.aa = antialias; A.d_oe = d_opacity_eff;
-    A.d_op = d_opacities;
+    A.d_op = d_opacities; A.act = activations;
     A.vec4 = sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)sh & 15) == 0);
     A.st_vec4 = d_sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)d_sh & 15) == 0);
     const int64_t blocks = ceil_div(N, kPreThreads);
@@ -942,7 +986,7 @@ int32_t mg_preprocess_forward(int64_t N, const float *means, const float *quats,
                               uint8_t *valid_mask, float *color, mg_stream_t stream) {
     return preprocess_fwd(N, means, quats, scales, sh, sh_rest, sh_fused, opacities, viewmat,
                           fx, fy, cx, cy, W, H, near_plane, far_plane, blur, max_radius,
-                          cam_center, sh_degree, false, nullptr, 0, uv, conic, depth, rxy,
+                          cam_center, sh_degree, false, nullptr, 0, 0, uv, conic, depth, rxy,
                           valid, valid_mask, color, nullptr, stream, "mg_preprocess_forward");
 }
 
@@ -953,13 +997,14 @@ int32_t mg_preprocess_forward_mip(int64_t N, const float *means, const float *qu
                                   int32_t W, int32_t H, float near_plane, float far_plane,
                                   float blur, float max_radius, const float *cam_center,
                                   int32_t sh_degree, const float *filter_3d, int32_t antialias,
-                                  float *uv, float *conic, float *depth, float *rxy,
+                                  int32_t activations, float *uv, float *conic, float *depth,
+                                  float *rxy,
                                   int32_t *valid, uint8_t *valid_mask, float *color,
                                   float *opacity_eff, mg_stream_t stream) {
     return preprocess_fwd(N, means, quats, scales, sh, sh_rest, sh_fused, opacities, viewmat,
                           fx, fy, cx, cy, W, H, near_plane, far_plane, blur, max_radius,
-                          cam_center, sh_degree, true, filter_3d, antialias, uv, conic, depth,
-                          rxy, valid, valid_mask, color, opacity_eff, stream,
+                          cam_center, sh_degree, true, filter_3d, antialias, activations, uv,
+                          conic, depth, rxy, valid, valid_mask, color, opacity_eff, stream,
                           "mg_preprocess_forward_mip");
 }
 
@@ -976,7 +1021,7 @@ int32_t mg_preprocess_backward(int64_t N, const float *means, const float *quats
     return preprocess_bwd(N, means, quats, scales, sh, sh_rest, sh_fused, d_uv, d_conic,
                           d_color, grad_stride, valid, viewmat, fx, fy, cx, cy, W, H, near_plane,
                           far_plane, blur, max_radius, cam_center, sh_degree, false, nullptr,
-                          nullptr, 0,
+                          nullptr, 0, 0,
                           nullptr, d_means, d_quats, d_scales, d_sh, d_sh_rest, nullptr, stream,
                           "mg_preprocess_backward");
 }
@@ -991,15 +1036,16 @@ int32_t mg_preprocess_backward_mip(int64_t N, const float *means, const float *q
                                    float blur, float max_radius, const float *cam_center,
                                    int32_t sh_degree, const float *opacities,
                                    const float *filter_3d, int32_t antialias,
+                                   int32_t activations,
                                    const float *d_opacity_eff, float *d_means, float *d_quats,
                                    float *d_scales, float *d_sh, float *d_sh_rest,
                                    float *d_opacities, mg_stream_t stream) {
     return preprocess_bwd(N, means, quats, scales, sh, sh_rest, sh_fused, d_uv, d_conic,
                           d_color, grad_stride, valid, viewmat, fx, fy, cx, cy, W, H,
                           near_plane, far_plane, blur, max_radius, cam_center, sh_degree, true,
-                          opacities, filter_3d,
-                          antialias, d_opacity_eff, d_means, d_quats, d_scales, d_sh, d_sh_rest,
-                          d_opacities, stream, "mg_preprocess_backward_mip");
+                          opacities, filter_3d, antialias, activations, d_opacity_eff,
+                          d_means, d_quats, d_scales, d_sh, d_sh_rest, d_opacities, stream,
+                          "mg_preprocess_backward_mip");
 }
 
 }  // extern "C"

@@ -131,17 +131,32 @@ constexpr int kTW = 32, kTH = 16;                 // output tile
 constexpr int kIW = kTW + 2 * kR, kIH = kTH + 2 * kR;   // 42 x 26 with halo
 constexpr int kSsimThreads = 256;
 
-// block_sums[b] gets the block's SSIM sum; with l1_sums, l1_sums[b] gets its
-// sum of |x - y| over the same pixels and channel.
+// Work items of the fused kernels: (output tile, channel) pairs, item =
+// 3 * tile + channel, tile = ty * tiles_x + tx. The items are dealt to the XCDs
+// in contiguous runs, so the three channels of a tile (which read the same
+// interleaved (H,W,3) lines) and its neighbours (which share the halo) run
+// under one L2 and the lines come from HBM about once.
+struct SsimItem {
+    int tx, ty, c;
+};
+__device__ __forceinline__ SsimItem ssim_item(int tiles_x) {
+    const int item = (int)xcd_contiguous(blockIdx.x, gridDim.x);
+    const int tile = item / 3;
+    return {tile % tiles_x, tile / tiles_x, item - 3 * tile};
+}
+
+// block_sums[b] gets work item b's SSIM sum; with l1_sums, l1_sums[b] gets
+// its sum of |x - y| over the same pixels and channel.
 __global__ __launch_bounds__(kSsimThreads) void ssim_fused_fwd_kernel(
-    const float *x, const float *y, const float *w, int H, int W, float *partials,
+    const float *x, const float *y, const float *w, int H, int W, int tiles_x, float *partials,
     float *block_sums, float *l1_sums) {
     __shared__ float s_x[kIH][kIW], s_y[kIH][kIW];
     __shared__ float s_h[5][kIH][kTW];
     __shared__ float s_w[2 * kR + 1];
     __shared__ float s_red[2][kSsimThreads / 64];
-    const int c = blockIdx.z;
-    const int x0 = blockIdx.x * kTW - kR, y0 = blockIdx.y * kTH - kR;
+    const SsimItem it = ssim_item(tiles_x);
+    const int c = it.c;
+    const int x0 = it.tx * kTW - kR, y0 = it.ty * kTH - kR;
     const int tid = threadIdx.x;
     if (tid < 2 * kR + 1) s_w[tid] = w[tid];
     for (int i = tid; i < kIH * kIW; i += kSsimThreads) {
@@ -183,7 +198,7 @@ __global__ __launch_bounds__(kSsimThreads) void ssim_fused_fwd_kernel(
     float local = 0.f, local_l1 = 0.f;
     for (int i = tid; i < kTH * kTW; i += kSsimThreads) {
         const int ly = i / kTW, lx = i - ly * kTW;
-        const int gx = blockIdx.x * kTW + lx, gy = blockIdx.y * kTH + ly;
+        const int gx = it.tx * kTW + lx, gy = it.ty * kTH + ly;
         if (gx >= W || gy >= H) continue;
         local_l1 += fabsf(s_x[ly + kR][lx + kR] - s_y[ly + kR][lx + kR]);
         float m[5] = {0, 0, 0, 0, 0};
@@ -217,8 +232,7 @@ __global__ __launch_bounds__(kSsimThreads) void ssim_fused_fwd_kernel(
             s += s_red[0][k];
             s1 += s_red[1][k];
         }
-        const int64_t bid =
-            ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        const int bid = 3 * (it.ty * tiles_x + it.tx) + c;
         block_sums[bid] = s;
         if (l1_sums) l1_sums[bid] = s1;
     }
@@ -271,12 +285,13 @@ __global__ __launch_bounds__(256) void photometric_loss_kernel(const float *ssim
 // a_l1 = 1 - lam that of the photometric loss.
 __global__ __launch_bounds__(kSsimThreads) void ssim_fused_bwd_kernel(
     const float *x, const float *y, const float *w, const float *partials, const float *scale_dev,
-    int H, int W, float a_ssim, float a_l1, float *dx) {
+    int H, int W, int tiles_x, float a_ssim, float a_l1, float *dx) {
     __shared__ float s_p[3][kIH][kIW];
     __shared__ float s_h[3][kIH][kTW];
     __shared__ float s_w[2 * kR + 1];
-    const int c = blockIdx.z;
-    const int x0 = blockIdx.x * kTW - kR, y0 = blockIdx.y * kTH - kR;
+    const SsimItem it = ssim_item(tiles_x);
+    const int c = it.c;
+    const int x0 = it.tx * kTW - kR, y0 = it.ty * kTH - kR;
     const int tid = threadIdx.x;
     const int64_t N = (int64_t)W * H;
     if (tid < 2 * kR + 1) s_w[tid] = w[tid];
@@ -313,7 +328,7 @@ __global__ __launch_bounds__(kSsimThreads) void ssim_fused_bwd_kernel(
     const float scale = scale_dev[0] / (float)(3 * N);
     for (int i = tid; i < kTH * kTW; i += kSsimThreads) {
         const int ly = i / kTW, lx = i - ly * kTW;
-        const int gx = blockIdx.x * kTW + lx, gy = blockIdx.y * kTH + ly;
+        const int gx = it.tx * kTW + lx, gy = it.ty * kTH + ly;
         if (gx >= W || gy >= H) continue;
         float b0 = 0, b1 = 0, b2 = 0;
 #pragma unroll
@@ -335,6 +350,7 @@ __global__ __launch_bounds__(kSsimThreads) void ssim_fused_bwd_kernel(
     }
 }
 
+// Work items (workgroups) of the fused kernels: one per (output tile, channel).
 inline int64_t ssim_blocks(int H, int W) {
     return ceil_div(W, kTW) * ceil_div(H, kTH) * 3;
 }
@@ -411,12 +427,14 @@ int32_t mg_ssim_fused_forward(const float *x, const float *y, const float *w, in
                "mg_ssim_fused_forward: workspace %lld bytes, need %lld",
                (long long)workspace_bytes, (long long)mg_ssim_fused_workspace_bytes(H, W));
     hipStream_t s = as_stream(stream);
-    dim3 grid((unsigned)ceil_div(W, kTW), (unsigned)ceil_div(H, kTH), 3);
+    const int tiles_x = (int)ceil_div(W, kTW);
+    const unsigned grid = (unsigned)ssim_blocks(H, W);
     float *sums = static_cast<float *>(workspace);
     TimedScope ts("ssim_fused_forward", s);
-    ssim_fused_fwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, H, W, partials, sums, nullptr);
+    ssim_fused_fwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, H, W, tiles_x, partials, sums,
+                                                        nullptr);
     MG_LAUNCHED("ssim_fused_fwd_kernel");
-    ssim_mean_kernel<<<1, 256, 0, s>>>(sums, ssim_blocks(H, W), 3LL * H * W, mean_out);
+    ssim_mean_kernel<<<1, 256, 0, s>>>(sums, (int64_t)grid, 3LL * H * W, mean_out);
     MG_LAUNCHED("ssim_mean_kernel");
     return MG_OK;
 }
@@ -427,10 +445,11 @@ int32_t mg_ssim_fused_backward(const float *x, const float *y, const float *w,
     MG_REQUIRE(H > 0 && W > 0 && x && y && w && partials && scale_dev && d_x,
                "mg_ssim_fused_backward: bad arguments");
     hipStream_t s = as_stream(stream);
-    dim3 grid((unsigned)ceil_div(W, kTW), (unsigned)ceil_div(H, kTH), 3);
+    const int tiles_x = (int)ceil_div(W, kTW);
+    const unsigned grid = (unsigned)ssim_blocks(H, W);
     TimedScope ts("ssim_fused_backward", s);
-    ssim_fused_bwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, partials, scale_dev, H, W, 1.0f,
-                                                        0.0f, d_x);
+    ssim_fused_bwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, partials, scale_dev, H, W,
+                                                        tiles_x, 1.0f, 0.0f, d_x);
     MG_LAUNCHED("ssim_fused_bwd_kernel");
     return MG_OK;
 }
@@ -447,11 +466,13 @@ int32_t mg_photometric_loss_forward(const float *x, const float *y, const float 
                "mg_photometric_loss_forward: workspace %lld bytes, need %lld",
                (long long)workspace_bytes, (long long)mg_ssim_fused_workspace_bytes(H, W));
     hipStream_t s = as_stream(stream);
-    dim3 grid((unsigned)ceil_div(W, kTW), (unsigned)ceil_div(H, kTH), 3);
+    const int tiles_x = (int)ceil_div(W, kTW);
     const int64_t nb = ssim_blocks(H, W);
+    const unsigned grid = (unsigned)nb;
     float *sums = static_cast<float *>(workspace);
     TimedScope ts("ssim_fused_forward", s);
-    ssim_fused_fwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, H, W, partials, sums, sums + nb);
+    ssim_fused_fwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, H, W, tiles_x, partials, sums,
+                                                        sums + nb);
     MG_LAUNCHED("ssim_fused_fwd_kernel");
     photometric_loss_kernel<<<1, 256, 0, s>>>(sums, sums + nb, nb, 3LL * H * W, ssim_weight, out);
     MG_LAUNCHED("photometric_loss_kernel");
@@ -468,9 +489,10 @@ int32_t mg_photometric_loss_backward(const float *x, const float *y, const float
                "mg_photometric_loss_backward: ssim_weight %g outside [0, 1]",
                (double)ssim_weight);
     hipStream_t s = as_stream(stream);
-    dim3 grid((unsigned)ceil_div(W, kTW), (unsigned)ceil_div(H, kTH), 3);
+    const int tiles_x = (int)ceil_div(W, kTW);
+    const unsigned grid = (unsigned)ssim_blocks(H, W);
     TimedScope ts("ssim_fused_backward", s);
-    ssim_fused_bwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, partials, grad_dev, H, W,
+    ssim_fused_bwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, partials, grad_dev, H, W, tiles_x,
                                                         -ssim_weight, 1.0f - ssim_weight, d_x);
     MG_LAUNCHED("ssim_fused_bwd_kernel");
     return MG_OK;

@@ -81,6 +81,15 @@ def test_bad_arguments_fail_before_any_launch():
     # sort bit range
     assert lib.mg_sort_pairs_u64(1, 1, 1, 1, 10, 0, 65, 1, 1 << 20, None) == 1
     assert "bit range" in lib.mg_last_error().decode()
+    # tile counting sort: tile count and aliasing
+    assert lib.mg_sort_pairs_by_tile(10, 1, 1, 5000, 1, 1, 1, 1 << 20, None) == 1
+    assert "tiles" in lib.mg_last_error().decode()
+    assert lib.mg_sort_pairs_by_tile(10, 1, 2, 16, 2, 1, 1, 1 << 20, None) == 1
+    assert "alias" in lib.mg_last_error().decode()
+    assert lib.mg_sort_pairs_by_tile(10, 1, 2, 16, 3, 1, 1, 1 << 20, None) == 1
+    assert "16-byte aligned" in lib.mg_last_error().decode()
+    assert lib.mg_sort_pairs_by_tile(10, 16, 2, 16, 3, 1, 1, 8, None) == 1
+    assert "workspace" in lib.mg_last_error().decode()
     # SH layout
     vm = (ctypes.c_float * 16)(*([0.0] * 16))
     cc = (ctypes.c_float * 3)(0.0, 0.0, 0.0)
@@ -102,6 +111,10 @@ def test_workspace_size_queries_are_pure():
     assert lib.mg_scan_workspace_bytes(1 << 20) >= 8 * ((1 << 20) // 2048)
     assert lib.mg_sort_workspace_bytes(3_500_000) >= 4 * 256 * (3_500_000 // 2048)
     assert lib.mg_ssim_fused_workspace_bytes(800, 800) == 2 * 4 * 25 * 50 * 3   # SSIM + L1 sums
+    # tile sort: one count per (tile, chunk) plus the tile totals
+    assert lib.mg_sort_pairs_by_tile_workspace_bytes(5_000_000, 2500) >= 4 * 2500 * 407
+    assert lib.mg_bin_lists_finish_workspace_bytes(5_000_000) >= \
+        lib.mg_sort_pairs_by_tile_workspace_bytes(5_000_000, 4096)
 
 
 @pytest.mark.parametrize("missing", [True])

@@ -101,6 +101,22 @@ def test_large_rectangles_bit_exact(dev, tile, ellipse):
     assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
 
 
+@pytest.mark.parametrize("spread", [0.0, 2e-6, 2e-3, 0.5, 3.0])
+def test_depth_windows_of_every_pass_count_bit_exact(dev, spread):
+    """The depth sort takes 12-bit passes over only the bits in which the
+    tiled Gaussians' depth keys differ, and leaves the order in one of two
+    buffers by the parity of those passes: all depths equal (no pass), a few
+    bits (one), about 20 bits (two), and a wide range (three). The lists must
+    equal the oracle's every time."""
+    s = ref_scene(N=4000, seed=21)
+    g = torch.Generator().manual_seed(22)
+    s["means"][:, 2] = 3.0 + spread * torch.randn(4000, generator=g).clamp(-0.9, 0.9)
+    gpu, ref = run_both(s, dev, 16)
+    assert np.array_equal(gpu[3], ref[3]), "sorted keys differ"
+    assert np.array_equal(gpu[0], ref[0]), "gauss_ids differ"
+    assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
+
+
 def test_rect_only_lists_bit_exact_and_longer(dev):
     s = ref_scene(seed=3)
     gpu_r, ref_r = run_both(s, dev, 16, ellipse=False)
@@ -219,6 +235,57 @@ def test_radix_sort_is_stable_and_exact(dev, n, bits):
                                      _lib.stream(kin)))
     assert np.array_equal(vout.cpu().numpy(), want_order.astype(np.int32))
     assert np.array_equal(kout.cpu().numpy(), keys[want_order])
+
+
+@pytest.mark.parametrize("n,n_tiles,kind", [
+    (1, 1, "uniform"), (7, 3, "uniform"), (2049, 300, "uniform"), (300_001, 2500, "uniform"),
+    (300_001, 4096, "descending"), (1_000_003, 1, "uniform"), (2_000_000, 2500, "one_hot"),
+    (5_000_011, 2500, "uniform"), (7_000_001, 4096, "uniform"), (100_000, 2500, "dropped")])
+def test_sort_pairs_by_tile_is_stable_and_exact(dev, n, n_tiles, kind):
+    """The one-pass counting sort behind mg_bin_lists_finish against numpy's
+    stable argsort: chunk plans from 8 to 64 pairs per lane (n up to 7M),
+    one tile, every pair in one tile, reversed input, and tiles past n_tiles
+    (dropped; the last offset counts the rest)."""
+    from metal_gauss_amd import _lib
+
+    lib = _lib.load()
+    g = np.random.default_rng(n + 7 * n_tiles)
+    tiles = g.integers(0, n_tiles, size=n, dtype=np.int64)
+    if kind == "descending":
+        tiles = np.sort(tiles)[::-1].copy()
+    elif kind == "one_hot":
+        tiles[:] = n_tiles // 3
+        tiles[g.random(n) < 0.01] = 0
+    elif kind == "dropped":
+        tiles[g.random(n) < 0.1] = n_tiles + 5
+    ids = g.integers(0, 2 ** 31 - 1, size=n, dtype=np.int64).astype(np.int32)
+    keep = tiles < n_tiles
+    order = np.argsort(np.where(keep, tiles, n_tiles), kind="stable")[:int(keep.sum())]
+    want_offs = np.searchsorted(tiles[order], np.arange(n_tiles + 1))
+    t_dev = torch.from_numpy(tiles.astype(np.uint32).view(np.int32)).to(dev)
+    i_dev = torch.from_numpy(ids).to(dev)
+    out = torch.full((n,), -1, dtype=torch.int32, device=dev)
+    offs = torch.full((n_tiles + 1,), -1, dtype=torch.int32, device=dev)
+    ws = torch.empty(lib.mg_sort_pairs_by_tile_workspace_bytes(n, n_tiles), dtype=torch.uint8,
+                     device=dev)
+    _lib.check(lib.mg_sort_pairs_by_tile(n, t_dev.data_ptr(), i_dev.data_ptr(), n_tiles,
+                                         out.data_ptr(), offs.data_ptr(), ws.data_ptr(),
+                                         ws.numel(), _lib.stream(t_dev)))
+    got = out.cpu().numpy()
+    assert np.array_equal(offs.cpu().numpy(), want_offs)
+    assert np.array_equal(got[:order.size], ids[order])
+    assert (got[order.size:] == -1).all(), "wrote past the kept pairs"
+
+
+def test_more_tiles_than_the_counting_sort_takes_bit_exact(dev):
+    """640 x 480 at 8-pixel tiles is 4800 tiles: the lists come from the radix
+    passes instead of the counting sort, and must equal the oracle's."""
+    s = ref_scene(N=20000, W=640, H=480, seed=5)
+    gpu, ref = run_both(s, dev, 8)
+    assert (640 // 8) * (480 // 8) > 4096
+    assert np.array_equal(gpu[3], ref[3]), "sorted keys differ"
+    assert np.array_equal(gpu[0], ref[0]), "gauss_ids differ"
+    assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
 
 
 @pytest.mark.parametrize("n", [1, 2048, 2049, 1_000_003])

@@ -301,3 +301,48 @@ def test_preview_renders_exactly_what_training_renders(dev, use_sh):
                                    colors=None if use_sh else leaves["colors"].detach(), **kw)
     assert torch.equal(trained.detach(), previewed)
     assert torch.equal(a_t.detach(), a_p)
+
+
+@pytest.mark.parametrize("antialias,filt,split", [(False, False, False), (False, False, True),
+                                                  (True, False, False), (True, True, True)])
+def test_activations_in_the_kernel_match_torch_activations(dev, antialias, filt, split):
+    """render(activations=True) on log scales and logits against render on
+    torch.exp / torch.sigmoid of them (the trainer's train.py:221-222), with
+    and without Mip's filters: the same lists and image, and through torch's
+    exp and sigmoid backward the same gradients on every leaf."""
+    from metal_gauss_amd import render
+
+    W, H = 96, 80
+    s = scene(n=500, seed=7)
+    K, vm = intrinsics(W, H), torch.eye(4)
+    g = torch.Generator().manual_seed(8)
+    f3 = (torch.rand(500, generator=g) * 0.02 + 0.005).to(dev) if filt else None
+    base = dict(means=s["means"], quats=s["quats"], log_scales=s["scales"].log(),
+                logits=torch.logit(s["opacities"]), sh=s["sh"])
+    outs = []
+    for fused in (False, True):
+        p = {k: t.clone().to(dev).requires_grad_(True) for k, t in base.items()}
+        if fused:
+            sc, op = p["log_scales"], p["logits"]
+        else:
+            sc, op = torch.exp(p["log_scales"]), torch.sigmoid(p["logits"])
+        if split:
+            dc = p["sh"][:, :1]
+            kw = dict(sh_rest=p["sh"][:, 1:])
+        else:
+            dc, kw = p["sh"], {}
+        rgb, alpha, info = render(p["means"], p["quats"], sc, op, dc, K, vm, W, H, sh_degree=3,
+                                  min_transmittance=0.0, antialias=antialias, filter_3d=f3,
+                                  activations=fused, **kw)
+        (rgb.square().mean() + 0.1 * alpha.square().mean()).backward()
+        outs.append((rgb.detach(), alpha.detach(), {k: v.grad for k, v in p.items()}, info))
+    (r0, a0, g0, i0), (r1, a1, g1, i1) = outs
+    assert i0["isect_total"] == i1["isect_total"] > 0
+    assert torch.equal(i0["valid_mask"], i1["valid_mask"])
+    assert (r0 - r1).abs().max() < 1e-6 and (a0 - a1).abs().max() < 1e-6
+    for k in base:
+        assert g1[k] is not None and rel_l2(g1[k].cpu(), g0[k].cpu()) < 1e-5, k
+    # The logit gradient is the opacity gradient through sigmoid: nonzero
+    # where a Gaussian is drawn, exactly zero where it is not.
+    assert (g1["logits"][~i1["valid_mask"]] == 0).all()
+    assert g1["logits"].abs().sum() > 0
