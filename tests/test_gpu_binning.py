@@ -117,6 +117,30 @@ def test_depth_windows_of_every_pass_count_bit_exact(dev, spread):
     assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
 
 
+@pytest.mark.parametrize("crowd", [False, True])
+def test_depth_ties_and_long_tile_lists_bit_exact(dev, crowd):
+    """Exact depth ties (Gaussians copied onto others, as MCMC's relocation
+    does) must come out in id order inside every tile, and lists longer than
+    one workgroup's 4096 entries (a crowd of splats over a few tiles) take the
+    chunked path; both must equal the oracle's lists."""
+    s = ref_scene(N=14000 if crowd else 6000, seed=31)
+    g = torch.Generator().manual_seed(32)
+    N = s["means"].shape[0]
+    if crowd:
+        s["means"][:, :2] = (torch.rand(N, 2, generator=g) - 0.5) * 0.06
+        s["scales"] = torch.rand(N, 3, generator=g) * 0.01 + 0.004
+    src = torch.randint(0, N, (N // 5,), generator=g)
+    dst = torch.randperm(N, generator=g)[:N // 5]
+    for k in ("means", "quats", "scales", "op"):
+        s[k][dst] = s[k][src]
+    gpu, ref = run_both(s, dev, 16)
+    if crowd:
+        assert int(np.diff(gpu[1]).max()) > 4096, int(np.diff(gpu[1]).max())
+    assert np.array_equal(gpu[3], ref[3]), "sorted keys differ"
+    assert np.array_equal(gpu[0], ref[0]), "gauss_ids differ"
+    assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
+
+
 def test_rect_only_lists_bit_exact_and_longer(dev):
     s = ref_scene(seed=3)
     gpu_r, ref_r = run_both(s, dev, 16, ellipse=False)
