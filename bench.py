@@ -37,16 +37,17 @@ METRIC = "train steps/sec & fwd+bwd ms at 1M Gaussians 800×800 SH3; % HBM roofl
 HBM_PEAK_GBS = 8000.0
 
 # Kernels timed by the library (names used in mg_timing_query).
-KERNELS = ["preprocess_forward", "bin_count", "depth_sort", "exclusive_scan", "bin_write",
-           "tile_sort", "tile_ranges", "rasterize_forward", "rasterize_backward",
+KERNELS = ["preprocess_forward", "bin_count", "exclusive_scan", "bin_write", "tile_sort",
+           "depth_sort", "rasterize_forward", "rasterize_backward",
            "preprocess_backward", "ssim_fused_forward", "ssim_fused_backward", "adam_step"]
 
-# Library timing label -> the kernel name rocprofv3 reports for it (the sorts
-# run three kernels per pass and are left out of the counter summary).
+# Library timing label -> the kernel name rocprofv3 reports for it (for the
+# tile sort, its scatter kernel; the scan runs three kernels and is left out).
 PROF_NAMES = {
     "preprocess_forward": "preprocess_fwd_kernel", "preprocess_backward": "preprocess_bwd_kernel",
     "bin_count": "bin_count_rec_kernel", "bin_write": "bin_write_rec_kernel",
-    "tile_ranges": "tile_ranges_u32_kernel", "rasterize_forward": "raster_fwd_kernel",
+    "tile_sort": "count_scatter_kernel", "depth_sort": "tile_depth_sort_kernel",
+    "rasterize_forward": "raster_fwd_kernel",
     "rasterize_backward": "raster_bwd_kernel", "ssim_fused_forward": "ssim_fused_fwd_kernel",
     "ssim_fused_backward": "ssim_fused_bwd_kernel", "adam_step": "adam_multi_kernel",
 }
@@ -205,8 +206,8 @@ def algorithmic_bytes(kernel, N, I, P, T, f_valid, n_floats):
         "preprocess_backward": (320 + 192 * f_valid) * N,
         "bin_count": 76 * N,                      # 40 B read; count, 32 B record
         "exclusive_scan": 8 * N,                  # counts read, offsets written
-        "bin_write": 36 * N + 8 * I,              # offset, record; key + id per pair
-        "tile_sort": 16 * I,                      # one counting pass: tiles read twice, ids once, ids written
+        "bin_write": 36 * N + 12 * I,             # offset, record; tile key + {id, depth} per pair
+        "tile_sort": 24 * I,                      # tiles read twice, 8-byte values read and written
         "depth_sort": 12 * I,                     # per tile list: ids read, depths gathered, ids written
         "tile_ranges": 4 * I + 4 * (T + 1),
         "rasterize_forward": 40 * I + 24 * P + 8 * T,
@@ -566,8 +567,9 @@ def adam_config(reps):
             "n_floats": n_floats}
 
 
-PMC_REGEX = ("raster_bwd|raster_fwd|adam_multi|preprocess_fwd|preprocess_bwd|radix_|scan_|"
-             "bin_write|bin_count|tile_hist|tile_scatter|ssim_fused|copyBuffer")
+PMC_REGEX = ("raster_bwd|raster_fwd|adam_multi|preprocess_fwd|preprocess_bwd|scan_|bin_write|"
+             "bin_count|count_hist|count_colscan|count_scatter|tile_depth_sort|ssim_fused|"
+             "copyBuffer")
 
 
 def _counter_rows(d):
