@@ -23,7 +23,10 @@ def make(n, seed, W, H, off_frac=0.0):
     return s
 
 
-def gpu_pre(s, W, H, dev, deg=3, split=False, grad=False):
+def gpu_pre(s, W, H, dev, deg=3, split=False, grad=False, unaligned=False):
+    """unaligned: the split rest rows handed over as a view one float into
+    its storage (not 16-byte aligned), which the kernels must read as they
+    are."""
     from metal_gauss_amd.backend import _PreprocessMetal, _camera
 
     K = intrinsics(W, H)
@@ -34,10 +37,16 @@ def gpu_pre(s, W, H, dev, deg=3, split=False, grad=False):
         dc = sh[:, :1].contiguous().requires_grad_(grad)
         rest = sh[:, 1:].contiguous().requires_grad_(grad)
         shl = [dc, rest]
+        rest_in = rest
+        if unaligned:
+            pad = torch.zeros(1, device=dev)
+            rest_in = torch.cat([pad, rest.flatten()])[1:].view(rest.shape)
+            assert rest_in.data_ptr() % 16 != 0
     else:
         shl = [sh.requires_grad_(grad), None]
-    out = _PreprocessMetal.apply(*leaves, shl[0], shl[1], s["opacities"].to(dev), vm_h, fx, fy,
-                                 cx, cy, W, H, 0.01, 100.0, 0.3, float(max(W, H)), cc, deg)
+        rest_in = None
+    out = _PreprocessMetal.apply(*leaves, shl[0], rest_in, s["opacities"].to(dev), vm_h, fx,
+                                 fy, cx, cy, W, H, 0.01, 100.0, 0.3, float(max(W, H)), cc, deg)
     return out, leaves, shl
 
 
@@ -78,12 +87,18 @@ def test_forward_matches_contract(dev, deg):
     assert float(color[inval].abs().max()) == 0.0 if inval.any() else True
 
 
-@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("split,n,unaligned", [(False, 2000, False), (True, 2000, False),
+                                               (False, 2003, False), (True, 2011, False),
+                                               (True, 2000, True)])
 @pytest.mark.parametrize("deg", [0, 1, 3])
-def test_backward_matches_autograd(dev, deg, split):
+def test_backward_matches_autograd(dev, deg, split, n, unaligned):
+    """Also: counts that end inside a 16-Gaussian round of the SH phase, and
+    split rest rows that are not 16-byte aligned (the rows are then read and
+    written without staging)."""
     W, H = 160, 120
-    s = make(2000, 10 + deg, W, H, off_frac=0.1)
-    (uv, conic, depth, rxy, valid, color), leaves, shl = gpu_pre(s, W, H, dev, deg, split, True)
+    s = make(n, 10 + deg, W, H, off_frac=0.1)
+    (uv, conic, depth, rxy, valid, color), leaves, shl = gpu_pre(s, W, H, dev, deg, split, True,
+                                                                 unaligned)
     (ruv, rconic, _, _, rvalid, rcolor), rleaves = ref_pre(s, W, H, deg)
     g = torch.Generator().manual_seed(deg)
     n = s["means"].shape[0]
