@@ -205,7 +205,7 @@ def algorithmic_bytes(kernel, N, I, P, T, f_valid, n_floats):
         "preprocess_forward": (96 + 192 * f_valid) * N,
         "preprocess_backward": (320 + 192 * f_valid) * N,
         "bin_count": 76 * N,                      # 40 B read; count, 32 B record
-        "exclusive_scan": 8 * N,                  # counts read, offsets written
+        "exclusive_scan": 16 * N // 256,          # per-workgroup totals read, block offsets written
         "bin_write": 36 * N + 12 * I,             # offset, record; tile key + {id, depth} per pair
         "tile_sort": 24 * I,                      # tiles read twice, 8-byte values read and written
         "depth_sort": 12 * I,                     # per tile list: ids read, depths gathered, ids written

@@ -372,7 +372,12 @@ int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy,
  * pixel's state at every unit's end, so mg_rasterize_backward can run the
  * units in parallel instead of one long chain per tile. Size it with
  * mg_rasterize_chunk_workspace_bytes(n_isect, tiles, tile), where n_isect
- * is the length of gauss_ids, and pass it unchanged to the backward. */
+ * is the length of gauss_ids, and pass it unchanged to the backward.
+ *
+ * zero_grads (device, 16-byte aligned, or NULL): the (N,10) gradient record
+ * buffer a later mg_rasterize_backward will fill, cleared by this launch's
+ * workgroups on the way (then pass grads_zeroed = 1 to the backward, which
+ * skips its own fill). */
 int64_t mg_rasterize_chunk_workspace_bytes(int64_t n_isect, int32_t n_tiles,
                                            int32_t tile);
 int32_t mg_rasterize_forward(
@@ -381,7 +386,7 @@ int32_t mg_rasterize_forward(
     int32_t W, int32_t H, int32_t tile, int32_t tiles_x, float t_min,
     const float *background, int64_t n_isect, void *chunk_ws,
     int64_t chunk_ws_bytes, float *out_rgb, float *out_alpha, float *out_T,
-    int32_t *out_stop, mg_stream_t stream);
+    int32_t *out_stop, float *zero_grads, mg_stream_t stream);
 
 /* Back-to-front replay of mg_rasterize_forward. Replaces rasterize_backward
  * (metal_gauss/csrc/rasterize.mm:147-194; kernel rasterize.metal:173-340),
@@ -396,7 +401,9 @@ int32_t mg_rasterize_forward(
  * background (host, or NULL), grad_rgb is the gradient of the blended colour
  * and alpha (the forward's out_alpha, device) adds the blend's share to
  * grad_alpha. n_isect / chunk_ws / chunk_ws_bytes are the forward's (chunk_ws
- * NULL: one workgroup per tile). */
+ * NULL: one workgroup per tile). grads_zeroed != 0: d_grads was cleared by the
+ * forward (its zero_grads), so the backward does not fill it first; 0: the
+ * backward zero-fills d_grads itself. */
 int32_t mg_rasterize_backward(
     int64_t N, const float *uv, const float *conic, const float *opacity,
     const float *color, const int32_t *gauss_ids, const int32_t *tile_offsets,
@@ -404,7 +411,7 @@ int32_t mg_rasterize_backward(
     const float *grad_alpha, const float *alpha, const float *background,
     int64_t n_isect, const void *chunk_ws, int64_t chunk_ws_bytes, int32_t W,
     int32_t H, int32_t tile, int32_t tiles_x, float *d_grads, int32_t absgrad,
-    mg_stream_t stream);
+    int32_t grads_zeroed, mg_stream_t stream);
 
 /* ------------------------------------------------------------------- Adam */
 

@@ -407,6 +407,11 @@ class _RasterizeMetal(torch.autograd.Function):
         chunk_ws = torch.empty(
             lib.mg_rasterize_chunk_workspace_bytes(n_isect, tile_offsets.numel() - 1, tile)
             if chunked else 0, dtype=torch.uint8, device=dev)
+        # The backward's gradient records, cleared by the forward kernel on
+        # the way (the backward then skips its own fill), when a backward can
+        # follow.
+        rec = (torch.empty(N, _REC, device=dev) if N and any(ctx.needs_input_grad[:4])
+               else None)
         _lib.check(lib.mg_rasterize_forward(
             N, _lib.dev_tensor(uv, "uv"), _lib.dev_tensor(conic, "conic"),
             _lib.dev_tensor(opacity, "opacity"), _lib.dev_tensor(color, "color"),
@@ -414,10 +419,11 @@ class _RasterizeMetal(torch.autograd.Function):
             _lib.dev_tensor(tile_offsets, "tile_offsets", torch.int32), W, H, tile, tiles_x,
             float(t_min), None if background is None else _lib.f32_array(background),
             n_isect, chunk_ws.data_ptr() if chunked else None, chunk_ws.numel(), rgb.data_ptr(),
-            alpha.data_ptr(),
-            T.data_ptr(), stop.data_ptr(), _lib.stream(uv)))
+            alpha.data_ptr(), T.data_ptr(), stop.data_ptr(),
+            None if rec is None else rec.data_ptr(), _lib.stream(uv)))
         ctx.save_for_backward(uv, conic, opacity, color, gauss_ids, tile_offsets, T, stop,
                               alpha if background is not None else None, chunk_ws)
+        ctx.rec = rec
         ctx.dims = (W, H, tile, tiles_x)
         ctx.background = background
         # An output nobody differentiates (alpha, most often) gets no
@@ -438,7 +444,10 @@ class _RasterizeMetal(torch.autograd.Function):
         N = uv.shape[0]
         dev = uv.device
         # One gradient record per Gaussian; autograd gets row views of it.
-        rec = torch.empty(N, _REC, device=dev)
+        rec, zeroed = ctx.rec, ctx.rec is not None
+        ctx.rec = None
+        if rec is None:
+            rec = torch.empty(N, _REC, device=dev)
         if grad_rgb is None and grad_alpha is None:
             return (None,) * 14
         grad_rgb = torch.zeros(H, W, 3, device=dev) if grad_rgb is None else grad_rgb.contiguous()
@@ -451,7 +460,7 @@ class _RasterizeMetal(torch.autograd.Function):
             None if bg is None else alpha.data_ptr(), None if bg is None else _lib.f32_array(bg),
             gauss_ids.numel(), chunk_ws.data_ptr() if chunk_ws.numel() else None,
             chunk_ws.numel(), W, H, tile, tiles_x, rec.data_ptr(),
-            int(ctx.absgrad_out is not None), _lib.stream(uv)))
+            int(ctx.absgrad_out is not None), int(zeroed), _lib.stream(uv)))
         if ctx.absgrad_out is not None:
             ctx.absgrad_out[:N] += rec[:, 9]
         return (rec[:, 0:2], rec[:, 2:5], rec[:, 5], rec[:, 6:9]) + (None,) * 10

@@ -442,10 +442,10 @@ int32_t exclusive_scan(const int32_t *in, const int32_t *idx, int64_t n, int32_t
 
 struct BinStats {
     unsigned long long total;       // intersections
-    unsigned long long scan_total;  // the scan's own total (same value)
+    unsigned long long scan_total;  // unused (kept zero)
 };
 
-// One per count workgroup, reduced by bin_stats_kernel. (Same-address
+// One per count workgroup, scanned by bin_offsets_kernel. (Same-address
 // atomics from every wave would serialise at the memory side: the eight
 // XCDs' L2s are not coherent with each other, so device-scope atomics are
 // performed there.)
@@ -525,18 +525,37 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
     }
 }
 
-// One workgroup folds the count pass's per-workgroup partials into *st.
-// One workgroup folds the count pass's per-workgroup partials into *st.
-__global__ __launch_bounds__(256) void bin_stats_kernel(const BinPart *parts, int64_t nparts,
-                                                        BinStats *st) {
-    __shared__ unsigned long long s_p[4];
-    unsigned long long tot = 0;
-    for (int64_t i = threadIdx.x; i < nparts; i += 256) tot += parts[i].total;
-    for (int o = 32; o >= 1; o >>= 1) tot += __shfl_xor(tot, o, 64);
-    if ((threadIdx.x & 63) == 0) s_p[threadIdx.x >> 6] = tot;
-    __syncthreads();
+// One workgroup scans the count pass's per-workgroup totals: part_off[i] is
+// the first pair of count workgroup i's Gaussians, st->total the intersection
+// total.
+__global__ __launch_bounds__(kScanThreads) void bin_offsets_kernel(const BinPart *parts,
+                                                                   int64_t nparts,
+                                                                   int64_t *part_off,
+                                                                   BinStats *st) {
+    // Blocked: thread t owns 16 consecutive totals of each 4096-entry step,
+    // all requested at once; one block scan per step.
+    constexpr int kPer = 16;
+    __shared__ int64_t s_wave[kScanThreads / 64];
+    int64_t carry = 0;
+    for (int64_t c0 = 0; c0 < nparts; c0 += kScanThreads * kPer) {
+        const int64_t i0 = c0 + (int64_t)threadIdx.x * kPer;
+        int64_t v[kPer], sum = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            v[j] = i0 + j < nparts ? (int64_t)parts[i0 + j].total : 0;
+            sum += v[j];
+        }
+        int64_t tot;
+        int64_t run = carry + block_excl_scan(sum, s_wave, &tot);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            if (i0 + j < nparts) part_off[i0 + j] = run;
+            run += v[j];
+        }
+        carry += tot;
+    }
     if (threadIdx.x == 0) {
-        st->total = s_p[0] + s_p[1] + s_p[2] + s_p[3];
+        st->total = (unsigned long long)carry;
         st->scan_total = 0;
     }
 }
@@ -559,33 +578,38 @@ constexpr int kBinStage = 2048;
 //     addresses.
 // With pairs (and depth) the value of a pair is {Gaussian id, its depth's
 // float bits} in one 8-byte store instead of the id alone in ids.
+// The workgroup's output range starts at part_off[blockIdx.x] (the count
+// workgroup of the same 256 Gaussians, scanned); each Gaussian's offset in it
+// is an exclusive scan of the counts, formed here.
 __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
-    const BinRec *recs, const int32_t *offsets, int64_t N, int64_t total, int tile, int W, int H,
-    int tiles_x, int test, uint32_t *tkeys, int32_t *ids, const float *depth, uint2 *pairs) {
+    const BinRec *recs, const int32_t *counts, const int64_t *part_off, int64_t N, int tile,
+    int W, int H, int tiles_x, int test, uint32_t *tkeys, int32_t *ids, const float *depth,
+    uint2 *pairs) {
     __shared__ uint32_t s_k[kBinStage];
     __shared__ int32_t s_i[kBinStage];
     __shared__ int32_t s_off[kBinStage];
     __shared__ BinRec s_rec[kBinThreads];
     __shared__ int32_t s_big[kBinThreads], s_g[kBinThreads];
-    __shared__ int32_t s_nbig, s_wsum[kBinThreads / 64];
+    __shared__ int32_t s_nbig, s_wsum[kBinThreads / 64], s_csum[kBinThreads / 64];
+    // Each Gaussian's offset in the range and count, for the wave walks of the
+    // large rectangles; they share s_off's storage, which the staging windows
+    // only use afterwards.
+    int32_t *s_at = s_off, *s_cap = s_off + kBinThreads;
     __shared__ float s_edge[kBinThreads / 64][kEdgeSlots];
     __shared__ uint32_t s_dk[kBinThreads];   // depth bits of the workgroup's Gaussians
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t k0 = (int64_t)blockIdx.x * kBinThreads;
     const int64_t k = k0 + tid;
-    const int64_t base = offsets[k0];
+    const int64_t base = part_off[blockIdx.x];
     if (pairs) s_dk[tid] = k < N ? __float_as_uint(depth[k]) : 0u;
     if (tid == 0) s_nbig = 0;
     __syncthreads();
     bool big = false;
     int small_cap = 0;        // pairs this thread stages (0 unless a small rectangle)
-    int64_t at = 0;
     int32_t g = 0;
     BinRec r{};
-    if (k < N) {
-        at = offsets[k];
-        const int64_t nxt = k + 1 < N ? (int64_t)offsets[k + 1] : total;
-        const int cap = (int)(nxt - at);
+    const int cap = k < N ? counts[k] : 0;
+    {
         if (cap > 0) {
             g = (int32_t)k;
             r = recs[g];
@@ -604,27 +628,37 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
     if (lane == 0 && m) slot = atomicAdd(&s_nbig, __popcll(m));
     slot = __shfl(slot, 0, 64);
     if (big) s_big[slot + rank_in(m)] = tid;
-    int incl = small_cap;
+    int incl = small_cap, cincl = cap;
     for (int o = 1; o < 64; o <<= 1) {
-        const int t = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += t;
+        const int t = __shfl_up(incl, o, 64), u = __shfl_up(cincl, o, 64);
+        if (lane >= o) {
+            incl += t;
+            cincl += u;
+        }
     }
-    if (lane == 63) s_wsum[wave] = incl;
+    if (lane == 63) {
+        s_wsum[wave] = incl;
+        s_csum[wave] = cincl;
+    }
     __syncthreads();
-    int first = incl - small_cap, n_small = 0;
+    int first = incl - small_cap, n_small = 0, off0 = cincl - cap;
     for (int w = 0; w < kBinThreads / 64; ++w) {
-        if (w < wave) first += s_wsum[w];
+        if (w < wave) {
+            first += s_wsum[w];
+            off0 += s_csum[w];
+        }
         n_small += s_wsum[w];
     }
+    s_at[tid] = off0;
+    s_cap[tid] = cap;
+    __syncthreads();
     // Large rectangles: direct stores.
     for (int e = wave; e < s_nbig; e += kBinThreads / 64) {
         const int j = s_big[e];
         const BinRec rb = s_rec[j];
         const int32_t gb = s_g[j];
-        const int64_t kj = k0 + j;
-        const int64_t atb = offsets[kj];
-        const int64_t nxt = kj + 1 < N ? (int64_t)offsets[kj + 1] : total;
-        const int cap = (int)(nxt - atb);
+        const int64_t atb = base + s_at[j];
+        const int capb = s_cap[j];
         const WaveWalk wk = wave_walk_setup(rb, test != 0, tile, W, H, s_edge[wave], lane);
         const int area = wk.w * wk.h;
         int row = lane / wk.w, col = lane % wk.w;
@@ -638,7 +672,7 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
             if (col >= wk.w) { col -= wk.w; ++row; }
             const uint64_t cm = ballot(claim);
             const int pos = emitted + rank_in(cm);
-            if (claim && pos < cap) {
+            if (claim && pos < capb) {
                 tkeys[atb + pos] = (uint32_t)(ty * tiles_x + tx);
                 if (pairs)
                     pairs[atb + pos] = make_uint2((uint32_t)gb, s_dk[j]);
@@ -649,8 +683,8 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
         }
         __builtin_amdgcn_wave_barrier();
     }
+    __syncthreads();   // s_at / s_cap read; s_off becomes the staging window
     // Small rectangles: LDS windows over the numbered runs.
-    const int off0 = (int)(at - base);
     for (int w0 = 0; w0 < n_small; w0 += kBinStage) {
         const int w1 = min(w0 + kBinStage, n_small);
         if (small_cap > 0 && first < w1 && first + small_cap > w0) {
@@ -1266,26 +1300,25 @@ __global__ __launch_bounds__(256) void gather_depth_pairs_kernel(const int32_t *
 }
 
 // Carves the begin/finish workspace identically on both calls. After begin,
-// counts and offsets hold each Gaussian's tile count and its exclusive scan,
-// recs the walk records.
+// counts holds each Gaussian's tile count, part_off the first pair of each
+// 256-Gaussian workgroup, recs the walk records.
 struct BeginWs {
-    int32_t *counts, *offsets;
+    int32_t *counts;
     BinRec *recs;
     BinPart *parts;
+    int64_t *part_off;
     BinStats *stats;
-    void *scan_ws;
-    int64_t scan_bytes, bytes;
+    int64_t bytes;
     BeginWs(void *base, int64_t N) {
         char *p = static_cast<char *>(base);
         int64_t off = 0;
         auto take = [&](int64_t b) { char *q = p ? p + off : nullptr; off += align256(b); return q; };
+        const int64_t nparts = ceil_div(N, kBinThreads);
         counts = (int32_t *)take(4 * N);
-        offsets = (int32_t *)take(4 * N);
         recs = (BinRec *)take((int64_t)sizeof(BinRec) * N);
-        parts = (BinPart *)take((int64_t)sizeof(BinPart) * ceil_div(N, kBinThreads));
+        parts = (BinPart *)take((int64_t)sizeof(BinPart) * nparts);
+        part_off = (int64_t *)take(8 * nparts);
         stats = (BinStats *)take(sizeof(BinStats));
-        scan_bytes = scan_ws_bytes(N);
-        scan_ws = take(scan_bytes);
         bytes = off;
     }
 };
@@ -1436,20 +1469,17 @@ int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy, const f
                                                                        ws.parts);
         MG_LAUNCHED("bin_count_rec_kernel");
     }
-    bin_stats_kernel<<<1, 256, 0, s>>>(ws.parts, nparts, ws.stats);
-    MG_LAUNCHED("bin_stats_kernel");
+    {
+        TimedScope ts("exclusive_scan", s);
+        bin_offsets_kernel<<<1, kScanThreads, 0, s>>>(ws.parts, nparts, ws.part_off, ws.stats);
+        MG_LAUNCHED("bin_offsets_kernel");
+    }
     // The one host read: the total sizes the caller's id buffer. It is copied
-    // into a pinned word behind an event, and the scan is queued before the
-    // host waits, so the GPU keeps working meanwhile.
+    // into a pinned word behind an event.
     HostReadback rb;
     if (!rb.ok()) return MG_ERR_RUNTIME;
     MG_HIP(hipMemcpyAsync(rb.slot, &ws.stats->total, sizeof(int64_t), hipMemcpyDeviceToHost, s));
     MG_HIP(hipEventRecord(rb.ev, s));
-    if (N > 0) {
-        rc = exclusive_scan(ws.counts, nullptr, N, ws.offsets, (int64_t *)&ws.stats->scan_total,
-                            ws.scan_ws, ws.scan_bytes, s, nullptr);
-        if (rc != MG_OK) return rc;
-    }
     MG_HIP(hipEventSynchronize(rb.ev));
     const int64_t total = *rb.slot;
     MG_REQUIRE(total >= 0 && total < (1LL << 31),
@@ -1512,7 +1542,7 @@ int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy, const 
         {
             TimedScope ts("bin_write", s);
             bin_write_rec_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(
-                ws.recs, ws.offsets, N, total, tile, W, H, tiles_x, conic != nullptr ? 1 : 0,
+                ws.recs, ws.counts, ws.part_off, N, tile, W, H, tiles_x, conic != nullptr ? 1 : 0,
                 tk_a, counting ? nullptr : ids_a, depth, counting ? pairs_a : nullptr);
             MG_LAUNCHED("bin_write_rec_kernel");
         }

@@ -54,6 +54,10 @@ struct RasterArgs {
     // Optional background: rgb += max(1 - alpha, 0) * bg (has_bg != 0).
     int32_t has_bg;
     float bg[3];
+    // Forward only, optional: zero_n floats (16-byte aligned) cleared on the
+    // way, a later backward's gradient records; each workgroup clears a slice.
+    float *zero;
+    int64_t zero_n;
 };
 
 __device__ __forceinline__ void tile_pixel(int tid, int tile, int &lx, int &ly, bool &inblk) {
@@ -357,6 +361,17 @@ __global__ __launch_bounds__(MAXW * 64) void raster_fwd_kernel(const RasterArgs 
                                                                int32_t *out_stop,
                                                                const ChunkPlan P) {
     __shared__ Stage<MAXW> S;
+    if (A.zero) {
+        // Slices of a multiple of 4 floats: float4 stores, a scalar tail.
+        const int64_t per = (((A.zero_n + gridDim.x - 1) / gridDim.x) + 3) & ~(int64_t)3;
+        const int64_t b = (int64_t)blockIdx.x * per, e = min(A.zero_n, b + per);
+        for (int64_t i = b + 4 * (int64_t)threadIdx.x; i < e; i += 4 * (int64_t)blockDim.x) {
+            if (i + 4 <= e)
+                *reinterpret_cast<float4 *>(A.zero + i) = make_float4(0.f, 0.f, 0.f, 0.f);
+            else
+                for (int64_t j = i; j < e; ++j) A.zero[j] = 0.f;
+        }
+    }
     const int tile_id = tile_of_block(blockIdx.x, A.tiles_x, A.n_tiles / A.tiles_x);
     if (tile_id < 0) return;   // whole workgroup
     const int tx = tile_id % A.tiles_x, ty = tile_id / A.tiles_x;
@@ -736,16 +751,20 @@ int32_t mg_rasterize_forward(int64_t N, const float *uv, const float *conic, con
                              int32_t tiles_x, float t_min, const float *background,
                              int64_t n_isect, void *chunk_ws, int64_t chunk_ws_size,
                              float *out_rgb, float *out_alpha, float *out_T, int32_t *out_stop,
-                             mg_stream_t stream) {
+                             float *zero_grads, mg_stream_t stream) {
     int32_t rc = check_raster("rasterize_forward", N, uv, conic, opacity, color, gauss_ids,
                               tile_offsets, W, H, tile, tiles_x);
     if (rc != MG_OK) return rc;
     MG_REQUIRE(out_rgb && out_alpha && out_T && out_stop, "rasterize_forward: null output");
+    MG_REQUIRE(zero_grads == nullptr || ((uintptr_t)zero_grads & 15) == 0,
+               "rasterize_forward: zero_grads not 16-byte aligned");
     const int tiles_y = (H + tile - 1) / tile;
     RasterArgs A{uv, conic, opacity, color, gauss_ids, tile_offsets, W, H, tile, tiles_x,
                  tiles_x * tiles_y, t_min, background != nullptr,
                  {background ? background[0] : 0.f, background ? background[1] : 0.f,
                   background ? background[2] : 0.f}};
+    A.zero = N > 0 ? zero_grads : nullptr;
+    A.zero_n = (int64_t)kRecFloats * N;
     hipStream_t s = as_stream(stream);
     ChunkPlan P{nullptr, nullptr, nullptr, 0};
     if (chunk_ws) {
@@ -777,7 +796,7 @@ int32_t mg_rasterize_backward(int64_t N, const float *uv, const float *conic,
                               const float *background, int64_t n_isect, const void *chunk_ws,
                               int64_t chunk_ws_size, int32_t W, int32_t H, int32_t tile,
                               int32_t tiles_x, float *d_grads, int32_t absgrad,
-                              mg_stream_t stream) {
+                              int32_t grads_zeroed, mg_stream_t stream) {
     int32_t rc = check_raster("rasterize_backward", N, uv, conic, opacity, color, gauss_ids,
                               tile_offsets, W, H, tile, tiles_x);
     if (rc != MG_OK) return rc;
@@ -785,7 +804,7 @@ int32_t mg_rasterize_backward(int64_t N, const float *uv, const float *conic,
     MG_REQUIRE(!background || alpha, "rasterize_backward: a background needs the forward's alpha");
     MG_REQUIRE(N == 0 || d_grads, "rasterize_backward: null gradient output");
     hipStream_t s = as_stream(stream);
-    if (N > 0) {
+    if (N > 0 && !grads_zeroed) {
         ZeroSpans Z{{d_grads, nullptr, nullptr, nullptr, nullptr},
                     {kRecFloats * N, 0, 0, 0, 0}};
         const int64_t blocks = min(ceil_div(kRecFloats * N, 256), (int64_t)4096);

@@ -63,7 +63,7 @@ def gpu_forward(args, W, H, tile, t_min, background=None, chunked=True):
                                         None if ws is None else ws.data_ptr(),
                                         0 if ws is None else ws.numel(), rgb.data_ptr(),
                                         alpha.data_ptr(), T.data_ptr(), stop.data_ptr(),
-                                        _lib.stream(uv)))
+                                        None, _lib.stream(uv)))
     return rgb, alpha, T, stop, ws
 
 
@@ -82,7 +82,7 @@ def gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile, absgrad=True, back
         alpha.data_ptr() if background is not None else None,
         None if background is None else _lib.f32_array(background), gids.numel(),
         None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), W, H, tile, tx,
-        rec.data_ptr(), int(absgrad), _lib.stream(uv)))
+        rec.data_ptr(), int(absgrad), 0, _lib.stream(uv)))
     # The record's slots as the reference's five tensors.
     return [rec[:, 0:2], rec[:, 2:5], rec[:, 5], rec[:, 6:9], rec[:, 9] if absgrad else None]
 
@@ -265,3 +265,41 @@ def test_missing_alpha_gradient_reads_as_zero(dev):
     zero = gpu_backward(args, fwd, grad_rgb, torch.zeros(H, W, device=dev), W, H, tile)
     for a, b in zip(none, zero):
         assert rel_l2(a.cpu(), b.cpu()) < 1e-6
+
+
+def test_forward_clears_the_backward_records(dev):
+    """mg_rasterize_forward(zero_grads=rec) clears the (N,10) record buffer
+    (here prefilled with 7.0, N odd so the slices end mid-float4), and the
+    backward told so (grads_zeroed = 1) gives the records of a backward that
+    fills its own buffer."""
+    from metal_gauss_amd import _lib
+
+    W, H, tile = 96, 70, 16
+    args = prepare(601, 23, W, H, tile, dev, elongate=True)
+    uv, conic, op, col, gids, offs, tx = args
+    N = uv.shape[0]
+    assert N % 2 == 1
+    lib = _lib.load()
+    rgb = torch.empty(H, W, 3, device=dev)
+    alpha = torch.empty(H, W, device=dev)
+    T = torch.empty(H, W, device=dev)
+    stop = torch.empty(H, W, dtype=torch.int32, device=dev)
+    rec = torch.full((N, 10), 7.0, device=dev)
+    _lib.check(lib.mg_rasterize_forward(N, uv.data_ptr(), conic.data_ptr(), op.data_ptr(),
+                                        col.data_ptr(), gids.data_ptr(), offs.data_ptr(), W, H,
+                                        tile, tx, 1e-4, None, gids.numel(), None, 0,
+                                        rgb.data_ptr(), alpha.data_ptr(), T.data_ptr(),
+                                        stop.data_ptr(), rec.data_ptr(), _lib.stream(uv)))
+    torch.cuda.synchronize()
+    assert float(rec.abs().max()) == 0.0
+    g = torch.Generator().manual_seed(5)
+    grad_rgb = torch.randn(H, W, 3, generator=g).to(dev)
+    want = gpu_backward(args, (rgb, alpha, T, stop, None), grad_rgb, None, W, H, tile,
+                        absgrad=True)
+    _lib.check(lib.mg_rasterize_backward(
+        N, uv.data_ptr(), conic.data_ptr(), op.data_ptr(), col.data_ptr(), gids.data_ptr(),
+        offs.data_ptr(), T.data_ptr(), stop.data_ptr(), grad_rgb.data_ptr(), None, None, None,
+        gids.numel(), None, 0, W, H, tile, tx, rec.data_ptr(), 1, 1, _lib.stream(uv)))
+    got = [rec[:, 0:2], rec[:, 2:5], rec[:, 5], rec[:, 6:9], rec[:, 9]]
+    for a, b in zip(got, want):
+        assert torch.allclose(a, b, rtol=1e-5, atol=1e-7), float((a - b).abs().max())
