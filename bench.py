@@ -39,12 +39,14 @@ HBM_PEAK_GBS = 8000.0
 # Kernels timed by the library (names used in mg_timing_query).
 KERNELS = ["preprocess_forward", "bin_count", "exclusive_scan", "bin_write", "tile_sort",
            "depth_sort", "rasterize_forward", "rasterize_backward",
-           "preprocess_backward", "ssim_fused_forward", "ssim_fused_backward", "adam_step"]
+           "preprocess_backward", "preprocess_backward_adam", "ssim_fused_forward",
+           "ssim_fused_backward", "adam_step"]
 
 # Library timing label -> the kernel name rocprofv3 reports for it (for the
 # tile sort, its scatter kernel; the scan runs three kernels and is left out).
 PROF_NAMES = {
     "preprocess_forward": "preprocess_fwd_kernel", "preprocess_backward": "preprocess_bwd_kernel",
+    "preprocess_backward_adam": "preprocess_bwd_adam_kernel",
     "bin_count": "bin_count_rec_kernel", "bin_write": "bin_write_rec_kernel",
     "tile_sort": "count_scatter_kernel", "depth_sort": "tile_depth_sort_kernel",
     "rasterize_forward": "raster_fwd_kernel",
@@ -62,9 +64,12 @@ def parse():
     ap.add_argument("--gaussians", type=int, default=1_000_000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--variant", default="base",
-                    choices=["base", "torch-act", "mip", "mip-torch"],
+                    choices=["base", "unfused-adam", "torch-act", "mip", "mip-torch"],
                     help="base: the config-4 step, exp/sigmoid of the parameters inside the "
-                         "projection kernel (render(activations=True)); torch-act: the same "
+                         "projection kernel (render(activations=True)) and FusedAdam's "
+                         "update inside its backward (render(optimizer=)); unfused-adam: the "
+                         "same with FusedAdam.step() as its own launch after the backward; "
+                         "torch-act: the same "
                          "step with exp/sigmoid in torch before render (train.py:221-222); "
                          "mip: with Mip-Splatting's 3D filter and the 2D antialias "
                          "compensation folded into the projection kernel "
@@ -172,10 +177,16 @@ class Step:
         # exp(log_scales) and sigmoid(logit_opac) (train.py:221-222) run inside
         # the projection kernel and its backward; the "-torch" variants take
         # them in torch as the reference's trainer does.
+        # With adam, "base" and "mip" run FusedAdam's update inside the
+        # projection backward (render(optimizer=)); the other variants, and
+        # "unfused-adam", take it as a separate launch after the backward.
         scales, opac = p["log_scales"], p["logit_opac"]
-        kw = dict(activations=True)
-        if self.variant == "mip":
-            kw = dict(filter_3d=self.f3d, antialias=True, activations=True)
+        epi = self.opt if adam else None
+        kw = dict(activations=True, optimizer=epi)
+        if self.variant == "unfused-adam":
+            kw = dict(activations=True)
+        elif self.variant == "mip":
+            kw = dict(filter_3d=self.f3d, antialias=True, activations=True, optimizer=epi)
         elif self.variant == "torch-act":
             scales, opac = torch.exp(scales), torch.sigmoid(opac)
             kw = {}
@@ -215,6 +226,10 @@ def algorithmic_bytes(kernel, N, I, P, T, f_valid, n_floats):
         "ssim_fused_forward": 60 * P,
         "ssim_fused_backward": 72 * P,
         "adam_step": 28 * n_floats,
+        # With the optimizer epilogue: the 59 floats of parameters and their
+        # two moments read and written, the valid flag and the record
+        # gradient read; no gradient written.
+        "preprocess_backward_adam": (1416 + 44) * N,
     }[kernel]
 
 
@@ -262,13 +277,16 @@ def gpu_bench(args):
     T = 50 * 50
     f_valid = float(step.last_valid.float().mean())
     n_floats = sum(p.numel() for p in step.p.values())
+    def nbytes_of(k):
+        return algorithmic_bytes(k, N, I, P, T, f_valid, n_floats)
+
     dominant = max(kern, key=lambda k: kern[k][0] * kern[k][1])
     avg_ms = kern[dominant][0]
-    nbytes = algorithmic_bytes(dominant, N, I, P, T, f_valid, n_floats)
+    nbytes = nbytes_of(dominant)
     achieved = nbytes / (avg_ms * 1e-3) / 1e9
     rows = {k: {"ms": round(v[0], 4), "per_step": v[1],
-                "GBps": round(algorithmic_bytes(k, N, I, P, T, f_valid, n_floats)
-                              / (v[0] * 1e-3) / 1e9, 1)} for k, v in kern.items()}
+                "GBps": round(nbytes_of(k) / (v[0] * 1e-3) / 1e9, 1)}
+            for k, v in kern.items()}
     f3d_ms = None
     if args.variant in ("mip", "mip-torch"):
         with _lib.KernelTimer():
@@ -660,7 +678,8 @@ def stats_summary(stats_csv, steps, variant="base", mcmc=False, config=None):
         ]
     else:
         vflag = "" if variant == "base" else f" --variant {variant}"
-        what = {"base": "", "torch-act": ", exp/sigmoid of the parameters in torch",
+        what = {"base": "", "unfused-adam": ", FusedAdam.step() after the backward",
+                "torch-act": ", exp/sigmoid of the parameters in torch",
                 "mip": ", Mip 3D filter + 2D antialias in the projection kernel",
                 "mip-torch": ", Mip 3D filter as torch reparameterisation"}[variant]
         lines = [
@@ -906,6 +925,7 @@ def main():
     }
     if args.variant != "base":
         out["config"]["workload"] += {
+            "unfused-adam": "; FusedAdam.step() after the backward, not in it",
             "torch-act": "; exp/sigmoid of the parameters in torch before render",
             "mip": "; Mip 3D filter + 2D antialias in the projection kernel",
             "mip-torch": "; Mip 3D filter as torch reparameterisation, 2D antialias in kernel",

@@ -134,6 +134,26 @@ int32_t mg_preprocess_forward_mip(
     int32_t *valid, uint8_t *valid_mask, float *color, float *opacity_eff,
     mg_stream_t stream);
 
+/* Optional optimizer epilogue of mg_preprocess_backward_mip. The reference's
+ * trainer runs FusedAdam after the backward (train.py:400-402, adam.metal);
+ * with an epilogue the backward applies that Adam step itself to the six
+ * parameter tensors, in the order means, quats, scales, opacities, sh (the
+ * DC band, or the fused (N,16,3) tensor) and sh_rest (NULL when fused),
+ * instead of writing their gradients: p, m (exp_avg) and v (exp_avg_sq) per
+ * tensor, its learning rate and its step count after this step (>= 1), and
+ * the shared betas and eps. The update is FusedAdam's (eps after the
+ * sqrt(bc2) divide, bc1 and bc2 from the step count in double); every row is
+ * updated, rows without gradient with g = 0. Needs sh_degree 3, d_color, and
+ * 16-byte aligned SH tensors and moments. */
+typedef struct mg_adam_epilogue {
+    float *p[6];
+    float *m[6];
+    float *v[6];
+    double lr[6];
+    int64_t step[6];
+    double beta1, beta2, eps;
+} mg_adam_epilogue;
+
 /* Analytic backward of mg_preprocess_forward_mip. d_opacity_eff is the
  * gradient of opacity_eff; d_opacities (N,) receives the gradient of the
  * unfiltered opacities, and the filters' share of the scale and covariance
@@ -141,7 +161,9 @@ int32_t mg_preprocess_forward_mip(
  * (the forward's), d_scales and d_opacities are the gradients of the log
  * scales and the logits: times exp(log scale), and times (1 - y) y for
  * y = sigmoid(logit), as torch's backward of exp and sigmoid. The reference
- * gets these from torch autograd of the same expressions. */
+ * gets these from torch autograd of the same expressions. With adam
+ * non-NULL the six gradients are not written (d_means .. d_opacities may be
+ * NULL): the epilogue above applies them to the parameters in place. */
 int32_t mg_preprocess_backward_mip(
     int64_t N, const float *means, const float *quats, const float *scales,
     const float *sh, const float *sh_rest, int32_t sh_fused,
@@ -152,7 +174,7 @@ int32_t mg_preprocess_backward_mip(
     const float *opacities, const float *filter_3d, int32_t antialias,
     int32_t activations, const float *d_opacity_eff, float *d_means, float *d_quats,
     float *d_scales, float *d_sh, float *d_sh_rest, float *d_opacities,
-    mg_stream_t stream);
+    const mg_adam_epilogue *adam, mg_stream_t stream);
 
 /* Per-Gaussian 3D filter size. Replaces compute_3d_filter
  * (metal_gauss/mipfilter.py:29-73). views: (n_views, 20) device floats per

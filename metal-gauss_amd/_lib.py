@@ -51,7 +51,7 @@ _SIGNATURES = {
     "mg_preprocess_backward_mip": (_i32, [
         _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _f32,
         _f32, _i32, _i32, _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp,
-        _vp, _vp, _vp, _vp, _vp, _vp]),
+        _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mg_compute_3d_filter": (_i32, [_i64, _vp, _i32, _vp, _f32, _f32, _vp, _vp, _vp]),
     "mg_add_noise": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _u64, _vp]),
     "mg_mcmc_workspace_bytes": (_i64, [_i64, _i64]),
@@ -162,6 +162,13 @@ def dev_tensor(t: torch.Tensor, what: str, dtype: torch.dtype | None = torch.flo
     if dtype is not None and t.dtype != dtype:
         raise RuntimeError(f"{what} must be {dtype}, got {t.dtype}")
     return t.data_ptr()
+
+
+class AdamEpilogue(ctypes.Structure):
+    """mg_adam_epilogue (include/mgauss.h): the preprocess backward's
+    optimizer epilogue over means, quats, scales, opacities, sh, sh_rest."""
+    _fields_ = [("p", _vp * 6), ("m", _vp * 6), ("v", _vp * 6), ("lr", _f64 * 6),
+                ("step", _i64 * 6), ("beta1", _f64), ("beta2", _f64), ("eps", _f64)]
 
 
 def ptr_array(ptrs):

@@ -27,6 +27,7 @@ directly.
 
 from __future__ import annotations
 
+import ctypes
 import math
 import time
 from pathlib import Path
@@ -486,7 +487,7 @@ class _PreprocessMip(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means, quats, scales, opacities, sh, sh_rest, filter_3d, antialias,
                 viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
-                sh_degree, valid_mask=None, activations=0):
+                sh_degree, valid_mask=None, activations=0, optimizer=None):
         lib = _load()
         N = means.shape[0]
         dev = means.device
@@ -528,6 +529,7 @@ class _PreprocessMip(torch.autograd.Function):
         ctx.has_sh = sh is not None
         ctx.antialias = bool(antialias)
         ctx.activations = int(activations)
+        ctx.optimizer = optimizer
         ctx.meta = (viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
                     sh_degree)
         ctx.mark_non_differentiable(depth, rxy, valid)
@@ -546,6 +548,22 @@ class _PreprocessMip(torch.autograd.Function):
             d_color, (d_oe,) = None, rest_grads
         N = means.shape[0]
         dev = means.device
+        params = (means, quats, scales, opacities, sh, None if ctx.fused else rest)
+        epi = _epilogue(ctx, params, deg)
+        (p_uv, p_conic, p_color, p_oe), stride, keep = _grad_inputs(
+            N, dev, d_uv, d_conic, d_color, d_oe, ctx.has_sh, True)
+        if epi is not None:
+            # The optimizer's step for these parameters runs inside the kernel;
+            # no gradient tensor is formed and autograd gets none.
+            _lib.check(lib.mg_preprocess_backward_mip(
+                N, means.data_ptr(), quats.data_ptr(), scales.data_ptr(), sh.data_ptr(),
+                None if rest is None else rest.data_ptr(), int(ctx.fused), p_uv, p_conic,
+                p_color, stride, valid.data_ptr(), _lib.host_f32(viewmat), fx, fy, cx, cy, W,
+                H, near, far, blur, max_radius, _lib.host_f32(cam_center), deg,
+                opacities.data_ptr(), None if filt is None else filt.data_ptr(),
+                int(ctx.antialias), ctx.activations, p_oe, None, None, None, None, None, None,
+                ctypes.byref(epi), _lib.stream(means)))
+            return (None,) * 24
         d_means = torch.empty(N, 3, device=dev)
         d_quats = torch.empty(N, 4, device=dev)
         d_scales = torch.empty(N, 3, device=dev)
@@ -554,8 +572,6 @@ class _PreprocessMip(torch.autograd.Function):
         if ctx.has_sh:
             d_sh = torch.empty_like(sh)
             d_rest = None if ctx.fused else torch.empty_like(rest)
-        (p_uv, p_conic, p_color, p_oe), stride, keep = _grad_inputs(
-            N, dev, d_uv, d_conic, d_color, d_oe, ctx.has_sh, True)
         _lib.check(lib.mg_preprocess_backward_mip(
             N, means.data_ptr(), quats.data_ptr(), scales.data_ptr(),
             None if sh is None else sh.data_ptr(), None if rest is None else rest.data_ptr(),
@@ -565,8 +581,27 @@ class _PreprocessMip(torch.autograd.Function):
             None if filt is None else filt.data_ptr(), int(ctx.antialias), ctx.activations,
             p_oe, d_means.data_ptr(), d_quats.data_ptr(),
             d_scales.data_ptr(), None if d_sh is None else d_sh.data_ptr(),
-            None if d_rest is None else d_rest.data_ptr(), d_op.data_ptr(), _lib.stream(means)))
-        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 17
+            None if d_rest is None else d_rest.data_ptr(), d_op.data_ptr(), None,
+            _lib.stream(means)))
+        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 18
+
+
+def _epilogue(ctx, params, sh_degree):
+    """The optimizer's step as the preprocess backward's epilogue, or None
+    when the ordinary gradients must be returned: no optimizer given, the
+    explicit-colour route, SH degree below 3, a parameter that does not
+    require grad, SH tensors or moments the kernel cannot stage (16-byte
+    alignment), or whatever the optimizer's own ``epilogue`` refuses."""
+    opt = ctx.optimizer
+    if opt is None or not ctx.has_sh or sh_degree != 3 or not hasattr(opt, "epilogue"):
+        return None
+    for t, need in zip(params, ctx.needs_input_grad[:6]):
+        if t is not None and not need:
+            return None
+    sh, rest = params[4], params[5]
+    if sh.data_ptr() % 16 or (rest is not None and rest.data_ptr() % 16):
+        return None
+    return opt.epilogue(list(params))
 
 
 # Names that describe this backend rather than the reference's.
@@ -638,7 +673,7 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
            background=(0.0, 0.0, 0.0), colors=None, max_radius_frac: float = 1.0,
            sh_rest=None, antialias: bool = False, absgrad_out=None,
            min_transmittance: float = DEFAULT_T_MIN, chunked_backward: bool = False,
-           filter_3d=None, activations: bool = False, **_ignored):
+           filter_3d=None, activations: bool = False, optimizer=None, **_ignored):
     """Render Gaussians from one camera; same signature as the reference's.
 
     means (N,3) world; quats (N,4) wxyz (need not be normalised); scales (N,3)
@@ -661,6 +696,14 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     their derivatives in its backward, so the gradients land on the log
     scales and logits (the same values as torch.exp / torch.sigmoid in
     front of ``render``).
+    ``optimizer`` (a FusedAdam over these parameters) moves its step for
+    means, quats, scales, opacities and the SH into the projection
+    backward: the kernel updates the parameters and moments in place, no
+    gradient tensors are formed, their ``.grad`` stays unset and the
+    optimizer's ``step()`` skips them. The result equals the backward
+    followed by ``step()`` only when this render is the sole use of those
+    parameters in the loss; otherwise (or when the optimizer or the tensors
+    do not allow it) the ordinary gradients are returned.
     """
     explicit_colors = colors is not None
     _require_gpu(means)
@@ -677,7 +720,7 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     # info["valid_mask"], written by the projection kernel itself.
     valid_b = torch.empty(means.shape[0], dtype=torch.bool, device=means.device)
 
-    if filter_3d is not None or antialias or activations:
+    if filter_3d is not None or antialias or activations or optimizer is not None:
         # Both filters (and the activations) in the projection kernel; the
         # compensated opacity is binned too, which gives a tighter, still
         # exact, ellipse bound (metal_backend.py:506-511).
@@ -686,14 +729,14 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
             uv, conic, depth, rxy, valid_i, opacities = _PreprocessMip.apply(
                 means, quats, scales, opacities, None, None, filter_3d, antialias, vm_h, fx,
                 fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree, valid_b,
-                act)
+                act, None)
             colors = colors.contiguous()
         else:
             sh_in, rest_in = _sh_inputs(sh, sh_rest)
             uv, conic, depth, rxy, valid_i, colors, opacities = _PreprocessMip.apply(
                 means, quats, scales, opacities, sh_in, rest_in, filter_3d, antialias, vm_h,
                 fx, fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree,
-                valid_b, act)
+                valid_b, act, optimizer)
     elif explicit_colors:
         uv, conic, depth, rxy, valid_i = _PreprocessMetal.apply(
             means, quats, scales, None, None, opacities.detach(), vm_h, fx, fy, cx, cy, W, H,

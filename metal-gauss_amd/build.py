@@ -36,6 +36,17 @@ CFLAGS = [
 ]
 
 
+# Multiply-add fusion only within one source expression (as written) for the
+# Adam update and the projection backward: the backward's gradient arithmetic
+# is instantiated twice, writing gradients and feeding the optimizer epilogue,
+# and hipcc's default cross-statement fusion may round the two differently;
+# with this both instantiations, and the separate Adam kernel, round alike.
+FILE_FLAGS = {
+    "adam.hip": ["-ffp-contract=on"],
+    "preprocess.hip": ["-ffp-contract=on"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -44,7 +55,7 @@ def hipcc() -> str:
 
 
 def _compile(src: Path, obj: Path) -> tuple[Path, str]:
-    cmd = [hipcc(), *CFLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *CFLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{p.stdout}\n{p.stderr}")

@@ -62,12 +62,8 @@ struct AdamTable {
 __device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v,
                                           const AdamTable &tab, float step_size,
                                           float inv_sqrt_bc2, bool eps_inside) {
-    const float eps = tab.eps;
-    m = fmaf(tab.b1, m, tab.omb1 * g);
-    v = fmaf(tab.b2, v, tab.omb2 * g * g);
-    const float sv = sqrtf(v);
-    const float denom = eps_inside ? (sv + eps) : (sv * inv_sqrt_bc2 + eps);
-    p = p - step_size * m / denom;
+    adam_update(p, g, m, v, tab.b1, tab.b2, tab.omb1, tab.omb2, tab.eps, step_size,
+                inv_sqrt_bc2, eps_inside);
 }
 
 __global__ __launch_bounds__(kAdamThreads) void adam_multi_kernel(const AdamTable tab) {

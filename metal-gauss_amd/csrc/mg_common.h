@@ -62,6 +62,22 @@ __device__ __forceinline__ int64_t xcd_contiguous(int64_t b, int64_t nb) {
     return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
 }
 
+// One Adam element update, torch's formula with eps after the sqrt(bc2)
+// divide (metal_gauss/csrc/adam.metal:34-41): step_size = lr / bc1 and
+// inv_sqrt_bc2 = 1 / sqrt(bc2), formed in double by the caller. Shared by the
+// optimizer kernels and the preprocess backward's optimizer epilogue so both
+// round identically.
+__device__ __forceinline__ void adam_update(float &p, float g, float &m, float &v, float b1,
+                                            float b2, float omb1, float omb2, float eps,
+                                            float step_size, float inv_sqrt_bc2,
+                                            bool eps_inside) {
+    m = fmaf(b1, m, omb1 * g);
+    v = fmaf(b2, v, omb2 * g * g);
+    const float sv = sqrtf(v);
+    const float denom = eps_inside ? (sv + eps) : (sv * inv_sqrt_bc2 + eps);
+    p = p - step_size * m / denom;
+}
+
 #define MG_REQUIRE(cond, ...)                                                  \
     do {                                                                       \
         if (!(cond)) {                                                         \

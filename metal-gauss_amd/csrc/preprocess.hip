@@ -625,6 +625,170 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFw
     }
 }
 
+// Adam applied in place by the backward instead of writing the gradients of
+// its six parameter tensors: means 0, quats 1, scales 2, opacities 3, sh (DC
+// or fused) 4, sh_rest 5.
+struct AdamEpi {
+    float *p[6], *m[6], *v[6];
+    float step_size[6], inv_sqrt_bc2[6];
+    float b1, b2, omb1, omb2, eps;
+};
+
+// Cache policy of the epilogue's traffic (bit 0: moment loads, bit 1: moment
+// stores, bit 2: parameter stores non-temporal). Ordinary accesses measured
+// best over the whole step at config 4: non-temporal moment stores cost the
+// kernel about 40 us, while ordinary ones leave dirty lines whose write-back
+// slows the next projection forward by about 30 us.
+constexpr int kEpiNt = 0;
+constexpr bool kNtLoad = kEpiNt & 1, kNtMom = kEpiNt & 2, kNtPar = kEpiNt & 4;
+
+typedef float v4a __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ float ld_nt(const float *q) {
+    return NT ? __builtin_nontemporal_load(q) : *q;
+}
+template <bool NT>
+__device__ __forceinline__ void st_nt(float *q, float x) {
+    if (NT) __builtin_nontemporal_store(x, q);
+    else *q = x;
+}
+template <bool NT>
+__device__ __forceinline__ float4 ld_nt4(const float *q) {
+    const v4a v = NT ? __builtin_nontemporal_load(reinterpret_cast<const v4a *>(q))
+                     : *reinterpret_cast<const v4a *>(q);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+template <bool NT>
+__device__ __forceinline__ void st_nt4(float *q, const float4 &a) {
+    v4a v = {a.x, a.y, a.z, a.w};
+    if (NT) __builtin_nontemporal_store(v, reinterpret_cast<v4a *>(q));
+    else *reinterpret_cast<v4a *>(q) = v;
+}
+
+// The moments could alias the parameters as far as the compiler knows, so it
+// keeps every load after every earlier store: each helper below therefore
+// requests all of its moments before it stores anything, one memory round
+// trip instead of one per element.
+
+// The Gaussian's 11 non-SH elements: means (3), quats (4), scales (3),
+// opacity (1), with their gradients.
+__device__ __forceinline__ void epi_rows(const AdamEpi &E, int64_t g, const float (&pm)[3],
+                                         const float (&pq)[4], const float (&ps)[3],
+                                         const float (&gm)[3], const float (&gq)[4],
+                                         const float (&gs)[3], float gop) {
+    float mm[3], vm[3], mq[4], vq[4], msc[3], vsc[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        mm[j] = ld_nt<kNtLoad>(E.m[0] + 3 * g + j);
+        vm[j] = ld_nt<kNtLoad>(E.v[0] + 3 * g + j);
+        msc[j] = ld_nt<kNtLoad>(E.m[2] + 3 * g + j);
+        vsc[j] = ld_nt<kNtLoad>(E.v[2] + 3 * g + j);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        mq[j] = ld_nt<kNtLoad>(E.m[1] + 4 * g + j);
+        vq[j] = ld_nt<kNtLoad>(E.v[1] + 4 * g + j);
+    }
+    float po = E.p[3][g];
+    float mo = ld_nt<kNtLoad>(E.m[3] + g), vo = ld_nt<kNtLoad>(E.v[3] + g);
+    float qm[3] = {pm[0], pm[1], pm[2]}, qq[4] = {pq[0], pq[1], pq[2], pq[3]};
+    float qs[3] = {ps[0], ps[1], ps[2]};
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        adam_update(qm[j], gm[j], mm[j], vm[j], E.b1, E.b2, E.omb1, E.omb2, E.eps,
+                    E.step_size[0], E.inv_sqrt_bc2[0], false);
+        adam_update(qs[j], gs[j], msc[j], vsc[j], E.b1, E.b2, E.omb1, E.omb2, E.eps,
+                    E.step_size[2], E.inv_sqrt_bc2[2], false);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        adam_update(qq[j], gq[j], mq[j], vq[j], E.b1, E.b2, E.omb1, E.omb2, E.eps,
+                    E.step_size[1], E.inv_sqrt_bc2[1], false);
+    adam_update(po, gop, mo, vo, E.b1, E.b2, E.omb1, E.omb2, E.eps, E.step_size[3],
+                E.inv_sqrt_bc2[3], false);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        st_nt<kNtPar>(E.p[0] + 3 * g + j, qm[j]);
+        st_nt<kNtMom>(E.m[0] + 3 * g + j, mm[j]);
+        st_nt<kNtMom>(E.v[0] + 3 * g + j, vm[j]);
+        st_nt<kNtPar>(E.p[2] + 3 * g + j, qs[j]);
+        st_nt<kNtMom>(E.m[2] + 3 * g + j, msc[j]);
+        st_nt<kNtMom>(E.v[2] + 3 * g + j, vsc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        st_nt<kNtPar>(E.p[1] + 4 * g + j, qq[j]);
+        st_nt<kNtMom>(E.m[1] + 4 * g + j, mq[j]);
+        st_nt<kNtMom>(E.v[1] + 4 * g + j, vq[j]);
+    }
+    st_nt<kNtPar>(E.p[3] + g, po);
+    st_nt<kNtMom>(E.m[3] + g, mo);
+    st_nt<kNtMom>(E.v[3] + g, vo);
+}
+
+// The staged round's Adam: the slice sb holds the round's d_sh and cb its
+// parameters (the same block positions; each lane reads back the float4s it
+// put there itself); moments are read and written at those positions of their
+// tensors. A float4 that runs past the round's ng Gaussians is handled per
+// element.
+__device__ __forceinline__ void stage_adam(const float4 *sb, const float4 *cb,
+                                           const AdamEpi &E, int fused, int64_t G0, int ng) {
+    const int lane = threadIdx.x & 63;
+    float4 m4[3], v4[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int f = 4 * (lane + 64 * i);
+        const int t = fused || f < 48 ? 4 : 5;
+        const int64_t off = fused ? G0 * 48 + f : (f < 48 ? G0 * 3 + f : G0 * 45 + (f - 48));
+        if (stage_row(fused, f + 3) < ng) {
+            m4[i] = ld_nt4<kNtLoad>(E.m[t] + off);
+            v4[i] = ld_nt4<kNtLoad>(E.v[t] + off);
+        } else {
+            float e[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (stage_row(fused, f + k) < ng) {
+                    e[k] = ld_nt<kNtLoad>(E.m[t] + off + k);
+                    e[4 + k] = ld_nt<kNtLoad>(E.v[t] + off + k);
+                }
+            }
+            m4[i] = make_float4(e[0], e[1], e[2], e[3]);
+            v4[i] = make_float4(e[4], e[5], e[6], e[7]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int f = 4 * (lane + 64 * i);
+        const int t = fused || f < 48 ? 4 : 5;
+        const int64_t off = fused ? G0 * 48 + f : (f < 48 ? G0 * 3 + f : G0 * 45 + (f - 48));
+        const float4 g4 = sb[lane + 64 * i];
+        float gs[4] = {g4.x, g4.y, g4.z, g4.w};
+        const float4 c4 = cb[lane + 64 * i];
+        float po[4] = {c4.x, c4.y, c4.z, c4.w};
+        float ms[4] = {m4[i].x, m4[i].y, m4[i].z, m4[i].w};
+        float vs[4] = {v4[i].x, v4[i].y, v4[i].z, v4[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            adam_update(po[k], gs[k], ms[k], vs[k], E.b1, E.b2, E.omb1, E.omb2, E.eps,
+                        E.step_size[t], E.inv_sqrt_bc2[t], false);
+        if (stage_row(fused, f + 3) < ng) {
+            st_nt4<kNtPar>(E.p[t] + off, make_float4(po[0], po[1], po[2], po[3]));
+            st_nt4<kNtMom>(E.m[t] + off, make_float4(ms[0], ms[1], ms[2], ms[3]));
+            st_nt4<kNtMom>(E.v[t] + off, make_float4(vs[0], vs[1], vs[2], vs[3]));
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (stage_row(fused, f + k) < ng) {
+                    st_nt<kNtPar>(E.p[t] + off + k, po[k]);
+                    st_nt<kNtMom>(E.m[t] + off + k, ms[k]);
+                    st_nt<kNtMom>(E.v[t] + off + k, vs[k]);
+                }
+            }
+        }
+    }
+}
+
 struct PreBwdArgs {
     Cam C;
     int64_t N;
@@ -644,11 +808,13 @@ struct PreBwdArgs {
     float *d_op;
     int32_t act;   // kActLogScale | kActLogitOpac (effective-opacity kernel only)
     int32_t stage; // SH rows and their gradients staged through LDS
+    AdamEpi E;     // the optimizer epilogue (EPI kernels)
 };
 
-template <bool MIP, bool STAGE>
-__global__ __launch_bounds__(kPreThreads) __attribute__((amdgpu_waves_per_eu(4)))
-void preprocess_bwd_kernel(const PreBwdArgs A) {
+// EPI: the optimizer epilogue replaces the six gradient outputs (needs MIP,
+// STAGE and d_color).
+template <bool MIP, bool STAGE, bool EPI>
+__device__ __forceinline__ void preprocess_bwd_body(const PreBwdArgs &A) {
     const Cam &C = A.C;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t g0 = (int64_t)blockIdx.x * kPreThreads + wave * 64;
@@ -695,7 +861,7 @@ void preprocess_bwd_kernel(const PreBwdArgs A) {
         // its coefficients get no gradient.
         const bool need = vld != 0 && (dcol[0] != 0.f || dcol[1] != 0.f || dcol[2] != 0.f);
         const int ng = (int)max((int64_t)0, min((int64_t)64, A.N - g0));
-        if (ballot(need) == 0) {
+        if (!EPI && ballot(need) == 0) {
             // Coalesced zero fill of the wave's rows.
             if (A.fused) {
                 for (int e = lane; e < ng * 48; e += 64) A.d_sh[g0 * 48 + e] = 0.f;
@@ -760,17 +926,23 @@ void preprocess_bwd_kernel(const PreBwdArgs A) {
                 float *sf = reinterpret_cast<float *>(sb);
                 const uint64_t nm = ballot(need);
                 const int nw = (int)max((int64_t)0, min((int64_t)64, A.N - g0));
+                // With the epilogue every row's parameters are read (all are
+                // updated) and a second slice keeps the round's own for it.
+                __shared__ float4 s_cur[EPI ? kPreThreads / 64 : 1][EPI ? kStageF4 : 1];
+                float4 *cb = s_cur[EPI ? wave : 0];
                 float4 pf[3];
-                stage_load(R, g0, min(16, nw), (uint32_t)(nm & 0xFFFFu), pf);
+                const uint64_t lm = EPI ? ~0ull : nm;
+                stage_load(R, g0, min(16, nw), (uint32_t)(lm & 0xFFFFu), pf);
 #pragma unroll 1
                 for (int r = 0; r < 4; ++r) {
                     const int ngr = min(16, max(0, nw - 16 * r));
                     stage_put(sb, pf);
+                    if (EPI) stage_put(cb, pf);
                     wave_lds_sync();
                     const int ngn = min(16, max(0, nw - 16 * (r + 1)));
                     if (r < 3 && ngn > 0)
                         stage_load(R, g0 + 16 * (r + 1), ngn,
-                                   (uint32_t)((nm >> (16 * (r + 1))) & 0xFFFFu), pf);
+                                   (uint32_t)((lm >> (16 * (r + 1))) & 0xFFFFu), pf);
                     const int gl = 16 * r + (lane >> 2);
                     float c[4][3], dsh[4][3];
                     stage_read(sf, A.fused, lane >> 2, q, c);
@@ -778,7 +950,10 @@ void preprocess_bwd_kernel(const PreBwdArgs A) {
                     wave_lds_sync();   // every coefficient read before d_sh replaces it
                     stage_write(sf, A.fused, lane >> 2, q, dsh);
                     wave_lds_sync();
-                    if (ngr > 0) stage_store(sb, A.d_sh, A.d_rest, A.fused, g0 + 16 * r, ngr);
+                    if (ngr > 0) {
+                        if (EPI) stage_adam(sb, cb, A.E, A.fused, g0 + 16 * r, ngr);
+                        else stage_store(sb, A.d_sh, A.d_rest, A.fused, g0 + 16 * r, ngr);
+                    }
                     wave_lds_sync();   // the slice is rewritten next round
                 }
             } else {
@@ -828,6 +1003,9 @@ void preprocess_bwd_kernel(const PreBwdArgs A) {
     if (!in) return;
 
     // ------------------------------------------ projection: lane = Gaussian
+    // The epilogue's gradients of the quats, scales and opacity (zero for a
+    // row that is not visible).
+    float gq[4] = {0.f, 0.f, 0.f, 0.f}, gsc[3] = {0.f, 0.f, 0.f}, gop = 0.f;
     if (vld != 0) {
         // s0: the activated scales before the 3D filter; op0: the activated
         // opacity.
@@ -974,16 +1152,22 @@ void preprocess_bwd_kernel(const PreBwdArgs A) {
             // Through the activations, as torch's backward of exp (grad *
             // result) and of sigmoid (grad * (1 - y) * y).
             if (A.act & kActLogitOpac) dop = dop * (1.0f - op0) * op0;
-            A.d_op[g] = dop;
+            if (EPI) gop = dop;
+            else A.d_op[g] = dop;
             if (A.act & kActLogScale) {
                 dsc[0] = dsc[0] * s0[0];
                 dsc[1] = dsc[1] * s0[1];
                 dsc[2] = dsc[2] * s0[2];
             }
         }
-        A.d_scales[3 * g] = dsc[0];
-        A.d_scales[3 * g + 1] = dsc[1];
-        A.d_scales[3 * g + 2] = dsc[2];
+        if (EPI) {
+#pragma unroll
+            for (int j = 0; j < 3; ++j) gsc[j] = dsc[j];
+        } else {
+            A.d_scales[3 * g] = dsc[0];
+            A.d_scales[3 * g + 1] = dsc[1];
+            A.d_scales[3 * g + 2] = dsc[2];
+        }
         // R(q) for unit q = (w,x,y,z): d/dq of sum G_ij R_ij.
         const float w = P.q[0], x = P.q[1], y = P.q[2], z = P.q[3];
         const float G00 = G[0], G01 = G[1], G02 = G[2], G10 = G[3], G11 = G[4], G12 = G[5],
@@ -995,19 +1179,46 @@ void preprocess_bwd_kernel(const PreBwdArgs A) {
         // through q/|q|
         const float dotq = w * dw + x * dxq + y * dyq + z * dzq;
         const float iq = 1.0f / fmaxf(P.qn, 1e-12f);
-        A.d_quats[4 * g] = (dw - w * dotq) * iq;
-        A.d_quats[4 * g + 1] = (dxq - x * dotq) * iq;
-        A.d_quats[4 * g + 2] = (dyq - y * dotq) * iq;
-        A.d_quats[4 * g + 3] = (dzq - z * dotq) * iq;
+        const float dq[4] = {(dw - w * dotq) * iq, (dxq - x * dotq) * iq,
+                             (dyq - y * dotq) * iq, (dzq - z * dotq) * iq};
+        if (EPI) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) gq[j] = dq[j];
+        } else {
+            A.d_quats[4 * g] = dq[0];
+            A.d_quats[4 * g + 1] = dq[1];
+            A.d_quats[4 * g + 2] = dq[2];
+            A.d_quats[4 * g + 3] = dq[3];
+        }
+    } else if (EPI) {
+        // No gradient (zeros above): Adam still decays the moments and steps
+        // the row.
     } else {
         if (MIP) A.d_op[g] = 0.f;
         A.d_scales[3 * g] = 0.f; A.d_scales[3 * g + 1] = 0.f; A.d_scales[3 * g + 2] = 0.f;
         A.d_quats[4 * g] = 0.f; A.d_quats[4 * g + 1] = 0.f;
         A.d_quats[4 * g + 2] = 0.f; A.d_quats[4 * g + 3] = 0.f;
     }
-    A.d_means[3 * g] = dmean[0];
-    A.d_means[3 * g + 1] = dmean[1];
-    A.d_means[3 * g + 2] = dmean[2];
+    if (EPI) {
+        const float pm[3] = {mx, my, mz};
+        epi_rows(A.E, g, pm, qv, sraw, dmean, gq, gsc, gop);
+    } else {
+        A.d_means[3 * g] = dmean[0];
+        A.d_means[3 * g + 1] = dmean[1];
+        A.d_means[3 * g + 2] = dmean[2];
+    }
+}
+
+template <bool MIP, bool STAGE>
+__global__ __launch_bounds__(kPreThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void preprocess_bwd_kernel(const PreBwdArgs A) {
+    preprocess_bwd_body<MIP, STAGE, false>(A);
+}
+
+// The backward with the optimizer epilogue: 168 VGPRs, 3 waves/SIMD.
+__global__ __launch_bounds__(kPreThreads) __attribute__((amdgpu_waves_per_eu(3)))
+void preprocess_bwd_adam_kernel(const PreBwdArgs A) {
+    preprocess_bwd_body<true, true, true>(A);
 }
 
 static int32_t make_cam(Cam &C, const float *viewmat, float fx, float fy, float cx, float cy,
@@ -1082,20 +1293,21 @@ static int32_t preprocess_bwd(int64_t N, const float *means, const float *quats,
                               int32_t activations,
                               const float *d_opacity_eff, float *d_means, float *d_quats,
                               float *d_scales, float *d_sh, float *d_sh_rest,
-                              float *d_opacities, mg_stream_t stream, const char *who) {
+                              float *d_opacities, const mg_adam_epilogue *adam,
+                              mg_stream_t stream, const char *who) {
     PreBwdArgs A{};
     int32_t rc = make_cam(A.C, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane, blur,
                           max_radius, cam_center, sh_degree, who);
     if (rc != MG_OK) return rc;
     MG_REQUIRE(N >= 0, "%s: N = %lld", who, (long long)N);
     if (N == 0) return MG_OK;
-    MG_REQUIRE(means && quats && scales && d_uv && d_conic && valid && d_means && d_quats &&
-                   d_scales, "%s: null tensor pointer", who);
+    MG_REQUIRE(means && quats && scales && d_uv && d_conic && valid &&
+                   (adam || (d_means && d_quats && d_scales)), "%s: null tensor pointer", who);
     if (d_color) {
-        MG_REQUIRE(sh && d_sh && (sh_fused || (sh_rest && d_sh_rest)),
+        MG_REQUIRE(sh && (adam || d_sh) && (sh_fused || (sh_rest && (adam || d_sh_rest))),
                    "SH must be either one (N,16,3) tensor or (N,1,3)+(N,15,3)");
     }
-    MG_REQUIRE(!mip || (opacities && d_opacity_eff && d_opacities),
+    MG_REQUIRE(!mip || (opacities && d_opacity_eff && (adam || d_opacities)),
                "%s: null opacity pointer", who);
     MG_REQUIRE(grad_stride == 0 || grad_stride >= 3, "%s: gradient record stride %d", who,
                grad_stride);
@@ -1117,9 +1329,50 @@ static int32_t preprocess_bwd(int64_t N, const float *means, const float *quats,
     A.st_vec4 = d_sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)d_sh & 15) == 0);
     A.stage = A.vec4 && A.st_vec4 && stage_aligned(sh, sh_rest, sh_fused) &&
               stage_aligned(d_sh, d_sh_rest, sh_fused);
+    if (adam) {
+        // The epilogue reads the parameters the kernel already holds and
+        // writes them back, so its tensors must be the kernel's inputs.
+        const float *in[6] = {means, quats, scales, opacities, sh, sh_fused ? nullptr : sh_rest};
+        for (int t = 0; t < 6; ++t) {
+            MG_REQUIRE(adam->p[t] == in[t] && (in[t] == nullptr || (adam->m[t] && adam->v[t])),
+                       "%s: optimizer epilogue tensor %d is not the kernel's input", who, t);
+            MG_REQUIRE(in[t] == nullptr || adam->step[t] >= 1,
+                       "%s: optimizer epilogue step %lld < 1", who, (long long)adam->step[t]);
+        }
+        MG_REQUIRE(mip && d_color && sh_degree == 3 && A.vec4 &&
+                       stage_aligned(sh, sh_rest, sh_fused) &&
+                       stage_aligned(adam->m[4], adam->m[5], sh_fused) &&
+                       stage_aligned(adam->v[4], adam->v[5], sh_fused),
+                   "%s: the optimizer epilogue needs the effective-opacity kernel, d_color, "
+                   "SH degree 3 and 16-byte aligned SH tensors and moments", who);
+        A.stage = 1;
+        AdamEpi &E = A.E;
+        E.b1 = (float)adam->beta1;
+        E.b2 = (float)adam->beta2;
+        E.omb1 = (float)(1.0 - adam->beta1);
+        E.omb2 = (float)(1.0 - adam->beta2);
+        E.eps = (float)adam->eps;
+        for (int t = 0; t < 6; ++t) {
+            E.p[t] = adam->p[t];
+            E.m[t] = adam->m[t];
+            E.v[t] = adam->v[t];
+            if (in[t] == nullptr) continue;
+            // Formed in double from the exact hyperparameters, as FusedAdam.
+            const double bc1 = 1.0 - std::pow(adam->beta1, (double)adam->step[t]);
+            const double bc2 = 1.0 - std::pow(adam->beta2, (double)adam->step[t]);
+            E.step_size[t] = (float)(adam->lr[t] / bc1);
+            E.inv_sqrt_bc2[t] = (float)(1.0 / std::sqrt(bc2));
+        }
+    }
     const int64_t blocks = ceil_div(N, kPreThreads);
-    TimedScope ts("preprocess_backward", as_stream(stream));
     hipStream_t st = as_stream(stream);
+    if (adam) {
+        TimedScope ts("preprocess_backward_adam", st);
+        preprocess_bwd_adam_kernel<<<(unsigned)blocks, kPreThreads, 0, st>>>(A);
+        MG_LAUNCHED("preprocess_bwd_adam_kernel");
+        return MG_OK;
+    }
+    TimedScope ts("preprocess_backward", st);
     if (mip && A.stage)
         preprocess_bwd_kernel<true, true><<<(unsigned)blocks, kPreThreads, 0, st>>>(A);
     else if (mip)
@@ -1184,8 +1437,8 @@ int32_t mg_preprocess_backward(int64_t N, const float *means, const float *quats
                           d_color, grad_stride, valid, viewmat, fx, fy, cx, cy, W, H, near_plane,
                           far_plane, blur, max_radius, cam_center, sh_degree, false, nullptr,
                           nullptr, 0, 0,
-                          nullptr, d_means, d_quats, d_scales, d_sh, d_sh_rest, nullptr, stream,
-                          "mg_preprocess_backward");
+                          nullptr, d_means, d_quats, d_scales, d_sh, d_sh_rest, nullptr, nullptr,
+                          stream, "mg_preprocess_backward");
 }
 
 int32_t mg_preprocess_backward_mip(int64_t N, const float *means, const float *quats,
@@ -1201,13 +1454,14 @@ int32_t mg_preprocess_backward_mip(int64_t N, const float *means, const float *q
                                    int32_t activations,
                                    const float *d_opacity_eff, float *d_means, float *d_quats,
                                    float *d_scales, float *d_sh, float *d_sh_rest,
-                                   float *d_opacities, mg_stream_t stream) {
+                                   float *d_opacities, const mg_adam_epilogue *adam,
+                                   mg_stream_t stream) {
     return preprocess_bwd(N, means, quats, scales, sh, sh_rest, sh_fused, d_uv, d_conic,
                           d_color, grad_stride, valid, viewmat, fx, fy, cx, cy, W, H,
                           near_plane, far_plane, blur, max_radius, cam_center, sh_degree, true,
                           opacities, filter_3d, antialias, activations, d_opacity_eff,
-                          d_means, d_quats, d_scales, d_sh, d_sh_rest, d_opacities, stream,
-                          "mg_preprocess_backward_mip");
+                          d_means, d_quats, d_scales, d_sh, d_sh_rest, d_opacities, adam,
+                          stream, "mg_preprocess_backward_mip");
 }
 
 }  // extern "C"

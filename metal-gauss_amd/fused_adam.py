@@ -25,6 +25,72 @@ class FusedAdam(torch.optim.Optimizer):
     def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-15):
         super().__init__(params, dict(lr=lr, betas=betas, eps=eps))
 
+    def _state_of(self, p):
+        st = self.state[p]
+        if not st:
+            st["step"] = 0
+            st["exp_avg"] = torch.zeros_like(p, memory_format=torch.contiguous_format)
+            st["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.contiguous_format)
+        return st
+
+    def epilogue(self, tensors):
+        """This step's Adam for the given tensors as the preprocess backward's
+        optimizer epilogue (``_lib.AdamEpilogue``), or None when it does not
+        apply: a tensor that is not one of this optimizer's parameters (by
+        storage), has a gradient already, is not a contiguous ROCm float32
+        tensor, or groups that differ in betas or eps. On success each
+        parameter's step count is advanced now, as ``step()`` would, and the
+        backward leaves its ``.grad`` unset, so ``step()`` skips it. Moments
+        that are not contiguous and 16-byte aligned (the kernel moves the SH
+        rows as float4) also refuse.
+
+        ``tensors``: means, quats, scales, opacities, sh, sh_rest (None when
+        the SH is one fused tensor)."""
+        owner = {}
+        for group in self.param_groups:
+            for p in group["params"]:
+                owner[(p.data_ptr(), tuple(p.shape))] = (p, group)
+        found = []
+        for t in tensors:
+            if t is None:
+                found.append(None)
+                continue
+            hit = owner.get((t.data_ptr(), tuple(t.shape)))
+            if hit is None:
+                return None
+            p, group = hit
+            if (p.grad is not None or p.device.type != "cuda" or p.dtype != torch.float32
+                    or not p.is_contiguous()):
+                return None
+            found.append(hit)
+        groups = [g for _, g in filter(None, found)]
+        keys = {(tuple(g["betas"]), float(g["eps"])) for g in groups}
+        if len(keys) != 1:
+            return None
+        (b1, b2), eps = next(iter(keys))
+        for hit in filter(None, found):
+            st = self._state_of(hit[0])
+            for mom in (st["exp_avg"], st["exp_avg_sq"]):
+                if (not mom.is_contiguous() or mom.data_ptr() % 16 or
+                        mom.shape != hit[0].shape):
+                    return None
+        epi = _lib.AdamEpilogue()
+        keep = []
+        for i, hit in enumerate(found):
+            if hit is None:
+                continue
+            p, group = hit
+            st = self._state_of(p)
+            st["step"] += 1
+            epi.p[i], epi.m[i], epi.v[i] = (p.data_ptr(), st["exp_avg"].data_ptr(),
+                                             st["exp_avg_sq"].data_ptr())
+            epi.lr[i] = float(group["lr"])
+            epi.step[i] = int(st["step"])
+            keep += [st["exp_avg"], st["exp_avg_sq"]]
+        epi.beta1, epi.beta2, epi.eps = float(b1), float(b2), float(eps)
+        epi._keep = keep
+        return epi
+
     @torch.no_grad()
     def step(self, closure=None):
         loss = None
@@ -45,11 +111,7 @@ class FusedAdam(torch.optim.Optimizer):
                         f"FusedAdam requires ROCm (cuda) parameters, got device '{p.device}'")
                 if not p.is_contiguous():
                     raise RuntimeError("FusedAdam parameters must be contiguous")
-                st = self.state[p]
-                if not st:
-                    st["step"] = 0
-                    st["exp_avg"] = torch.zeros_like(p, memory_format=torch.contiguous_format)
-                    st["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.contiguous_format)
+                st = self._state_of(p)
                 st["step"] += 1
                 g = g.contiguous()
                 key = (float(b1), float(b2), float(group["eps"]), p.device)

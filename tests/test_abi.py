@@ -101,6 +101,26 @@ def test_bad_arguments_fail_before_any_launch():
                                    0.01, 100.0, 0.3, 8.0, cc, 4, 1, 1, 1, 1, 1, None, None,
                                    None)
     assert rc == 1 and "sh_degree" in lib.mg_last_error().decode()
+    # optimizer epilogue: its tensors must be the kernel's inputs, and the SH
+    # must be 16-byte aligned (host pointers only; nothing is dereferenced)
+    ins = [16, 32, 48, 96, 64, 80]     # means quats scales opacities sh sh_rest
+
+    def bwd(epi, sh=64):
+        return lib.mg_preprocess_backward_mip(
+            4, 16, 32, 48, sh, 80, 0, 1, 1, 1, 10, 1, vm, 1.0, 1.0, 0.0, 0.0, 8, 8, 0.01,
+            100.0, 0.3, 8.0, cc, 3, 96, None, 0, 3, 1, None, None, None, None, None, None,
+            ctypes.byref(epi), None)
+
+    epi = _lib.AdamEpilogue()
+    for i, ptr in enumerate(ins):
+        epi.p[i], epi.m[i], epi.v[i], epi.lr[i], epi.step[i] = ptr, 1 << 20, 2 << 20, 1e-3, 1
+    epi.beta1, epi.beta2, epi.eps = 0.9, 0.999, 1e-15
+    epi.p[3] = 112
+    assert bwd(epi) == 1 and "tensor 3 is not the kernel's input" in lib.mg_last_error().decode()
+    epi.p[3], epi.p[4] = 96, 68
+    assert bwd(epi, sh=68) == 1 and "16-byte aligned" in lib.mg_last_error().decode()
+    epi.p[4], epi.step[2] = 64, 0
+    assert bwd(epi) == 1 and "step 0 < 1" in lib.mg_last_error().decode()
 
 
 def test_workspace_size_queries_are_pure():

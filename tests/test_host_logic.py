@@ -171,3 +171,20 @@ def test_fused_adam_refuses_cpu_parameters():
     t.grad = torch.ones_like(t)
     with pytest.raises(RuntimeError, match="ROCm"):
         FusedAdam([t]).step()
+
+
+def test_fused_adam_epilogue_refusals_count_no_step():
+    """FusedAdam.epilogue (the projection backward's optimizer epilogue)
+    declines, without advancing any step count, for a tensor that is not one
+    of its parameters, a parameter that already holds a gradient, and
+    parameters off the GPU."""
+    from metal_gauss_amd import FusedAdam
+
+    a = torch.zeros(8, 3, requires_grad=True)
+    b = torch.zeros(8, 4, requires_grad=True)
+    opt = FusedAdam([{"params": [a], "lr": 1e-3}, {"params": [b], "lr": 1e-2}])
+    assert opt.epilogue([a, torch.zeros(8, 4), None]) is None     # not a parameter
+    assert opt.epilogue([a, b, None]) is None                     # CPU parameters
+    b.grad = torch.zeros_like(b)
+    assert opt.epilogue([b, a]) is None                           # gradient already there
+    assert all(not opt.state[t] or opt.state[t]["step"] == 0 for t in (a, b))
