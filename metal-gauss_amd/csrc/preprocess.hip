@@ -636,9 +636,10 @@ struct AdamEpi {
 
 // Cache policy of the epilogue's traffic (bit 0: moment loads, bit 1: moment
 // stores, bit 2: parameter stores non-temporal). Ordinary accesses measured
-// best over the whole step at config 4: non-temporal moment stores cost the
-// kernel about 40 us, while ordinary ones leave dirty lines whose write-back
-// slows the next projection forward by about 30 us.
+// best over the whole config-4 step: every non-temporal combination slowed
+// this kernel by 5 to 50 us, more than it gained in the projection forward
+// that follows (52 to 88 us after this kernel against 55 us after a
+// separate Adam).
 constexpr int kEpiNt = 0;
 constexpr bool kNtLoad = kEpiNt & 1, kNtMom = kEpiNt & 2, kNtPar = kEpiNt & 4;
 
