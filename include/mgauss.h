@@ -161,7 +161,13 @@ typedef struct mg_adam_epilogue {
  * (the forward's), d_scales and d_opacities are the gradients of the log
  * scales and the logits: times exp(log scale), and times (1 - y) y for
  * y = sigmoid(logit), as torch's backward of exp and sigmoid. The reference
- * gets these from torch autograd of the same expressions. With adam
+ * gets these from torch autograd of the same expressions.
+ * reg_opacity and reg_scale (0 for none) add, on every row visible or not,
+ * the gradient of reg_opacity * sum(opacity) + reg_scale * sum(scale) over
+ * all elements of the activated opacities (N,) and scales (N,3): the
+ * trainer's regularisers opac_reg * mean(sigmoid(logit)) + scale_reg *
+ * mean(exp(log_scales)) (metal_gauss/train.py:396-398) are
+ * reg_opacity = opac_reg / N and reg_scale = scale_reg / (3 N). With adam
  * non-NULL the six gradients are not written (d_means .. d_opacities may be
  * NULL): the epilogue above applies them to the parameters in place. */
 int32_t mg_preprocess_backward_mip(
@@ -172,7 +178,8 @@ int32_t mg_preprocess_backward_mip(
     float cy, int32_t W, int32_t H, float near_plane, float far_plane,
     float blur, float max_radius, const float *cam_center, int32_t sh_degree,
     const float *opacities, const float *filter_3d, int32_t antialias,
-    int32_t activations, const float *d_opacity_eff, float *d_means, float *d_quats,
+    int32_t activations, float reg_opacity, float reg_scale,
+    const float *d_opacity_eff, float *d_means, float *d_quats,
     float *d_scales, float *d_sh, float *d_sh_rest, float *d_opacities,
     const mg_adam_epilogue *adam, mg_stream_t stream);
 

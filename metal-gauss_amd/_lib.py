@@ -50,8 +50,8 @@ _SIGNATURES = {
         _vp, _vp]),
     "mg_preprocess_backward_mip": (_i32, [
         _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _f32,
-        _f32, _i32, _i32, _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _i32, _i32, _vp, _vp,
-        _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+        _f32, _i32, _i32, _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _i32, _i32, _f32, _f32,
+        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mg_compute_3d_filter": (_i32, [_i64, _vp, _i32, _vp, _f32, _f32, _vp, _vp, _vp]),
     "mg_add_noise": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _u64, _vp]),
     "mg_mcmc_workspace_bytes": (_i64, [_i64, _i64]),

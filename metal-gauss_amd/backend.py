@@ -32,6 +32,7 @@ import math
 import time
 from pathlib import Path
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -481,13 +482,15 @@ class _PreprocessMip(torch.autograd.Function):
     ``activations`` (bit 0: scales are log scales, bit 1: opacities are
     logits) moves the trainer's torch.exp / torch.sigmoid (train.py:221-222)
     into the same kernels; the gradients then land on the log scales and
-    logits.
+    logits. ``reg`` = (opacity weight, scale weight) adds the gradient of
+    w_o * mean(opacity) + w_s * mean(scale) over the activated values, the
+    trainer's regularisers (train.py:396-398), to every row in the kernel.
     """
 
     @staticmethod
     def forward(ctx, means, quats, scales, opacities, sh, sh_rest, filter_3d, antialias,
                 viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
-                sh_degree, valid_mask=None, activations=0, optimizer=None):
+                sh_degree, valid_mask=None, activations=0, optimizer=None, reg=None):
         lib = _load()
         N = means.shape[0]
         dev = means.device
@@ -530,6 +533,7 @@ class _PreprocessMip(torch.autograd.Function):
         ctx.antialias = bool(antialias)
         ctx.activations = int(activations)
         ctx.optimizer = optimizer
+        ctx.reg = _reg_coefficients(reg, N)
         ctx.meta = (viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
                     sh_degree)
         ctx.mark_non_differentiable(depth, rxy, valid)
@@ -561,9 +565,9 @@ class _PreprocessMip(torch.autograd.Function):
                 p_color, stride, valid.data_ptr(), _lib.host_f32(viewmat), fx, fy, cx, cy, W,
                 H, near, far, blur, max_radius, _lib.host_f32(cam_center), deg,
                 opacities.data_ptr(), None if filt is None else filt.data_ptr(),
-                int(ctx.antialias), ctx.activations, p_oe, None, None, None, None, None, None,
-                ctypes.byref(epi), _lib.stream(means)))
-            return (None,) * 24
+                int(ctx.antialias), ctx.activations, *ctx.reg, p_oe, None, None, None, None,
+                None, None, ctypes.byref(epi), _lib.stream(means)))
+            return (None,) * 25
         d_means = torch.empty(N, 3, device=dev)
         d_quats = torch.empty(N, 4, device=dev)
         d_scales = torch.empty(N, 3, device=dev)
@@ -579,11 +583,22 @@ class _PreprocessMip(torch.autograd.Function):
             _lib.host_f32(viewmat), fx, fy, cx, cy, W, H, near, far, blur, max_radius,
             _lib.host_f32(cam_center), deg, opacities.data_ptr(),
             None if filt is None else filt.data_ptr(), int(ctx.antialias), ctx.activations,
-            p_oe, d_means.data_ptr(), d_quats.data_ptr(),
+            *ctx.reg, p_oe, d_means.data_ptr(), d_quats.data_ptr(),
             d_scales.data_ptr(), None if d_sh is None else d_sh.data_ptr(),
             None if d_rest is None else d_rest.data_ptr(), d_op.data_ptr(), None,
             _lib.stream(means)))
-        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 18
+        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 19
+
+
+def _reg_coefficients(reg, n):
+    """Per-element gradients (reg_opacity, reg_scale) of the regulariser
+    weights (w_o, w_s) on mean(opacity) over n rows and mean(scale) over 3n
+    elements, rounded as torch's float32 mean backward forms them
+    (weight / count)."""
+    if reg is None or n == 0:
+        return (0.0, 0.0)
+    w_o, w_s = (float(np.float32(w)) for w in reg)
+    return (float(np.float32(w_o) / np.float32(n)), float(np.float32(w_s) / np.float32(3 * n)))
 
 
 def _epilogue(ctx, params, sh_degree):
@@ -673,7 +688,8 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
            background=(0.0, 0.0, 0.0), colors=None, max_radius_frac: float = 1.0,
            sh_rest=None, antialias: bool = False, absgrad_out=None,
            min_transmittance: float = DEFAULT_T_MIN, chunked_backward: bool = False,
-           filter_3d=None, activations: bool = False, optimizer=None, **_ignored):
+           filter_3d=None, activations: bool = False, optimizer=None,
+           opacity_reg: float = 0.0, scale_reg: float = 0.0, **_ignored):
     """Render Gaussians from one camera; same signature as the reference's.
 
     means (N,3) world; quats (N,4) wxyz (need not be normalised); scales (N,3)
@@ -696,16 +712,26 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     their derivatives in its backward, so the gradients land on the log
     scales and logits (the same values as torch.exp / torch.sigmoid in
     front of ``render``).
+    ``opacity_reg`` and ``scale_reg`` add the trainer's regularisers
+    opacity_reg * mean(opacity) + scale_reg * mean(scale) of the activated
+    values (with ``activations``: mean(sigmoid(logit)) and
+    mean(exp(log_scales)), train.py:396-398) to the loss this render's
+    backward differentiates: their gradient is added to every row inside the
+    projection backward, and ``info["regularizer"]()`` returns their value
+    (a device scalar) for the loss the caller reports.
     ``optimizer`` (a FusedAdam over these parameters) moves its step for
     means, quats, scales, opacities and the SH into the projection
     backward: the kernel updates the parameters and moments in place, no
     gradient tensors are formed, their ``.grad`` stays unset and the
-    optimizer's ``step()`` skips them. The result equals the backward
-    followed by ``step()`` only when this render is the sole use of those
-    parameters in the loss; otherwise (or when the optimizer or the tensors
-    do not allow it) the ordinary gradients are returned.
+    optimizer's ``step()`` skips them. That equals the backward followed by
+    ``step()`` when this render (with its regularisers) is the only use of
+    those parameters in the loss. Any other use would reach them as a
+    ``.grad`` after their update: ``step()`` then raises instead of updating
+    them a second time. When the optimizer or the tensors do not allow the
+    epilogue, the ordinary gradients are returned.
     """
     explicit_colors = colors is not None
+    opacities_in = opacities
     _require_gpu(means)
     if tile is None:
         tile = 16
@@ -720,7 +746,11 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     # info["valid_mask"], written by the projection kernel itself.
     valid_b = torch.empty(means.shape[0], dtype=torch.bool, device=means.device)
 
-    if filter_3d is not None or antialias or activations or optimizer is not None:
+    reg = None
+    if opacity_reg or scale_reg:
+        reg = (float(opacity_reg), float(scale_reg))
+    if (filter_3d is not None or antialias or activations or optimizer is not None
+            or reg is not None):
         # Both filters (and the activations) in the projection kernel; the
         # compensated opacity is binned too, which gives a tighter, still
         # exact, ellipse bound (metal_backend.py:506-511).
@@ -729,14 +759,14 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
             uv, conic, depth, rxy, valid_i, opacities = _PreprocessMip.apply(
                 means, quats, scales, opacities, None, None, filter_3d, antialias, vm_h, fx,
                 fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree, valid_b,
-                act, None)
+                act, None, reg)
             colors = colors.contiguous()
         else:
             sh_in, rest_in = _sh_inputs(sh, sh_rest)
             uv, conic, depth, rxy, valid_i, colors, opacities = _PreprocessMip.apply(
                 means, quats, scales, opacities, sh_in, rest_in, filter_3d, antialias, vm_h,
                 fx, fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree,
-                valid_b, act, optimizer)
+                valid_b, act, optimizer, reg)
     elif explicit_colors:
         uv, conic, depth, rxy, valid_i = _PreprocessMetal.apply(
             means, quats, scales, None, None, opacities.detach(), vm_h, fx, fy, cx, cy, W, H,
@@ -767,6 +797,9 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     if uv.requires_grad:
         uv.retain_grad()
 
+    info_reg = None
+    if reg is not None:
+        info_reg = _regularizer_value(scales, opacities_in, reg, bool(activations))
     return rgb, alpha, {
         "uv": uv,
         "tiles": int(tile_offsets.numel() - 1),
@@ -775,4 +808,19 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
         "isect_dropped_frac": 0.0,
         "valid_mask": valid_b,
         "backend": "hip",
+        "regularizer": info_reg,
     }
+
+
+def _regularizer_value(scales, opacities, reg, activations):
+    """A callable returning the regularisers' value w_o * mean(opacity) +
+    w_s * mean(scale) (activated values) as a device scalar, computed when
+    called; its gradient is already part of render's backward."""
+    w_o, w_s = reg
+
+    def value():
+        with torch.no_grad():
+            op = torch.sigmoid(opacities) if activations else opacities
+            sc = torch.exp(scales) if activations else scales
+            return w_o * op.mean() + w_s * sc.mean()
+    return value

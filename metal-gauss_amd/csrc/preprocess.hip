@@ -809,6 +809,10 @@ struct PreBwdArgs {
     float *d_op;
     int32_t act;   // kActLogScale | kActLogitOpac (effective-opacity kernel only)
     int32_t stage; // SH rows and their gradients staged through LDS
+    // Regularisers (effective-opacity kernel only): the gradient of
+    // reg_op * sum(opacity) + reg_sc * sum(scale) over every element of the
+    // activated opacities and scales, added to every row (0: none).
+    float reg_op, reg_sc;
     AdamEpi E;     // the optimizer epilogue (EPI kernels)
 };
 
@@ -1004,8 +1008,8 @@ __device__ __forceinline__ void preprocess_bwd_body(const PreBwdArgs &A) {
     if (!in) return;
 
     // ------------------------------------------ projection: lane = Gaussian
-    // The epilogue's gradients of the quats, scales and opacity (zero for a
-    // row that is not visible).
+    // The gradients of the quats, scales and opacity (zero for a row that is
+    // not visible, before the regularisers).
     float gq[4] = {0.f, 0.f, 0.f, 0.f}, gsc[3] = {0.f, 0.f, 0.f}, gop = 0.f;
     if (vld != 0) {
         // s0: the activated scales before the 3D filter; op0: the activated
@@ -1153,22 +1157,15 @@ __device__ __forceinline__ void preprocess_bwd_body(const PreBwdArgs &A) {
             // Through the activations, as torch's backward of exp (grad *
             // result) and of sigmoid (grad * (1 - y) * y).
             if (A.act & kActLogitOpac) dop = dop * (1.0f - op0) * op0;
-            if (EPI) gop = dop;
-            else A.d_op[g] = dop;
+            gop = dop;
             if (A.act & kActLogScale) {
                 dsc[0] = dsc[0] * s0[0];
                 dsc[1] = dsc[1] * s0[1];
                 dsc[2] = dsc[2] * s0[2];
             }
         }
-        if (EPI) {
 #pragma unroll
-            for (int j = 0; j < 3; ++j) gsc[j] = dsc[j];
-        } else {
-            A.d_scales[3 * g] = dsc[0];
-            A.d_scales[3 * g + 1] = dsc[1];
-            A.d_scales[3 * g + 2] = dsc[2];
-        }
+        for (int j = 0; j < 3; ++j) gsc[j] = dsc[j];
         // R(q) for unit q = (w,x,y,z): d/dq of sum G_ij R_ij.
         const float w = P.q[0], x = P.q[1], y = P.q[2], z = P.q[3];
         const float G00 = G[0], G01 = G[1], G02 = G[2], G10 = G[3], G11 = G[4], G12 = G[5],
@@ -1182,28 +1179,38 @@ __device__ __forceinline__ void preprocess_bwd_body(const PreBwdArgs &A) {
         const float iq = 1.0f / fmaxf(P.qn, 1e-12f);
         const float dq[4] = {(dw - w * dotq) * iq, (dxq - x * dotq) * iq,
                              (dyq - y * dotq) * iq, (dzq - z * dotq) * iq};
-        if (EPI) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) gq[j] = dq[j];
-        } else {
-            A.d_quats[4 * g] = dq[0];
-            A.d_quats[4 * g + 1] = dq[1];
-            A.d_quats[4 * g + 2] = dq[2];
-            A.d_quats[4 * g + 3] = dq[3];
+        for (int j = 0; j < 4; ++j) gq[j] = dq[j];
+    }
+    // A row that is not visible keeps zero photometric gradients; with the
+    // epilogue Adam still decays its moments and steps it.
+    if (MIP && (A.reg_op != 0.0f || A.reg_sc != 0.0f)) {
+        // The regularisers' share, on every row: d/dx of reg_op * sigmoid(x)
+        // is reg_op * (1 - y) * y and of reg_sc * exp(x) is reg_sc * exp(x),
+        // as torch's sigmoid and exp backward form them; without the
+        // activations the opacities and scales are the regularised values.
+        float ro = A.reg_op;
+        if (A.act & kActLogitOpac) {
+            const float y = act_sigmoid(A.opac[g]);
+            ro = ro * (1.0f - y) * y;
         }
-    } else if (EPI) {
-        // No gradient (zeros above): Adam still decays the moments and steps
-        // the row.
-    } else {
-        if (MIP) A.d_op[g] = 0.f;
-        A.d_scales[3 * g] = 0.f; A.d_scales[3 * g + 1] = 0.f; A.d_scales[3 * g + 2] = 0.f;
-        A.d_quats[4 * g] = 0.f; A.d_quats[4 * g + 1] = 0.f;
-        A.d_quats[4 * g + 2] = 0.f; A.d_quats[4 * g + 3] = 0.f;
+        gop += ro;
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            gsc[j] += (A.act & kActLogScale) ? A.reg_sc * expf(sraw[j]) : A.reg_sc;
     }
     if (EPI) {
         const float pm[3] = {mx, my, mz};
         epi_rows(A.E, g, pm, qv, sraw, dmean, gq, gsc, gop);
     } else {
+        if (MIP) A.d_op[g] = gop;
+        A.d_scales[3 * g] = gsc[0];
+        A.d_scales[3 * g + 1] = gsc[1];
+        A.d_scales[3 * g + 2] = gsc[2];
+        A.d_quats[4 * g] = gq[0];
+        A.d_quats[4 * g + 1] = gq[1];
+        A.d_quats[4 * g + 2] = gq[2];
+        A.d_quats[4 * g + 3] = gq[3];
         A.d_means[3 * g] = dmean[0];
         A.d_means[3 * g + 1] = dmean[1];
         A.d_means[3 * g + 2] = dmean[2];
@@ -1291,7 +1298,7 @@ static int32_t preprocess_bwd(int64_t N, const float *means, const float *quats,
                               float blur, float max_radius, const float *cam_center,
                               int32_t sh_degree, bool mip,
                               const float *opacities, const float *filter_3d, int32_t antialias,
-                              int32_t activations,
+                              int32_t activations, float reg_opacity, float reg_scale,
                               const float *d_opacity_eff, float *d_means, float *d_quats,
                               float *d_scales, float *d_sh, float *d_sh_rest,
                               float *d_opacities, const mg_adam_epilogue *adam,
@@ -1315,6 +1322,12 @@ static int32_t preprocess_bwd(int64_t N, const float *means, const float *quats,
     MG_REQUIRE((activations & ~(kActLogScale | kActLogitOpac)) == 0 && (mip || activations == 0),
                "%s: activations %d (bit 0: log scales, bit 1: logit opacities)", who,
                activations);
+    MG_REQUIRE(mip || (reg_opacity == 0.0f && reg_scale == 0.0f),
+               "%s: regularisers need the effective-opacity kernel", who);
+    MG_REQUIRE(std::isfinite(reg_opacity) && std::isfinite(reg_scale),
+               "%s: regulariser weights must be finite", who);
+    A.reg_op = reg_opacity;
+    A.reg_sc = reg_scale;
     A.su = grad_stride ? grad_stride : 2;
     A.sk = grad_stride ? grad_stride : 3;
     A.sc = grad_stride ? grad_stride : 3;
@@ -1437,7 +1450,7 @@ int32_t mg_preprocess_backward(int64_t N, const float *means, const float *quats
     return preprocess_bwd(N, means, quats, scales, sh, sh_rest, sh_fused, d_uv, d_conic,
                           d_color, grad_stride, valid, viewmat, fx, fy, cx, cy, W, H, near_plane,
                           far_plane, blur, max_radius, cam_center, sh_degree, false, nullptr,
-                          nullptr, 0, 0,
+                          nullptr, 0, 0, 0.0f, 0.0f,
                           nullptr, d_means, d_quats, d_scales, d_sh, d_sh_rest, nullptr, nullptr,
                           stream, "mg_preprocess_backward");
 }
@@ -1452,7 +1465,7 @@ int32_t mg_preprocess_backward_mip(int64_t N, const float *means, const float *q
                                    float blur, float max_radius, const float *cam_center,
                                    int32_t sh_degree, const float *opacities,
                                    const float *filter_3d, int32_t antialias,
-                                   int32_t activations,
+                                   int32_t activations, float reg_opacity, float reg_scale,
                                    const float *d_opacity_eff, float *d_means, float *d_quats,
                                    float *d_scales, float *d_sh, float *d_sh_rest,
                                    float *d_opacities, const mg_adam_epilogue *adam,
@@ -1460,7 +1473,8 @@ int32_t mg_preprocess_backward_mip(int64_t N, const float *means, const float *q
     return preprocess_bwd(N, means, quats, scales, sh, sh_rest, sh_fused, d_uv, d_conic,
                           d_color, grad_stride, valid, viewmat, fx, fy, cx, cy, W, H,
                           near_plane, far_plane, blur, max_radius, cam_center, sh_degree, true,
-                          opacities, filter_3d, antialias, activations, d_opacity_eff,
+                          opacities, filter_3d, antialias, activations, reg_opacity,
+                          reg_scale, d_opacity_eff,
                           d_means, d_quats, d_scales, d_sh, d_sh_rest, d_opacities, adam,
                           stream, "mg_preprocess_backward_mip");
 }

@@ -24,6 +24,9 @@ _MAX_PER_LAUNCH = 32
 class FusedAdam(torch.optim.Optimizer):
     def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-15):
         super().__init__(params, dict(lr=lr, betas=betas, eps=eps))
+        # Parameters whose update a render(optimizer=) backward has applied
+        # since the last step(), by id.
+        self._epilogue_applied: dict[int, torch.Tensor] = {}
 
     def _state_of(self, p):
         st = self.state[p]
@@ -45,7 +48,11 @@ class FusedAdam(torch.optim.Optimizer):
         rows as float4) also refuse.
 
         ``tensors``: means, quats, scales, opacities, sh, sh_rest (None when
-        the SH is one fused tensor)."""
+        the SH is one fused tensor).
+
+        A parameter this step has already updated (a second render with
+        ``optimizer=`` before ``step()``) raises: a second epilogue would be
+        a second Adam step."""
         owner = {}
         for group in self.param_groups:
             for p in group["params"]:
@@ -59,6 +66,11 @@ class FusedAdam(torch.optim.Optimizer):
             if hit is None:
                 return None
             p, group = hit
+            if id(p) in self._epilogue_applied:
+                raise RuntimeError(
+                    "FusedAdam: render(optimizer=) already applied this step's update to a "
+                    f"parameter of shape {tuple(p.shape)}; call step() after each such render's "
+                    "backward, or render without optimizer= and call step() once")
             if (p.grad is not None or p.device.type != "cuda" or p.dtype != torch.float32
                     or not p.is_contiguous()):
                 return None
@@ -82,6 +94,7 @@ class FusedAdam(torch.optim.Optimizer):
             p, group = hit
             st = self._state_of(p)
             st["step"] += 1
+            self._epilogue_applied[id(p)] = p
             epi.p[i], epi.m[i], epi.v[i] = (p.data_ptr(), st["exp_avg"].data_ptr(),
                                              st["exp_avg_sq"].data_ptr())
             epi.lr[i] = float(group["lr"])
@@ -97,6 +110,15 @@ class FusedAdam(torch.optim.Optimizer):
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
+        applied, self._epilogue_applied = self._epilogue_applied, {}
+        for p in applied.values():
+            if p.grad is not None:
+                raise RuntimeError(
+                    f"FusedAdam.step(): a parameter of shape {tuple(p.shape)} has a gradient, "
+                    "but render(optimizer=) already applied this step's update to it: the "
+                    "loss uses it outside the render (a regulariser, for instance). Pass "
+                    "the trainer's regularisers to render (opacity_reg=, scale_reg=), or "
+                    "render without optimizer=.")
         batches: dict[tuple, list] = {}
         for group in self.param_groups:
             b1, b2 = group["betas"]

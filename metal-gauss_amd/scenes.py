@@ -17,7 +17,8 @@ The five configurations are those of BASELINE.json ``configs``:
   4  1M Gaussians as config 2, 100 cameras on a radius-4 sphere at 800x800
   5  3M Gaussians in a 4x4x4 domain, log-scales N(-5,0.7), logits N(0.5,1.5),
      SH 3, 1920x1080 from inside the cloud at 2.0 from the centre, fov 60 deg
-     (horizontal)
+     (horizontal); config5_crowded adds a dense cluster in front of the
+     camera so that tile lists exceed 10k entries and the keys 30M
 Quaternions are N(0,1)^4 (normalised by the renderer) everywhere.
 """
 
@@ -187,3 +188,28 @@ def config5(n=3_000_000):
     cam = Camera(intrinsics(1920, 1080, 60.0, horizontal=True),
                  look_at((2.0, 0.0, 0.0), (0.0, 0.0, 0.0)), 1920, 1080)
     return s, cam, (0.0, 0.0, 0.0)
+
+
+def config5_crowded(n=3_000_000, n_cluster=600_000):
+    """Config 5 with the stress its text names actually reached: the same
+    scene and camera plus a cluster of ``n_cluster`` Gaussians uniform in a
+    ball of radius 0.2 centred 1.0 in front of the camera (log-scales
+    N(-5, 0.5), logits N(0.5, 1.5), SH as config 2), drawn from seed 44 after
+    the base scene. At the defaults the lists hold about 39M intersections,
+    over a thousand tiles hold more than 10k entries and the longest about
+    23k."""
+    s, cam, bg = config5(n)
+    g = torch.Generator().manual_seed(44)
+    d = torch.randn(n_cluster, 3, generator=g)
+    d = d / d.norm(dim=1, keepdim=True)
+    r = 0.2 * torch.rand(n_cluster, 1, generator=g) ** (1.0 / 3.0)
+    means = torch.tensor([1.0, 0.0, 0.0]) + d * r
+    log_scales = torch.randn(n_cluster, 3, generator=g) * 0.5 - 5.0
+    quats = torch.randn(n_cluster, 4, generator=g)
+    logit = torch.randn(n_cluster, generator=g) * 1.5 + 0.5
+    dc = torch.randn(n_cluster, 1, 3, generator=g) * 0.3
+    rest = torch.randn(n_cluster, 15, 3, generator=g) * 0.05
+    cat = torch.cat
+    return Scene(cat([s.means, means]), cat([s.log_scales, log_scales]), cat([s.quats, quats]),
+                 cat([s.logit_opac, logit]), cat([s.sh_dc, dc]), cat([s.sh_rest, rest]),
+                 3), cam, bg

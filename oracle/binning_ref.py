@@ -25,6 +25,7 @@ Pinned by tests/test_oracle_binning.py:
 from __future__ import annotations
 
 import math
+import os
 
 import numpy as np
 
@@ -68,19 +69,30 @@ def tile_rects(uv, rxy, W, H, tile):
     tf = f32(tile)
     u, v = uv[:, 0].astype(f32), uv[:, 1].astype(f32)
     rx, ry = rxy[:, 0].astype(f32), rxy[:, 1].astype(f32)
-    x0 = np.clip(np.floor((u - rx) / tf).astype(np.int64), 0, tx_n - 1)
-    x1 = np.clip(np.floor((u + rx) / tf).astype(np.int64), 0, tx_n - 1)
-    y0 = np.clip(np.floor((v - ry) / tf).astype(np.int64), 0, ty_n - 1)
-    y1 = np.clip(np.floor((v + ry) / tf).astype(np.int64), 0, ty_n - 1)
+    # Gaussians that are not valid may carry non-finite extents; their
+    # rectangles are never used.
+    with np.errstate(invalid="ignore"):
+        x0 = np.clip(np.floor((u - rx) / tf).astype(np.int64), 0, tx_n - 1)
+        x1 = np.clip(np.floor((u + rx) / tf).astype(np.int64), 0, tx_n - 1)
+        y0 = np.clip(np.floor((v - ry) / tf).astype(np.int64), 0, ty_n - 1)
+        y1 = np.clip(np.floor((v + ry) / tf).astype(np.int64), 0, ty_n - 1)
     return x0, x1, y0, y1, tx_n, ty_n
 
 
-def emit_pairs(uv, rxy, conic, opacity, valid, depth, W, H, tile, ellipse=True):
+# Candidate (Gaussian, tile) tests per chunk of Gaussians: large scenes are
+# cut into chunks of whole Gaussians so the temporaries stay small, and the
+# chunks run on a thread pool (numpy releases the GIL inside its loops).
+_CHUNK_PAIRS = 1 << 21
+
+
+def emit_pairs(uv, rxy, conic, opacity, valid, depth, W, H, tile, ellipse=True, workers=None):
     """All surviving (Gaussian, tile) pairs in emission order.
 
     Returns (keys uint64, ids int32, counts int32 per Gaussian). With
     ``ellipse`` False (no conic), every tile of the rectangle is kept, the
-    circular-bounds contract of metal_backend.py:111-147.
+    circular-bounds contract of metal_backend.py:111-147. Gaussians are
+    processed in chunks, concatenated in Gaussian order, so the result does
+    not depend on the chunking.
     """
     N = uv.shape[0]
     x0, x1, y0, y1, tx_n, _ = tile_rects(uv, rxy, W, H, tile)
@@ -90,8 +102,36 @@ def emit_pairs(uv, rxy, conic, opacity, valid, depth, W, H, tile, ellipse=True):
     if ellipse:
         thr, live = level_threshold(opacity)
         per = np.where(live, per, 0)
+    cum = np.cumsum(per)
+    bounds = [0]
+    while bounds[-1] < N:
+        base = int(cum[bounds[-1] - 1]) if bounds[-1] else 0
+        nxt = int(np.searchsorted(cum, base + _CHUNK_PAIRS, side="right"))
+        bounds.append(min(N, max(nxt, bounds[-1] + 1)))
+    spans = list(zip(bounds[:-1], bounds[1:]))
+
+    def run(span):
+        a, b = span
+        return _emit_span(a, b, uv, conic, depth, x0, y0, nx, per, thr, ellipse, W, H, tile,
+                          tx_n)
+
+    if len(spans) > 1:
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(max_workers=workers or min(16, os.cpu_count() or 1)) as ex:
+            parts = list(ex.map(run, spans))
+    else:
+        parts = [run(s) for s in spans]
+    keys = np.concatenate([k for k, _ in parts]) if parts else np.zeros(0, np.uint64)
+    owner = np.concatenate([o for _, o in parts]) if parts else np.zeros(0, np.int64)
+    counts = np.bincount(owner, minlength=N).astype(np.int32)
+    return keys, owner.astype(np.int32), counts
+
+
+def _emit_span(a, b, uv, conic, depth, x0, y0, nx, per, thr, ellipse, W, H, tile, tx_n):
+    """Pairs of Gaussians a..b-1, in emission order: (keys, owner int64)."""
+    per = per[a:b]
     total = int(per.sum())
-    owner = np.repeat(np.arange(N, dtype=np.int64), per)
+    owner = np.repeat(np.arange(a, b, dtype=np.int64), per)
     k = np.arange(total, dtype=np.int64) - np.repeat(np.cumsum(per) - per, per)
     ty = y0[owner] + k // nx[owner]
     tx = x0[owner] + k % nx[owner]
@@ -105,11 +145,9 @@ def emit_pairs(uv, rxy, conic, opacity, valid, depth, W, H, tile, ellipse=True):
                              conic[owner, 2], X0, X1, Y0, Y1)
         keep = mq < thr[owner]
     owner, tx, ty = owner[keep], tx[keep], ty[keep]
-    counts = np.bincount(owner, minlength=N).astype(np.int32)
     tid = (ty * tx_n + tx).astype(np.uint64)
     dbits = depth.astype(f32).view(np.uint32).astype(np.uint64)[owner]
-    keys = (tid << np.uint64(32)) | dbits
-    return keys, owner.astype(np.int32), counts
+    return (tid << np.uint64(32)) | dbits, owner
 
 
 def sort_pairs(keys, ids):

@@ -108,8 +108,8 @@ def test_bad_arguments_fail_before_any_launch():
     def bwd(epi, sh=64):
         return lib.mg_preprocess_backward_mip(
             4, 16, 32, 48, sh, 80, 0, 1, 1, 1, 10, 1, vm, 1.0, 1.0, 0.0, 0.0, 8, 8, 0.01,
-            100.0, 0.3, 8.0, cc, 3, 96, None, 0, 3, 1, None, None, None, None, None, None,
-            ctypes.byref(epi), None)
+            100.0, 0.3, 8.0, cc, 3, 96, None, 0, 3, 0.0, 0.0, 1, None, None, None, None,
+            None, None, ctypes.byref(epi), None)
 
     epi = _lib.AdamEpilogue()
     for i, ptr in enumerate(ins):
