@@ -35,6 +35,8 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "train steps/sec & fwd+bwd ms at 1M Gaussians 800×800 SH3; % HBM roofline"
 HBM_PEAK_GBS = 8000.0
+# Opacity and scale regulariser weights of the reference's step.
+REG = 0.01
 
 # Kernels timed by the library (names used in mg_timing_query).
 KERNELS = ["preprocess_forward", "bin_count", "exclusive_scan", "bin_write", "tile_sort",
@@ -76,6 +78,11 @@ def parse():
                          "(render(filter_3d=, antialias=True)); mip-torch: the same step with "
                          "the activations and the 3D filter applied as the reference's torch "
                          "reparameterisation (apply_3d_filter, train.py:223-227) before render")
+    ap.add_argument("--reg", action="store_true",
+                    help="add the reference trainer's opacity and scale regularisers, "
+                         "0.01 mean sigmoid(logit) + 0.01 mean exp(log_scales) "
+                         "(bench/step_profile.py:101-102), to the configuration's loss "
+                         "0.8 L1 + 0.2 (1 - SSIM)")
     ap.add_argument("--cpu-only", action="store_true", help="time only the CPU baseline")
     ap.add_argument("--config", type=int, choices=[1, 2, 3, 5], default=None,
                     help="time another BASELINE configuration instead of the config-4 step: "
@@ -116,7 +123,7 @@ def copy_calibration(mib):
 class Step:
     """The config-4 training step on the GPU."""
 
-    def __init__(self, n, dev, variant="base"):
+    def __init__(self, n, dev, variant="base", reg=False):
         import torch
 
         from metal_gauss_amd import FusedAdam, gaussian_kernel, scenes
@@ -142,6 +149,7 @@ class Step:
         self.k = 0
         self.last_isect = 0
         self.variant = variant
+        self.reg = reg
         self.f3d = None
         self.f3d_ms = None
         if variant in ("mip", "mip-torch"):
@@ -180,25 +188,43 @@ class Step:
         # With adam, "base" and "mip" run FusedAdam's update inside the
         # projection backward (render(optimizer=)); the other variants, and
         # "unfused-adam", take it as a separate launch after the backward.
+        # With reg, the reference trainer's opacity and scale regularisers,
+        # 0.01 mean(sigmoid(logit)) + 0.01 mean(exp(log_scales))
+        # (bench/step_profile.py:101-102, train.py:396-398 with the defaults
+        # at 733-734), join the configuration's loss: inside the projection
+        # backward for "base" and "mip" (render(opacity_reg=, scale_reg=)),
+        # in torch for the others.
+        reg = dict(opacity_reg=REG, scale_reg=REG) if self.reg else {}
         scales, opac = p["log_scales"], p["logit_opac"]
         epi = self.opt if adam else None
-        kw = dict(activations=True, optimizer=epi)
+        kw = dict(activations=True, optimizer=epi, **reg)
+        torch_reg = False
         if self.variant == "unfused-adam":
             kw = dict(activations=True)
+            torch_reg = self.reg
         elif self.variant == "mip":
-            kw = dict(filter_3d=self.f3d, antialias=True, activations=True, optimizer=epi)
+            kw = dict(filter_3d=self.f3d, antialias=True, activations=True, optimizer=epi, **reg)
         elif self.variant == "torch-act":
             scales, opac = torch.exp(scales), torch.sigmoid(opac)
             kw = {}
+            torch_reg = self.reg
         elif self.variant == "mip-torch":
             from metal_gauss_amd import apply_3d_filter
             scales, opac = apply_3d_filter(torch.exp(scales), torch.sigmoid(opac), self.f3d)
             kw = dict(antialias=True)
+            torch_reg = self.reg
         rgb, alpha, info = render(p["means"], p["quats"], scales, opac, p["sh_dc"], cam.K,
                                   cam.viewmat, cam.W, cam.H, sh_degree=3, sh_rest=p["sh_rest"],
                                   background=self.bg, **kw)
         # 0.8 * |rgb - gt|.mean() + 0.2 * (1 - ssim(rgb, gt)) (train.py:389-390), fused.
         loss, _ = photometric_loss(rgb, gt, self.window, 0.2)
+        if torch_reg:
+            loss = loss + REG * torch.sigmoid(p["logit_opac"]).mean() \
+                + REG * torch.exp(p["log_scales"]).mean()
+        elif info["regularizer"] is not None:
+            # The loss value the trainer reports; the regularisers' gradient
+            # is already in render's backward.
+            loss = loss + info["regularizer"]()
         self.opt.zero_grad(set_to_none=True)
         loss.backward()
         if adam:
@@ -239,7 +265,7 @@ def gpu_bench(args):
     from metal_gauss_amd import _lib
 
     dev = torch.device("cuda:0")
-    step = Step(args.gaussians, dev, args.variant)
+    step = Step(args.gaussians, dev, args.variant, reg=args.reg)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -909,7 +935,9 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": ("config 4: 1M Gaussians SH3, 800x800, 100 seeded views, "
-                         "fwd + bwd + FusedAdam, loss 0.8 L1 + 0.2 (1-SSIM)"),
+                         "fwd + bwd + FusedAdam, loss 0.8 L1 + 0.2 (1-SSIM)"
+                         + (" + 0.01 mean sigmoid(logit) + 0.01 mean exp(log scale)"
+                            if args.reg else "")),
             "n_gaussians": args.gaussians, "width": 800, "height": 800, "sh_degree": 3,
             "tile": 16, "mean_intersections": int(r["I"]),
             "valid_fraction": round(r["f_valid"], 4),

@@ -284,11 +284,11 @@ def test_step_refuses_a_second_update_after_the_epilogue(dev):
     assert all(opt.state[t]["step"] == 1 for t in p.values())
 
     opt.zero_grad(set_to_none=True)
-    for _ in range(2):
+    for it in range(2):
         rgb, _, _ = render(p["means"], p["quats"], p["log_scales"], p["logits"], p["sh_dc"], K,
                            vm, W, H, sh_degree=3, sh_rest=p["sh_rest"], activations=True,
                            optimizer=opt)
-        if _ == 0:
+        if it == 0:
             rgb.square().mean().backward()
         else:
             with pytest.raises(RuntimeError, match="already applied this step's update"):

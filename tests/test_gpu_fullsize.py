@@ -103,42 +103,56 @@ def _subsample(n, seed):
     return torch.randperm(n, generator=g)[:SUB].sort().values
 
 
-def _reference_rows(sc, idx, cam):
-    """float64 leaves of the subsample and render_ref.preprocess on them,
+def _reference_rows(sc, idx, cam, dtype=torch.float64):
+    """Leaves of the subsample in ``dtype`` and render_ref.preprocess on them,
     with the trainer's exp / sigmoid in front (train.py:221-222)."""
-    leaves = {k: t[idx].double().clone().requires_grad_(True) for k, t in
+    leaves = {k: t[idx].to(dtype).clone().requires_grad_(True) for k, t in
               (("means", sc.means), ("quats", sc.quats), ("log_scales", sc.log_scales),
                ("logits", sc.logit_opac), ("sh_dc", sc.sh_dc), ("sh_rest", sc.sh_rest))}
-    K = cam.K.double()
+    K = cam.K.to(dtype)
     op = torch.sigmoid(leaves["logits"])
     sh = torch.cat([leaves["sh_dc"], leaves["sh_rest"]], dim=1)
     out = render_ref.preprocess(leaves["means"], leaves["quats"], torch.exp(leaves["log_scales"]),
-                                op, sh, cam.viewmat.double(), float(K[0, 0]), float(K[1, 1]),
+                                op, sh, cam.viewmat.to(dtype), float(K[0, 0]), float(K[1, 1]),
                                 float(K[0, 2]), float(K[1, 2]), cam.W, cam.H)
     return leaves, out, op
 
 
-def _projection_parity(sc, cam, outs, idx, rec):
+def _tol(a, b):
+    """Largest relative error, the denominator floored at 1% of the tensor's
+    largest magnitude: u = fx px / z + cx near 0 cancels two terms of ~W/2,
+    so float32 holds it only to about one ulp of W/2."""
+    b = b.detach()
+    floor = 1e-2 * float(b.abs().max())
+    return float(((a.detach().cpu().double() - b).abs() / (b.abs() + floor)).max())
+
+
+def _projection_parity(sc, cam, outs, idx, rec, label):
     """Forward outputs of the subsample rows against float64 render_ref, and
     the backward's gradients with the rasteriser's gradients of those rows
-    (rows visible on both sides) against float64 autograd."""
+    (rows visible on both sides) against float64 autograd.
+
+    Each bar is the larger of a fixed tolerance and twice the error of the
+    same restatement evaluated in float32 on the CPU: heavy-tailed scales
+    (config 5) give near rank-1 covariances whose conic loses digits to the
+    a c - b^2 cancellation in any float32 evaluation; the kernel must be as
+    accurate as float32 arithmetic of the reference's formulas allows."""
     uv, conic, depth, rxy, valid, color, op_eff = outs
     leaves, (ruv, rconic, rdepth, rrxy, rvalid, rcolor), rop = _reference_rows(sc, idx, cam)
+    l32, (fuv, fconic, fdepth, frxy, _, fcolor), fop = _reference_rows(sc, idx, cam,
+                                                                        torch.float32)
     dev = uv.device
     gi = idx.to(dev)
     gv = _np(valid[gi]) != 0
     agree = gv == rvalid.numpy()
     assert agree.mean() > 0.999, f"{(~agree).sum()} validity flips of {SUB}"
     both = torch.from_numpy(agree & gv)
-
-    def tol(a, b):
-        b = b.detach()
-        floor = 1e-3 * float(b.abs().max())
-        return float(((a.detach().cpu().double() - b).abs() / (b.abs() + floor)).max())
-    assert tol(uv[gi][both], ruv[both]) < 1e-5
-    assert tol(conic[gi][both], rconic[both]) < 1e-4
-    assert tol(depth[gi][both], rdepth[both]) < 1e-6
-    assert tol(rxy[gi][both], rrxy[both]) < 1e-4
+    for name, a, f, b, bar in (("uv", uv, fuv, ruv, 1e-5), ("conic", conic, fconic, rconic, 1e-4),
+                               ("depth", depth, fdepth, rdepth, 1e-6),
+                               ("rxy", rxy, frxy, rrxy, 1e-4)):
+        got, f32 = _tol(a[gi][both], b[both]), _tol(f[both], b[both])
+        print(f"{label} {name}: GPU {got:.2e}, CPU float32 {f32:.2e}", flush=True)
+        assert got < max(bar, 2.0 * f32), f"{name}: {got:.2e} (float32 CPU {f32:.2e})"
     assert float((color[gi][both].cpu().double() - rcolor[both].detach()).abs().max()) < 1e-5
     assert float((op_eff[gi].cpu().double() - rop.detach()).abs().max()) < 1e-6
 
@@ -148,15 +162,15 @@ def _projection_parity(sc, cam, outs, idx, rec):
     g_conic = rec[1][gi].cpu().double() * m[:, None]
     g_op = rec[2][gi].cpu().double() * m
     g_col = rec[3][gi].cpu().double() * m[:, None]
-    torch.autograd.backward([ruv, rconic, rcolor, rop], [g_uv, g_conic, g_col, g_op])
-    return leaves, (g_uv, g_conic, g_col, g_op), both
+    grads = (g_uv, g_conic, g_col, g_op)
+    torch.autograd.backward([ruv, rconic, rcolor, rop], list(grads))
+    torch.autograd.backward([fuv, fconic, fcolor, fop], [g.float() for g in grads])
+    return leaves, l32, grads, both
 
 
 def _gpu_projection_grads(sc, cam, idx, grads, dev):
     """The product's projection backward on the subsample rows with the same
     incoming gradients (the kernel treats every row on its own)."""
-    from metal_gauss_amd import backend
-
     p = {k: t[idx].to(dev).clone().requires_grad_(True) for k, t in
          (("means", sc.means), ("quats", sc.quats), ("log_scales", sc.log_scales),
           ("logits", sc.logit_opac), ("sh_dc", sc.sh_dc), ("sh_rest", sc.sh_rest))}
@@ -166,14 +180,27 @@ def _gpu_projection_grads(sc, cam, idx, grads, dev):
     return p
 
 
-def _check_projection_grads(p, leaves, both):
+def _check_projection_grads(p, leaves, l32, both, label):
+    """Relative L2 of every parameter gradient against float64 autograd:
+    below 1e-4, or twice the float32 restatement's own error."""
+    # Rows visible on both sides (the others get no incoming gradient; the
+    # float32 restatement's overflowing covariances of huge invisible splats
+    # give 0 * inf = nan there).
     for k in ("means", "quats", "log_scales", "logits", "sh_dc", "sh_rest"):
-        a = p[k].grad.detach().cpu().double()
-        b = leaves[k].grad
-        assert rel_l2(a, b) < 1e-4, f"{k}: rel L2 {rel_l2(a, b):.2e}"
+        a = p[k].grad.detach().cpu().double()[both]
+        b = leaves[k].grad[both]
+        got, f32 = rel_l2(a, b), rel_l2(l32[k].grad[both], b)
+        print(f"{label} d_{k}: GPU {got:.2e}, CPU float32 {f32:.2e}", flush=True)
+        assert got < max(1e-4, 2.0 * f32), f"{k}: rel L2 {got:.2e} (float32 CPU {f32:.2e})"
     inv = ~both
     if inv.any():
         assert float(p["quats"].grad[inv.to(p["quats"].device)].abs().max()) == 0.0
+
+
+def _projection_check(sc, cam, outs, idx, rec, dev, label):
+    leaves, l32, grads, both = _projection_parity(sc, cam, outs, idx, rec, label)
+    _check_projection_grads(_gpu_projection_grads(sc, cam, idx, grads, dev), leaves, l32, both,
+                            label)
 
 
 # ------------------------------------------------------------------ config 4
@@ -203,9 +230,8 @@ def test_config4_step_parity(dev, view):
     grad_rgb = rgb0.grad.contiguous()
     _, rec = _raster_parity(args, W, H, grad_rgb, None)
 
-    idx = _subsample(sc.n, 400 + view)
-    leaves, grads, both = _projection_parity(sc, cam, outs, idx, rec)
-    _check_projection_grads(_gpu_projection_grads(sc, cam, idx, grads, dev), leaves, both)
+    _projection_check(sc, cam, outs, _subsample(sc.n, 400 + view), rec, dev,
+                      f"config 4 view {view}")
 
 
 def test_config4_epilogue_equals_backward_then_step_at_full_size(dev):
@@ -322,9 +348,7 @@ def test_config5_parity(dev, crowded):
     grad_rgb = torch.randn(H, W, 3, device=dev, generator=g) / (H * W)
     grad_alpha = torch.randn(H, W, device=dev, generator=g) / (H * W)
     _, rec = _raster_parity(args, W, H, grad_rgb, grad_alpha)
-    idx = _subsample(sc.n, 500 + int(crowded))
-    leaves, grads, both = _projection_parity(sc, cam, outs, idx, rec)
-    _check_projection_grads(_gpu_projection_grads(sc, cam, idx, grads, dev), leaves, both)
+    _projection_check(sc, cam, outs, _subsample(sc.n, 500 + int(crowded)), rec, dev, label)
 
 
 # ------------------------------------------------------------------ config 3
