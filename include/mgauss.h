@@ -531,6 +531,18 @@ int32_t mg_photometric_loss_forward(const float *x, const float *y,
                                     float *out, void *workspace,
                                     int64_t workspace_bytes,
                                     mg_stream_t stream);
+/* mg_photometric_loss_forward without a workspace argument: the block sums
+ * live in a static device array of the library (2 MiB per GPU, held until
+ * the process ends), so the call allocates nothing and takes no scratch from
+ * the caller. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops). Limit: 2^18 blocks of 32x16 pixels and one colour, e.g. an image
+ * of 8192x5440; larger ones are refused with MG_ERR_ARG. The array keeps
+ * the last call's contents; calls that overlap on one GPU race on it. */
+int32_t mg_photometric_loss_forward_noalloc(const float *x, const float *y,
+                                            const float *w, int32_t H, int32_t W,
+                                            float ssim_weight, float *partials,
+                                            float *out, mg_stream_t stream);
 int32_t mg_photometric_loss_backward(const float *x, const float *y,
                                      const float *w, const float *partials,
                                      const float *grad_dev, int32_t H,

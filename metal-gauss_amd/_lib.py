@@ -103,6 +103,8 @@ _SIGNATURES = {
     "mg_ssim_fused_backward": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "mg_photometric_loss_forward": (_i32, [_vp, _vp, _vp, _i32, _i32, _f32, _vp, _vp, _vp, _i64,
                                            _vp]),
+    "mg_photometric_loss_forward_noalloc": (_i32, [_vp, _vp, _vp, _i32, _i32, _f32, _vp, _vp,
+                                                   _vp]),
     "mg_photometric_loss_backward": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp,
                                             _vp]),
 }

@@ -16,6 +16,10 @@ void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 // After a launch: maps hipGetLastError to MG_ERR_LAUNCH with the kernel name.
 int32_t check_launch(const char *kernel);
 
+// Device address, on the current device, of the static scratch array of the
+// allocation-free loss entry point (looked up once per device).
+int32_t static_scratch(float **out, const char *who);
+
 // Event timing around one launch (active only while mg_timing_enable(1)).
 struct TimedScope {
     TimedScope(const char *kernel, hipStream_t stream);

@@ -166,7 +166,9 @@ int32_t mg_init(void) {
                       hipGetErrorString(e));
         return MG_ERR_RUNTIME;
     }
-    return MG_OK;
+    // The allocation-free entry point's scratch address on this device.
+    float *scratch = nullptr;
+    return mg::static_scratch(&scratch, "mg_init");
 }
 
 int32_t mg_max_tile(void) { return 32; }

@@ -14,6 +14,8 @@
 //     chain.
 // Math: S = (2 mx my + C1)(2 sxy + C2) / ((mx^2 + my^2 + C1)(sxx + syy + C2))
 // (metal_gauss/ssim.py:54-108).
+#include <mutex>
+
 #include "mg_common.h"
 
 namespace mg {
@@ -355,6 +357,67 @@ inline int64_t ssim_blocks(int H, int W) {
     return ceil_div(W, kTW) * ceil_div(H, kTH) * 3;
 }
 
+// ------------------------------------------------ allocation-free variant
+// mg_photometric_loss_forward_noalloc keeps the loss forward's block sums in
+// this file-scope device array instead of a caller workspace, for callers
+// that cannot allocate device memory (graph capture, serving loops). Every
+// GPU the library runs on holds its own copy until the process ends; calls
+// that overlap on one GPU share it and race.
+constexpr int64_t kStaticLossBlocks = int64_t(1) << 18;   // SSIM + L1 sums: 2 MiB
+static __device__ __align__(256) float scratch[2 * kStaticLossBlocks];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static float *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per
+// device with that device current. Host code passes this address to kernels;
+// the array's name is only a host-side stand-in.
+int32_t static_scratch(float **out, const char *who) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        set_error("%s: hipGetDevice failed: %s", who, hipGetErrorString(e));
+        return MG_ERR_RUNTIME;
+    }
+    MG_REQUIRE(dev >= 0 && dev < kMaxDevices, "%s: device %d beyond the %d supported", who, dev,
+               kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr) {
+            set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev,
+                      hipGetErrorString(e));
+            return MG_ERR_RUNTIME;
+        }
+        g_scratch_ptr[dev] = static_cast<float *>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return MG_OK;
+}
+
+// The trainer's loss forward on `sums` (2 * ssim_blocks(H, W) floats): the
+// fused SSIM pass writes every block's SSIM and L1 sums (each block its own
+// entries, so nothing needs clearing), then one workgroup reduces them.
+static int32_t photometric_forward(const float *x, const float *y, const float *w, int32_t H,
+                                   int32_t W, float ssim_weight, float *partials, float *out,
+                                   float *sums, mg_stream_t stream, const char *who) {
+    MG_REQUIRE(ssim_weight >= 0.0f && ssim_weight <= 1.0f, "%s: ssim_weight %g outside [0, 1]",
+               who, (double)ssim_weight);
+    hipStream_t s = as_stream(stream);
+    const int tiles_x = (int)ceil_div(W, kTW);
+    const int64_t nb = ssim_blocks(H, W);
+    const unsigned grid = (unsigned)nb;
+    TimedScope ts("ssim_fused_forward", s);
+    ssim_fused_fwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, H, W, tiles_x, partials, sums,
+                                                        sums + nb);
+    MG_LAUNCHED("ssim_fused_fwd_kernel");
+    photometric_loss_kernel<<<1, 256, 0, s>>>(sums, sums + nb, nb, 3LL * H * W, ssim_weight, out);
+    MG_LAUNCHED("photometric_loss_kernel");
+    return MG_OK;
+}
+
 }  // namespace mg
 
 using namespace mg;
@@ -460,23 +523,27 @@ int32_t mg_photometric_loss_forward(const float *x, const float *y, const float 
                                     mg_stream_t stream) {
     MG_REQUIRE(H > 0 && W > 0 && x && y && w && partials && out,
                "mg_photometric_loss_forward: bad arguments");
-    MG_REQUIRE(ssim_weight >= 0.0f && ssim_weight <= 1.0f,
-               "mg_photometric_loss_forward: ssim_weight %g outside [0, 1]", (double)ssim_weight);
     MG_REQUIRE(workspace && workspace_bytes >= mg_ssim_fused_workspace_bytes(H, W),
                "mg_photometric_loss_forward: workspace %lld bytes, need %lld",
                (long long)workspace_bytes, (long long)mg_ssim_fused_workspace_bytes(H, W));
-    hipStream_t s = as_stream(stream);
-    const int tiles_x = (int)ceil_div(W, kTW);
-    const int64_t nb = ssim_blocks(H, W);
-    const unsigned grid = (unsigned)nb;
-    float *sums = static_cast<float *>(workspace);
-    TimedScope ts("ssim_fused_forward", s);
-    ssim_fused_fwd_kernel<<<grid, kSsimThreads, 0, s>>>(x, y, w, H, W, tiles_x, partials, sums,
-                                                        sums + nb);
-    MG_LAUNCHED("ssim_fused_fwd_kernel");
-    photometric_loss_kernel<<<1, 256, 0, s>>>(sums, sums + nb, nb, 3LL * H * W, ssim_weight, out);
-    MG_LAUNCHED("photometric_loss_kernel");
-    return MG_OK;
+    return photometric_forward(x, y, w, H, W, ssim_weight, partials, out,
+                               static_cast<float *>(workspace), stream,
+                               "mg_photometric_loss_forward");
+}
+
+int32_t mg_photometric_loss_forward_noalloc(const float *x, const float *y, const float *w,
+                                            int32_t H, int32_t W, float ssim_weight,
+                                            float *partials, float *out, mg_stream_t stream) {
+    const char *who = "mg_photometric_loss_forward_noalloc";
+    MG_REQUIRE(H > 0 && W > 0 && x && y && w && partials && out, "%s: bad arguments", who);
+    MG_REQUIRE(ssim_blocks(H, W) <= kStaticLossBlocks,
+               "%s: a %dx%d image needs %lld block sums (3 per 32x16-pixel tile), more "
+               "than the %lld the static scratch holds",
+               who, H, W, (long long)ssim_blocks(H, W), (long long)kStaticLossBlocks);
+    float *sums = nullptr;
+    const int32_t rc = static_scratch(&sums, who);
+    if (rc != MG_OK) return rc;
+    return photometric_forward(x, y, w, H, W, ssim_weight, partials, out, sums, stream, who);
 }
 
 int32_t mg_photometric_loss_backward(const float *x, const float *y, const float *w,
