@@ -8,8 +8,8 @@ to this module:
   background blend; returns (rgb (H,W,3), alpha (H,W), info);
 * ``build_tile_lists`` (metal_backend.py:111-214) and
   ``build_tile_lists_metal`` (metal_backend.py:217-285) - tile lists, here both
-  on the GPU: count, scan, key emission, radix sort and tile ranges are all
-  HIP kernels (the reference keeps argsort/cumsum/searchsorted in torch);
+  on the GPU: count, scan, pair emission and the stable tile and depth sorts
+  are HIP kernels (the reference keeps argsort/cumsum/searchsorted in torch);
 * ``_PreprocessMetal`` / ``_RasterizeMetal`` (metal_backend.py:288-364) - the
   autograd bridges, under the same names;
 * ``antialias_scale`` (metal_backend.py:367-393), ``_load`` (76-108) and
@@ -101,14 +101,15 @@ def _empty_lists(n_tiles: int, tx: int, device):
 
 
 def _bin(uv, rxy, depth, valid_i, conic, opacity, W, H, tile):
-    """Tile lists on the GPU, depth-first (mg_bin_lists_begin / _finish).
+    """Tile lists on the GPU (mg_bin_lists_begin / _finish).
 
-    Counts with the exact ellipse test, one 32-bit radix sort of the
-    Gaussians by depth, the scan in that order, then emission in depth order
-    and a stable sort of the pairs by tile id alone. Returns (gauss_ids,
-    tile_offsets, tiles_x). One device->host read per call: the intersection
-    total that sizes the pair buffers (the reference's .item(),
-    metal_backend.py:247-248).
+    Per-Gaussian counts with the exact ellipse test and their scan, then the
+    (tile, Gaussian) pairs emitted in Gaussian order, a stable counting sort
+    of the pairs by tile (radix passes past 4096 tiles) and a stable sort of
+    every tile's list by depth: the order of a stable sort of the
+    (tile << 32 | depth bits) keys. Returns (gauss_ids, tile_offsets,
+    tiles_x). One device->host read per call: the intersection total that
+    sizes the pair buffers (the reference's .item(), metal_backend.py:247-248).
     """
     lib = _load()
     device = uv.device
@@ -214,7 +215,7 @@ def build_tile_lists_metal(uv, rxy, depth, valid, conic, opacity, W, H, tile,
 
     Returns (gauss_ids int32 sorted by (tile, depth), tile_offsets int32
     (n_tiles+1), tiles_x). Equal keys keep emission order (Gaussian, row,
-    column): the radix sort is stable.
+    column): both sorts are stable.
     """
     _require_gpu(uv)
     valid_i = valid.to(torch.int32).contiguous()

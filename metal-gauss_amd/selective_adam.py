@@ -30,7 +30,8 @@ _MAX_PER_LAUNCH = 32
 
 
 class SelectiveAdam(torch.optim.Optimizer):
-    """Adam with per-row updates for Gaussian parameters."""
+    """Row-masked Adam: each Gaussian row steps only when visible, with its own
+    step count; groups marked ``rowwise=False`` take ordinary dense Adam."""
 
     def __init__(self, groups: list[dict], eps: float = 1e-15,
                  betas: tuple[float, float] = (0.9, 0.999)):
@@ -67,7 +68,8 @@ class SelectiveAdam(torch.optim.Optimizer):
 
     @torch.no_grad()
     def step(self, visible: torch.Tensor, closure=None):
-        """Update visible Gaussian rows and any dense auxiliary groups."""
+        """One step: rows with ``visible`` set in the row-wise groups (one
+        launch for all of them), every element of the dense groups."""
         loss = None
         if closure is not None:
             with torch.enable_grad():

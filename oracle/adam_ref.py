@@ -1,8 +1,16 @@
 """numpy restatement of the two Adam updates. TEST INFRASTRUCTURE ONLY.
 
-adam_step: metal_gauss/csrc/adam.metal:34-41 with the bias corrections formed
-in double on the host (rasterize.mm:338-342): torch.optim.Adam's formula, eps
-added after the sqrt(bias_correction2) divide.
+adam_step: torch.optim.Adam's update, the oracle of the reference's own
+FusedAdam test (tests/test_fused_adam.py:21-38), in the arrangement of
+metal_gauss/csrc/adam.metal:34-41 (eps added after the sqrt(bias_correction2)
+divide, bias corrections formed in double on the host, rasterize.mm:338-342).
+One rounding follows torch rather than that kernel, deliberately: the moment
+weights are (1 - beta) rounded from double, as torch's lerp weight and
+addcmul value, where adam.metal takes 1 - fp32(beta) in fp32. For beta2 =
+0.999 the two weights differ by 1.3e-5 relative (beta1 = 0.9: 2.4e-7), so
+exp_avg_sq settles about 1.3e-5 above the reference kernel's and each update
+differs by about 6.5e-6 of its own size (far below the parameters' 1e-6
+relative bar); the reference's test holds its kernel to torch at 1e-5.
 
 selective_adam_step: metal_gauss/selective_adam.py:116-149 (_step_indexed):
 rows with visible[r] get steps[r] += 1 and
@@ -12,7 +20,7 @@ rows past the mask are untouched.
 dense_eps_inside_step: selective_adam.py:189-206, ordinary Adam with a scalar
 step and eps inside the root (the auxiliary, non-rowwise groups).
 
-Pinned by tests/test_oracle_adam.py: the closed form of step 1
+Pinned by tests/test_oracle_adam_ssim_raster.py: the closed form of step 1
 (dp = -lr g / (|g| + eps)), torch.optim.Adam over 30 and 101 steps, and a
 float64 per-row brute force (each row runs plain Adam on exactly the steps
 where it was visible, with its own step count).

@@ -17,7 +17,7 @@
  * fused multiply-adds), so the only differences to the GPU are the exp
  * implementation and the order of the per-Gaussian gradient sums.
  *
- * Pinned by tests/test_oracle_raster.py: against the torch restatement of
+ * Pinned by tests/test_oracle_adam_ssim_raster.py: against the torch restatement of
  * torch_ref (oracle/render_ref.py) on the same tile lists with t_min = 0, and
  * its backward against torch autograd of that restatement.
  *

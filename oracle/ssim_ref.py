@@ -6,8 +6,11 @@ a separable 11-tap Gaussian window (sigma 1.5, train.py:40-49) under zero
 padding, then S = (2 mx my + C1)(2 sxy + C2) / ((mx^2 + my^2 + C1)(sxx + syy
 + C2)), mean over pixels and channels. Gradient by torch autograd.
 
-Pinned by tests/test_oracle_ssim.py: SSIM(a, a) = 1, the separable blur
-against a direct 11x11 2-D convolution in float64, and float64 gradcheck.
+Pinned by tests/test_oracle_adam_ssim_raster.py: SSIM(a, a) = 1; the
+separable blur against a direct 11x11 2-D convolution in float64; the window
+against scipy's Gaussian window and its second moment sigma^2 = 2.25; C1 by
+the closed form of constant images, C2 by that of a checkerboard pair, and
+the window's width inside SSIM by that of a ramp pair; float64 gradcheck.
 """
 
 from __future__ import annotations

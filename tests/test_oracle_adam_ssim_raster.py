@@ -100,6 +100,87 @@ def test_separable_blur_equals_direct_2d_convolution():
     assert (got - want).abs().max() < 1e-12
 
 
+def _scipy_window():
+    """The 11-tap sigma-1.5 Gaussian from scipy's own window routine,
+    normalised: an implementation independent of ssim_ref.window."""
+    from scipy.signal import windows
+
+    w = windows.gaussian(11, std=1.5, sym=True)
+    return torch.from_numpy(w / w.sum())
+
+
+def test_ssim_window_is_the_sigma_1_5_gaussian():
+    """train.py:40-49: 11 taps, sigma 1.5. Against scipy's Gaussian window,
+    and its discrete second moment sum k^2 w_k is sigma^2 = 2.25 up to the
+    truncation at +-5 taps (a window of sigma 1.0 or 2.0 gives about 1.0 or
+    3.4)."""
+    w = ssim_ref.window(dtype=torch.float64)
+    assert (w - _scipy_window()).abs().max() < 1e-15
+    k = torch.arange(-5, 6, dtype=torch.float64)
+    m2 = float((k * k * w).sum())
+    assert abs(m2 - 2.25) < 0.05, m2
+    assert abs(float(w.sum()) - 1.0) < 1e-15
+
+
+def _interior(t, r=5):
+    return t[..., r:-r, r:-r]
+
+
+def test_ssim_constants_from_constant_images():
+    """Constant images a = alpha, b = beta: away from the zero-padded border
+    the local variances and covariance vanish, so SSIM = (2 alpha beta + C1) /
+    (alpha^2 + beta^2 + C1) with C1 = (0.01 L)^2, L = 1 (Wang et al. 2004,
+    the constants of ssim.py:35-36). With alpha, beta of order 0.01 a C1 off
+    by a factor of two moves the value in the second digit."""
+    for alpha, beta in ((0.01, 0.02), (0.3, 0.7), (0.05, 0.05)):
+        a = torch.full((24, 30, 3), alpha, dtype=torch.float64)
+        b = torch.full((24, 30, 3), beta, dtype=torch.float64)
+        got = _interior(ssim_ref.ssim_map(a, b))
+        want = (2 * alpha * beta + 1e-4) / (alpha ** 2 + beta ** 2 + 1e-4)
+        assert (got - want).abs().max() < 1e-12, (alpha, beta)
+
+
+def test_ssim_c2_from_a_checkerboard_pair():
+    """x = mu + s c, y = mu + t c with c = (-1)^(i+j): with rho = sum_k w_k
+    (-1)^k of the window, the interior moments are mu_x = mu + s rho^2 c,
+    var_x = s^2 (1 - rho^4), var_y = t^2 (1 - rho^4), cov = s t (1 - rho^4),
+    so SSIM = (2 mu_x mu_y + C1)(2 cov + C2) / ((mu_x^2 + mu_y^2 + C1)
+    (var_x + var_y + C2)) with C2 = (0.03 L)^2. s = 0.01, t = 0.03 give 0.79
+    with that C2 and 0.64 with C2 = 1e-4."""
+    w = _scipy_window()
+    rho = float((w * torch.tensor([(-1.0) ** k for k in range(11)], dtype=torch.float64)).sum())
+    mu, s, t = 0.4, 0.01, 0.03
+    i = torch.arange(26, dtype=torch.float64)[:, None]
+    j = torch.arange(33, dtype=torch.float64)[None, :]
+    c = 1.0 - 2.0 * ((i + j) % 2)
+    a = (mu + s * c)[..., None].expand(26, 33, 3).contiguous()
+    b = (mu + t * c)[..., None].expand(26, 33, 3).contiguous()
+    got = _interior(ssim_ref.ssim_map(a, b))[0, 0]
+    mx, my = mu + s * rho ** 2 * c, mu + t * rho ** 2 * c
+    q = 1 - rho ** 4
+    want = ((2 * mx * my + 1e-4) * (2 * s * t * q + 9e-4)) / \
+        ((mx * mx + my * my + 1e-4) * ((s * s + t * t) * q + 9e-4))
+    assert (got - _interior(want)).abs().max() < 1e-12
+
+
+def test_ssim_window_second_moment_from_a_ramp_pair():
+    """Horizontal ramps x = a j, y = b j: the window is symmetric and sums to
+    1, so the interior means stay a j and b j while var_x = a^2 m2, var_y =
+    b^2 m2, cov = a b m2 with m2 = sum_k k^2 w_k of the (scipy) window. The
+    closed form pins the window's width inside the SSIM itself."""
+    w = _scipy_window()
+    m2 = float((torch.arange(-5, 6, dtype=torch.float64) ** 2 * w).sum())
+    ca, cb = 0.01, 0.015
+    j = torch.arange(40, dtype=torch.float64)[None, :].expand(20, 40)
+    a = (ca * j)[..., None].expand(20, 40, 3).contiguous()
+    b = (cb * j)[..., None].expand(20, 40, 3).contiguous()
+    got = _interior(ssim_ref.ssim_map(a, b))[0, 0]
+    jj = _interior(j)
+    want = ((2 * ca * cb * jj * jj + 1e-4) * (2 * ca * cb * m2 + 9e-4)) / \
+        (((ca * ca + cb * cb) * jj * jj + 1e-4) * ((ca * ca + cb * cb) * m2 + 9e-4))
+    assert (got - want).abs().max() < 1e-12
+
+
 def test_ssim_gradcheck():
     g = torch.Generator().manual_seed(2)
     a = torch.rand(9, 11, 3, generator=g).double().requires_grad_(True)
