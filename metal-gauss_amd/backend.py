@@ -66,12 +66,19 @@ def stale_lock_message(build_dir, now: float | None = None) -> str | None:
 
 
 def _load():
-    """The native library, loaded and initialised (metal_backend.py:76-108).
+    """The native extension, loaded and initialised (metal_backend.py:76-108).
 
-    The reference compiles Metal source at first use; libmgauss.so is built
-    ahead of time, so this only loads it. Raises if it is missing.
+    Returns the module of the reference's thirteen tensor-level functions
+    (``metal_gauss_amd.ext``: rasterize_forward/backward, preprocess_forward/
+    backward, bin_count, bin_write, adam_step, the five SSIM kernels, init)
+    over libmgauss.so. The reference compiles Metal source at first use;
+    libmgauss.so is built ahead of time, so this only loads it. Raises if it
+    is missing.
     """
-    return _lib.load()
+    from . import ext
+
+    _lib.load()
+    return ext
 
 
 def _require_gpu(t: torch.Tensor) -> None:
@@ -111,7 +118,7 @@ def _bin(uv, rxy, depth, valid_i, conic, opacity, W, H, tile):
     tiles_x). One device->host read per call: the intersection total that
     sizes the pair buffers (the reference's .item(), metal_backend.py:247-248).
     """
-    lib = _load()
+    lib = _lib.load()
     device = uv.device
     tx, ty = _tile_grid(W, H, tile)
     n_tiles = tx * ty
@@ -145,7 +152,7 @@ def _bin_keys64(uv, rxy, depth, valid_i, conic, opacity, W, H, tile):
     mg_exclusive_scan_i32 -> mg_bin_write (64-bit (tile|depth) keys) ->
     mg_sort_pairs_u64 -> mg_tile_ranges. Returns (gauss_ids, tile_offsets,
     tiles_x, sorted keys as int64)."""
-    lib = _load()
+    lib = _lib.load()
     device = uv.device
     tx, ty = _tile_grid(W, H, tile)
     n_tiles = tx * ty
@@ -312,7 +319,7 @@ class _PreprocessMetal(torch.autograd.Function):
                 W, H, near, far, blur, max_radius, cam_center, sh_degree, valid_mask=None):
         # valid_mask: an optional (N,) bool buffer the kernel also fills with
         # the visibility flags (render's info["valid_mask"]).
-        lib = _load()
+        lib = _lib.load()
         N = means.shape[0]
         dev = means.device
         means, quats, scales = (t.contiguous() for t in (means, quats, scales))
@@ -361,7 +368,7 @@ class _PreprocessMetal(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, d_uv, d_conic, d_depth, d_rxy, d_valid, d_color=None):
-        lib = _load()
+        lib = _lib.load()
         means, quats, scales, sh, rest, valid = ctx.saved_tensors
         viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center, deg = ctx.meta
         N = means.shape[0]
@@ -397,7 +404,7 @@ class _RasterizeMetal(torch.autograd.Function):
         blend's gradient too. ``chunked`` runs the backward as independent
         512-entry units per tile from checkpoints the forward records, which
         pays when a few tiles hold most of the intersections."""
-        lib = _load()
+        lib = _lib.load()
         dev = uv.device
         uv, conic, opacity, color = (t.contiguous() for t in (uv, conic, opacity, color))
         N = uv.shape[0]
@@ -439,7 +446,7 @@ class _RasterizeMetal(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_rgb, grad_alpha):
-        lib = _load()
+        lib = _lib.load()
         (uv, conic, opacity, color, gauss_ids, tile_offsets, T, stop, alpha,
          chunk_ws) = ctx.saved_tensors
         W, H, tile, tiles_x = ctx.dims
@@ -492,7 +499,7 @@ class _PreprocessMip(torch.autograd.Function):
     def forward(ctx, means, quats, scales, opacities, sh, sh_rest, filter_3d, antialias,
                 viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
                 sh_degree, valid_mask=None, activations=0, optimizer=None, reg=None):
-        lib = _load()
+        lib = _lib.load()
         N = means.shape[0]
         dev = means.device
         means, quats, scales, opacities = (t.contiguous() for t in
@@ -544,7 +551,7 @@ class _PreprocessMip(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, d_uv, d_conic, d_depth, d_rxy, d_valid, *rest_grads):
-        lib = _load()
+        lib = _lib.load()
         means, quats, scales, opacities, sh, rest, filt, valid = ctx.saved_tensors
         viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center, deg = ctx.meta
         if ctx.has_sh:
