@@ -37,6 +37,8 @@ METRIC = "train steps/sec & fwd+bwd ms at 1M Gaussians 800×800 SH3; % HBM roofl
 HBM_PEAK_GBS = 8000.0
 # Opacity and scale regulariser weights of the reference's step.
 REG = 0.01
+# Seconds of sustained load before the warm-up steps (bench/quick.py:110-133).
+RAMP_S = 2.0
 
 # Kernels timed by the library (names used in mg_timing_query).
 KERNELS = ["preprocess_forward", "bin_count", "exclusive_scan", "bin_write", "tile_sort",
@@ -61,7 +63,7 @@ TRAFFIC_FILE = ROOT / "profiles" / "pmc_traffic_config4.txt"
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--gaussians", type=int, default=1_000_000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -78,6 +80,12 @@ def parse():
                          "(render(filter_3d=, antialias=True)); mip-torch: the same step with "
                          "the activations and the 3D filter applied as the reference's torch "
                          "reparameterisation (apply_3d_filter, train.py:223-227) before render")
+    ap.add_argument("--ramp", type=float, default=RAMP_S,
+                    help="seconds of sustained forward+backward load before the warm-up "
+                         "steps (the reference's clock ramp); 0 for profiling runs")
+    ap.add_argument("--counter-summary", nargs="+", metavar="DIR",
+                    help="print the per-kernel counter summary of rocprofv3 --pmc runs (one "
+                         "directory per pass, with a kernel_stats.csv among them) and exit")
     ap.add_argument("--reg", action="store_true",
                     help="add the reference trainer's opacity and scale regularisers, "
                          "0.01 mean sigmoid(logit) + 0.01 mean exp(log_scales) "
@@ -266,14 +274,29 @@ def gpu_bench(args):
 
     dev = torch.device("cuda:0")
     step = Step(args.gaussians, dev, args.variant, reg=args.reg)
+    # Clock ramp as the reference's bench/quick.py:110-133 does (2 s of
+    # sustained load), with forward + backward only so the parameters the
+    # timed steps start from are untouched; then the warm-up steps.
+    ramp_end = time.perf_counter() + args.ramp
+    while time.perf_counter() < ramp_end:
+        step(adam=False)
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
+    # K timed steps: wall clock around all of them (the value), and a HIP
+    # event between consecutive steps on the stream the kernels run on (the
+    # median per step).
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for k in range(args.steps):
+        events[k].record()
         step()
+    events[-1].record()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    per_step = sorted(events[k].elapsed_time(events[k + 1]) for k in range(args.steps))
+    median_ms = per_step[len(per_step) // 2]
 
     # fwd+bwd alone (no optimizer step), fewer iterations.
     nfb = max(10, args.steps // 4)
@@ -319,8 +342,92 @@ def gpu_bench(args):
             wall = step.refresh_filter()
             tot, cnt = _lib.KernelTimer.query("compute_3d_filter")
         f3d_ms = (tot / max(cnt, 1), wall)
-    return dict(ms=ms, fb_ms=fb_ms, kernels=rows, dominant=dominant, achieved=achieved,
-                nbytes=nbytes, I=I, f_valid=f_valid, n_floats=n_floats, f3d_ms=f3d_ms)
+    work = raster_work(step, kern)
+    return dict(ms=ms, median_ms=median_ms, fb_ms=fb_ms, kernels=rows, dominant=dominant,
+                achieved=achieved, nbytes=nbytes, I=I, f_valid=f_valid, n_floats=n_floats,
+                f3d_ms=f3d_ms, work=work, copy=stream_copy())
+
+
+def raster_work(step, kern, views=8):
+    """The rasteriser's work count E over `views` of the step's cameras at the
+    current parameters: E_fwd = sum over pixels of the list entries the
+    per-pixel compositing evaluates (up to the stop entry when the pixel's
+    transmittance fell below 1e-4, else the whole tile list), E_bwd = sum of
+    the entries the backward replays (tile start to stop index). From the
+    forward's own stop indices and final T; per second against the step's
+    mean raster kernel times."""
+    import torch
+
+    from metal_gauss_amd import _lib, backend
+
+    lib = _lib.load()
+    p = step.p
+    e_f = e_b = 0.0
+    n = 0
+    for v in step.order[:views]:
+        cam = step.cams[v]
+        fx, fy, cx, cy, vm_h, cc = backend._camera(cam.K, cam.viewmat)
+        with torch.no_grad():
+            valid_b = torch.empty(p["means"].shape[0], dtype=torch.bool, device=p["means"].device)
+            uv, conic, depth, rxy, valid, color, op = backend._PreprocessMip.apply(
+                p["means"], p["quats"], p["log_scales"], p["logit_opac"], p["sh_dc"],
+                p["sh_rest"], None, False, vm_h, fx, fy, cx, cy, cam.W, cam.H, 0.01, 100.0, 0.3,
+                float(max(cam.W, cam.H)), cc, 3, valid_b, 3)
+            ids, offs, tx = backend._bin(uv, rxy, depth, valid, conic, op, cam.W, cam.H, 16)
+            W, H = cam.W, cam.H
+            rgb = torch.empty(H, W, 3, device=uv.device)
+            alpha = torch.empty(H, W, device=uv.device)
+            T = torch.empty(H, W, device=uv.device)
+            stop = torch.empty(H, W, dtype=torch.int32, device=uv.device)
+            _lib.check(lib.mg_rasterize_forward(
+                uv.shape[0], uv.data_ptr(), conic.data_ptr(), op.data_ptr(), color.data_ptr(),
+                ids.data_ptr(), offs.data_ptr(), W, H, 16, tx, backend.DEFAULT_T_MIN, None,
+                ids.numel(), None, 0, rgb.data_ptr(), alpha.data_ptr(), T.data_ptr(),
+                stop.data_ptr(), None, _lib.stream(uv)))
+            ty_ = torch.arange(H, device=uv.device) // 16
+            tx_ = torch.arange(W, device=uv.device) // 16
+            tile = ty_[:, None] * tx + tx_[None, :]
+            start = offs[tile].long()
+            end = offs[tile + 1].long()
+            done = T < backend.DEFAULT_T_MIN
+            e_f += float(torch.where(done, stop.long() - start, end - start).sum())
+            e_b += float((stop.long() - start).sum())
+            n += 1
+    e_f, e_b = e_f / n, e_b / n
+    out = {"views": n, "E_fwd": int(e_f), "E_bwd": int(e_b)}
+    if "rasterize_forward" in kern:
+        out["fwd_E_per_s"] = round(e_f / (kern["rasterize_forward"][0] * 1e-3), 1)
+    if "rasterize_backward" in kern:
+        out["bwd_E_per_s"] = round(e_b / (kern["rasterize_backward"][0] * 1e-3), 1)
+    return out
+
+
+def stream_copy(mib=1024, reps=20):
+    """STREAM Copy bandwidth on this GPU: the library's float4 copy kernel
+    (mg_stream_copy) over `mib` MiB, timed with HIP events on its stream;
+    bytes moved = read + write."""
+    import torch
+
+    from metal_gauss_amd import _lib
+
+    lib = _lib.load()
+    n = mib * (1 << 20)
+    src = torch.ones(n // 4, device="cuda")
+    dst = torch.empty_like(src)
+    s = _lib.stream(src)
+    for _ in range(3):
+        _lib.check(lib.mg_stream_copy(src.data_ptr(), dst.data_ptr(), n, s))
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        _lib.check(lib.mg_stream_copy(src.data_ptr(), dst.data_ptr(), n, s))
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    assert bool((dst == 1.0).all())
+    del src, dst
+    return {"GBps": round(2 * n / (ms * 1e-3) / 1e9, 1), "bytes_per_copy": 2 * n,
+            "kernel": "stream_copy_kernel (mg_stream_copy, float4)"}
 
 
 def mcmc_bench(args):
@@ -672,6 +779,110 @@ def pmc_summary(fetch_dir, write_dir, copy_mib):
     return "\n".join(lines)
 
 
+COUNTER_REGEX = ("raster_bwd|raster_fwd|adam_multi|preprocess_fwd|preprocess_bwd|scan_|"
+                 "bin_write|bin_count|bin_offsets|count_hist|count_colscan|count_scatter|"
+                 "tile_depth_sort|ssim_fused|photometric_loss|stream_copy|copyBuffer")
+
+
+def _kernel_base(name):
+    """'void mg::raster_bwd_kernel<4, false, true>(mg::RasterArgs, ...)' ->
+    'raster_bwd_kernel'."""
+    n = name.split("(")[0].replace("void ", "").strip()
+    n = n.split("<")[0]
+    return n.split("::")[-1]
+
+
+def counter_summary(dirs, copy_mib=1024):
+    """Per-kernel table from rocprofv3 runs of the config-4 step: one
+    --kernel-trace --stats run (kernel_stats.csv) and --pmc passes (one
+    *counter_collection.csv each). Counters are averaged over a kernel's
+    dispatches; FETCH_SIZE and WRITE_SIZE are calibrated by the run's own
+    copy of copy_mib MiB (__amd_rocclr_copyBuffer) when it is there."""
+    import csv
+
+    dur, vgpr, lds = {}, {}, {}
+    cnt = {}
+    for d in dirs:
+        for f in sorted(Path(d).rglob("*kernel_stats.csv")):
+            with open(f, newline="") as fh:
+                for r in csv.DictReader(fh):
+                    dur[_kernel_base(r["Name"])] = float(r["AverageNs"])
+        for f in sorted(Path(d).rglob("*counter_collection.csv")):
+            with open(f, newline="") as fh:
+                for r in csv.DictReader(fh):
+                    k = _kernel_base(r["Kernel_Name"])
+                    cnt.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(
+                        float(r["Counter_Value"]))
+                    vgpr[k] = r.get("VGPR_Count", "")
+                    lds[k] = r.get("LDS_Block_Size", "")
+    mean = {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in cnt.items()}
+    nbytes = copy_mib * (1 << 20)
+    cp = mean.get("__amd_rocclr_copyBuffer", {})
+    cf = nbytes / (max(cnt["__amd_rocclr_copyBuffer"]["FETCH_SIZE"]) * 1024) \
+        if "FETCH_SIZE" in cp else None
+    cw = nbytes / (max(cnt["__amd_rocclr_copyBuffer"]["WRITE_SIZE"]) * 1024) \
+        if "WRITE_SIZE" in cp else None
+    head = (f"{'kernel':26s} {'avg_us':>7s} {'VGPR':>4s} {'LDS_B':>6s} {'occ_w/CU':>8s} "
+            f"{'VALUbusy%':>9s} {'VALU_Minst':>10s} {'VALU_G/s':>9s} {'LDS_Minst':>9s} "
+            f"{'bankconf%':>9s} {'wait%':>6s} {'atomics_M':>9s} {'HBM_rd_MB':>9s} "
+            f"{'HBM_wr_MB':>9s} {'HBM_GB/s':>8s}")
+    lines = [head]
+
+    def g(k, c):
+        return mean.get(k, {}).get(c)
+
+    order = sorted((k for k in mean if k != "__amd_rocclr_copyBuffer"),
+                   key=lambda k: -dur.get(k, 0.0))
+    for k in order:
+        t = dur.get(k)
+        vi = g(k, "SQ_INSTS_VALU")
+        li = g(k, "SQ_INSTS_LDS")
+        bc, al = g(k, "SQ_LDS_BANK_CONFLICT"), g(k, "SQ_ACTIVE_INST_LDS")
+        wa, wc = g(k, "SQ_WAIT_INST_ANY"), g(k, "SQ_WAVE_CYCLES")
+        at = sum(x for x in (g(k, "TCP_TCC_ATOMIC_WITH_RET_REQ_sum"),
+                             g(k, "TCP_TCC_ATOMIC_WITHOUT_RET_REQ_sum")) if x is not None)
+        rd = cf * g(k, "FETCH_SIZE") * 1024 if cf and g(k, "FETCH_SIZE") is not None else None
+        wr = cw * g(k, "WRITE_SIZE") * 1024 if cw and g(k, "WRITE_SIZE") is not None else None
+
+        def fmt(x, w, p=1, scale=1.0):
+            return f"{x * scale:{w}.{p}f}" if x is not None else f"{'-':>{w}s}"
+        vp = vi / (t * 1e-9) / 1e9 if vi and t else None
+        bcp = 100 * bc / al if bc is not None and al else None
+        wp = 100 * wa / wc if wa is not None and wc else None
+        gbs = (rd + wr) / (t * 1e-9) / 1e9 if rd is not None and wr is not None and t else None
+        lines.append(
+            f"{k[:26]:26s} {fmt(t, 7, 1, 1e-3)} {str(vgpr.get(k, '')):>4s} "
+            f"{str(lds.get(k, '')):>6s} {fmt(g(k, 'MeanOccupancyPerCU'), 8, 1)} "
+            f"{fmt(g(k, 'VALUBusy'), 9, 1)} {fmt(vi, 10, 2, 1e-6)} {fmt(vp, 9, 1)} "
+            f"{fmt(li, 9, 2, 1e-6)} {fmt(bcp, 9, 2)} {fmt(wp, 6, 1)} "
+            f"{fmt(at if at else None, 9, 2, 1e-6)} {fmt(rd, 9, 1, 1e-6)} {fmt(wr, 9, 1, 1e-6)} "
+            f"{fmt(gbs, 8, 0)}")
+    notes = [
+        "# Per-kernel counters, config-4 step (1M Gaussians SH3, 800x800, tile 16), MI355X",
+        "# made by (from the repository root; TMPDIR=/tmp; B='bench.py --steps 3 --warmup 2",
+        "#   --no-cpu-baseline --ramp 0 --copy-mib 1024'; R = the --kernel-include-regex",
+        f"#   '{COUNTER_REGEX}'):",
+        "#   rocprofv3 --kernel-trace --stats -f csv -T -d KT -o kt -- python3 -u $B",
+        "#   rocprofv3 --pmc <pass> --kernel-include-regex $R -f csv -T -d P<i> -o pmc -- "
+        "python3 -u $B",
+        "#   for the passes: P1 'SQ_WAVES SQ_INSTS_VALU SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT",
+        "#   SQ_ACTIVE_INST_LDS SQ_WAIT_INST_ANY SQ_WAVE_CYCLES GRBM_GUI_ACTIVE', P2 VALUBusy,",
+        "#   P3 MeanOccupancyPerCU, P4 'TCP_TCC_ATOMIC_WITH_RET_REQ_sum",
+        "#   TCP_TCC_ATOMIC_WITHOUT_RET_REQ_sum', P5 FETCH_SIZE, P6 WRITE_SIZE; then",
+        "#   python bench.py --counter-summary KT P1 P2 P3 P4 P5 P6 --copy-mib 1024",
+        "# columns: avg_us from the kernel trace; VGPR and LDS bytes per workgroup as",
+        "#   rocprofv3 reports them; occ_w/CU = MeanOccupancyPerCU (waves resident per CU);",
+        "#   VALUbusy% = VALUBusy; VALU_Minst = SQ_INSTS_VALU (wave instructions) per",
+        "#   dispatch; VALU_G/s = SQ_INSTS_VALU / avg time (wave instructions per second);",
+        "#   LDS_Minst = SQ_INSTS_LDS; bankconf% = SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS;",
+        "#   wait% = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES; atomics_M = TCP->TCC atomic requests",
+        "#   (with + without return); HBM rd/wr = FETCH_SIZE, WRITE_SIZE calibrated by a",
+        f"#   {copy_mib} MiB device copy (factors "
+        f"{'-' if cf is None else f'{cf:.3f}'} / {'-' if cw is None else f'{cw:.3f}'}).",
+    ]
+    return "\n".join(notes + lines)
+
+
 def stats_summary(stats_csv, steps, variant="base", mcmc=False, config=None):
     """Text summary of a rocprofv3 --kernel-trace --stats kernel_stats.csv."""
     import csv
@@ -740,7 +951,7 @@ def committed_traffic(label):
     return None
 
 
-def cpu_baseline(n_gaussians=1_000_000, crop=800):
+def cpu_baseline(n_gaussians=1_000_000, crop=800, k=3):
     """The CPU oracle on one config-4 step.
 
     The full config-4 scene (all N Gaussians projected, SH evaluated, and
@@ -751,8 +962,9 @@ def cpu_baseline(n_gaussians=1_000_000, crop=800):
     denser than the frame, the crop's time is scaled by the ratio of the
     oracle's own intersection counts (3-sigma boxes at tile 16,
     render_ref.tile_lists) over the full view and over the crop. The
-    projection is run once untimed first (allocator and thread-pool warm-up).
-    The whole view needs about 40 GB of host memory.
+    projection is run once untimed first (allocator and thread-pool warm-up);
+    each part is then timed k times and its median taken. The whole view
+    needs about 40 GB of host memory.
     """
     import torch
 
@@ -797,43 +1009,54 @@ def cpu_baseline(n_gaussians=1_000_000, crop=800):
                                               w, h, 0.01, 100.0, max_radius_frac=W / w)
             return R.tile_lists(uvc, rc, vc, dc, w, h, 16)[3]
 
+    def median(xs):
+        return sorted(xs)[len(xs) // 2]
+
     # Projection of all N (forward + backward through a dummy reduction of the
-    # same outputs the rasteriser consumes); once untimed, then timed.
+    # same outputs the rasteriser consumes); once untimed, then k timed runs.
     for t in (project_part(),):
         (t[0].sum() + t[1].sum() + t[3].sum() + t[2].sum()).backward()
-    for t in leaves.values():
-        t.grad = None
-    t0 = time.perf_counter()
-    uv, conic, op, col, depth, radius, valid = project_part()
-    (uv.sum() + conic.sum() + col.sum() + op.sum()).backward()
-    t_proj = time.perf_counter() - t0
+    t_proj = []
+    for _ in range(k):
+        for t in leaves.values():
+            t.grad = None
+        t0 = time.perf_counter()
+        uv, conic, op, col, depth, radius, valid = project_part()
+        (uv.sum() + conic.sum() + col.sum() + op.sum()).backward()
+        t_proj.append(time.perf_counter() - t0)
     for t in leaves.values():
         t.grad = None
     # Raster + loss on the crop (the projection repeated outside the timer).
-    uv, conic, op, col, depth, radius, valid = project_part()
-    t0 = time.perf_counter()
-    rgb, alpha, info = R.rasterize(uv, conic, op, col, depth, radius, valid, crop, crop, tile=16,
-                                   background=(0.0, 0.0, 0.0))
-    loss = 0.8 * (rgb - gt).abs().mean() + 0.2 * (1.0 - ssim_ref.ssim(rgb, gt))
-    loss.backward()
-    t_crop = time.perf_counter() - t0
+    t_crop = []
+    for _ in range(k):
+        uv, conic, op, col, depth, radius, valid = project_part()
+        t0 = time.perf_counter()
+        rgb, alpha, info = R.rasterize(uv, conic, op, col, depth, radius, valid, crop, crop,
+                                       tile=16, background=(0.0, 0.0, 0.0))
+        loss = 0.8 * (rgb - gt).abs().mean() + 0.2 * (1.0 - ssim_ref.ssim(rgb, gt))
+        loss.backward()
+        t_crop.append(time.perf_counter() - t0)
+        del rgb, alpha, loss
     # Adam over all parameters.
     opt = torch.optim.Adam(list(leaves.values()), lr=1e-3, eps=1e-15)
-    for t in leaves.values():
-        t.grad = torch.zeros_like(t)
-    t0 = time.perf_counter()
-    opt.step()
-    t_adam = time.perf_counter() - t0
+    t_adam = []
+    for _ in range(k):
+        for t in leaves.values():
+            t.grad = torch.zeros_like(t)
+        t0 = time.perf_counter()
+        opt.step()
+        t_adam.append(time.perf_counter() - t0)
+    tp, tc, ta = median(t_proj), median(t_crop), median(t_adam)
     i_full = isect_count(cam.K, W, H) if crop < W else info["isect_total"]
     scale = i_full / max(1, info["isect_total"])
-    t_step = t_proj + t_adam + t_crop * scale
+    t_step = tp + ta + tc * scale
     return {
         "value": round(1.0 / t_step, 6), "unit": "steps/s", "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"config-4 step, CPU oracle (torch_ref restatement): projection+SH fwd+bwd of "
-                   f"all {n_gaussians} Gaussians {t_proj:.2f}s + Adam over all params "
-                   f"{t_adam:.2f}s + raster/loss fwd+bwd on a {crop}x{crop} centre crop "
-                   f"{t_crop:.2f}s x {scale:.2f} (oracle intersections, full view "
+        "sample": (f"config-4 step, CPU oracle (torch_ref restatement), median of {k} runs of "
+                   f"each part: projection+SH fwd+bwd of all {n_gaussians} Gaussians {tp:.2f}s + "
+                   f"Adam over all params {ta:.2f}s + raster/loss fwd+bwd on a {crop}x{crop} "
+                   f"centre crop {tc:.2f}s x {scale:.2f} (oracle intersections, full view "
                    f"{i_full} / crop {info['isect_total']}); os.cpu_count()={cores}"),
     }
 
@@ -857,6 +1080,9 @@ def main():
         sys.exit(2)
     if args.pmc_summary:
         print(pmc_summary(*args.pmc_summary, args.copy_mib or 1024))
+        return
+    if args.counter_summary:
+        print(counter_summary(args.counter_summary, args.copy_mib or 1024))
         return
     if args.stats_summary:
         print(stats_summary(args.stats_summary, args.steps if args.config else 20,
@@ -927,6 +1153,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(r["ms"], 4),
+        "median_ms_per_step": round(r["median_ms"], 4),
+        "ramp_s": args.ramp,
         "fwd_bwd_ms": round(r["fb_ms"], 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -950,6 +1178,8 @@ def main():
             "algorithmic_bytes_per_launch": int(r["nbytes"]),
         },
         "kernels": r["kernels"],
+        "raster_work": r["work"],
+        "stream_copy": r["copy"],
     }
     if args.variant != "base":
         out["config"]["workload"] += {

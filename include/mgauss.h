@@ -68,6 +68,12 @@ int32_t mg_timing_enable(int32_t on);
 int32_t mg_timing_reset(void);
 int32_t mg_timing_query(const char *kernel, double *total_ms, int64_t *count);
 
+/* STREAM "Copy" of `bytes` (a multiple of 16, 16-byte aligned buffers) from
+ * src to dst, a hand-written float4 kernel: the achievable HBM bandwidth the
+ * bench reports beside its roofline fractions. No counterpart in the
+ * reference (its benchmark notes cite a STREAM-style copy). */
+int32_t mg_stream_copy(const void *src, void *dst, int64_t bytes, mg_stream_t stream);
+
 /* ------------------------------------------------------------- preprocess */
 
 /* Fused projection + EWA covariance + SnugBox extents + validity + SH colour.

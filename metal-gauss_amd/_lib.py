@@ -38,6 +38,7 @@ _SIGNATURES = {
     "mg_timing_reset": (_i32, []),
     "mg_timing_query": (_i32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                ctypes.POINTER(_i64)]),
+    "mg_stream_copy": (_i32, [_vp, _vp, _i64, _vp]),
     "mg_preprocess_forward": (_i32, [
         _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _f32, _f32, _i32, _i32,
         _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),

@@ -22,7 +22,11 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from . import ssim as _ssim
+from .ssim import blur15 as _blur15
+from .ssim import chain_backward as _chain_backward
+from .ssim import stack_blur_h as _stack_blur_h
+from .ssim import tail_backward as _tail_backward
+from .ssim import tail_forward as _tail_forward
 
 # The reference kernel's per-pixel stop transmittance (rasterize.metal:149).
 _T_MIN = 1e-4
@@ -187,12 +191,12 @@ def adam_step(p, g, m, v, lr, b1, b2, eps, step):
 
 def ssim_tail_forward(b, H, W):
     """rasterize.mm:383-389: SSIM map (1,3,H,W) of a blurred (15,H,W) stack."""
-    return _ssim.tail_forward(b, int(H), int(W))
+    return _tail_forward(b, int(H), int(W))
 
 
 def ssim_tail_backward(b, gout, H, W):
     """rasterize.mm:391-397: gradient of the blurred stack, shaped like b."""
-    return _ssim.tail_backward(b, gout, int(H), int(W))
+    return _tail_backward(b, gout, int(H), int(W))
 
 
 def ssim_stack_blur_h(x, y, w, H, W):
@@ -200,18 +204,18 @@ def ssim_stack_blur_h(x, y, w, H, W):
     images, blurred along rows by the 11-tap window w."""
     if x.numel() != 3 * H * W or y.numel() != x.numel():
         raise RuntimeError("expected (H,W,3)")
-    return _ssim.stack_blur_h(x, y, w, int(H), int(W))
+    return _stack_blur_h(x, y, w, int(H), int(W))
 
 
 def ssim_blur15(src, w, dir, H, W):  # noqa: A002  (the reference's argument name)
     """rasterize.mm:421-440: the 15-channel stack blurred along columns
     (dir 1) or rows (dir 0)."""
-    return _ssim.blur15(src, w, int(dir), int(H), int(W))
+    return _blur15(src, w, int(dir), int(H), int(W))
 
 
 def ssim_chain_backward(x, y, d_stack, H, W):
     """rasterize.mm:442-461: the gradient of x through the moment stack."""
-    return _ssim.chain_backward(x, y, d_stack, int(H), int(W))
+    return _chain_backward(x, y, d_stack, int(H), int(W))
 
 
 def bin_count(uv, rxy, conic, opacity, valid, W, H, tile, tiles_x, tiles_y):
