@@ -98,33 +98,52 @@ __device__ __forceinline__ int tile_of_block(int bid, int tiles_x, int tiles_y) 
     return tx < tiles_x && ty < tiles_y ? ty * tiles_x + tx : -1;
 }
 
-// The exponent of the splat at offset (dx, dy). Written with explicit fmas so
-// the forward and the backward round identically: the backward divides the
-// forward's (1 - alpha) back out and must see the same alpha bit for bit.
-__device__ __forceinline__ float splat_power(float dx, float dy, float a, float b, float c) {
-    const float q = fmaf(a * dx, dx, fmaf(2.0f * b * dx, dy, c * dy * dy));
-    return -0.5f * q;
+// The conic as the walks keep it in LDS: (-a/2, -b, -c/2), so that the
+// splat's exponent -(a dx^2 + 2 b dx dy + c dy^2) / 2 is one fma chain.
+// Scaling by -1/2 and -1 is exact in floating point, so every product and
+// sum rounds to exactly the negated half of what the unscaled expression
+// fma(a dx, dx, fma(2 b dx, dy, c dy dy)) rounds to: the exponent is bit for
+// bit the one of the per-pixel contract, with two instructions fewer per
+// (entry, wave). Folding log2(e) in as well saves one more but rounds
+// differently: on config 5's near-singular conics, whose terms cancel, that
+// moved alphas across the 1/255 cutoff.
+__device__ __forceinline__ float4 scale_conic(const float4 con) {
+    return make_float4(-0.5f * con.x, -con.y, -0.5f * con.z, 0.f);
+}
+
+// The exponent of the splat at offset (dx, dy) from the staged conic.
+// Written with explicit fmas so the forward and the backward round
+// identically: the backward divides the forward's (1 - alpha) back out and
+// must see the same alpha bit for bit.
+__device__ __forceinline__ float splat_power(float dx, float dy, const float4 k) {
+    return fmaf(k.x * dx, dx, fmaf(k.y * dx, dy, k.z * dy * dy));
+}
+
+// The raw conic (a, b, c) back from its staged form (exact).
+__device__ __forceinline__ float3 raw_conic(const float4 k) {
+    return make_float3(-2.0f * k.x, -k.y, -2.0f * k.z);
 }
 
 // Conservative per-wave cull: minimum of the quadratic form over the box of
 // the wave's pixel centres, against 2 ln(255 op) widened by a rounding margin
-// (the reference's own margin, rasterize.metal:150-151).
-__device__ __forceinline__ float rect_min_q(float mux, float muy, float ca, float cb, float cc,
-                                            float x0, float x1, float y0, float y1) {
+// (the reference's own margin, rasterize.metal:150-151). The entry's 1/a and
+// 1/c are formed once for all its wave boxes (a and c clamped at 1e-12).
+__device__ __forceinline__ float rect_min_q(float mux, float muy, float a, float b, float c,
+                                                float ia, float ic, float x0, float x1,
+                                                float y0, float y1) {
     if (mux >= x0 && mux <= x1 && muy >= y0 && muy <= y1) return 0.0f;
-    const float a = fmaxf(ca, 1e-12f), b = cb, c = fmaxf(cc, 1e-12f);
     float best = __builtin_inff();
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const float yc = e == 0 ? y0 : y1;
-        const float xs = fminf(fmaxf(mux - b * (yc - muy) / a, x0), x1);
+        const float xs = fminf(fmaxf(mux - b * (yc - muy) * ia, x0), x1);
         const float ex = xs - mux, ey = yc - muy;
         best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
     }
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const float xc = e == 0 ? x0 : x1;
-        const float ys = fminf(fmaxf(muy - b * (xc - mux) / c, y0), y1);
+        const float ys = fminf(fmaxf(muy - b * (xc - mux) * ic, y0), y1);
         const float ex = xc - mux, ey = ys - muy;
         best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
     }
@@ -220,16 +239,18 @@ __device__ __forceinline__ Rec gather_rec(const RasterArgs &A, int g) {
 template <class S_>
 __device__ __forceinline__ void put_rec(S_ &S, int t, const Rec &r, int nwaves) {
     S.geo[t] = r.geo;
-    S.con[t] = r.con;
+    S.con[t] = scale_conic(r.con);
     S.col[t] = r.col;
     S.id[t] = r.id;
     const float thr = 2.0f * __logf(fmaxf(255.0f * r.geo.z, 1.0f));
     const float thr_m = thr * 1.0001f + 1e-4f;
     uint32_t m = 0;
+    const float ca = fmaxf(r.con.x, 1e-12f), cc = fmaxf(r.con.z, 1e-12f);
+    const float ia = __builtin_amdgcn_rcpf(ca), ic = __builtin_amdgcn_rcpf(cc);
     for (int w = 0; w < nwaves; ++w) {
         const float4 q = S.rect[w];
         if (q.x <= q.y &&
-            rect_min_q(r.geo.x, r.geo.y, r.con.x, r.con.y, r.con.z, q.x, q.y, q.z, q.w) < thr_m)
+            rect_min_q(r.geo.x, r.geo.y, ca, r.con.y, cc, ia, ic, q.x, q.y, q.z, q.w) < thr_m)
             m |= 1u << w;
     }
     S.live[t] = m;
@@ -404,28 +425,48 @@ __global__ __launch_bounds__(MAXW * 64) void raster_fwd_kernel(const RasterArgs 
         stage_batch(S, A, base, n, nwaves);
         __syncthreads();
         const int cnt = compact_live(S, n, n, wave, lane);
-        if (ballot(!done) != 0) {
-            for (int k = 0; k < cnt; ++k) {
-                const int j = S.list[wave][k];
-                if (!done) {
-                    const float4 geo = S.geo[j];
-                    const float4 con = S.con[j];
-                    const float dx = fx - geo.x, dy = fy - geo.y;
-                    const float power = splat_power(dx, dy, con.x, con.y, con.z);
-                    if (power <= 0.0f) {
-                        const float alpha = fminf(kAlphaMax, geo.z * __expf(power));
-                        if (alpha >= kAlphaMin) {
-                            const float4 col = S.col[j];
-                            const float w = alpha * T;
-                            cr = fmaf(w, col.x, cr);
-                            cg = fmaf(w, col.y, cg);
-                            cb = fmaf(w, col.z, cb);
-                            acc += w;
-                            T = T * (1.0f - alpha);
-                            stop = base + j + 1;
-                            if (T < A.t_min) done = true;
-                        }
-                    }
+        // Branch-free walk, U entries per round: the records of the round
+        // are requested together, each entry updates the pixel with selects
+        // (a lane that is done, or outside the splat, adds w = 0 and keeps T:
+        // bit for bit what branches give), and the wave checks once per round
+        // whether all its pixels are done. The list is read 64 indices at a
+        // time into a register and each index taken with a lane read. With a
+        // branch per entry the walk issued about as many scalar instructions
+        // (exec-mask updates) as vector ones, and the CU's one scalar unit,
+        // shared by its four SIMDs, set the pace: 171 us against 117 us here
+        // at config 4 (U = 2: 126 us, U = 8: 134 us).
+        constexpr int U = 4;
+        if (cnt > 0 && ballot(!done) != 0) {
+            int lreg = S.list[wave][lane];
+            for (int k = 0; k < cnt; k += U) {
+                if ((k & 63) == 0 && k) lreg = S.list[wave][k + lane];
+                int jj[U];
+                float4 gg[U], kk[U], cc[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int ku = k + u < cnt ? k + u : k;
+                    jj[u] = __builtin_amdgcn_readlane(lreg, ku & 63);
+                    gg[u] = S.geo[jj[u]];
+                    kk[u] = S.con[jj[u]];
+                    cc[u] = S.col[jj[u]];
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const float dx = fx - gg[u].x, dy = fy - gg[u].y;
+                    const float power = splat_power(dx, dy, kk[u]);
+                    const float alpha = fminf(kAlphaMax,
+                                              gg[u].z * __expf(power));
+                    const bool live = (u == 0 || k + u < cnt) && !done && power <= 0.0f &&
+                                      alpha >= kAlphaMin;
+                    const float w = live ? alpha * T : 0.0f;
+                    cr = fmaf(w, cc[u].x, cr);
+                    cg = fmaf(w, cc[u].y, cg);
+                    cb = fmaf(w, cc[u].z, cb);
+                    acc += w;
+                    const float Tn = T * (1.0f - alpha);
+                    T = live ? Tn : T;
+                    stop = live ? base + jj[u] + 1 : stop;
+                    done = done || (live && Tn < A.t_min);
                 }
                 if (ballot(!done) == 0) break;
             }
@@ -547,7 +588,7 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
     auto entry = [&](const int j, const int i, const float4 geo, const float4 con,
                      const float4 col) {
         const float dx = fx - geo.x, dy = fy - geo.y;
-        const float power = splat_power(dx, dy, con.x, con.y, con.z);
+        const float power = splat_power(dx, dy, con);
         const float gauss = __expf(power);
         const float op = geo.z;
         const float alpha_raw = op * gauss;
@@ -582,7 +623,8 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
         v[8] = dg;
         if (ABS) {
             // |d uv| of this pixel over op: |dg| |(a dx + b dy, b dx + c dy)|.
-            const float ex = fmaf(con.x, dx, con.y * dy), ey = fmaf(con.y, dx, con.z * dy);
+            const float3 kc = raw_conic(con);
+            const float ex = fmaf(kc.x, dx, kc.y * dy), ey = fmaf(kc.y, dx, kc.z * dy);
             v[9] = fabsf(dg) * __builtin_amdgcn_sqrtf(fmaf(ex, ex, ey * ey));
         } else {
             v[9] = 0.0f;
@@ -613,7 +655,7 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
 #pragma unroll
         for (int q = 0; q < kGradSlots; ++q) s[q] = S.grad[q][e];
         const float op = S.geo[e].z;
-        const float4 con = S.con[e];
+        const float3 con = raw_conic(S.con[e]);
         S.grad[0][e] = op * fmaf(con.x, s[3], con.y * s[4]);
         S.grad[1][e] = op * fmaf(con.y, s[3], con.z * s[4]);
         S.grad[2][e] = -0.5f * op * s[5];
