@@ -82,7 +82,8 @@ __device__ __forceinline__ bool make_rec(const BinArgs &A, int64_t g, BinRec &r)
 }
 
 // Walks the rectangle, rows outer and columns inner (binning.metal:74-77),
-// calling emit(n, tile_id) for the n-th claimed tile; returns the count.
+// calling emit(n, tile_id, loc) for the n-th claimed tile, loc being its
+// row-major index in the rectangle; returns the count.
 //
 // A tile is claimed when the minimum over the tile rectangle of
 // q(d) = a dx^2 + 2 b dx dy + c dy^2 is below the threshold. The minimum is 0
@@ -100,10 +101,10 @@ __device__ __forceinline__ int rec_walk(const BinRec &r, bool test, int tile, in
 #pragma clang fp contract(off)
     const int x0 = (int)(r.xs & 0xffffu), x1 = (int)(r.xs >> 16);
     const int y0 = (int)(r.ys & 0xffffu), y1 = (int)(r.ys >> 16);
-    int n = 0;
+    int n = 0, loc = 0;
     if (!test) {
         for (int ty = y0; ty <= y1; ++ty)
-            for (int tx = x0; tx <= x1; ++tx) emit(n++, (uint32_t)(ty * tiles_x + tx));
+            for (int tx = x0; tx <= x1; ++tx, ++loc) emit(n++, (uint32_t)(ty * tiles_x + tx), loc);
         return n;
     }
     const float mux = r.ux, muy = r.uy, a = r.a, b = r.b, c = r.c;
@@ -133,7 +134,8 @@ __device__ __forceinline__ int rec_walk(const BinRec &r, bool test, int tile, in
                 best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
                 claim = best < r.thr;
             }
-            if (claim) emit(n++, (uint32_t)(ty * tiles_x + tx));
+            if (claim) emit(n++, (uint32_t)(ty * tiles_x + tx), loc);
+            ++loc;
             rx0 = rx1;      // equal to (tx + 1) * tile unless this is the last column
             v0 = v1;
         }
@@ -276,7 +278,8 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_kernel(const BinArgs A,
     BinRec r;
     int n = 0;
     if (make_rec(A, g, r))
-        n = rec_walk(r, A.conic != nullptr, A.tile, A.W, A.H, A.tiles_x, [](int, uint32_t) {});
+        n = rec_walk(r, A.conic != nullptr, A.tile, A.W, A.H, A.tiles_x,
+                     [](int, uint32_t, int) {});
     counts[g] = n;
 }
 
@@ -289,7 +292,7 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_kernel(const BinArgs A,
     if (!make_rec(A, g, r)) return;
     const uint64_t dbits = (uint64_t)__float_as_uint(A.depth[g]);
     const int64_t at = offsets[g];
-    rec_walk(r, A.conic != nullptr, A.tile, A.W, A.H, A.tiles_x, [&](int n, uint32_t t) {
+    rec_walk(r, A.conic != nullptr, A.tile, A.W, A.H, A.tiles_x, [&](int n, uint32_t t, int) {
         keys[at + n] = ((uint64_t)t << 32) | dbits;
         ids[at + n] = (int32_t)g;
     });
@@ -457,6 +460,7 @@ struct BinPart {
 // walk record; per workgroup the intersection total.
 __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArgs A,
                                                                     int32_t *counts, BinRec *recs,
+                                                                    uint32_t *masks,
                                                                     BinPart *parts) {
     __shared__ BinPart s_p[kBinThreads / 64];
     __shared__ BinRec s_rec[kBinThreads];
@@ -470,6 +474,7 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
     __syncthreads();
     int n = 0;
     bool big = false;
+    uint32_t mask = 0;
     if (g < A.N) {
         BinRec r;
         if (make_rec(A, g, r)) {
@@ -478,9 +483,13 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
                 big = true;
                 s_rec[tid] = r;
             } else {
-                n = rec_walk(r, test, A.tile, A.W, A.H, A.tiles_x, [](int, uint32_t) {});
+                n = rec_walk(r, test, A.tile, A.W, A.H, A.tiles_x,
+                             [&](int, uint32_t, int loc) { mask |= 1u << loc; });
             }
         }
+        // The claimed tiles of a small rectangle, bit loc for its row-major
+        // tile loc: the write pass emits from them without testing again.
+        masks[g] = mask;
     }
     // Large rectangles: compacted in LDS, one wave each.
     const uint64_t m = ballot(big);
@@ -582,9 +591,9 @@ constexpr int kBinStage = 2048;
 // workgroup of the same 256 Gaussians, scanned); each Gaussian's offset in it
 // is an exclusive scan of the counts, formed here.
 __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
-    const BinRec *recs, const int32_t *counts, const int64_t *part_off, int64_t N, int tile,
-    int W, int H, int tiles_x, int test, uint32_t *tkeys, int32_t *ids, const float *depth,
-    uint2 *pairs) {
+    const BinRec *recs, const int32_t *counts, const uint32_t *masks, const int64_t *part_off,
+    int64_t N, int tile, int W, int H, int tiles_x, int test, uint32_t *tkeys, int32_t *ids,
+    const float *depth, uint2 *pairs) {
     __shared__ uint32_t s_k[kBinStage];
     __shared__ int32_t s_i[kBinStage];
     __shared__ int32_t s_off[kBinStage];
@@ -608,6 +617,7 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
     int small_cap = 0;        // pairs this thread stages (0 unless a small rectangle)
     int32_t g = 0;
     BinRec r{};
+    uint32_t mask = 0;
     const int cap = k < N ? counts[k] : 0;
     {
         if (cap > 0) {
@@ -619,6 +629,7 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
                 s_g[tid] = g;
             } else {
                 small_cap = cap;
+                mask = masks[g];
             }
         }
     }
@@ -688,14 +699,23 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
     for (int w0 = 0; w0 < n_small; w0 += kBinStage) {
         const int w1 = min(w0 + kBinStage, n_small);
         if (small_cap > 0 && first < w1 && first + small_cap > w0) {
-            rec_walk(r, test != 0, tile, W, H, tiles_x, [&](int n, uint32_t t) {
+            // The count pass's claimed tiles, in the walk's row-major order:
+            // row = floor(loc / w) as (loc * ceil(2^16 / w)) >> 16, exact for
+            // loc < 32 <= 2^16 / w.
+            const int x0 = (int)(r.xs & 0xffffu), y0 = (int)(r.ys & 0xffffu);
+            const int w = (int)(r.xs >> 16) - x0 + 1;
+            const uint32_t inv = (65536u + (uint32_t)w - 1u) / (uint32_t)w;
+            int n = 0;
+            for (uint32_t mm = mask; mm != 0 && n < small_cap; mm &= mm - 1u, ++n) {
                 const int sl = first + n;
-                if (n < small_cap && sl >= w0 && sl < w1) {
-                    s_k[sl - w0] = t;
-                    s_i[sl - w0] = g;
-                    s_off[sl - w0] = off0 + n;
-                }
-            });
+                if (sl < w0 || sl >= w1) continue;
+                const int loc = __builtin_ctz(mm);
+                const int row = (int)(((uint32_t)loc * inv) >> 16);
+                const int col = loc - row * w;
+                s_k[sl - w0] = (uint32_t)((y0 + row) * tiles_x + x0 + col);
+                s_i[sl - w0] = g;
+                s_off[sl - w0] = off0 + n;
+            }
         }
         __syncthreads();
         for (int i = tid; i < w1 - w0; i += kBinThreads) {
@@ -1304,6 +1324,7 @@ __global__ __launch_bounds__(256) void gather_depth_pairs_kernel(const int32_t *
 // 256-Gaussian workgroup, recs the walk records.
 struct BeginWs {
     int32_t *counts;
+    uint32_t *masks;
     BinRec *recs;
     BinPart *parts;
     int64_t *part_off;
@@ -1315,6 +1336,7 @@ struct BeginWs {
         auto take = [&](int64_t b) { char *q = p ? p + off : nullptr; off += align256(b); return q; };
         const int64_t nparts = ceil_div(N, kBinThreads);
         counts = (int32_t *)take(4 * N);
+        masks = (uint32_t *)take(4 * N);
         recs = (BinRec *)take((int64_t)sizeof(BinRec) * N);
         parts = (BinPart *)take((int64_t)sizeof(BinPart) * nparts);
         part_off = (int64_t *)take(8 * nparts);
@@ -1466,7 +1488,7 @@ int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy, const f
     if (N > 0) {
         TimedScope ts("bin_count", s);
         bin_count_rec_kernel<<<(unsigned)nparts, kBinThreads, 0, s>>>(A, ws.counts, ws.recs,
-                                                                       ws.parts);
+                                                                       ws.masks, ws.parts);
         MG_LAUNCHED("bin_count_rec_kernel");
     }
     {
@@ -1542,7 +1564,8 @@ int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy, const 
         {
             TimedScope ts("bin_write", s);
             bin_write_rec_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(
-                ws.recs, ws.counts, ws.part_off, N, tile, W, H, tiles_x, conic != nullptr ? 1 : 0,
+                ws.recs, ws.counts, ws.masks, ws.part_off, N, tile, W, H, tiles_x,
+                conic != nullptr ? 1 : 0,
                 tk_a, counting ? nullptr : ids_a, depth, counting ? pairs_a : nullptr);
             MG_LAUNCHED("bin_write_rec_kernel");
         }
