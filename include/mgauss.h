@@ -475,8 +475,11 @@ int32_t mg_adam_step_multi(int32_t count, float *const *p,
 /* Row-masked Adam with a per-row float step count, over up to 32 tensors in
  * one launch. Tensor k has rows[k] rows of width[k] floats; rows r with
  * r < n_visible and visible[r] != 0 get steps[r] += 1 and
- * p -= lr * sqrt(1-b2^k)/(1-b1^k) * m/(sqrt(v)+eps); other rows are left
- * untouched. visible: (n_visible,) uint8 (torch.bool). The reference has no
+ * p -= lr * sqrt(1-b2^k)/(1-b1^k) * m/(sqrt(v)+eps); other rows keep their
+ * values. visible: (n_visible,) uint8 (torch.bool). When p, g, m, v and
+ * steps are 16-byte aligned, rows that keep their values may be stored back
+ * unchanged (whole-line writes), so no two tensors may share p, m, v or
+ * steps, and nothing else may write them during the call. The reference has no
  * kernel for this; it replaces SelectiveAdam._step_indexed / _step_masked
  * (selective_adam.py:116-187). */
 int32_t mg_selective_adam_step(int32_t count, float *const *p,

@@ -14,6 +14,7 @@
 // The selective / dense-auxiliary variant of metal_gauss/selective_adam.py
 // (lines 144-148, 182-186, 201-206) puts eps inside instead:
 //     p -= lr * sqrt(bc2) / bc1 * m / (sqrt(v) + eps)
+#include <algorithm>
 #include <cmath>
 
 #include "mg_common.h"
@@ -140,10 +141,32 @@ __global__ __launch_bounds__(kAdamThreads) void adam_multi_kernel(const AdamTabl
 }
 
 // ------------------------------------------------------------ selective Adam
-// One workgroup owns kSelRows consecutive rows of one tensor, so the per-row
-// step count can be read, bumped and written back without any other
-// workgroup touching it. Invisible rows issue no loads at all.
-constexpr int kSelRows = 256;
+// One workgroup owns a run of consecutive rows of one tensor (T.block_rows of
+// them), so the per-row step count can be read, bumped and written back
+// without any other workgroup touching it.
+//
+// Writes go to HBM in whole 64-byte chunks or not at all, because a partly
+// written chunk costs the memory side a read-modify-write (measured at
+// config 3: skipping per 32 or 16 bytes made the kernel 9% and 14% slower
+// than per 64, for less data moved). With 16-byte aligned tensors:
+//  * narrow tensors (fewer than 16 floats per row: means, scales, quats,
+//    opacity, the DC band) hold one or more rows per chunk, so at any useful
+//    visibility almost every chunk has a visible row. They are moved whole
+//    as float4s (visible elements updated, the others stored back
+//    unchanged), and their loads are issued before the step-count prologue,
+//    whose latency they then overlap. A block holds at most 2048 floats (two
+//    float4s per thread).
+//  * wide tensors (16 floats or more per row, e.g. the 45-float SH rest) span
+//    at most two rows per chunk; a chunk with no visible row is skipped, the
+//    others are moved whole. Their blocks are short (64 rows: measured 30 us
+//    faster than 256 at config 3, the long blocks' serial prologue and tail
+//    no longer dominating), and the host puts the widest tensors first.
+//  * the step counts (one float per row) are moved whole as well.
+// Each visible element's arithmetic is the same on every path.
+constexpr int kSelRowsMax = 1024;
+constexpr int kSelRowsWide = 64;
+constexpr int kSelWideMin = 16;            // floats per row of a wide tensor
+constexpr int kSelDenseFloats = 2048;      // floats per narrow-tensor block
 
 struct SelTensor {
     float *p;
@@ -154,12 +177,15 @@ struct SelTensor {
     int64_t rows;
     int32_t width;
     int32_t block_begin;
+    int32_t block_rows;   // rows per workgroup
     float lr;
     // ceil(2^32 / width) when 1 < width < 256 (1 when width is 1), else 0:
-    // then an element index e < kSelRows * width < 2^16 has row
+    // then an element index e < block_rows * width < 2^16 has row
     // __umulhi(e, wmagic) exactly (the round-up error times e stays below
     // 2^32).
     uint32_t wmagic;
+    // 0: element by element; 1: narrow, moved whole; 2: wide, chunk-skipped.
+    int32_t mode;
 };
 
 struct SelTable {
@@ -171,21 +197,84 @@ struct SelTable {
     double l2b1, l2b2;               // log2 of the fp32 betas, in double
 };
 
+// Rows a workgroup of a tensor of this width owns on each path.
+inline int sel_block_rows(int width, int mode) {
+    if (mode != 1) return kSelRowsWide;
+    int r = kSelRowsMax;
+    while (r * width > kSelDenseFloats) r >>= 1;
+    return r;
+}
+
+__device__ __forceinline__ void sel_update(float &p, float g, float &m, float &v, float ss,
+                                           float b1, float b2, float omb1, float omb2,
+                                           float eps) {
+    const float mn = m * b1 + g * omb1;
+    const float vn = v * b2 + g * g * omb2;
+    p = p - ss * mn / (sqrtf(vn) + eps);
+    m = mn;
+    v = vn;
+}
+
+// Element e of float4s of p, g, m, v.
+__device__ __forceinline__ void sel_update4(v4f &p, const v4f &g, v4f &m, v4f &v, int e,
+                                            float ss, float b1, float b2, float omb1,
+                                            float omb2, float eps) {
+    float pe = p[e], me = m[e], ve = v[e];
+    sel_update(pe, g[e], me, ve, ss, b1, b2, omb1, omb2, eps);
+    p[e] = pe;
+    m[e] = me;
+    v[e] = ve;
+}
+
 __global__ __launch_bounds__(kAdamThreads) void selective_adam_kernel(const SelTable tab) {
-    __shared__ float s_step_size[kSelRows];
-    __shared__ uint8_t s_vis[kSelRows];
+    __shared__ float s_step_size[kSelRowsMax];
+    __shared__ uint8_t s_vis[kSelRowsMax];
 
     int k = 0;
     const int bid = blockIdx.x;
     while (k + 1 < tab.count && bid >= tab.t[k + 1].block_begin) ++k;
     const SelTensor &T = tab.t[k];
-    const int64_t r0 = (int64_t)(bid - T.block_begin) * kSelRows;
-    const int nrows = (int)min((int64_t)kSelRows, T.rows - r0);
+    const int R = T.block_rows;
+    const int64_t r0 = (int64_t)(bid - T.block_begin) * R;
+    const int nrows = (int)min((int64_t)R, T.rows - r0);
+    const int64_t e0 = r0 * T.width;
+    const int ne = nrows * T.width;
+    const int n4 = ne >> 2;
+    const float b1 = tab.b1, b2 = tab.b2, omb1 = tab.omb1, omb2 = tab.omb2, eps = tab.eps;
+    const v4f *g4 = reinterpret_cast<const v4f *>(T.g + e0);
+    v4f *m4 = reinterpret_cast<v4f *>(T.m + e0);
+    v4f *v4 = reinterpret_cast<v4f *>(T.v + e0);
+    v4f *p4 = reinterpret_cast<v4f *>(T.p + e0);
+    auto row_of = [&](uint32_t le) {
+        return T.width == 1 ? (int)le : (int)__umulhi(le, T.wmagic);
+    };
 
-    for (int t = threadIdx.x; t < kSelRows; t += kAdamThreads) {
+    // Narrow tensors: every float4 of the block is loaded now (n4 <= kD * 256).
+    constexpr int kD = kSelDenseFloats / 4 / kAdamThreads;
+    v4f gq[kD], mq[kD], vq[kD], pq[kD];
+    if (T.mode == 1) {
+#pragma unroll
+        for (int u = 0; u < kD; ++u) {
+            const int q = (int)threadIdx.x + u * kAdamThreads;
+            if (q < n4) {
+                gq[u] = __builtin_nontemporal_load(g4 + q);
+                mq[u] = __builtin_nontemporal_load(m4 + q);
+                vq[u] = __builtin_nontemporal_load(v4 + q);
+                pq[u] = __builtin_nontemporal_load(p4 + q);
+            }
+        }
+    }
+
+    for (int t = threadIdx.x; t < R; t += kAdamThreads) {
         const int64_t r = r0 + t;
+        // On the whole-line paths the block's step counts are read (with
+        // the mask, not after it) and written whole, an invisible row's
+        // stored back unchanged.
+        const bool whole = t < nrows && T.mode != 0;
+        float k0 = whole ? T.steps[r] : 0.f;
         uint8_t vis = 0;
         if (t < nrows && r < tab.n_visible) vis = tab.visible[r] != 0;
+        if (vis && !whole) k0 = T.steps[r];
         float ss = 0.f;
         if (vis) {
             // Per-row bias correction in fp32, as torch evaluates
@@ -193,70 +282,90 @@ __global__ __launch_bounds__(kAdamThreads) void selective_adam_kernel(const SelT
             // power is formed in double as exp2(k log2 b), with log2 b from
             // the host: relative error ~1e-14 for any step count, far below
             // fp32's, at a fraction of a double pow's cost.
-            const float kf = T.steps[r] + 1.0f;
+            const float kf = k0 + 1.0f;
             const float pw1 = (float)exp2((double)kf * tab.l2b1);
             const float pw2 = (float)exp2((double)kf * tab.l2b2);
             const float bc1 = 1.0f - pw1;
             const float bc2 = 1.0f - pw2;
             ss = T.lr * (sqrtf(bc2) / bc1);
             T.steps[r] = kf;
+        } else if (whole) {
+            T.steps[r] = k0;
         }
         s_step_size[t] = ss;
         s_vis[t] = vis;
     }
     __syncthreads();
 
-    const int64_t e0 = r0 * T.width;
-    const float b1 = tab.b1, b2 = tab.b2, omb1 = tab.omb1, omb2 = tab.omb2, eps = tab.eps;
-    auto update = [&](int64_t i, int lr_) {
-        const float g = __builtin_nontemporal_load(T.g + i);
-        float m = __builtin_nontemporal_load(T.m + i) * b1 + g * omb1;
-        float v = __builtin_nontemporal_load(T.v + i) * b2 + g * g * omb2;
-        const float pn = __builtin_nontemporal_load(T.p + i) - s_step_size[lr_] * m /
-                         (sqrtf(v) + eps);
-        __builtin_nontemporal_store(m, T.m + i);
-        __builtin_nontemporal_store(v, T.v + i);
-        __builtin_nontemporal_store(pn, T.p + i);
-    };
-    if (T.wmagic != 0) {
-        // Four elements per thread per round, their loads issued together.
-        constexpr int kU = 4;
-        const uint32_t ne = (uint32_t)nrows * (uint32_t)T.width;
-        for (uint32_t l0 = threadIdx.x; l0 < ne; l0 += kU * kAdamThreads) {
-            float g[kU], m[kU], v[kU], pp[kU];
-            int row[kU];
+    if (T.mode == 1) {
+#pragma unroll
+        for (int u = 0; u < kD; ++u) {
+            const int q = (int)threadIdx.x + u * kAdamThreads;
+            if (q >= n4) continue;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = row_of(4u * (uint32_t)q + e);
+                if (!s_vis[row]) continue;
+                sel_update4(pq[u], gq[u], mq[u], vq[u], e, s_step_size[row], b1, b2, omb1,
+                            omb2, eps);
+            }
+            __builtin_nontemporal_store(mq[u], m4 + q);
+            __builtin_nontemporal_store(vq[u], v4 + q);
+            __builtin_nontemporal_store(pq[u], p4 + q);
+        }
+    } else if (T.mode == 2) {
+        // A chunk is 4 float4s; chunk c holds elements of rows row_of(16 c)
+        // through row_of(16 c + 15), at most two rows as width >= 16.
+        constexpr int kU = 2;
+        for (int q0 = threadIdx.x; q0 < n4; q0 += kU * kAdamThreads) {
+            v4f gw[kU], mw[kU], vw[kU], pw[kU];
             bool on[kU];
 #pragma unroll
             for (int u = 0; u < kU; ++u) {
-                const uint32_t le = l0 + u * kAdamThreads;
-                row[u] = T.width == 1 ? (int)le : (int)__umulhi(le, T.wmagic);
-                on[u] = le < ne && s_vis[min(row[u], kSelRows - 1)];
+                const int q = q0 + u * kAdamThreads;
+                const uint32_t first = (uint32_t)(q >> 2) * 16u;
+                const uint32_t last = min(first + 15u, (uint32_t)ne - 1u);
+                on[u] = q < n4 && (s_vis[min(row_of(first), R - 1)] |
+                                   s_vis[min(row_of(last), R - 1)]);
                 if (on[u]) {
-                    const int64_t i = e0 + le;
-                    g[u] = __builtin_nontemporal_load(T.g + i);
-                    m[u] = __builtin_nontemporal_load(T.m + i);
-                    v[u] = __builtin_nontemporal_load(T.v + i);
-                    pp[u] = __builtin_nontemporal_load(T.p + i);
+                    gw[u] = __builtin_nontemporal_load(g4 + q);
+                    mw[u] = __builtin_nontemporal_load(m4 + q);
+                    vw[u] = __builtin_nontemporal_load(v4 + q);
+                    pw[u] = __builtin_nontemporal_load(p4 + q);
                 }
             }
 #pragma unroll
             for (int u = 0; u < kU; ++u) {
                 if (!on[u]) continue;
-                const int64_t i = e0 + l0 + u * kAdamThreads;
-                const float mn = m[u] * b1 + g[u] * omb1;
-                const float vn = v[u] * b2 + g[u] * g[u] * omb2;
-                const float pn = pp[u] - s_step_size[row[u]] * mn / (sqrtf(vn) + eps);
-                __builtin_nontemporal_store(mn, T.m + i);
-                __builtin_nontemporal_store(vn, T.v + i);
-                __builtin_nontemporal_store(pn, T.p + i);
+                const int q = q0 + u * kAdamThreads;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int row = row_of(4u * (uint32_t)q + e);
+                    if (!s_vis[row]) continue;
+                    sel_update4(pw[u], gw[u], mw[u], vw[u], e, s_step_size[row], b1, b2,
+                                omb1, omb2, eps);
+                }
+                __builtin_nontemporal_store(mw[u], m4 + q);
+                __builtin_nontemporal_store(vw[u], v4 + q);
+                __builtin_nontemporal_store(pw[u], p4 + q);
             }
         }
-    } else {
-        const int64_t ne = (int64_t)nrows * T.width;
-        for (int64_t le = threadIdx.x; le < ne; le += kAdamThreads) {
-            const int lr_ = (int)(le / T.width);
-            if (s_vis[lr_]) update(e0 + le, lr_);
-        }
+    }
+    // Elements past the block's last float4 (whole-line paths), or all of
+    // them (element path), one by one.
+    for (int le = (T.mode != 0 ? 4 * n4 : 0) + (int)threadIdx.x; le < ne;
+         le += kAdamThreads) {
+        const int row = T.wmagic != 0 ? row_of((uint32_t)le) : le / T.width;
+        if (!s_vis[row]) continue;
+        const int64_t i = e0 + le;
+        float pp = __builtin_nontemporal_load(T.p + i);
+        float mm = __builtin_nontemporal_load(T.m + i);
+        float vv = __builtin_nontemporal_load(T.v + i);
+        sel_update(pp, __builtin_nontemporal_load(T.g + i), mm, vv, s_step_size[row], b1, b2,
+                   omb1, omb2, eps);
+        __builtin_nontemporal_store(mm, T.m + i);
+        __builtin_nontemporal_store(vv, T.v + i);
+        __builtin_nontemporal_store(pp, T.p + i);
     }
 }
 
@@ -347,9 +456,16 @@ int32_t mg_selective_adam_step(int32_t count, float *const *p,
     tab.n_visible = n_visible;
     tab.l2b1 = std::log2((double)tab.b1);
     tab.l2b2 = std::log2((double)tab.b2);
+    // Widest tensors first: their workgroups are the longest, and the short
+    // ones then fill the tail of the launch.
+    int order[kAdamMaxTensors];
+    for (int i = 0; i < count; ++i) order[i] = i;
+    std::stable_sort(order, order + count,
+                     [&](int a, int b) { return width[a] > width[b]; });
     int64_t blocks = 0;
     int c = 0;
-    for (int i = 0; i < count; ++i) {
+    for (int oi = 0; oi < count; ++oi) {
+        const int i = order[oi];
         MG_REQUIRE(rows[i] >= 0 && width[i] >= 1,
                    "mg_selective_adam_step: tensor %d has rows %lld width %d", i,
                    (long long)rows[i], width[i]);
@@ -368,8 +484,12 @@ int32_t mg_selective_adam_step(int32_t count, float *const *p,
         T.wmagic = width[i] == 1 ? 1u : width[i] < 256
             ? (uint32_t)(((1ULL << 32) + (uint64_t)width[i] - 1) / (uint64_t)width[i]) : 0u;
         T.lr = lr[i];
+        const bool aligned = (((uintptr_t)p[i] | (uintptr_t)g[i] | (uintptr_t)m[i] |
+                               (uintptr_t)v[i] | (uintptr_t)steps[i]) & 15) == 0;
+        T.mode = !aligned || T.wmagic == 0 ? 0 : width[i] < kSelWideMin ? 1 : 2;
+        T.block_rows = sel_block_rows(width[i], T.mode);
         T.block_begin = (int32_t)blocks;
-        blocks += ceil_div(rows[i], kSelRows);
+        blocks += ceil_div(rows[i], (int64_t)T.block_rows);
     }
     tab.count = c;
     if (c == 0) return MG_OK;

@@ -204,3 +204,68 @@ def test_selective_adam_dense_auxiliary_group(dev):
         dense.step()
     assert torch.allclose(app, ref, atol=1e-6)
     assert "step" in opt.state[app] and "steps" not in opt.state[app]
+
+
+# Widths on each of the kernel's paths: narrow tensors moved whole (1-15
+# floats per row), wide tensors skipped per 64-byte chunk (16-255), and the
+# element-by-element path (256 and up, or any tensor not 16-byte aligned).
+@pytest.mark.parametrize("width", [1, 2, 3, 4, 5, 8, 15, 16, 17, 31, 32, 45, 64, 255, 300])
+@pytest.mark.parametrize("aligned", [True, False])
+def test_selective_adam_every_path_through_the_c_abi(dev, width, aligned):
+    """mg_selective_adam_step on ragged row counts (one, a partial block, a
+    block boundary and past it) and masks shorter than the tensor, dense to
+    empty: visible rows within 1e-6 of the restatement with exact step
+    counts, every other row (parameters, moments and step count) bit-for-bit
+    as it was."""
+    from metal_gauss_amd import _lib
+
+    lib = _lib.load()
+    rng = np.random.default_rng(width * 2 + aligned)
+    for rows, n_vis, dens in ((1, 1, 1.0), (63, 50, 0.6), (64, 64, 0.05), (1025, 1000, 0.6),
+                              (2111, 2111, 1.0), (700, 700, 0.0)):
+        host = {k: rng.standard_normal((rows, width)).astype(np.float32) for k in "pg"}
+        host["g"] *= np.float32(1e-3)
+        host["m"] = (rng.random((rows, width)) * 1e-3).astype(np.float32)
+        host["v"] = (rng.random((rows, width)) * 1e-6).astype(np.float32)
+        steps0 = rng.integers(0, 5, rows).astype(np.float32)
+        vis = rng.random(n_vis) < dens
+        off = 0 if aligned else 1
+        dev_t = {}
+        for k, a in host.items():
+            buf = torch.zeros(a.size + off, device=dev)
+            buf[off:] = torch.from_numpy(a.ravel()).to(dev)
+            dev_t[k] = buf
+        st_buf = torch.zeros(rows + off, device=dev)
+        st_buf[off:] = torch.from_numpy(steps0).to(dev)
+        vis_d = torch.from_numpy(vis).to(dev)
+
+        def ptr(t):
+            return t.data_ptr() + 4 * off
+
+        _lib.check(lib.mg_selective_adam_step(
+            1, _lib.ptr_array([ptr(dev_t["p"])]), _lib.ptr_array([ptr(dev_t["g"])]),
+            _lib.ptr_array([ptr(dev_t["m"])]), _lib.ptr_array([ptr(dev_t["v"])]),
+            _lib.ptr_array([ptr(st_buf)]), _lib.i64_array([rows]), _lib.i32_array([width]),
+            _lib.f32_array([1e-2]), vis_d.data_ptr(), n_vis, 0.9, 0.999, 1e-15,
+            _lib.stream(vis_d)))
+        torch.cuda.synchronize()
+        got = {k: t[off:].cpu().numpy().reshape(rows, width) for k, t in dev_t.items()}
+        got_steps = st_buf[off:].cpu().numpy()
+        want = {k: a.copy() for k, a in host.items()}
+        want_steps = steps0.copy()
+        adam_ref.selective_adam_step(want["p"], want["g"], want["m"], want["v"], want_steps,
+                                     vis, 1e-2, 0.9, 0.999, 1e-15)
+        case = f"rows={rows} n_vis={n_vis} dens={dens}"
+        assert np.array_equal(got_steps, want_steps), case
+        assert np.array_equal(got["g"], host["g"]), case
+        seen = np.zeros(rows, bool)
+        seen[:n_vis] = vis
+        for k in "pmv":
+            assert np.array_equal(got[k][~seen], host[k][~seen]), (case, k)
+        if seen.any():
+            assert _max_rel_step(got["p"], want["p"], host["p"]) < 1e-6, case
+            for k in "mv":
+                # A one-ulp difference of a multiply-add at the moment's
+                # magnitude is the only slack.
+                np.testing.assert_allclose(got[k][seen], want[k][seen], rtol=1e-6,
+                                           atol=1e-6 * np.abs(want[k]).max(), err_msg=case)
