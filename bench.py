@@ -86,6 +86,10 @@ def parse():
     ap.add_argument("--counter-summary", nargs="+", metavar="DIR",
                     help="print the per-kernel counter summary of rocprofv3 --pmc runs (one "
                          "directory per pass, with a kernel_stats.csv among them) and exit")
+    ap.add_argument("--lists", choices=["capacity", "sync"], default="capacity",
+                    help="tile-list sizing in the timed step: capacity-sized with a device "
+                         "overflow check (no host read inside the step; default), or by a "
+                         "host read of the total in every render as the reference")
     ap.add_argument("--reg", action="store_true",
                     help="add the reference trainer's opacity and scale regularisers, "
                          "0.01 mean sigmoid(logit) + 0.01 mean exp(log_scales) "
@@ -131,10 +135,10 @@ def copy_calibration(mib):
 class Step:
     """The config-4 training step on the GPU."""
 
-    def __init__(self, n, dev, variant="base", reg=False):
+    def __init__(self, n, dev, variant="base", reg=False, lists="capacity"):
         import torch
 
-        from metal_gauss_amd import FusedAdam, gaussian_kernel, scenes
+        from metal_gauss_amd import FusedAdam, ListCapacity, gaussian_kernel, scenes
 
         sc, cams, self.bg = scenes.config4(n)
         sc = sc.to(dev)
@@ -158,6 +162,11 @@ class Step:
         self.last_isect = 0
         self.variant = variant
         self.reg = reg
+        # "capacity": tile lists sized by a ListCapacity, no host read inside
+        # the step (an overflowed step changes nothing and runs again);
+        # "sync": sized by reading the total on the host, as the reference.
+        self.cap = ListCapacity() if lists == "capacity" else None
+        self.reruns = 0
         self.f3d = None
         self.f3d_ms = None
         if variant in ("mip", "mip-torch"):
@@ -183,12 +192,27 @@ class Step:
         return (time.perf_counter() - t0) * 1e3
 
     def __call__(self, adam=True):
+        v = self.order[self.k % len(self.order)]
+        self.k += 1
+        while True:
+            loss, info = self.once(v, adam)
+            if self.cap is None:
+                self.last_isect = info["isect_total"]
+                return loss
+            if not self.cap.overflowed():
+                self.last_isect = self.cap.last_total
+                return loss
+            # The lists overflowed: the kernels changed nothing; the step
+            # counts are taken back and the step runs again, larger.
+            self.reruns += 1
+            if adam:
+                self.opt.rewind()
+
+    def once(self, v, adam):
         import torch
 
         from metal_gauss_amd import photometric_loss, render
 
-        v = self.order[self.k % len(self.order)]
-        self.k += 1
         cam, gt, p = self.cams[v], self.targets[v], self.p
         # exp(log_scales) and sigmoid(logit_opac) (train.py:221-222) run inside
         # the projection kernel and its backward; the "-torch" variants take
@@ -221,9 +245,12 @@ class Step:
             scales, opac = apply_3d_filter(torch.exp(scales), torch.sigmoid(opac), self.f3d)
             kw = dict(antialias=True)
             torch_reg = self.reg
+        cap = None if self.cap is None else self.cap.value
         rgb, alpha, info = render(p["means"], p["quats"], scales, opac, p["sh_dc"], cam.K,
                                   cam.viewmat, cam.W, cam.H, sh_degree=3, sh_rest=p["sh_rest"],
-                                  background=self.bg, **kw)
+                                  background=self.bg, list_capacity=cap, **kw)
+        if self.cap is not None:
+            self.cap.watch(info["lists_status"])
         # 0.8 * |rgb - gt|.mean() + 0.2 * (1 - ssim(rgb, gt)) (train.py:389-390), fused.
         loss, _ = photometric_loss(rgb, gt, self.window, 0.2)
         if torch_reg:
@@ -236,10 +263,9 @@ class Step:
         self.opt.zero_grad(set_to_none=True)
         loss.backward()
         if adam:
-            self.opt.step()
-        self.last_isect = info["isect_total"]
+            self.opt.step(skip=info["lists_status"])
         self.last_valid = info["valid_mask"]
-        return loss
+        return loss, info
 
 
 def algorithmic_bytes(kernel, N, I, P, T, f_valid, n_floats):
@@ -273,7 +299,7 @@ def gpu_bench(args):
     from metal_gauss_amd import _lib
 
     dev = torch.device("cuda:0")
-    step = Step(args.gaussians, dev, args.variant, reg=args.reg)
+    step = Step(args.gaussians, dev, args.variant, reg=args.reg, lists=args.lists)
     # Clock ramp as the reference's bench/quick.py:110-133 does (2 s of
     # sustained load), with forward + backward only so the parameters the
     # timed steps start from are untouched; then the warm-up steps.
@@ -287,6 +313,7 @@ def gpu_bench(args):
     # event between consecutive steps on the stream the kernels run on (the
     # median per step).
     events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    reruns0 = step.reruns
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for k in range(args.steps):
@@ -297,6 +324,23 @@ def gpu_bench(args):
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     per_step = sorted(events[k].elapsed_time(events[k + 1]) for k in range(args.steps))
     median_ms = per_step[len(per_step) // 2]
+
+    reruns = step.reruns - reruns0
+    # The same steps with the lists sized by a host read in every render (the
+    # reference's way), fewer of them.
+    sync_ms = None
+    if step.cap is not None:
+        cap, step.cap = step.cap, None
+        nsync = max(10, args.steps // 4)
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(nsync):
+            step()
+        torch.cuda.synchronize()
+        sync_ms = (time.perf_counter() - t0) * 1e3 / nsync
+        step.cap = cap
 
     # fwd+bwd alone (no optimizer step), fewer iterations.
     nfb = max(10, args.steps // 4)
@@ -345,7 +389,61 @@ def gpu_bench(args):
     work = raster_work(step, kern)
     return dict(ms=ms, median_ms=median_ms, fb_ms=fb_ms, kernels=rows, dominant=dominant,
                 achieved=achieved, nbytes=nbytes, I=I, f_valid=f_valid, n_floats=n_floats,
-                f3d_ms=f3d_ms, work=work, copy=stream_copy())
+                f3d_ms=f3d_ms, work=work, copy=stream_copy(), reruns=reruns, sync_ms=sync_ms,
+                fwd=forward_fps(step))
+
+
+def forward_fps(step, frames=100):
+    """Forward-only rendering of the step's views at its current
+    parameters (no autograd): frames enqueued back to back with
+    capacity-sized lists (an overflowed frame found one frame later is
+    rendered again), and one synchronised frame at a time with the lists
+    sized by a host read, the reference's way (bench/render_fps.py:30-44)."""
+    import torch
+
+    from metal_gauss_amd import ListCapacity, render
+
+    p = step.p
+    views = [step.cams[step.order[i % len(step.order)]] for i in range(frames)]
+
+    def frame(cam, cap):
+        return render(p["means"], p["quats"], p["log_scales"], p["logit_opac"], p["sh_dc"],
+                      cam.K, cam.viewmat, cam.W, cam.H, sh_degree=3, sh_rest=p["sh_rest"],
+                      background=step.bg, activations=True, list_capacity=cap)
+
+    cap = ListCapacity(initial=step.cap.value if step.cap is not None else 0)
+    redo = 0
+    with torch.no_grad():
+        for rep in range(2):              # the first pass sizes the capacity
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            tickets = []
+            for i, cam in enumerate(views):
+                _, _, info = frame(cam, cap.value)
+                tickets.append(cap.watch(info["lists_status"]))
+                if i and cap.overflowed(tickets[i - 1]):
+                    redo += rep
+                    _, _, info = frame(views[i - 1], cap.value)
+                    cap.overflowed(cap.watch(info["lists_status"]))
+            if cap.overflowed(tickets[-1]):
+                redo += rep
+                frame(views[-1], cap.value)
+            torch.cuda.synchronize()
+            pipelined = (time.perf_counter() - t0) * 1e3 / frames
+        ts = []
+        for cam in views[:30]:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            frame(cam, None)
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+    ts.sort()
+    sync_ms = 1e3 * ts[len(ts) // 2]
+    return {"pipelined_capacity_lists": {"ms_per_frame": round(pipelined, 4),
+                                         "fps": round(1e3 / pipelined, 1), "rerendered": redo},
+            "synchronised_sync_lists": {"ms_per_frame": round(sync_ms, 4),
+                                        "fps": round(1e3 / sync_ms, 1)},
+            "frames": frames, "workload": "config-4 views, 1M Gaussians, 800x800"}
 
 
 def raster_work(step, kern, views=8):
@@ -1185,6 +1283,12 @@ def main():
         "kernels": r["kernels"],
         "raster_work": r["work"],
         "stream_copy": r["copy"],
+        "tile_lists": {
+            "sizing": args.lists,
+            "reruns_in_timed_steps": r["reruns"],
+            "sync_lists_ms_per_step": None if r["sync_ms"] is None else round(r["sync_ms"], 4),
+        },
+        "forward_fps": r["fwd"],
     }
     if args.variant != "base":
         out["config"]["workload"] += {

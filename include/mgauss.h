@@ -158,6 +158,11 @@ typedef struct mg_adam_epilogue {
     double lr[6];
     int64_t step[6];
     double beta1, beta2, eps;
+    /* NULL, or the status words of the render's capacity-bounded tile lists
+     * (mg_bin_lists_capped, device): when skip[1] != 0 (the lists
+     * overflowed) the launch does nothing at all, so the step can be run
+     * again with larger lists. */
+    const int64_t *skip;
 } mg_adam_epilogue;
 
 /* Analytic backward of mg_preprocess_forward_mip. d_opacity_eff is the
@@ -391,6 +396,30 @@ int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy,
                             void *finish_workspace,
                             int64_t finish_workspace_bytes, mg_stream_t stream);
 
+/* Tile lists with no host read: the lists of mg_bin_lists_begin + _finish,
+ * built in one call into buffers sized by the caller's capacity, so that a
+ * render (or a training step) can be enqueued, or captured, whole. The
+ * intersection total stays on the device: status (device, 2 int64) receives
+ * status[0] = the total and status[1] = 1 if it exceeds capacity, else 0.
+ * Within capacity, gauss_ids[0 .. total) and tile_offsets equal the two-call
+ * result; past it every list is empty (tile_offsets all 0) and the caller
+ * renders again with capacity >= status[0]. Entries of gauss_ids past the
+ * kept pairs (all of them after an overflow) are unspecified (past 4096
+ * tiles the sort uses the buffer as scratch). gauss_ids: (capacity,), may
+ * be NULL when capacity is 0; tile_offsets: (tiles_x*tiles_y + 1,); one
+ * workspace of mg_bin_lists_capped_workspace_bytes(N, capacity) bytes.
+ * Replaces the .item() read that sizes the reference's pair buffers
+ * (metal_gauss/metal_backend.py:246-248) with a device-side check. */
+int64_t mg_bin_lists_capped_workspace_bytes(int64_t N, int64_t capacity);
+int32_t mg_bin_lists_capped(int64_t N, const float *uv, const float *rxy,
+                            const float *conic, const float *opacity,
+                            const int32_t *valid, const float *depth, int32_t W,
+                            int32_t H, int32_t tile, int32_t tiles_x,
+                            int32_t tiles_y, int64_t capacity,
+                            int32_t *gauss_ids, int32_t *tile_offsets,
+                            int64_t *status, void *workspace,
+                            int64_t workspace_bytes, mg_stream_t stream);
+
 /* -------------------------------------------------------------- rasteriser */
 
 /* Front-to-back compositing, one workgroup per tile, one thread per pixel.
@@ -471,6 +500,19 @@ int32_t mg_adam_step_multi(int32_t count, float *const *p,
                            const double *lr, const int64_t *step, double beta1,
                            double beta2, double eps, int32_t eps_inside,
                            mg_stream_t stream);
+
+/* mg_adam_step_multi that does nothing when skip[1] != 0, skip (device, 2
+ * int64) being the status of capacity-bounded tile lists
+ * (mg_bin_lists_capped): the step of a render whose lists overflowed leaves
+ * every parameter and moment as it was, to be run again. No counterpart in
+ * the reference, whose tile lists are sized by a host read. */
+int32_t mg_adam_step_multi_guarded(int32_t count, float *const *p,
+                                   const float *const *g, float *const *m,
+                                   float *const *v, const int64_t *n,
+                                   const double *lr, const int64_t *step,
+                                   double beta1, double beta2, double eps,
+                                   int32_t eps_inside, const int64_t *skip,
+                                   mg_stream_t stream);
 
 /* Row-masked Adam with a per-row float step count, over up to 32 tensors in
  * one launch. Tensor k has rows[k] rows of width[k] floats; rows r with

@@ -13,6 +13,7 @@ Public surface (names of the reference's modules):
     mcmc                   relocate / grow / add_noise / reset_adam_state
     io                     Splats, load_ply, save_ply, export_ply
     ext                    the reference's native-extension functions (backend._load())
+    ListCapacity           tile-list sizing without a host read (render(list_capacity=))
 """
 
 from .api import BACKENDS, render  # noqa: F401
@@ -20,6 +21,7 @@ from .fused_adam import FusedAdam  # noqa: F401
 from .selective_adam import SelectiveAdam  # noqa: F401
 from .ssim import gaussian_kernel, photometric_loss, ssim  # noqa: F401
 from .mipfilter import apply_3d_filter, compute_3d_filter  # noqa: F401
+from .backend import ListCapacity  # noqa: F401
 from . import backend, ext  # noqa: F401
 
 __version__ = "0.1.0"

@@ -81,6 +81,9 @@ _SIGNATURES = {
                                   _i32, _vp, _i64, _vp, _vp]),
     "mg_bin_lists_finish": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                    _i32, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
+    "mg_bin_lists_capped_workspace_bytes": (_i64, [_i64, _i64]),
+    "mg_bin_lists_capped": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
+                                   _i32, _i64, _vp, _vp, _vp, _vp, _i64, _vp]),
     "mg_rasterize_chunk_workspace_bytes": (_i64, [_i64, _i32, _i32]),
     "mg_rasterize_forward": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                     _f32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -91,6 +94,9 @@ _SIGNATURES = {
     "mg_adam_step_multi": (_i32, [_i32, _pp, _pp, _pp, _pp, ctypes.POINTER(_i64),
                                   ctypes.POINTER(_f64), ctypes.POINTER(_i64), _f64, _f64, _f64,
                                   _i32, _vp]),
+    "mg_adam_step_multi_guarded": (_i32, [_i32, _pp, _pp, _pp, _pp, ctypes.POINTER(_i64),
+                                          ctypes.POINTER(_f64), ctypes.POINTER(_i64), _f64, _f64,
+                                          _f64, _i32, _vp, _vp]),
     "mg_selective_adam_step": (_i32, [_i32, _pp, _pp, _pp, _pp, _pp, ctypes.POINTER(_i64),
                                       ctypes.POINTER(_i32), ctypes.POINTER(_f32), _vp, _i64,
                                       _f64, _f64, _f64, _vp]),
@@ -171,7 +177,8 @@ class AdamEpilogue(ctypes.Structure):
     """mg_adam_epilogue (include/mgauss.h): the preprocess backward's
     optimizer epilogue over means, quats, scales, opacities, sh, sh_rest."""
     _fields_ = [("p", _vp * 6), ("m", _vp * 6), ("v", _vp * 6), ("lr", _f64 * 6),
-                ("step", _i64 * 6), ("beta1", _f64), ("beta2", _f64), ("eps", _f64)]
+                ("step", _i64 * 6), ("beta1", _f64), ("beta2", _f64), ("eps", _f64),
+                ("skip", _vp)]
 
 
 def ptr_array(ptrs):

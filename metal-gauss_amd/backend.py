@@ -147,6 +147,92 @@ def _bin(uv, rxy, depth, valid_i, conic, opacity, W, H, tile):
     return gauss_ids, tile_offsets, tx
 
 
+def _bin_capped(uv, rxy, depth, valid_i, conic, opacity, W, H, tile, capacity):
+    """The lists of ``_bin`` with no host read (mg_bin_lists_capped): ids in a
+    (capacity,) buffer, and a device int64 (2,) status = (intersection
+    total, 1 if it exceeded ``capacity`` else 0). After an overflow every
+    list is empty. Returns (gauss_ids, tile_offsets, tiles_x, status)."""
+    lib = _lib.load()
+    device = uv.device
+    tx, ty = _tile_grid(W, H, tile)
+    N = uv.shape[0]
+    capacity = int(capacity)
+    if capacity < 0 or capacity >= 2 ** 31:
+        raise ValueError(f"list capacity {capacity} outside [0, 2^31)")
+    s = _lib.stream(uv)
+    gauss_ids = torch.empty(capacity, dtype=torch.int32, device=device)
+    tile_offsets = torch.empty(tx * ty + 1, dtype=torch.int32, device=device)
+    status = torch.empty(2, dtype=torch.int64, device=device)
+    ws = torch.empty(lib.mg_bin_lists_capped_workspace_bytes(N, capacity), dtype=torch.uint8,
+                     device=device)
+    _lib.check(lib.mg_bin_lists_capped(
+        N, _lib.dev_tensor(uv, "uv"), _lib.dev_tensor(rxy, "rxy"),
+        _lib.dev_tensor(conic, "conic") if conic is not None else None,
+        _lib.dev_tensor(opacity, "opacity") if opacity is not None else None,
+        _lib.dev_tensor(valid_i, "valid", torch.int32), _lib.dev_tensor(depth, "depth"),
+        W, H, tile, tx, ty, capacity, gauss_ids.data_ptr() if capacity else None,
+        tile_offsets.data_ptr(), status.data_ptr(), ws.data_ptr(), ws.numel(), s))
+    return gauss_ids, tile_offsets, tx, status
+
+
+class ListCapacity:
+    """Sizes a render's tile lists without a host read in the render.
+
+    ``render(..., list_capacity=cap.value)`` builds the lists in buffers of
+    that many intersections and reports, on the device, the total and
+    whether it overflowed (``info["lists_status"]``); an overflowed render
+    has empty lists (a background image), and optimizer steps given that
+    status as ``skip`` leave every parameter as it was. ``watch`` queues a
+    copy of the status to pinned host memory right after the render and
+    returns a ticket; ``overflowed(ticket)`` waits for that copy only (by
+    then the rest of the step, or the next frame, is usually enqueued
+    behind it) and, on overflow, raises ``value`` to ``headroom`` times the
+    total seen, for that render to be run again. Up to ``depth`` watched
+    renders may be outstanding. The reference sizes its buffers by reading
+    the total on the host in the middle of every render
+    (metal_backend.py:246-248), which drains the queue once per render.
+    """
+
+    def __init__(self, initial: int = 0, headroom: float = 1.25, depth: int = 4):
+        self.value = int(initial)
+        self.headroom = float(headroom)
+        self.depth = int(depth)
+        self.last_total = None
+        self.overflows = 0
+        self._slots = None
+        self._events = None
+        self._issued = 0
+
+    def watch(self, status: torch.Tensor) -> int:
+        if self._slots is None:
+            self._slots = torch.zeros(self.depth, 2, dtype=torch.int64, pin_memory=True)
+            self._events = [torch.cuda.Event() for _ in range(self.depth)]
+        ticket = self._issued
+        k = ticket % self.depth
+        self._slots[k].copy_(status, non_blocking=True)
+        self._events[k].record(torch.cuda.current_stream(status.device))
+        self._issued += 1
+        return ticket
+
+    def overflowed(self, ticket: int | None = None) -> bool:
+        """Whether the render watched under ``ticket`` (default: the latest)
+        overflowed; waits for its status copy."""
+        if ticket is None:
+            ticket = self._issued - 1
+        if ticket < 0 or ticket >= self._issued or ticket < self._issued - self.depth:
+            raise RuntimeError(f"ListCapacity: no outstanding watch for ticket {ticket}")
+        k = ticket % self.depth
+        self._events[k].synchronize()
+        total, over = int(self._slots[k, 0]), int(self._slots[k, 1])
+        self.last_total = total
+        if over:
+            self.overflows += 1
+            self.value = max(self.value, int(math.ceil(total * self.headroom)), total)
+            if self.value >= 2 ** 31:
+                raise RuntimeError(f"{total} tile intersections exceed the int32 index range")
+        return bool(over)
+
+
 def _bin_keys64(uv, rxy, depth, valid_i, conic, opacity, W, H, tile):
     """The same lists through the reference's ABI pipeline: mg_bin_count ->
     mg_exclusive_scan_i32 -> mg_bin_write (64-bit (tile|depth) keys) ->
@@ -498,7 +584,8 @@ class _PreprocessMip(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means, quats, scales, opacities, sh, sh_rest, filter_3d, antialias,
                 viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
-                sh_degree, valid_mask=None, activations=0, optimizer=None, reg=None):
+                sh_degree, valid_mask=None, activations=0, optimizer=None, reg=None,
+                lists=None):
         lib = _lib.load()
         N = means.shape[0]
         dev = means.device
@@ -542,6 +629,9 @@ class _PreprocessMip(torch.autograd.Function):
         ctx.activations = int(activations)
         ctx.optimizer = optimizer
         ctx.reg = _reg_coefficients(reg, N)
+        # render() puts the status of capacity-bounded lists here once they
+        # are built: the epilogue's update is skipped if they overflowed.
+        ctx.lists = lists
         ctx.meta = (viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
                     sh_degree)
         ctx.mark_non_differentiable(depth, rxy, valid)
@@ -575,7 +665,7 @@ class _PreprocessMip(torch.autograd.Function):
                 opacities.data_ptr(), None if filt is None else filt.data_ptr(),
                 int(ctx.antialias), ctx.activations, *ctx.reg, p_oe, None, None, None, None,
                 None, None, ctypes.byref(epi), _lib.stream(means)))
-            return (None,) * 25
+            return (None,) * 26
         d_means = torch.empty(N, 3, device=dev)
         d_quats = torch.empty(N, 4, device=dev)
         d_scales = torch.empty(N, 3, device=dev)
@@ -595,7 +685,7 @@ class _PreprocessMip(torch.autograd.Function):
             d_scales.data_ptr(), None if d_sh is None else d_sh.data_ptr(),
             None if d_rest is None else d_rest.data_ptr(), d_op.data_ptr(), None,
             _lib.stream(means)))
-        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 19
+        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 20
 
 
 def _reg_coefficients(reg, n):
@@ -624,7 +714,10 @@ def _epilogue(ctx, params, sh_degree):
     sh, rest = params[4], params[5]
     if sh.data_ptr() % 16 or (rest is not None and rest.data_ptr() % 16):
         return None
-    return opt.epilogue(list(params))
+    skip = ctx.lists[0] if ctx.lists else None
+    if skip is None:
+        return opt.epilogue(list(params))
+    return opt.epilogue(list(params), skip=skip)
 
 
 # Names that describe this backend rather than the reference's.
@@ -697,7 +790,8 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
            sh_rest=None, antialias: bool = False, absgrad_out=None,
            min_transmittance: float = DEFAULT_T_MIN, chunked_backward: bool = False,
            filter_3d=None, activations: bool = False, optimizer=None,
-           opacity_reg: float = 0.0, scale_reg: float = 0.0, **_ignored):
+           opacity_reg: float = 0.0, scale_reg: float = 0.0, list_capacity: int | None = None,
+           **_ignored):
     """Render Gaussians from one camera; same signature as the reference's.
 
     means (N,3) world; quats (N,4) wxyz (need not be normalised); scales (N,3)
@@ -737,6 +831,14 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     ``.grad`` after their update: ``step()`` then raises instead of updating
     them a second time. When the optimizer or the tensors do not allow the
     epilogue, the ordinary gradients are returned.
+    ``list_capacity`` (an int, see ``ListCapacity``) builds the tile lists
+    in buffers of that many intersections with no host read, so the render
+    enqueues without waiting for the GPU. ``info["lists_status"]`` is then a
+    device int64 (2,): the intersection total, and 1 if it exceeded the
+    capacity, in which case every list is empty (the image is the
+    background), the epilogue of ``optimizer`` does nothing, and the caller
+    renders again with a larger capacity. ``info["isect_total"]`` is then
+    that device total (0-d) instead of an int.
     """
     explicit_colors = colors is not None
     opacities_in = opacities
@@ -757,6 +859,8 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     reg = None
     if opacity_reg or scale_reg:
         reg = (float(opacity_reg), float(scale_reg))
+    # The epilogue's skip word, filled in once the lists are built.
+    lists = [None] if list_capacity is not None else None
     if (filter_3d is not None or antialias or activations or optimizer is not None
             or reg is not None):
         # Both filters (and the activations) in the projection kernel; the
@@ -774,7 +878,7 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
             uv, conic, depth, rxy, valid_i, colors, opacities = _PreprocessMip.apply(
                 means, quats, scales, opacities, sh_in, rest_in, filter_3d, antialias, vm_h,
                 fx, fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree,
-                valid_b, act, optimizer, reg)
+                valid_b, act, optimizer, reg, lists)
     elif explicit_colors:
         uv, conic, depth, rxy, valid_i = _PreprocessMetal.apply(
             means, quats, scales, None, None, opacities.detach(), vm_h, fx, fy, cx, cy, W, H,
@@ -786,9 +890,17 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
             means, quats, scales, sh_in, rest_in, opacities.detach(), vm_h, fx, fy, cx, cy,
             W, H, near, far, 0.3, max_radius, cam_center, sh_degree, valid_b)
 
-    gauss_ids, tile_offsets, tiles_x = build_tile_lists_metal(
-        uv.detach(), rxy.detach(), depth.detach(), valid_i, conic.detach(),
-        opacities.detach(), W, H, tile)
+    status = None
+    if list_capacity is None:
+        gauss_ids, tile_offsets, tiles_x = build_tile_lists_metal(
+            uv.detach(), rxy.detach(), depth.detach(), valid_i, conic.detach(),
+            opacities.detach(), W, H, tile)
+    else:
+        gauss_ids, tile_offsets, tiles_x, status = _bin_capped(
+            uv.detach().contiguous(), rxy.detach().contiguous(), depth.detach().contiguous(),
+            valid_i.contiguous(), conic.detach().contiguous(), opacities.detach().contiguous(),
+            W, H, tile, list_capacity)
+        lists[0] = status
 
     # A constant background (tuple, list or CPU tensor without grad) is
     # blended inside the raster kernels; a device or trainable one by the
@@ -811,7 +923,8 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     return rgb, alpha, {
         "uv": uv,
         "tiles": int(tile_offsets.numel() - 1),
-        "isect_total": int(gauss_ids.numel()),
+        "isect_total": int(gauss_ids.numel()) if status is None else status[0],
+        "lists_status": status,
         "isect_dropped": 0,
         "isect_dropped_frac": 0.0,
         "valid_mask": valid_b,

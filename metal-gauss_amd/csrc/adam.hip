@@ -58,6 +58,7 @@ struct AdamTable {
     int32_t count;
     float b1, b2, omb1, omb2, eps;   // omb = 1 - beta, formed in double
     int32_t eps_inside;
+    const int64_t *skip;             // NULL, or do nothing when skip[1] != 0
 };
 
 __device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v,
@@ -68,6 +69,7 @@ __device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v,
 }
 
 __global__ __launch_bounds__(kAdamThreads) void adam_multi_kernel(const AdamTable tab) {
+    if (tab.skip && tab.skip[1] != 0) return;
     // Find this workgroup's tensor: a uniform linear scan over <= 32 entries.
     int k = 0;
     const int bid = blockIdx.x;
@@ -380,6 +382,15 @@ int32_t mg_adam_step_multi(int32_t count, float *const *p, const float *const *g
                            const double *lr, const int64_t *step, double beta1,
                            double beta2, double eps, int32_t eps_inside,
                            mg_stream_t stream) {
+    return mg_adam_step_multi_guarded(count, p, g, m, v, n, lr, step, beta1, beta2, eps,
+                                      eps_inside, nullptr, stream);
+}
+
+int32_t mg_adam_step_multi_guarded(int32_t count, float *const *p, const float *const *g,
+                                   float *const *m, float *const *v, const int64_t *n,
+                                   const double *lr, const int64_t *step, double beta1,
+                                   double beta2, double eps, int32_t eps_inside,
+                                   const int64_t *skip, mg_stream_t stream) {
     MG_REQUIRE(count >= 0 && count <= kAdamMaxTensors,
                "mg_adam_step_multi: %d tensors, at most %d per launch", count,
                kAdamMaxTensors);
@@ -393,6 +404,7 @@ int32_t mg_adam_step_multi(int32_t count, float *const *p, const float *const *g
     tab.omb2 = (float)(1.0 - beta2);
     tab.eps = (float)eps;
     tab.eps_inside = eps_inside;
+    tab.skip = skip;
     int64_t blocks = 0;
     int c = 0;
     for (int i = 0; i < count; ++i) {

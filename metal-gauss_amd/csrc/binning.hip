@@ -537,10 +537,14 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
 // One workgroup scans the count pass's per-workgroup totals: part_off[i] is
 // the first pair of count workgroup i's Gaussians, st->total the intersection
 // total.
+// With status (capacity-bounded lists) it also writes status[0] = the total
+// and status[1] = 1 if the total exceeds capacity, else 0.
 __global__ __launch_bounds__(kScanThreads) void bin_offsets_kernel(const BinPart *parts,
                                                                    int64_t nparts,
                                                                    int64_t *part_off,
-                                                                   BinStats *st) {
+                                                                   BinStats *st,
+                                                                   int64_t capacity,
+                                                                   int64_t *status) {
     // Blocked: thread t owns 16 consecutive totals of each 4096-entry step,
     // all requested at once; one block scan per step.
     constexpr int kPer = 16;
@@ -566,7 +570,17 @@ __global__ __launch_bounds__(kScanThreads) void bin_offsets_kernel(const BinPart
     if (threadIdx.x == 0) {
         st->total = (unsigned long long)carry;
         st->scan_total = 0;
+        if (status) {
+            status[0] = carry;
+            status[1] = carry > capacity ? 1 : 0;
+        }
     }
+}
+
+// Pairs the capacity-bounded lists hold: the total, or none when it
+// overflowed the capacity.
+__device__ __forceinline__ int64_t lists_kept(const int64_t *status) {
+    return status[1] != 0 ? 0 : status[0];
 }
 
 // Pairs staged in LDS per workgroup before the coalesced store.
@@ -593,7 +607,9 @@ constexpr int kBinStage = 2048;
 __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
     const BinRec *recs, const int32_t *counts, const uint32_t *masks, const int64_t *part_off,
     int64_t N, int tile, int W, int H, int tiles_x, int test, uint32_t *tkeys, int32_t *ids,
-    const float *depth, uint2 *pairs) {
+    const float *depth, uint2 *pairs, const int64_t *status) {
+    // Capacity-bounded lists that overflowed emit nothing.
+    if (status && status[1] != 0) return;
     __shared__ uint32_t s_k[kBinStage];
     __shared__ int32_t s_i[kBinStage];
     __shared__ int32_t s_off[kBinStage];
@@ -768,6 +784,13 @@ inline int tile_bits(int n_tiles) {
 constexpr int kCsBuckets = 4096;
 constexpr int kCsThreads = 256, kCsWaves = kCsThreads / 64;
 constexpr int64_t kCsMaxChunks = 512;   // about two workgroups per CU
+// Capacity-bounded lists plan for the capacity, which runs above the pairs
+// actually sorted (by the caller's headroom, or more). With twice the limit
+// the kept pairs get chunks no longer than the exact plan's as long as the
+// capacity is at most twice their count; with the same limit a headroom that
+// crossed it would lengthen the chunks a step and leave part of the GPU idle
+// (measured: 94 -> 113 us at config 4).
+constexpr int64_t kCsMaxChunksCapped = 2 * kCsMaxChunks;
 constexpr int kColWaves = 16;           // waves of the column scan's workgroups
 
 struct CsPlan {
@@ -775,18 +798,19 @@ struct CsPlan {
     int64_t nchunks;
 };
 
-// The smallest chunk that needs no more than kCsMaxChunks workgroups.
-inline CsPlan cs_plan(int64_t n) {
+// The smallest chunk that needs no more than max_chunks workgroups.
+inline CsPlan cs_plan(int64_t n, int64_t max_chunks = kCsMaxChunks) {
     static const int kPers[] = {8, 16, 24, 32, 48, 64};
     for (int p : kPers) {
         const int64_t nc = ceil_div(n, (int64_t)kCsThreads * p);
-        if (nc <= kCsMaxChunks || p == 64) return {p, nc};
+        if (nc <= max_chunks || p == 64) return {p, nc};
     }
     return {64, ceil_div(n, (int64_t)kCsThreads * 64)};
 }
 
-inline int64_t tile_sort_ws_bytes(int64_t n, int nb) {
-    return align256(4 * (int64_t)nb * cs_plan(n).nchunks) + align256(4 * (int64_t)nb);
+inline int64_t tile_sort_ws_bytes(int64_t n, int nb, int64_t max_chunks = kCsMaxChunks) {
+    return align256(4 * (int64_t)nb * cs_plan(n, max_chunks).nchunks) +
+           align256(4 * (int64_t)nb);
 }
 
 // V is the value moved with each tile key: an int32 id, or a uint2
@@ -800,7 +824,25 @@ struct CsPass {
     V *out;
     int32_t *offsets;               // tile starts, nb + 1
     uint32_t *hist, *tot;           // hist[nchunks][nb], tot[nb]
+    // Capacity-bounded lists: n is the capacity and the pairs to sort are
+    // lists_kept(status), read on the device; NULL: n pairs.
+    const int64_t *status;
+    int64_t chunk;                  // pairs per chunk
 };
+
+template <typename V>
+__device__ __forceinline__ int64_t cs_count(const CsPass<V> &P) {
+    return P.status ? min(lists_kept(P.status), P.n) : P.n;
+}
+
+// Chunks holding pairs: the grid, or for capacity-bounded lists the chunks
+// of the kept pairs (at least one, chunk 0 writing the offsets). Workgroups
+// past them do nothing; the others are dealt to the XCDs in contiguous runs
+// over these chunks alone, so that every XCD gets a share of the work.
+template <typename V>
+__device__ __forceinline__ int64_t cs_active(const CsPass<V> &P, int64_t n) {
+    return P.status ? max((int64_t)1, (n + P.chunk - 1) / P.chunk) : (int64_t)gridDim.x;
+}
 
 // A chunk's tiles as kPer / 4 16-byte loads per thread, all in flight at once
 // (chunk starts are multiples of 2048 pairs, so 16-byte aligned); ~0 past n.
@@ -826,9 +868,12 @@ __device__ __forceinline__ void load_chunk_tiles(const uint32_t *tiles, int64_t 
 template <int kPer, typename V>
 __global__ __launch_bounds__(kCsThreads) void count_hist_kernel(const CsPass<V> P) {
     __shared__ uint32_t s_h[kCsBuckets];
-    const int64_t c = xcd_contiguous(blockIdx.x, gridDim.x);
+    const int64_t n = cs_count(P);
+    const int64_t nact = cs_active(P, n);
+    if ((int64_t)blockIdx.x >= nact) return;
+    const int64_t c = xcd_contiguous(blockIdx.x, nact);
     uint32_t t[kPer];
-    load_chunk_tiles<kPer>(P.tiles, P.n, c * kCsThreads * kPer, t);
+    load_chunk_tiles<kPer>(P.tiles, n, c * kCsThreads * kPer, t);
     for (int i = threadIdx.x; i < P.nb; i += kCsThreads) s_h[i] = 0;
     __syncthreads();
 #pragma unroll
@@ -849,6 +894,7 @@ __global__ __launch_bounds__(64 * kColWaves) void count_colscan_kernel(const CsP
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int bkt = blockIdx.x * 64 + lane;
     const bool in = bkt < P.nb;
+    if (P.status) nchunks = cs_active(P, cs_count(P));
     const int64_t q = (nchunks + kColWaves - 1) / kColWaves;
     const int64_t c0 = wave * q, c1 = min(nchunks, c0 + q);
     uint32_t sum = 0;
@@ -882,9 +928,11 @@ __global__ __launch_bounds__(kCsThreads) void count_scatter_kernel(const CsPass<
     __shared__ uint32_t s_wh[kCsWaves][kCsBuckets];   // per wave: count, then next slot
     __shared__ uint32_t s_part[kCsWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t c = xcd_contiguous(blockIdx.x, gridDim.x);
+    const int64_t n = cs_count(P);
+    const int64_t nact = cs_active(P, n);
+    if ((int64_t)blockIdx.x >= nact) return;
+    const int64_t c = xcd_contiguous(blockIdx.x, nact);
     const int64_t pb = c * kChunk + wave * kPart;
-    const int64_t n = P.n;
     const int nb = P.nb;
     // The wave's part: pair pb + 64 r + lane is (tile t[r], id v[r]); a tile
     // of nb or more marks a dropped or absent pair.
@@ -984,13 +1032,14 @@ __global__ __launch_bounds__(kCsThreads) void count_scatter_kernel(const CsPass<
 template <typename V>
 static int32_t tile_count_sort(const uint32_t *tiles, const V *ids, int64_t n, int n_tiles,
                                V *out, int32_t *tile_offsets, void *ws, int64_t ws_bytes,
-                               hipStream_t s) {
+                               hipStream_t s, const int64_t *status = nullptr) {
     MG_REQUIRE(n > 0 && n < (1LL << 31) && n_tiles >= 1 && n_tiles <= kCsBuckets,
                "tile sort: %lld pairs over %d tiles", (long long)n, n_tiles);
-    MG_REQUIRE(ws && ws_bytes >= tile_sort_ws_bytes(n, n_tiles),
+    const int64_t max_chunks = status ? kCsMaxChunksCapped : kCsMaxChunks;
+    MG_REQUIRE(ws && ws_bytes >= tile_sort_ws_bytes(n, n_tiles, max_chunks),
                "tile sort: workspace %lld bytes, need %lld", (long long)ws_bytes,
-               (long long)tile_sort_ws_bytes(n, n_tiles));
-    const CsPlan plan = cs_plan(n);
+               (long long)tile_sort_ws_bytes(n, n_tiles, max_chunks));
+    const CsPlan plan = cs_plan(n, max_chunks);
     CsPass<V> P{};
     P.tiles = tiles;
     P.ids = ids;
@@ -1002,6 +1051,8 @@ static int32_t tile_count_sort(const uint32_t *tiles, const V *ids, int64_t n, i
     P.hist = static_cast<uint32_t *>(ws);
     P.tot = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) +
                                          align256(4 * (int64_t)n_tiles * plan.nchunks));
+    P.status = status;
+    P.chunk = (int64_t)kCsThreads * plan.per;
     const unsigned grid = (unsigned)plan.nchunks;
     TimedScope ts("tile_sort", s);
 #define MG_CS(PER)                                                                     \
@@ -1310,13 +1361,27 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
 
 // {id, depth bits} pairs from ids and the depth array (the radix route, for
 // more tiles than the counting sort takes).
+// (With status, only the kept pairs of capacity-bounded lists.)
 __global__ __launch_bounds__(256) void gather_depth_pairs_kernel(const int32_t *ids,
                                                                  const float *depth, int64_t n,
-                                                                 uint2 *pairs) {
+                                                                 uint2 *pairs,
+                                                                 const int64_t *status) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
+    if (i >= (status ? lists_kept(status) : n)) return;
     const int32_t g = ids[i];
     pairs[i] = make_uint2((uint32_t)g, __float_as_uint(depth[g]));
+}
+
+// Capacity-bounded lists on the radix route: the slots past the kept pairs
+// get a tile key above every tile (they sort last and no list holds them)
+// and id 0.
+__global__ __launch_bounds__(256) void lists_tail_kernel(uint32_t *tiles, int32_t *ids,
+                                                         int64_t capacity,
+                                                         const int64_t *status) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= capacity || i < lists_kept(status)) return;
+    tiles[i] = 0xFFFFFFFFu;
+    ids[i] = 0;
 }
 
 // Carves the begin/finish workspace identically on both calls. After begin,
@@ -1358,6 +1423,92 @@ static int32_t check_bin_args(const char *who, int64_t N, const void *uv, const 
     MG_REQUIRE(N == 0 || (uv && rxy && valid), "%s: null tensor pointer", who);
     MG_REQUIRE((conic == nullptr) == (opac == nullptr),
                "%s: conic and opacity must be given together (or both omitted)", who);
+    return MG_OK;
+}
+
+// Scratch of either tile sort: the radix passes' histograms, or the counting
+// sort's per-chunk counts at its largest tile count.
+static int64_t finish_sort_bytes(int64_t T, bool capped) {
+    return align256(std::max(sort_ws_bytes(T),
+                             tile_sort_ws_bytes(T, kCsBuckets,
+                                                capped ? kCsMaxChunksCapped : kCsMaxChunks)));
+}
+
+// Pairs in Gaussian order, grouped by tile, then each tile's list sorted by
+// depth, into gauss_ids and tile_offsets. n is the pair count (status NULL),
+// or the capacity of capacity-bounded lists, whose kernels read the pairs to
+// keep from status on the device (none after an overflow: every list empty).
+// Up to kCsBuckets tiles, bin_write emits {id, depth bits} values that the
+// one-pass counting sort carries (and it writes the offsets). Otherwise
+// bin_write emits ids, radix passes sort them into gauss_ids (from the id
+// buffer their last pass will NOT write, so they end there whatever the pass
+// count's parity), tile_ranges writes the offsets, and the depth bits are
+// gathered afterwards; capacity-bounded lists fill the slots past the kept
+// pairs with a tile key above every tile, which the key width then holds.
+static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
+                             const float *depth, int W, int H, int tile, int tiles_x,
+                             int n_tiles, int64_t n, const int64_t *status, int32_t *gauss_ids,
+                             int32_t *tile_offsets, void *finish_workspace, hipStream_t s) {
+    const int64_t T = n > 0 ? n : 1;
+    const int64_t T4 = align256(4 * T);
+    char *f = static_cast<char *>(finish_workspace);
+    uint2 *pairs_a = (uint2 *)f;                      // region A: 2 * T4 bytes
+    uint2 *pairs_b = (uint2 *)(f + 2 * T4);           // region B: 2 * T4 bytes
+    uint32_t *tk_a = (uint32_t *)(f + 4 * T4);
+    void *sort_ws = f + 5 * T4;
+    const int64_t sort_bytes = finish_sort_bytes(T, status != nullptr);
+    uint32_t *res_tiles = tk_a;
+    if (n == 0 || N == 0) {
+        TimedScope ts("tile_ranges", s);
+        tile_ranges_u32_kernel<<<1, 256, 0, s>>>(res_tiles, 0, n_tiles, tile_offsets);
+        MG_LAUNCHED("tile_ranges_u32_kernel");
+        return MG_OK;
+    }
+    int32_t rc = MG_OK;
+    const bool counting = n_tiles <= kCsBuckets;
+    const int bits = tile_bits(status ? n_tiles + 1 : n_tiles);
+    const bool even = ((bits + 7) / 8) % 2 == 0;
+    uint32_t *tk_b = (uint32_t *)pairs_a;
+    int32_t *ids_tmp = (int32_t *)((char *)pairs_a + T4);
+    int32_t *ids_a = even ? gauss_ids : ids_tmp;
+    int32_t *ids_b = even ? ids_tmp : gauss_ids;
+    {
+        TimedScope ts("bin_write", s);
+        bin_write_rec_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(
+            ws.recs, ws.counts, ws.masks, ws.part_off, N, tile, W, H, tiles_x,
+            conic != nullptr ? 1 : 0, tk_a, counting ? nullptr : ids_a, depth,
+            counting ? pairs_a : nullptr, status);
+        MG_LAUNCHED("bin_write_rec_kernel");
+    }
+    if (counting) {
+        rc = tile_count_sort<uint2>(tk_a, pairs_a, n, n_tiles, pairs_b, tile_offsets, sort_ws,
+                                    sort_bytes, s, status);
+        if (rc != MG_OK) return rc;
+    } else {
+        if (status) {
+            lists_tail_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, s>>>(tk_a, ids_a, n, status);
+            MG_LAUNCHED("lists_tail_kernel");
+        }
+        int32_t *rv;
+        rc = radix_sort_passes<uint32_t>(tk_a, ids_a, tk_b, ids_b, n, 0, bits, sort_ws,
+                                         sort_bytes, s, "tile_sort", &res_tiles, &rv, 0u,
+                                         0xFFFFFFFFu, nullptr);
+        if (rc != MG_OK) return rc;
+        MG_REQUIRE(rv == gauss_ids, "tile lists: ids landed in the wrong buffer");
+        {
+            TimedScope ts("tile_ranges", s);
+            tile_ranges_u32_kernel<<<(unsigned)ceil_div(n + 1, 256), 256, 0, s>>>(
+                res_tiles, n, n_tiles, tile_offsets);
+            MG_LAUNCHED("tile_ranges_u32_kernel");
+        }
+        gather_depth_pairs_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, s>>>(gauss_ids, depth, n,
+                                                                           pairs_b, status);
+        MG_LAUNCHED("gather_depth_pairs_kernel");
+    }
+    TdArgs D{tile_offsets, pairs_b, pairs_a, gauss_ids};
+    TimedScope ts("depth_sort", s);
+    tile_depth_sort_kernel<<<(unsigned)n_tiles, kTdThreads, 0, s>>>(D);
+    MG_LAUNCHED("tile_depth_sort_kernel");
     return MG_OK;
 }
 
@@ -1454,19 +1605,13 @@ int32_t mg_sort_pairs_by_tile(int64_t n, const uint32_t *tiles, const int32_t *i
 
 int64_t mg_bin_lists_workspace_bytes(int64_t N) { return BeginWs(nullptr, N > 0 ? N : 1).bytes; }
 
-// Scratch of either tile sort: the radix passes' histograms, or the counting
-// sort's per-chunk counts at its largest tile count.
-static int64_t finish_sort_bytes(int64_t T) {
-    return align256(std::max(sort_ws_bytes(T), tile_sort_ws_bytes(T, kCsBuckets)));
-}
-
 // Two regions of 8 bytes per pair (the pairs' {id, depth bits} values, and
 // the tile-sorted copy), the pairs' tile keys, then the sort scratch. The
 // radix route (more than kCsBuckets tiles) keeps its second key buffer and
 // id buffer in the first region.
 int64_t mg_bin_lists_finish_workspace_bytes(int64_t total) {
     const int64_t T = total > 0 ? total : 1;
-    return 5 * align256(4 * T) + finish_sort_bytes(T);
+    return 5 * align256(4 * T) + finish_sort_bytes(T, false);
 }
 
 int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy, const float *conic,
@@ -1493,7 +1638,8 @@ int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy, const f
     }
     {
         TimedScope ts("exclusive_scan", s);
-        bin_offsets_kernel<<<1, kScanThreads, 0, s>>>(ws.parts, nparts, ws.part_off, ws.stats);
+        bin_offsets_kernel<<<1, kScanThreads, 0, s>>>(ws.parts, nparts, ws.part_off, ws.stats,
+                                                       0, nullptr);
         MG_LAUNCHED("bin_offsets_kernel");
     }
     // The one host read: the total sizes the caller's id buffer. It is copied
@@ -1531,76 +1677,60 @@ int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy, const 
                "mg_bin_lists_finish: workspace %lld bytes, need %lld",
                (long long)finish_workspace_bytes,
                (long long)mg_bin_lists_finish_workspace_bytes(total));
-    hipStream_t s = as_stream(stream);
-    const int n_tiles = tiles_x * tiles_y;
-    const int64_t T = total > 0 ? total : 1;
-    const int64_t T4 = align256(4 * T);
-    char *f = static_cast<char *>(finish_workspace);
-    uint2 *pairs_a = (uint2 *)f;                      // region A: 2 * T4 bytes
-    uint2 *pairs_b = (uint2 *)(f + 2 * T4);           // region B: 2 * T4 bytes
-    uint32_t *tk_a = (uint32_t *)(f + 4 * T4);
-    void *sort_ws = f + 5 * T4;
-    const int64_t sort_bytes = finish_sort_bytes(T);
-    uint32_t *res_tiles = tk_a;
     if (total > 0) {
         MG_REQUIRE(gauss_ids, "mg_bin_lists_finish: null gauss_ids");
         MG_REQUIRE(N > 0, "mg_bin_lists_finish: %lld intersections from no Gaussians",
                    (long long)total);
         MG_REQUIRE(depth, "mg_bin_lists_finish: null depth");
-        // Pairs in Gaussian order, grouped by tile, then each tile's list
-        // sorted by depth. Up to kCsBuckets tiles, bin_write emits {id, depth
-        // bits} values that the one-pass counting sort carries (and it writes
-        // the offsets). Otherwise bin_write emits ids, radix passes sort them
-        // into gauss_ids (from the id buffer their last pass will NOT write,
-        // so they end there whatever the pass count's parity), tile_ranges
-        // writes the offsets, and the depth bits are gathered afterwards.
-        const bool counting = n_tiles <= kCsBuckets;
-        const int bits = tile_bits(n_tiles);
-        const bool even = ((bits + 7) / 8) % 2 == 0;
-        uint32_t *tk_b = (uint32_t *)pairs_a;
-        int32_t *ids_tmp = (int32_t *)((char *)pairs_a + T4);
-        int32_t *ids_a = even ? gauss_ids : ids_tmp;
-        int32_t *ids_b = even ? ids_tmp : gauss_ids;
-        {
-            TimedScope ts("bin_write", s);
-            bin_write_rec_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(
-                ws.recs, ws.counts, ws.masks, ws.part_off, N, tile, W, H, tiles_x,
-                conic != nullptr ? 1 : 0,
-                tk_a, counting ? nullptr : ids_a, depth, counting ? pairs_a : nullptr);
-            MG_LAUNCHED("bin_write_rec_kernel");
-        }
-        if (counting) {
-            rc = tile_count_sort<uint2>(tk_a, pairs_a, total, n_tiles, pairs_b, tile_offsets,
-                                        sort_ws, sort_bytes, s);
-            if (rc != MG_OK) return rc;
-        } else {
-            int32_t *rv;
-            rc = radix_sort_passes<uint32_t>(tk_a, ids_a, tk_b, ids_b, total, 0, bits, sort_ws,
-                                             sort_bytes, s, "tile_sort", &res_tiles, &rv, 0u,
-                                             0xFFFFFFFFu, nullptr);
-            if (rc != MG_OK) return rc;
-            MG_REQUIRE(rv == gauss_ids, "mg_bin_lists_finish: ids landed in the wrong buffer");
-            {
-                TimedScope ts("tile_ranges", s);
-                tile_ranges_u32_kernel<<<(unsigned)ceil_div(total + 1, 256), 256, 0, s>>>(
-                    res_tiles, total, n_tiles, tile_offsets);
-                MG_LAUNCHED("tile_ranges_u32_kernel");
-            }
-            gather_depth_pairs_kernel<<<(unsigned)ceil_div(total, 256), 256, 0, s>>>(
-                gauss_ids, depth, total, pairs_b);
-            MG_LAUNCHED("gather_depth_pairs_kernel");
-        }
-        TdArgs D{tile_offsets, pairs_b, pairs_a, gauss_ids};
-        TimedScope ts("depth_sort", s);
-        tile_depth_sort_kernel<<<(unsigned)n_tiles, kTdThreads, 0, s>>>(D);
-        MG_LAUNCHED("tile_depth_sort_kernel");
-        return MG_OK;
     }
-    TimedScope ts("tile_ranges", s);
-    tile_ranges_u32_kernel<<<(unsigned)ceil_div(total + 1, 256), 256, 0, s>>>(res_tiles, total,
-                                                                              n_tiles, tile_offsets);
-    MG_LAUNCHED("tile_ranges_u32_kernel");
-    return MG_OK;
+    return emit_and_sort(ws, N, conic, depth, W, H, tile, tiles_x, tiles_x * tiles_y, total,
+                         nullptr, gauss_ids, tile_offsets, finish_workspace, as_stream(stream));
+}
+
+int64_t mg_bin_lists_capped_workspace_bytes(int64_t N, int64_t capacity) {
+    if (N < 0 || capacity < 0) return 0;
+    const int64_t T = capacity > 0 ? capacity : 1;
+    return BeginWs(nullptr, N > 0 ? N : 1).bytes + 5 * align256(4 * T) +
+           finish_sort_bytes(T, true);
+}
+
+int32_t mg_bin_lists_capped(int64_t N, const float *uv, const float *rxy, const float *conic,
+                            const float *opacity, const int32_t *valid, const float *depth,
+                            int32_t W, int32_t H, int32_t tile, int32_t tiles_x, int32_t tiles_y,
+                            int64_t capacity, int32_t *gauss_ids, int32_t *tile_offsets,
+                            int64_t *status, void *workspace, int64_t workspace_bytes,
+                            mg_stream_t stream) {
+    int32_t rc = check_bin_args("mg_bin_lists_capped", N, uv, rxy, conic, opacity, valid, W, H,
+                                tile, tiles_x, tiles_y);
+    if (rc != MG_OK) return rc;
+    MG_REQUIRE(capacity >= 0 && capacity < (1LL << 31), "mg_bin_lists_capped: capacity %lld",
+               (long long)capacity);
+    MG_REQUIRE(tile_offsets && status, "mg_bin_lists_capped: null tile_offsets or status");
+    MG_REQUIRE(capacity == 0 || gauss_ids, "mg_bin_lists_capped: null gauss_ids");
+    MG_REQUIRE(depth || N == 0, "mg_bin_lists_capped: null depth");
+    const int64_t need = mg_bin_lists_capped_workspace_bytes(N, capacity);
+    MG_REQUIRE(workspace && workspace_bytes >= need,
+               "mg_bin_lists_capped: workspace %lld bytes, need %lld",
+               (long long)workspace_bytes, (long long)need);
+    BeginWs ws(workspace, N > 0 ? N : 1);
+    hipStream_t s = as_stream(stream);
+    BinArgs A{N, uv, rxy, conic, opacity, depth, valid, W, H, tile, tiles_x, tiles_y};
+    const int64_t nparts = N > 0 ? ceil_div(N, kBinThreads) : 0;
+    if (N > 0) {
+        TimedScope ts("bin_count", s);
+        bin_count_rec_kernel<<<(unsigned)nparts, kBinThreads, 0, s>>>(A, ws.counts, ws.recs,
+                                                                       ws.masks, ws.parts);
+        MG_LAUNCHED("bin_count_rec_kernel");
+    }
+    {
+        TimedScope ts("exclusive_scan", s);
+        bin_offsets_kernel<<<1, kScanThreads, 0, s>>>(ws.parts, nparts, ws.part_off, ws.stats,
+                                                       capacity, status);
+        MG_LAUNCHED("bin_offsets_kernel");
+    }
+    return emit_and_sort(ws, N, conic, depth, W, H, tile, tiles_x, tiles_x * tiles_y,
+                         N > 0 ? capacity : 0, status, gauss_ids, tile_offsets,
+                         static_cast<char *>(workspace) + ws.bytes, s);
 }
 
 }  // extern "C"

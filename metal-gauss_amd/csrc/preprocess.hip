@@ -632,6 +632,7 @@ struct AdamEpi {
     float *p[6], *m[6], *v[6];
     float step_size[6], inv_sqrt_bc2[6];
     float b1, b2, omb1, omb2, eps;
+    const int64_t *skip;   // NULL, or the launch does nothing when skip[1] != 0
 };
 
 // Cache policy of the epilogue's traffic (bit 0: moment loads, bit 1: moment
@@ -1226,6 +1227,7 @@ void preprocess_bwd_kernel(const PreBwdArgs A) {
 // The backward with the optimizer epilogue: 168 VGPRs, 3 waves/SIMD.
 __global__ __launch_bounds__(kPreThreads) __attribute__((amdgpu_waves_per_eu(3)))
 void preprocess_bwd_adam_kernel(const PreBwdArgs A) {
+    if (A.E.skip && A.E.skip[1] != 0) return;
     preprocess_bwd_body<true, true, true>(A);
 }
 
@@ -1366,6 +1368,7 @@ static int32_t preprocess_bwd(int64_t N, const float *means, const float *quats,
         E.omb1 = (float)(1.0 - adam->beta1);
         E.omb2 = (float)(1.0 - adam->beta2);
         E.eps = (float)adam->eps;
+        E.skip = adam->skip;
         for (int t = 0; t < 6; ++t) {
             E.p[t] = adam->p[t];
             E.m[t] = adam->m[t];

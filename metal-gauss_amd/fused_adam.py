@@ -27,6 +27,8 @@ class FusedAdam(torch.optim.Optimizer):
         # Parameters whose update a render(optimizer=) backward has applied
         # since the last step(), by id.
         self._epilogue_applied: dict[int, torch.Tensor] = {}
+        # Parameters whose step count the last step() advanced (rewind()).
+        self._last_stepped: list[torch.Tensor] = []
 
     def _state_of(self, p):
         st = self.state[p]
@@ -36,7 +38,7 @@ class FusedAdam(torch.optim.Optimizer):
             st["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.contiguous_format)
         return st
 
-    def epilogue(self, tensors):
+    def epilogue(self, tensors, skip=None):
         """This step's Adam for the given tensors as the preprocess backward's
         optimizer epilogue (``_lib.AdamEpilogue``), or None when it does not
         apply: a tensor that is not one of this optimizer's parameters (by
@@ -52,7 +54,11 @@ class FusedAdam(torch.optim.Optimizer):
 
         A parameter this step has already updated (a second render with
         ``optimizer=`` before ``step()``) raises: a second epilogue would be
-        a second Adam step."""
+        a second Adam step.
+
+        ``skip``: the device status of the render's capacity-bounded tile
+        lists; the kernel leaves everything as it was if they overflowed
+        (``rewind()`` after ``step()`` then takes back the step counts)."""
         owner = {}
         for group in self.param_groups:
             for p in group["params"]:
@@ -101,16 +107,25 @@ class FusedAdam(torch.optim.Optimizer):
             epi.step[i] = int(st["step"])
             keep += [st["exp_avg"], st["exp_avg_sq"]]
         epi.beta1, epi.beta2, epi.eps = float(b1), float(b2), float(eps)
+        if skip is not None:
+            epi.skip = _skip_ptr(skip)
+            keep.append(skip)
         epi._keep = keep
         return epi
 
     @torch.no_grad()
-    def step(self, closure=None):
+    def step(self, closure=None, skip=None):
+        """One Adam step. ``skip`` (the device status of capacity-bounded
+        tile lists, ``render(list_capacity=)``'s ``info["lists_status"]``)
+        makes the launch do nothing when the lists overflowed; after such a
+        step, ``rewind()`` takes back the step counts before it is run
+        again."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
         applied, self._epilogue_applied = self._epilogue_applied, {}
+        self._last_stepped = list(applied.values())
         for p in applied.values():
             if p.grad is not None:
                 raise RuntimeError(
@@ -135,6 +150,7 @@ class FusedAdam(torch.optim.Optimizer):
                     raise RuntimeError("FusedAdam parameters must be contiguous")
                 st = self._state_of(p)
                 st["step"] += 1
+                self._last_stepped.append(p)
                 g = g.contiguous()
                 key = (float(b1), float(b2), float(group["eps"]), p.device)
                 batches.setdefault(key, []).append(
@@ -145,7 +161,7 @@ class FusedAdam(torch.optim.Optimizer):
                 for i in range(0, len(items), _MAX_PER_LAUNCH):
                     chunk = items[i:i + _MAX_PER_LAUNCH]
                     s = _lib.stream(chunk[0][0])
-                    _lib.check(lib.mg_adam_step_multi(
+                    _lib.check(lib.mg_adam_step_multi_guarded(
                         len(chunk),
                         _lib.ptr_array([it[0].data_ptr() for it in chunk]),
                         _lib.ptr_array([it[1].data_ptr() for it in chunk]),
@@ -154,7 +170,23 @@ class FusedAdam(torch.optim.Optimizer):
                         _lib.i64_array([it[0].numel() for it in chunk]),
                         _lib.f64_array([it[4] for it in chunk]),
                         _lib.i64_array([it[5] for it in chunk]),
-                        b1, b2, eps, 0, s))
+                        b1, b2, eps, 0, None if skip is None else _skip_ptr(skip), s))
                     # Gradients made contiguous above must outlive the launch.
                     del chunk
         return loss
+
+    def rewind(self):
+        """Take back the step counts of the last ``step()`` (and of the
+        epilogues it closed), whose device update a ``skip`` status turned
+        off: parameters and moments are as before that step, and running it
+        again advances the counts once more."""
+        for p in getattr(self, "_last_stepped", ()):
+            self.state[p]["step"] -= 1
+        self._last_stepped = []
+
+
+def _skip_ptr(skip):
+    if (not isinstance(skip, torch.Tensor) or skip.dtype != torch.int64 or skip.numel() != 2
+            or skip.device.type != "cuda" or not skip.is_contiguous()):
+        raise TypeError("skip must be the device int64 (2,) status of render(list_capacity=)")
+    return skip.data_ptr()

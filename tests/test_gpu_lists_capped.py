@@ -1,0 +1,201 @@
+"""Tile lists without a host read: mg_bin_lists_capped, render(list_capacity=)
+and ListCapacity, against the two-call lists of mg_bin_lists_begin/_finish
+(which the binning tests hold bit-exact to the oracle).
+
+Within capacity the lists must be IDENTICAL to the two-call lists and the
+status must read (total, 0); past it the status must read (total, 1) and
+every list must be empty (the ids buffer is scratch then); an optimizer step given an
+overflowed status must leave parameters, moments and step counts exactly as
+they were, and the step run again with the reported capacity must match the
+reference order of work (sync-sized lists, backward, step())."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import intrinsics, scene
+from test_gpu_binning import gpu_preprocess, ref_scene
+
+pytestmark = pytest.mark.gpu
+
+
+def _both(s, dev, tile, ellipse, capacity_of):
+    """Two-call lists, then capacity-bounded lists at capacity_of(total)
+    into a sentinel-filled ids buffer."""
+    from metal_gauss_amd import _lib, backend
+
+    uv, conic, depth, rxy, valid, _ = gpu_preprocess(s, dev)
+    op = s["op"].to(dev)
+    args = (uv, rxy, depth, valid, conic if ellipse else None, op if ellipse else None,
+            s["W"], s["H"], tile)
+    ids, offs, tx = backend._bin(*args)
+    total = ids.numel()
+    cap = capacity_of(total)
+    lib = _lib.load()
+    n_tiles = offs.numel() - 1
+    got_ids = torch.full((max(cap, 1),), -7, dtype=torch.int32, device=dev)
+    got_offs = torch.full((n_tiles + 1,), -7, dtype=torch.int32, device=dev)
+    status = torch.full((2,), -7, dtype=torch.int64, device=dev)
+    N = uv.shape[0]
+    ws = torch.empty(lib.mg_bin_lists_capped_workspace_bytes(N, cap), dtype=torch.uint8,
+                     device=dev)
+    _lib.check(lib.mg_bin_lists_capped(
+        N, uv.data_ptr(), rxy.data_ptr(), conic.data_ptr() if ellipse else None,
+        op.data_ptr() if ellipse else None, valid.data_ptr(), depth.data_ptr(), s["W"], s["H"],
+        tile, tx, n_tiles // tx, cap, got_ids.data_ptr() if cap else None, got_offs.data_ptr(),
+        status.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(uv)))
+    torch.cuda.synchronize()
+    return (ids.cpu().numpy(), offs.cpu().numpy(), total, cap, got_ids.cpu().numpy(),
+            got_offs.cpu().numpy(), status.cpu().numpy())
+
+
+CAPS = {
+    "exact": lambda t: t,
+    "roomy": lambda t: t + 777,
+    "double": lambda t: 2 * t + 1,
+    "one_short": lambda t: max(t - 1, 0),
+    "zero": lambda t: 0,
+}
+
+
+@pytest.mark.parametrize("case", [
+    # (N, W, H, tile, ellipse): counting sort; rectangles only; the radix
+    # route (4800 tiles); the radix route at exactly 2^13 tiles, where the
+    # tile key of the unused slots needs one more bit than the tiles.
+    (20000, 240, 320, 16, True), (20000, 240, 320, 16, False), (20000, 640, 480, 8, True),
+    (6000, 2048, 1024, 16, True)])
+@pytest.mark.parametrize("cap", list(CAPS))
+def test_capped_lists_equal_the_two_call_lists(dev, case, cap):
+    n, W, H, tile, ellipse = case
+    s = ref_scene(N=n, W=W, H=H, seed=7)
+    if W == 2048:
+        s["f"] = 900.0
+    ids, offs, total, capacity, got_ids, got_offs, status = _both(
+        s, dev, tile, ellipse, CAPS[cap])
+    assert total > 0
+    assert status[0] == total, (status, total)
+    if total <= capacity:
+        assert status[1] == 0
+        assert np.array_equal(got_offs, offs), "tile offsets differ"
+        assert np.array_equal(got_ids[:total], ids), "gauss_ids differ"
+    else:
+        assert status[1] == 1
+        assert (got_offs == 0).all(), "an overflowed build must leave every list empty"
+
+
+def test_capped_lists_of_no_gaussians(dev):
+    from metal_gauss_amd import backend
+
+    e = torch.zeros(0, 2, device=dev)
+    ids, offs, tx, status = backend._bin_capped(
+        e, e, torch.zeros(0, device=dev), torch.zeros(0, dtype=torch.int32, device=dev), None,
+        None, 64, 48, 16, 100)
+    torch.cuda.synchronize()
+    assert status.tolist() == [0, 0]
+    assert (offs == 0).all() and offs.numel() == 4 * 3 + 1
+
+
+def _leaves(s, dev):
+    base = dict(means=s["means"], quats=s["quats"], log_scales=s["scales"].log(),
+                logits=torch.logit(s["opacities"]), sh_dc=s["sh"][:, :1].contiguous(),
+                sh_rest=s["sh"][:, 1:].contiguous())
+    return {k: t.clone().to(dev).requires_grad_(True) for k, t in base.items()}
+
+
+LRS = {"means": 1.6e-4, "quats": 1e-3, "log_scales": 5e-3, "logits": 5e-2, "sh_dc": 2.5e-3,
+       "sh_rest": 1.25e-4}
+W, H = 200, 150
+
+
+def _render(p, capacity, opt=None, bg=(0.1, 0.2, 0.3)):
+    from metal_gauss_amd import render
+
+    return render(p["means"], p["quats"], p["log_scales"], p["logits"], p["sh_dc"],
+                  intrinsics(W, H), torch.eye(4), W, H, sh_degree=3, sh_rest=p["sh_rest"],
+                  background=bg, activations=True, optimizer=opt, list_capacity=capacity)
+
+
+def test_render_with_capacity_equals_render(dev):
+    """Same image bit for bit within capacity; the background past it."""
+    s = scene(n=3000, seed=21, sh=True)
+    p = _leaves(s, dev)
+    with torch.no_grad():
+        rgb0, a0, info0 = _render(p, None)
+        total = info0["isect_total"]
+        for cap in (total, total + 5000):
+            rgb, a, info = _render(p, cap)
+            assert info["lists_status"].tolist() == [total, 0]
+            assert int(info["isect_total"]) == total
+            assert torch.equal(rgb, rgb0) and torch.equal(a, a0)
+        rgb, a, info = _render(p, total - 1)
+        assert info["lists_status"].tolist() == [total, 1]
+        assert (a == 0).all()
+        assert torch.equal(rgb, torch.tensor([0.1, 0.2, 0.3], device=dev).expand_as(rgb))
+
+
+def _state(opt, p):
+    out = {}
+    for k, t in p.items():
+        st = opt.state[t]
+        out[k] = (t.detach().clone(), st["exp_avg"].clone(), st["exp_avg_sq"].clone(),
+                  st["step"])
+    return out
+
+
+@pytest.mark.parametrize("epilogue", [True, False])
+def test_overflowed_step_changes_nothing_and_the_rerun_matches(dev, epilogue):
+    """Three training steps two ways: sync-sized lists with backward and
+    step() (the reference's order), and ListCapacity starting at 0, whose
+    first render overflows. The overflowed step must leave every parameter,
+    moment and step count exactly as it was; after rewind() and the rerun,
+    the parameters must match the reference run (the rasteriser's float
+    atomics reorder gradient sums run to run: same closeness bar as the
+    epilogue's whole-render test)."""
+    from metal_gauss_amd import FusedAdam, ListCapacity
+
+    s = scene(n=4000, seed=22, sh=True)
+    gt = torch.rand(H, W, 3, generator=torch.Generator().manual_seed(5)).to(dev)
+
+    def make():
+        p = _leaves(s, dev)
+        return p, FusedAdam([{"params": [t], "lr": LRS[k]} for k, t in p.items()], eps=1e-15)
+
+    p_ref, o_ref = make()
+    for _ in range(3):
+        rgb, _, _ = _render(p_ref, None)
+        o_ref.zero_grad(set_to_none=True)
+        (rgb - gt).abs().mean().backward()
+        o_ref.step()
+
+    p, opt = make()
+    cap = ListCapacity(initial=0)
+    for t in p.values():        # moments exist before the first (overflowed) step
+        opt._state_of(t)
+    before = _state(opt, p)
+    reruns = 0
+    for step in range(3):
+        while True:
+            rgb, _, info = _render(p, cap.value, opt if epilogue else None)
+            cap.watch(info["lists_status"])
+            opt.zero_grad(set_to_none=True)
+            (rgb - gt).abs().mean().backward()
+            opt.step(skip=info["lists_status"])
+            if not cap.overflowed():
+                break
+            reruns += 1
+            opt.rewind()
+            if step == 0 and reruns == 1:
+                after = _state(opt, p)
+                for k in p:
+                    for a, b in zip(after[k][:3], before[k][:3]):
+                        assert torch.equal(a, b), k
+                    assert after[k][3] == before[k][3] == 0, k
+    assert reruns == 1 and cap.overflows == 1
+    assert cap.value >= cap.last_total > 0
+    for k in p:
+        a, b = p[k].detach(), p_ref[k].detach()
+        close = torch.isclose(a, b, rtol=1e-3, atol=1e-4 * LRS[k])
+        assert float(close.double().mean()) > 0.999, k
+        assert opt.state[p[k]]["step"] == o_ref.state[p_ref[k]]["step"] == 3
