@@ -439,10 +439,43 @@ def forward_fps(step, frames=100):
             ts.append(time.perf_counter() - t0)
     ts.sort()
     sync_ms = 1e3 * ts[len(ts) // 2]
+
+    # One view, frames back to back: eager, and captured once as a HIP graph
+    # (no host read in the frame) and replayed.
+    cam = views[0]
+    with torch.no_grad():
+        def one_view_ms(run):
+            for _ in range(5):
+                run()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(frames):
+                run()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3 / frames
+
+        eager_ms = one_view_ms(lambda: frame(cam, cap.value))
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            frame(cam, cap.value)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            _, _, g_info = frame(cam, cap.value)
+        graph_ms = one_view_ms(graph.replay)
+        if int(g_info["lists_status"][1]):
+            raise RuntimeError("graph-captured frame overflowed its lists")
+        del graph
     return {"pipelined_capacity_lists": {"ms_per_frame": round(pipelined, 4),
                                          "fps": round(1e3 / pipelined, 1), "rerendered": redo},
             "synchronised_sync_lists": {"ms_per_frame": round(sync_ms, 4),
                                         "fps": round(1e3 / sync_ms, 1)},
+            "one_view_eager": {"ms_per_frame": round(eager_ms, 4),
+                               "fps": round(1e3 / eager_ms, 1)},
+            "one_view_graph_replay": {"ms_per_frame": round(graph_ms, 4),
+                                      "fps": round(1e3 / graph_ms, 1)},
             "frames": frames, "workload": "config-4 views, 1M Gaussians, 800x800"}
 
 

@@ -199,3 +199,41 @@ def test_overflowed_step_changes_nothing_and_the_rerun_matches(dev, epilogue):
         close = torch.isclose(a, b, rtol=1e-3, atol=1e-4 * LRS[k])
         assert float(close.double().mean()) > 0.999, k
         assert opt.state[p[k]]["step"] == o_ref.state[p_ref[k]]["step"] == 3
+
+
+def test_forward_frame_captured_in_a_graph_replays_exactly(dev):
+    """With capacity-sized lists a render has no host read, so a whole
+    forward frame (projection, binning, sorts, compositing) can be captured
+    in a HIP graph. Replayed three times, with eager renders and
+    synchronisations between the replays, every replay must give the eager
+    image bit for bit; moving the camera's scene (the parameters, in place)
+    between replays must give the eager image of the moved scene."""
+    s = scene(n=3000, seed=23, sh=True)
+    p = _leaves(s, dev)
+    with torch.no_grad():
+        _, _, info = _render(p, None)
+        cap = int(info["isect_total"]) * 2
+        want, want_a, _ = _render(p, cap)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            _render(p, cap)                     # warm the allocator on this stream
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            g_rgb, g_a, g_info = _render(p, cap)
+        for rep in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(g_rgb, want) and torch.equal(g_a, want_a), rep
+            assert g_info["lists_status"].tolist() == [int(info["isect_total"]), 0]
+            eager, _, _ = _render(p, cap)       # eager work between replays
+            torch.cuda.synchronize()
+            assert torch.equal(eager, want)
+        p["means"].add_(0.01)
+        moved, moved_a, _ = _render(p, cap)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert not torch.equal(moved, want)
+        assert torch.equal(g_rgb, moved) and torch.equal(g_a, moved_a)
