@@ -301,12 +301,15 @@ def test_sort_pairs_by_tile_is_stable_and_exact(dev, n, n_tiles, kind):
     assert (got[order.size:] == -1).all(), "wrote past the kept pairs"
 
 
-def test_more_tiles_than_the_counting_sort_takes_bit_exact(dev):
-    """640 x 480 at 8-pixel tiles is 4800 tiles: the lists come from the radix
-    passes instead of the counting sort, and must equal the oracle's."""
-    s = ref_scene(N=20000, W=640, H=480, seed=5)
-    gpu, ref = run_both(s, dev, 8)
-    assert (640 // 8) * (480 // 8) > 4096
+@pytest.mark.parametrize("W,H,tile", [(640, 480, 8), (1920, 1080, 16), (2048, 2048, 8)])
+def test_more_tiles_bit_exact(dev, W, H, tile):
+    """4800, 8160 and 65536 tiles: past 4096 tiles the lists come from the
+    radix passes instead of the counting sort, and must equal the
+    oracle's."""
+    s = ref_scene(N=20000, W=W, H=H, seed=5)
+    s["f"] = 200.0 * W / 640
+    gpu, ref = run_both(s, dev, tile)
+    assert (W // tile) * (H // tile) > 4096
     assert np.array_equal(gpu[3], ref[3]), "sorted keys differ"
     assert np.array_equal(gpu[0], ref[0]), "gauss_ids differ"
     assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"

@@ -61,17 +61,18 @@ CAPS = {
 
 
 @pytest.mark.parametrize("case", [
-    # (N, W, H, tile, ellipse): counting sort; rectangles only; the radix
-    # route (4800 tiles); the radix route at exactly 2^13 tiles, where the
-    # tile key of the unused slots needs one more bit than the tiles.
+    # (N, W, H, tile, ellipse): the counting sort at 300 tiles, once with
+    # rectangles only; past 4096 tiles the radix route, at 4800 and 65536
+    # tiles, and at 2^13 and 2^15 tiles, where the tile key of the unused
+    # slots needs one more bit than the tiles.
     (20000, 240, 320, 16, True), (20000, 240, 320, 16, False), (20000, 640, 480, 8, True),
-    (6000, 2048, 1024, 16, True)])
+    (6000, 2048, 1024, 16, True), (6000, 4096, 2048, 16, True), (6000, 2048, 2048, 8, True)])
 @pytest.mark.parametrize("cap", list(CAPS))
 def test_capped_lists_equal_the_two_call_lists(dev, case, cap):
     n, W, H, tile, ellipse = case
     s = ref_scene(N=n, W=W, H=H, seed=7)
-    if W == 2048:
-        s["f"] = 900.0
+    if W >= 2048:
+        s["f"] = 900.0 * W / 2048
     ids, offs, total, capacity, got_ids, got_offs, status = _both(
         s, dev, tile, ellipse, CAPS[cap])
     assert total > 0
