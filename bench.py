@@ -393,6 +393,23 @@ def gpu_bench(args):
                 fwd=forward_fps(step))
 
 
+def valu_roofline(kernels):
+    """The rasteriser's kernels against the VALU issue rate: wave
+    instructions per launch (SQ_INSTS_VALU from the committed counter
+    summary of this step) over the live mean launch time."""
+    out = {}
+    for label in ("rasterize_backward", "rasterize_forward"):
+        n = committed_valu(label)
+        row = kernels.get(label)
+        if n is None or row is None:
+            continue
+        achieved = n / (row["ms"] * 1e-3) / 1e9
+        out[label] = {"bound": "valu", "achieved": round(achieved, 1), "peak": VALU_PEAK_GIPS,
+                      "unit": "G wave-instructions/s", "frac": round(achieved / VALU_PEAK_GIPS, 4),
+                      "instructions_per_launch": int(n)}
+    return out
+
+
 def forward_fps(step, frames=100):
     """Forward-only rendering of the step's views at its current
     parameters (no autograd): frames enqueued back to back with
@@ -854,11 +871,6 @@ def adam_config(reps):
             "n_floats": n_floats}
 
 
-PMC_REGEX = ("raster_bwd|raster_fwd|adam_multi|preprocess_fwd|preprocess_bwd|scan_|bin_write|"
-             "bin_count|count_hist|count_colscan|count_scatter|tile_depth_sort|ssim_fused|"
-             "copyBuffer")
-
-
 def _counter_rows(d):
     import csv
 
@@ -892,8 +904,8 @@ def pmc_summary(fetch_dir, write_dir, copy_mib):
     lines = [
         "# HBM traffic per launch, config-4 step (1M Gaussians SH3, 800x800, tile 16), MI355X",
         "# made by (from the repository root, TMPDIR=/tmp):",
-        f"#   rocprofv3 --pmc FETCH_SIZE --kernel-include-regex '{PMC_REGEX}' -f csv -T "
-        "-d F -o pmc -- python -u bench.py --steps 3 --warmup 2 --no-cpu-baseline "
+        f"#   rocprofv3 --pmc FETCH_SIZE --kernel-include-regex '{COUNTER_REGEX}' -f csv -T "
+        "-d F -o pmc -- python3 -u bench.py --steps 3 --warmup 2 --no-cpu-baseline --ramp 0 "
         f"--copy-mib {copy_mib}",
         "#   (the same with --pmc WRITE_SIZE -d W)",
         f"#   python bench.py --pmc-summary F W --copy-mib {copy_mib}",
@@ -1019,7 +1031,7 @@ def counter_summary(dirs, copy_mib=1024):
     return "\n".join(notes + lines)
 
 
-def stats_summary(stats_csv, steps, variant="base", mcmc=False, config=None):
+def stats_summary(stats_csv, steps, variant="base", mcmc=False, config=None, render_fps=False):
     """Text summary of a rocprofv3 --kernel-trace --stats kernel_stats.csv."""
     import csv
 
@@ -1037,6 +1049,15 @@ def stats_summary(stats_csv, steps, variant="base", mcmc=False, config=None):
             "#   rocprofv3 --kernel-trace --stats -f csv -T -d P -o kt -- python -u bench.py "
             f"--config {config} --steps {steps}",
             f"#   python bench.py --stats-summary P/kt_kernel_stats.csv --config {config}",
+        ]
+    elif render_fps:
+        lines = [
+            "# rocprofv3 kernel statistics, forward-only render sweep (100k/300k/600k Gaussians "
+            "SH3 x 256..768^2, fixed view), MI355X",
+            "# made by (from the repository root, TMPDIR=/tmp):",
+            "#   rocprofv3 --kernel-trace --stats -f csv -T -d P -o kt -- python -u bench.py "
+            "--render-fps",
+            "#   python bench.py --stats-summary P/kt_kernel_stats.csv --render-fps",
         ]
     elif mcmc:
         lines = [
@@ -1060,10 +1081,11 @@ def stats_summary(stats_csv, steps, variant="base", mcmc=False, config=None):
             f"{what}), MI355X",
             "# made by (from the repository root, TMPDIR=/tmp):",
             "#   rocprofv3 --kernel-trace --stats -f csv -T -d P -o kt -- python -u bench.py "
-            f"--steps {steps} --warmup 5 --no-cpu-baseline{vflag}",
+            f"--steps {steps} --warmup 5 --ramp 0.5 --no-cpu-baseline{vflag}",
             f"#   python bench.py --stats-summary P/kt_kernel_stats.csv{vflag}",
-            "# The run covers warmup + timed steps + the fwd+bwd-only loop + 10 per-kernel "
-            "timing steps.",
+            "# The run covers a 0.5 s ramp of fwd+bwd steps, warmup + timed steps, the same "
+            "steps with host-read list sizing, the fwd+bwd-only loop, 10 per-kernel timing "
+            "steps and the forward-only frames.",
         ]
     lines += [
         f"{'kernel':36s} {'calls':>7s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'share_%':>8s}",
@@ -1073,6 +1095,35 @@ def stats_summary(stats_csv, steps, variant="base", mcmc=False, config=None):
                      f"{float(r['MinNs']) / 1e3:9.1f} {float(r['MaxNs']) / 1e3:9.1f} "
                      f"{100 * float(r['TotalDurationNs']) / total:8.2f}")
     return "\n".join(lines)
+
+
+# Issue rate of non-packed 32-bit VALU wave64 instructions: 256 CUs x 4
+# SIMDs, one instruction every 4 clocks (16 lanes wide) at 2.4 GHz. The
+# published 157.3 TFLOP/s vector FP32 peak counts packed FP32 (two lanes'
+# worth per instruction), which this build does not emit.
+VALU_PEAK_GIPS = 256 * 4 * 2.4 / 4
+COUNTERS_FILE = ROOT / "profiles" / "counters_config4.txt"
+
+
+def committed_valu(label):
+    """SQ_INSTS_VALU (wave instructions) per launch of a kernel from the
+    committed counter summary, or None."""
+    name = PROF_NAMES.get(label)
+    if name is None or not COUNTERS_FILE.exists():
+        return None
+    lines = COUNTERS_FILE.read_text().splitlines()
+    head = next((ln.split() for ln in lines if ln.startswith("kernel ")), None)
+    if head is None or "VALU_Minst" not in head:
+        return None
+    col = head.index("VALU_Minst")
+    for ln in lines:
+        parts = ln.split()
+        if parts and parts[0] == name and not ln.startswith("#"):
+            try:
+                return float(parts[col]) * 1e6
+            except (IndexError, ValueError):
+                return None
+    return None
 
 
 def committed_traffic(label):
@@ -1222,7 +1273,7 @@ def main():
         return
     if args.stats_summary:
         print(stats_summary(args.stats_summary, args.steps if args.config else 20,
-                            args.variant, args.mcmc, args.config))
+                            args.variant, args.mcmc, args.config, args.render_fps))
         return
     if args.cpu_only:
         print(json.dumps(cpu_baseline(args.gaussians, crop=_cpu_crop())))
@@ -1313,6 +1364,7 @@ def main():
             "traffic": committed_traffic(r["dominant"]),
             "algorithmic_bytes_per_launch": int(r["nbytes"]),
         },
+        "roofline_valu": valu_roofline(r["kernels"]),
         "kernels": r["kernels"],
         "raster_work": r["work"],
         "stream_copy": r["copy"],
