@@ -275,9 +275,9 @@ def algorithmic_bytes(kernel, N, I, P, T, f_valid, n_floats):
         # record gradient read and the logit gradient written (backward).
         "preprocess_forward": (96 + 192 * f_valid) * N,
         "preprocess_backward": (320 + 192 * f_valid) * N,
-        "bin_count": 76 * N,                      # 40 B read; count, 32 B record
+        "bin_count": 80 * N,                      # 40 B read; count, 32 B record, claim mask
         "exclusive_scan": 16 * N // 256,          # per-workgroup totals read, block offsets written
-        "bin_write": 36 * N + 12 * I,             # offset, record; tile key + {id, depth} per pair
+        "bin_write": 40 * N + 12 * I,             # count, record, mask; tile key + {id, depth} per pair
         "tile_sort": 24 * I,                      # tiles read twice, 8-byte values read and written
         "depth_sort": 12 * I,                     # per tile list: ids read, depths gathered, ids written
         "tile_ranges": 4 * I + 4 * (T + 1),
@@ -789,7 +789,7 @@ def render_fps(ramp_s=1.0, k=21):
     with a constant black background and no autograd."""
     import torch
 
-    from metal_gauss_amd import render, scenes
+    from metal_gauss_amd import ListCapacity, render, scenes
 
     dev = torch.device("cuda:0")
     rows = []
@@ -800,8 +800,9 @@ def render_fps(ramp_s=1.0, k=21):
             K = scenes.intrinsics(res, res, 45.0)
             vm = torch.eye(4)
 
-            def frame():
-                return render(m, q, sca, op, sh, K, vm, res, res, sh_degree=3)
+            def frame(cap=None):
+                return render(m, q, sca, op, sh, K, vm, res, res, sh_degree=3,
+                              list_capacity=cap)
 
             with torch.no_grad():
                 end = time.perf_counter() + ramp_s
@@ -814,11 +815,32 @@ def render_fps(ramp_s=1.0, k=21):
                     _, _, info = frame()
                     torch.cuda.synchronize()
                     ts.append(time.perf_counter() - t0)
+                # Frames enqueued back to back with capacity-sized lists (no
+                # host read in a frame; each frame's overflow word checked
+                # one frame later).
+                cap = ListCapacity()
+                while True:
+                    _, _, ci = frame(cap.value)
+                    if not cap.overflowed(cap.watch(ci["lists_status"])):
+                        break
+                nf = 4 * k
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                prev = None
+                for _ in range(nf):
+                    _, _, ci = frame(cap.value)
+                    t = cap.watch(ci["lists_status"])
+                    if prev is not None and cap.overflowed(prev):
+                        raise RuntimeError("a frame overflowed its sized lists")
+                    prev = t
+                torch.cuda.synchronize()
+                pipe = (time.perf_counter() - t0) * 1e3 / nf
             ts.sort()
             ms = 1e3 * float(sum(ts[1:-1]) / len(ts[1:-1])) if k > 2 else 1e3 * ts[0]
             med = 1e3 * ts[len(ts) // 2]
             row = {"splats": n, "res": res, "ms": round(med, 4), "fps": round(1e3 / med, 1),
-                   "trimmed_mean_ms": round(ms, 4), "intersections": info["isect_total"]}
+                   "trimmed_mean_ms": round(ms, 4), "intersections": info["isect_total"],
+                   "pipelined_ms": round(pipe, 4), "pipelined_fps": round(1e3 / pipe, 1)}
             if (n, res) in REF_FPS:
                 row["reference_m5_fps"] = REF_FPS[(n, res)]
             rows.append(row)
@@ -1304,6 +1326,7 @@ def main():
                           "data": "synthetic (seeded frustum scene; the reference renders a ply)",
                           "config": {"workload": "forward-only render, fixed view, fov 45 deg"},
                           "vs_reference_m5": round(head["fps"] / REF_FPS[(600_000, 768)], 2),
+                          "pipelined_fps": head["pipelined_fps"],
                           "rows": rows}))
         return
     if args.config is not None:
