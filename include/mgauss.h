@@ -532,6 +532,18 @@ int32_t mg_selective_adam_step(int32_t count, float *const *p,
                                int64_t n_visible, double beta1, double beta2,
                                double eps, mg_stream_t stream);
 
+/* mg_selective_adam_step that does nothing (step counts included) when
+ * skip[1] != 0, skip (device, 2 int64) being the status of capacity-bounded
+ * tile lists (mg_bin_lists_capped). No counterpart in the reference. */
+int32_t mg_selective_adam_step_guarded(int32_t count, float *const *p,
+                                       const float *const *g, float *const *m,
+                                       float *const *v, float *const *steps,
+                                       const int64_t *rows, const int32_t *width,
+                                       const float *lr, const uint8_t *visible,
+                                       int64_t n_visible, double beta1,
+                                       double beta2, double eps,
+                                       const int64_t *skip, mg_stream_t stream);
+
 /* ------------------------------------------------------------------- SSIM */
 
 /* The five SSIM entry points of the reference, same math and layouts

@@ -100,6 +100,10 @@ _SIGNATURES = {
     "mg_selective_adam_step": (_i32, [_i32, _pp, _pp, _pp, _pp, _pp, ctypes.POINTER(_i64),
                                       ctypes.POINTER(_i32), ctypes.POINTER(_f32), _vp, _i64,
                                       _f64, _f64, _f64, _vp]),
+    "mg_selective_adam_step_guarded": (_i32, [_i32, _pp, _pp, _pp, _pp, _pp,
+                                              ctypes.POINTER(_i64), ctypes.POINTER(_i32),
+                                              ctypes.POINTER(_f32), _vp, _i64, _f64, _f64,
+                                              _f64, _vp, _vp]),
     "mg_ssim_stack_blur_h": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "mg_ssim_blur15": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp]),
     "mg_ssim_tail_forward": (_i32, [_vp, _i32, _i32, _vp, _vp]),

@@ -197,6 +197,7 @@ struct SelTable {
     const uint8_t *visible;
     int64_t n_visible;
     double l2b1, l2b2;               // log2 of the fp32 betas, in double
+    const int64_t *skip;             // NULL, or do nothing when skip[1] != 0
 };
 
 // Rows a workgroup of a tensor of this width owns on each path.
@@ -232,6 +233,7 @@ __global__ __launch_bounds__(kAdamThreads) void selective_adam_kernel(const SelT
     __shared__ float s_step_size[kSelRowsMax];
     __shared__ uint8_t s_vis[kSelRowsMax];
 
+    if (tab.skip && tab.skip[1] != 0) return;
     int k = 0;
     const int bid = blockIdx.x;
     while (k + 1 < tab.count && bid >= tab.t[k + 1].block_begin) ++k;
@@ -453,6 +455,17 @@ int32_t mg_selective_adam_step(int32_t count, float *const *p,
                                const float *lr, const uint8_t *visible,
                                int64_t n_visible, double beta1, double beta2,
                                double eps, mg_stream_t stream) {
+    return mg_selective_adam_step_guarded(count, p, g, m, v, steps, rows, width, lr, visible,
+                                          n_visible, beta1, beta2, eps, nullptr, stream);
+}
+
+int32_t mg_selective_adam_step_guarded(int32_t count, float *const *p,
+                                       const float *const *g, float *const *m,
+                                       float *const *v, float *const *steps,
+                                       const int64_t *rows, const int32_t *width,
+                                       const float *lr, const uint8_t *visible,
+                                       int64_t n_visible, double beta1, double beta2,
+                                       double eps, const int64_t *skip, mg_stream_t stream) {
     MG_REQUIRE(count >= 0 && count <= kAdamMaxTensors,
                "mg_selective_adam_step: %d tensors, at most %d per launch", count,
                kAdamMaxTensors);
@@ -468,6 +481,7 @@ int32_t mg_selective_adam_step(int32_t count, float *const *p,
     tab.n_visible = n_visible;
     tab.l2b1 = std::log2((double)tab.b1);
     tab.l2b2 = std::log2((double)tab.b2);
+    tab.skip = skip;
     // Widest tensors first: their workgroups are the longest, and the short
     // ones then fill the tail of the launch.
     int order[kAdamMaxTensors];

@@ -25,6 +25,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .fused_adam import _skip_ptr
 
 _MAX_PER_LAUNCH = 32
 
@@ -67,9 +68,15 @@ class SelectiveAdam(torch.optim.Optimizer):
         return grad.contiguous()
 
     @torch.no_grad()
-    def step(self, visible: torch.Tensor, closure=None):
+    def step(self, visible: torch.Tensor, closure=None, skip=None):
         """One step: rows with ``visible`` set in the row-wise groups (one
-        launch for all of them), every element of the dense groups."""
+        launch for all of them), every element of the dense groups.
+
+        ``skip`` (the device status of capacity-bounded tile lists,
+        ``render(list_capacity=)``'s ``info["lists_status"]``) makes every
+        launch do nothing when the lists overflowed, the per-row step counts
+        included; ``rewind()`` then takes back the dense groups' step
+        counts before the step is run again."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -80,6 +87,8 @@ class SelectiveAdam(torch.optim.Optimizer):
         rows_by_key: dict[tuple, list] = {}
         dense_by_key: dict[tuple, list] = {}
         vis_dev = None
+        skip_ptr = None if skip is None else _skip_ptr(skip)
+        self._last_dense_stepped = []
         for group in self.param_groups:
             b1, b2 = group["betas"]
             key = (float(b1), float(b2), float(group["eps"]))
@@ -90,6 +99,7 @@ class SelectiveAdam(torch.optim.Optimizer):
                     g = self._check_gradient(p)
                     st = self._state_for(p, rowwise=False)
                     st["step"] += 1
+                    self._last_dense_stepped.append(p)
                     dense_by_key.setdefault(key, []).append(
                         (p, g, st["exp_avg"], st["exp_avg_sq"], float(group["lr"]), st["step"]))
                     continue
@@ -111,7 +121,7 @@ class SelectiveAdam(torch.optim.Optimizer):
             for i in range(0, len(items), _MAX_PER_LAUNCH):
                 chunk = items[i:i + _MAX_PER_LAUNCH]
                 p0 = chunk[0][0]
-                _lib.check(lib.mg_selective_adam_step(
+                _lib.check(lib.mg_selective_adam_step_guarded(
                     len(chunk),
                     _lib.ptr_array([it[0].data_ptr() for it in chunk]),
                     _lib.ptr_array([it[1].data_ptr() for it in chunk]),
@@ -122,11 +132,11 @@ class SelectiveAdam(torch.optim.Optimizer):
                     _lib.i32_array([it[0].numel() // max(1, it[0].shape[0]) for it in chunk]),
                     _lib.f32_array([it[5] for it in chunk]),
                     vis_dev.data_ptr() if vis_dev.numel() else None, vis_dev.numel(),
-                    b1, b2, eps, _lib.stream(p0)))
+                    b1, b2, eps, skip_ptr, _lib.stream(p0)))
         for (b1, b2, eps), items in dense_by_key.items():
             for i in range(0, len(items), _MAX_PER_LAUNCH):
                 chunk = items[i:i + _MAX_PER_LAUNCH]
-                _lib.check(lib.mg_adam_step_multi(
+                _lib.check(lib.mg_adam_step_multi_guarded(
                     len(chunk),
                     _lib.ptr_array([it[0].data_ptr() for it in chunk]),
                     _lib.ptr_array([it[1].data_ptr() for it in chunk]),
@@ -135,5 +145,13 @@ class SelectiveAdam(torch.optim.Optimizer):
                     _lib.i64_array([it[0].numel() for it in chunk]),
                     _lib.f64_array([it[4] for it in chunk]),
                     _lib.i64_array([it[5] for it in chunk]),
-                    b1, b2, eps, 1, _lib.stream(chunk[0][0])))
+                    b1, b2, eps, 1, skip_ptr, _lib.stream(chunk[0][0])))
         return loss
+
+    def rewind(self):
+        """Take back the dense groups' step counts of the last ``step()``,
+        whose launches a ``skip`` status turned off (the per-row counts of
+        the row-wise groups live on the device and were not advanced)."""
+        for p in getattr(self, "_last_dense_stepped", ()):
+            self.state[p]["step"] -= 1
+        self._last_dense_stepped = []
