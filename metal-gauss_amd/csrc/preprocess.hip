@@ -635,14 +635,21 @@ struct AdamEpi {
     const int64_t *skip;   // NULL, or the launch does nothing when skip[1] != 0
 };
 
-// Cache policy of the epilogue's traffic (bit 0: moment loads, bit 1: moment
-// stores, bit 2: parameter stores non-temporal). Ordinary accesses measured
-// best over the whole config-4 step: every non-temporal combination slowed
-// this kernel by 5 to 50 us, more than it gained in the projection forward
-// that follows (52 to 88 us after this kernel against 55 us after a
-// separate Adam).
-constexpr int kEpiNt = 0;
+// Cache policy of the epilogue's traffic. The SH rows' moments (48 of the 59
+// floats per Gaussian, moved as whole float4 lines) are loaded and stored
+// non-temporally, so the 470 MB of moment traffic streams past the caches
+// and the parameters the next projection forward reads stay resident: at
+// config 4 that forward took 82 us after this kernel with ordinary moment
+// accesses and 64 us with these, and the step 1.080 -> 1.060 ms, this
+// kernel unchanged. The 11 non-SH moments of a Gaussian are stored as
+// 4-byte pieces of 12- and 16-byte rows; non-temporal, those stores leave
+// lines partly written and slowed this kernel by 25 us, so they stay
+// ordinary, as do the parameter accesses; their loads are non-temporal
+// (1.061 -> 1.059 ms). Bits: 0 non-SH moment loads, 1 non-SH moment stores,
+// 2 parameter stores non-temporal.
+constexpr int kEpiNt = 1;
 constexpr bool kNtLoad = kEpiNt & 1, kNtMom = kEpiNt & 2, kNtPar = kEpiNt & 4;
+constexpr bool kShNtMom = true;   // SH rows' moment loads and stores
 
 typedef float v4a __attribute__((ext_vector_type(4)));
 
@@ -744,15 +751,15 @@ __device__ __forceinline__ void stage_adam(const float4 *sb, const float4 *cb,
         const int t = fused || f < 48 ? 4 : 5;
         const int64_t off = fused ? G0 * 48 + f : (f < 48 ? G0 * 3 + f : G0 * 45 + (f - 48));
         if (stage_row(fused, f + 3) < ng) {
-            m4[i] = ld_nt4<kNtLoad>(E.m[t] + off);
-            v4[i] = ld_nt4<kNtLoad>(E.v[t] + off);
+            m4[i] = ld_nt4<kShNtMom>(E.m[t] + off);
+            v4[i] = ld_nt4<kShNtMom>(E.v[t] + off);
         } else {
             float e[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 if (stage_row(fused, f + k) < ng) {
-                    e[k] = ld_nt<kNtLoad>(E.m[t] + off + k);
-                    e[4 + k] = ld_nt<kNtLoad>(E.v[t] + off + k);
+                    e[k] = ld_nt<kShNtMom>(E.m[t] + off + k);
+                    e[4 + k] = ld_nt<kShNtMom>(E.v[t] + off + k);
                 }
             }
             m4[i] = make_float4(e[0], e[1], e[2], e[3]);
@@ -776,15 +783,15 @@ __device__ __forceinline__ void stage_adam(const float4 *sb, const float4 *cb,
                         E.step_size[t], E.inv_sqrt_bc2[t], false);
         if (stage_row(fused, f + 3) < ng) {
             st_nt4<kNtPar>(E.p[t] + off, make_float4(po[0], po[1], po[2], po[3]));
-            st_nt4<kNtMom>(E.m[t] + off, make_float4(ms[0], ms[1], ms[2], ms[3]));
-            st_nt4<kNtMom>(E.v[t] + off, make_float4(vs[0], vs[1], vs[2], vs[3]));
+            st_nt4<kShNtMom>(E.m[t] + off, make_float4(ms[0], ms[1], ms[2], ms[3]));
+            st_nt4<kShNtMom>(E.v[t] + off, make_float4(vs[0], vs[1], vs[2], vs[3]));
         } else {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 if (stage_row(fused, f + k) < ng) {
                     st_nt<kNtPar>(E.p[t] + off + k, po[k]);
-                    st_nt<kNtMom>(E.m[t] + off + k, ms[k]);
-                    st_nt<kNtMom>(E.v[t] + off + k, vs[k]);
+                    st_nt<kShNtMom>(E.m[t] + off + k, ms[k]);
+                    st_nt<kShNtMom>(E.v[t] + off + k, vs[k]);
                 }
             }
         }
