@@ -456,6 +456,88 @@ struct BinPart {
     unsigned long long total;
 };
 
+// Inclusive max over the wave of non-negative v, in lane order (DPP row
+// shifts, then the row broadcasts).
+__device__ __forceinline__ int wave_incl_max(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false));   // row_shr:1
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false));   // row_shr:2
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false));   // row_shr:4
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false));   // row_shr:8
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false));   // row_bcast:15
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false));   // row_bcast:31
+    return v;
+}
+
+// The small rectangles' tile tests of one wave, one (Gaussian, tile)
+// candidate per lane: a per-lane walk made every lane wait for the wave's
+// largest rectangle. Lane l's rectangle has ar tiles (0 for none) and its
+// candidates are [pre, pre + ar) of the wave's row; a candidate finds its
+// rectangle as the last head mark at or before it (an inclusive max over the
+// lanes), and its tile from its row-major index. Each tile's decision is
+// tile_claim, the walk's own expressions, so the result is bit for bit the
+// walk's. Returns this lane's claim mask (bit loc for tile loc).
+__device__ __forceinline__ uint32_t wave_small_claims(const BinRec &r, int ar, bool test,
+                                                      int tile, int W, int H, BinRec *w_rec,
+                                                      int32_t *w_pre, uint32_t *w_msk,
+                                                      uint8_t *w_own, int lane) {
+    if (!test) return ar >= 32 ? 0xFFFFFFFFu : (1u << ar) - 1u;
+    int incl = ar;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
+    }
+    const int pre = incl - ar;
+    const int total = __shfl(incl, 63, 64);
+    if (total == 0) return 0u;   // wave-uniform
+    w_rec[lane] = r;
+    w_pre[lane] = pre;
+    w_msk[lane] = 0u;
+    for (int i = lane; i < (total + 3) / 4; i += 64) reinterpret_cast<uint32_t *>(w_own)[i] = 0u;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (ar > 0) w_own[pre] = (uint8_t)(lane + 1);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int carry = 0;
+    for (int c0 = 0; c0 < total; c0 += 64) {
+        const int c = c0 + lane;
+        const bool valid = c < total;
+        const int h = valid ? (int)w_own[c] : 0;
+        const int own = max(wave_incl_max(h), carry);   // owner lane + 1 (>= 1 when valid)
+        carry = __shfl(own, 63, 64);
+        const int ol = max(own - 1, 0);
+        const BinRec q = w_rec[ol];
+        const int loc = c - w_pre[ol];
+        bool claim = false;
+        if (valid) {
+            const int x0 = (int)(q.xs & 0xffffu), y0 = (int)(q.ys & 0xffffu);
+            const int w = (int)(q.xs >> 16) - x0 + 1;
+            // loc < 32 and w <= 32: loc * ceil(2^16 / w) >> 16 is loc / w exactly.
+            const int row = (int)(((uint32_t)loc * ((65535u + (uint32_t)w) / (uint32_t)w)) >> 16);
+            const int col = loc - row * w;
+            claim = tile_claim(q, true, x0 + col, y0 + row, tile, W, H);
+        }
+        // The candidates of one rectangle in this round are a run of lanes
+        // starting at a head mark (or at lane 0); the run's first lane folds
+        // the run's claims into the rectangle's mask.
+        const uint64_t cm = ballot(claim);
+        const uint64_t hm = ballot(valid && (h != 0 || lane == 0));
+        if (valid && (h != 0 || lane == 0)) {
+            const uint64_t above = lane == 63 ? 0ull : hm >> (lane + 1);
+            const int len = above ? __builtin_ctzll(above) + 1 : min(64, total - c0) - lane;
+            const uint32_t bits = (uint32_t)((cm >> lane) & ((len >= 64) ? ~0ull
+                                                                          : ((1ull << len) - 1ull)));
+            w_msk[ol] |= bits << loc;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    return w_msk[lane];
+}
+
 // Count pass in Gaussian order (coalesced reads): the tile count and the
 // walk record; per workgroup the intersection total.
 __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArgs A,
@@ -467,6 +549,9 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
     __shared__ int32_t s_big[kBinThreads], s_cnt[kBinThreads];
     __shared__ int32_t s_nbig;
     __shared__ float s_edge[kBinThreads / 64][kEdgeSlots];
+    __shared__ int32_t s_pre[kBinThreads];
+    __shared__ uint32_t s_msk[kBinThreads];
+    __shared__ __align__(4) uint8_t s_own[kBinThreads / 64][64 * kWaveWalkArea];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t g = (int64_t)blockIdx.x * kBinThreads + tid;
     const bool test = A.conic != nullptr;
@@ -475,22 +560,25 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
     int n = 0;
     bool big = false;
     uint32_t mask = 0;
-    if (g < A.N) {
-        BinRec r;
-        if (make_rec(A, g, r)) {
-            recs[g] = r;
-            if (rec_area(r) > kWaveWalkArea) {
-                big = true;
-                s_rec[tid] = r;
-            } else {
-                n = rec_walk(r, test, A.tile, A.W, A.H, A.tiles_x,
-                             [&](int, uint32_t, int loc) { mask |= 1u << loc; });
-            }
+    BinRec r{};
+    int ar = 0;
+    if (g < A.N && make_rec(A, g, r)) {
+        recs[g] = r;
+        ar = rec_area(r);
+        if (ar > kWaveWalkArea) {
+            big = true;
+            ar = 0;
         }
-        // The claimed tiles of a small rectangle, bit loc for its row-major
-        // tile loc: the write pass emits from them without testing again.
-        masks[g] = mask;
     }
+    // The claimed tiles of a small rectangle, bit loc for its row-major tile
+    // loc: the write pass emits from them without testing again.
+    mask = wave_small_claims(r, ar, test, A.tile, A.W, A.H, s_rec + wave * 64,
+                             s_pre + wave * 64, s_msk + wave * 64, s_own[wave], lane);
+    n = __popc(mask);
+    if (g < A.N) masks[g] = mask;
+    // s_rec's wave slice now holds the big rectangles' records (a lane's own
+    // record, written by wave_small_claims or here).
+    if (big) s_rec[tid] = r;
     // Large rectangles: compacted in LDS, one wave each.
     const uint64_t m = ballot(big);
     int at = 0;
