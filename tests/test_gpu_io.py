@@ -124,3 +124,48 @@ def test_round_trip_at_a_million(dev, tmp_path):
     q = p["quats"] / p["quats"].norm(dim=1, keepdim=True).clamp_min(1e-12)
     assert torch.allclose(sp.quats, q, atol=1e-6)
     assert torch.equal(sp.sh, torch.cat([p["sh_dc"], p["sh_rest"]], dim=1))
+
+
+# The GPU decode against the oracle rather than the CPU decode: the known
+# answers of the reference's PLY tests, and the spec-level decode of
+# oracle/ply_ref.py, both written independently of the package's reader.
+from test_io import DECODE_CASES, _file, _stored, _tagged_rest  # noqa: E402
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=[c[0] for c in DECODE_CASES])
+def test_gpu_decode_known_answers(dev, tmp_path, case):
+    from metal_gauss_amd.io import load_ply
+
+    name, stored, field, want, rel = case
+    sp = load_ply(_file(tmp_path, f"{name}.ply", _stored(3, **stored)), device="cuda")
+    got = (sp.sh[:, 0] if field == "sh[:, 0]" else getattr(sp, field)).cpu().numpy()
+    assert got == pytest.approx(want.astype(np.float32), rel=rel, abs=0 if rel else 1e-12)
+
+
+def test_gpu_decode_zero_quaternion_and_channel_major_rest(dev, tmp_path):
+    from metal_gauss_amd.io import load_ply
+
+    rot = np.array([[0.0, 0.0, 0.0, 0.0], [1.0, 0.0, 0.0, 0.0], [0.0, 2.0, 0.0, 0.0]])
+    sp = load_ply(_file(tmp_path, "z.ply", _stored(3, rot=rot, rest=_tagged_rest(3, 15))),
+                  device="cuda")
+    assert torch.isfinite(sp.quats).all()
+    band = torch.arange(1, 16)[None, :, None]
+    chan = torch.arange(3)[None, None, :]
+    splat = torch.arange(3)[:, None, None]
+    assert torch.equal(sp.sh[:, 1:, :].cpu(), (1000 * splat + 15 * chan + band - 1).float())
+
+
+def test_gpu_decode_matches_the_spec_level_decode(dev, tmp_path):
+    from metal_gauss_amd.io import load_ply
+
+    rng = np.random.default_rng(7)
+    n = 500
+    cols = _stored(n, xyz=rng.standard_normal((n, 3)), rot=rng.standard_normal((n, 4)),
+                   log_scale=rng.standard_normal((n, 3)) - 3, logit=3 * rng.standard_normal(n),
+                   dc=rng.standard_normal((n, 3)), rest=rng.standard_normal((n, 15, 3)))
+    path = _file(tmp_path, "rand.ply", cols)
+    sp = load_ply(path, device="cuda")
+    want = ply_ref.decode(ply_ref.read_ply_bytes(path.read_bytes()))
+    for f, w in zip(("means", "quats", "scales", "opacities", "sh"), want[:5]):
+        assert ulps(getattr(sp, f), torch.from_numpy(w.astype(np.float32))) <= 1, f
+    assert sp.sh_degree == want[5]
