@@ -245,12 +245,9 @@ class Step:
             scales, opac = apply_3d_filter(torch.exp(scales), torch.sigmoid(opac), self.f3d)
             kw = dict(antialias=True)
             torch_reg = self.reg
-        cap = None if self.cap is None else self.cap.value
         rgb, alpha, info = render(p["means"], p["quats"], scales, opac, p["sh_dc"], cam.K,
                                   cam.viewmat, cam.W, cam.H, sh_degree=3, sh_rest=p["sh_rest"],
-                                  background=self.bg, list_capacity=cap, **kw)
-        if self.cap is not None:
-            self.cap.watch(info["lists_status"])
+                                  background=self.bg, list_capacity=self.cap, **kw)
         # 0.8 * |rgb - gt|.mean() + 0.2 * (1 - ssim(rgb, gt)) (train.py:389-390), fused.
         loss, _ = photometric_loss(rgb, gt, self.window, 0.2)
         if torch_reg:
@@ -312,20 +309,26 @@ def gpu_bench(args):
     # K timed steps: wall clock around all of them (the value), and a HIP
     # event between consecutive steps on the stream the kernels run on (the
     # median per step).
-    events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     reruns0 = step.reruns
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for k in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    reruns = step.reruns - reruns0
+    # The median step from HIP events recorded between consecutive steps, in
+    # a loop of its own (an event on the stream costs each step a few us).
+    ne = max(10, args.steps // 5)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(ne + 1)]
+    for k in range(ne):
         events[k].record()
         step()
     events[-1].record()
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    per_step = sorted(events[k].elapsed_time(events[k + 1]) for k in range(args.steps))
+    per_step = sorted(events[k].elapsed_time(events[k + 1]) for k in range(ne))
     median_ms = per_step[len(per_step) // 2]
 
-    reruns = step.reruns - reruns0
     # The same steps with the lists sized by a host read in every render (the
     # reference's way), fewer of them.
     sync_ms = None
@@ -436,15 +439,15 @@ def forward_fps(step, frames=100):
             t0 = time.perf_counter()
             tickets = []
             for i, cam in enumerate(views):
-                _, _, info = frame(cam, cap.value)
-                tickets.append(cap.watch(info["lists_status"]))
+                _, _, info = frame(cam, cap)
+                tickets.append(info["lists_ticket"])
                 if i and cap.overflowed(tickets[i - 1]):
                     redo += rep
-                    _, _, info = frame(views[i - 1], cap.value)
-                    cap.overflowed(cap.watch(info["lists_status"]))
+                    _, _, info = frame(views[i - 1], cap)
+                    cap.overflowed(info["lists_ticket"])
             if cap.overflowed(tickets[-1]):
                 redo += rep
-                frame(views[-1], cap.value)
+                frame(views[-1], cap)
             torch.cuda.synchronize()
             pipelined = (time.perf_counter() - t0) * 1e3 / frames
         ts = []
@@ -471,7 +474,7 @@ def forward_fps(step, frames=100):
             torch.cuda.synchronize()
             return (time.perf_counter() - t0) * 1e3 / frames
 
-        eager_ms = one_view_ms(lambda: frame(cam, cap.value))
+        eager_ms = one_view_ms(lambda: frame(cam, cap))
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -820,16 +823,16 @@ def render_fps(ramp_s=1.0, k=21):
                 # one frame later).
                 cap = ListCapacity()
                 while True:
-                    _, _, ci = frame(cap.value)
-                    if not cap.overflowed(cap.watch(ci["lists_status"])):
+                    _, _, ci = frame(cap)
+                    if not cap.overflowed(ci["lists_ticket"]):
                         break
                 nf = 4 * k
                 torch.cuda.synchronize()
                 t0 = time.perf_counter()
                 prev = None
                 for _ in range(nf):
-                    _, _, ci = frame(cap.value)
-                    t = cap.watch(ci["lists_status"])
+                    _, _, ci = frame(cap)
+                    t = ci["lists_ticket"]
                     if prev is not None and cap.overflowed(prev):
                         raise RuntimeError("a frame overflowed its sized lists")
                     prev = t

@@ -408,6 +408,10 @@ int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy,
  * tiles the sort uses the buffer as scratch). gauss_ids: (capacity,), may
  * be NULL when capacity is 0; tile_offsets: (tiles_x*tiles_y + 1,); one
  * workspace of mg_bin_lists_capped_workspace_bytes(N, capacity) bytes.
+ * status_host (NULL, or 3 int64 of host memory the device can write, e.g.
+ * from hipHostMalloc) receives the same two words and then tag in
+ * status_host[2] with a system-scope release, so the host can wait for the
+ * words by polling for the tag, with no copy or event on the stream.
  * Replaces the .item() read that sizes the reference's pair buffers
  * (metal_gauss/metal_backend.py:246-248) with a device-side check. */
 int64_t mg_bin_lists_capped_workspace_bytes(int64_t N, int64_t capacity);
@@ -417,7 +421,8 @@ int32_t mg_bin_lists_capped(int64_t N, const float *uv, const float *rxy,
                             int32_t H, int32_t tile, int32_t tiles_x,
                             int32_t tiles_y, int64_t capacity,
                             int32_t *gauss_ids, int32_t *tile_offsets,
-                            int64_t *status, void *workspace,
+                            int64_t *status, int64_t *status_host,
+                            int64_t tag, void *workspace,
                             int64_t workspace_bytes, mg_stream_t stream);
 
 /* -------------------------------------------------------------- rasteriser */

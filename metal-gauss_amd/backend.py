@@ -147,11 +147,14 @@ def _bin(uv, rxy, depth, valid_i, conic, opacity, W, H, tile):
     return gauss_ids, tile_offsets, tx
 
 
-def _bin_capped(uv, rxy, depth, valid_i, conic, opacity, W, H, tile, capacity):
+def _bin_capped(uv, rxy, depth, valid_i, conic, opacity, W, H, tile, capacity,
+                host_slot=None, tag=0):
     """The lists of ``_bin`` with no host read (mg_bin_lists_capped): ids in a
     (capacity,) buffer, and a device int64 (2,) status = (intersection
     total, 1 if it exceeded ``capacity`` else 0). After an overflow every
-    list is empty. Returns (gauss_ids, tile_offsets, tiles_x, status)."""
+    list is empty. ``host_slot`` (an address of 3 int64 of pinned host
+    memory) also receives the two words and then ``tag``. Returns
+    (gauss_ids, tile_offsets, tiles_x, status)."""
     lib = _lib.load()
     device = uv.device
     tx, ty = _tile_grid(W, H, tile)
@@ -171,59 +174,88 @@ def _bin_capped(uv, rxy, depth, valid_i, conic, opacity, W, H, tile, capacity):
         _lib.dev_tensor(opacity, "opacity") if opacity is not None else None,
         _lib.dev_tensor(valid_i, "valid", torch.int32), _lib.dev_tensor(depth, "depth"),
         W, H, tile, tx, ty, capacity, gauss_ids.data_ptr() if capacity else None,
-        tile_offsets.data_ptr(), status.data_ptr(), ws.data_ptr(), ws.numel(), s))
+        tile_offsets.data_ptr(), status.data_ptr(), host_slot, int(tag), ws.data_ptr(),
+        ws.numel(), s))
     return gauss_ids, tile_offsets, tx, status
 
 
 class ListCapacity:
     """Sizes a render's tile lists without a host read in the render.
 
-    ``render(..., list_capacity=cap.value)`` builds the lists in buffers of
-    that many intersections and reports, on the device, the total and
-    whether it overflowed (``info["lists_status"]``); an overflowed render
-    has empty lists (a background image), and optimizer steps given that
-    status as ``skip`` leave every parameter as it was. ``watch`` queues a
-    copy of the status to pinned host memory right after the render and
-    returns a ticket; ``overflowed(ticket)`` waits for that copy only (by
-    then the rest of the step, or the next frame, is usually enqueued
-    behind it) and, on overflow, raises ``value`` to ``headroom`` times the
-    total seen, for that render to be run again. Up to ``depth`` watched
-    renders may be outstanding. The reference sizes its buffers by reading
-    the total on the host in the middle of every render
-    (metal_backend.py:246-248), which drains the queue once per render.
+    Pass the object itself as ``render(..., list_capacity=cap)``: the lists
+    are built in buffers of ``cap.value`` intersections, and the kernel that
+    forms the intersection total also writes it, with an overflow word and a
+    ticket's tag, into a pinned host slot of this object, so no copy or
+    event joins the stream. ``cap.overflowed(ticket)`` (default: the latest
+    render) polls that slot and, on overflow, raises ``value`` to
+    ``headroom`` times the total seen, for that render to be run again. An
+    overflowed render has empty lists (a background image), and optimizer
+    steps given its ``info["lists_status"]`` as ``skip`` leave every
+    parameter as it was. With an int capacity instead, ``watch(status)``
+    queues a copy of the device status words to pinned memory behind an
+    event, and ``overflowed`` waits for that event. Up to ``depth`` renders
+    may be outstanding. The reference sizes its buffers by reading the total
+    on the host in the middle of every render (metal_backend.py:246-248),
+    which drains the queue once per render.
     """
 
-    def __init__(self, initial: int = 0, headroom: float = 1.25, depth: int = 4):
+    def __init__(self, initial: int = 0, headroom: float = 1.25, depth: int = 8):
         self.value = int(initial)
         self.headroom = float(headroom)
         self.depth = int(depth)
         self.last_total = None
         self.overflows = 0
-        self._slots = None
+        self._slots = None      # pinned (depth, 3) int64: total, overflow, tag
+        self._view = None       # the same memory as a numpy array, for polling
         self._events = None
+        self._event_mode = None
         self._issued = 0
 
-    def watch(self, status: torch.Tensor) -> int:
+    def _next(self, event_mode: bool) -> int:
         if self._slots is None:
-            self._slots = torch.zeros(self.depth, 2, dtype=torch.int64, pin_memory=True)
-            self._events = [torch.cuda.Event() for _ in range(self.depth)]
+            self._slots = torch.zeros(self.depth, 3, dtype=torch.int64, pin_memory=True)
+            self._view = self._slots.numpy()
+            self._events = [None] * self.depth
+            self._event_mode = [False] * self.depth
         ticket = self._issued
-        k = ticket % self.depth
-        self._slots[k].copy_(status, non_blocking=True)
-        self._events[k].record(torch.cuda.current_stream(status.device))
         self._issued += 1
+        k = ticket % self.depth
+        self._view[k, 2] = -1
+        self._event_mode[k] = event_mode
         return ticket
 
-    def overflowed(self, ticket: int | None = None) -> bool:
-        """Whether the render watched under ``ticket`` (default: the latest)
-        overflowed; waits for its status copy."""
+    def claim(self) -> tuple[int, int, int]:
+        """(host slot address, tag, ticket) for the next render; render()
+        calls this when given the object."""
+        ticket = self._next(False)
+        k = ticket % self.depth
+        return self._slots[k].data_ptr(), ticket + 1, ticket
+
+    def watch(self, status: torch.Tensor) -> int:
+        ticket = self._next(True)
+        k = ticket % self.depth
+        self._slots[k, :2].copy_(status, non_blocking=True)
+        if self._events[k] is None:
+            self._events[k] = torch.cuda.Event()
+        self._events[k].record(torch.cuda.current_stream(status.device))
+        return ticket
+
+    def overflowed(self, ticket: int | None = None, timeout_s: float = 60.0) -> bool:
+        """Whether the render under ``ticket`` (default: the latest)
+        overflowed; waits for its status."""
         if ticket is None:
             ticket = self._issued - 1
         if ticket < 0 or ticket >= self._issued or ticket < self._issued - self.depth:
-            raise RuntimeError(f"ListCapacity: no outstanding watch for ticket {ticket}")
+            raise RuntimeError(f"ListCapacity: no outstanding render for ticket {ticket}")
         k = ticket % self.depth
-        self._events[k].synchronize()
-        total, over = int(self._slots[k, 0]), int(self._slots[k, 1])
+        if self._event_mode[k]:
+            self._events[k].synchronize()
+        else:
+            end = time.perf_counter() + timeout_s
+            while self._view[k, 2] != ticket + 1:
+                if time.perf_counter() > end:
+                    raise RuntimeError("ListCapacity: the lists' status never arrived")
+        total, over = int(self._view[k, 0]), int(self._view[k, 1])
         self.last_total = total
         if over:
             self.overflows += 1
@@ -790,7 +822,7 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
            sh_rest=None, antialias: bool = False, absgrad_out=None,
            min_transmittance: float = DEFAULT_T_MIN, chunked_backward: bool = False,
            filter_3d=None, activations: bool = False, optimizer=None,
-           opacity_reg: float = 0.0, scale_reg: float = 0.0, list_capacity: int | None = None,
+           opacity_reg: float = 0.0, scale_reg: float = 0.0, list_capacity=None,
            **_ignored):
     """Render Gaussians from one camera; same signature as the reference's.
 
@@ -831,14 +863,16 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     ``.grad`` after their update: ``step()`` then raises instead of updating
     them a second time. When the optimizer or the tensors do not allow the
     epilogue, the ordinary gradients are returned.
-    ``list_capacity`` (an int, see ``ListCapacity``) builds the tile lists
+    ``list_capacity`` (a ``ListCapacity``, or an int) builds the tile lists
     in buffers of that many intersections with no host read, so the render
     enqueues without waiting for the GPU. ``info["lists_status"]`` is then a
     device int64 (2,): the intersection total, and 1 if it exceeded the
     capacity, in which case every list is empty (the image is the
     background), the epilogue of ``optimizer`` does nothing, and the caller
-    renders again with a larger capacity. ``info["isect_total"]`` is then
-    that device total (0-d) instead of an int.
+    renders again with a larger capacity; with a ``ListCapacity`` the same
+    words reach its host slot and ``info["lists_ticket"]`` is the ticket to
+    check with ``overflowed``. ``info["isect_total"]`` is then that device
+    total (0-d) instead of an int.
     """
     explicit_colors = colors is not None
     opacities_in = opacities
@@ -891,15 +925,20 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
             W, H, near, far, 0.3, max_radius, cam_center, sh_degree, valid_b)
 
     status = None
+    ticket = None
     if list_capacity is None:
         gauss_ids, tile_offsets, tiles_x = build_tile_lists_metal(
             uv.detach(), rxy.detach(), depth.detach(), valid_i, conic.detach(),
             opacities.detach(), W, H, tile)
     else:
+        slot, tag, capacity = None, 0, list_capacity
+        if isinstance(list_capacity, ListCapacity):
+            slot, tag, ticket = list_capacity.claim()
+            capacity = list_capacity.value
         gauss_ids, tile_offsets, tiles_x, status = _bin_capped(
             uv.detach().contiguous(), rxy.detach().contiguous(), depth.detach().contiguous(),
             valid_i.contiguous(), conic.detach().contiguous(), opacities.detach().contiguous(),
-            W, H, tile, list_capacity)
+            W, H, tile, capacity, slot, tag)
         lists[0] = status
 
     # A constant background (tuple, list or CPU tensor without grad) is
@@ -925,6 +964,7 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
         "tiles": int(tile_offsets.numel() - 1),
         "isect_total": int(gauss_ids.numel()) if status is None else status[0],
         "lists_status": status,
+        "lists_ticket": ticket,
         "isect_dropped": 0,
         "isect_dropped_frac": 0.0,
         "valid_mask": valid_b,

@@ -626,13 +626,18 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
 // the first pair of count workgroup i's Gaussians, st->total the intersection
 // total.
 // With status (capacity-bounded lists) it also writes status[0] = the total
-// and status[1] = 1 if the total exceeds capacity, else 0.
+// and status[1] = 1 if the total exceeds capacity, else 0; with status_host
+// (host memory the device can write) the same two words and then tag in
+// status_host[2], ordered by a system-scope release, so the host can wait by
+// polling for the tag instead of an event.
 __global__ __launch_bounds__(kScanThreads) void bin_offsets_kernel(const BinPart *parts,
                                                                    int64_t nparts,
                                                                    int64_t *part_off,
                                                                    BinStats *st,
                                                                    int64_t capacity,
-                                                                   int64_t *status) {
+                                                                   int64_t *status,
+                                                                   int64_t *status_host,
+                                                                   int64_t tag) {
     // Blocked: thread t owns 16 consecutive totals of each 4096-entry step,
     // all requested at once; one block scan per step.
     constexpr int kPer = 16;
@@ -661,6 +666,13 @@ __global__ __launch_bounds__(kScanThreads) void bin_offsets_kernel(const BinPart
         if (status) {
             status[0] = carry;
             status[1] = carry > capacity ? 1 : 0;
+        }
+        if (status_host) {
+            __hip_atomic_store(status_host, carry, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(status_host + 1, (int64_t)(carry > capacity ? 1 : 0),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(status_host + 2, tag, __ATOMIC_RELEASE,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
 }
@@ -1727,7 +1739,7 @@ int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy, const f
     {
         TimedScope ts("exclusive_scan", s);
         bin_offsets_kernel<<<1, kScanThreads, 0, s>>>(ws.parts, nparts, ws.part_off, ws.stats,
-                                                       0, nullptr);
+                                                       0, nullptr, nullptr, 0);
         MG_LAUNCHED("bin_offsets_kernel");
     }
     // The one host read: the total sizes the caller's id buffer. It is copied
@@ -1786,8 +1798,8 @@ int32_t mg_bin_lists_capped(int64_t N, const float *uv, const float *rxy, const 
                             const float *opacity, const int32_t *valid, const float *depth,
                             int32_t W, int32_t H, int32_t tile, int32_t tiles_x, int32_t tiles_y,
                             int64_t capacity, int32_t *gauss_ids, int32_t *tile_offsets,
-                            int64_t *status, void *workspace, int64_t workspace_bytes,
-                            mg_stream_t stream) {
+                            int64_t *status, int64_t *status_host, int64_t tag,
+                            void *workspace, int64_t workspace_bytes, mg_stream_t stream) {
     int32_t rc = check_bin_args("mg_bin_lists_capped", N, uv, rxy, conic, opacity, valid, W, H,
                                 tile, tiles_x, tiles_y);
     if (rc != MG_OK) return rc;
@@ -1813,7 +1825,8 @@ int32_t mg_bin_lists_capped(int64_t N, const float *uv, const float *rxy, const 
     {
         TimedScope ts("exclusive_scan", s);
         bin_offsets_kernel<<<1, kScanThreads, 0, s>>>(ws.parts, nparts, ws.part_off, ws.stats,
-                                                       capacity, status);
+                                                       capacity, status, status_host,
+                                                       tag);
         MG_LAUNCHED("bin_offsets_kernel");
     }
     return emit_and_sort(ws, N, conic, depth, W, H, tile, tiles_x, tiles_x * tiles_y,

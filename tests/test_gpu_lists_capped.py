@@ -38,6 +38,7 @@ def _both(s, dev, tile, ellipse, capacity_of):
     got_ids = torch.full((max(cap, 1),), -7, dtype=torch.int32, device=dev)
     got_offs = torch.full((n_tiles + 1,), -7, dtype=torch.int32, device=dev)
     status = torch.full((2,), -7, dtype=torch.int64, device=dev)
+    host = torch.full((3,), -7, dtype=torch.int64, pin_memory=True)
     N = uv.shape[0]
     ws = torch.empty(lib.mg_bin_lists_capped_workspace_bytes(N, cap), dtype=torch.uint8,
                      device=dev)
@@ -45,10 +46,12 @@ def _both(s, dev, tile, ellipse, capacity_of):
         N, uv.data_ptr(), rxy.data_ptr(), conic.data_ptr() if ellipse else None,
         op.data_ptr() if ellipse else None, valid.data_ptr(), depth.data_ptr(), s["W"], s["H"],
         tile, tx, n_tiles // tx, cap, got_ids.data_ptr() if cap else None, got_offs.data_ptr(),
-        status.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream(uv)))
+        status.data_ptr(), host.data_ptr(), 99, ws.data_ptr(), ws.numel(), _lib.stream(uv)))
     torch.cuda.synchronize()
+    st = status.cpu().numpy()
+    assert host.tolist() == [int(st[0]), int(st[1]), 99], "host slot differs from the device words"
     return (ids.cpu().numpy(), offs.cpu().numpy(), total, cap, got_ids.cpu().numpy(),
-            got_offs.cpu().numpy(), status.cpu().numpy())
+            got_offs.cpu().numpy(), st)
 
 
 CAPS = {
@@ -136,6 +139,35 @@ def test_render_with_capacity_equals_render(dev):
         assert torch.equal(rgb, torch.tensor([0.1, 0.2, 0.3], device=dev).expand_as(rgb))
 
 
+def test_list_capacity_host_slots_and_device_copies(dev):
+    """ListCapacity given to render gets the status words in its pinned
+    slots from the kernel itself (several renders outstanding, checked out
+    of order); with int capacities, watch() copies them behind an event.
+    Both report the total, flag the overflow and grow the capacity."""
+    from metal_gauss_amd import ListCapacity
+
+    s = scene(n=3000, seed=21, sh=True)
+    p = _leaves(s, dev)
+    with torch.no_grad():
+        total = _render(p, None)[2]["isect_total"]
+        cap = ListCapacity(initial=total - 1, depth=4)
+        tickets = [_render(p, cap)[2]["lists_ticket"] for _ in range(3)]
+        assert tickets == [0, 1, 2]
+        assert cap.overflowed(tickets[2]) and cap.last_total == total
+        assert cap.overflowed(tickets[0])
+        assert cap.value >= total and cap.overflows == 2
+        rgb, _, info = _render(p, cap)
+        assert not cap.overflowed(info["lists_ticket"]) and cap.last_total == total
+        _render(p, cap)                      # a fifth render reuses ticket 0's slot
+        with pytest.raises(RuntimeError, match="no outstanding render"):
+            cap.overflowed(0)
+        old = ListCapacity(initial=total - 1)
+        _, _, info = _render(p, old.value)
+        assert old.overflowed(old.watch(info["lists_status"])) and old.last_total == total
+        _, _, info = _render(p, old.value)
+        assert not old.overflowed(old.watch(info["lists_status"]))
+
+
 def _state(opt, p):
     out = {}
     for k, t in p.items():
@@ -178,12 +210,11 @@ def test_overflowed_step_changes_nothing_and_the_rerun_matches(dev, epilogue):
     reruns = 0
     for step in range(3):
         while True:
-            rgb, _, info = _render(p, cap.value, opt if epilogue else None)
-            cap.watch(info["lists_status"])
+            rgb, _, info = _render(p, cap, opt if epilogue else None)
             opt.zero_grad(set_to_none=True)
             (rgb - gt).abs().mean().backward()
             opt.step(skip=info["lists_status"])
-            if not cap.overflowed():
+            if not cap.overflowed(info["lists_ticket"]):
                 break
             reruns += 1
             opt.rewind()
