@@ -986,17 +986,55 @@ __global__ __launch_bounds__(kCsThreads) void count_hist_kernel(const CsPass<V> 
 
 // One workgroup per 64 tiles, lane = tile; each of its 16 waves scans a
 // sixteenth of the chunks (coalesced rows), the waves' sums are joined
-// through LDS, and each wave writes its running exclusive prefixes.
+// through LDS, and each wave writes its running exclusive prefixes. Up to
+// kColRows rows per wave (1024 chunks) all of a wave's rows are requested at
+// once and parked in LDS as 16-bit counts (a chunk holds at most 16384
+// pairs) for the prefix pass; walking the rows in batches instead makes a
+// chain of dependent HBM round trips (12 us at config 4).
+constexpr int kColRows = 64;
+static_assert((int64_t)kCsThreads * 64 <= 65535, "per-chunk tile counts must fit 16 bits");
+
 template <typename V>
 __global__ __launch_bounds__(64 * kColWaves) void count_colscan_kernel(const CsPass<V> P,
                                                                        int64_t nchunks) {
     __shared__ uint32_t s_sum[kColWaves][64];
+    __shared__ uint16_t s_val[kColWaves][kColRows][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int bkt = blockIdx.x * 64 + lane;
     const bool in = bkt < P.nb;
     if (P.status) nchunks = cs_active(P, cs_count(P));
     const int64_t q = (nchunks + kColWaves - 1) / kColWaves;
     const int64_t c0 = wave * q, c1 = min(nchunks, c0 + q);
+    if (q <= kColRows) {   // workgroup-uniform
+        const uint32_t *row = P.hist + c0 * P.nb + bkt;
+        uint32_t vals[kColRows];
+#pragma unroll
+        for (int i = 0; i < kColRows; ++i)
+            vals[i] = in && c0 + i < c1 ? row[(int64_t)i * P.nb] : 0u;
+        uint32_t sum = 0;
+#pragma unroll
+        for (int i = 0; i < kColRows; ++i) {
+            s_val[wave][i][lane] = (uint16_t)vals[i];
+            sum += vals[i];
+        }
+        s_sum[wave][lane] = sum;
+        __syncthreads();
+        uint32_t run = 0, all = 0;
+#pragma unroll
+        for (int w = 0; w < kColWaves; ++w) {
+            const uint32_t v = s_sum[w][lane];
+            run += w < wave ? v : 0u;
+            all += v;
+        }
+        if (in) {
+            for (int64_t c = c0; c < c1; ++c) {
+                P.hist[c * P.nb + bkt] = run;
+                run += s_val[wave][c - c0][lane];
+            }
+            if (wave == 0) P.tot[bkt] = all;
+        }
+        return;
+    }
     uint32_t sum = 0;
 #pragma unroll 8
     for (int64_t c = c0; c < c1; ++c) sum += in ? P.hist[c * P.nb + bkt] : 0u;
