@@ -131,7 +131,20 @@ __global__ void ssim_chain_bwd_kernel(const float *x, const float *y, const floa
 // ------------------------------------------------------------- fused kernels
 constexpr int kTW = 32, kTH = 16;                 // output tile
 constexpr int kIW = kTW + 2 * kR, kIH = kTH + 2 * kR;   // 42 x 26 with halo
+constexpr int kIWP = 44;                          // LDS row stride: 16-byte rows
 constexpr int kSsimThreads = 256;
+// Register blocking of the separable blur: a horizontal task makes kHRun
+// neighbouring outputs of one row from one read of its kHRun + 2 kR inputs;
+// a vertical task makes kVRun outputs of one column.
+constexpr int kHRun = 4, kVRun = 2;
+constexpr int kHTasks = kIH * (kTW / kHRun);      // 208
+constexpr int kVTasks = (kTH / kVRun) * kTW;      // 256
+static_assert(kHTasks <= kSsimThreads && kVTasks == kSsimThreads, "blur tasks per thread");
+static_assert(kHRun + 2 * kR <= 16 && (kTW / kHRun - 1) * kHRun + 16 <= kIWP,
+              "a horizontal task reads four float4s of its row");
+// Halo elements per thread: all of a thread's loads are requested before any
+// of them is stored to LDS (a rolled loop waits for each in turn).
+constexpr int kLoadIters = (kIH * kIW + kSsimThreads - 1) / kSsimThreads;   // 5
 
 // Work items of the fused kernels: (output tile, channel) pairs, item =
 // 3 * tile + channel, tile = ty * tiles_x + tx. The items are dealt to the XCDs
@@ -147,76 +160,134 @@ __device__ __forceinline__ SsimItem ssim_item(int tiles_x) {
     return {tile % tiles_x, tile / tiles_x, item - 3 * tile};
 }
 
+// The horizontal task of thread t: row t / (kTW / kHRun), first output column
+// kHRun * (t % (kTW / kHRun)); its inputs are 16 floats of that LDS row from
+// the same column.
+__device__ __forceinline__ void h_inputs(const float (*src)[kIWP], int t, int &row, int &c0,
+                                         float (&v)[16]) {
+    row = t / (kTW / kHRun);
+    c0 = kHRun * (t % (kTW / kHRun));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 f = *reinterpret_cast<const float4 *>(&src[row][c0 + 4 * q]);
+        v[4 * q] = f.x;
+        v[4 * q + 1] = f.y;
+        v[4 * q + 2] = f.z;
+        v[4 * q + 3] = f.w;
+    }
+}
+
 // block_sums[b] gets work item b's SSIM sum; with l1_sums, l1_sums[b] gets
 // its sum of |x - y| over the same pixels and channel.
 __global__ __launch_bounds__(kSsimThreads) void ssim_fused_fwd_kernel(
-    const float *x, const float *y, const float *w, int H, int W, int tiles_x, float *partials,
-    float *block_sums, float *l1_sums) {
-    __shared__ float s_x[kIH][kIW], s_y[kIH][kIW];
-    __shared__ float s_h[5][kIH][kTW];
-    __shared__ float s_w[2 * kR + 1];
+    const float *x, const float *y, const float *__restrict__ w, int H, int W, int tiles_x,
+    float *partials, float *block_sums, float *l1_sums) {
+    __shared__ __align__(16) float s_x[kIH][kIWP];
+    __shared__ __align__(16) float s_y[kIH][kIWP];
+    __shared__ __align__(16) float s_h[5][kIH][kTW];
     __shared__ float s_red[2][kSsimThreads / 64];
     const SsimItem it = ssim_item(tiles_x);
     const int c = it.c;
     const int x0 = it.tx * kTW - kR, y0 = it.ty * kTH - kR;
     const int tid = threadIdx.x;
-    if (tid < 2 * kR + 1) s_w[tid] = w[tid];
-    for (int i = tid; i < kIH * kIW; i += kSsimThreads) {
-        const int ly = i / kIW, lx = i - ly * kIW;
-        const int gx = x0 + lx, gy = y0 + ly;
-        float xv = 0.f, yv = 0.f;
-        if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
-            const int64_t o = ((int64_t)gy * W + gx) * 3 + c;
-            xv = x[o];
-            yv = y[o];
-        }
-        s_x[ly][lx] = xv;
-        s_y[ly][lx] = yv;
-    }
-    __syncthreads();
-    // Horizontal pass over the full halo height.
-    for (int i = tid; i < kIH * kTW; i += kSsimThreads) {
-        const int ly = i / kTW, lx = i - ly * kTW;
-        float sx = 0, sy = 0, sxx = 0, syy = 0, sxy = 0;
+    float wk[2 * kR + 1];
 #pragma unroll
-        for (int k = 0; k <= 2 * kR; ++k) {
-            const float wk = s_w[k];
-            const float xv = s_x[ly][lx + k], yv = s_y[ly][lx + k];
-            sx += wk * xv;
-            sy += wk * yv;
-            sxx += wk * xv * xv;
-            syy += wk * yv * yv;
-            sxy += wk * xv * yv;
+    for (int k = 0; k <= 2 * kR; ++k) wk[k] = w[k];
+    {
+        float xv[kLoadIters], yv[kLoadIters];
+#pragma unroll
+        for (int r = 0; r < kLoadIters; ++r) {
+            const int i = tid + r * kSsimThreads;
+            const int ly = i / kIW, lx = i - ly * kIW;
+            const int gx = x0 + lx, gy = y0 + ly;
+            xv[r] = 0.f;
+            yv[r] = 0.f;
+            if (i < kIH * kIW && gx >= 0 && gx < W && gy >= 0 && gy < H) {
+                const int64_t o = ((int64_t)gy * W + gx) * 3 + c;
+                xv[r] = x[o];
+                yv[r] = y[o];
+            }
         }
-        s_h[0][ly][lx] = sx;
-        s_h[1][ly][lx] = sy;
-        s_h[2][ly][lx] = sxx;
-        s_h[3][ly][lx] = syy;
-        s_h[4][ly][lx] = sxy;
+#pragma unroll
+        for (int r = 0; r < kLoadIters; ++r) {
+            const int i = tid + r * kSsimThreads;
+            if (i < kIH * kIW) {
+                const int ly = i / kIW, lx = i - ly * kIW;
+                s_x[ly][lx] = xv[r];
+                s_y[ly][lx] = yv[r];
+            }
+        }
+    }
+    // The pad columns are read by the last task of a row (weights beyond
+    // its window are never applied to them, but they must be finite).
+    for (int i = tid; i < kIH * (kIWP - kIW); i += kSsimThreads) {
+        const int ly = i / (kIWP - kIW), lx = kIW + i % (kIWP - kIW);
+        s_x[ly][lx] = 0.f;
+        s_y[ly][lx] = 0.f;
     }
     __syncthreads();
-    // Vertical pass and the SSIM tail at the tile's own pixels.
+    // Horizontal pass over the full halo height: each input's x, y, x^2,
+    // y^2 and xy once, into the kHRun outputs whose window holds it.
+    if (tid < kHTasks) {
+        int row, c0;
+        float xv[16], yv[16];
+        h_inputs(s_x, tid, row, c0, xv);
+        h_inputs(s_y, tid, row, c0, yv);
+        float m[5][kHRun] = {};
+#pragma unroll
+        for (int j = 0; j < kHRun + 2 * kR; ++j) {
+            const float a = xv[j], b = yv[j], aa = a * a, bb = b * b, ab = a * b;
+#pragma unroll
+            for (int o = 0; o < kHRun; ++o) {
+                const int k = j - o;
+                if (k < 0 || k > 2 * kR) continue;
+                m[0][o] = fmaf(wk[k], a, m[0][o]);
+                m[1][o] = fmaf(wk[k], b, m[1][o]);
+                m[2][o] = fmaf(wk[k], aa, m[2][o]);
+                m[3][o] = fmaf(wk[k], bb, m[3][o]);
+                m[4][o] = fmaf(wk[k], ab, m[4][o]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 5; ++q)
+            *reinterpret_cast<float4 *>(&s_h[q][row][c0]) =
+                make_float4(m[q][0], m[q][1], m[q][2], m[q][3]);
+    }
+    __syncthreads();
+    // Vertical pass and the SSIM tail: thread t makes rows kVRun * (t / kTW)
+    // + [0, kVRun) of column t % kTW.
     const int64_t N = (int64_t)W * H;
     float local = 0.f, local_l1 = 0.f;
-    for (int i = tid; i < kTH * kTW; i += kSsimThreads) {
-        const int ly = i / kTW, lx = i - ly * kTW;
-        const int gx = it.tx * kTW + lx, gy = it.ty * kTH + ly;
-        if (gx >= W || gy >= H) continue;
-        local_l1 += fabsf(s_x[ly + kR][lx + kR] - s_y[ly + kR][lx + kR]);
-        float m[5] = {0, 0, 0, 0, 0};
+    {
+        const int lx = tid % kTW, r0 = kVRun * (tid / kTW);
+        float m[kVRun][5] = {};
 #pragma unroll
-        for (int k = 0; k <= 2 * kR; ++k) {
-            const float wk = s_w[k];
+        for (int j = 0; j < kVRun + 2 * kR; ++j) {
+            float h[5];
 #pragma unroll
-            for (int q = 0; q < 5; ++q) m[q] += wk * s_h[q][ly + k][lx];
+            for (int q = 0; q < 5; ++q) h[q] = s_h[q][r0 + j][lx];
+#pragma unroll
+            for (int o = 0; o < kVRun; ++o) {
+                const int k = j - o;
+                if (k < 0 || k > 2 * kR) continue;
+#pragma unroll
+                for (int q = 0; q < 5; ++q) m[o][q] = fmaf(wk[k], h[q], m[o][q]);
+            }
         }
-        float S, pm, pxx, pxy;
-        ssim_terms(m[0], m[1], m[2], m[3], m[4], S, pm, pxx, pxy);
-        local += S;
-        const int64_t o = (int64_t)gy * W + gx;
-        partials[(0 + c) * N + o] = pm;
-        partials[(3 + c) * N + o] = pxx;
-        partials[(6 + c) * N + o] = pxy;
+        const int gx = it.tx * kTW + lx;
+#pragma unroll
+        for (int o = 0; o < kVRun; ++o) {
+            const int ly = r0 + o, gy = it.ty * kTH + ly;
+            if (gx >= W || gy >= H) continue;
+            local_l1 += fabsf(s_x[ly + kR][lx + kR] - s_y[ly + kR][lx + kR]);
+            float S, pm, pxx, pxy;
+            ssim_terms(m[o][0], m[o][1], m[o][2], m[o][3], m[o][4], S, pm, pxx, pxy);
+            local += S;
+            const int64_t po = (int64_t)gy * W + gx;
+            partials[(0 + c) * N + po] = pm;
+            partials[(3 + c) * N + po] = pxx;
+            partials[(6 + c) * N + po] = pxy;
+        }
     }
     // Deterministic per-block sums (fixed reduction order).
     for (int off = 32; off >= 1; off >>= 1) {
@@ -240,11 +311,40 @@ __global__ __launch_bounds__(kSsimThreads) void ssim_fused_fwd_kernel(
     }
 }
 
+// Sums of K arrays of block sums (nb >= 1) in double, for a one-workgroup
+// reduction: each thread requests kSumPer values of every array at once per
+// step (a rolled loop waits for each load in turn).
+constexpr int kSumPer = 16;
+template <int K>
+__device__ __forceinline__ void sum_blocks(const float *const (&v)[K], int64_t nb, double (&s)[K]) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) s[k] = 0.0;
+    for (int64_t b = 0; b < nb; b += 256 * kSumPer) {
+        float t[K][kSumPer];
+        // Unconditional loads of a clamped index, then a select: a guarded
+        // load becomes a branch that waits for it before the next.
+#pragma unroll
+        for (int j = 0; j < kSumPer; ++j) {
+            const int64_t i = b + threadIdx.x + 256 * j;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const float u = v[k][min(i, nb - 1)];
+                t[k][j] = i < nb ? u : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kSumPer; ++j)
+#pragma unroll
+            for (int k = 0; k < K; ++k) s[k] += (double)t[k][j];
+    }
+}
+
 __global__ __launch_bounds__(256) void ssim_mean_kernel(const float *block_sums, int64_t nb,
                                                         int64_t count, float *mean_out) {
     __shared__ double s_red[4];
-    double s = 0.0;
-    for (int64_t i = threadIdx.x; i < nb; i += 256) s += (double)block_sums[i];
+    double sv[1];
+    sum_blocks<1>({block_sums}, nb, sv);
+    double s = sv[0];
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
     if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = s;
     __syncthreads();
@@ -258,11 +358,9 @@ __global__ __launch_bounds__(256) void photometric_loss_kernel(const float *ssim
                                                                int64_t count, float lam,
                                                                float *out) {
     __shared__ double s_red[2][4];
-    double s = 0.0, s1 = 0.0;
-    for (int64_t i = threadIdx.x; i < nb; i += 256) {
-        s += (double)ssim_sums[i];
-        s1 += (double)l1_sums[i];
-    }
+    double sv[2];
+    sum_blocks<2>({ssim_sums, l1_sums}, nb, sv);
+    double s = sv[0], s1 = sv[1];
     for (int off = 32; off >= 1; off >>= 1) {
         s += __shfl_xor(s, off, 64);
         s1 += __shfl_xor(s1, off, 64);
@@ -286,69 +384,102 @@ __global__ __launch_bounds__(256) void photometric_loss_kernel(const float *ssim
 // a_ssim = 1, a_l1 = 0 is the gradient of the SSIM mean; a_ssim = -lam,
 // a_l1 = 1 - lam that of the photometric loss.
 __global__ __launch_bounds__(kSsimThreads) void ssim_fused_bwd_kernel(
-    const float *x, const float *y, const float *w, const float *partials, const float *scale_dev,
-    int H, int W, int tiles_x, float a_ssim, float a_l1, float *dx) {
-    __shared__ float s_p[3][kIH][kIW];
-    __shared__ float s_h[3][kIH][kTW];
-    __shared__ float s_w[2 * kR + 1];
+    const float *x, const float *y, const float *__restrict__ w, const float *partials,
+    const float *scale_dev, int H, int W, int tiles_x, float a_ssim, float a_l1, float *dx) {
+    __shared__ __align__(16) float s_p[3][kIH][kIWP];
+    __shared__ __align__(16) float s_h[3][kIH][kTW];
     const SsimItem it = ssim_item(tiles_x);
     const int c = it.c;
     const int x0 = it.tx * kTW - kR, y0 = it.ty * kTH - kR;
     const int tid = threadIdx.x;
     const int64_t N = (int64_t)W * H;
-    if (tid < 2 * kR + 1) s_w[tid] = w[tid];
-    for (int i = tid; i < kIH * kIW; i += kSsimThreads) {
-        const int ly = i / kIW, lx = i - ly * kIW;
-        const int gx = x0 + lx, gy = y0 + ly;
-        float a = 0.f, b = 0.f, d = 0.f;
-        if (gx >= 0 && gx < W && gy >= 0 && gy < H) {
-            const int64_t o = (int64_t)gy * W + gx;
-            a = partials[(0 + c) * N + o];
-            b = partials[(3 + c) * N + o];
-            d = partials[(6 + c) * N + o];
+    float wk[2 * kR + 1];
+#pragma unroll
+    for (int k = 0; k <= 2 * kR; ++k) wk[k] = w[k];
+    {
+        float pv[3][kLoadIters];
+#pragma unroll
+        for (int r = 0; r < kLoadIters; ++r) {
+            const int i = tid + r * kSsimThreads;
+            const int ly = i / kIW, lx = i - ly * kIW;
+            const int gx = x0 + lx, gy = y0 + ly;
+#pragma unroll
+            for (int q = 0; q < 3; ++q) pv[q][r] = 0.f;
+            if (i < kIH * kIW && gx >= 0 && gx < W && gy >= 0 && gy < H) {
+                const int64_t o = (int64_t)gy * W + gx;
+#pragma unroll
+                for (int q = 0; q < 3; ++q) pv[q][r] = partials[(3 * q + c) * N + o];
+            }
         }
-        s_p[0][ly][lx] = a;
-        s_p[1][ly][lx] = b;
-        s_p[2][ly][lx] = d;
+#pragma unroll
+        for (int r = 0; r < kLoadIters; ++r) {
+            const int i = tid + r * kSsimThreads;
+            if (i < kIH * kIW) {
+                const int ly = i / kIW, lx = i - ly * kIW;
+#pragma unroll
+                for (int q = 0; q < 3; ++q) s_p[q][ly][lx] = pv[q][r];
+            }
+        }
+    }
+    for (int i = tid; i < kIH * (kIWP - kIW); i += kSsimThreads) {
+        const int ly = i / (kIWP - kIW), lx = kIW + i % (kIWP - kIW);
+        s_p[0][ly][lx] = 0.f;
+        s_p[1][ly][lx] = 0.f;
+        s_p[2][ly][lx] = 0.f;
     }
     __syncthreads();
-    for (int i = tid; i < kIH * kTW; i += kSsimThreads) {
-        const int ly = i / kTW, lx = i - ly * kTW;
-        float s0 = 0, s1 = 0, s2 = 0;
+    if (tid < kHTasks) {
+        int row, c0;
+        float v[3][16];
 #pragma unroll
-        for (int k = 0; k <= 2 * kR; ++k) {
-            const float wk = s_w[k];
-            s0 += wk * s_p[0][ly][lx + k];
-            s1 += wk * s_p[1][ly][lx + k];
-            s2 += wk * s_p[2][ly][lx + k];
+        for (int q = 0; q < 3; ++q) h_inputs(s_p[q], tid, row, c0, v[q]);
+        float m[3][kHRun] = {};
+#pragma unroll
+        for (int j = 0; j < kHRun + 2 * kR; ++j) {
+#pragma unroll
+            for (int o = 0; o < kHRun; ++o) {
+                const int k = j - o;
+                if (k < 0 || k > 2 * kR) continue;
+#pragma unroll
+                for (int q = 0; q < 3; ++q) m[q][o] = fmaf(wk[k], v[q][j], m[q][o]);
+            }
         }
-        s_h[0][ly][lx] = s0;
-        s_h[1][ly][lx] = s1;
-        s_h[2][ly][lx] = s2;
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+            *reinterpret_cast<float4 *>(&s_h[q][row][c0]) =
+                make_float4(m[q][0], m[q][1], m[q][2], m[q][3]);
     }
     __syncthreads();
     const float scale = scale_dev[0] / (float)(3 * N);
-    for (int i = tid; i < kTH * kTW; i += kSsimThreads) {
-        const int ly = i / kTW, lx = i - ly * kTW;
-        const int gx = it.tx * kTW + lx, gy = it.ty * kTH + ly;
-        if (gx >= W || gy >= H) continue;
-        float b0 = 0, b1 = 0, b2 = 0;
+    const int lx = tid % kTW, r0 = kVRun * (tid / kTW);
+    float m[kVRun][3] = {};
 #pragma unroll
-        for (int k = 0; k <= 2 * kR; ++k) {
-            const float wk = s_w[k];
-            b0 += wk * s_h[0][ly + k][lx];
-            b1 += wk * s_h[1][ly + k][lx];
-            b2 += wk * s_h[2][ly + k][lx];
+    for (int j = 0; j < kVRun + 2 * kR; ++j) {
+        float h[3];
+#pragma unroll
+        for (int q = 0; q < 3; ++q) h[q] = s_h[q][r0 + j][lx];
+#pragma unroll
+        for (int o = 0; o < kVRun; ++o) {
+            const int k = j - o;
+            if (k < 0 || k > 2 * kR) continue;
+#pragma unroll
+            for (int q = 0; q < 3; ++q) m[o][q] = fmaf(wk[k], h[q], m[o][q]);
         }
-        const int64_t o = ((int64_t)gy * W + gx) * 3 + c;
-        const float xv = x[o], yv = y[o];
-        float d = a_ssim * (b0 + 2.0f * xv * b1 + yv * b2);
+    }
+    const int gx = it.tx * kTW + lx;
+#pragma unroll
+    for (int o = 0; o < kVRun; ++o) {
+        const int gy = it.ty * kTH + r0 + o;
+        if (gx >= W || gy >= H) continue;
+        const int64_t po = ((int64_t)gy * W + gx) * 3 + c;
+        const float xv = x[po], yv = y[po];
+        float d = a_ssim * (m[o][0] + 2.0f * xv * m[o][1] + yv * m[o][2]);
         if (a_l1 != 0.0f) {
             // torch's abs backward: sign, with 0 at x == y.
             const float sg = xv > yv ? 1.0f : (xv < yv ? -1.0f : 0.0f);
             d += a_l1 * sg;
         }
-        dx[o] = scale * d;
+        dx[po] = scale * d;
     }
 }
 
