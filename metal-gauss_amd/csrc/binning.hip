@@ -1234,6 +1234,7 @@ static int32_t tile_count_sort(const uint32_t *tiles, const V *ids, int64_t n, i
 // LDS mask per digit: each ORs in its lane bit, then reads the mask back.
 constexpr int kTdThreads = 256, kTdWaves = kTdThreads / 64, kTdPer = 16;
 constexpr int kTdCap = kTdThreads * kTdPer;
+constexpr int kTdBatch = 8;   // long lists: entries per thread per batch of loads
 
 struct TdArgs {
     const int32_t *offsets;
@@ -1372,15 +1373,16 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
         for (int r = 0; r < kTdPer; ++r) {
             const int i = pb + 64 * r;
             const bool ok = r < rounds && i < len && 64 * r < part;
-            uint2 q = make_uint2(0u, 0u);
-            if (ok) q = in[i];
-            v[r] = (int32_t)q.x;
-            k[r] = q.y;
-            if (ok) {
-                valid |= 1u << r;
-                kmin = min(kmin, k[r]);
-                kmax = max(kmax, k[r]);
-            }
+            // Every round's load is issued before any is used: unconditional
+            // (a clamped index), and everything after it branch-free. A load
+            // whose value is used only under `if (ok)` is sunk into that
+            // branch, which then waits for it before the next round's.
+            const uint2 qa = in[min(i, (int)len - 1)];
+            v[r] = ok ? (int32_t)qa.x : 0;
+            k[r] = ok ? qa.y : 0u;
+            valid |= ok ? 1u << r : 0u;
+            kmin = min(kmin, ok ? qa.y : 0xFFFFFFFFu);
+            kmax = max(kmax, k[r]);
         }
         td_minmax(kmin, kmax, S.red);
         const uint32_t span = kmax - kmin;
@@ -1422,11 +1424,20 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
 
     // Longer lists: key range, then passes over chunks of kTdCap in order,
     // ping-ponging between the input pairs and pairs_b.
+    // The list is read kTdBatch entries per thread at a time, the loads
+    // unconditional (clamped index) so that a batch is in flight at once.
     uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
-    for (int64_t i = tid; i < len; i += kTdThreads) {
-        const uint32_t kk = in[i].y;
-        kmin = min(kmin, kk);
-        kmax = max(kmax, kk);
+    for (int64_t b = 0; b < len; b += (int64_t)kTdThreads * kTdBatch) {
+        uint32_t kk[kTdBatch];
+#pragma unroll
+        for (int j = 0; j < kTdBatch; ++j)
+            kk[j] = in[min(b + tid + (int64_t)kTdThreads * j, len - 1)].y;
+#pragma unroll
+        for (int j = 0; j < kTdBatch; ++j) {
+            const bool ok = b + tid + (int64_t)kTdThreads * j < len;
+            kmin = min(kmin, ok ? kk[j] : 0xFFFFFFFFu);
+            kmax = max(kmax, ok ? kk[j] : 0u);
+        }
     }
     td_minmax(kmin, kmax, S.red);
     const uint32_t span = kmax - kmin;
@@ -1436,8 +1447,17 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
         // Digit totals over the list -> the running digit starts S.run.
         S.tot[tid] = 0;
         __syncthreads();
-        for (int64_t i = tid; i < len; i += kTdThreads)
-            atomicAdd(&S.tot[((pin[i].y - kmin) >> shift) & 255u], 1u);
+        for (int64_t b = 0; b < len; b += (int64_t)kTdThreads * kTdBatch) {
+            uint32_t kk[kTdBatch];
+#pragma unroll
+            for (int j = 0; j < kTdBatch; ++j)
+                kk[j] = pin[min(b + tid + (int64_t)kTdThreads * j, len - 1)].y;
+#pragma unroll
+            for (int j = 0; j < kTdBatch; ++j) {
+                const bool ok = b + tid + (int64_t)kTdThreads * j < len;
+                atomicAdd(&S.tot[((kk[j] - kmin) >> shift) & 255u], ok ? 1u : 0u);
+            }
+        }
         __syncthreads();
         {
             const uint32_t cnt = S.tot[tid];
@@ -1494,7 +1514,16 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
         pin = pout;
         pout = tp;
     }
-    for (int64_t i = tid; i < len; i += kTdThreads) A.ids[s0 + i] = (int32_t)pin[i].x;
+    // Past the end a lane rewrites the last entry with its own value.
+    for (int64_t b = 0; b < len; b += (int64_t)kTdThreads * kTdBatch) {
+        uint32_t id[kTdBatch];
+#pragma unroll
+        for (int j = 0; j < kTdBatch; ++j)
+            id[j] = pin[min(b + tid + (int64_t)kTdThreads * j, len - 1)].x;
+#pragma unroll
+        for (int j = 0; j < kTdBatch; ++j)
+            A.ids[s0 + min(b + tid + (int64_t)kTdThreads * j, len - 1)] = (int32_t)id[j];
+    }
 }
 
 // {id, depth bits} pairs from ids and the depth array (the radix route, for
