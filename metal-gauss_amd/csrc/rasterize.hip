@@ -552,16 +552,26 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
     const int start = tile_start + chunk * kChunk;   // this workgroup's entries
     const int cend = P.ckpt ? min(start + kChunk, tile_end) : tile_end;
     const int64_t o = inimg ? (int64_t)py * A.W + px : 0;
-    const int my_stop = inimg ? min(G.stop[o], cend) : start;
-    const float gr = inimg ? G.grad_rgb[3 * o] : 0.f;
-    const float gg = inimg ? G.grad_rgb[3 * o + 1] : 0.f;
-    const float gb = inimg ? G.grad_rgb[3 * o + 2] : 0.f;
-    float ga = inimg && G.grad_alpha ? G.grad_alpha[o] : 0.f;
+    // The pixel's inputs are loaded unconditionally (o is 0 outside the
+    // image; an absent optional input reads final_T instead) and selected
+    // after: a load in a conditional arm becomes a branch that waits for it
+    // before the next load is issued.
+    const int stop_o = G.stop[o];
+    const float gr_o = G.grad_rgb[3 * o], gg_o = G.grad_rgb[3 * o + 1];
+    const float gb_o = G.grad_rgb[3 * o + 2];
+    const float ga_o = (G.grad_alpha ? G.grad_alpha : G.final_T)[o];
+    const float alpha_o = (A.has_bg ? G.alpha : G.final_T)[o];
+    const float T_o = G.final_T[o];
+    const int my_stop = inimg ? min(stop_o, cend) : start;
+    const float gr = inimg ? gr_o : 0.f;
+    const float gg = inimg ? gg_o : 0.f;
+    const float gb = inimg ? gb_o : 0.f;
+    float ga = inimg && G.grad_alpha ? ga_o : 0.f;
     // The background blend's share: d rgb_out / d alpha = -bg where
     // 1 - alpha >= 0 (torch's clamp_min passes the gradient at the bound).
-    if (A.has_bg && inimg && 1.0f - G.alpha[o] >= 0.0f)
+    if (A.has_bg && inimg && 1.0f - alpha_o >= 0.0f)
         ga -= gr * A.bg[0] + gg * A.bg[1] + gb * A.bg[2];
-    float T = inimg ? G.final_T[o] : 1.0f;
+    float T = inimg ? T_o : 1.0f;
     // Gs = gr sr + gg sg + gb sb + ga sa over the colour (sr, sg, sb) and
     // coverage sa composited behind the current entry. With a chunk plan the
     // walk starts at the chunk's end: colour behind = final - prefix there,
