@@ -1244,10 +1244,16 @@ struct TdArgs {
 };
 
 struct TdShared {
-    uint32_t key[kTdCap];
-    int32_t id[kTdCap];
+    // The exchange buffer and the per-digit lane masks are never live at
+    // once, so they share storage (38 KB in all: four workgroups per CU).
+    union {
+        struct {
+            uint32_t key[kTdCap];
+            int32_t id[kTdCap];
+        } x;
+        unsigned long long mask[kTdWaves][256];   // per wave: lanes of a round per digit
+    } u;
     uint32_t wh[kTdWaves][256];               // per wave: digit counts, then slots
-    unsigned long long mask[kTdWaves][256];   // per wave: lanes of a round per digit
     uint32_t run[256], tot[256];
     uint32_t red[2 * kTdWaves];
 };
@@ -1361,7 +1367,7 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
         return;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) S.mask[wave][lane + 64 * j] = 0ull;
+    for (int j = 0; j < 4; ++j) S.u.mask[wave][lane + 64 * j] = 0ull;
 
     if (len <= kTdCap) {
         const int part = td_part((int)len), rounds = part / 64;
@@ -1388,12 +1394,19 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
         const uint32_t span = kmax - kmin;
         const int bits = span == 0u ? 0 : 32 - __builtin_clz(span);
         for (int shift = 0; shift < bits; shift += 8) {
+            if (shift > 0) {
+                // The exchange has overwritten the masks: clear them once
+                // every thread has read its entries back.
+                __syncthreads();
+#pragma unroll
+                for (int j = 0; j < 4; ++j) S.u.mask[wave][lane + 64 * j] = 0ull;
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) S.wh[wave][lane + 64 * j] = 0;
             __syncthreads();
 #pragma unroll
             for (int r = 0; r < kTdPer; ++r) d[r] = ((k[r] - kmin) >> shift) & 255u;
-            td_rank(d, valid, rounds, rank, S.wh[wave], S.mask[wave]);
+            td_rank(d, valid, rounds, rank, S.wh[wave], S.u.mask[wave]);
             __syncthreads();
             td_slots(S, nullptr, nullptr);
             __syncthreads();
@@ -1401,8 +1414,8 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
             for (int r = 0; r < kTdPer; ++r) {
                 if ((valid >> r) & 1u) {
                     const uint32_t pos = S.wh[wave][d[r]] + rank[r];
-                    S.key[pos] = k[r];
-                    S.id[pos] = v[r];
+                    S.u.x.key[pos] = k[r];
+                    S.u.x.id[pos] = v[r];
                 }
             }
             __syncthreads();
@@ -1410,8 +1423,8 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
             for (int r = 0; r < kTdPer; ++r) {
                 if ((valid >> r) & 1u) {
                     const int i = pb + 64 * r;
-                    k[r] = S.key[i];
-                    v[r] = S.id[i];
+                    k[r] = S.u.x.key[i];
+                    v[r] = S.u.x.id[i];
                 }
             }
             // The next pass rewrites wh and red only after its barrier.
@@ -1493,7 +1506,7 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
 #pragma unroll
             for (int j = 0; j < 4; ++j) S.wh[wave][lane + 64 * j] = 0;
             __syncthreads();
-            td_rank(d, valid, rounds, rank, S.wh[wave], S.mask[wave]);
+            td_rank(d, valid, rounds, rank, S.wh[wave], S.u.mask[wave]);
             __syncthreads();
             td_slots(S, S.tot, S.run);
             __syncthreads();
