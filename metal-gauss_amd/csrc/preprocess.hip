@@ -741,6 +741,21 @@ __device__ __forceinline__ void epi_rows(const AdamEpi &E, int64_t g, const floa
 // put there itself); moments are read and written at those positions of their
 // tensors. A float4 that runs past the round's ng Gaussians is handled per
 // element.
+//
+// A lane's tensor (t = 4, the SH or its DC rows, or 5, the rest rows) varies
+// across the wave, so its pointers and step constants are selected from the
+// two constant-index entries (held in scalar registers) rather than indexed
+// by t: an index into the argument's tables is a vector load of the pointer,
+// and every moment access waited for one.
+struct EpiRow {
+    float *p, *m, *v;
+    float step_size, inv_sqrt_bc2;
+};
+__device__ __forceinline__ EpiRow epi_row(const AdamEpi &E, bool dc) {
+    return {dc ? E.p[4] : E.p[5], dc ? E.m[4] : E.m[5], dc ? E.v[4] : E.v[5],
+            dc ? E.step_size[4] : E.step_size[5], dc ? E.inv_sqrt_bc2[4] : E.inv_sqrt_bc2[5]};
+}
+
 __device__ __forceinline__ void stage_adam(const float4 *sb, const float4 *cb,
                                            const AdamEpi &E, int fused, int64_t G0, int ng) {
     const int lane = threadIdx.x & 63;
@@ -748,18 +763,18 @@ __device__ __forceinline__ void stage_adam(const float4 *sb, const float4 *cb,
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int f = 4 * (lane + 64 * i);
-        const int t = fused || f < 48 ? 4 : 5;
+        const EpiRow R = epi_row(E, fused || f < 48);
         const int64_t off = fused ? G0 * 48 + f : (f < 48 ? G0 * 3 + f : G0 * 45 + (f - 48));
         if (stage_row(fused, f + 3) < ng) {
-            m4[i] = ld_nt4<kShNtMom>(E.m[t] + off);
-            v4[i] = ld_nt4<kShNtMom>(E.v[t] + off);
+            m4[i] = ld_nt4<kShNtMom>(R.m + off);
+            v4[i] = ld_nt4<kShNtMom>(R.v + off);
         } else {
             float e[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 if (stage_row(fused, f + k) < ng) {
-                    e[k] = ld_nt<kShNtMom>(E.m[t] + off + k);
-                    e[4 + k] = ld_nt<kShNtMom>(E.v[t] + off + k);
+                    e[k] = ld_nt<kShNtMom>(R.m + off + k);
+                    e[4 + k] = ld_nt<kShNtMom>(R.v + off + k);
                 }
             }
             m4[i] = make_float4(e[0], e[1], e[2], e[3]);
@@ -769,7 +784,7 @@ __device__ __forceinline__ void stage_adam(const float4 *sb, const float4 *cb,
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int f = 4 * (lane + 64 * i);
-        const int t = fused || f < 48 ? 4 : 5;
+        const EpiRow R = epi_row(E, fused || f < 48);
         const int64_t off = fused ? G0 * 48 + f : (f < 48 ? G0 * 3 + f : G0 * 45 + (f - 48));
         const float4 g4 = sb[lane + 64 * i];
         float gs[4] = {g4.x, g4.y, g4.z, g4.w};
@@ -780,18 +795,18 @@ __device__ __forceinline__ void stage_adam(const float4 *sb, const float4 *cb,
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             adam_update(po[k], gs[k], ms[k], vs[k], E.b1, E.b2, E.omb1, E.omb2, E.eps,
-                        E.step_size[t], E.inv_sqrt_bc2[t], false);
+                        R.step_size, R.inv_sqrt_bc2, false);
         if (stage_row(fused, f + 3) < ng) {
-            st_nt4<kNtPar>(E.p[t] + off, make_float4(po[0], po[1], po[2], po[3]));
-            st_nt4<kShNtMom>(E.m[t] + off, make_float4(ms[0], ms[1], ms[2], ms[3]));
-            st_nt4<kShNtMom>(E.v[t] + off, make_float4(vs[0], vs[1], vs[2], vs[3]));
+            st_nt4<kNtPar>(R.p + off, make_float4(po[0], po[1], po[2], po[3]));
+            st_nt4<kShNtMom>(R.m + off, make_float4(ms[0], ms[1], ms[2], ms[3]));
+            st_nt4<kShNtMom>(R.v + off, make_float4(vs[0], vs[1], vs[2], vs[3]));
         } else {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 if (stage_row(fused, f + k) < ng) {
-                    st_nt<kNtPar>(E.p[t] + off + k, po[k]);
-                    st_nt<kShNtMom>(E.m[t] + off + k, ms[k]);
-                    st_nt<kShNtMom>(E.v[t] + off + k, vs[k]);
+                    st_nt<kNtPar>(R.p + off + k, po[k]);
+                    st_nt<kShNtMom>(R.m + off + k, ms[k]);
+                    st_nt<kShNtMom>(R.v + off + k, vs[k]);
                 }
             }
         }
