@@ -1541,15 +1541,27 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
 
 // {id, depth bits} pairs from ids and the depth array (the radix route, for
 // more tiles than the counting sort takes).
-// (With status, only the kept pairs of capacity-bounded lists.)
+// (With status, only the kept pairs of capacity-bounded lists.) A thread
+// takes kGatherPer pairs a workgroup-width apart: their ids, then their
+// depths, are requested together (unconditional loads at a clamped index),
+// rather than one id and one dependent depth read at a time.
+constexpr int kGatherPer = 4;
 __global__ __launch_bounds__(256) void gather_depth_pairs_kernel(const int32_t *ids,
                                                                  const float *depth, int64_t n,
                                                                  uint2 *pairs,
                                                                  const int64_t *status) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (status ? lists_kept(status) : n)) return;
-    const int32_t g = ids[i];
-    pairs[i] = make_uint2((uint32_t)g, __float_as_uint(depth[g]));
+    const int64_t m = status ? lists_kept(status) : n;
+    const int64_t b = (int64_t)blockIdx.x * (256 * kGatherPer) + threadIdx.x;
+    if (b >= m) return;
+    int32_t g[kGatherPer];
+    float d[kGatherPer];
+#pragma unroll
+    for (int j = 0; j < kGatherPer; ++j) g[j] = ids[min(b + 256 * j, m - 1)];
+#pragma unroll
+    for (int j = 0; j < kGatherPer; ++j) d[j] = depth[g[j]];
+#pragma unroll
+    for (int j = 0; j < kGatherPer; ++j)
+        if (b + 256 * j < m) pairs[b + 256 * j] = make_uint2((uint32_t)g[j], __float_as_uint(d[j]));
 }
 
 // Capacity-bounded lists on the radix route: the slots past the kept pairs
@@ -1681,8 +1693,8 @@ static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
                 res_tiles, n, n_tiles, tile_offsets);
             MG_LAUNCHED("tile_ranges_u32_kernel");
         }
-        gather_depth_pairs_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, s>>>(gauss_ids, depth, n,
-                                                                           pairs_b, status);
+        gather_depth_pairs_kernel<<<(unsigned)ceil_div(n, 256 * kGatherPer), 256, 0, s>>>(
+            gauss_ids, depth, n, pairs_b, status);
         MG_LAUNCHED("gather_depth_pairs_kernel");
     }
     TdArgs D{tile_offsets, pairs_b, pairs_a, gauss_ids};
