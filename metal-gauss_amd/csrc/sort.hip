@@ -79,10 +79,17 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const K *ke
     __syncthreads();
     constexpr int kSortTile = kSortThreads * kSortItems;
     const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    // Every key is requested before any is counted: loads at a clamped index
+    // (n >= 1), and a count of 0 past n, so no load sits in a branch that
+    // waits for it before the next.
+    K kv[kSortItems];
+#pragma unroll
+    for (int r = 0; r < kSortItems; ++r)
+        kv[r] = keys[min(base + (int64_t)r * kSortThreads + threadIdx.x, n - 1)];
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
         const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
-        if (i < n) atomicAdd(&s_h[wave][digit_of(keys[i], shift, mask, win)], 1u);
+        atomicAdd(&s_h[wave][digit_of(kv[r], shift, mask, win)], i < n ? 1u : 0u);
     }
     __syncthreads();
     for (int d = threadIdx.x; d < kRadix; d += kSortThreads) {
