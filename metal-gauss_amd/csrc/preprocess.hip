@@ -839,15 +839,26 @@ struct PreBwdArgs {
     AdamEpi E;     // the optimizer epilogue (EPI kernels)
 };
 
+// Gaussians per wave of the epilogue kernel: two SH rounds. At 3 waves per
+// SIMD the GPU holds 3072 of its waves; with 64 Gaussians each, config 4's
+// 15625 waves filled those slots 5.09 times, and the last, nearly empty
+// round of waves ran at a fraction of the bandwidth (per-wave timestamps:
+// 47 us per wave, 35 of them in the SH rounds at about 6.4 TB/s overall).
+// 32 per wave: 1.006 -> 0.994 ms per step (48: 0.996; 16: 1.014).
+constexpr int kEpiGaussians = 32;
+
 // EPI: the optimizer epilogue replaces the six gradient outputs (needs MIP,
-// STAGE and d_color).
+// STAGE and d_color). A wave takes kGpw consecutive Gaussians (a multiple of
+// the 16 of an SH round), one per lane; lanes past kGpw have none.
 template <bool MIP, bool STAGE, bool EPI>
 __device__ __forceinline__ void preprocess_bwd_body(const PreBwdArgs &A) {
     const Cam &C = A.C;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t g0 = (int64_t)blockIdx.x * kPreThreads + wave * 64;
+    constexpr int kGpw = EPI ? kEpiGaussians : 64;
+    static_assert(kGpw % 16 == 0 && kGpw <= 64, "whole SH rounds per wave");
+    const int64_t g0 = ((int64_t)blockIdx.x * (kPreThreads / 64) + wave) * kGpw;
     const int64_t g = g0 + lane;
-    const bool in = g < A.N;
+    const bool in = lane < kGpw && g < A.N;
 
     float mx = 0.f, my = 0.f, mz = 0.f;
     int vld = 0;
@@ -888,7 +899,7 @@ __device__ __forceinline__ void preprocess_bwd_body(const PreBwdArgs &A) {
         // The colour of a Gaussian that is not visible is the constant 0, so
         // its coefficients get no gradient.
         const bool need = vld != 0 && (dcol[0] != 0.f || dcol[1] != 0.f || dcol[2] != 0.f);
-        const int ng = (int)max((int64_t)0, min((int64_t)64, A.N - g0));
+        const int ng = (int)max((int64_t)0, min((int64_t)kGpw, A.N - g0));
         if (!EPI && ballot(need) == 0) {
             // Coalesced zero fill of the wave's rows.
             if (A.fused) {
@@ -953,7 +964,7 @@ __device__ __forceinline__ void preprocess_bwd_body(const PreBwdArgs &A) {
                 float4 *sb = s_st[wave];
                 float *sf = reinterpret_cast<float *>(sb);
                 const uint64_t nm = ballot(need);
-                const int nw = (int)max((int64_t)0, min((int64_t)64, A.N - g0));
+                const int nw = (int)max((int64_t)0, min((int64_t)kGpw, A.N - g0));
                 // With the epilogue every row's parameters are read (all are
                 // updated) and a second slice keeps the round's own for it.
                 __shared__ float4 s_cur[EPI ? kPreThreads / 64 : 1][EPI ? kStageF4 : 1];
@@ -964,6 +975,7 @@ __device__ __forceinline__ void preprocess_bwd_body(const PreBwdArgs &A) {
 #pragma unroll 1
                 for (int r = 0; r < 4; ++r) {
                     const int ngr = min(16, max(0, nw - 16 * r));
+                    if (ngr == 0) break;   // wave-uniform: no Gaussian left
                     stage_put(sb, pf);
                     if (EPI) stage_put(cb, pf);
                     wave_lds_sync();
@@ -1246,7 +1258,8 @@ void preprocess_bwd_kernel(const PreBwdArgs A) {
     preprocess_bwd_body<MIP, STAGE, false>(A);
 }
 
-// The backward with the optimizer epilogue: 168 VGPRs, 3 waves/SIMD.
+// The backward with the optimizer epilogue: 166 VGPRs, 3 waves/SIMD, a wave
+// per kEpiGaussians Gaussians.
 __global__ __launch_bounds__(kPreThreads) __attribute__((amdgpu_waves_per_eu(3)))
 void preprocess_bwd_adam_kernel(const PreBwdArgs A) {
     if (A.E.skip && A.E.skip[1] != 0) return;
@@ -1407,7 +1420,8 @@ static int32_t preprocess_bwd(int64_t N, const float *means, const float *quats,
     hipStream_t st = as_stream(stream);
     if (adam) {
         TimedScope ts("preprocess_backward_adam", st);
-        preprocess_bwd_adam_kernel<<<(unsigned)blocks, kPreThreads, 0, st>>>(A);
+        preprocess_bwd_adam_kernel<<<(unsigned)ceil_div(N, (kPreThreads / 64) * kEpiGaussians),
+                                     kPreThreads, 0, st>>>(A);
         MG_LAUNCHED("preprocess_bwd_adam_kernel");
         return MG_OK;
     }
