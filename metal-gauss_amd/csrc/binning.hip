@@ -1222,19 +1222,28 @@ static int32_t tile_count_sort(const uint32_t *tiles, const V *ids, int64_t n, i
 // order as their bits), on only the bits in which the list's keys differ:
 // LSD passes of 8 bits. The list arrives in ascending id, so ties keep id
 // order. The ids are written to gauss_ids.
-//   * Up to kTdCap entries: the list lives in registers, each wave holding
-//     one contiguous quarter (rounded up to 64 entries); each pass ranks
-//     every wave's quarter against a wave-private LDS histogram, joins the
-//     waves through a digit scan, and exchanges the entries through LDS into
-//     their new order.
-//   * Longer lists: the same pass over chunks of kTdCap, in order, with the
-//     digit starts carried from chunk to chunk, ping-ponging between the
-//     input pairs and scratch of the list's own range.
+//   * Up to kTdCap entries whose keys differ in at most kTdKeyBits + 8 bits:
+//     the keys live in registers, each wave holding one contiguous quarter
+//     (rounded up to 64 entries); each pass ranks every wave's quarter
+//     against a wave-private LDS histogram, joins the waves through a digit
+//     scan, and exchanges the entries through LDS into their new order as
+//     one word, the entry's index in the list (12 bits) over the key bits
+//     still to sort (at most 20 after the first pass). After the last pass
+//     the exchanged indices give each sorted position its entry, whose id is
+//     read from the list (L2-resident) and stored coalesced. With one word
+//     instead of a (key, id) pair the exchange buffer is 16 KB.
+//   * Longer lists, or keys spanning more bits: the same pass over chunks of
+//     kTdCap, in order, with the digit starts carried from chunk to chunk,
+//     ping-ponging between the input pairs and scratch of the list's own
+//     range.
 // Lanes of a round holding the same digit find each other through a 64-bit
 // LDS mask per digit: each ORs in its lane bit, then reads the mask back.
 constexpr int kTdThreads = 256, kTdWaves = kTdThreads / 64, kTdPer = 16;
 constexpr int kTdCap = kTdThreads * kTdPer;
 constexpr int kTdBatch = 8;   // long lists: entries per thread per batch of loads
+constexpr int kTdKeyBits = 20;   // key bits exchanged beside a 12-bit list index
+constexpr uint32_t kTdKeyMask = (1u << kTdKeyBits) - 1u;
+static_assert(kTdCap <= (1 << (32 - kTdKeyBits)), "a list index fits beside the key bits");
 
 struct TdArgs {
     const int32_t *offsets;
@@ -1245,18 +1254,24 @@ struct TdArgs {
 
 struct TdShared {
     // The exchange buffer and the per-digit lane masks are never live at
-    // once, so they share storage (38 KB in all: four workgroups per CU).
+    // once, so they share storage (22 KB in all; 110 VGPRs hold the
+    // workgroup to four per CU).
     union {
-        struct {
-            uint32_t key[kTdCap];
-            int32_t id[kTdCap];
-        } x;
+        uint32_t xk[kTdCap];   // exchange: list index << kTdKeyBits | key bits left
         unsigned long long mask[kTdWaves][256];   // per wave: lanes of a round per digit
     } u;
     uint32_t wh[kTdWaves][256];               // per wave: digit counts, then slots
     uint32_t run[256], tot[256];
     uint32_t red[2 * kTdWaves];
 };
+
+// Waits until this wave's outstanding LDS reads have returned. Needed before
+// a barrier after which other waves overwrite what this wave has read: the
+// barrier's own fence waits for LDS writes, not for reads whose values are
+// first used after it.
+__device__ __forceinline__ void lds_reads_done() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
 
 // Workgroup min and max of the keys.
 __device__ __forceinline__ void td_minmax(uint32_t &kmin, uint32_t &kmax, uint32_t *red) {
@@ -1372,67 +1387,87 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
     if (len <= kTdCap) {
         const int part = td_part((int)len), rounds = part / 64;
         const int pb = wave * part + lane;   // entry of round r: pb + 64 r
-        uint32_t k[kTdPer], d[kTdPer], rank[kTdPer];
-        int32_t v[kTdPer];
+        const uint32_t *in_key = reinterpret_cast<const uint32_t *>(in) + 1;
+        uint32_t k[kTdPer], rank[kTdPer];
         uint32_t valid = 0, kmin = 0xFFFFFFFFu, kmax = 0u;
 #pragma unroll
         for (int r = 0; r < kTdPer; ++r) {
             const int i = pb + 64 * r;
             const bool ok = r < rounds && i < len && 64 * r < part;
-            // Every round's load is issued before any is used: unconditional
-            // (a clamped index), and everything after it branch-free. A load
-            // whose value is used only under `if (ok)` is sunk into that
-            // branch, which then waits for it before the next round's.
-            const uint2 qa = in[min(i, (int)len - 1)];
-            v[r] = ok ? (int32_t)qa.x : 0;
-            k[r] = ok ? qa.y : 0u;
+            const uint32_t ka = in_key[2 * min(i, (int)len - 1)];
+            k[r] = ok ? ka : 0u;
             valid |= ok ? 1u << r : 0u;
-            kmin = min(kmin, ok ? qa.y : 0xFFFFFFFFu);
+            kmin = min(kmin, ok ? ka : 0xFFFFFFFFu);
             kmax = max(kmax, k[r]);
         }
         td_minmax(kmin, kmax, S.red);
         const uint32_t span = kmax - kmin;
         const int bits = span == 0u ? 0 : 32 - __builtin_clz(span);
-        for (int shift = 0; shift < bits; shift += 8) {
-            if (shift > 0) {
-                // The exchange has overwritten the masks: clear them once
-                // every thread has read its entries back.
+        if (bits <= kTdKeyBits + 8) {   // workgroup-uniform
+            // First pass: k is the key less kmin; later passes: k is the
+            // exchanged word, the entry's list index over its key bits left.
+#pragma unroll
+            for (int r = 0; r < kTdPer; ++r) k[r] = ((valid >> r) & 1u) ? k[r] - kmin : 0u;
+            for (int shift = 0; shift < bits; shift += 8) {
+                if (shift > 0) {
+                    // The masks share storage with the words every wave has
+                    // just read back; those reads must have returned before
+                    // any wave clears them. A barrier alone does not wait for
+                    // LDS reads whose values are first used after it, and
+                    // another wave's writes may then overtake them.
+                    lds_reads_done();
+                    __syncthreads();
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) S.u.mask[wave][lane + 64 * j] = 0ull;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) S.wh[wave][lane + 64 * j] = 0;
                 __syncthreads();
+                uint32_t d[kTdPer];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) S.u.mask[wave][lane + 64 * j] = 0ull;
-            }
+                for (int r = 0; r < kTdPer; ++r) d[r] = k[r] & 255u;
+                td_rank(d, valid, rounds, rank, S.wh[wave], S.u.mask[wave]);
+                __syncthreads();
+                td_slots(S, nullptr, nullptr);
+                __syncthreads();
+                const bool last = shift + 8 >= bits;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) S.wh[wave][lane + 64 * j] = 0;
-            __syncthreads();
-#pragma unroll
-            for (int r = 0; r < kTdPer; ++r) d[r] = ((k[r] - kmin) >> shift) & 255u;
-            td_rank(d, valid, rounds, rank, S.wh[wave], S.u.mask[wave]);
-            __syncthreads();
-            td_slots(S, nullptr, nullptr);
-            __syncthreads();
-#pragma unroll
-            for (int r = 0; r < kTdPer; ++r) {
-                if ((valid >> r) & 1u) {
-                    const uint32_t pos = S.wh[wave][d[r]] + rank[r];
-                    S.u.x.key[pos] = k[r];
-                    S.u.x.id[pos] = v[r];
+                for (int r = 0; r < kTdPer; ++r) {
+                    if ((valid >> r) & 1u) {
+                        const uint32_t pos = S.wh[wave][d[r]] + rank[r];
+                        const uint32_t idx = shift == 0 ? (uint32_t)(pb + 64 * r)
+                                                        : k[r] >> kTdKeyBits;
+                        const uint32_t rest = (shift == 0 ? k[r] : k[r] & kTdKeyMask) >> 8;
+                        // After the last pass only the index is needed.
+                        S.u.xk[pos] = last ? idx : (idx << kTdKeyBits) | rest;
+                    }
                 }
-            }
-            __syncthreads();
+                __syncthreads();
+                if (last) break;
 #pragma unroll
-            for (int r = 0; r < kTdPer; ++r) {
-                if ((valid >> r) & 1u) {
-                    const int i = pb + 64 * r;
-                    k[r] = S.u.x.key[i];
-                    v[r] = S.u.x.id[i];
-                }
+                for (int r = 0; r < kTdPer; ++r)
+                    if ((valid >> r) & 1u) k[r] = S.u.xk[pb + 64 * r];
             }
-            // The next pass rewrites wh and red only after its barrier.
+            if (bits == 0) {   // one key: the list order stands
+                __syncthreads();
+                for (int i = tid; i < len; i += kTdThreads) S.u.xk[i] = (uint32_t)i;
+                __syncthreads();
+            }
+            // S.u.xk[i]: the list index of the entry at sorted position i.
+            // Past len a lane rewrites the last position with its own value.
+            uint32_t ix[kTdPer];
+            int32_t id[kTdPer];
+#pragma unroll
+            for (int j = 0; j < kTdPer; ++j) ix[j] = S.u.xk[min(tid + kTdThreads * j, (int)len - 1)];
+#pragma unroll
+            for (int j = 0; j < kTdPer; ++j) id[j] = (int32_t)in[ix[j]].x;
+#pragma unroll
+            for (int j = 0; j < kTdPer; ++j)
+                A.ids[s0 + min(tid + kTdThreads * j, (int)len - 1)] = id[j];
+            return;
         }
-#pragma unroll
-        for (int r = 0; r < kTdPer; ++r)
-            if ((valid >> r) & 1u) A.ids[s0 + pb + 64 * r] = v[r];
-        return;
+        // Keys spanning more bits take the chunked passes below.
+        __syncthreads();
     }
 
     // Longer lists: key range, then passes over chunks of kTdCap in order,
