@@ -103,11 +103,10 @@ def test_large_rectangles_bit_exact(dev, tile, ellipse):
 
 @pytest.mark.parametrize("spread", [0.0, 2e-6, 2e-3, 0.5, 3.0])
 def test_depth_windows_of_every_pass_count_bit_exact(dev, spread):
-    """The depth sort takes 12-bit passes over only the bits in which the
-    tiled Gaussians' depth keys differ, and leaves the order in one of two
-    buffers by the parity of those passes: all depths equal (no pass), a few
-    bits (one), about 20 bits (two), and a wide range (three). The lists must
-    equal the oracle's every time."""
+    """The per-tile depth sort takes 8-bit passes over only the bits in which
+    a tile's depth keys differ: all depths equal (no pass), a few bits (one),
+    about 20 bits (three), and a wide range. The lists must equal the
+    oracle's every time."""
     s = ref_scene(N=4000, seed=21)
     g = torch.Generator().manual_seed(22)
     s["means"][:, 2] = 3.0 + spread * torch.randn(4000, generator=g).clamp(-0.9, 0.9)
@@ -136,6 +135,37 @@ def test_depth_ties_and_long_tile_lists_bit_exact(dev, crowd):
     gpu, ref = run_both(s, dev, 16)
     if crowd:
         assert int(np.diff(gpu[1]).max()) > 4096, int(np.diff(gpu[1]).max())
+    assert np.array_equal(gpu[3], ref[3]), "sorted keys differ"
+    assert np.array_equal(gpu[0], ref[0]), "gauss_ids differ"
+    assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
+
+
+def test_lists_over_2048_entries_with_four_passes_bit_exact(dev):
+    """Every tile's list between 2048 and 4096 entries (one workgroup, its
+    four waves' quarters past the 2048 LDS words the lane masks share with the
+    exchange buffer) and depth keys spanning about 27 bits (four 8-bit
+    passes): 400k small splats placed by pixel over a 256x256 image, depths
+    log-uniform in [0.05, 40]. A pass that cleared the masks before every
+    wave's read of the shared words had returned gave these lists index 0 in
+    their first 2048 positions."""
+    N, W, H, f = 400_000, 256, 256, 200.0
+    g = torch.Generator().manual_seed(41)
+    u = torch.rand(N, generator=g) * W
+    v = torch.rand(N, generator=g) * H
+    z = torch.exp(torch.rand(N, generator=g) * (math.log(40.0) - math.log(0.05))
+                  + math.log(0.05))
+    means = torch.stack([(u - W / 2) * z / f, (v - H / 2) * z / f, z], 1)
+    quats = torch.zeros(N, 4)
+    quats[:, 0] = 1.0
+    scales = (z * 1.3 / f)[:, None].expand(N, 3).contiguous()
+    s = dict(means=means, quats=quats, scales=scales, op=torch.full((N,), 0.6),
+             sh=torch.zeros(N, 16, 3), W=W, H=H, f=f)
+    gpu, ref = run_both(s, dev, 16)
+    lens = np.diff(gpu[1])
+    assert (lens > 2048).mean() > 0.9 and lens.max() <= 4096, (lens.min(), lens.max())
+    span_bits = [int(int(k[-1] & 0xFFFFFFFF) - int(k[0] & 0xFFFFFFFF)).bit_length()
+                 for k in np.split(gpu[3], gpu[1][1:-1]) if k.size > 1]
+    assert min(span_bits) > 24, min(span_bits)
     assert np.array_equal(gpu[3], ref[3]), "sorted keys differ"
     assert np.array_equal(gpu[0], ref[0]), "gauss_ids differ"
     assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
