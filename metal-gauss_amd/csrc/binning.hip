@@ -1063,7 +1063,11 @@ template <int kPer, typename V>
 __global__ __launch_bounds__(kCsThreads) void count_scatter_kernel(const CsPass<V> P) {
     constexpr int64_t kChunk = (int64_t)kCsThreads * kPer, kPart = 64 * kPer;
     constexpr int kTPer = kCsBuckets / kCsThreads;   // tiles owned per thread
-    __shared__ uint32_t s_wh[kCsWaves][kCsBuckets];   // per wave: count, then next slot
+    // Per wave and tile: the count, then the next slot; sized by the launch
+    // to the tile count (kCsWaves * nb words), so that at config 4's 2500
+    // tiles four workgroups share a CU and every chunk's workgroup is
+    // resident at once (two with room for 4096 tiles).
+    extern __shared__ uint32_t s_wh[];
     __shared__ uint32_t s_part[kCsWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t n = cs_count(P);
@@ -1094,12 +1098,12 @@ __global__ __launch_bounds__(kCsThreads) void count_scatter_kernel(const CsPass<
     }
     for (int i = tid; i < nb; i += kCsThreads) {
 #pragma unroll
-        for (int w = 0; w < kCsWaves; ++w) s_wh[w][i] = 0;
+        for (int w = 0; w < kCsWaves; ++w) s_wh[w * nb + i] = 0;
     }
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < kPer; ++r)
-        if (t[r] < (uint32_t)nb) atomicAdd(&s_wh[wave][t[r]], 1u);
+        if (t[r] < (uint32_t)nb) atomicAdd(&s_wh[wave * nb + t[r]], 1u);
     __syncthreads();
     uint32_t sum = 0;
 #pragma unroll
@@ -1121,8 +1125,8 @@ __global__ __launch_bounds__(kCsThreads) void count_scatter_kernel(const CsPass<
             uint32_t slot = start + hv[j];
 #pragma unroll
             for (int w = 0; w < kCsWaves; ++w) {
-                const uint32_t cnt = s_wh[w][tt];
-                s_wh[w][tt] = slot;
+                const uint32_t cnt = s_wh[w * nb + tt];
+                s_wh[w * nb + tt] = slot;
                 slot += cnt;
             }
         }
@@ -1132,7 +1136,7 @@ __global__ __launch_bounds__(kCsThreads) void count_scatter_kernel(const CsPass<
     if (c == 0 && tid == kCsThreads - 1) P.offsets[nb] = (int32_t)start;
     __syncthreads();
     const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    uint32_t *wh = s_wh[wave];
+    uint32_t *wh = s_wh + wave * nb;
     // Lanes whose pair is in the same tile (kept pairs only): one ballot per
     // tile bit, kept where the bit agrees; x is -1 where this lane's bit is 0.
     auto peers_of = [&](uint32_t tt) {
@@ -1200,7 +1204,7 @@ static int32_t tile_count_sort(const uint32_t *tiles, const V *ids, int64_t n, i
         count_colscan_kernel<V><<<(unsigned)ceil_div(n_tiles, 64), 64 * kColWaves, 0, s>>>( \
             P, plan.nchunks);                                                          \
         MG_LAUNCHED("count_colscan_kernel");                                           \
-        count_scatter_kernel<PER, V><<<grid, kCsThreads, 0, s>>>(P);                   \
+        count_scatter_kernel<PER, V><<<grid, kCsThreads, 4 * kCsWaves * n_tiles, s>>>(P); \
         MG_LAUNCHED("count_scatter_kernel");                                           \
         break;
     switch (plan.per) {
