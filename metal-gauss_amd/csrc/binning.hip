@@ -1535,10 +1535,9 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
             for (int r = 0; r < kTdPer; ++r) {
                 const int i = pb + 64 * r;
                 const bool ok = r < rounds && i < cl && 64 * r < part;
-                uint2 q = make_uint2(0u, 0u);
-                if (ok) q = pin[c0 + i];
-                v[r] = (int32_t)q.x;
-                k[r] = q.y;
+                const uint2 q = pin[c0 + min(i, cl - 1)];   // loads issued together
+                v[r] = ok ? (int32_t)q.x : 0;
+                k[r] = ok ? q.y : 0u;
                 valid |= ok ? 1u << r : 0u;
                 d[r] = ((k[r] - kmin) >> shift) & 255u;
             }
