@@ -376,8 +376,11 @@ __global__ __launch_bounds__(1024) void chunk_plan_kernel(const int32_t *offsets
     if (threadIdx.x == 0) P.base[n_tiles] = s_carry;
 }
 
+// Eight waves per SIMD (at most 64 VGPRs; 62 without spills): eight
+// workgroups share a CU (LDS allows nine), so config 4's 2500 tiles take
+// 1.22 rounds of workgroups instead of 1.63 at 73 VGPRs (step -2.5 us).
 template <int MAXW>
-__global__ __launch_bounds__(MAXW * 64) void raster_fwd_kernel(const RasterArgs A, float *out_rgb,
+__global__ __launch_bounds__(MAXW * 64) __attribute__((amdgpu_waves_per_eu(8))) void raster_fwd_kernel(const RasterArgs A, float *out_rgb,
                                                                float *out_alpha, float *out_T,
                                                                int32_t *out_stop,
                                                                const ChunkPlan P) {
