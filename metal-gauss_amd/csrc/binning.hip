@@ -51,11 +51,26 @@ struct __align__(16) BinRec {
 };
 
 // False when the Gaussian claims no tile (invalid, or alpha below 1/255 at
-// every point).
+// every point); r is then filled from zeroed inputs and not used. Every input
+// is requested before any is tested: a load whose value is needed only past
+// a branch is issued there and waited for, one memory round trip per branch.
 __device__ __forceinline__ bool make_rec(const BinArgs &A, int64_t g, BinRec &r) {
-    if (A.valid[g] == 0) return false;
-    const float ux = A.uv[2 * g], uy = A.uv[2 * g + 1];
-    const float rx = A.rxy[2 * g], ry = A.rxy[2 * g + 1];
+    const bool test = A.conic != nullptr;
+    const bool vld = A.valid[g] != 0;
+    float ux = A.uv[2 * g], uy = A.uv[2 * g + 1];
+    float rx = A.rxy[2 * g], ry = A.rxy[2 * g + 1];
+    float op = 0.0f, ca = 0.0f, cb = 0.0f, cc = 0.0f;
+    if (test) {
+        op = A.opac[g];
+        ca = A.conic[3 * g];
+        cb = A.conic[3 * g + 1];
+        cc = A.conic[3 * g + 2];
+    }
+    // Invalid Gaussians may carry non-finite extents.
+    ux = vld ? ux : 0.0f;
+    uy = vld ? uy : 0.0f;
+    rx = vld ? rx : 0.0f;
+    ry = vld ? ry : 0.0f;
     const float tf = (float)A.tile;
     int x0 = (int)floorf((ux - rx) / tf), x1 = (int)floorf((ux + rx) / tf);
     int y0 = (int)floorf((uy - ry) / tf), y1 = (int)floorf((uy + ry) / tf);
@@ -67,18 +82,14 @@ __device__ __forceinline__ bool make_rec(const BinArgs &A, int64_t g, BinRec &r)
     r.uy = uy;
     r.xs = (uint32_t)x0 | ((uint32_t)x1 << 16);
     r.ys = (uint32_t)y0 | ((uint32_t)y1 << 16);
-    r.a = r.b = r.c = r.thr = 0.0f;
     // Without a conic (the circular-bounds caller of metal_backend.py:111-147)
     // every tile of the rectangle is claimed.
-    if (A.conic != nullptr) {
-        bool live;
-        r.thr = level_threshold(A.opac[g], live);
-        if (!live) return false;
-        r.a = fmaxf(A.conic[3 * g], 1e-12f);
-        r.b = A.conic[3 * g + 1];
-        r.c = fmaxf(A.conic[3 * g + 2], 1e-12f);
-    }
-    return true;
+    bool live = true;
+    r.thr = test ? level_threshold(op, live) : 0.0f;
+    r.a = test ? fmaxf(ca, 1e-12f) : 0.0f;
+    r.b = test ? cb : 0.0f;
+    r.c = test ? fmaxf(cc, 1e-12f) : 0.0f;
+    return vld && live;
 }
 
 // Walks the rectangle, rows outer and columns inner (binning.metal:74-77),
@@ -175,88 +186,114 @@ __device__ __forceinline__ bool tile_claim(const BinRec &r, bool test, int tx, i
     return best < r.thr;
 }
 
-// Rectangles larger than this many tiles are walked by a whole wave (64
-// tiles a step) instead of one thread: near-camera Gaussians can cover
-// thousands of tiles, and one thread walking them holds up its workgroup.
+// Rectangles larger than this many tiles are walked by a whole wave instead
+// of one thread: near-camera Gaussians can cover thousands of tiles, and one
+// thread walking them holds up its workgroup.
 constexpr int kWaveWalkArea = 32;
 
-// A wave's walk of one large rectangle. The edge minimisers of every row
-// boundary (u, h + 1 of them) and column boundary (v, w + 1) are computed
-// once into the wave's LDS slice, with the walk's own expressions, and each
-// lane then tests its tiles from them; lanes step through the row-major tile
-// order without integer division. Rectangles whose boundaries do not fit the
-// slice test each tile from scratch (tile_claim).
-constexpr int kEdgeSlots = 256;
+// A wave's walk of one large rectangle, lanes on fixed columns. The
+// rectangle is cut into strips of s columns; a step covers R rows of a strip
+// (lane = row group * s + column), with R and s chosen per rectangle for the
+// fewest steps. A tile's four edge minima are then selects between values
+// that depend on a row boundary, a column boundary or one corner:
+//   * the top edge of row i, at x = clamp(u_i, X_j, X_j+1): the corner value
+//     at X_j (u_i below the tile), at X_j+1 (above), else M_i, the minimum on
+//     the row boundary line; likewise the bottom edge with boundary i + 1 and
+//     the left / right edges with the column boundaries' v_j, v_j+1, N_j, N_j+1;
+//   * a corner value (A_j + P_j ey_i) + C_i splits the walk's quadratic form
+//     a ex^2 + 2 b ex ey + c ey^2 (evaluated left to right, no contraction)
+//     into its column part A = a ex ex, P = 2 b ex and row part C = c ey ey.
+// Every value is the walk's own fp32 expression on the same operands (the
+// clamped coordinate equals the corner, or u / v itself), so each decision
+// is bit for bit the walk's. The row boundaries {u, Y, C, M} are computed
+// once per rectangle into the wave's LDS slice, the column boundaries once
+// per strip into registers. Rectangles taller than the slice test each tile
+// with tile_claim. The tiles are visited strip by strip, not in row-major
+// order: a Gaussian's pairs go to distinct tiles, so their order within its
+// run does not reach the sorted tile lists.
+constexpr int kRowSlots = 128;
+static_assert(kRowSlots * 16 == 64 * kWaveWalkArea, "the row slice aliases the small-claim bytes");
 
-struct WaveWalk {
-    const BinRec *r;
-    const float *u, *v;     // LDS: row / column boundary minimisers, or null
-    int x0, y0, w, h;
-    bool test;
-    int tile, W, H;
-
-    __device__ __forceinline__ bool claim(int row, int col) const {
+template <class Step>
+__device__ __forceinline__ void strip_walk(const BinRec &r, bool test, int tile, int W, int H,
+                                           float4 *rows, int lane, Step &&step) {
 #pragma clang fp contract(off)
-        if (!test) return true;
-        if (u == nullptr) return tile_claim(*r, true, x0 + col, y0 + row, tile, W, H);
-        const int tx = x0 + col, ty = y0 + row;
-        const float mux = r->ux, muy = r->uy, a = r->a, b = r->b, c = r->c;
-        const float ry0 = (float)(ty * tile), ry1 = fminf((float)((ty + 1) * tile), (float)H);
-        const float rx0 = (float)(tx * tile), rx1 = fminf((float)((tx + 1) * tile), (float)W);
-        if (muy >= ry0 && muy <= ry1 && mux >= rx0 && mux <= rx1) return true;
-        const float u0 = u[row], u1 = u[row + 1], v0 = v[col], v1 = v[col + 1];
-        const float ey0 = ry0 - muy, ey1 = ry1 - muy;
-        float ex = fminf(fmaxf(u0, rx0), rx1) - mux;
-        float best = a * ex * ex + 2.0f * b * ex * ey0 + c * ey0 * ey0;
-        ex = fminf(fmaxf(u1, rx0), rx1) - mux;
-        best = fminf(best, a * ex * ex + 2.0f * b * ex * ey1 + c * ey1 * ey1);
-        float ey = fminf(fmaxf(v0, ry0), ry1) - muy;
-        ex = rx0 - mux;
-        best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
-        ey = fminf(fmaxf(v1, ry0), ry1) - muy;
-        ex = rx1 - mux;
-        best = fminf(best, a * ex * ex + 2.0f * b * ex * ey + c * ey * ey);
-        return best < r->thr;
+    const int x0 = (int)(r.xs & 0xffffu), y0 = (int)(r.ys & 0xffffu);
+    const int w = (int)(r.xs >> 16) - x0 + 1, h = (int)(r.ys >> 16) - y0 + 1;
+    // Lane l prices R = l + 1 rows a step (strips of min(w, 64 / R)
+    // columns); the wave takes the fewest steps, the smallest R on ties.
+    uint64_t key;
+    {
+        const int R = lane + 1, s = min(w, 64 / R);
+        const uint64_t steps = (uint64_t)((w + s - 1) / s) * (uint64_t)((h + R - 1) / R);
+        key = steps << 6 | (uint64_t)lane;
+        for (int o = 32; o >= 1; o >>= 1) {
+            const uint64_t t = __shfl_xor(key, o, 64);
+            key = t < key ? t : key;
+        }
     }
-};
-
-// Fills the wave's edge slice for rectangle r (all 64 lanes call it) and
-// returns the walk.
-__device__ __forceinline__ WaveWalk wave_walk_setup(const BinRec &r, bool test, int tile, int W,
-                                                    int H, float *slice, int lane) {
-#pragma clang fp contract(off)
-    WaveWalk k;
-    k.r = &r;
-    k.x0 = (int)(r.xs & 0xffffu);
-    k.y0 = (int)(r.ys & 0xffffu);
-    k.w = (int)(r.xs >> 16) - k.x0 + 1;
-    k.h = (int)(r.ys >> 16) - k.y0 + 1;
-    k.test = test;
-    k.tile = tile;
-    k.W = W;
-    k.H = H;
-    k.u = k.v = nullptr;
-    if (test && k.h + 1 + k.w + 1 <= kEdgeSlots) {
-        const float mux = r.ux, muy = r.uy, a = r.a, b = r.b, c = r.c;
-        for (int i = lane; i <= k.h; i += 64) {
+    const int R = __builtin_amdgcn_readfirstlane((int)(key & 63u)) + 1;
+    const int s = min(w, 64 / R);
+    const int ns = (w + s - 1) / s, nr = (h + R - 1) / R;
+    const int rg = lane / s, cl = lane - rg * s;
+    const bool lane_ok = lane < R * s;
+    const float mux = r.ux, muy = r.uy, a = r.a, b = r.b, c = r.c, thr = r.thr;
+    const bool fast = test && h + 1 <= kRowSlots;
+    if (fast) {
+        for (int i = lane; i <= h; i += 64) {
             // Row boundary of row y0 + i: its top edge; the last is the
             // bottom of row y1, clamped to the image as the walk clamps it.
-            const int ty = k.y0 + i;
-            const float ry = i == 0 ? (float)(ty * tile) : fminf((float)(ty * tile), (float)H);
-            slice[i] = mux - b * (ry - muy) / a;
-        }
-        for (int j = lane; j <= k.w; j += 64) {
-            const int tx = k.x0 + j;
-            const float rx = j == 0 ? (float)(tx * tile) : fminf((float)(tx * tile), (float)W);
-            slice[k.h + 1 + j] = muy - b * (rx - mux) / c;
+            const int ty = y0 + i;
+            const float Y = i == 0 ? (float)(ty * tile) : fminf((float)(ty * tile), (float)H);
+            const float u = mux - b * (Y - muy) / a;
+            const float ey = Y - muy, ex = u - mux;
+            const float C = c * ey * ey;
+            rows[i] = make_float4(u, Y, C, a * ex * ex + 2.0f * b * ex * ey + C);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        k.u = slice;
-        k.v = slice + k.h + 1;
     }
-    return k;
+    for (int k = 0; k < ns; ++k) {
+        const int j = k * s + cl;
+        const bool col_ok = lane_ok && j < w;
+        const int tx = x0 + min(j, w - 1);
+        // Column boundaries j and j + 1 (the tile's left and right edges).
+        const float Xl = (float)(tx * tile), Xr = fminf((float)((tx + 1) * tile), (float)W);
+        const float vl = muy - b * (Xl - mux) / c, vr = muy - b * (Xr - mux) / c;
+        const float exl = Xl - mux, exr = Xr - mux;
+        const float Al = a * exl * exl, Pl = 2.0f * b * exl;
+        const float Ar = a * exr * exr, Pr = 2.0f * b * exr;
+        const float eyl = vl - muy, eyr = vr - muy;
+        const float Nl = Al + Pl * eyl + c * eyl * eyl, Nr = Ar + Pr * eyr + c * eyr * eyr;
+        const bool in_x = mux >= Xl && mux <= Xr;
+        for (int t = 0; t < nr; ++t) {
+            const int i = t * R + rg;
+            const bool ok = col_ok && i < h;
+            const int ty = y0 + min(i, h - 1);
+            bool claim = ok;
+            if (fast) {
+                const float4 r0 = rows[min(i, h - 1)], r1 = rows[min(i, h - 1) + 1];
+                const float ey0 = r0.y - muy, ey1 = r1.y - muy;
+                const float F00 = Al + Pl * ey0 + r0.z, F01 = Ar + Pr * ey0 + r0.z;
+                const float F10 = Al + Pl * ey1 + r1.z, F11 = Ar + Pr * ey1 + r1.z;
+                const float top = r0.x >= Xl ? (r0.x > Xr ? F01 : r0.w) : F00;
+                const float bot = r1.x >= Xl ? (r1.x > Xr ? F11 : r1.w) : F10;
+                const float lft = vl >= r0.y ? (vl > r1.y ? F10 : Nl) : F00;
+                const float rgt = vr >= r0.y ? (vr > r1.y ? F11 : Nr) : F01;
+                float best = fminf(top, bot);
+                best = fminf(best, lft);
+                best = fminf(best, rgt);
+                const bool in = in_x && muy >= r0.y && muy <= r1.y;
+                claim = ok && (in || best < thr);
+            } else if (test) {
+                claim = ok && tile_claim(r, true, tx, ty, tile, W, H);
+            }
+            step(claim, tx, ty);
+        }
+    }
+    // The slice is rewritten for the wave's next rectangle.
+    __builtin_amdgcn_wave_barrier();
 }
 
 __device__ __forceinline__ int rec_area(const BinRec &r) {
@@ -548,10 +585,11 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
     __shared__ BinRec s_rec[kBinThreads];
     __shared__ int32_t s_big[kBinThreads], s_cnt[kBinThreads];
     __shared__ int32_t s_nbig;
-    __shared__ float s_edge[kBinThreads / 64][kEdgeSlots];
     __shared__ int32_t s_pre[kBinThreads];
     __shared__ uint32_t s_msk[kBinThreads];
-    __shared__ __align__(4) uint8_t s_own[kBinThreads / 64][64 * kWaveWalkArea];
+    // Per wave: the small claims' owner marks, then the strip walk's row
+    // boundaries.
+    __shared__ float4 s_rows[kBinThreads / 64][kRowSlots];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t g = (int64_t)blockIdx.x * kBinThreads + tid;
     const bool test = A.conic != nullptr;
@@ -573,7 +611,8 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
     // The claimed tiles of a small rectangle, bit loc for its row-major tile
     // loc: the write pass emits from them without testing again.
     mask = wave_small_claims(r, ar, test, A.tile, A.W, A.H, s_rec + wave * 64,
-                             s_pre + wave * 64, s_msk + wave * 64, s_own[wave], lane);
+                             s_pre + wave * 64, s_msk + wave * 64,
+                             reinterpret_cast<uint8_t *>(s_rows[wave]), lane);
     n = __popc(mask);
     if (g < A.N) masks[g] = mask;
     // s_rec's wave slice now holds the big rectangles' records (a lane's own
@@ -589,22 +628,11 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
     for (int e = wave; e < s_nbig; e += kBinThreads / 64) {
         const int j = s_big[e];
         const BinRec r = s_rec[j];
-        const WaveWalk k = wave_walk_setup(r, test, A.tile, A.W, A.H, s_edge[wave], lane);
-        const int area = k.w * k.h;
-        // Lane l starts at tile l of the row-major order and steps by 64.
-        int row = lane / k.w, col = lane % k.w;
-        const int drow = 64 / k.w, dcol = 64 % k.w;
         int cnt = 0;
-        for (int t = lane; t < area; t += 64) {
-            cnt += k.claim(row, col) ? 1 : 0;
-            row += drow;
-            col += dcol;
-            if (col >= k.w) { col -= k.w; ++row; }
-        }
+        strip_walk(r, test, A.tile, A.W, A.H, s_rows[wave], lane,
+                   [&](bool claim, int, int) { cnt += claim ? 1 : 0; });
         for (int o = 32; o >= 1; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
         if (lane == 0) s_cnt[j] = cnt;
-        // The slice is rewritten for the wave's next rectangle.
-        __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
     if (g < A.N) {
@@ -694,11 +722,10 @@ constexpr int kBinStage = 2048;
 //     256 x 32 pairs) and staged in windows of kBinStage slots, each slot
 //     with its position in the range, then stored by consecutive lanes, so
 //     adjacent runs land as coalesced stores.
-//   * Large rectangles (more than kWaveWalkArea tiles) are walked by a wave,
-//     64 tiles a step in row-major order; the claimed tiles of a step take
-//     consecutive positions by lane rank (the walk's emission order), and
-//     the wave stores them directly, consecutive lanes on consecutive
-//     addresses.
+//   * Large rectangles (more than kWaveWalkArea tiles) are walked by a wave
+//     (strip_walk, up to 64 tiles a step); the claimed tiles of a step take
+//     consecutive positions by lane rank, and the wave stores them directly,
+//     consecutive lanes on consecutive addresses.
 // With pairs (and depth) the value of a pair is {Gaussian id, its depth's
 // float bits} in one 8-byte store instead of the id alone in ids.
 // The workgroup's output range starts at part_off[blockIdx.x] (the count
@@ -710,8 +737,11 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
     const float *depth, uint2 *pairs, const int64_t *status) {
     // Capacity-bounded lists that overflowed emit nothing.
     if (status && status[1] != 0) return;
-    __shared__ uint32_t s_k[kBinStage];
+    // s_k also holds each wave's strip-walk row slice before the staging
+    // windows use it.
+    __shared__ __align__(16) uint32_t s_k[kBinStage];
     __shared__ int32_t s_i[kBinStage];
+    static_assert(kBinStage * 4 >= (kBinThreads / 64) * kRowSlots * 16, "row slices fit s_k");
     __shared__ int32_t s_off[kBinStage];
     __shared__ BinRec s_rec[kBinThreads];
     __shared__ int32_t s_big[kBinThreads], s_g[kBinThreads];
@@ -720,7 +750,6 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
     // large rectangles; they share s_off's storage, which the staging windows
     // only use afterwards.
     int32_t *s_at = s_off, *s_cap = s_off + kBinThreads;
-    __shared__ float s_edge[kBinThreads / 64][kEdgeSlots];
     __shared__ uint32_t s_dk[kBinThreads];   // depth bits of the workgroup's Gaussians
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t k0 = (int64_t)blockIdx.x * kBinThreads;
@@ -786,29 +815,21 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
         const int32_t gb = s_g[j];
         const int64_t atb = base + s_at[j];
         const int capb = s_cap[j];
-        const WaveWalk wk = wave_walk_setup(rb, test != 0, tile, W, H, s_edge[wave], lane);
-        const int area = wk.w * wk.h;
-        int row = lane / wk.w, col = lane % wk.w;
-        const int drow = 64 / wk.w, dcol = 64 % wk.w;
+        const uint32_t dk = s_dk[j];
         int emitted = 0;
-        for (int t0 = 0; t0 < area; t0 += 64) {
-            const bool claim = t0 + lane < area && wk.claim(row, col);
-            const int tx = wk.x0 + col, ty = wk.y0 + row;
-            row += drow;
-            col += dcol;
-            if (col >= wk.w) { col -= wk.w; ++row; }
-            const uint64_t cm = ballot(claim);
-            const int pos = emitted + rank_in(cm);
-            if (claim && pos < capb) {
-                tkeys[atb + pos] = (uint32_t)(ty * tiles_x + tx);
-                if (pairs)
-                    pairs[atb + pos] = make_uint2((uint32_t)gb, s_dk[j]);
-                else
-                    ids[atb + pos] = gb;
-            }
-            emitted += __popcll(cm);
-        }
-        __builtin_amdgcn_wave_barrier();
+        strip_walk(rb, test != 0, tile, W, H, reinterpret_cast<float4 *>(s_k) + wave * kRowSlots,
+                   lane, [&](bool claim, int tx, int ty) {
+                       const uint64_t cm = ballot(claim);
+                       const int pos = emitted + rank_in(cm);
+                       if (claim && pos < capb) {
+                           tkeys[atb + pos] = (uint32_t)(ty * tiles_x + tx);
+                           if (pairs)
+                               pairs[atb + pos] = make_uint2((uint32_t)gb, dk);
+                           else
+                               ids[atb + pos] = gb;
+                       }
+                       emitted += __popcll(cm);
+                   });
     }
     __syncthreads();   // s_at / s_cap read; s_off becomes the staging window
     // Small rectangles: LDS windows over the numbered runs.
