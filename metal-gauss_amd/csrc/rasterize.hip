@@ -213,9 +213,75 @@ __device__ __forceinline__ void reduce10_to_rows(const float v[10], float &q0, f
     q2 = row_allsum(p4 + z);
 }
 
+// Wave sums of two entries' nine values each (a: entry A, b: entry B), for
+// one LDS atomic per sum. The two swap stages above leave, in lane bits 5 and
+// 4, the entry and the parity of the value index; three transposing DPP
+// stages then halve the values again per lane bit while summing (row_ror:8
+// pairs lane bit 3, row_half_mirror pairs lanes l and 7 - l of an 8-lane
+// group across bit 2, quad_perm l ^ 2 bit 1), and quad_perm l ^ 1 ends the
+// sum. Lane l returns the full sum of value
+//   4 b2 + 2 b3 + b4   when bit 1 is clear,
+//   8                  when bit 1 is set and bits 2-4 are clear,
+// of entry bit 5 (bits b_i of l); its pair partner l ^ 1 holds the same sum,
+// and the other lanes with bit 1 set hold the zero padding. reduce18_slot
+// names each lane's value, -1 for lanes that deposit nothing. 44 VALU
+// operations for eighteen sums, against 2 x 26 plus twice the deposits.
+__device__ __forceinline__ int reduce18_slot(int lane) {
+    if (lane & 1) return -1;
+    if (lane & 2) return (lane & 0x1C) == 0 ? 8 : -1;
+    return 4 * ((lane >> 2) & 1) + 2 * ((lane >> 3) & 1) + ((lane >> 4) & 1);
+}
+__device__ __forceinline__ float reduce18(const float a[9], const float b[9], int lane) {
+    float x0 = a[0], x1 = a[1], x2 = a[2], x3 = a[3], x4 = a[4], x5 = a[5], x6 = a[6];
+    float x7 = a[7], x8 = a[8];
+    float y0 = b[0], y1 = b[1], y2 = b[2], y3 = b[3], y4 = b[4], y5 = b[5], y6 = b[6];
+    float y7 = b[7], y8 = b[8];
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_permlane32_swap_b32 %0, %1\n\t"
+        "v_permlane32_swap_b32 %2, %3\n\t"
+        "v_permlane32_swap_b32 %4, %5\n\t"
+        "v_permlane32_swap_b32 %6, %7\n\t"
+        "v_permlane32_swap_b32 %8, %9\n\t"
+        "v_permlane32_swap_b32 %10, %11\n\t"
+        "v_permlane32_swap_b32 %12, %13\n\t"
+        "v_permlane32_swap_b32 %14, %15\n\t"
+        "v_permlane32_swap_b32 %16, %17"
+        : "+v"(x0), "+v"(y0), "+v"(x1), "+v"(y1), "+v"(x2), "+v"(y2), "+v"(x3), "+v"(y3),
+          "+v"(x4), "+v"(y4), "+v"(x5), "+v"(y5), "+v"(x6), "+v"(y6), "+v"(x7), "+v"(y7),
+          "+v"(x8), "+v"(y8));
+    // Lanes 0-31: entry A's half sums of value i; lanes 32-63: entry B's.
+    float p0 = x0 + y0, p1 = x1 + y1, p2 = x2 + y2, p3 = x3 + y3, p4 = x4 + y4;
+    float p5 = x5 + y5, p6 = x6 + y6, p7 = x7 + y7, p8 = x8 + y8;
+    float z = 0.0f;
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_permlane16_swap_b32 %0, %1\n\t"
+        "v_permlane16_swap_b32 %2, %3\n\t"
+        "v_permlane16_swap_b32 %4, %5\n\t"
+        "v_permlane16_swap_b32 %6, %7\n\t"
+        "v_permlane16_swap_b32 %8, %9"
+        : "+v"(p0), "+v"(p1), "+v"(p2), "+v"(p3), "+v"(p4), "+v"(p5), "+v"(p6), "+v"(p7),
+          "+v"(p8), "+v"(z));
+    // Row (bit 4) r of q_m: value 2m + r (q4: value 8, padding).
+    const float q0 = p0 + p1, q1 = p2 + p3, q2 = p4 + p5, q3 = p6 + p7, q4 = p8 + z;
+    const bool b3 = lane & 8, b2 = lane & 4, b1 = lane & 2;
+    const float r0 = (b3 ? q1 : q0) + dpp_f<0x128>(b3 ? q0 : q1);   // row_ror:8
+    const float r1 = (b3 ? q3 : q2) + dpp_f<0x128>(b3 ? q2 : q3);
+    const float r2 = q4 + dpp_f<0x128>(q4);
+    const float s0 = (b2 ? r1 : r0) + dpp_f<0x141>(b2 ? r0 : r1);   // row_half_mirror
+    const float s1 = r2 + dpp_f<0x141>(r2);
+    const float t = (b1 ? s1 : s0) + dpp_f<0x4E>(b1 ? s0 : s1);     // quad_perm 2,3,0,1
+    return t + dpp_f<0xB1>(t);                                       // quad_perm 1,0,3,2
+}
+
+// S.grad rows are padded by one float: the deposits and the flush touch the
+// ten slots of one entry together, which then fall in distinct LDS banks.
+constexpr int kGradStride = kBatch + 1;
+
 template <int MAXW>
 struct StageBwd : Stage<MAXW> {
-    float grad[kGradSlots][kBatch];   // per batch entry, summed over waves
+    float grad[kGradSlots][kGradStride];   // per batch entry, summed over waves
 };
 
 // One list entry's record, gathered from the per-Gaussian arrays.
@@ -597,9 +663,10 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
     int bstop = start;
     for (int w = 0; w < nwaves; ++w) bstop = max(bstop, S.flag[w]);
 
-    // One list entry: the pixel's update and the wave's sums into S.grad.
-    auto entry = [&](const int j, const int i, const float4 geo, const float4 con,
-                     const float4 col) {
+    // One list entry's update of the pixel; v gets the pixel's share of the
+    // entry's sums (zeros where it is not active). Returns whether it is.
+    auto update = [&](const int i, const float4 geo, const float4 con, const float4 col,
+                      float v[kGradSlots]) {
         const float dx = fx - geo.x, dy = fy - geo.y;
         const float power = splat_power(dx, dy, con);
         const float gauss = __expf(power);
@@ -607,12 +674,11 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
         const float alpha_raw = op * gauss;
         const float alpha = fminf(kAlphaMax, alpha_raw);
         const bool active = inimg && i < my_stop && power <= 0.0f && alpha >= kAlphaMin;
-        if (ballot(active) == 0) return;
         // Branchless: inactive lanes compute on finite values and select
-        // zeros (never multiply by 0, which would keep an inf as NaN). T
-        // before this entry is recovered as T / (1 - alpha) with a 1-ulp
-        // reciprocal; the forward's rounding of T (1 - alpha) already makes
-        // the recovery approximate.
+        // zeros (never multiply by 0, which would keep an inf as NaN); T and
+        // Gs keep their values. T before this entry is recovered as
+        // T / (1 - alpha) with a 1-ulp reciprocal; the forward's rounding of
+        // T (1 - alpha) already makes the recovery approximate.
         const float om = fmaxf(1.0f - alpha, 1e-8f);
         const float iom = __builtin_amdgcn_rcpf(om);
         const float gc = fmaf(gb, col.z, fmaf(gg, col.y, fmaf(gr, col.x, ga)));
@@ -623,7 +689,6 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
         Gs = fmaf(w, gc, Gs);
         // Past the 0.999 clamp alpha no longer depends on the splat.
         const float dg = active && alpha_raw <= kAlphaMax ? dal * gauss : 0.0f;
-        float v[kGradSlots];
         v[0] = w * gr;
         v[1] = w * gg;
         v[2] = w * gb;
@@ -642,6 +707,15 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
         } else {
             v[9] = 0.0f;
         }
+        return active;
+    };
+
+    // One list entry: the pixel's update and the wave's sums into S.grad.
+    auto entry = [&](const int j, const int i, const float4 geo, const float4 con,
+                     const float4 col) {
+        float v[kGradSlots];
+        // With no lane active the update leaves T and Gs as they were.
+        if (ballot(update(i, geo, con, col, v)) == 0) return;
         // Sums over the wave of v[0..9], deposited into S.grad[.][j] with
         // four lanes per LDS atomic (see reduce10_to_rows).
         float q0, q1, q2;
@@ -658,6 +732,20 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
             atomicAdd(&S.grad[4 + s0][j], q1);
             atomicAdd(&S.grad[8 + (row >> 1)][j], q2);
         }
+    };
+
+    // Two consecutive entries (back to front: a, then b), their eighteen
+    // sums in one reduction and one LDS atomic per sum (without |d uv|).
+    const int slot18 = reduce18_slot(lane);
+    auto entry2 = [&](const int ja, const float4 geo_a, const float4 con_a, const float4 col_a,
+                      const int jb, const float4 geo_b, const float4 con_b,
+                      const float4 col_b, const int base) {
+        float va[kGradSlots], vb[kGradSlots];
+        const bool act_a = update(base + ja, geo_a, con_a, col_a, va);
+        const bool act_b = update(base + jb, geo_b, con_b, col_b, vb);
+        if (ballot(act_a || act_b) == 0) return;
+        const float sum = reduce18(va, vb, lane);
+        if (slot18 >= 0) atomicAdd(&S.grad[slot18][(lane & 32) ? jb : ja], sum);
     };
 
     // After a batch's walk, entry e's sums become its gradient record slots,
@@ -714,7 +802,7 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
         } else {
             stage_batch(S, A, base, n, nwaves);
         }
-        for (int q = t; q < kGradSlots * kBatch; q += blockDim.x) (&S.grad[0][0])[q] = 0.f;
+        for (int q = t; q < kGradSlots * kGradStride; q += blockDim.x) (&S.grad[0][0])[q] = 0.f;
         __syncthreads();
         if (PIPE) {
             // Batches below the first are full.
@@ -726,7 +814,58 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
         // the records of the next entry read before this one's math. The
         // list is read 64 indices at a time into a register and the entry's
         // index taken from it with a lane read, so it is wave-uniform.
-        if (cnt > 0) {
+        if (cnt > 0 && !ABS) {
+            // Entries k and k - 1 share one reduction; entry k - 2's records
+            // are read before their math. Two pairs per iteration, so the
+            // read-ahead record alternates between the a and c registers.
+            int k = cnt - 1;
+            int lreg = S.list[wave][(k & ~63) + lane];
+            int ja = __builtin_amdgcn_readlane(lreg, k & 63), jc;
+            float4 geo_a = S.geo[ja], con_a = S.con[ja], col_a = S.col[ja];
+            float4 geo_c, con_c, col_c;
+            // Entry k - 1 into (jx, x) and entry max(k - 2, 0) into (jy, y).
+            auto read2 = [&](int &jx, float4 &gx, float4 &kx, float4 &cx, int &jy, float4 &gy,
+                             float4 &ky, float4 &cy) {
+                const int kb = k - 1;
+                if ((kb & 63) == 63) lreg = S.list[wave][(kb & ~63) + lane];
+                jx = __builtin_amdgcn_readlane(lreg, kb & 63);
+                gx = S.geo[jx];
+                kx = S.con[jx];
+                cx = S.col[jx];
+                const int kc = max(k - 2, 0);
+                if ((kc & 63) == 63) lreg = S.list[wave][(kc & ~63) + lane];
+                jy = __builtin_amdgcn_readlane(lreg, kc & 63);
+                gy = S.geo[jy];
+                ky = S.con[jy];
+                cy = S.col[jy];
+            };
+            for (;;) {
+                if (k == 0) {
+                    entry(ja, base + ja, geo_a, con_a, col_a);
+                    break;
+                }
+                {
+                    int jb;
+                    float4 geo_b, con_b, col_b;
+                    read2(jb, geo_b, con_b, col_b, jc, geo_c, con_c, col_c);
+                    entry2(ja, geo_a, con_a, col_a, jb, geo_b, con_b, col_b, base);
+                }
+                k -= 2;
+                if (k < 0) break;
+                if (k == 0) {
+                    entry(jc, base + jc, geo_c, con_c, col_c);
+                    break;
+                }
+                {
+                    int jd;
+                    float4 geo_d, con_d, col_d;
+                    read2(jd, geo_d, con_d, col_d, ja, geo_a, con_a, col_a);
+                    entry2(jc, geo_c, con_c, col_c, jd, geo_d, con_d, col_d, base);
+                }
+                k -= 2;
+                if (k < 0) break;
+            }
+        } else if (cnt > 0) {
             int k = cnt - 1;
             int lreg = S.list[wave][(k & ~63) + lane];
             int ja = __builtin_amdgcn_readlane(lreg, k & 63);
