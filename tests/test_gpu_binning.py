@@ -83,8 +83,9 @@ def test_tile_lists_bit_exact(dev, tile):
 @pytest.mark.parametrize("ellipse", [True, False])
 def test_large_rectangles_bit_exact(dev, tile, ellipse):
     """Near, wide splats whose rectangles span tens to hundreds of tiles take
-    the wave-parallel walk (more than 32 tiles); mixed with small ones, the
-    lists must still equal the oracle's, emission order included."""
+    the wave-parallel strip walk (more than 32 tiles), where each tile's edge
+    minima are selects between row, column and corner values; mixed with
+    small ones, the sorted lists must still equal the oracle's."""
     s = ref_scene(N=6000, seed=11)
     g = torch.Generator().manual_seed(12)
     k = 600
@@ -96,6 +97,31 @@ def test_large_rectangles_bit_exact(dev, tile, ellipse):
     big = ((2 * rxy[:, 0] / tile + 1) * (2 * rxy[:, 1] / tile + 1) > 32) & \
         (valid.cpu().numpy() != 0)
     assert big.sum() > 100, big.sum()
+    assert np.array_equal(gpu[3], ref[3]), "sorted keys differ"
+    assert np.array_equal(gpu[0], ref[0]), "gauss_ids differ"
+    assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
+
+
+@pytest.mark.parametrize("tile", [8, 16])
+def test_rectangles_taller_than_the_row_slice_bit_exact(dev, tile):
+    """Rectangles of more than 127 tile rows do not fit the strip walk's LDS
+    row slice and test each tile from scratch. On a 96 x 4096 image, near
+    splats stretched along y span a few hundred tile rows (tile 8 also takes
+    the radix route: 6144 tiles). The lists must equal the oracle's."""
+    s = ref_scene(N=3000, W=96, H=4096, seed=41)
+    g = torch.Generator().manual_seed(42)
+    k = 40
+    s["means"][:k, 0] = (torch.rand(k, generator=g) - 0.5) * 0.4
+    s["means"][:k, 1] = (torch.rand(k, generator=g) - 0.5) * 4.0
+    s["means"][:k, 2] = torch.rand(k, generator=g) * 0.6 + 1.2
+    s["scales"][:k, 0] = 0.05
+    s["scales"][:k, 1] = torch.rand(k, generator=g) * 2.0 + 1.5
+    s["scales"][:k, 2] = 0.05
+    s["quats"][:k] = torch.tensor([1.0, 0.0, 0.0, 0.0])
+    gpu, ref = run_both(s, dev, tile)
+    _, _, _, rxy, valid, _ = gpu_preprocess(s, dev)
+    ry, v = rxy[:, 1].cpu().numpy(), valid.cpu().numpy() != 0
+    assert ((2 * ry / 16 > 130) & v).sum() >= 5, "no rectangle taller than the row slice"
     assert np.array_equal(gpu[3], ref[3]), "sorted keys differ"
     assert np.array_equal(gpu[0], ref[0]), "gauss_ids differ"
     assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
