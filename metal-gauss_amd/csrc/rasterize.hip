@@ -513,7 +513,9 @@ __global__ __launch_bounds__(MAXW * 64) __attribute__((amdgpu_waves_per_eu(8))) 
                 float4 gg[U], kk[U], cc[U];
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    const int ku = k + u < cnt ? k + u : k;
+                    // Past the end, the round's last real entry again (masked
+                    // below); a scalar min keeps the lane index in scalar registers.
+                    const int ku = min(k + u, cnt - 1);
                     jj[u] = __builtin_amdgcn_readlane(lreg, ku & 63);
                     gg[u] = S.geo[jj[u]];
                     kk[u] = S.con[jj[u]];
