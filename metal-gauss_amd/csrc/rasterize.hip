@@ -451,7 +451,10 @@ __global__ __launch_bounds__(MAXW * 64) __attribute__((amdgpu_waves_per_eu(8))) 
                                                                int32_t *out_stop,
                                                                const ChunkPlan P) {
     __shared__ Stage<MAXW> S;
-    if (A.zero) {
+    // The gradient records' clearing goes out last: on this GPU a load's
+    // wait also waits for every earlier store of the wave.
+    auto zero_fill = [&]() {
+        if (!A.zero) return;
         // Slices of a multiple of 4 floats: float4 stores, a scalar tail.
         const int64_t per = (((A.zero_n + gridDim.x - 1) / gridDim.x) + 3) & ~(int64_t)3;
         const int64_t b = (int64_t)blockIdx.x * per, e = min(A.zero_n, b + per);
@@ -461,9 +464,12 @@ __global__ __launch_bounds__(MAXW * 64) __attribute__((amdgpu_waves_per_eu(8))) 
             else
                 for (int64_t j = i; j < e; ++j) A.zero[j] = 0.f;
         }
-    }
+    };
     const int tile_id = tile_of_block(blockIdx.x, A.tiles_x, A.n_tiles / A.tiles_x);
-    if (tile_id < 0) return;   // whole workgroup
+    if (tile_id < 0) {   // whole workgroup
+        zero_fill();
+        return;
+    }
     const int tx = tile_id % A.tiles_x, ty = tile_id / A.tiles_x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nwaves = blockDim.x >> 6;
@@ -553,6 +559,7 @@ __global__ __launch_bounds__(MAXW * 64) __attribute__((amdgpu_waves_per_eu(8))) 
     // A tile that turned opaque early: its later chunks end in the final state.
     for (; unit < unit_end; ++unit)
         if (inimg) P.ckpt[(int64_t)unit * tile2 + pslot] = make_float4(T, cr, cg, cb);
+    zero_fill();
     if (!inimg) return;
     const int64_t o = (int64_t)py * A.W + px;
     if (A.has_bg) {
