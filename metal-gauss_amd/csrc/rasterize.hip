@@ -688,7 +688,9 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
         // Gs keep their values. T before this entry is recovered as
         // T / (1 - alpha) with a 1-ulp reciprocal; the forward's rounding of
         // T (1 - alpha) already makes the recovery approximate.
-        const float om = fmaxf(1.0f - alpha, 1e-8f);
+        // alpha <= 0.999 (fminf returns 0.999 for a NaN product too), so
+        // 1 - alpha >= 0.001 needs no lower clamp.
+        const float om = 1.0f - alpha;
         const float iom = __builtin_amdgcn_rcpf(om);
         const float gc = fmaf(gb, col.z, fmaf(gg, col.y, fmaf(gr, col.x, ga)));
         const float dal = (T * gc - Gs) * iom;
