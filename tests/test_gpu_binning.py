@@ -127,6 +127,47 @@ def test_rectangles_taller_than_the_row_slice_bit_exact(dev, tile):
     assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
 
 
+@pytest.mark.parametrize("seed", [51, 52])
+def test_synthetic_conics_on_large_rectangles_bit_exact(dev, seed):
+    """The strip walk's selects against the oracle's per-tile test over
+    geometries a scene rarely produces: near-singular conics (b^2 within
+    1e-3 of ac), very anisotropic ones, both signs of b, a and c at the
+    1e-12 clamp, centres off the image (clamped rectangles) and on tile
+    boundaries, on rectangles of 33 to a few thousand tiles. Inputs are
+    drawn directly, not projected."""
+    from metal_gauss_amd.backend import _bin
+
+    rng = np.random.default_rng(seed)
+    N, W, H, tile = 3000, 640, 480, 16
+    f32 = np.float32
+    uv = np.stack([rng.uniform(-80, W + 80, N), rng.uniform(-80, H + 80, N)], 1).astype(f32)
+    on_edge = rng.random(N) < 0.1   # centres exactly on tile boundaries
+    uv[on_edge] = (np.round(uv[on_edge] / tile) * tile).astype(f32)
+    rxy = rng.uniform(40, 400, (N, 2)).astype(f32)
+    a = np.exp(rng.uniform(np.log(1e-5), np.log(1.0), N)).astype(f32)
+    c = np.exp(rng.uniform(np.log(1e-5), np.log(1.0), N)).astype(f32)
+    corr = rng.uniform(-1.0, 1.0, N)
+    near = rng.random(N) < 0.3      # |b| within 1e-3 of sqrt(ac)
+    corr[near] = np.sign(corr[near]) * (1.0 - rng.uniform(0.0, 1e-3, near.sum()))
+    b = (corr * np.sqrt(a.astype(np.float64) * c)).astype(f32)
+    tiny = rng.random(N) < 0.05
+    a[tiny] = f32(1e-13)
+    conic = np.stack([a, b, c], 1).astype(f32)
+    op = rng.uniform(0.01, 0.99, N).astype(f32)
+    valid = (rng.random(N) < 0.9).astype(np.int32)
+    depth = rng.uniform(0.5, 20.0, N).astype(f32)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    gids, offs, _ = _bin(t(uv), t(rxy), t(depth), t(valid), t(conic), t(op), W, H, tile)
+    rids, roffs, _, _ = binning_ref.build_tile_lists(uv, rxy, conic, op, valid, depth, W, H,
+                                                     tile, ellipse=True)
+    area = ((np.floor((uv[:, 0] + rxy[:, 0]) / tile) - np.floor((uv[:, 0] - rxy[:, 0]) / tile) + 1)
+            * (np.floor((uv[:, 1] + rxy[:, 1]) / tile) - np.floor((uv[:, 1] - rxy[:, 1]) / tile) + 1))
+    assert ((area > 32) & (valid != 0)).sum() > 1000
+    assert gids.numel() > 10000, gids.numel()
+    assert np.array_equal(offs.cpu().numpy(), roffs), "tile offsets differ"
+    assert np.array_equal(gids.cpu().numpy(), rids), "gauss_ids differ"
+
+
 @pytest.mark.parametrize("spread", [0.0, 2e-6, 2e-3, 0.5, 3.0])
 def test_depth_windows_of_every_pass_count_bit_exact(dev, spread):
     """The per-tile depth sort takes 8-bit passes over only the bits in which
