@@ -194,7 +194,8 @@ class ListCapacity:
     parameter as it was. With an int capacity instead, ``watch(status)``
     queues a copy of the device status words to pinned memory behind an
     event, and ``overflowed`` waits for that event. Up to ``depth`` renders
-    may be outstanding. The reference sizes its buffers by reading the total
+    may be outstanding: issuing one more first polls the oldest, and
+    raises if that render overflowed unchecked. The reference sizes its buffers by reading the total
     on the host in the middle of every render (metal_backend.py:246-248),
     which drains the queue once per render.
     """
@@ -217,11 +218,25 @@ class ListCapacity:
             self._view = self._slots.numpy()
             self._events = [None] * self.depth
             self._event_mode = [False] * self.depth
+            self._observed = [True] * self.depth
         ticket = self._issued
-        self._issued += 1
         k = ticket % self.depth
+        if not self._observed[k]:
+            # The slot still holds a render nobody polled (more than
+            # ``depth`` outstanding): read it before its status is
+            # overwritten. An overflow there means an optimizer step that
+            # changed nothing on the device while the host counted it.
+            old = ticket - self.depth
+            if self.overflowed(old):
+                raise RuntimeError(
+                    f"ListCapacity: render {old} overflowed its lists and was never checked; "
+                    f"more than depth={self.depth} renders were outstanding. Poll each "
+                    "render with overflowed(ticket) (and rewind() its optimizer step on "
+                    "overflow) within depth renders, or raise depth.")
+        self._issued += 1
         self._view[k, 2] = -1
         self._event_mode[k] = event_mode
+        self._observed[k] = False
         return ticket
 
     def claim(self) -> tuple[int, int, int]:
@@ -252,10 +267,17 @@ class ListCapacity:
             self._events[k].synchronize()
         else:
             end = time.perf_counter() + timeout_s
+            spins = 0
             while self._view[k, 2] != ticket + 1:
+                # Spin briefly (a status is usually there within microseconds
+                # of the render's binning), then yield the GIL and back off.
+                spins += 1
+                if spins > 64:
+                    time.sleep(0.0 if spins < 1024 else 2e-5)
                 if time.perf_counter() > end:
                     raise RuntimeError("ListCapacity: the lists' status never arrived")
         total, over = int(self._view[k, 0]), int(self._view[k, 1])
+        self._observed[k] = True
         self.last_total = total
         if over:
             self.overflows += 1

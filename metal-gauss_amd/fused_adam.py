@@ -124,9 +124,9 @@ class FusedAdam(torch.optim.Optimizer):
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
-        applied, self._epilogue_applied = self._epilogue_applied, {}
-        self._last_stepped = list(applied.values())
-        for p in applied.values():
+        # Checked before the bookkeeping is reset, so a caller that catches
+        # the error and steps again still skips these parameters.
+        for p in self._epilogue_applied.values():
             if p.grad is not None:
                 raise RuntimeError(
                     f"FusedAdam.step(): a parameter of shape {tuple(p.shape)} has a gradient, "
@@ -134,6 +134,8 @@ class FusedAdam(torch.optim.Optimizer):
                     "loss uses it outside the render (a regulariser, for instance). Pass "
                     "the trainer's regularisers to render (opacity_reg=, scale_reg=), or "
                     "render without optimizer=.")
+        applied, self._epilogue_applied = self._epilogue_applied, {}
+        self._last_stepped = list(applied.values())
         batches: dict[tuple, list] = {}
         for group in self.param_groups:
             b1, b2 = group["betas"]

@@ -236,6 +236,16 @@ def test_lists_over_2048_entries_with_four_passes_bit_exact(dev):
     assert np.array_equal(gpu[3], ref[3]), "sorted keys differ"
     assert np.array_equal(gpu[0], ref[0]), "gauss_ids differ"
     assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
+    # The same build repeated in one process: a read-after-barrier race shows
+    # up as a run-to-run difference; every repetition must equal the oracle.
+    from metal_gauss_amd.backend import _bin
+
+    uv, conic, depth, rxy, valid, _ = gpu_preprocess(s, dev)
+    op = s["op"].to(dev)
+    for rep in range(8):
+        gids, offs, _ = _bin(uv, rxy, depth, valid, conic, op, W, H, 16)
+        assert np.array_equal(offs.cpu().numpy(), ref[1]), f"repetition {rep}: offsets differ"
+        assert np.array_equal(gids.cpu().numpy(), ref[0]), f"repetition {rep}: gauss_ids differ"
 
 
 def test_rect_only_lists_bit_exact_and_longer(dev):

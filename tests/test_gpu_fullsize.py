@@ -203,6 +203,83 @@ def _projection_check(sc, cam, outs, idx, rec, dev, label):
                             label)
 
 
+# ------------------------------------------------------------------ config 2
+
+def test_config2_parameter_gradients_through_render(dev):
+    """BASELINE configs[1] end to end through render(): 300k Gaussians, SH 3,
+    800x800, white background, L1 against the 5x5 box-blurred target. The
+    gradients of the activated inputs render takes (means, quats, scales,
+    opacities, SH) on a seeded 20k-row subsample, against float64 autograd
+    of render_ref.preprocess driven by raster_seq.c's forward and backward
+    on the same lists with the same image gradient (the reference's own
+    gradient check, tests/test_metal.py:95-117, at the configuration's
+    size). Bar: 1e-3 relative L2 per parameter."""
+    from metal_gauss_amd import render, scenes
+    from metal_gauss_amd.backend import _PreprocessMetal, _camera, build_tile_lists_metal
+
+    sc, cam, bg = scenes.config2()
+    W, H = cam.W, cam.H
+    act = [t.to(dev) for t in sc.activated()]     # means, quats, scales, opacities, sh (N,16,3)
+    leaves = [t.clone().requires_grad_(True) for t in act]
+    rgb, alpha, info = render(*leaves, cam.K, cam.viewmat, W, H, sh_degree=3, background=bg)
+    target = scenes.config2_target().to(dev)
+    # L1's gradient, formed once from the GPU image and given to both sides
+    # (sign() at |rgb - target| < 1e-4 would otherwise differ between them).
+    grad_rgb = (torch.sign(rgb.detach() - target) / rgb.numel()).contiguous()
+    rgb.backward(grad_rgb)
+    torch.cuda.synchronize()
+
+    # The C contract on the same projection and lists.
+    fx, fy, cx, cy, vm_h, cc = _camera(cam.K, cam.viewmat)
+    with torch.no_grad():
+        uv, conic, depth, rxy, valid, col = _PreprocessMetal.apply(
+            act[0], act[1], act[2], act[4], None, act[3], vm_h, fx, fy, cx, cy, W, H, 0.01,
+            100.0, 0.3, float(max(W, H)), cc, 3)
+        gids, offs, _ = build_tile_lists_metal(uv, rxy, depth, valid, conic, act[3], W, H, 16)
+    assert gids.numel() == int(info["isect_total"])
+    c_in = [_np(t) for t in (uv, conic, act[3], col, gids, offs)]
+    r = raster_ref.forward(*c_in, W, H, 16, 1e-4)
+    ok = ~r[4]
+    img = r[0] + (1.0 - r[1])[..., None]
+    assert np.abs(_np(rgb) - img)[ok].max() < 1e-4
+    g_rgb = _np(grad_rgb)
+    g_alpha = -(g_rgb.sum(axis=-1))                         # through the white blend
+    d_uv, d_conic, d_op, d_col, _ = raster_ref.backward(*c_in, r[2], r[3], g_rgb, g_alpha,
+                                                         W, H, 16)
+
+    # float64 (and float32) autograd of the projection on the subsample.
+    idx = _subsample(sc.n, 200)
+    gi = idx.to(dev)
+    K = cam.K.double()
+    ref = {}
+    for dt in (torch.float64, torch.float32):
+        lv = [t[idx].to(dt).clone().requires_grad_(True) for t in sc.activated()]
+        ruv, rconic, _, _, rvalid, rcol = render_ref.preprocess(
+            lv[0], lv[1], lv[2], lv[3], lv[4], cam.viewmat.to(dt), float(K[0, 0]),
+            float(K[1, 1]), float(K[0, 2]), float(K[1, 2]), W, H)
+        grads = [torch.from_numpy(a[idx.numpy()]).to(dt) for a in (d_uv, d_conic, d_col)]
+        torch.autograd.backward([ruv, rconic, rcol], grads)
+        lv[3].grad = torch.from_numpy(d_op[idx.numpy()]).to(dt)   # op enters only the raster
+        ref[dt] = (lv, rvalid)
+    (r64, rvalid), (r32, _) = ref[torch.float64], ref[torch.float32]
+    gv = _np(valid[gi]) != 0
+    agree = gv == rvalid.numpy()
+    assert agree.mean() > 0.999, f"{(~agree).sum()} validity flips of {SUB}"
+    both = torch.from_numpy(agree & gv)
+    print(f"config 2: {gids.numel()} intersections, {int(gv.sum())} of {SUB} rows visible",
+          flush=True)
+    for name, a, b, f in zip(("means", "quats", "scales", "opacities", "sh"), leaves, r64, r32):
+        got = rel_l2(a.grad[gi].cpu().double()[both], b.grad[both])
+        f32 = rel_l2(f.grad[both].double(), b.grad[both])
+        print(f"config 2 d_{name}: GPU {got:.2e}, CPU float32 {f32:.2e}", flush=True)
+        assert got < 1e-3, f"d_{name}: relative L2 {got:.2e} (float32 CPU {f32:.2e})"
+    # Rows the projection marked invalid: exact zeros.
+    hidden = torch.from_numpy(~gv).to(dev)
+    if bool(hidden.any()):
+        for a in leaves:
+            assert float(a.grad[gi][hidden].abs().max()) == 0.0
+
+
 # ------------------------------------------------------------------ config 4
 
 @pytest.mark.parametrize("view", [0, 57])

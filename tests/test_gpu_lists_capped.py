@@ -161,6 +161,17 @@ def test_list_capacity_host_slots_and_device_copies(dev):
         _render(p, cap)                      # a fifth render reuses ticket 0's slot
         with pytest.raises(RuntimeError, match="no outstanding render"):
             cap.overflowed(0)
+        # More than `depth` renders without a poll: the oldest is read before
+        # its slot is reused; one that overflowed unchecked is an error.
+        quiet = ListCapacity(initial=total + 10, depth=2)
+        for _ in range(5):
+            _render(p, quiet)
+        assert quiet.overflows == 0 and not quiet.overflowed()
+        lost = ListCapacity(initial=total - 1, depth=2)
+        _render(p, lost)
+        _render(p, lost)
+        with pytest.raises(RuntimeError, match="never checked"):
+            _render(p, lost)
         old = ListCapacity(initial=total - 1)
         _, _, info = _render(p, old.value)
         assert old.overflowed(old.watch(info["lists_status"])) and old.last_total == total

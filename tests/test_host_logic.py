@@ -188,3 +188,19 @@ def test_fused_adam_epilogue_refusals_count_no_step():
     b.grad = torch.zeros_like(b)
     assert opt.epilogue([b, a]) is None                           # gradient already there
     assert all(not opt.state[t] or opt.state[t]["step"] == 0 for t in (a, b))
+
+
+def test_fused_adam_refused_step_keeps_the_epilogue_bookkeeping():
+    """A step() refused because a parameter the epilogue already updated has
+    a gradient must leave that parameter recognised: calling step() again
+    refuses again instead of applying Adam to it a second time."""
+    from metal_gauss_amd import FusedAdam
+
+    p = torch.zeros(8, 3, requires_grad=True)
+    opt = FusedAdam([p], lr=1e-3)
+    opt._epilogue_applied = {id(p): p}       # as render(optimizer=opt)'s epilogue leaves it
+    p.grad = torch.ones_like(p)
+    for _ in range(2):
+        with pytest.raises(RuntimeError, match="already applied"):
+            opt.step()
+    assert opt._epilogue_applied == {id(p): p}
