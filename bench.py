@@ -44,7 +44,7 @@ RAMP_S = 2.0
 KERNELS = ["preprocess_forward", "bin_count", "exclusive_scan", "bin_write", "tile_sort",
            "depth_sort", "rasterize_forward", "rasterize_backward",
            "preprocess_backward", "preprocess_backward_adam", "ssim_fused_forward",
-           "ssim_fused_backward", "adam_step"]
+           "ssim_fused_backward", "adam_step", "tile_ranges"]
 
 # Library timing label -> the kernel name rocprofv3 reports for it (for the
 # tile sort, its scatter kernel; the scan runs three kernels and is left out).
@@ -100,6 +100,11 @@ def parse():
                     help="time another BASELINE configuration instead of the config-4 step: "
                          "1 forward at 10k/256^2; 2 fwd+bwd at 300k/800^2; 3 FusedAdam and "
                          "SelectiveAdam over 1M Gaussians; 5 fwd+bwd at 3M/1920x1080")
+    ap.add_argument("--crowded", action="store_true",
+                    help="with --config 5: the crowded variant (a dense cluster in front of the "
+                         "camera: tile lists over 10k entries, over 30M intersections)")
+    ap.add_argument("--chunked-backward", choices=["off", "on"], default="off",
+                    help="with --config 2/5: render(chunked_backward=...)")
     ap.add_argument("--render-fps", action="store_true",
                     help="forward-only frames per second at the reference's published points "
                          "(bench/render_fps.py, README.md:145-148)")
@@ -683,10 +688,11 @@ def _kernel_means(fn, reps, labels):
     return out
 
 
-def render_config(which, reps):
+def render_config(which, reps, crowded=False, chunked=False):
     """Configs 1, 2 and 5 ([1], [4]): one view, render
     forward (config 1) or forward + L1 loss + backward (2, 5), on the
-    configuration's seeded scene and camera."""
+    configuration's seeded scene and camera (config 5 ``crowded``: the
+    variant that reaches the configuration's stated stress)."""
     import torch
 
     from metal_gauss_amd import render, scenes
@@ -699,7 +705,7 @@ def render_config(which, reps):
         sc, cam, bg = scenes.config2()
         target = scenes.config2_target(cam.H, cam.W).to(dev)
     else:
-        sc, cam, bg = scenes.config5()
+        sc, cam, bg = scenes.config5_crowded() if crowded else scenes.config5()
         target = torch.zeros(cam.H, cam.W, 3, device=dev)
     sc = sc.to(dev)
     leaves = {k: getattr(sc, k).clone().requires_grad_(which != 1)
@@ -711,7 +717,7 @@ def render_config(which, reps):
         rgb, alpha, inf = render(L["means"], L["quats"], torch.exp(L["log_scales"]),
                                  torch.sigmoid(L["logit_opac"]), L["sh_dc"], cam.K, cam.viewmat,
                                  cam.W, cam.H, sh_degree=sc.sh_degree, sh_rest=L["sh_rest"],
-                                 background=bg)
+                                 background=bg, chunked_backward=chunked)
         info.update(inf)
         return rgb
 
@@ -1334,16 +1340,24 @@ def main():
         return
     if args.config is not None:
         c = args.config
-        res = adam_config(args.steps) if c == 3 else render_config(c, min(args.steps, 50))
+        if args.crowded and c != 5:
+            print("--crowded applies to --config 5 only", file=sys.stderr)
+            sys.exit(2)
+        res = adam_config(args.steps) if c == 3 else render_config(
+            c, min(args.steps, 50), args.crowded, args.chunked_backward == "on")
         metric = {1: "forward ms at 10k Gaussians 256x256 SH0",
                   2: "fwd+bwd ms at 300k Gaussians 800x800 SH3",
                   3: "Adam ms per step over 1M Gaussians x 59 floats",
                   5: "fwd+bwd ms at 3M Gaussians 1920x1080 SH3"}[c]
+        if args.crowded:
+            metric = "fwd+bwd ms at 3.6M Gaussians 1920x1080 SH3 (crowded: >30M intersections)"
         value = (res["fused"]["ms_per_step"] if c == 3 else
                  res["fwd_ms"] if c == 1 else res["fwd_bwd_ms"])
         print(json.dumps({"metric": metric, "value": value, "unit": "ms", "n_gpus": 1,
                           "higher_is_better": False, "dtype": "f32", "data": "synthetic",
-                          "config": {"workload": f"BASELINE configs[{c - 1}] (config {c})"},
+                          "config": {"workload": f"BASELINE configs[{c - 1}] (config {c})"
+                                                 + (", crowded variant" if args.crowded else ""),
+                                     "chunked_backward": args.chunked_backward},
                           "result": res}))
         return
     if args.mcmc:

@@ -204,6 +204,38 @@ def test_info_contract(dev):
     assert info["uv"].grad is not None and info["uv"].grad.shape == (800, 2)
 
 
+def test_uv_grad_is_retained_like_retain_grad(dev):
+    """info["uv"].grad (metal_backend.py:548-549 retains it for the
+    trainer's densification statistics) equals the gradient at uv, sums over
+    repeated backwards as retain_grad does, starts again after a reset, and
+    raises no non-leaf warning."""
+    import warnings
+
+    from metal_gauss_amd import render
+
+    W, H, n = 96, 64, 500
+    s = scene(n=n, seed=12)
+    args = (s["quats"].to(dev), s["scales"].to(dev), s["opacities"].to(dev), None,
+            intrinsics(W, H), torch.eye(4), W, H)
+    m = s["means"].to(dev).requires_grad_(True)
+    # The gradient at uv from a separate render, by torch.autograd.grad.
+    rgb0, _, info0 = render(m, *args, colors=s["colors"].to(dev))
+    (g_ref,) = torch.autograd.grad(rgb0.square().mean(), info0["uv"])
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        rgb, _, info = render(m, *args, colors=s["colors"].to(dev))
+        uv = info["uv"]
+        loss = rgb.square().mean()
+        loss.backward(retain_graph=True)
+        g1 = uv.grad.clone()
+        assert torch.allclose(g1, g_ref, rtol=1e-4, atol=1e-9) and float(g1.abs().max()) > 0
+        loss.backward(retain_graph=True)
+        assert torch.allclose(uv.grad, 2 * g1, rtol=1e-4, atol=1e-9)
+        uv.grad = None
+        loss.backward()
+        assert torch.allclose(uv.grad, g1, rtol=1e-4, atol=1e-9)
+
+
 def test_background_blend_matches_reference(dev):
     W, H = 96, 64
     s = scene(n=400, seed=8)
