@@ -1598,41 +1598,14 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
     }
 }
 
-// {id, depth bits} pairs from ids and the depth array (the radix route, for
-// more tiles than the counting sort takes).
-// (With status, only the kept pairs of capacity-bounded lists.) A thread
-// takes kGatherPer pairs a workgroup-width apart: their ids, then their
-// depths, are requested together (unconditional loads at a clamped index),
-// rather than one id and one dependent depth read at a time.
-constexpr int kGatherPer = 4;
-__global__ __launch_bounds__(256) void gather_depth_pairs_kernel(const int32_t *ids,
-                                                                 const float *depth, int64_t n,
-                                                                 uint2 *pairs,
-                                                                 const int64_t *status) {
-    const int64_t m = status ? lists_kept(status) : n;
-    const int64_t b = (int64_t)blockIdx.x * (256 * kGatherPer) + threadIdx.x;
-    if (b >= m) return;
-    int32_t g[kGatherPer];
-    float d[kGatherPer];
-#pragma unroll
-    for (int j = 0; j < kGatherPer; ++j) g[j] = ids[min(b + 256 * j, m - 1)];
-#pragma unroll
-    for (int j = 0; j < kGatherPer; ++j) d[j] = depth[g[j]];
-#pragma unroll
-    for (int j = 0; j < kGatherPer; ++j)
-        if (b + 256 * j < m) pairs[b + 256 * j] = make_uint2((uint32_t)g[j], __float_as_uint(d[j]));
-}
-
 // Capacity-bounded lists on the radix route: the slots past the kept pairs
-// get a tile key above every tile (they sort last and no list holds them)
-// and id 0.
-__global__ __launch_bounds__(256) void lists_tail_kernel(uint32_t *tiles, int32_t *ids,
-                                                         int64_t capacity,
+// get a tile key above every tile (they sort last and no list holds them;
+// their values are never read).
+__global__ __launch_bounds__(256) void lists_tail_kernel(uint32_t *tiles, int64_t capacity,
                                                          const int64_t *status) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= capacity || i < lists_kept(status)) return;
     tiles[i] = 0xFFFFFFFFu;
-    ids[i] = 0;
 }
 
 // Carves the begin/finish workspace identically on both calls. After begin,
@@ -1689,13 +1662,13 @@ static int64_t finish_sort_bytes(int64_t T, bool capped) {
 // depth, into gauss_ids and tile_offsets. n is the pair count (status NULL),
 // or the capacity of capacity-bounded lists, whose kernels read the pairs to
 // keep from status on the device (none after an overflow: every list empty).
-// Up to kCsBuckets tiles, bin_write emits {id, depth bits} values that the
-// one-pass counting sort carries (and it writes the offsets). Otherwise
-// bin_write emits ids, radix passes sort them into gauss_ids (from the id
-// buffer their last pass will NOT write, so they end there whatever the pass
-// count's parity), tile_ranges writes the offsets, and the depth bits are
-// gathered afterwards; capacity-bounded lists fill the slots past the kept
-// pairs with a tile key above every tile, which the key width then holds.
+// bin_write emits each pair's tile key and its {id, depth bits} value. Up to
+// kCsBuckets tiles the one-pass counting sort carries the values by tile (and
+// writes the offsets); otherwise radix passes on the tile bits carry them
+// (the keys ping-pong through gauss_ids, which only the depth sort writes),
+// and tile_ranges writes the offsets; capacity-bounded lists fill the slots
+// past the kept pairs with a tile key above every tile, which the key width
+// then holds.
 static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
                              const float *depth, int W, int H, int tile, int tiles_x,
                              int n_tiles, int64_t n, const int64_t *status, int32_t *gauss_ids,
@@ -1718,45 +1691,37 @@ static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
     int32_t rc = MG_OK;
     const bool counting = n_tiles <= kCsBuckets;
     const int bits = tile_bits(status ? n_tiles + 1 : n_tiles);
-    const bool even = ((bits + 7) / 8) % 2 == 0;
-    uint32_t *tk_b = (uint32_t *)pairs_a;
-    int32_t *ids_tmp = (int32_t *)((char *)pairs_a + T4);
-    int32_t *ids_a = even ? gauss_ids : ids_tmp;
-    int32_t *ids_b = even ? ids_tmp : gauss_ids;
     {
         TimedScope ts("bin_write", s);
         bin_write_rec_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(
             ws.recs, ws.counts, ws.masks, ws.part_off, N, tile, W, H, tiles_x,
-            conic != nullptr ? 1 : 0, tk_a, counting ? nullptr : ids_a, depth,
-            counting ? pairs_a : nullptr, status);
+            conic != nullptr ? 1 : 0, tk_a, nullptr, depth, pairs_a, status);
         MG_LAUNCHED("bin_write_rec_kernel");
     }
+    // The tile-sorted pairs, and the other region (the long lists' scratch).
+    uint2 *sorted = pairs_b, *scratch = pairs_a;
     if (counting) {
         rc = tile_count_sort<uint2>(tk_a, pairs_a, n, n_tiles, pairs_b, tile_offsets, sort_ws,
                                     sort_bytes, s, status);
         if (rc != MG_OK) return rc;
     } else {
         if (status) {
-            lists_tail_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, s>>>(tk_a, ids_a, n, status);
+            lists_tail_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, s>>>(tk_a, n, status);
             MG_LAUNCHED("lists_tail_kernel");
         }
-        int32_t *rv;
-        rc = radix_sort_passes<uint32_t>(tk_a, ids_a, tk_b, ids_b, n, 0, bits, sort_ws,
-                                         sort_bytes, s, "tile_sort", &res_tiles, &rv, 0u,
-                                         0xFFFFFFFFu, nullptr);
+        rc = radix_sort_passes<uint32_t, uint2>(
+            tk_a, pairs_a, reinterpret_cast<uint32_t *>(gauss_ids), pairs_b, n, 0, bits, sort_ws,
+            sort_bytes, s, "tile_sort", &res_tiles, &sorted, 0u, 0xFFFFFFFFu, nullptr);
         if (rc != MG_OK) return rc;
-        MG_REQUIRE(rv == gauss_ids, "tile lists: ids landed in the wrong buffer");
+        scratch = sorted == pairs_a ? pairs_b : pairs_a;
         {
             TimedScope ts("tile_ranges", s);
             tile_ranges_u32_kernel<<<(unsigned)ceil_div(n + 1, 256), 256, 0, s>>>(
                 res_tiles, n, n_tiles, tile_offsets);
             MG_LAUNCHED("tile_ranges_u32_kernel");
         }
-        gather_depth_pairs_kernel<<<(unsigned)ceil_div(n, 256 * kGatherPer), 256, 0, s>>>(
-            gauss_ids, depth, n, pairs_b, status);
-        MG_LAUNCHED("gather_depth_pairs_kernel");
     }
-    TdArgs D{tile_offsets, pairs_b, pairs_a, gauss_ids};
+    TdArgs D{tile_offsets, sorted, scratch, gauss_ids};
     TimedScope ts("depth_sort", s);
     tile_depth_sort_kernel<<<(unsigned)n_tiles, kTdThreads, 0, s>>>(D);
     MG_LAUNCHED("tile_depth_sort_kernel");
@@ -1858,8 +1823,8 @@ int64_t mg_bin_lists_workspace_bytes(int64_t N) { return BeginWs(nullptr, N > 0 
 
 // Two regions of 8 bytes per pair (the pairs' {id, depth bits} values, and
 // the tile-sorted copy), the pairs' tile keys, then the sort scratch. The
-// radix route (more than kCsBuckets tiles) keeps its second key buffer and
-// id buffer in the first region.
+// radix route (more than kCsBuckets tiles) ping-pongs the values between the
+// two regions and the keys through the caller's gauss_ids.
 int64_t mg_bin_lists_finish_workspace_bytes(int64_t total) {
     const int64_t T = total > 0 ? total : 1;
     return 5 * align256(4 * T) + finish_sort_bytes(T, false);

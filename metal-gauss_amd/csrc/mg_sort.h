@@ -26,17 +26,18 @@ int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *val
                          int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
                          hipStream_t s, const char *who);
 
-// The passes only: the sorted data stays in whichever ping-pong buffer the
+// The passes only, for int32 or uint2 values (uint2: a tile key's
+// {Gaussian id, depth bits}): the sorted data stays in whichever ping-pong buffer the
 // last pass wrote (*res_k, *res_v), saving the final copy when the pass count
 // is even. Digits come from min(key, hi) - lo, so keys known to lie in
 // [lo, hi] sort on bits [0, bit_width(hi - lo)) alone. With dw (device) the
 // window and live bit count are read on the device instead of lo/hi, and
 // passes at or above dw->bits copy the values only: the sorted values are
 // the result, the keys are left unspecified. Instantiated for uint32_t keys.
-template <typename K>
-int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *vals_out,
+template <typename K, typename V>
+int32_t radix_sort_passes(K *keys_in, V *vals_in, K *keys_out, V *vals_out,
                           int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
-                          hipStream_t s, const char *who, K **res_k, int32_t **res_v, K lo,
+                          hipStream_t s, const char *who, K **res_k, V **res_v, K lo,
                           K hi, const DevWin<K> *dw);
 
 // Workspace bytes for an exclusive scan of n int32 values.

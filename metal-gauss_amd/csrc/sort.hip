@@ -1,4 +1,4 @@
-// Stable LSD radix sort of (key, int32 value) pairs, 8-bit digits, tiles of
+// Stable LSD radix sort of (key, value) pairs, 8-bit digits, tiles of
 // 1024 to 4096 keys (large sorts use 4096, so a tile's run of one digit
 // averages 16 keys: 64-byte stores).
 //
@@ -147,15 +147,15 @@ __global__ __launch_bounds__(kSortThreads) void radix_scan_kernel(uint32_t *hist
 // starts an exclusive scan over digits; position in the tile = digit start
 // + wave prefix + rank in wave. Items are thus ranked in tile order (wave,
 // round, lane), which makes every pass stable.
-template <typename K, int kSortItems>
+template <typename K, typename V, int kSortItems>
 __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
-    const K *keys_in, const int32_t *vals_in, K *keys_out, int32_t *vals_out, int64_t n,
+    const K *keys_in, const V *vals_in, K *keys_out, V *vals_out, int64_t n,
     int shift, uint32_t mask, KeyWin<K> win0, const DevWin<K> *dw, const uint32_t *hist,
     int64_t ntiles, const uint32_t *totals) {
     constexpr int kSortTile = kSortThreads * kSortItems;
     constexpr int kChunk = kSortTile / kSortWaves;       // keys per wave
     __shared__ K s_keys[kSortTile];
-    __shared__ int32_t s_vals[kSortTile];
+    __shared__ V s_vals[kSortTile];
     __shared__ uint32_t s_base[kRadix];     // global slot of this tile's digit run
     __shared__ uint32_t s_loc[kRadix];      // start of each digit inside the tile
     __shared__ uint32_t s_wh[kSortWaves][kRadix];   // per-wave digit counts
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     for (int i = lane; i < kRadix; i += 64) s_wh[wave][i] = 0;
 
     K key[kSortItems];
-    int32_t val[kSortItems];
+    V val[kSortItems];
     uint32_t rank[kSortItems];
     const int c0 = wave * kChunk;
 #pragma unroll
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
             val[r] = vals_in[base + idx];
         } else {
             key[r] = 0;
-            val[r] = 0;
+            val[r] = V{};
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -294,10 +294,10 @@ int64_t sort_ws_bytes(int64_t n) {
 
 // Runs the passes; on return *res_k / *res_v point at whichever ping-pong
 // buffer holds the sorted data (keys_out when the pass count is odd).
-template <typename K>
-int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *vals_out,
+template <typename K, typename V>
+int32_t radix_sort_passes(K *keys_in, V *vals_in, K *keys_out, V *vals_out,
                           int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
-                          hipStream_t s, const char *who, K **res_k, int32_t **res_v, K lo,
+                          hipStream_t s, const char *who, K **res_k, V **res_v, K lo,
                           K hi, const DevWin<K> *dw) {
     MG_REQUIRE(n >= 0 && n < (1LL << 31), "%s: n = %lld", who, (long long)n);
     MG_REQUIRE(begin_bit >= 0 && end_bit <= (int)(8 * sizeof(K)) && begin_bit <= end_bit,
@@ -313,7 +313,7 @@ int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *va
     uint32_t *hist = static_cast<uint32_t *>(ws);
     uint32_t *totals = hist + kRadix * ntiles;
     K *src_k = keys_in, *dst_k = keys_out;
-    int32_t *src_v = vals_in, *dst_v = vals_out;
+    V *src_v = vals_in, *dst_v = vals_out;
     MG_REQUIRE(lo <= hi, "%s: empty key window", who);
     const KeyWin<K> win{lo, hi};
     TimedScope ts(who, s);
@@ -327,7 +327,7 @@ int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *va
     radix_scan_kernel<<<kRadix, kSortThreads, 0, s>>>(hist, ntiles, totals, b,             \
                                                       dw ? &dw->bits : nullptr);           \
     MG_LAUNCHED("radix_scan_kernel");                                                      \
-    radix_downsweep_kernel<K, IT><<<(unsigned)ntiles, kSortThreads, 0, s>>>(               \
+    radix_downsweep_kernel<K, V, IT><<<(unsigned)ntiles, kSortThreads, 0, s>>>(            \
         src_k, src_v, dst_k, dst_v, n, b, mask, win, dw, hist, ntiles, totals);            \
     MG_LAUNCHED("radix_downsweep_kernel");
         if (items == 16) { MG_SORT_PASS(16) }
@@ -335,7 +335,7 @@ int32_t radix_sort_passes(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *va
         else { MG_SORT_PASS(4) }
 #undef MG_SORT_PASS
         K *tk = src_k; src_k = dst_k; dst_k = tk;
-        int32_t *tv = src_v; src_v = dst_v; dst_v = tv;
+        V *tv = src_v; src_v = dst_v; dst_v = tv;
     }
     *res_k = src_k;      // after the last swap src_* holds the sorted data
     *res_v = src_v;
@@ -348,7 +348,7 @@ int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *val
                          hipStream_t s, const char *who) {
     K *rk;
     int32_t *rv;
-    int32_t rc = radix_sort_passes<K>(keys_in, vals_in, keys_out, vals_out, n, begin_bit,
+    int32_t rc = radix_sort_passes<K, int32_t>(keys_in, vals_in, keys_out, vals_out, n, begin_bit,
                                       end_bit, ws, ws_bytes, s, who, &rk, &rv, K(0), ~K(0),
                                       nullptr);
     if (rc != MG_OK) return rc;
@@ -363,10 +363,16 @@ template int32_t radix_sort_pairs<uint32_t>(uint32_t *, int32_t *, uint32_t *, i
                                             int, int, void *, int64_t, hipStream_t, const char *);
 template int32_t radix_sort_pairs<uint64_t>(uint64_t *, int32_t *, uint64_t *, int32_t *, int64_t,
                                             int, int, void *, int64_t, hipStream_t, const char *);
-template int32_t radix_sort_passes<uint32_t>(uint32_t *, int32_t *, uint32_t *, int32_t *,
-                                             int64_t, int, int, void *, int64_t, hipStream_t,
-                                             const char *, uint32_t **, int32_t **, uint32_t,
-                                             uint32_t, const DevWin<uint32_t> *);
+template int32_t radix_sort_passes<uint32_t, int32_t>(uint32_t *, int32_t *, uint32_t *,
+                                                      int32_t *, int64_t, int, int, void *,
+                                                      int64_t, hipStream_t, const char *,
+                                                      uint32_t **, int32_t **, uint32_t, uint32_t,
+                                                      const DevWin<uint32_t> *);
+template int32_t radix_sort_passes<uint32_t, uint2>(uint32_t *, uint2 *, uint32_t *, uint2 *,
+                                                    int64_t, int, int, void *, int64_t,
+                                                    hipStream_t, const char *, uint32_t **,
+                                                    uint2 **, uint32_t, uint32_t,
+                                                    const DevWin<uint32_t> *);
 
 }  // namespace mg
 
