@@ -133,7 +133,8 @@ class FusedAdam(torch.optim.Optimizer):
                     "but render(optimizer=) already applied this step's update to it: the "
                     "loss uses it outside the render (a regulariser, for instance). Pass "
                     "the trainer's regularisers to render (opacity_reg=, scale_reg=), or "
-                    "render without optimizer=.")
+                    "render without optimizer=; zero_grad() then step() closes this step "
+                    "without a second update.")
         applied, self._epilogue_applied = self._epilogue_applied, {}
         self._last_stepped = list(applied.values())
         batches: dict[tuple, list] = {}

@@ -263,7 +263,9 @@ def test_step_refuses_a_second_update_after_the_epilogue(dev):
     trainer's regularisers written in torch) reaches them as .grad after the
     epilogue has updated them: step() raises instead of taking a second Adam
     step, and leaves every parameter and step count as the epilogue left
-    them. A second render(optimizer=) before step() raises too."""
+    them, also when it is called again; once the gradients are cleared,
+    step() closes the step without an update. A second render(optimizer=)
+    before step() raises too."""
     from metal_gauss_amd import render
 
     n, W, H = 1000, 96, 80
@@ -278,12 +280,17 @@ def test_step_refuses_a_second_update_after_the_epilogue(dev):
     (rgb.square().mean() + _trainer_reg(p)).backward()
     assert p["logits"].grad is not None and p["means"].grad is None
     after = {k: t.detach().clone() for k, t in p.items()}
-    with pytest.raises(RuntimeError, match="already applied this step's update"):
-        opt.step()
+    for _ in range(2):     # a retried step() is refused again, not applied twice
+        with pytest.raises(RuntimeError, match="already applied this step's update"):
+            opt.step()
+    assert all(torch.equal(after[k], p[k].detach()) for k in p)
+    assert all(opt.state[t]["step"] == 1 for t in p.values())
+    # Without the stray gradients step() closes the step and changes nothing.
+    opt.zero_grad(set_to_none=True)
+    opt.step()
     assert all(torch.equal(after[k], p[k].detach()) for k in p)
     assert all(opt.state[t]["step"] == 1 for t in p.values())
 
-    opt.zero_grad(set_to_none=True)
     for it in range(2):
         rgb, _, _ = render(p["means"], p["quats"], p["log_scales"], p["logits"], p["sh_dc"], K,
                            vm, W, H, sh_degree=3, sh_rest=p["sh_rest"], activations=True,
