@@ -867,13 +867,35 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
     }
 }
 
+// Offsets of sorted tile keys: offsets[t] = the first i with tiles[i] >= t
+// (n for t past the last key). A thread takes kRangePer consecutive keys,
+// read as two 16-byte loads, and the key before them; at a change of key
+// from a to b at position i it writes offsets[a + 1 .. b] = i.
+constexpr int kRangePer = 8;
 __global__ __launch_bounds__(256) void tile_ranges_u32_kernel(const uint32_t *tiles, int64_t n,
                                                               int32_t n_tiles, int32_t *offsets) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i > n) return;
-    const int64_t prev = i == 0 ? -1 : (int64_t)tiles[i - 1];
-    const int64_t cur = i == n ? (int64_t)n_tiles : (int64_t)tiles[i];
-    for (int64_t t = prev + 1; t <= cur && t <= n_tiles; ++t) offsets[t] = (int32_t)i;
+    const int64_t b = ((int64_t)blockIdx.x * 256 + threadIdx.x) * kRangePer;
+    if (b > n) return;
+    int64_t key[kRangePer + 1];   // key[j] is tiles[b + j - 1]; -1 before the first
+    key[0] = b == 0 ? -1 : (int64_t)tiles[b - 1];
+    if (b + kRangePer <= n && ((reinterpret_cast<uintptr_t>(tiles + b) & 15) == 0)) {
+        const uint4 q0 = *reinterpret_cast<const uint4 *>(tiles + b);
+        const uint4 q1 = *reinterpret_cast<const uint4 *>(tiles + b + 4);
+        key[1] = q0.x; key[2] = q0.y; key[3] = q0.z; key[4] = q0.w;
+        key[5] = q1.x; key[6] = q1.y; key[7] = q1.z; key[8] = q1.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < kRangePer; ++j)
+            key[j + 1] = b + j < n ? (int64_t)tiles[b + j] : (int64_t)n_tiles;
+    }
+#pragma unroll
+    for (int j = 0; j < kRangePer; ++j) {
+        const int64_t i = b + j;
+        if (i > n) break;
+        // Position n closes every tile after the last key.
+        const int64_t cur = i == n ? (int64_t)n_tiles : key[j + 1];
+        for (int64_t t = key[j] + 1; t <= cur && t <= n_tiles; ++t) offsets[t] = (int32_t)i;
+    }
 }
 
 inline int tile_bits(int n_tiles) {
@@ -1716,7 +1738,7 @@ static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
         scratch = sorted == pairs_a ? pairs_b : pairs_a;
         {
             TimedScope ts("tile_ranges", s);
-            tile_ranges_u32_kernel<<<(unsigned)ceil_div(n + 1, 256), 256, 0, s>>>(
+            tile_ranges_u32_kernel<<<(unsigned)ceil_div(n + 1, 256 * kRangePer), 256, 0, s>>>(
                 res_tiles, n, n_tiles, tile_offsets);
             MG_LAUNCHED("tile_ranges_u32_kernel");
         }
