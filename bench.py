@@ -161,6 +161,9 @@ class Step:
         ], eps=1e-15)
         self.targets = [scenes.config4_target(v).to(dev) for v in range(len(cams))]
         self.window = gaussian_kernel(device=dev, groups=15)
+        # d loss / d loss, allocated once: loss.backward() would fill a new
+        # one every step (a kernel launch of its own).
+        self.seed = torch.ones((), device=dev)
         g = torch.Generator().manual_seed(3)
         self.order = torch.randperm(len(cams), generator=g).tolist()
         self.k = 0
@@ -263,7 +266,7 @@ class Step:
             # is already in render's backward.
             loss = loss + info["regularizer"]()
         self.opt.zero_grad(set_to_none=True)
-        loss.backward()
+        loss.backward(self.seed)
         if adam:
             self.opt.step(skip=info["lists_status"])
         self.last_valid = info["valid_mask"]
@@ -960,7 +963,8 @@ def pmc_summary(fetch_dir, write_dir, copy_mib):
 
 COUNTER_REGEX = ("raster_bwd|raster_fwd|adam_multi|preprocess_fwd|preprocess_bwd|scan_|"
                  "bin_write|bin_count|bin_offsets|count_hist|count_colscan|count_scatter|"
-                 "tile_depth_sort|ssim_fused|photometric_loss|stream_copy|copyBuffer")
+                 "tile_depth_sort|radix_|tile_ranges|ssim_fused|photometric_loss|stream_copy|"
+                 "copyBuffer")
 
 
 def _kernel_base(name):
@@ -971,8 +975,9 @@ def _kernel_base(name):
     return n.split("::")[-1]
 
 
-def counter_summary(dirs, copy_mib=1024):
-    """Per-kernel table from rocprofv3 runs of the config-4 step: one
+def counter_summary(dirs, copy_mib=1024, config=None, crowded=False):
+    """Per-kernel table from rocprofv3 runs of the config-4 step (or, with
+    config 5, its fwd + bwd, crowded or not): one
     --kernel-trace --stats run (kernel_stats.csv) and --pmc passes (one
     *counter_collection.csv each). Counters are averaged over a kernel's
     dispatches; FETCH_SIZE and WRITE_SIZE are calibrated by the run's own
@@ -1036,10 +1041,20 @@ def counter_summary(dirs, copy_mib=1024):
             f"{fmt(li, 9, 2, 1e-6)} {fmt(bcp, 9, 2)} {fmt(wp, 6, 1)} "
             f"{fmt(at if at else None, 9, 2, 1e-6)} {fmt(rd, 9, 1, 1e-6)} {fmt(wr, 9, 1, 1e-6)} "
             f"{fmt(gbs, 8, 0)}")
+    if config == 5:
+        what = ("config 5 crowded: forward + L1 + backward, 3.6M Gaussians SH3, 1920x1080, "
+                "over 30M intersections" if crowded else
+                "config 5: forward + L1 + backward, 3M Gaussians SH3, 1920x1080")
+        bflag = "--config 5 --crowded --steps 3" if crowded else "--config 5 --steps 3"
+        sflag = " --config 5 --crowded" if crowded else " --config 5"
+    else:
+        what = "config-4 step (1M Gaussians SH3, 800x800, tile 16)"
+        bflag = "--steps 3 --warmup 2 --no-cpu-baseline --ramp 0"
+        sflag = ""
     notes = [
-        "# Per-kernel counters, config-4 step (1M Gaussians SH3, 800x800, tile 16), MI355X",
-        "# made by (from the repository root; TMPDIR=/tmp; B='bench.py --steps 3 --warmup 2",
-        "#   --no-cpu-baseline --ramp 0 --copy-mib 1024'; R = the --kernel-include-regex",
+        f"# Per-kernel counters, {what}, MI355X",
+        f"# made by (from the repository root; TMPDIR=/tmp; B='bench.py {bflag}",
+        "#   --copy-mib 1024'; R = the --kernel-include-regex",
         f"#   '{COUNTER_REGEX}'):",
         "#   rocprofv3 --kernel-trace --stats -f csv -T -d KT -o kt -- python3 -u $B",
         "#   rocprofv3 --pmc <pass> --kernel-include-regex $R -f csv -T -d P<i> -o pmc -- "
@@ -1048,7 +1063,7 @@ def counter_summary(dirs, copy_mib=1024):
         "#   SQ_ACTIVE_INST_LDS SQ_WAIT_INST_ANY SQ_WAVE_CYCLES GRBM_GUI_ACTIVE', P2 VALUBusy,",
         "#   P3 MeanOccupancyPerCU, P4 'TCP_TCC_ATOMIC_WITH_RET_REQ_sum",
         "#   TCP_TCC_ATOMIC_WITHOUT_RET_REQ_sum', P5 FETCH_SIZE, P6 WRITE_SIZE; then",
-        "#   python bench.py --counter-summary KT P1 P2 P3 P4 P5 P6 --copy-mib 1024",
+        f"#   python bench.py --counter-summary KT P1 P2 P3 P4 P5 P6 --copy-mib 1024{sflag}",
         "# columns: avg_us from the kernel trace; VGPR and LDS bytes per workgroup as",
         "#   rocprofv3 reports them; occ_w/CU = MeanOccupancyPerCU (waves resident per CU);",
         "#   VALUbusy% = VALUBusy; VALU_Minst = SQ_INSTS_VALU (wave instructions) per",
@@ -1062,7 +1077,8 @@ def counter_summary(dirs, copy_mib=1024):
     return "\n".join(notes + lines)
 
 
-def stats_summary(stats_csv, steps, variant="base", mcmc=False, config=None, render_fps=False):
+def stats_summary(stats_csv, steps, variant="base", mcmc=False, config=None, render_fps=False,
+                  crowded=False):
     """Text summary of a rocprofv3 --kernel-trace --stats kernel_stats.csv."""
     import csv
 
@@ -1074,12 +1090,17 @@ def stats_summary(stats_csv, steps, variant="base", mcmc=False, config=None, ren
                 2: "config 2: forward + L1 + backward, 300k Gaussians SH3, 800x800",
                 3: "config 3: FusedAdam and SelectiveAdam over 1M Gaussians x 59 floats",
                 5: "config 5: forward + L1 + backward, 3M Gaussians SH3, 1920x1080"}[config]
+        cflag = f"--config {config}"
+        if crowded:
+            what = ("config 5 crowded: forward + L1 + backward, 3.6M Gaussians SH3, 1920x1080, "
+                    "over 30M intersections")
+            cflag += " --crowded"
         lines = [
             f"# rocprofv3 kernel statistics, {what}, MI355X",
             "# made by (from the repository root, TMPDIR=/tmp):",
             "#   rocprofv3 --kernel-trace --stats -f csv -T -d P -o kt -- python -u bench.py "
-            f"--config {config} --steps {steps}",
-            f"#   python bench.py --stats-summary P/kt_kernel_stats.csv --config {config}",
+            f"{cflag} --steps {steps}",
+            f"#   python bench.py --stats-summary P/kt_kernel_stats.csv {cflag}",
         ]
     elif render_fps:
         lines = [
@@ -1300,11 +1321,12 @@ def main():
         print(pmc_summary(*args.pmc_summary, args.copy_mib or 1024))
         return
     if args.counter_summary:
-        print(counter_summary(args.counter_summary, args.copy_mib or 1024))
+        print(counter_summary(args.counter_summary, args.copy_mib or 1024, args.config,
+                              args.crowded))
         return
     if args.stats_summary:
         print(stats_summary(args.stats_summary, args.steps if args.config else 20,
-                            args.variant, args.mcmc, args.config, args.render_fps))
+                            args.variant, args.mcmc, args.config, args.render_fps, args.crowded))
         return
     if args.cpu_only:
         print(json.dumps(cpu_baseline(args.gaussians, crop=_cpu_crop())))
