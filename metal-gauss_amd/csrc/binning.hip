@@ -1416,112 +1416,105 @@ __device__ __forceinline__ void td_slots(TdShared &S, uint32_t *tot, const uint3
 // to whole rounds of 64.
 __device__ __forceinline__ int td_part(int len) { return ((len + 4 * 64 - 1) / (4 * 64)) * 64; }
 
-__global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArgs A) {
-    __shared__ TdShared S;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t = (int)xcd_contiguous(blockIdx.x, gridDim.x);
-    const int64_t s0 = A.offsets[t];
-    const int64_t len = (int64_t)A.offsets[t + 1] - s0;
-    if (len <= 0) return;   // workgroup-uniform
-    const uint2 *in = A.pairs + s0;
-    if (len == 1) {
-        if (tid == 0) A.ids[s0] = (int32_t)in[0].x;
-        return;
-    }
+// Clears every wave's lane masks. They share storage with the exchange
+// buffer, which every wave may just have read: those reads must have
+// returned before any wave clears the words (a barrier alone does not wait
+// for LDS reads whose values are first used after it).
+__device__ __forceinline__ void td_clear_masks(TdShared &S) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    lds_reads_done();
+    __syncthreads();
 #pragma unroll
     for (int j = 0; j < 4; ++j) S.u.mask[wave][lane + 64 * j] = 0ull;
+}
 
-    if (len <= kTdCap) {
-        const int part = td_part((int)len), rounds = part / 64;
-        const int pb = wave * part + lane;   // entry of round r: pb + 64 r
-        const uint32_t *in_key = reinterpret_cast<const uint32_t *>(in) + 1;
-        uint32_t k[kTdPer], rank[kTdPer];
-        uint32_t valid = 0, kmin = 0xFFFFFFFFu, kmax = 0u;
+// Sorts the len (2..kTdCap) entries at in by key, stably, in registers and
+// LDS (see above), and writes their ids in sorted order to out. Returns
+// false, having written nothing, when the keys span more than kTdKeyBits + 8
+// bits. Workgroup-uniform. masks_clear: the lane masks are known zero (at
+// the start of a workgroup, each wave having cleared its own), so the first
+// pass need not clear them behind a barrier.
+__device__ __forceinline__ bool td_fast(TdShared &S, const uint2 *in, int len, int32_t *out,
+                                        bool masks_clear) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int part = td_part(len), rounds = part / 64;
+    const int pb = wave * part + lane;   // entry of round r: pb + 64 r
+    const uint32_t *in_key = reinterpret_cast<const uint32_t *>(in) + 1;
+    uint32_t k[kTdPer], rank[kTdPer];
+    uint32_t valid = 0, kmin = 0xFFFFFFFFu, kmax = 0u;
+#pragma unroll
+    for (int r = 0; r < kTdPer; ++r) {
+        const int i = pb + 64 * r;
+        const bool ok = r < rounds && i < len && 64 * r < part;
+        const uint32_t ka = in_key[2 * min(i, len - 1)];
+        k[r] = ok ? ka : 0u;
+        valid |= ok ? 1u << r : 0u;
+        kmin = min(kmin, ok ? ka : 0xFFFFFFFFu);
+        kmax = max(kmax, k[r]);
+    }
+    td_minmax(kmin, kmax, S.red);
+    const uint32_t span = kmax - kmin;
+    const int bits = span == 0u ? 0 : 32 - __builtin_clz(span);
+    if (bits > kTdKeyBits + 8) return false;   // workgroup-uniform
+    // First pass: k is the key less kmin; later passes: k is the exchanged
+    // word, the entry's list index over its key bits left.
+#pragma unroll
+    for (int r = 0; r < kTdPer; ++r) k[r] = ((valid >> r) & 1u) ? k[r] - kmin : 0u;
+    for (int shift = 0; shift < bits; shift += 8) {
+        if (shift > 0 || !masks_clear) td_clear_masks(S);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) S.wh[wave][lane + 64 * j] = 0;
+        __syncthreads();
+        uint32_t d[kTdPer];
+#pragma unroll
+        for (int r = 0; r < kTdPer; ++r) d[r] = k[r] & 255u;
+        td_rank(d, valid, rounds, rank, S.wh[wave], S.u.mask[wave]);
+        __syncthreads();
+        td_slots(S, nullptr, nullptr);
+        __syncthreads();
+        const bool last = shift + 8 >= bits;
 #pragma unroll
         for (int r = 0; r < kTdPer; ++r) {
-            const int i = pb + 64 * r;
-            const bool ok = r < rounds && i < len && 64 * r < part;
-            const uint32_t ka = in_key[2 * min(i, (int)len - 1)];
-            k[r] = ok ? ka : 0u;
-            valid |= ok ? 1u << r : 0u;
-            kmin = min(kmin, ok ? ka : 0xFFFFFFFFu);
-            kmax = max(kmax, k[r]);
-        }
-        td_minmax(kmin, kmax, S.red);
-        const uint32_t span = kmax - kmin;
-        const int bits = span == 0u ? 0 : 32 - __builtin_clz(span);
-        if (bits <= kTdKeyBits + 8) {   // workgroup-uniform
-            // First pass: k is the key less kmin; later passes: k is the
-            // exchanged word, the entry's list index over its key bits left.
-#pragma unroll
-            for (int r = 0; r < kTdPer; ++r) k[r] = ((valid >> r) & 1u) ? k[r] - kmin : 0u;
-            for (int shift = 0; shift < bits; shift += 8) {
-                if (shift > 0) {
-                    // The masks share storage with the words every wave has
-                    // just read back; those reads must have returned before
-                    // any wave clears them. A barrier alone does not wait for
-                    // LDS reads whose values are first used after it, and
-                    // another wave's writes may then overtake them.
-                    lds_reads_done();
-                    __syncthreads();
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) S.u.mask[wave][lane + 64 * j] = 0ull;
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) S.wh[wave][lane + 64 * j] = 0;
-                __syncthreads();
-                uint32_t d[kTdPer];
-#pragma unroll
-                for (int r = 0; r < kTdPer; ++r) d[r] = k[r] & 255u;
-                td_rank(d, valid, rounds, rank, S.wh[wave], S.u.mask[wave]);
-                __syncthreads();
-                td_slots(S, nullptr, nullptr);
-                __syncthreads();
-                const bool last = shift + 8 >= bits;
-#pragma unroll
-                for (int r = 0; r < kTdPer; ++r) {
-                    if ((valid >> r) & 1u) {
-                        const uint32_t pos = S.wh[wave][d[r]] + rank[r];
-                        const uint32_t idx = shift == 0 ? (uint32_t)(pb + 64 * r)
-                                                        : k[r] >> kTdKeyBits;
-                        const uint32_t rest = (shift == 0 ? k[r] : k[r] & kTdKeyMask) >> 8;
-                        // After the last pass only the index is needed.
-                        S.u.xk[pos] = last ? idx : (idx << kTdKeyBits) | rest;
-                    }
-                }
-                __syncthreads();
-                if (last) break;
-#pragma unroll
-                for (int r = 0; r < kTdPer; ++r)
-                    if ((valid >> r) & 1u) k[r] = S.u.xk[pb + 64 * r];
+            if ((valid >> r) & 1u) {
+                const uint32_t pos = S.wh[wave][d[r]] + rank[r];
+                const uint32_t idx = shift == 0 ? (uint32_t)(pb + 64 * r) : k[r] >> kTdKeyBits;
+                const uint32_t rest = (shift == 0 ? k[r] : k[r] & kTdKeyMask) >> 8;
+                // After the last pass only the index is needed.
+                S.u.xk[pos] = last ? idx : (idx << kTdKeyBits) | rest;
             }
-            if (bits == 0) {   // one key: the list order stands
-                __syncthreads();
-                for (int i = tid; i < len; i += kTdThreads) S.u.xk[i] = (uint32_t)i;
-                __syncthreads();
-            }
-            // S.u.xk[i]: the list index of the entry at sorted position i.
-            // Past len a lane rewrites the last position with its own value.
-            uint32_t ix[kTdPer];
-            int32_t id[kTdPer];
-#pragma unroll
-            for (int j = 0; j < kTdPer; ++j) ix[j] = S.u.xk[min(tid + kTdThreads * j, (int)len - 1)];
-#pragma unroll
-            for (int j = 0; j < kTdPer; ++j) id[j] = (int32_t)in[ix[j]].x;
-#pragma unroll
-            for (int j = 0; j < kTdPer; ++j)
-                A.ids[s0 + min(tid + kTdThreads * j, (int)len - 1)] = id[j];
-            return;
         }
-        // Keys spanning more bits take the chunked passes below.
+        __syncthreads();
+        if (last) break;
+#pragma unroll
+        for (int r = 0; r < kTdPer; ++r)
+            if ((valid >> r) & 1u) k[r] = S.u.xk[pb + 64 * r];
+    }
+    if (bits == 0) {   // one key: the list order stands
+        __syncthreads();
+        for (int i = tid; i < len; i += kTdThreads) S.u.xk[i] = (uint32_t)i;
         __syncthreads();
     }
+    // S.u.xk[i]: the list index of the entry at sorted position i. Past len
+    // a lane rewrites the last position with its own value.
+    uint32_t ix[kTdPer];
+    int32_t id[kTdPer];
+#pragma unroll
+    for (int j = 0; j < kTdPer; ++j) ix[j] = S.u.xk[min(tid + kTdThreads * j, len - 1)];
+#pragma unroll
+    for (int j = 0; j < kTdPer; ++j) id[j] = (int32_t)in[ix[j]].x;
+#pragma unroll
+    for (int j = 0; j < kTdPer; ++j) out[min(tid + kTdThreads * j, len - 1)] = id[j];
+    return true;
+}
 
-    // Longer lists: key range, then passes over chunks of kTdCap in order,
-    // ping-ponging between the input pairs and pairs_b.
+// Workgroup min and max of the len keys at in.
+__device__ __forceinline__ void td_key_range(TdShared &S, const uint2 *in, int64_t len,
+                                             uint32_t &kmin, uint32_t &kmax) {
+    const int tid = threadIdx.x;
+    kmin = 0xFFFFFFFFu;
+    kmax = 0u;
     // The list is read kTdBatch entries per thread at a time, the loads
     // unconditional (clamped index) so that a batch is in flight at once.
-    uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
     for (int64_t b = 0; b < len; b += (int64_t)kTdThreads * kTdBatch) {
         uint32_t kk[kTdBatch];
 #pragma unroll
@@ -1535,11 +1528,21 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
         }
     }
     td_minmax(kmin, kmax, S.red);
-    const uint32_t span = kmax - kmin;
-    const int bits = span == 0u ? 0 : 32 - __builtin_clz(span);
-    uint2 *pin = A.pairs + s0, *pout = A.pairs_b + s0;
-    for (int shift = 0; shift < bits; shift += 8) {
-        // Digit totals over the list -> the running digit starts S.run.
+}
+
+// Stable LSD passes of 8 bits over the len entries at pin, digits of
+// (key - kmin) from bit shift0 up to bit end, in chunks of kTdCap through
+// global memory: per pass the digit totals over the list, their scan into
+// running starts (S.run), and the chunks in order, each ranked by its waves
+// and scattered to the other buffer. With starts, the first pass's digit
+// starts are also copied there (256 + 1 entries). Returns the buffer holding
+// the result (pin or pout).
+__device__ __forceinline__ uint2 *td_lsd_passes(TdShared &S, uint2 *pin, uint2 *pout,
+                                                int64_t len, uint32_t kmin, int shift0,
+                                                int end, uint32_t *starts) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int shift = shift0; shift < end; shift += 8) {
+        td_clear_masks(S);
         S.tot[tid] = 0;
         __syncthreads();
         for (int64_t b = 0; b < len; b += (int64_t)kTdThreads * kTdBatch) {
@@ -1566,6 +1569,10 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
             uint32_t start = incl - cnt;
             for (int w = 0; w < wave; ++w) start += S.red[w];
             S.run[tid] = start;
+            if (starts && shift == shift0) {
+                starts[tid] = start;
+                if (tid == kTdThreads - 1) starts[256] = start + cnt;
+            }
         }
         for (int64_t c0 = 0; c0 < len; c0 += kTdCap) {
             const int cl = (int)min((int64_t)kTdCap, len - c0);
@@ -1608,16 +1615,100 @@ __global__ __launch_bounds__(kTdThreads) void tile_depth_sort_kernel(const TdArg
         pin = pout;
         pout = tp;
     }
+    return pin;
+}
+
+// The ids of the len entries at in, in order, to out.
+__device__ __forceinline__ void td_write_ids(const uint2 *in, int64_t len, int32_t *out) {
+    const int tid = threadIdx.x;
     // Past the end a lane rewrites the last entry with its own value.
     for (int64_t b = 0; b < len; b += (int64_t)kTdThreads * kTdBatch) {
         uint32_t id[kTdBatch];
 #pragma unroll
-        for (int j = 0; j < kTdBatch; ++j)
-            id[j] = pin[min(b + tid + (int64_t)kTdThreads * j, len - 1)].x;
+        for (int j = 0; j < kTdBatch; ++j) id[j] = in[min(b + tid + (int64_t)kTdThreads * j, len - 1)].x;
 #pragma unroll
         for (int j = 0; j < kTdBatch; ++j)
-            A.ids[s0 + min(b + tid + (int64_t)kTdThreads * j, len - 1)] = (int32_t)id[j];
+            out[min(b + tid + (int64_t)kTdThreads * j, len - 1)] = (int32_t)id[j];
     }
+}
+
+// Lists the fast path does not take: longer than kTdCap, or keys spanning
+// more than kTdKeyBits + 8 bits. One LSD pass on the top 8 of the key bits
+// (through global memory, into pairs_b) groups the list into up to 256
+// buckets of consecutive key ranges, stably; runs of whole buckets of up to
+// kTdCap entries are then sorted by the fast path, each its own segment of
+// the ids (a bucket of more than kTdCap entries, or a run whose keys still
+// span too many bits, takes the LSD passes on its own). Against LSD passes
+// over the whole list this reads and writes the list through global memory
+// once instead of once per 8 key bits. Not inlined: the kernel reaches it
+// rarely, and inlined its registers made the fast path spill.
+__device__ __noinline__ void td_long(TdShared &S, const TdArgs A, int64_t s0, int64_t len) {
+    const int tid = threadIdx.x;
+    __shared__ uint32_t s_starts[257];
+    uint2 *in = A.pairs + s0, *tmp = A.pairs_b + s0;
+    int32_t *out = A.ids + s0;
+    uint32_t kmin, kmax;
+    td_key_range(S, in, len, kmin, kmax);
+    const uint32_t span = kmax - kmin;
+    const int bits = span == 0u ? 0 : 32 - __builtin_clz(span);
+    if (bits <= 8) {
+        td_write_ids(td_lsd_passes(S, in, tmp, len, kmin, 0, bits, nullptr), len, out);
+        return;
+    }
+    // in -> tmp, grouped by the digit of bits [bits - 8, bits).
+    td_lsd_passes(S, in, tmp, len, kmin, bits - 8, bits, s_starts);
+    __syncthreads();
+    // Runs of whole buckets [b, e): every thread walks the same bucket
+    // starts, so the loop is workgroup-uniform.
+    int64_t b = 0;
+    for (int dg = 0; dg <= 256; ++dg) {
+        const int64_t e = s_starts[dg];   // end of bucket dg - 1
+        const int64_t nxt = dg < 256 ? (int64_t)s_starts[dg + 1] : e;
+        // Close the run before bucket dg if bucket dg would overfill it (or
+        // at the end).
+        if (dg == 256 || (nxt - b > kTdCap && e > b)) {
+            const int64_t n = e - b;
+            if (n == 1) {
+                if (tid == 0) out[b] = (int32_t)tmp[b].x;
+            } else if (n > 1) {
+                if (n > kTdCap || !td_fast(S, tmp + b, (int)n, out + b, false)) {
+                    // The run's own key range and LSD passes; the input region
+                    // of the list is free scratch by now.
+                    uint32_t rmin, rmax;
+                    td_key_range(S, tmp + b, n, rmin, rmax);
+                    const uint32_t rs = rmax - rmin;
+                    const int rb = rs == 0u ? 0 : 32 - __builtin_clz(rs);
+                    td_write_ids(td_lsd_passes(S, tmp + b, in + b, n, rmin, 0, rb, nullptr), n,
+                                 out + b);
+                }
+            }
+            __syncthreads();
+            b = e;
+        }
+    }
+}
+
+// Four workgroups per CU: at most 128 VGPRs.
+__global__ __launch_bounds__(kTdThreads) __attribute__((amdgpu_waves_per_eu(4))) void
+tile_depth_sort_kernel(const TdArgs A) {
+    __shared__ TdShared S;
+    const int tid = threadIdx.x;
+    const int t = (int)xcd_contiguous(blockIdx.x, gridDim.x);
+    const int64_t s0 = A.offsets[t];
+    const int64_t len = (int64_t)A.offsets[t + 1] - s0;
+    if (len <= 0) return;   // workgroup-uniform
+    const uint2 *in = A.pairs + s0;
+    if (len == 1) {
+        if (tid == 0) A.ids[s0] = (int32_t)in[0].x;
+        return;
+    }
+    {
+        const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) S.u.mask[wave][lane + 64 * j] = 0ull;
+    }
+    if (len <= kTdCap && td_fast(S, in, (int)len, A.ids + s0, true)) return;
+    td_long(S, A, s0, len);
 }
 
 // Capacity-bounded lists on the radix route: the slots past the kept pairs

@@ -207,6 +207,40 @@ def test_depth_ties_and_long_tile_lists_bit_exact(dev, crowd):
     assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
 
 
+@pytest.mark.parametrize("seed", [51, 52])
+def test_long_lists_crowding_one_depth_bucket_bit_exact(dev, seed):
+    """Lists of over 4096 entries are first grouped by the top 8 of their key
+    bits, and runs of whole groups are sorted as short lists. Here most of a
+    list sits at one depth (3.0 plus under 1e-4) with a few splats far in
+    front and behind (depths 0.05 to 90: a 27-bit key span), so one group
+    holds more than 4096 entries and takes the long passes on its own, and
+    a fifth of the splats are exact copies of others (depth ties, id order);
+    the lists must equal the oracle's."""
+    N, W, H, f = 12000, 64, 48, 200.0
+    g = torch.Generator().manual_seed(seed)
+    z = 3.0 + torch.rand(N, generator=g) * 1e-4
+    far = torch.randperm(N, generator=g)[:600]
+    z[far] = torch.exp(torch.rand(600, generator=g) * (math.log(90.0) - math.log(0.05))
+                       + math.log(0.05))
+    uv = (torch.rand(N, 2, generator=g) - 0.5) * torch.tensor([20.0, 16.0])
+    means = torch.stack([uv[:, 0] * z / f, uv[:, 1] * z / f, z], 1)
+    quats = torch.randn(N, 4, generator=g)
+    scales = (z * 2.0 / f)[:, None] * (torch.rand(N, 3, generator=g) + 0.5)
+    op = torch.rand(N, generator=g) * 0.9 + 0.05
+    src = torch.randint(0, N, (N // 5,), generator=g)
+    dst = torch.randperm(N, generator=g)[:N // 5]
+    for t in (means, quats, scales, op):
+        t[dst] = t[src]
+    s = dict(means=means, quats=quats, scales=scales, op=op, sh=torch.zeros(N, 16, 3),
+             W=W, H=H, f=f)
+    gpu, ref = run_both(s, dev, 16)
+    lens = np.diff(gpu[1])
+    assert lens.max() > 4096, lens.max()
+    assert np.array_equal(gpu[3], ref[3]), "sorted keys differ"
+    assert np.array_equal(gpu[0], ref[0]), "gauss_ids differ"
+    assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
+
+
 def test_lists_over_2048_entries_with_four_passes_bit_exact(dev):
     """Every tile's list between 2048 and 4096 entries (one workgroup, its
     four waves' quarters past the 2048 LDS words the lane masks share with the

@@ -14,8 +14,9 @@ The check compiles every source to gfx950 assembly with the library's own
 flags and runs a dataflow pass over each kernel's control-flow graph: the
 number of LDS reads (``ds_read*``/``ds_load*``) issued since the last
 ``s_waitcnt lgkmcnt(n)`` that covers them, maximised over paths, must be
-zero at every ``s_barrier``. It is pinned by the depth sort built without its
-wait, which the pass must flag. CPU only: hipcc cross-compiles here.
+zero at every ``s_barrier``. It is pinned by a planted kernel with the race
+(flagged) and the same kernel with the wait (not flagged). CPU only: hipcc
+cross-compiles here.
 """
 
 from __future__ import annotations
@@ -159,17 +160,37 @@ def test_no_barrier_waits_on_outstanding_lds_reads(assembly):
     assert not bad, "barriers reached with LDS reads outstanding:\n" + "\n".join(bad)
 
 
-def test_the_check_flags_the_depth_sort_without_its_wait(tmp_path):
-    """The planted mistake: binning.hip with the depth sort's lds_reads_done()
-    call taken out must be flagged at that kernel's barrier."""
-    b = _build_module()
-    text = (b.CSRC / "binning.hip").read_text()
-    planted, n = re.subn(r"^(\s*)lds_reads_done\(\);$", r"\1/* wait removed */", text,
-                         flags=re.M)
-    assert n >= 1
-    src = tmp_path / "binning_nowait.hip"
-    src.write_text(planted)
-    funcs = _functions(_assemble(src, tmp_path / "binning_nowait.s", "binning.hip"))
-    sort_fn = [f for f in funcs if "tile_depth_sort" in f]
-    assert sort_fn
-    assert any(any(pending_reads_at_barriers(funcs[f])) for f in sort_fn)
+# The hazard in its smallest form: each iteration a wave reads a word that
+# another wave wrote, and first uses the value after the next iteration's
+# barrier, behind which the word is rewritten. WAIT is empty (the race) or a
+# wait for the wave's LDS reads before that barrier (the fix).
+PLANTED = r"""
+#include <hip/hip_runtime.h>
+__device__ __forceinline__ void lds_reads_done() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+extern "C" __global__ void __launch_bounds__(256) planted(const float *in, float *out, int n) {
+    __shared__ float s[256];
+    float v = 0.f;
+    for (int it = 0; it < n; ++it) {
+        WAIT
+        __syncthreads();
+        s[threadIdx.x] = in[it * 256 + threadIdx.x] + v;
+        __syncthreads();
+        v = s[255 - threadIdx.x];
+    }
+    out[threadIdx.x] = v;
+}
+"""
+
+
+@pytest.mark.parametrize("wait,flagged", [("", True), ("lds_reads_done();", False)])
+def test_the_check_flags_a_read_first_used_after_the_next_barrier(tmp_path, wait, flagged):
+    """The planted mistake (a loop whose LDS read is used after the next
+    barrier) is flagged at that barrier; with the wave's reads waited for
+    before it, it is not."""
+    src = tmp_path / "planted.hip"
+    src.write_text(PLANTED.replace("WAIT", wait))
+    funcs = _functions(_assemble(src, tmp_path / "planted.s", "planted.hip"))
+    assert "planted" in funcs
+    assert any(pending_reads_at_barriers(funcs["planted"])) == flagged
