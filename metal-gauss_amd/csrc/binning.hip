@@ -214,12 +214,18 @@ constexpr int kWaveWalkArea = 32;
 constexpr int kRowSlots = 128;
 static_assert(kRowSlots * 16 == 64 * kWaveWalkArea, "the row slice aliases the small-claim bytes");
 
-template <class Step>
-__device__ __forceinline__ void strip_walk(const BinRec &r, bool test, int tile, int W, int H,
-                                           float4 *rows, int lane, Step &&step) {
-#pragma clang fp contract(off)
-    const int x0 = (int)(r.xs & 0xffffu), y0 = (int)(r.ys & 0xffffu);
-    const int w = (int)(r.xs >> 16) - x0 + 1, h = (int)(r.ys >> 16) - y0 + 1;
+// The shape of a wave's walk over one large rectangle: ns strips of s
+// columns, each nr steps of R rows; lane = row group rg * s + column cl.
+// A function of the rectangle's size alone, so the count and write passes
+// step through a rectangle identically.
+struct StripPlan {
+    int R, s, ns, nr, rg, cl;
+    bool lane_ok;
+};
+
+__device__ __forceinline__ StripPlan strip_plan(const BinRec &r, int lane) {
+    const int w = (int)(r.xs >> 16) - (int)(r.xs & 0xffffu) + 1;
+    const int h = (int)(r.ys >> 16) - (int)(r.ys & 0xffffu) + 1;
     // Lane l prices R = l + 1 rows a step (strips of min(w, 64 / R)
     // columns); the wave takes the fewest steps, the smallest R on ties.
     uint64_t key;
@@ -232,11 +238,26 @@ __device__ __forceinline__ void strip_walk(const BinRec &r, bool test, int tile,
             key = t < key ? t : key;
         }
     }
-    const int R = __builtin_amdgcn_readfirstlane((int)(key & 63u)) + 1;
-    const int s = min(w, 64 / R);
-    const int ns = (w + s - 1) / s, nr = (h + R - 1) / R;
-    const int rg = lane / s, cl = lane - rg * s;
-    const bool lane_ok = lane < R * s;
+    StripPlan P;
+    P.R = __builtin_amdgcn_readfirstlane((int)(key & 63u)) + 1;
+    P.s = min(w, 64 / P.R);
+    P.ns = (w + P.s - 1) / P.s;
+    P.nr = (h + P.R - 1) / P.R;
+    P.rg = lane / P.s;
+    P.cl = lane - P.rg * P.s;
+    P.lane_ok = lane < P.R * P.s;
+    return P;
+}
+
+template <class Step>
+__device__ __forceinline__ void strip_walk(const BinRec &r, const StripPlan &P, bool test,
+                                           int tile, int W, int H, float4 *rows, int lane,
+                                           Step &&step) {
+#pragma clang fp contract(off)
+    const int x0 = (int)(r.xs & 0xffffu), y0 = (int)(r.ys & 0xffffu);
+    const int w = (int)(r.xs >> 16) - x0 + 1, h = (int)(r.ys >> 16) - y0 + 1;
+    const int R = P.R, s = P.s, ns = P.ns, nr = P.nr, rg = P.rg, cl = P.cl;
+    const bool lane_ok = P.lane_ok;
     const float mux = r.ux, muy = r.uy, a = r.a, b = r.b, c = r.c, thr = r.thr;
     const bool fast = test && h + 1 <= kRowSlots;
     if (fast) {
@@ -295,6 +316,25 @@ __device__ __forceinline__ void strip_walk(const BinRec &r, bool test, int tile,
     // The slice is rewritten for the wave's next rectangle.
     __builtin_amdgcn_wave_barrier();
 }
+
+// The count pass keeps each large rectangle's claims, one 64-bit word per
+// walk step (the wave's ballot of that step's claims), so the write pass
+// replays the steps instead of testing every tile again. A count workgroup
+// has kBlockWords words, taken by its rectangles as their walks start; a
+// rectangle whose steps no longer fit is walked again by the write pass.
+// Its mask word records where its words are: 1 + the first word's index,
+// plus the step count from bit kWordSteps (0: not kept).
+constexpr int kBlockWords = 1024;
+constexpr int kWordSteps = 11;
+static_assert(kBlockWords < (1 << kWordSteps), "the first word's index + 1 fits below the steps");
+
+__device__ __forceinline__ uint32_t kept_mask(int first, int nst) {
+    return (uint32_t)(first + 1) | ((uint32_t)nst << kWordSteps);
+}
+__device__ __forceinline__ int kept_first(uint32_t m) {
+    return (int)(m & ((1u << kWordSteps) - 1u)) - 1;
+}
+__device__ __forceinline__ int kept_steps(uint32_t m) { return (int)(m >> kWordSteps); }
 
 __device__ __forceinline__ int rec_area(const BinRec &r) {
     return ((int)(r.xs >> 16) - (int)(r.xs & 0xffffu) + 1) *
@@ -576,15 +616,16 @@ __device__ __forceinline__ uint32_t wave_small_claims(const BinRec &r, int ar, b
 }
 
 // Count pass in Gaussian order (coalesced reads): the tile count and the
-// walk record; per workgroup the intersection total.
-__global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArgs A,
-                                                                    int32_t *counts, BinRec *recs,
-                                                                    uint32_t *masks,
-                                                                    BinPart *parts) {
+// walk record (with a small rectangle's claim mask, or a large one's kept
+// step words); per workgroup the intersection total. At most 80 VGPRs, so
+// six waves fit per SIMD.
+__global__ __launch_bounds__(kBinThreads) __attribute__((amdgpu_waves_per_eu(6))) void
+bin_count_rec_kernel(const BinArgs A, int32_t *counts, BinRec *recs, uint32_t *masks,
+                     uint64_t *words, BinPart *parts) {
     __shared__ BinPart s_p[kBinThreads / 64];
     __shared__ BinRec s_rec[kBinThreads];
     __shared__ int32_t s_big[kBinThreads], s_cnt[kBinThreads];
-    __shared__ int32_t s_nbig;
+    __shared__ int32_t s_nbig, s_used;
     __shared__ int32_t s_pre[kBinThreads];
     __shared__ uint32_t s_msk[kBinThreads];
     // Per wave: the small claims' owner marks, then the strip walk's row
@@ -593,7 +634,10 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t g = (int64_t)blockIdx.x * kBinThreads + tid;
     const bool test = A.conic != nullptr;
-    if (tid == 0) s_nbig = 0;
+    if (tid == 0) {
+        s_nbig = 0;
+        s_used = 0;
+    }
     __syncthreads();
     int n = 0;
     bool big = false;
@@ -614,7 +658,6 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
                              s_pre + wave * 64, s_msk + wave * 64,
                              reinterpret_cast<uint8_t *>(s_rows[wave]), lane);
     n = __popc(mask);
-    if (g < A.N) masks[g] = mask;
     // s_rec's wave slice now holds the big rectangles' records (a lane's own
     // record, written by wave_small_claims or here).
     if (big) s_rec[tid] = r;
@@ -625,19 +668,40 @@ __global__ __launch_bounds__(kBinThreads) void bin_count_rec_kernel(const BinArg
     at = __shfl(at, 0, 64);
     if (big) s_big[at + rank_in(m)] = tid;
     __syncthreads();
+    // Each walk's step ballots go to the workgroup's words while they fit
+    // (kept_mask records where; s_pre holds it, the small claims being done
+    // with their slices).
     for (int e = wave; e < s_nbig; e += kBinThreads / 64) {
         const int j = s_big[e];
         const BinRec r = s_rec[j];
-        int cnt = 0;
-        strip_walk(r, test, A.tile, A.W, A.H, s_rows[wave], lane,
-                   [&](bool claim, int, int) { cnt += claim ? 1 : 0; });
+        const StripPlan P = strip_plan(r, lane);
+        const int nst = P.ns * P.nr;
+        int first = 0;
+        if (lane == 0) first = atomicAdd(&s_used, min(nst, kBlockWords + 1));
+        first = __builtin_amdgcn_readfirstlane(first);
+        const bool keep = first + nst <= kBlockWords;
+        uint64_t *const wp = words + (int64_t)blockIdx.x * kBlockWords + first;
+        int cnt = 0, t = 0;
+        strip_walk(r, P, test, A.tile, A.W, A.H, s_rows[wave], lane,
+                   [&](bool claim, int, int) {
+                       cnt += claim ? 1 : 0;
+                       if (keep) {
+                           const uint64_t cm = ballot(claim);
+                           if (lane == 0) wp[t] = cm;
+                       }
+                       ++t;
+                   });
         for (int o = 32; o >= 1; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
-        if (lane == 0) s_cnt[j] = cnt;
+        if (lane == 0) {
+            s_cnt[j] = cnt;
+            s_pre[j] = (int32_t)(keep ? kept_mask(first, nst) : 0u);
+        }
     }
     __syncthreads();
     if (g < A.N) {
         if (big) n = s_cnt[tid];
         counts[g] = n;
+        masks[g] = big ? (uint32_t)s_pre[tid] : mask;
     }
     unsigned long long tot = (unsigned long long)n;
     for (int o = 32; o >= 1; o >>= 1) tot += __shfl_xor(tot, o, 64);
@@ -714,6 +778,36 @@ __device__ __forceinline__ int64_t lists_kept(const int64_t *status) {
 // Pairs staged in LDS per workgroup before the coalesced store.
 constexpr int kBinStage = 2048;
 
+// Exclusive sum and exclusive max of one value each per thread over a
+// kBinThreads workgroup (max of non-negative values; 0 before thread 0).
+// One barrier; sc holds 2 x (kBinThreads / 64) ints of its own.
+__device__ __forceinline__ void block_excl_sum_max(int vs, int vm, int &ex_s, int &ex_m,
+                                                   int *sc) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int is = vs, im = vm;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int ts = __shfl_up(is, o, 64), tm = __shfl_up(im, o, 64);
+        if (lane >= o) {
+            is += ts;
+            im = max(im, tm);
+        }
+    }
+    if (lane == 63) {
+        sc[wave] = is;
+        sc[kBinThreads / 64 + wave] = im;
+    }
+    __syncthreads();
+    int bs = 0, bm = 0;
+    for (int w = 0; w < wave; ++w) {
+        bs += sc[w];
+        bm = max(bm, sc[kBinThreads / 64 + w]);
+    }
+    ex_s = bs + is - vs;
+    // The inclusive max of the lanes before this one: shift by one lane.
+    const int prev = __shfl_up(im, 1, 64);
+    ex_m = max(bm, lane > 0 ? prev : 0);
+}
+
 // Thread k emits the pairs of Gaussian k (tile id key, Gaussian id) at its
 // scanned offset; the workgroup's 256 Gaussians own one contiguous output
 // range.
@@ -722,41 +816,68 @@ constexpr int kBinStage = 2048;
 //     256 x 32 pairs) and staged in windows of kBinStage slots, each slot
 //     with its position in the range, then stored by consecutive lanes, so
 //     adjacent runs land as coalesced stores.
-//   * Large rectangles (more than kWaveWalkArea tiles) are walked by a wave
-//     (strip_walk, up to 64 tiles a step); the claimed tiles of a step take
-//     consecutive positions by lane rank, and the wave stores them directly,
-//     consecutive lanes on consecutive addresses.
+//   * Large rectangles (more than kWaveWalkArea tiles) are replayed from the
+//     step words the count pass kept. Those words are one run per rectangle
+//     from the start of the workgroup's kBlockWords. The workgroup loads
+//     them, finds each word's rectangle (the last run start at or before it,
+//     an exclusive max scan), its step's first tile and the claims before it
+//     in its rectangle (an exclusive sum scan of the words' bit counts), and
+//     the four waves take the words in turn: a rectangle's steps are spread
+//     over the waves however the rectangles' sizes fall. A step's claims
+//     take consecutive positions by lane rank, stored directly, consecutive
+//     lanes on consecutive addresses. Rectangles the count pass kept no words
+//     for are walked again, a wave each (strip_walk, up to 64 tiles a step).
 // With pairs (and depth) the value of a pair is {Gaussian id, its depth's
 // float bits} in one 8-byte store instead of the id alone in ids.
 // The workgroup's output range starts at part_off[blockIdx.x] (the count
 // workgroup of the same 256 Gaussians, scanned); each Gaussian's offset in it
 // is an exclusive scan of the counts, formed here.
 __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
-    const BinRec *recs, const int32_t *counts, const uint32_t *masks, const int64_t *part_off,
-    int64_t N, int tile, int W, int H, int tiles_x, int test, uint32_t *tkeys, int32_t *ids,
-    const float *depth, uint2 *pairs, const int64_t *status) {
+    const BinRec *recs, const int32_t *counts, const uint32_t *masks, const uint64_t *words,
+    const int64_t *part_off, int64_t N, int tile, int W, int H, int tiles_x, int test,
+    uint32_t *tkeys, int32_t *ids, const float *depth, uint2 *pairs, const int64_t *status) {
     // Capacity-bounded lists that overflowed emit nothing.
     if (status && status[1] != 0) return;
-    // s_k also holds each wave's strip-walk row slice before the staging
-    // windows use it.
+    // The staging windows' arrays hold, until the small runs are staged:
+    //   s_k: per kept word its step's first tile (s_tb), per rectangle the
+    //        bit count before its first word (s_pf) and its walk plan
+    //        (s_pl, s_pnr); then each wave's strip-walk row slice;
+    //   s_i: the kept words;
+    //   s_off: each Gaussian's offset in the range and count (s_at, s_cap),
+    //        per kept word its rectangle + 1 (s_hown, 16 bits; run starts
+    //        first) and the bit count before it (s_pw).
     __shared__ __align__(16) uint32_t s_k[kBinStage];
-    __shared__ int32_t s_i[kBinStage];
+    __shared__ __align__(16) int32_t s_i[kBinStage];
+    __shared__ __align__(16) int32_t s_off[kBinStage];
     static_assert(kBinStage * 4 >= (kBinThreads / 64) * kRowSlots * 16, "row slices fit s_k");
-    __shared__ int32_t s_off[kBinStage];
+    static_assert(kBinStage == 2 * kBlockWords && kBinThreads * 4 == kBlockWords,
+                  "the replay arrays fit the staging arrays");
+    uint64_t *const s_words = reinterpret_cast<uint64_t *>(s_i);
+    uint32_t *const s_tb = s_k;
+    int32_t *const s_pf = reinterpret_cast<int32_t *>(s_k) + kBlockWords;
+    uint32_t *const s_pl = s_k + kBlockWords + kBinThreads;
+    int32_t *const s_pnr = reinterpret_cast<int32_t *>(s_k) + kBlockWords + 2 * kBinThreads;
+    int32_t *const s_at = s_off, *const s_cap = s_off + kBinThreads;
+    uint16_t *const s_hown = reinterpret_cast<uint16_t *>(s_off + 2 * kBinThreads);
+    int32_t *const s_pw = s_off + kBlockWords;
     __shared__ BinRec s_rec[kBinThreads];
     __shared__ int32_t s_big[kBinThreads], s_g[kBinThreads];
-    __shared__ int32_t s_nbig, s_wsum[kBinThreads / 64], s_csum[kBinThreads / 64];
-    // Each Gaussian's offset in the range and count, for the wave walks of the
-    // large rectangles; they share s_off's storage, which the staging windows
-    // only use afterwards.
-    int32_t *s_at = s_off, *s_cap = s_off + kBinThreads;
+    __shared__ uint32_t s_wm[kBinThreads];   // a large rectangle's kept_mask (or 0)
+    __shared__ int32_t s_nbig, s_nfall, s_wext, s_wsum[kBinThreads / 64],
+        s_csum[kBinThreads / 64], s_sc[2 * (kBinThreads / 64)];
     __shared__ uint32_t s_dk[kBinThreads];   // depth bits of the workgroup's Gaussians
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t k0 = (int64_t)blockIdx.x * kBinThreads;
     const int64_t k = k0 + tid;
     const int64_t base = part_off[blockIdx.x];
     if (pairs) s_dk[tid] = k < N ? __float_as_uint(depth[k]) : 0u;
-    if (tid == 0) s_nbig = 0;
+    if (tid == 0) {
+        s_nbig = 0;
+        s_nfall = 0;
+        s_wext = 0;
+    }
+    reinterpret_cast<uint32_t *>(s_hown)[2 * tid] = 0u;
+    reinterpret_cast<uint32_t *>(s_hown)[2 * tid + 1] = 0u;
     __syncthreads();
     bool big = false;
     int small_cap = 0;        // pairs this thread stages (0 unless a small rectangle)
@@ -768,13 +889,21 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
         if (cap > 0) {
             g = (int32_t)k;
             r = recs[g];
+            mask = masks[g];
             if (rec_area(r) > kWaveWalkArea) {
                 big = true;
                 s_rec[tid] = r;
                 s_g[tid] = g;
+                s_wm[tid] = mask;
+                if (mask != 0) {
+                    // Its run of words, marked at its start.
+                    atomicMax(&s_wext, kept_first(mask) + kept_steps(mask));
+                    s_hown[kept_first(mask)] = (uint16_t)(tid + 1);
+                } else {
+                    atomicAdd(&s_nfall, 1);
+                }
             } else {
                 small_cap = cap;
-                mask = masks[g];
             }
         }
     }
@@ -807,29 +936,105 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
     }
     s_at[tid] = off0;
     s_cap[tid] = cap;
+    const int wext = s_wext, nbig = s_nbig;
+    if (wext > 0) {   // workgroup-uniform
+        // The kept rectangles' walk plans, a wave each.
+        for (int e = wave; e < nbig; e += kBinThreads / 64) {
+            const int j = s_big[e];
+            if (s_wm[j] == 0) continue;
+            const StripPlan P = strip_plan(s_rec[j], lane);
+            if (lane == 0) {
+                // R and s up to 64, ceil(2^16 / s) up to 2^16.
+                s_pl[j] = (uint32_t)P.R | (uint32_t)P.s << 7 |
+                          ((65535u + (uint32_t)P.s) / (uint32_t)P.s) << 14;
+                s_pnr[j] = P.nr;
+            }
+        }
+        // Words 4 tid .. 4 tid + 3, all requested at once.
+        const int i0 = 4 * tid;
+        uint64_t v[4];
+        int hp[4], pc[4], runmax = 0, psum = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = i0 + q;
+            v[q] = i < wext ? words[(int64_t)blockIdx.x * kBlockWords + i] : 0ull;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = i0 + q;
+            // A run start marks its own position + 1; the max of those at
+            // or before word i is its run's start + 1.
+            runmax = max(runmax, (i < wext && s_hown[i] != 0) ? i + 1 : 0);
+            hp[q] = runmax;
+            pc[q] = psum;
+            psum += __popcll(v[q]);
+        }
+        int ex_s, ex_m;
+        block_excl_sum_max(psum, runmax, ex_s, ex_m, s_sc);   // orders the plans too
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = i0 + q;
+            if (i >= wext) break;
+            const int st = max(hp[q], ex_m) - 1;      // the run's first word
+            const int j = (int)s_hown[st] - 1;
+            const int t = i - st, nr = s_pnr[j];
+            const int kk = t / nr, u = t - kk * nr;
+            const uint32_t pl = s_pl[j];
+            const BinRec rj = s_rec[j];
+            s_words[i] = v[q];
+            s_tb[i] = ((rj.xs & 0xffffu) + (uint32_t)kk * ((pl >> 7) & 127u)) |
+                      (((rj.ys & 0xffffu) + (uint32_t)u * (pl & 127u)) << 16);
+            s_pw[i] = ex_s + pc[q];
+            if (st == i) s_pf[j] = ex_s + pc[q];
+            // Every word's entry now names its rectangle (a run start's is
+            // unchanged, and only those are read by other threads here).
+            s_hown[i] = (uint16_t)(j + 1);
+        }
+    }
     __syncthreads();
-    // Large rectangles: direct stores.
-    for (int e = wave; e < s_nbig; e += kBinThreads / 64) {
-        const int j = s_big[e];
-        const BinRec rb = s_rec[j];
-        const int32_t gb = s_g[j];
-        const int64_t atb = base + s_at[j];
-        const int capb = s_cap[j];
-        const uint32_t dk = s_dk[j];
-        int emitted = 0;
-        strip_walk(rb, test != 0, tile, W, H, reinterpret_cast<float4 *>(s_k) + wave * kRowSlots,
-                   lane, [&](bool claim, int tx, int ty) {
-                       const uint64_t cm = ballot(claim);
-                       const int pos = emitted + rank_in(cm);
-                       if (claim && pos < capb) {
-                           tkeys[atb + pos] = (uint32_t)(ty * tiles_x + tx);
-                           if (pairs)
-                               pairs[atb + pos] = make_uint2((uint32_t)gb, dk);
-                           else
-                               ids[atb + pos] = gb;
-                       }
-                       emitted += __popcll(cm);
-                   });
+    // A step's claims (cm, the walk's ballot): the lane's tile (tx, ty) at
+    // position pos0 + its rank among them, within rectangle j's run.
+    auto emit = [&](uint64_t cm, int j, int tx, int ty, int pos0) {
+        const int pos = pos0 + rank_in(cm);
+        if (((cm >> lane) & 1ull) && pos < s_cap[j]) {
+            const int64_t at = base + s_at[j] + pos;
+            tkeys[at] = (uint32_t)(ty * tiles_x + tx);
+            if (pairs)
+                pairs[at] = make_uint2((uint32_t)s_g[j], s_dk[j]);
+            else
+                ids[at] = s_g[j];
+        }
+    };
+    // The kept words, the four waves in turn.
+    for (int i = wave; i < wext; i += kBinThreads / 64) {
+        const uint64_t cm = s_words[i];
+        if (cm == 0) continue;
+        const int j = (int)s_hown[i] - 1;
+        const uint32_t tb = s_tb[i], pl = s_pl[j];
+        // lane = rg * s + cl, rg = floor(lane / s) as lane * ceil(2^16 / s) >> 16
+        // (exact for lane < 64 <= 2^16 / s).
+        const int sw = (int)((pl >> 7) & 127u);
+        const int rg = (int)(((uint32_t)lane * (pl >> 14)) >> 16), cl = lane - rg * sw;
+        emit(cm, j, (int)(tb & 0xffffu) + cl, (int)(tb >> 16) + rg, s_pw[i] - s_pf[j]);
+    }
+    // Rectangles without kept words: walked again, a wave each, in the row
+    // slices (s_k, once the replay is done with it).
+    if (s_nfall > 0) {   // workgroup-uniform
+        __syncthreads();
+        for (int e = wave; e < nbig; e += kBinThreads / 64) {
+            const int j = s_big[e];
+            if (s_wm[j] != 0) continue;
+            const BinRec rb = s_rec[j];
+            const StripPlan P = strip_plan(rb, lane);
+            int emitted = 0;
+            strip_walk(rb, P, test != 0, tile, W, H,
+                       reinterpret_cast<float4 *>(s_k) + wave * kRowSlots, lane,
+                       [&](bool claim, int tx, int ty) {
+                           const uint64_t cm = ballot(claim);
+                           emit(cm, j, tx, ty, emitted);
+                           emitted += __popcll(cm);
+                       });
+        }
     }
     __syncthreads();   // s_at / s_cap read; s_off becomes the staging window
     // Small rectangles: LDS windows over the numbered runs.
@@ -1728,6 +1933,7 @@ struct BeginWs {
     int32_t *counts;
     uint32_t *masks;
     BinRec *recs;
+    uint64_t *words;    // kBlockWords per count workgroup
     BinPart *parts;
     int64_t *part_off;
     BinStats *stats;
@@ -1740,6 +1946,7 @@ struct BeginWs {
         counts = (int32_t *)take(4 * N);
         masks = (uint32_t *)take(4 * N);
         recs = (BinRec *)take((int64_t)sizeof(BinRec) * N);
+        words = (uint64_t *)take(8 * kBlockWords * nparts);
         parts = (BinPart *)take((int64_t)sizeof(BinPart) * nparts);
         part_off = (int64_t *)take(8 * nparts);
         stats = (BinStats *)take(sizeof(BinStats));
@@ -1807,7 +2014,7 @@ static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
     {
         TimedScope ts("bin_write", s);
         bin_write_rec_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(
-            ws.recs, ws.counts, ws.masks, ws.part_off, N, tile, W, H, tiles_x,
+            ws.recs, ws.counts, ws.masks, ws.words, ws.part_off, N, tile, W, H, tiles_x,
             conic != nullptr ? 1 : 0, tk_a, nullptr, depth, pairs_a, status);
         MG_LAUNCHED("bin_write_rec_kernel");
     }
@@ -1962,7 +2169,8 @@ int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy, const f
     if (N > 0) {
         TimedScope ts("bin_count", s);
         bin_count_rec_kernel<<<(unsigned)nparts, kBinThreads, 0, s>>>(A, ws.counts, ws.recs,
-                                                                       ws.masks, ws.parts);
+                                                                       ws.masks, ws.words,
+                                                                       ws.parts);
         MG_LAUNCHED("bin_count_rec_kernel");
     }
     {
@@ -2048,7 +2256,8 @@ int32_t mg_bin_lists_capped(int64_t N, const float *uv, const float *rxy, const 
     if (N > 0) {
         TimedScope ts("bin_count", s);
         bin_count_rec_kernel<<<(unsigned)nparts, kBinThreads, 0, s>>>(A, ws.counts, ws.recs,
-                                                                       ws.masks, ws.parts);
+                                                                       ws.masks, ws.words,
+                                                                       ws.parts);
         MG_LAUNCHED("bin_count_rec_kernel");
     }
     {

@@ -168,6 +168,52 @@ def test_synthetic_conics_on_large_rectangles_bit_exact(dev, seed):
     assert np.array_equal(gids.cpu().numpy(), rids), "gauss_ids differ"
 
 
+@pytest.mark.parametrize("ellipse", [True, False])
+def test_kept_and_rewalked_large_rectangles_bit_exact(dev, ellipse):
+    """The count pass keeps a large rectangle's claims as one 64-bit word per
+    walk step, up to 256 words per wave of its workgroup, and the write pass
+    replays them; a rectangle that no longer fits is walked again. At
+    1920x1080 and tile 16 a rectangle over the whole image (120 x 68 tiles)
+    takes 136 steps. Eight of them lead the first 256-Gaussian block, dealt
+    two to each of its four waves: each wave keeps the first (136 words) and
+    walks the second again (272 > 256). The second block holds a hundred
+    rectangles of about 120 to 4000 tiles (near-singular conics among them),
+    25 per wave: each wave keeps them until its words run out and walks the
+    rest again. The lists must equal the oracle's."""
+    from metal_gauss_amd.backend import _bin
+
+    rng = np.random.default_rng(61)
+    N, W, H, tile = 512, 1920, 1080, 16
+    f32 = np.float32
+    uv = np.stack([rng.uniform(0, W, N), rng.uniform(0, H, N)], 1).astype(f32)
+    rxy = rng.uniform(2, 7, (N, 2)).astype(f32)
+    a = np.exp(rng.uniform(np.log(1e-4), np.log(0.5), N))
+    c = np.exp(rng.uniform(np.log(1e-4), np.log(0.5), N))
+    corr = rng.uniform(-0.999, 0.999, N)
+    # First block: eight whole-image rectangles, wide ellipses.
+    uv[:8] = (W / 2, H / 2)
+    rxy[:8] = (1500, 900)
+    a[:8], c[:8], corr[:8] = 1e-6, 2e-6, rng.uniform(-0.5, 0.5, 8)
+    # Second block: a hundred large rectangles.
+    big = np.arange(300, 400)
+    rxy[big] = rng.uniform(80, 500, (100, 2))
+    corr[big[:30]] = np.sign(corr[big[:30]]) * (1.0 - rng.uniform(0.0, 1e-3, 30))
+    b = corr * np.sqrt(a * c)
+    conic = np.stack([a, b, c], 1).astype(f32)
+    op = rng.uniform(0.05, 0.99, N).astype(f32)
+    valid = np.ones(N, np.int32)
+    depth = rng.uniform(0.5, 20.0, N).astype(f32)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    cn, o = (t(conic), t(op)) if ellipse else (None, None)
+    gids, offs, _ = _bin(t(uv), t(rxy), t(depth), t(valid), cn, o, W, H, tile)
+    rids, roffs, _, _ = binning_ref.build_tile_lists(uv, rxy, conic, op, valid, depth, W, H,
+                                                     tile, ellipse=ellipse)
+    counts = np.bincount(rids, minlength=N)
+    assert (counts[:8] == (W // tile) * ((H + tile - 1) // tile)).all(), counts[:8]
+    assert np.array_equal(offs.cpu().numpy(), roffs), "tile offsets differ"
+    assert np.array_equal(gids.cpu().numpy(), rids), "gauss_ids differ"
+
+
 @pytest.mark.parametrize("spread", [0.0, 2e-6, 2e-3, 0.5, 3.0])
 def test_depth_windows_of_every_pass_count_bit_exact(dev, spread):
     """The per-tile depth sort takes 8-bit passes over only the bits in which
