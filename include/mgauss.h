@@ -365,7 +365,9 @@ int32_t mg_tile_ranges(const uint64_t *sorted_keys, int64_t n,
  * and their exclusive scan, then one synchronous host read of the
  * intersection total, which goes to total_host (host) when not NULL; the
  * stream is always synchronised once. The workspace
- * (mg_bin_lists_workspace_bytes(N)) carries state to finish and must not be
+ * (mg_bin_lists_workspace_bytes(N), about 72 bytes per Gaussian: its count,
+ * walk record, claimed tiles, and the claims of rectangles over 32 tiles as
+ * one 64-bit word per walk step) carries state to finish and must not be
  * touched in between.
  *
  * finish: emits each Gaussian's (tile id, Gaussian id) pairs, Gaussian by
