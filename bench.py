@@ -695,10 +695,16 @@ def render_config(which, reps, crowded=False, chunked=False):
     """Configs 1, 2 and 5 ([1], [4]): one view, render
     forward (config 1) or forward + L1 loss + backward (2, 5), on the
     configuration's seeded scene and camera (config 5 ``crowded``: the
-    variant that reaches the configuration's stated stress)."""
+    variant that reaches the configuration's stated stress). As in the
+    config-4 step, exp and sigmoid of the log-scales and opacity logits run
+    inside the projection kernels (render(activations=True)) and the tile
+    lists are capacity-sized (a ListCapacity, no host read inside the call;
+    a call whose lists overflowed runs again and is counted). The same
+    calls with the lists sized by the host read, the reference's way, are
+    timed beside them."""
     import torch
 
-    from metal_gauss_amd import render, scenes
+    from metal_gauss_amd import ListCapacity, render, scenes
 
     dev = torch.device("cuda:0")
     if which == 1:
@@ -714,27 +720,51 @@ def render_config(which, reps, crowded=False, chunked=False):
     leaves = {k: getattr(sc, k).clone().requires_grad_(which != 1)
               for k in ("means", "log_scales", "quats", "logit_opac", "sh_dc", "sh_rest")}
     info = {}
+    cap = ListCapacity()
+    reruns = [0]
 
-    def fwd():
+    def fwd(sized):
         L = leaves
-        rgb, alpha, inf = render(L["means"], L["quats"], torch.exp(L["log_scales"]),
-                                 torch.sigmoid(L["logit_opac"]), L["sh_dc"], cam.K, cam.viewmat,
-                                 cam.W, cam.H, sh_degree=sc.sh_degree, sh_rest=L["sh_rest"],
-                                 background=bg, chunked_backward=chunked)
+        rgb, alpha, inf = render(L["means"], L["quats"], L["log_scales"], L["logit_opac"],
+                                 L["sh_dc"], cam.K, cam.viewmat, cam.W, cam.H,
+                                 sh_degree=sc.sh_degree, sh_rest=L["sh_rest"], background=bg,
+                                 chunked_backward=chunked, activations=True,
+                                 list_capacity=cap if sized else None)
         info.update(inf)
         return rgb
 
-    def fwd_bwd():
-        for t in leaves.values():
-            t.grad = None
-        (fwd() - target).abs().mean().backward()
+    def overflowed(sized):
+        # Polled once the whole call is enqueued, so the GPU is not left idle.
+        if sized and cap.overflowed(info["lists_ticket"]):
+            reruns[0] += 1
+            return True
+        return False
+
+    def fwd_only(sized=True):
+        while True:
+            fwd(sized)
+            if not overflowed(sized):
+                return
+
+    def fwd_bwd(sized=True):
+        while True:
+            for t in leaves.values():
+                t.grad = None
+            torch.nn.functional.l1_loss(fwd(sized), target).backward()
+            if not overflowed(sized):
+                return
 
     with torch.no_grad():
-        fwd_ms = _timed_ms(fwd, reps)
-    out = {"fwd_ms": round(fwd_ms, 4)}
-    step = fwd if which == 1 else fwd_bwd
+        fwd_only()                        # sizes the lists
+        reruns[0] = 0
+        fwd_ms = _timed_ms(fwd_only, reps)
+        fwd_ms_host = _timed_ms(lambda: fwd_only(False), reps)
+    out = {"fwd_ms": round(fwd_ms, 4), "fwd_ms_host_read_lists": round(fwd_ms_host, 4)}
+    step = fwd_only if which == 1 else fwd_bwd
     if which != 1:
         out["fwd_bwd_ms"] = round(_timed_ms(fwd_bwd, reps), 4)
+        out["fwd_bwd_ms_host_read_lists"] = round(_timed_ms(lambda: fwd_bwd(False), reps), 4)
+    out["reruns_after_sizing"] = reruns[0]
     out["kernels"] = _kernel_means(step, 5, KERNELS)
     gids_len = None
     with torch.no_grad():

@@ -1075,10 +1075,13 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
 // Offsets of sorted tile keys: offsets[t] = the first i with tiles[i] >= t
 // (n for t past the last key). A thread takes kRangePer consecutive keys,
 // read as two 16-byte loads, and the key before them; at a change of key
-// from a to b at position i it writes offsets[a + 1 .. b] = i.
+// from a to b at position i it writes offsets[a + 1 .. b] = i. With status
+// (capacity-bounded lists, n the capacity) n is the pairs kept.
 constexpr int kRangePer = 8;
 __global__ __launch_bounds__(256) void tile_ranges_u32_kernel(const uint32_t *tiles, int64_t n,
-                                                              int32_t n_tiles, int32_t *offsets) {
+                                                              int32_t n_tiles, int32_t *offsets,
+                                                              const int64_t *status) {
+    if (status) n = min(lists_kept(status), n);
     const int64_t b = ((int64_t)blockIdx.x * 256 + threadIdx.x) * kRangePer;
     if (b > n) return;
     int64_t key[kRangePer + 1];   // key[j] is tiles[b + j - 1]; -1 before the first
@@ -1916,16 +1919,6 @@ tile_depth_sort_kernel(const TdArgs A) {
     td_long(S, A, s0, len);
 }
 
-// Capacity-bounded lists on the radix route: the slots past the kept pairs
-// get a tile key above every tile (they sort last and no list holds them;
-// their values are never read).
-__global__ __launch_bounds__(256) void lists_tail_kernel(uint32_t *tiles, int64_t capacity,
-                                                         const int64_t *status) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= capacity || i < lists_kept(status)) return;
-    tiles[i] = 0xFFFFFFFFu;
-}
-
 // Carves the begin/finish workspace identically on both calls. After begin,
 // counts holds each Gaussian's tile count, part_off the first pair of each
 // 256-Gaussian workgroup, recs the walk records.
@@ -1986,9 +1979,8 @@ static int64_t finish_sort_bytes(int64_t T, bool capped) {
 // kCsBuckets tiles the one-pass counting sort carries the values by tile (and
 // writes the offsets); otherwise radix passes on the tile bits carry them
 // (the keys ping-pong through gauss_ids, which only the depth sort writes),
-// and tile_ranges writes the offsets; capacity-bounded lists fill the slots
-// past the kept pairs with a tile key above every tile, which the key width
-// then holds.
+// and tile_ranges writes the offsets; for capacity-bounded lists both read
+// the kept count from status and leave the slots past it alone.
 static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
                              const float *depth, int W, int H, int tile, int tiles_x,
                              int n_tiles, int64_t n, const int64_t *status, int32_t *gauss_ids,
@@ -2004,13 +1996,13 @@ static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
     uint32_t *res_tiles = tk_a;
     if (n == 0 || N == 0) {
         TimedScope ts("tile_ranges", s);
-        tile_ranges_u32_kernel<<<1, 256, 0, s>>>(res_tiles, 0, n_tiles, tile_offsets);
+        tile_ranges_u32_kernel<<<1, 256, 0, s>>>(res_tiles, 0, n_tiles, tile_offsets, nullptr);
         MG_LAUNCHED("tile_ranges_u32_kernel");
         return MG_OK;
     }
     int32_t rc = MG_OK;
     const bool counting = n_tiles <= kCsBuckets;
-    const int bits = tile_bits(status ? n_tiles + 1 : n_tiles);
+    const int bits = tile_bits(n_tiles);
     {
         TimedScope ts("bin_write", s);
         bin_write_rec_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(
@@ -2025,19 +2017,15 @@ static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
                                     sort_bytes, s, status);
         if (rc != MG_OK) return rc;
     } else {
-        if (status) {
-            lists_tail_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, s>>>(tk_a, n, status);
-            MG_LAUNCHED("lists_tail_kernel");
-        }
         rc = radix_sort_passes<uint32_t, uint2>(
             tk_a, pairs_a, reinterpret_cast<uint32_t *>(gauss_ids), pairs_b, n, 0, bits, sort_ws,
-            sort_bytes, s, "tile_sort", &res_tiles, &sorted, 0u, 0xFFFFFFFFu, nullptr);
+            sort_bytes, s, "tile_sort", &res_tiles, &sorted, 0u, 0xFFFFFFFFu, nullptr, status);
         if (rc != MG_OK) return rc;
         scratch = sorted == pairs_a ? pairs_b : pairs_a;
         {
             TimedScope ts("tile_ranges", s);
             tile_ranges_u32_kernel<<<(unsigned)ceil_div(n + 1, 256 * kRangePer), 256, 0, s>>>(
-                res_tiles, n, n_tiles, tile_offsets);
+                res_tiles, n, n_tiles, tile_offsets, status);
             MG_LAUNCHED("tile_ranges_u32_kernel");
         }
     }

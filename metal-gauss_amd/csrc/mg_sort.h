@@ -33,12 +33,15 @@ int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *val
 // [lo, hi] sort on bits [0, bit_width(hi - lo)) alone. With dw (device) the
 // window and live bit count are read on the device instead of lo/hi, and
 // passes at or above dw->bits copy the values only: the sorted values are
-// the result, the keys are left unspecified. Instantiated for uint32_t keys.
+// the result, the keys are left unspecified. With status (capacity-bounded
+// tile lists: n is the capacity) only the pairs kept are sorted: none if
+// status[1] != 0, else the first min(status[0], n). Instantiated for
+// uint32_t keys.
 template <typename K, typename V>
 int32_t radix_sort_passes(K *keys_in, V *vals_in, K *keys_out, V *vals_out,
                           int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
                           hipStream_t s, const char *who, K **res_k, V **res_v, K lo,
-                          K hi, const DevWin<K> *dw);
+                          K hi, const DevWin<K> *dw, const int64_t *status = nullptr);
 
 // Workspace bytes for an exclusive scan of n int32 values.
 int64_t scan_ws_bytes(int64_t n);

@@ -63,22 +63,37 @@ __device__ __forceinline__ KeyWin<K> pass_window(KeyWin<K> win, const DevWin<K> 
     return KeyWin<K>{dw->lo, dw->hi};
 }
 
+// The keys a pass sorts: n, or with a status (capacity-bounded tile lists,
+// n being the capacity) the pairs kept, read on the device: none if
+// status[1] flags an overflow, else min(status[0], n). Tiles past them
+// count nothing and move nothing.
+__device__ __forceinline__ int64_t sort_count(int64_t n, const int64_t *status) {
+    return status ? (status[1] != 0 ? 0 : min(status[0], n)) : n;
+}
+
 template <typename K, int kSortItems>
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(const K *keys, int64_t n,
                                                                      int shift, uint32_t mask,
                                                                      KeyWin<K> win0,
                                                                      const DevWin<K> *dw,
                                                                      uint32_t *hist,
-                                                                     int64_t ntiles) {
+                                                                     int64_t ntiles,
+                                                                     const int64_t *status) {
     __shared__ uint32_t s_h[kSortWaves][kRadix];
     bool copy;
     const KeyWin<K> win = pass_window(win0, dw, shift, copy);
     if (copy) return;   // whole workgroup
+    constexpr int kSortTile = kSortThreads * kSortItems;
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    n = sort_count(n, status);
+    if (base >= n) {   // workgroup-uniform: a tile past the keys counts nothing
+        for (int d = threadIdx.x; d < kRadix; d += kSortThreads)
+            hist[(int64_t)d * ntiles + blockIdx.x] = 0u;
+        return;
+    }
     const int wave = threadIdx.x >> 6;
     for (int i = threadIdx.x; i < kSortWaves * kRadix; i += kSortThreads) (&s_h[0][0])[i] = 0;
     __syncthreads();
-    constexpr int kSortTile = kSortThreads * kSortItems;
-    const int64_t base = (int64_t)blockIdx.x * kSortTile;
     // Every key is requested before any is counted: loads at a clamped index
     // (n >= 1), and a count of 0 past n, so no load sits in a branch that
     // waits for it before the next.
@@ -151,7 +166,7 @@ template <typename K, typename V, int kSortItems>
 __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     const K *keys_in, const V *vals_in, K *keys_out, V *vals_out, int64_t n,
     int shift, uint32_t mask, KeyWin<K> win0, const DevWin<K> *dw, const uint32_t *hist,
-    int64_t ntiles, const uint32_t *totals) {
+    int64_t ntiles, const uint32_t *totals, const int64_t *status) {
     constexpr int kSortTile = kSortThreads * kSortItems;
     constexpr int kChunk = kSortTile / kSortWaves;       // keys per wave
     __shared__ K s_keys[kSortTile];
@@ -163,6 +178,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    n = sort_count(n, status);
+    if (base >= n) return;   // workgroup-uniform: no key of this tile is sorted
     const int nitems = (int)min((int64_t)kSortTile, n - base);
     const int nbits = 32 - __builtin_clz(mask);          // live digit bits (mask = 2^b - 1)
     bool copy;
@@ -298,7 +315,7 @@ template <typename K, typename V>
 int32_t radix_sort_passes(K *keys_in, V *vals_in, K *keys_out, V *vals_out,
                           int64_t n, int begin_bit, int end_bit, void *ws, int64_t ws_bytes,
                           hipStream_t s, const char *who, K **res_k, V **res_v, K lo,
-                          K hi, const DevWin<K> *dw) {
+                          K hi, const DevWin<K> *dw, const int64_t *status) {
     MG_REQUIRE(n >= 0 && n < (1LL << 31), "%s: n = %lld", who, (long long)n);
     MG_REQUIRE(begin_bit >= 0 && end_bit <= (int)(8 * sizeof(K)) && begin_bit <= end_bit,
                "%s: bit range [%d, %d)", who, begin_bit, end_bit);
@@ -322,13 +339,13 @@ int32_t radix_sort_passes(K *keys_in, V *vals_in, K *keys_out, V *vals_out,
         const uint32_t mask = (1u << width) - 1u;
 #define MG_SORT_PASS(IT)                                                                   \
     radix_upsweep_kernel<K, IT><<<(unsigned)ntiles, kSortThreads, 0, s>>>(                 \
-        src_k, n, b, mask, win, dw, hist, ntiles);                                         \
+        src_k, n, b, mask, win, dw, hist, ntiles, status);                                 \
     MG_LAUNCHED("radix_upsweep_kernel");                                                   \
     radix_scan_kernel<<<kRadix, kSortThreads, 0, s>>>(hist, ntiles, totals, b,             \
                                                       dw ? &dw->bits : nullptr);           \
     MG_LAUNCHED("radix_scan_kernel");                                                      \
     radix_downsweep_kernel<K, V, IT><<<(unsigned)ntiles, kSortThreads, 0, s>>>(            \
-        src_k, src_v, dst_k, dst_v, n, b, mask, win, dw, hist, ntiles, totals);            \
+        src_k, src_v, dst_k, dst_v, n, b, mask, win, dw, hist, ntiles, totals, status);    \
     MG_LAUNCHED("radix_downsweep_kernel");
         if (items == 16) { MG_SORT_PASS(16) }
         else if (items == 8) { MG_SORT_PASS(8) }
@@ -350,7 +367,7 @@ int32_t radix_sort_pairs(K *keys_in, int32_t *vals_in, K *keys_out, int32_t *val
     int32_t *rv;
     int32_t rc = radix_sort_passes<K, int32_t>(keys_in, vals_in, keys_out, vals_out, n, begin_bit,
                                       end_bit, ws, ws_bytes, s, who, &rk, &rv, K(0), ~K(0),
-                                      nullptr);
+                                      nullptr, nullptr);
     if (rc != MG_OK) return rc;
     if (n > 0 && rk != keys_out) {
         MG_HIP(hipMemcpyAsync(keys_out, rk, n * sizeof(K), hipMemcpyDeviceToDevice, s));
@@ -367,12 +384,12 @@ template int32_t radix_sort_passes<uint32_t, int32_t>(uint32_t *, int32_t *, uin
                                                       int32_t *, int64_t, int, int, void *,
                                                       int64_t, hipStream_t, const char *,
                                                       uint32_t **, int32_t **, uint32_t, uint32_t,
-                                                      const DevWin<uint32_t> *);
+                                                      const DevWin<uint32_t> *, const int64_t *);
 template int32_t radix_sort_passes<uint32_t, uint2>(uint32_t *, uint2 *, uint32_t *, uint2 *,
                                                     int64_t, int, int, void *, int64_t,
                                                     hipStream_t, const char *, uint32_t **,
                                                     uint2 **, uint32_t, uint32_t,
-                                                    const DevWin<uint32_t> *);
+                                                    const DevWin<uint32_t> *, const int64_t *);
 
 }  // namespace mg
 
