@@ -233,27 +233,45 @@ struct StripPlan {
     bool lane_ok;
 };
 
+// min(v, v of the lane the DPP control names); lanes with no such lane, or
+// outside the row mask, keep v.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_min_u32(uint32_t v) {
+    return min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)0xFFFFFFFFu, (int)v, CTRL,
+                                                        ROW_MASK, 0xf, false));
+}
+
 __device__ __forceinline__ StripPlan strip_plan(const BinRec &r, int lane) {
     const int w = (int)(r.xs >> 16) - (int)(r.xs & 0xffffu) + 1;
     const int h = (int)(r.ys >> 16) - (int)(r.ys & 0xffffu) + 1;
     // Lane l prices R = l + 1 rows a step (strips of min(w, 64 / R)
     // columns); the wave takes the fewest steps, the smallest R on ties.
-    uint64_t key;
+    // The quotients of these small integers (w, h < 2^16, R <= 64) come from
+    // correctly rounded float divisions, exact after floor / ceil; the step
+    // count is held below 2^26 (beyond it any choice is as good), so the key
+    // steps << 6 | lane fits 32 bits and the minimum takes DPP row shifts
+    // and broadcasts rather than lane shuffles.
+    uint32_t key;
     {
-        const int R = lane + 1, s = min(w, 64 / R);
-        const uint64_t steps = (uint64_t)((w + s - 1) / s) * (uint64_t)((h + R - 1) / R);
-        key = steps << 6 | (uint64_t)lane;
-        for (int o = 32; o >= 1; o >>= 1) {
-            const uint64_t t = __shfl_xor(key, o, 64);
-            key = t < key ? t : key;
-        }
+        const int R = lane + 1;
+        const int s = min(w, (int)(64.0f / (float)R));
+        const uint32_t ns = (uint32_t)ceilf((float)w / (float)s);
+        const uint32_t nr = (uint32_t)ceilf((float)h / (float)R);
+        const uint32_t steps = min(ns * nr, (1u << 26) - 1u);
+        key = steps << 6 | (uint32_t)lane;
+        key = dpp_min_u32<0x111>(key);        // row_shr:1
+        key = dpp_min_u32<0x112>(key);        // row_shr:2
+        key = dpp_min_u32<0x114>(key);        // row_shr:4
+        key = dpp_min_u32<0x118>(key);        // row_shr:8
+        key = dpp_min_u32<0x142, 0xa>(key);   // row_bcast:15
+        key = dpp_min_u32<0x143, 0xc>(key);   // row_bcast:31
     }
     StripPlan P;
-    P.R = __builtin_amdgcn_readfirstlane((int)(key & 63u)) + 1;
-    P.s = min(w, 64 / P.R);
-    P.ns = (w + P.s - 1) / P.s;
-    P.nr = (h + P.R - 1) / P.R;
-    P.rg = lane / P.s;
+    P.R = (int)(__builtin_amdgcn_readlane(key, 63) & 63u) + 1;
+    P.s = min(w, (int)(64.0f / (float)P.R));
+    P.ns = (int)ceilf((float)w / (float)P.s);
+    P.nr = (int)ceilf((float)h / (float)P.R);
+    P.rg = (int)((float)lane / (float)P.s);
     P.cl = lane - P.rg * P.s;
     P.lane_ok = lane < P.R * P.s;
     return P;
