@@ -282,8 +282,13 @@ __device__ __forceinline__ void strip_walk(const BinRec &r, const StripPlan &P, 
                                            int tile, int W, int H, float4 *rows, int lane,
                                            Step &&step) {
 #pragma clang fp contract(off)
-    const int x0 = (int)(r.xs & 0xffffu), y0 = (int)(r.ys & 0xffffu);
-    const int w = (int)(r.xs >> 16) - x0 + 1, h = (int)(r.ys >> 16) - y0 + 1;
+    // The rectangle is the wave's (read from LDS at one address): said so,
+    // the compiler keeps its bounds in scalar registers and branches on
+    // `fast` once instead of masking both step bodies every step.
+    const uint32_t xs = __builtin_amdgcn_readfirstlane(r.xs);
+    const uint32_t ys = __builtin_amdgcn_readfirstlane(r.ys);
+    const int x0 = (int)(xs & 0xffffu), y0 = (int)(ys & 0xffffu);
+    const int w = (int)(xs >> 16) - x0 + 1, h = (int)(ys >> 16) - y0 + 1;
     const int R = P.R, s = P.s, ns = P.ns, nr = P.nr, rg = P.rg, cl = P.cl;
     const bool lane_ok = P.lane_ok;
     const float mux = r.ux, muy = r.uy, a = r.a, b = r.b, c = r.c, thr = r.thr;
