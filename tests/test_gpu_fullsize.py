@@ -12,6 +12,8 @@ own entry points, against the CPU oracle.
 * Config 5 (3M, 1920x1080, 8160 tiles: the radix route past 4096 tiles) and
   its crowded variant (tile lists over 10k entries, over 30M intersections):
   the same binning, raster and projection checks.
+* At each of these, the capacity-sized lists (no host read; capacity equal
+  to the total and 25% above it) equal the host-read lists bit for bit.
 * Config 3 (1M x 59 floats): SelectiveAdam with Bernoulli(0.6) masks and
   FusedAdam, 1 and 101 steps, against oracle/adam_ref.py on a seeded
   subsample of rows (every row's update is independent of the others), the
@@ -75,6 +77,17 @@ def _binning_bit_exact(uv, rxy, conic, op, valid, depth, W, H, label):
     tiles = np.repeat(np.arange(o.size - 1, dtype=np.uint64), np.diff(o))
     dbits = cpu[5].astype(np.float32).view(np.uint32).astype(np.uint64)[g]
     assert np.array_equal((tiles << np.uint64(32)) | dbits, rkeys), "sorted keys differ"
+    # The same lists sized by a capacity instead of the host read (exact, and
+    # with the 25% headroom ListCapacity keeps): past 4096 tiles the radix
+    # passes and the tile ranges then take the kept count from the device.
+    total = int(rids.size)
+    for cap in (total, total + total // 4):
+        cids, coffs, _, status = backend._bin_capped(uv.detach(), rxy, depth, valid,
+                                                      conic.detach(), op.detach(), W, H, 16,
+                                                      cap)
+        assert status.tolist() == [total, 0], (status.tolist(), total, cap)
+        assert np.array_equal(_np(coffs), roffs), f"capacity {cap}: tile offsets differ"
+        assert np.array_equal(_np(cids)[:total], rids), f"capacity {cap}: gauss_ids differ"
     return gids, offs, tx, rids.size, longest
 
 
