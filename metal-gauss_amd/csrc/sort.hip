@@ -1,6 +1,6 @@
-// Stable LSD radix sort of (key, value) pairs, 8-bit digits, tiles of
-// 1024 to 4096 keys (large sorts use 4096, so a tile's run of one digit
-// averages 16 keys: 64-byte stores).
+// Stable LSD radix sort of (key, value) pairs, digits of up to 8 bits,
+// tiles of 1024 to 4096 keys (large sorts use 4096, so a tile's run of one
+// digit averages at least 16 keys: 64-byte stores).
 //
 // Each pass is reduce-then-scan, with no inter-workgroup waiting:
 //   1. upsweep   - every workgroup histograms the digit of its tile;
@@ -162,6 +162,12 @@ __global__ __launch_bounds__(kSortThreads) void radix_scan_kernel(uint32_t *hist
 // starts an exclusive scan over digits; position in the tile = digit start
 // + wave prefix + rank in wave. Items are thus ranked in tile order (wave,
 // round, lane), which makes every pass stable.
+//
+// The keys and then the values go through one LDS exchange buffer in turn
+// (sized for the wider of the two), so a workgroup holds 37 KB of LDS rather
+// than 53 KB and four fit on a CU instead of two. The store loop of the keys
+// leaves each sorted position's digit in the thread's registers for the
+// values' store loop.
 template <typename K, typename V, int kSortItems>
 __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     const K *keys_in, const V *vals_in, K *keys_out, V *vals_out, int64_t n,
@@ -169,8 +175,10 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     int64_t ntiles, const uint32_t *totals, const int64_t *status) {
     constexpr int kSortTile = kSortThreads * kSortItems;
     constexpr int kChunk = kSortTile / kSortWaves;       // keys per wave
-    __shared__ K s_keys[kSortTile];
-    __shared__ V s_vals[kSortTile];
+    constexpr int kItemBytes = sizeof(K) > sizeof(V) ? sizeof(K) : sizeof(V);
+    __shared__ __align__(16) unsigned char s_x[kSortTile * kItemBytes];
+    K *s_keys = reinterpret_cast<K *>(s_x);  // the exchange buffer, keys first
+    V *s_vals = reinterpret_cast<V *>(s_x);  // then values
     __shared__ uint32_t s_base[kRadix];     // global slot of this tile's digit run
     __shared__ uint32_t s_loc[kRadix];      // start of each digit inside the tile
     __shared__ uint32_t s_wh[kSortWaves][kRadix];   // per-wave digit counts
@@ -279,25 +287,46 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
         if (tid < kRadix) s_loc[tid] = before + incl - cnt;
         __syncthreads();
     }
+    // rank[r] becomes the item's position in the tile (kSortTile past the
+    // keys: no item there).
 #pragma unroll
     for (int r = 0; r < kSortItems; ++r) {
+        uint32_t lp = (uint32_t)kSortTile;
         if (c0 + r * 64 + lane < nitems) {
             const uint32_t d = digit_of(key[r], shift, mask, win);
-            const uint32_t lp = s_loc[d] + s_wh[wave][d] + rank[r];
-            if (lp < (uint32_t)kSortTile) {
-                s_keys[lp] = key[r];
-                s_vals[lp] = val[r];
-            }
+            lp = s_loc[d] + s_wh[wave][d] + rank[r];
         }
+        rank[r] = lp;
+        if (lp < (uint32_t)kSortTile) s_keys[lp] = key[r];
     }
     __syncthreads();
-    for (int i = tid; i < nitems; i += kSortThreads) {
-        const K k = s_keys[i];
-        const uint32_t d = digit_of(k, shift, mask, win);
-        const uint32_t dst = s_base[d] + (uint32_t)i - s_loc[d];
-        if ((int64_t)dst < n) {   // always true for a consistent histogram
-            keys_out[dst] = k;
-            vals_out[dst] = s_vals[i];
+    // Sorted position tid + 256 j has digit byte j % 4 of dig[j / 4].
+    uint32_t dig[kSortItems / 4];
+#pragma unroll
+    for (int j = 0; j < kSortItems / 4; ++j) dig[j] = 0u;
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+        const int i = tid + j * kSortThreads;
+        if (i < nitems) {
+            const K k = s_keys[i];
+            const uint32_t d = digit_of(k, shift, mask, win);
+            dig[j >> 2] |= d << (8 * (j & 3));
+            const uint32_t dst = s_base[d] + (uint32_t)i - s_loc[d];
+            if ((int64_t)dst < n) keys_out[dst] = k;   // always, for a consistent histogram
+        }
+    }
+    __syncthreads();   // every key is read before the values overwrite them
+#pragma unroll
+    for (int r = 0; r < kSortItems; ++r)
+        if (rank[r] < (uint32_t)kSortTile) s_vals[rank[r]] = val[r];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+        const int i = tid + j * kSortThreads;
+        if (i < nitems) {
+            const uint32_t d = (dig[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+            const uint32_t dst = s_base[d] + (uint32_t)i - s_loc[d];
+            if ((int64_t)dst < n) vals_out[dst] = s_vals[i];
         }
     }
 }
@@ -334,8 +363,12 @@ int32_t radix_sort_passes(K *keys_in, V *vals_in, K *keys_out, V *vals_out,
     MG_REQUIRE(lo <= hi, "%s: empty key window", who);
     const KeyWin<K> win{lo, hi};
     TimedScope ts(who, s);
-    for (int b = begin_bit; b < end_bit; b += 8) {
-        const int width = min(8, end_bit - b);
+    // Passes of at most 8 bits, the widths as even as the bit count allows
+    // (13 bits: 7 + 6, not 8 + 5), so no pass has short digit runs.
+    const int npass = (end_bit - begin_bit + 7) / 8;
+    int pass = 0;
+    for (int b = begin_bit; b < end_bit; ++pass) {
+        const int width = (end_bit - begin_bit) / npass + (pass < (end_bit - begin_bit) % npass);
         const uint32_t mask = (1u << width) - 1u;
 #define MG_SORT_PASS(IT)                                                                   \
     radix_upsweep_kernel<K, IT><<<(unsigned)ntiles, kSortThreads, 0, s>>>(                 \
@@ -351,6 +384,7 @@ int32_t radix_sort_passes(K *keys_in, V *vals_in, K *keys_out, V *vals_out,
         else if (items == 8) { MG_SORT_PASS(8) }
         else { MG_SORT_PASS(4) }
 #undef MG_SORT_PASS
+        b += width;
         K *tk = src_k; src_k = dst_k; dst_k = tk;
         V *tv = src_v; src_v = dst_v; dst_v = tv;
     }
