@@ -504,7 +504,13 @@ template <bool MIP>
 __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFwdArgs A) {
     const Cam &C = A.C;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t g0 = (int64_t)blockIdx.x * kPreThreads + wave * 64;
+    // Blocks take the Gaussians from the last block to the first. In a
+    // training step this kernel follows the optimizer update, which walks
+    // them first to last, so the first blocks dispatched read the parameters
+    // written last, which are still in the memory-side cache, before the
+    // rest of this kernel's reads evict them (config 4: 62.5-63.5 -> 58-59 us,
+    // step -4 us).
+    const int64_t g0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * kPreThreads + wave * 64;
     const int64_t g = g0 + lane;
     const bool in = g < A.N;
 
@@ -859,6 +865,16 @@ __device__ __forceinline__ void preprocess_bwd_body(const PreBwdArgs &A) {
     const int64_t g0 = ((int64_t)blockIdx.x * (kPreThreads / 64) + wave) * kGpw;
     const int64_t g = g0 + lane;
     const bool in = lane < kGpw && g < A.N;
+    // With the epilogue every row of the wave's first SH round is read
+    // whatever the gradients, so that round's rows are requested first and
+    // arrive during the prologue's dependent loads and the basis evaluation
+    // (config 4: 275-276 -> 272 us).
+    float4 pf0[3];
+    if (EPI) {
+        const ShRows R0{A.sh, A.rest, A.fused, A.vec4};
+        const int nw0 = (int)max((int64_t)0, min((int64_t)kGpw, A.N - g0));
+        stage_load(R0, g0, min(16, nw0), 0xFFFFu, pf0);
+    }
 
     float mx = 0.f, my = 0.f, mz = 0.f;
     int vld = 0;
@@ -971,7 +987,11 @@ __device__ __forceinline__ void preprocess_bwd_body(const PreBwdArgs &A) {
                 float4 *cb = s_cur[EPI ? wave : 0];
                 float4 pf[3];
                 const uint64_t lm = EPI ? ~0ull : nm;
-                stage_load(R, g0, min(16, nw), (uint32_t)(lm & 0xFFFFu), pf);
+                if (EPI) {
+                    pf[0] = pf0[0]; pf[1] = pf0[1]; pf[2] = pf0[2];
+                } else {
+                    stage_load(R, g0, min(16, nw), (uint32_t)(lm & 0xFFFFu), pf);
+                }
 #pragma unroll 1
                 for (int r = 0; r < 4; ++r) {
                     const int ngr = min(16, max(0, nw - 16 * r));
@@ -1258,7 +1278,7 @@ void preprocess_bwd_kernel(const PreBwdArgs A) {
     preprocess_bwd_body<MIP, STAGE, false>(A);
 }
 
-// The backward with the optimizer epilogue: 166 VGPRs, 3 waves/SIMD, a wave
+// The backward with the optimizer epilogue: 153 VGPRs, 3 waves/SIMD, a wave
 // per kEpiGaussians Gaussians.
 __global__ __launch_bounds__(kPreThreads) __attribute__((amdgpu_waves_per_eu(3)))
 void preprocess_bwd_adam_kernel(const PreBwdArgs A) {
