@@ -542,7 +542,7 @@ def raster_work(step, kern, views=8):
                 uv.shape[0], uv.data_ptr(), conic.data_ptr(), op.data_ptr(), color.data_ptr(),
                 ids.data_ptr(), offs.data_ptr(), W, H, 16, tx, backend.DEFAULT_T_MIN, None,
                 ids.numel(), None, 0, rgb.data_ptr(), alpha.data_ptr(), T.data_ptr(),
-                stop.data_ptr(), None, _lib.stream(uv)))
+                stop.data_ptr(), None, None, _lib.stream(uv)))
             ty_ = torch.arange(H, device=uv.device) // 16
             tx_ = torch.arange(W, device=uv.device) // 16
             tile = ty_[:, None] * tx + tx_[None, :]

@@ -448,16 +448,24 @@ int32_t mg_bin_lists_capped(int64_t N, const float *uv, const float *rxy,
  * zero_grads (device, 16-byte aligned, or NULL): the (N,10) gradient record
  * buffer a later mg_rasterize_backward will fill, cleared by this launch's
  * workgroups on the way (then pass grads_zeroed = 1 to the backward, which
- * skips its own fill). */
+ * skips its own fill).
+ *
+ * sched (device int32, mg_rasterize_sched_ints(W, H, tile) of them, or NULL)
+ * is a backward schedule: the forward records in its first half, per
+ * workgroup, the tile's walk length (its largest stop index minus its first
+ * entry; -1 for a workgroup without a tile), and a backward given the same
+ * buffer runs its tiles longest walk first (see mg_rasterize_backward). It
+ * changes no result of the forward. */
 int64_t mg_rasterize_chunk_workspace_bytes(int64_t n_isect, int32_t n_tiles,
                                            int32_t tile);
+int64_t mg_rasterize_sched_ints(int32_t W, int32_t H, int32_t tile);
 int32_t mg_rasterize_forward(
     int64_t N, const float *uv, const float *conic, const float *opacity,
     const float *color, const int32_t *gauss_ids, const int32_t *tile_offsets,
     int32_t W, int32_t H, int32_t tile, int32_t tiles_x, float t_min,
     const float *background, int64_t n_isect, void *chunk_ws,
     int64_t chunk_ws_bytes, float *out_rgb, float *out_alpha, float *out_T,
-    int32_t *out_stop, float *zero_grads, mg_stream_t stream);
+    int32_t *out_stop, float *zero_grads, int32_t *sched, mg_stream_t stream);
 
 /* Back-to-front replay of mg_rasterize_forward. Replaces rasterize_backward
  * (metal_gauss/csrc/rasterize.mm:147-194; kernel rasterize.metal:173-340),
@@ -474,7 +482,14 @@ int32_t mg_rasterize_forward(
  * grad_alpha. n_isect / chunk_ws / chunk_ws_bytes are the forward's (chunk_ws
  * NULL: one workgroup per tile). grads_zeroed != 0: d_grads was cleared by the
  * forward (its zero_grads), so the backward does not fill it first; 0: the
- * backward zero-fills d_grads itself. */
+ * backward zero-fills d_grads itself. sched (or NULL) is the buffer the
+ * forward recorded the walk lengths in: the backward first orders each XCD's
+ * tiles by them, longest first (a counting sort on the length, exact below
+ * 768 entries, in bins of 32 above; tiles of one bin in no fixed order), into
+ * the buffer's second half, and its workgroups take the tiles in that order,
+ * which shortens the kernel's tail. No effect with chunk_ws, or past 8192
+ * workgroups (1024 per XCD). The gradients are the same up to the order of
+ * the float atomics. */
 int32_t mg_rasterize_backward(
     int64_t N, const float *uv, const float *conic, const float *opacity,
     const float *color, const int32_t *gauss_ids, const int32_t *tile_offsets,
@@ -482,7 +497,7 @@ int32_t mg_rasterize_backward(
     const float *grad_alpha, const float *alpha, const float *background,
     int64_t n_isect, const void *chunk_ws, int64_t chunk_ws_bytes, int32_t W,
     int32_t H, int32_t tile, int32_t tiles_x, float *d_grads, int32_t absgrad,
-    int32_t grads_zeroed, mg_stream_t stream);
+    int32_t grads_zeroed, int32_t *sched, mg_stream_t stream);
 
 /* ------------------------------------------------------------------- Adam */
 

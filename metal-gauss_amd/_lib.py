@@ -85,11 +85,13 @@ _SIGNATURES = {
     "mg_bin_lists_capped": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                    _i32, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
     "mg_rasterize_chunk_workspace_bytes": (_i64, [_i64, _i32, _i32]),
+    "mg_rasterize_sched_ints": (_i64, [_i32, _i32, _i32]),
     "mg_rasterize_forward": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
-                                    _f32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
+                                    _f32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
+                                    _vp]),
     "mg_rasterize_backward": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                      _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _i32,
-                                     _i32, _vp]),
+                                     _i32, _vp, _vp]),
     "mg_adam_step": (_i32, [_vp, _vp, _vp, _vp, _i64, _f64, _f64, _f64, _f64, _i64, _vp]),
     "mg_adam_step_multi": (_i32, [_i32, _pp, _pp, _pp, _pp, ctypes.POINTER(_i64),
                                   ctypes.POINTER(_f64), ctypes.POINTER(_i64), _f64, _f64, _f64,

@@ -564,6 +564,10 @@ class _RasterizeMetal(torch.autograd.Function):
         # follow.
         rec = (torch.empty(N, _REC, device=dev) if N and any(ctx.needs_input_grad[:4])
                else None)
+        # With a backward to come, the forward records each tile's walk
+        # length so that the backward can run the longest walks first.
+        sched = (torch.empty(lib.mg_rasterize_sched_ints(W, H, tile), dtype=torch.int32,
+                             device=dev) if rec is not None and not chunked else None)
         _lib.check(lib.mg_rasterize_forward(
             N, _lib.dev_tensor(uv, "uv"), _lib.dev_tensor(conic, "conic"),
             _lib.dev_tensor(opacity, "opacity"), _lib.dev_tensor(color, "color"),
@@ -572,10 +576,12 @@ class _RasterizeMetal(torch.autograd.Function):
             float(t_min), None if background is None else _lib.f32_array(background),
             n_isect, chunk_ws.data_ptr() if chunked else None, chunk_ws.numel(), rgb.data_ptr(),
             alpha.data_ptr(), T.data_ptr(), stop.data_ptr(),
-            None if rec is None else rec.data_ptr(), _lib.stream(uv)))
+            None if rec is None else rec.data_ptr(),
+            None if sched is None else sched.data_ptr(), _lib.stream(uv)))
         ctx.save_for_backward(uv, conic, opacity, color, gauss_ids, tile_offsets, T, stop,
                               alpha if background is not None else None, chunk_ws)
         ctx.rec = rec
+        ctx.sched = sched
         ctx.dims = (W, H, tile, tiles_x)
         ctx.background = background
         # An output nobody differentiates (alpha, most often) gets no
@@ -598,6 +604,7 @@ class _RasterizeMetal(torch.autograd.Function):
         # One gradient record per Gaussian; autograd gets row views of it.
         rec, zeroed = ctx.rec, ctx.rec is not None
         ctx.rec = None
+        sched = ctx.sched
         if rec is None:
             rec = torch.empty(N, _REC, device=dev)
         if grad_rgb is None and grad_alpha is None:
@@ -612,7 +619,8 @@ class _RasterizeMetal(torch.autograd.Function):
             None if bg is None else alpha.data_ptr(), None if bg is None else _lib.f32_array(bg),
             gauss_ids.numel(), chunk_ws.data_ptr() if chunk_ws.numel() else None,
             chunk_ws.numel(), W, H, tile, tiles_x, rec.data_ptr(),
-            int(ctx.absgrad_out is not None), int(zeroed), _lib.stream(uv)))
+            int(ctx.absgrad_out is not None), int(zeroed),
+            None if sched is None else sched.data_ptr(), _lib.stream(uv)))
         if ctx.absgrad_out is not None:
             ctx.absgrad_out[:N] += rec[:, 9]
         return (rec[:, 0:2], rec[:, 2:5], rec[:, 5], rec[:, 6:9]) + (None,) * 10

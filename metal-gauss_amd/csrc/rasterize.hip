@@ -58,6 +58,10 @@ struct RasterArgs {
     // way, a later backward's gradient records; each workgroup clears a slice.
     float *zero;
     int64_t zero_n;
+    // Optional backward schedule: the forward writes each tile's walk length
+    // (work, n_tiles); the backward's workgroup b takes tile order[b].
+    int32_t *work;
+    const int32_t *order;
 };
 
 __device__ __forceinline__ void tile_pixel(int tid, int tile, int &lx, int &ly, bool &inblk) {
@@ -442,6 +446,73 @@ __global__ __launch_bounds__(1024) void chunk_plan_kernel(const int32_t *offsets
     if (threadIdx.x == 0) P.base[n_tiles] = s_carry;
 }
 
+// ------------------------------------------------- backward tile schedule
+// A backward workgroup lives about as long as its tile's walk, which runs
+// from the tile's largest stop index back to its first entry, and it runs no
+// faster when the CU empties around it: per-workgroup wall-clock stamps at
+// config 4 showed lives of 71 us on average (p90 96, longest 140-220 us),
+// and walks that started late with long tiles left the GPU draining, less
+// than fully occupied, for the last 90 us of a 212-262 us kernel. So the
+// forward records each tile's walk length (work) and, before the backward,
+// one workgroup per XCD orders the tiles that tile_of_block deals that XCD,
+// longest walk first; the backward's workgroup b takes the (b / kXcds)-th
+// tile of XCD b % kXcds's list. Each XCD runs the same tiles as without the
+// schedule (and keeps their L2 reuse); only the order changes, as in
+// longest-processing-time-first scheduling.
+//
+// The buffer holds 2 * grid ints: the forward's workgroup b writes its
+// tile's walk length at [b] (-1 without a tile), the backward's order kernel
+// the tile for workgroup b at [grid + b] (-1: none).
+constexpr int kOrderThreads = 1024;   // most tiles an XCD's list may hold
+constexpr int kOrderBins = 1024;
+
+inline int64_t sched_ints(int grid) { return 2 * (int64_t)grid; }
+inline bool sched_fits(int grid) { return (grid + kXcds - 1) / kXcds <= kOrderThreads; }
+
+// Counting-sort bin of a walk length: exact below 768 entries, 32 entries a
+// bin above, the last bin from 8928 up. A higher bin is a longer walk.
+__device__ __forceinline__ int order_bin(int w) {
+    return w < 768 ? w : min(kOrderBins - 1, 768 + ((w - 768) >> 5));
+}
+
+// One workgroup per XCD: a counting sort of its list by bin, longest first.
+// Tiles of one bin are placed in the order their LDS atomics land.
+__global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(const int32_t *work,
+                                                                   int32_t *order, int grid,
+                                                                   int tiles_x, int tiles_y) {
+    __shared__ uint32_t s_cnt[kOrderBins];
+    __shared__ uint32_t s_wave[kOrderThreads / 64];
+    const int x = blockIdx.x, j = threadIdx.x, lane = j & 63, wave = j >> 6;
+    const int K = (grid - x + kXcds - 1) / kXcds;   // blocks x, x + kXcds, ... below grid
+    const int w = j < K ? work[x + kXcds * j] : -1;
+    for (int i = j; i < kOrderBins; i += kOrderThreads) s_cnt[i] = 0;
+    __syncthreads();
+    const int q = w >= 0 ? order_bin(w) : 0;
+    uint32_t in_bin = 0;
+    if (w >= 0) in_bin = atomicAdd(&s_cnt[q], 1u);
+    __syncthreads();
+    // Thread i scans bin kOrderBins - 1 - i: exclusive starts, longest first.
+    const uint32_t c = s_cnt[kOrderBins - 1 - j];
+    uint32_t incl = c;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t u = (uint32_t)__shfl_up((int)incl, o, 64);
+        if (lane >= o) incl += u;
+    }
+    if (lane == 63) s_wave[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+    for (int v = 0; v < kOrderThreads / 64; ++v) {
+        const uint32_t s = s_wave[v];
+        if (v < wave) before += s;
+        total += s;
+    }
+    s_cnt[kOrderBins - 1 - j] = before + incl - c;
+    __syncthreads();
+    if (w >= 0) order[x + kXcds * (int)(s_cnt[q] + in_bin)] = tile_of_block(x + kXcds * j,
+                                                                            tiles_x, tiles_y);
+    if (j < K && (uint32_t)j >= total) order[x + kXcds * j] = -1;
+}
+
 // Eight waves per SIMD (at most 64 VGPRs; 62 without spills): eight
 // workgroups share a CU (LDS allows nine), so config 4's 2500 tiles take
 // 1.22 rounds of workgroups instead of 1.63 at 73 VGPRs (step -2.5 us).
@@ -467,6 +538,7 @@ __global__ __launch_bounds__(MAXW * 64) __attribute__((amdgpu_waves_per_eu(8))) 
     };
     const int tile_id = tile_of_block(blockIdx.x, A.tiles_x, A.n_tiles / A.tiles_x);
     if (tile_id < 0) {   // whole workgroup
+        if (A.work && threadIdx.x == 0) A.work[blockIdx.x] = -1;
         zero_fill();
         return;
     }
@@ -556,6 +628,19 @@ __global__ __launch_bounds__(MAXW * 64) __attribute__((amdgpu_waves_per_eu(8))) 
             ++unit;
         }
     }
+    if (A.work) {
+        // The backward's walk over this tile starts at its largest stop
+        // index (pixels outside the image keep stop = start).
+        __shared__ int32_t s_wmax[MAXW];
+        const int wm = wave_max_i(stop);
+        if (lane == 0) s_wmax[wave] = wm;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int m = start;
+            for (int w = 0; w < nwaves; ++w) m = max(m, s_wmax[w]);
+            A.work[blockIdx.x] = m - start;
+        }
+    }
     // A tile that turned opaque early: its later chunks end in the final state.
     for (; unit < unit_end; ++unit)
         if (inimg) P.ckpt[(int64_t)unit * tile2 + pslot] = make_float4(T, cr, cg, cb);
@@ -611,8 +696,9 @@ __global__ __launch_bounds__(MAXW * 64) void raster_bwd_kernel(const RasterArgs 
         const int nck = (tile_end - tile_start + kChunk - 1) / kChunk;
         if (chunk < 0 || chunk >= nck || P.base[tile_id] + nck > P.cap) return;
     } else {
-        tile_id = tile_of_block(blockIdx.x, A.tiles_x, A.n_tiles / A.tiles_x);
-        if (tile_id < 0) return;
+        tile_id = A.order ? A.order[blockIdx.x]
+                          : tile_of_block(blockIdx.x, A.tiles_x, A.n_tiles / A.tiles_x);
+        if (tile_id < 0 || tile_id >= A.n_tiles) return;
         tile_start = A.offsets[tile_id];
         tile_end = A.offsets[tile_id + 1];
     }
@@ -950,13 +1036,19 @@ int64_t mg_rasterize_chunk_workspace_bytes(int64_t n_isect, int32_t n_tiles, int
     return chunk_ws_bytes(n_isect, n_tiles, tile);
 }
 
+int64_t mg_rasterize_sched_ints(int32_t W, int32_t H, int32_t tile) {
+    if (W < 1 || H < 1 || tile < 1) return 0;
+    const int tiles_x = (W + tile - 1) / tile, tiles_y = (H + tile - 1) / tile;
+    return sched_ints(raster_grid(tiles_x, tiles_y));
+}
+
 int32_t mg_rasterize_forward(int64_t N, const float *uv, const float *conic, const float *opacity,
                              const float *color, const int32_t *gauss_ids,
                              const int32_t *tile_offsets, int32_t W, int32_t H, int32_t tile,
                              int32_t tiles_x, float t_min, const float *background,
                              int64_t n_isect, void *chunk_ws, int64_t chunk_ws_size,
                              float *out_rgb, float *out_alpha, float *out_T, int32_t *out_stop,
-                             float *zero_grads, mg_stream_t stream) {
+                             float *zero_grads, int32_t *sched, mg_stream_t stream) {
     int32_t rc = check_raster("rasterize_forward", N, uv, conic, opacity, color, gauss_ids,
                               tile_offsets, W, H, tile, tiles_x);
     if (rc != MG_OK) return rc;
@@ -970,6 +1062,7 @@ int32_t mg_rasterize_forward(int64_t N, const float *uv, const float *conic, con
                   background ? background[2] : 0.f}};
     A.zero = N > 0 ? zero_grads : nullptr;
     A.zero_n = (int64_t)kRecFloats * N;
+    A.work = sched;
     hipStream_t s = as_stream(stream);
     ChunkPlan P{nullptr, nullptr, nullptr, 0};
     if (chunk_ws) {
@@ -1001,7 +1094,7 @@ int32_t mg_rasterize_backward(int64_t N, const float *uv, const float *conic,
                               const float *background, int64_t n_isect, const void *chunk_ws,
                               int64_t chunk_ws_size, int32_t W, int32_t H, int32_t tile,
                               int32_t tiles_x, float *d_grads, int32_t absgrad,
-                              int32_t grads_zeroed, mg_stream_t stream) {
+                              int32_t grads_zeroed, int32_t *sched, mg_stream_t stream) {
     int32_t rc = check_raster("rasterize_backward", N, uv, conic, opacity, color, gauss_ids,
                               tile_offsets, W, H, tile, tiles_x);
     if (rc != MG_OK) return rc;
@@ -1035,6 +1128,12 @@ int32_t mg_rasterize_backward(int64_t N, const float *uv, const float *conic,
     }
     const int threads = ((tile * tile + 63) / 64) * 64;
     TimedScope ts("rasterize_backward", s);
+    if (grid > 0 && sched && !chunk_ws && sched_fits(grid)) {
+        int32_t *order = sched + grid;
+        tile_order_kernel<<<kXcds, kOrderThreads, 0, s>>>(sched, order, grid, tiles_x, tiles_y);
+        MG_LAUNCHED("tile_order_kernel");
+        A.order = order;
+    }
     if (grid > 0) {
         // One batch entry per thread (tile 16 and up) takes the pipelined
         // batch loop.

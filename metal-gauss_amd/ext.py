@@ -72,7 +72,7 @@ def rasterize_forward(uv, conic, opacity, color, gauss_ids, tile_offsets, W, H, 
         _dev(color, "input"), _dev(gauss_ids, "input", torch.int32),
         _dev(tile_offsets, "input", torch.int32), W, H, tile, tiles_x, _T_MIN, None,
         gauss_ids.numel(), None, 0, rgb.data_ptr(), alpha.data_ptr(), T.data_ptr(),
-        n_contrib.data_ptr(), None, _lib.stream(uv)))
+        n_contrib.data_ptr(), None, None, _lib.stream(uv)))
     return [rgb, alpha, T, n_contrib]
 
 
@@ -96,7 +96,7 @@ def rasterize_backward(uv, conic, opacity, color, gauss_ids, tile_offsets, final
         _dev(tile_offsets, "input", torch.int32), _dev(final_T, "final_T"),
         _dev(n_contrib, "n_contrib", torch.int32), _dev(grad_rgb, "grad_rgb"),
         _dev(grad_alpha, "grad_alpha"), None, None, gauss_ids.numel(), None, 0, W, H, tile,
-        tiles_x, rec.data_ptr(), int(bool(want_absgrad)), 0, _lib.stream(uv)))
+        tiles_x, rec.data_ptr(), int(bool(want_absgrad)), 0, None, _lib.stream(uv)))
     d_absuv = rec[:, 9].contiguous() if want_absgrad else torch.zeros(1, device=dev)
     return [rec[:, 0:2].contiguous(), rec[:, 2:5].contiguous(), rec[:, 5].contiguous(),
             rec[:, 6:9].contiguous(), d_absuv]

@@ -55,7 +55,7 @@ def test_oversized_tile_is_refused_with_the_reference_message():
 
     lib = _lib.open_library()
     rc = lib.mg_rasterize_forward(0, None, None, None, None, None, 1, 96, 64, 64, 2, 1e-4,
-                                  None, 0, None, 0, 1, 1, 1, 1, None, None)
+                                  None, 0, None, 0, 1, 1, 1, 1, None, None, None)
     assert rc == 1
     assert "threads per threadgroup" in lib.mg_last_error().decode()
 

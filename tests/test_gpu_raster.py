@@ -39,7 +39,7 @@ def prepare(n, seed, W, H, tile, dev, elongate=False, sh=False):
     return uv, conic, op, col, gids, offs, tx
 
 
-def gpu_forward(args, W, H, tile, t_min, background=None, chunked=True):
+def gpu_forward(args, W, H, tile, t_min, background=None, chunked=True, sched=None):
     """mg_rasterize_forward; returns (rgb, alpha, T, stop, chunk workspace or None)."""
     from metal_gauss_amd import _lib
 
@@ -63,11 +63,13 @@ def gpu_forward(args, W, H, tile, t_min, background=None, chunked=True):
                                         None if ws is None else ws.data_ptr(),
                                         0 if ws is None else ws.numel(), rgb.data_ptr(),
                                         alpha.data_ptr(), T.data_ptr(), stop.data_ptr(),
-                                        None, _lib.stream(uv)))
+                                        None, None if sched is None else sched.data_ptr(),
+                                        _lib.stream(uv)))
     return rgb, alpha, T, stop, ws
 
 
-def gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile, absgrad=True, background=None):
+def gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile, absgrad=True, background=None,
+                 sched=None):
     from metal_gauss_amd import _lib
 
     uv, conic, op, col, gids, offs, tx = args
@@ -82,7 +84,8 @@ def gpu_backward(args, fwd, grad_rgb, grad_alpha, W, H, tile, absgrad=True, back
         alpha.data_ptr() if background is not None else None,
         None if background is None else _lib.f32_array(background), gids.numel(),
         None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), W, H, tile, tx,
-        rec.data_ptr(), int(absgrad), 0, _lib.stream(uv)))
+        rec.data_ptr(), int(absgrad), 0, None if sched is None else sched.data_ptr(),
+        _lib.stream(uv)))
     # The record's slots as the reference's five tensors.
     return [rec[:, 0:2], rec[:, 2:5], rec[:, 5], rec[:, 6:9], rec[:, 9] if absgrad else None]
 
@@ -197,6 +200,79 @@ def test_config2_scale_forward_and_backward(dev):
         assert rel_l2(np_(a), b) < 1e-3, f"{name} rel L2 {rel_l2(np_(a), b):.2e}"
 
 
+def _tile_of_block(b, tiles_x, tiles_y, sup=4, xcds=8):
+    """The raster kernels' workgroup -> tile dealing (rasterize.hip
+    tile_of_block): 4x4-tile super-tiles round-robin over the eight XCDs."""
+    xcd, k = b % xcds, b // xcds
+    s = (k // (sup * sup)) * xcds + xcd
+    sx, sy = -(-tiles_x // sup), -(-tiles_y // sup)
+    if s >= sx * sy:
+        return -1
+    loc = k % (sup * sup)
+    x, y = (s % sx) * sup + loc % sup, (s // sx) * sup + loc // sup
+    return y * tiles_x + x if x < tiles_x and y < tiles_y else -1
+
+
+def _order_bin(w):
+    """The schedule's counting-sort bin of a walk length (rasterize.hip
+    order_bin): exact below 768, 32 entries a bin above, capped at 1023."""
+    return w if w < 768 else min(1023, 768 + ((w - 768) >> 5))
+
+
+def test_backward_schedule_config2(dev):
+    """The backward schedule on config 2's full-size lists (2500 tiles):
+    mg_rasterize_forward(sched=) leaves its outputs bit for bit as without it
+    and records, for each workgroup, its tile's walk length max(stop) - first
+    entry (-1 for a workgroup without a tile); the backward given the buffer
+    writes, per XCD, the tiles tile_of_block deals it, each once, longest walk
+    (bin) first, then -1 for the empty slots, and returns the unscheduled
+    backward's gradients up to the order of the float atomics."""
+    from metal_gauss_amd import _lib, scenes
+    from metal_gauss_amd.backend import _PreprocessMetal, _camera, build_tile_lists_metal
+
+    sc, cam, _ = scenes.config2()
+    m, q, sca, op, sh = (t.to(dev) for t in sc.activated())
+    fx, fy, cx, cy, vm_h, cc = _camera(cam.K, cam.viewmat)
+    W, H, tile = cam.W, cam.H, 16
+    with torch.no_grad():
+        uv, conic, depth, rxy, valid, col = _PreprocessMetal.apply(
+            m, q, sca, sh, None, op, vm_h, fx, fy, cx, cy, W, H, 0.01, 100.0, 0.3,
+            float(max(W, H)), cc, 3)
+        gids, offs, tx = build_tile_lists_metal(uv, rxy, depth, valid, conic, op, W, H, tile)
+    args = (uv, conic, op, col, gids, offs, tx)
+    lib = _lib.load()
+    ty = -(-H // tile)
+    grid = -(-(-(-tx // 4) * -(-ty // 4)) // 8) * 8 * 16
+    assert lib.mg_rasterize_sched_ints(W, H, tile) == 2 * grid
+    sched = torch.full((2 * grid,), -7, dtype=torch.int32, device=dev)
+    plain = gpu_forward(args, W, H, tile, 1e-4, chunked=False)
+    fwd = gpu_forward(args, W, H, tile, 1e-4, chunked=False, sched=sched)
+    for a, b in zip(plain[:4], fwd[:4]):
+        assert torch.equal(a, b)
+    stop = np_(fwd[3]).astype(np.int64)
+    o = np_(offs).astype(np.int64)
+    tmax = stop.reshape(ty, tile, tx, tile).max(axis=(1, 3)).reshape(-1)
+    work = np.maximum(tmax, o[:-1]) - o[:-1]
+    dealt = [_tile_of_block(b, tx, ty) for b in range(grid)]
+    assert np_(sched[:grid]).tolist() == [int(work[t]) if t >= 0 else -1 for t in dealt]
+
+    g = torch.Generator().manual_seed(11)
+    grad_rgb = torch.randn(H, W, 3, generator=g).to(dev)
+    want = gpu_backward(args, fwd, grad_rgb, None, W, H, tile)
+    got = gpu_backward(args, fwd, grad_rgb, None, W, H, tile, sched=sched)
+    for name, a, b in zip(("d_uv", "d_conic", "d_opacity", "d_color", "absgrad"), got, want):
+        assert rel_l2(np_(a), np_(b)) < 1e-5, f"{name} rel L2 {rel_l2(np_(a), np_(b)):.2e}"
+
+    order = np_(sched[grid:])
+    for x in range(8):
+        mine = [t for t in dealt[x::8] if t >= 0]
+        lst = order[x::8].tolist()
+        assert sorted(lst[:len(mine)]) == sorted(mine), f"XCD {x}: not its tiles"
+        assert lst[len(mine):] == [-1] * (len(lst) - len(mine)), f"XCD {x}: empty slots"
+        bins = [_order_bin(int(work[t])) for t in lst[:len(mine)]]
+        assert all(a >= b for a, b in zip(bins, bins[1:])), f"XCD {x}: not longest first"
+
+
 def test_background_blend_in_kernel(dev):
     """The in-kernel blend equals the reference's torch expression
     rgb + (1 - alpha).clamp_min(0) * bg (metal_backend.py:539-541), and its
@@ -289,7 +365,8 @@ def test_forward_clears_the_backward_records(dev):
                                         col.data_ptr(), gids.data_ptr(), offs.data_ptr(), W, H,
                                         tile, tx, 1e-4, None, gids.numel(), None, 0,
                                         rgb.data_ptr(), alpha.data_ptr(), T.data_ptr(),
-                                        stop.data_ptr(), rec.data_ptr(), _lib.stream(uv)))
+                                        stop.data_ptr(), rec.data_ptr(), None,
+                                        _lib.stream(uv)))
     torch.cuda.synchronize()
     assert float(rec.abs().max()) == 0.0
     g = torch.Generator().manual_seed(5)
@@ -299,7 +376,7 @@ def test_forward_clears_the_backward_records(dev):
     _lib.check(lib.mg_rasterize_backward(
         N, uv.data_ptr(), conic.data_ptr(), op.data_ptr(), col.data_ptr(), gids.data_ptr(),
         offs.data_ptr(), T.data_ptr(), stop.data_ptr(), grad_rgb.data_ptr(), None, None, None,
-        gids.numel(), None, 0, W, H, tile, tx, rec.data_ptr(), 1, 1, _lib.stream(uv)))
+        gids.numel(), None, 0, W, H, tile, tx, rec.data_ptr(), 1, 1, None, _lib.stream(uv)))
     got = [rec[:, 0:2], rec[:, 2:5], rec[:, 5], rec[:, 6:9], rec[:, 9]]
     for a, b in zip(got, want):
         assert torch.allclose(a, b, rtol=1e-5, atol=1e-7), float((a - b).abs().max())
