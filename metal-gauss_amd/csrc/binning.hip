@@ -1192,9 +1192,10 @@ inline CsPlan cs_plan(int64_t n, int64_t max_chunks = kCsMaxChunks) {
     return {64, ceil_div(n, (int64_t)kCsThreads * 64)};
 }
 
+// Per-chunk counts, the tiles' totals, and the depth sort's tile order.
 inline int64_t tile_sort_ws_bytes(int64_t n, int nb, int64_t max_chunks = kCsMaxChunks) {
     return align256(4 * (int64_t)nb * cs_plan(n, max_chunks).nchunks) +
-           align256(4 * (int64_t)nb);
+           2 * align256(4 * (int64_t)nb);
 }
 
 // V is the value moved with each tile key: an int32 id, or a uint2
@@ -1212,6 +1213,8 @@ struct CsPass {
     // lists_kept(status), read on the device; NULL: n pairs.
     const int64_t *status;
     int64_t chunk;                  // pairs per chunk
+    // Optional: the tiles longest list first, for the per-tile depth sort.
+    int32_t *order;
 };
 
 template <typename V>
@@ -1219,13 +1222,14 @@ __device__ __forceinline__ int64_t cs_count(const CsPass<V> &P) {
     return P.status ? min(lists_kept(P.status), P.n) : P.n;
 }
 
-// Chunks holding pairs: the grid, or for capacity-bounded lists the chunks
-// of the kept pairs (at least one, chunk 0 writing the offsets). Workgroups
-// past them do nothing; the others are dealt to the XCDs in contiguous runs
-// over these chunks alone, so that every XCD gets a share of the work.
+// Chunks holding pairs: all grid chunks, or for capacity-bounded lists the
+// chunks of the kept pairs (at least one, chunk 0 writing the offsets).
+// Workgroups past them do nothing; the others are dealt to the XCDs in
+// contiguous runs over these chunks alone, so that every XCD gets a share of
+// the work.
 template <typename V>
-__device__ __forceinline__ int64_t cs_active(const CsPass<V> &P, int64_t n) {
-    return P.status ? max((int64_t)1, (n + P.chunk - 1) / P.chunk) : (int64_t)gridDim.x;
+__device__ __forceinline__ int64_t cs_active(const CsPass<V> &P, int64_t n, int64_t grid) {
+    return P.status ? max((int64_t)1, (n + P.chunk - 1) / P.chunk) : grid;
 }
 
 // A chunk's tiles as kPer / 4 16-byte loads per thread, all in flight at once
@@ -1253,7 +1257,7 @@ template <int kPer, typename V>
 __global__ __launch_bounds__(kCsThreads) void count_hist_kernel(const CsPass<V> P) {
     __shared__ uint32_t s_h[kCsBuckets];
     const int64_t n = cs_count(P);
-    const int64_t nact = cs_active(P, n);
+    const int64_t nact = cs_active(P, n, (int64_t)gridDim.x);
     if ((int64_t)blockIdx.x >= nact) return;
     const int64_t c = xcd_contiguous(blockIdx.x, nact);
     uint32_t t[kPer];
@@ -1286,7 +1290,7 @@ __global__ __launch_bounds__(64 * kColWaves) void count_colscan_kernel(const CsP
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int bkt = blockIdx.x * 64 + lane;
     const bool in = bkt < P.nb;
-    if (P.status) nchunks = cs_active(P, cs_count(P));
+    if (P.status) nchunks = cs_active(P, cs_count(P), nchunks);
     const int64_t q = (nchunks + kColWaves - 1) / kColWaves;
     const int64_t c0 = wave * q, c1 = min(nchunks, c0 + q);
     if (q <= kColRows) {   // workgroup-uniform
@@ -1343,6 +1347,67 @@ __global__ __launch_bounds__(64 * kColWaves) void count_colscan_kernel(const CsP
     }
 }
 
+// Bin of a list length for the depth sort's order: exact below 64, then 16
+// bins an octave (the four bits below the leading one), the last from 2^18
+// entries up. A higher bin is a longer list.
+__device__ __forceinline__ int len_bin(uint32_t L) {
+    if (L < 64u) return (int)L;
+    const int e = 31 - __builtin_clz(L);
+    return min(255, 64 + 16 * (e - 6) + (int)((L >> (e - 4)) & 15u));
+}
+
+// The per-tile depth sort runs one workgroup per tile, each about as long as
+// its list, in more rounds of workgroups than the GPU holds; taken longest
+// list first, its last round holds the shortest lists (longest-processing-
+// time first). The tile scatter launches one workgroup more than it has
+// chunks, which writes that order from the tiles' totals (complete since the
+// column scan) while the others scatter.
+template <typename V>
+__device__ __forceinline__ void cs_depth_order(const CsPass<V> &P, uint32_t *s_wh,
+                                               uint32_t *s_part) {
+    constexpr int kTPer = kCsBuckets / kCsThreads;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nb = P.nb, t0 = tid * kTPer;
+
+    // A counting sort of the tiles over 256 list-length bins (tiles of one
+    // bin in no fixed order), in the LDS of the scatter's wave counters.
+    if (nb < kCsThreads / kCsWaves) {
+        // Fewer words of wave counters than bins: the tiles in order.
+        for (int i = tid; i < nb; i += kCsThreads) P.order[i] = i;
+        return;
+    }
+    uint32_t *hb = s_wh;   // kCsThreads bins
+    hb[tid] = 0;
+    __syncthreads();
+    int bin[kTPer];
+    uint32_t slot[kTPer];
+#pragma unroll
+    for (int j = 0; j < kTPer; ++j) {
+        const int tt = t0 + j;
+        bin[j] = tt < nb ? len_bin(P.tot[tt]) : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kTPer; ++j)
+        if (bin[j] >= 0) slot[j] = atomicAdd(&hb[bin[j]], 1u);
+    __syncthreads();
+    // Exclusive starts, longest bin first: thread i scans bin 255 - i.
+    const uint32_t cnt = hb[kCsThreads - 1 - tid];
+    uint32_t incl = cnt;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t u = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += u;
+    }
+    if (lane == 63) s_part[wave] = incl;
+    __syncthreads();
+    uint32_t before = incl - cnt;
+    for (int w = 0; w < wave; ++w) before += s_part[w];
+    hb[kCsThreads - 1 - tid] = before;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kTPer; ++j)
+        if (bin[j] >= 0) P.order[hb[bin[j]] + slot[j]] = t0 + j;
+}
+
 template <int kPer, typename V>
 __global__ __launch_bounds__(kCsThreads) void count_scatter_kernel(const CsPass<V> P) {
     constexpr int64_t kChunk = (int64_t)kCsThreads * kPer, kPart = 64 * kPer;
@@ -1354,8 +1419,12 @@ __global__ __launch_bounds__(kCsThreads) void count_scatter_kernel(const CsPass<
     extern __shared__ uint32_t s_wh[];
     __shared__ uint32_t s_part[kCsWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (P.order && blockIdx.x == gridDim.x - 1) {   // the depth sort's order
+        cs_depth_order(P, s_wh, s_part);
+        return;
+    }
     const int64_t n = cs_count(P);
-    const int64_t nact = cs_active(P, n);
+    const int64_t nact = cs_active(P, n, (int64_t)gridDim.x - (P.order ? 1 : 0));
     if ((int64_t)blockIdx.x >= nact) return;
     const int64_t c = xcd_contiguous(blockIdx.x, nact);
     const int64_t pb = c * kChunk + wave * kPart;
@@ -1458,7 +1527,8 @@ __global__ __launch_bounds__(kCsThreads) void count_scatter_kernel(const CsPass<
 template <typename V>
 static int32_t tile_count_sort(const uint32_t *tiles, const V *ids, int64_t n, int n_tiles,
                                V *out, int32_t *tile_offsets, void *ws, int64_t ws_bytes,
-                               hipStream_t s, const int64_t *status = nullptr) {
+                               hipStream_t s, const int64_t *status = nullptr,
+                               int32_t **depth_order = nullptr) {
     MG_REQUIRE(n > 0 && n < (1LL << 31) && n_tiles >= 1 && n_tiles <= kCsBuckets,
                "tile sort: %lld pairs over %d tiles", (long long)n, n_tiles);
     const int64_t max_chunks = status ? kCsMaxChunksCapped : kCsMaxChunks;
@@ -1477,6 +1547,11 @@ static int32_t tile_count_sort(const uint32_t *tiles, const V *ids, int64_t n, i
     P.hist = static_cast<uint32_t *>(ws);
     P.tot = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) +
                                          align256(4 * (int64_t)n_tiles * plan.nchunks));
+    if (depth_order) {
+        P.order = reinterpret_cast<int32_t *>(reinterpret_cast<char *>(P.tot) +
+                                              align256(4 * (int64_t)n_tiles));
+        *depth_order = P.order;
+    }
     P.status = status;
     P.chunk = (int64_t)kCsThreads * plan.per;
     const unsigned grid = (unsigned)plan.nchunks;
@@ -1488,7 +1563,8 @@ static int32_t tile_count_sort(const uint32_t *tiles, const V *ids, int64_t n, i
         count_colscan_kernel<V><<<(unsigned)ceil_div(n_tiles, 64), 64 * kColWaves, 0, s>>>( \
             P, plan.nchunks);                                                          \
         MG_LAUNCHED("count_colscan_kernel");                                           \
-        count_scatter_kernel<PER, V><<<grid, kCsThreads, 4 * kCsWaves * n_tiles, s>>>(P); \
+        count_scatter_kernel<PER, V><<<grid + (P.order ? 1 : 0), kCsThreads,             \
+                                       4 * kCsWaves * n_tiles, s>>>(P);                   \
         MG_LAUNCHED("count_scatter_kernel");                                           \
         break;
     switch (plan.per) {
@@ -1538,6 +1614,7 @@ struct TdArgs {
     uint2 *pairs;                     // {id, depth bits}, grouped by tile (clobbered)
     uint2 *pairs_b;                   // scratch for lists longer than kTdCap
     int32_t *ids;                     // gauss_ids
+    const int32_t *order;             // workgroup -> tile, longest list first (or NULL)
 };
 
 struct TdShared {
@@ -1934,7 +2011,7 @@ __global__ __launch_bounds__(kTdThreads) __attribute__((amdgpu_waves_per_eu(4)))
 tile_depth_sort_kernel(const TdArgs A) {
     __shared__ TdShared S;
     const int tid = threadIdx.x;
-    const int t = (int)xcd_contiguous(blockIdx.x, gridDim.x);
+    const int t = A.order ? A.order[blockIdx.x] : (int)xcd_contiguous(blockIdx.x, gridDim.x);
     const int64_t s0 = A.offsets[t];
     const int64_t len = (int64_t)A.offsets[t + 1] - s0;
     if (len <= 0) return;   // workgroup-uniform
@@ -2045,9 +2122,10 @@ static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
     }
     // The tile-sorted pairs, and the other region (the long lists' scratch).
     uint2 *sorted = pairs_b, *scratch = pairs_a;
+    int32_t *order = nullptr;
     if (counting) {
         rc = tile_count_sort<uint2>(tk_a, pairs_a, n, n_tiles, pairs_b, tile_offsets, sort_ws,
-                                    sort_bytes, s, status);
+                                    sort_bytes, s, status, &order);
         if (rc != MG_OK) return rc;
     } else {
         rc = radix_sort_passes<uint32_t, uint2>(
@@ -2062,7 +2140,7 @@ static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
             MG_LAUNCHED("tile_ranges_u32_kernel");
         }
     }
-    TdArgs D{tile_offsets, sorted, scratch, gauss_ids};
+    TdArgs D{tile_offsets, sorted, scratch, gauss_ids, order};
     TimedScope ts("depth_sort", s);
     tile_depth_sort_kernel<<<(unsigned)n_tiles, kTdThreads, 0, s>>>(D);
     MG_LAUNCHED("tile_depth_sort_kernel");
