@@ -484,7 +484,10 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(const int32_t
     __shared__ uint32_t s_wave[kOrderThreads / 64];
     const int x = blockIdx.x, j = threadIdx.x, lane = j & 63, wave = j >> 6;
     const int K = (grid - x + kXcds - 1) / kXcds;   // blocks x, x + kXcds, ... below grid
-    const int w = j < K ? work[x + kXcds * j] : -1;
+    // Which slots hold a tile comes from the dealing itself, so a buffer the
+    // forward did not fill can only reorder the tiles, never drop one.
+    const int tb = j < K ? tile_of_block(x + kXcds * j, tiles_x, tiles_y) : -1;
+    const int w = tb >= 0 ? max(work[x + kXcds * j], 0) : -1;
     for (int i = j; i < kOrderBins; i += kOrderThreads) s_cnt[i] = 0;
     __syncthreads();
     const int q = w >= 0 ? order_bin(w) : 0;
@@ -508,8 +511,7 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(const int32_t
     }
     s_cnt[kOrderBins - 1 - j] = before + incl - c;
     __syncthreads();
-    if (w >= 0) order[x + kXcds * (int)(s_cnt[q] + in_bin)] = tile_of_block(x + kXcds * j,
-                                                                            tiles_x, tiles_y);
+    if (w >= 0) order[x + kXcds * (int)(s_cnt[q] + in_bin)] = tb;
     if (j < K && (uint32_t)j >= total) order[x + kXcds * j] = -1;
 }
 

@@ -226,7 +226,8 @@ def test_backward_schedule_config2(dev):
     entry (-1 for a workgroup without a tile); the backward given the buffer
     writes, per XCD, the tiles tile_of_block deals it, each once, longest walk
     (bin) first, then -1 for the empty slots, and returns the unscheduled
-    backward's gradients up to the order of the float atomics."""
+    backward's gradients up to the order of the float atomics, also from a
+    buffer of garbage the forward never wrote."""
     from metal_gauss_amd import _lib, scenes
     from metal_gauss_amd.backend import _PreprocessMetal, _camera, build_tile_lists_metal
 
@@ -262,6 +263,11 @@ def test_backward_schedule_config2(dev):
     got = gpu_backward(args, fwd, grad_rgb, None, W, H, tile, sched=sched)
     for name, a, b in zip(("d_uv", "d_conic", "d_opacity", "d_color", "absgrad"), got, want):
         assert rel_l2(np_(a), np_(b)) < 1e-5, f"{name} rel L2 {rel_l2(np_(a), np_(b)):.2e}"
+    # A buffer the forward never filled only reorders the tiles.
+    junk = torch.randint(-2**31, 2**31 - 1, (2 * grid,), generator=g, dtype=torch.int32).to(dev)
+    got_junk = gpu_backward(args, fwd, grad_rgb, None, W, H, tile, sched=junk)
+    for name, a, b in zip(("d_uv", "d_conic", "d_opacity", "d_color", "absgrad"), got_junk, want):
+        assert rel_l2(np_(a), np_(b)) < 1e-5, f"junk schedule: {name}"
 
     order = np_(sched[grid:])
     for x in range(8):
