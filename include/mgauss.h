@@ -489,7 +489,8 @@ int32_t mg_rasterize_forward(
  * the buffer's second half, and its workgroups take the tiles in that order,
  * which shortens the kernel's tail. No effect with chunk_ws, or past 8192
  * workgroups (1024 per XCD). The gradients are the same up to the order of
- * the float atomics. */
+ * the float atomics, whatever the buffer holds (contents the forward did not
+ * write only change the order). */
 int32_t mg_rasterize_backward(
     int64_t N, const float *uv, const float *conic, const float *opacity,
     const float *color, const int32_t *gauss_ids, const int32_t *tile_offsets,
