@@ -128,6 +128,10 @@ int32_t mg_preprocess_backward(
  *     takes scales and opacities as given.
  * opacity_eff (N,) receives the opacity binning and compositing use. rxy and
  * valid see the opacity after the 3D filter and before the 2D one, as in the
+ * reference.
+ * block_work (device, ceil(N/256) int32, or NULL; needs tile >= 1) receives
+ * per 256 Gaussians an estimate of mg_bin_lists_capped's work over tiles of
+ * `tile` pixels, for its block_work argument. No counterpart in the
  * reference. */
 int32_t mg_preprocess_forward_mip(
     int64_t N, const float *means, const float *quats, const float *scales,
@@ -138,7 +142,7 @@ int32_t mg_preprocess_forward_mip(
     int32_t sh_degree, const float *filter_3d, int32_t antialias,
     int32_t activations, float *uv, float *conic, float *depth, float *rxy,
     int32_t *valid, uint8_t *valid_mask, float *color, float *opacity_eff,
-    mg_stream_t stream);
+    int32_t tile, int32_t *block_work, mg_stream_t stream);
 
 /* Optional optimizer epilogue of mg_preprocess_backward_mip. The reference's
  * trainer runs FusedAdam after the backward (train.py:400-402, adam.metal);
@@ -414,6 +418,9 @@ int32_t mg_bin_lists_finish(int64_t N, const float *uv, const float *rxy,
  * from hipHostMalloc) receives the same two words and then tag in
  * status_host[2] with a system-scope release, so the host can wait for the
  * words by polling for the tag, with no copy or event on the stream.
+ * block_work (device, ceil(N/256) int32, or NULL) orders the count and write
+ * passes' blocks of 256 Gaussians heaviest first (mg_preprocess_forward_mip
+ * writes it); any contents give the same lists, they only reorder the work.
  * Replaces the .item() read that sizes the reference's pair buffers
  * (metal_gauss/metal_backend.py:246-248) with a device-side check. */
 int64_t mg_bin_lists_capped_workspace_bytes(int64_t N, int64_t capacity);
@@ -425,7 +432,8 @@ int32_t mg_bin_lists_capped(int64_t N, const float *uv, const float *rxy,
                             int32_t *gauss_ids, int32_t *tile_offsets,
                             int64_t *status, int64_t *status_host,
                             int64_t tag, void *workspace,
-                            int64_t workspace_bytes, mg_stream_t stream);
+                            int64_t workspace_bytes, const int32_t *block_work,
+                            mg_stream_t stream);
 
 /* -------------------------------------------------------------- rasteriser */
 

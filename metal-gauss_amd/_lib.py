@@ -48,7 +48,7 @@ _SIGNATURES = {
     "mg_preprocess_forward_mip": (_i32, [
         _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _f32, _f32, _i32, _i32,
         _f32, _f32, _f32, _f32, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-        _vp, _vp]),
+        _vp, _i32, _vp, _vp]),
     "mg_preprocess_backward_mip": (_i32, [
         _i64, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _f32, _f32,
         _f32, _i32, _i32, _f32, _f32, _f32, _f32, _vp, _i32, _vp, _vp, _i32, _i32, _f32, _f32,
@@ -83,7 +83,8 @@ _SIGNATURES = {
                                    _i32, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
     "mg_bin_lists_capped_workspace_bytes": (_i64, [_i64, _i64]),
     "mg_bin_lists_capped": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
-                                   _i32, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
+                                   _i32, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp,
+                                   _vp]),
     "mg_rasterize_chunk_workspace_bytes": (_i64, [_i64, _i32, _i32]),
     "mg_rasterize_sched_ints": (_i64, [_i32, _i32, _i32]),
     "mg_rasterize_forward": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,

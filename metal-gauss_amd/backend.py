@@ -149,13 +149,21 @@ def _bin(uv, rxy, depth, valid_i, conic, opacity, W, H, tile):
     return gauss_ids, tile_offsets, tx
 
 
+# Tile count past which render orders the capacity lists' binning blocks by
+# their estimated work: below it the heavy blocks are not long enough to
+# trail the count and write passes.
+_BLOCK_ORDER_TILES = 4096
+
+
 def _bin_capped(uv, rxy, depth, valid_i, conic, opacity, W, H, tile, capacity,
-                host_slot=None, tag=0):
+                host_slot=None, tag=0, block_work=None):
     """The lists of ``_bin`` with no host read (mg_bin_lists_capped): ids in a
     (capacity,) buffer, and a device int64 (2,) status = (intersection
     total, 1 if it exceeded ``capacity`` else 0). After an overflow every
     list is empty. ``host_slot`` (an address of 3 int64 of pinned host
-    memory) also receives the two words and then ``tag``. Returns
+    memory) also receives the two words and then ``tag``. ``block_work``
+    (int32, one per 256 Gaussians, or None) orders the passes' blocks
+    heaviest first; it does not change the lists. Returns
     (gauss_ids, tile_offsets, tiles_x, status)."""
     lib = _lib.load()
     device = uv.device
@@ -177,7 +185,9 @@ def _bin_capped(uv, rxy, depth, valid_i, conic, opacity, W, H, tile, capacity,
         _lib.dev_tensor(valid_i, "valid", torch.int32), _lib.dev_tensor(depth, "depth"),
         W, H, tile, tx, ty, capacity, gauss_ids.data_ptr() if capacity else None,
         tile_offsets.data_ptr(), status.data_ptr(), host_slot, int(tag), ws.data_ptr(),
-        ws.numel(), s))
+        ws.numel(),
+        None if block_work is None else _lib.dev_tensor(block_work, "block_work", torch.int32),
+        s))
     return gauss_ids, tile_offsets, tx, status
 
 
@@ -649,7 +659,7 @@ class _PreprocessMip(torch.autograd.Function):
     def forward(ctx, means, quats, scales, opacities, sh, sh_rest, filter_3d, antialias,
                 viewmat, fx, fy, cx, cy, W, H, near, far, blur, max_radius, cam_center,
                 sh_degree, valid_mask=None, activations=0, optimizer=None, reg=None,
-                lists=None):
+                lists=None, block_work=None):
         lib = _lib.load()
         N = means.shape[0]
         dev = means.device
@@ -684,7 +694,8 @@ class _PreprocessMip(torch.autograd.Function):
             int(activations), uv.data_ptr(), conic.data_ptr(), depth.data_ptr(), rxy.data_ptr(), valid.data_ptr(),
             None if valid_mask is None else _lib.dev_tensor(valid_mask, "valid_mask", torch.bool),
             None if color is None else color.data_ptr(), op_eff.data_ptr(),
-            _lib.stream(means)))
+            block_work[0] if block_work else 0,
+            block_work[1].data_ptr() if block_work else None, _lib.stream(means)))
         ctx.save_for_backward(means, quats, scales, opacities, sh, rest, filt, valid)
         ctx.set_materialize_grads(False)
         ctx.fused = fused
@@ -729,7 +740,7 @@ class _PreprocessMip(torch.autograd.Function):
                 opacities.data_ptr(), None if filt is None else filt.data_ptr(),
                 int(ctx.antialias), ctx.activations, *ctx.reg, p_oe, None, None, None, None,
                 None, None, ctypes.byref(epi), _lib.stream(means)))
-            return (None,) * 26
+            return (None,) * 27
         d_means = torch.empty(N, 3, device=dev)
         d_quats = torch.empty(N, 4, device=dev)
         d_scales = torch.empty(N, 3, device=dev)
@@ -749,7 +760,7 @@ class _PreprocessMip(torch.autograd.Function):
             d_scales.data_ptr(), None if d_sh is None else d_sh.data_ptr(),
             None if d_rest is None else d_rest.data_ptr(), d_op.data_ptr(), None,
             _lib.stream(means)))
-        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 20
+        return (d_means, d_quats, d_scales, d_op, d_sh, d_rest) + (None,) * 21
 
 
 def _reg_coefficients(reg, n):
@@ -927,6 +938,15 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
         reg = (float(opacity_reg), float(scale_reg))
     # The epilogue's skip word, filled in once the lists are built.
     lists = [None] if list_capacity is not None else None
+    # Past _BLOCK_ORDER_TILES tiles the capacity lists' count and write passes
+    # take their blocks of 256 Gaussians heaviest first, from a per-block
+    # work estimate the projection kernel writes (the mip projection only).
+    block_work = None
+    if list_capacity is not None:
+        tx, ty = _tile_grid(W, H, tile)
+        if tx * ty > _BLOCK_ORDER_TILES and means.shape[0] > 0:
+            block_work = (tile, torch.empty((means.shape[0] + 255) // 256, dtype=torch.int32,
+                                            device=means.device))
     if (filter_3d is not None or antialias or activations or optimizer is not None
             or reg is not None):
         # Both filters (and the activations) in the projection kernel; the
@@ -937,20 +957,22 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
             uv, conic, depth, rxy, valid_i, opacities = _PreprocessMip.apply(
                 means, quats, scales, opacities, None, None, filter_3d, antialias, vm_h, fx,
                 fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree, valid_b,
-                act, None, reg)
+                act, None, reg, None, block_work)
             colors = colors.contiguous()
         else:
             sh_in, rest_in = _sh_inputs(sh, sh_rest)
             uv, conic, depth, rxy, valid_i, colors, opacities = _PreprocessMip.apply(
                 means, quats, scales, opacities, sh_in, rest_in, filter_3d, antialias, vm_h,
                 fx, fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree,
-                valid_b, act, optimizer, reg, lists)
+                valid_b, act, optimizer, reg, lists, block_work)
     elif explicit_colors:
+        block_work = None
         uv, conic, depth, rxy, valid_i = _PreprocessMetal.apply(
             means, quats, scales, None, None, opacities.detach(), vm_h, fx, fy, cx, cy, W, H,
             near, far, 0.3, max_radius, cam_center, sh_degree, valid_b)
         colors = colors.contiguous()
     else:
+        block_work = None
         sh_in, rest_in = _sh_inputs(sh, sh_rest)
         uv, conic, depth, rxy, valid_i, colors = _PreprocessMetal.apply(
             means, quats, scales, sh_in, rest_in, opacities.detach(), vm_h, fx, fy, cx, cy,
@@ -970,7 +992,7 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
         gauss_ids, tile_offsets, tiles_x, status = _bin_capped(
             uv.detach().contiguous(), rxy.detach().contiguous(), depth.detach().contiguous(),
             valid_i.contiguous(), conic.detach().contiguous(), opacities.detach().contiguous(),
-            W, H, tile, capacity, slot, tag)
+            W, H, tile, capacity, slot, tag, None if block_work is None else block_work[1])
         lists[0] = status
 
     # A constant background (tuple, list or CPU tensor without grad) is

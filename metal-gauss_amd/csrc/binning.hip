@@ -648,13 +648,85 @@ __device__ __forceinline__ uint32_t wave_small_claims(const BinRec &r, int ar, b
     return w_msk[lane];
 }
 
+// The count and write passes' workgroup order, from a per-block work
+// estimate (the tiles a block's rectangles cover, which the projection can
+// emit): heaviest block first, so that the few blocks whose wave walks span
+// thousands of tiles start at once instead of trailing the launch. One
+// workgroup counting-sorts the blocks over kBlkBins bins: exact below 256,
+// then 32 bins per octave. Every block lands in order exactly once, whatever
+// the estimates hold (a negative one counts as 0): they only reorder the
+// blocks, and both passes index their outputs by block, not by workgroup.
+constexpr int kBlkOrderThreads = 1024, kBlkBins = 1024, kBlkPer = 16;
+
+__device__ __forceinline__ int block_bin(int32_t w) {
+    const uint32_t L = (uint32_t)max(w, 0);
+    if (L < 256u) return (int)L;
+    const int e = 31 - __builtin_clz(L);
+    return min(kBlkBins - 1, 256 + 32 * (e - 8) + (int)((L >> (e - 5)) & 31u));
+}
+
+__global__ __launch_bounds__(kBlkOrderThreads) void block_order_kernel(
+    const int32_t *__restrict__ block_work, int64_t nparts, int32_t *__restrict__ order) {
+    __shared__ uint32_t s_cnt[kBlkBins];
+    __shared__ uint32_t s_wave[kBlkOrderThreads / 64];
+    const int j = threadIdx.x, lane = j & 63, wave = j >> 6;
+    constexpr int64_t kBatch = (int64_t)kBlkOrderThreads * kBlkPer;
+    s_cnt[j] = 0;   // nparts >= 1
+    __syncthreads();
+    // Each batch's loads are issued together, then binned.
+    for (int64_t b0 = 0; b0 < nparts; b0 += kBatch) {
+        int bin[kBlkPer];
+#pragma unroll
+        for (int r = 0; r < kBlkPer; ++r) {
+            // Every load in range and its value always used (negative past
+            // nparts), so no branch separates the batch's loads.
+            const int64_t i = b0 + j + (int64_t)kBlkOrderThreads * r;
+            bin[r] = block_bin(block_work[min(i, nparts - 1)]) - (i < nparts ? 0 : 4096);
+        }
+#pragma unroll
+        for (int r = 0; r < kBlkPer; ++r)
+            if (bin[r] >= 0) atomicAdd(&s_cnt[bin[r]], 1u);
+    }
+    __syncthreads();
+    // Exclusive scan over the bins from the heaviest down: thread j owns bin
+    // kBlkBins - 1 - j.
+    const uint32_t c = s_cnt[kBlkBins - 1 - j];
+    uint32_t incl = c;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t u = (uint32_t)__shfl_up((int)incl, o, 64);
+        if (lane >= o) incl += u;
+    }
+    if (lane == 63) s_wave[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0;
+    for (int v = 0; v < wave; ++v) before += s_wave[v];
+    s_cnt[kBlkBins - 1 - j] = before + incl - c;
+    __syncthreads();
+    for (int64_t b0 = 0; b0 < nparts; b0 += kBatch) {
+        int bin[kBlkPer];
+#pragma unroll
+        for (int r = 0; r < kBlkPer; ++r) {
+            // Every load in range and its value always used (negative past
+            // nparts), so no branch separates the batch's loads.
+            const int64_t i = b0 + j + (int64_t)kBlkOrderThreads * r;
+            bin[r] = block_bin(block_work[min(i, nparts - 1)]) - (i < nparts ? 0 : 4096);
+        }
+#pragma unroll
+        for (int r = 0; r < kBlkPer; ++r) {
+            if (bin[r] >= 0)
+                order[atomicAdd(&s_cnt[bin[r]], 1u)] =
+                    (int32_t)(b0 + j + (int64_t)kBlkOrderThreads * r);
+        }
+    }
+}
+
 // Count pass in Gaussian order (coalesced reads): the tile count and the
 // walk record (with a small rectangle's claim mask, or a large one's kept
 // step words); per workgroup the intersection total. At most 80 VGPRs, so
 // six waves fit per SIMD.
 __global__ __launch_bounds__(kBinThreads) __attribute__((amdgpu_waves_per_eu(6))) void
 bin_count_rec_kernel(const BinArgs A, int32_t *counts, BinRec *recs, uint32_t *masks,
-                     uint64_t *words, BinPart *parts) {
+                     uint64_t *words, BinPart *parts, const int32_t *order) {
     __shared__ BinPart s_p[kBinThreads / 64];
     __shared__ BinRec s_rec[kBinThreads];
     __shared__ int32_t s_big[kBinThreads], s_cnt[kBinThreads];
@@ -665,7 +737,9 @@ bin_count_rec_kernel(const BinArgs A, int32_t *counts, BinRec *recs, uint32_t *m
     // boundaries.
     __shared__ float4 s_rows[kBinThreads / 64][kRowSlots];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t g = (int64_t)blockIdx.x * kBinThreads + tid;
+    // The block of 256 Gaussians this workgroup takes (see block_order_kernel).
+    const int64_t blk = order ? order[blockIdx.x] : blockIdx.x;
+    const int64_t g = blk * kBinThreads + tid;
     const bool test = A.conic != nullptr;
     if (tid == 0) {
         s_nbig = 0;
@@ -713,7 +787,7 @@ bin_count_rec_kernel(const BinArgs A, int32_t *counts, BinRec *recs, uint32_t *m
         if (lane == 0) first = atomicAdd(&s_used, min(nst, kBlockWords + 1));
         first = __builtin_amdgcn_readfirstlane(first);
         const bool keep = first + nst <= kBlockWords;
-        uint64_t *const wp = words + (int64_t)blockIdx.x * kBlockWords + first;
+        uint64_t *const wp = words + blk * kBlockWords + first;
         int cnt = 0, t = 0;
         strip_walk(r, P, test, A.tile, A.W, A.H, s_rows[wave], lane,
                    [&](bool claim, int, int) {
@@ -743,7 +817,7 @@ bin_count_rec_kernel(const BinArgs A, int32_t *counts, BinRec *recs, uint32_t *m
     if (threadIdx.x == 0) {
         BinPart b = s_p[0];
         for (int w = 1; w < kBinThreads / 64; ++w) b.total += s_p[w].total;
-        parts[blockIdx.x] = b;
+        parts[blk] = b;
     }
 }
 
@@ -868,7 +942,8 @@ __device__ __forceinline__ void block_excl_sum_max(int vs, int vm, int &ex_s, in
 __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
     const BinRec *recs, const int32_t *counts, const uint32_t *masks, const uint64_t *words,
     const int64_t *part_off, int64_t N, int tile, int W, int H, int tiles_x, int test,
-    uint32_t *tkeys, int32_t *ids, const float *depth, uint2 *pairs, const int64_t *status) {
+    uint32_t *tkeys, int32_t *ids, const float *depth, uint2 *pairs, const int64_t *status,
+    const int32_t *order) {
     // Capacity-bounded lists that overflowed emit nothing.
     if (status && status[1] != 0) return;
     // The staging windows' arrays hold, until the small runs are staged:
@@ -900,9 +975,10 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
         s_csum[kBinThreads / 64], s_sc[2 * (kBinThreads / 64)];
     __shared__ uint32_t s_dk[kBinThreads];   // depth bits of the workgroup's Gaussians
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t k0 = (int64_t)blockIdx.x * kBinThreads;
+    const int64_t blk = order ? order[blockIdx.x] : blockIdx.x;   // as in bin_count
+    const int64_t k0 = blk * kBinThreads;
     const int64_t k = k0 + tid;
-    const int64_t base = part_off[blockIdx.x];
+    const int64_t base = part_off[blk];
     if (pairs) s_dk[tid] = k < N ? __float_as_uint(depth[k]) : 0u;
     if (tid == 0) {
         s_nbig = 0;
@@ -990,7 +1066,7 @@ __global__ __launch_bounds__(kBinThreads) void bin_write_rec_kernel(
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int i = i0 + q;
-            v[q] = i < wext ? words[(int64_t)blockIdx.x * kBlockWords + i] : 0ull;
+            v[q] = i < wext ? words[blk * kBlockWords + i] : 0ull;
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -2040,6 +2116,7 @@ struct BeginWs {
     BinPart *parts;
     int64_t *part_off;
     BinStats *stats;
+    int32_t *order;     // the blocks' processing order (with a block work estimate)
     int64_t bytes;
     BeginWs(void *base, int64_t N) {
         char *p = static_cast<char *>(base);
@@ -2053,6 +2130,7 @@ struct BeginWs {
         parts = (BinPart *)take((int64_t)sizeof(BinPart) * nparts);
         part_off = (int64_t *)take(8 * nparts);
         stats = (BinStats *)take(sizeof(BinStats));
+        order = (int32_t *)take(4 * nparts);
         bytes = off;
     }
 };
@@ -2094,7 +2172,8 @@ static int64_t finish_sort_bytes(int64_t T, bool capped) {
 static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
                              const float *depth, int W, int H, int tile, int tiles_x,
                              int n_tiles, int64_t n, const int64_t *status, int32_t *gauss_ids,
-                             int32_t *tile_offsets, void *finish_workspace, hipStream_t s) {
+                             int32_t *tile_offsets, void *finish_workspace, hipStream_t s,
+                             const int32_t *block_order = nullptr) {
     const int64_t T = n > 0 ? n : 1;
     const int64_t T4 = align256(4 * T);
     char *f = static_cast<char *>(finish_workspace);
@@ -2117,7 +2196,7 @@ static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
         TimedScope ts("bin_write", s);
         bin_write_rec_kernel<<<(unsigned)ceil_div(N, kBinThreads), kBinThreads, 0, s>>>(
             ws.recs, ws.counts, ws.masks, ws.words, ws.part_off, N, tile, W, H, tiles_x,
-            conic != nullptr ? 1 : 0, tk_a, nullptr, depth, pairs_a, status);
+            conic != nullptr ? 1 : 0, tk_a, nullptr, depth, pairs_a, status, block_order);
         MG_LAUNCHED("bin_write_rec_kernel");
     }
     // The tile-sorted pairs, and the other region (the long lists' scratch).
@@ -2267,9 +2346,8 @@ int32_t mg_bin_lists_begin(int64_t N, const float *uv, const float *rxy, const f
     const int64_t nparts = N > 0 ? ceil_div(N, kBinThreads) : 0;
     if (N > 0) {
         TimedScope ts("bin_count", s);
-        bin_count_rec_kernel<<<(unsigned)nparts, kBinThreads, 0, s>>>(A, ws.counts, ws.recs,
-                                                                       ws.masks, ws.words,
-                                                                       ws.parts);
+        bin_count_rec_kernel<<<(unsigned)nparts, kBinThreads, 0, s>>>(
+            A, ws.counts, ws.recs, ws.masks, ws.words, ws.parts, nullptr);
         MG_LAUNCHED("bin_count_rec_kernel");
     }
     {
@@ -2335,7 +2413,8 @@ int32_t mg_bin_lists_capped(int64_t N, const float *uv, const float *rxy, const 
                             int32_t W, int32_t H, int32_t tile, int32_t tiles_x, int32_t tiles_y,
                             int64_t capacity, int32_t *gauss_ids, int32_t *tile_offsets,
                             int64_t *status, int64_t *status_host, int64_t tag,
-                            void *workspace, int64_t workspace_bytes, mg_stream_t stream) {
+                            void *workspace, int64_t workspace_bytes,
+                            const int32_t *block_work, mg_stream_t stream) {
     int32_t rc = check_bin_args("mg_bin_lists_capped", N, uv, rxy, conic, opacity, valid, W, H,
                                 tile, tiles_x, tiles_y);
     if (rc != MG_OK) return rc;
@@ -2352,11 +2431,15 @@ int32_t mg_bin_lists_capped(int64_t N, const float *uv, const float *rxy, const 
     hipStream_t s = as_stream(stream);
     BinArgs A{N, uv, rxy, conic, opacity, depth, valid, W, H, tile, tiles_x, tiles_y};
     const int64_t nparts = N > 0 ? ceil_div(N, kBinThreads) : 0;
+    const int32_t *order = (block_work && N > 0) ? ws.order : nullptr;
     if (N > 0) {
         TimedScope ts("bin_count", s);
-        bin_count_rec_kernel<<<(unsigned)nparts, kBinThreads, 0, s>>>(A, ws.counts, ws.recs,
-                                                                       ws.masks, ws.words,
-                                                                       ws.parts);
+        if (order) {
+            block_order_kernel<<<1, kBlkOrderThreads, 0, s>>>(block_work, nparts, ws.order);
+            MG_LAUNCHED("block_order_kernel");
+        }
+        bin_count_rec_kernel<<<(unsigned)nparts, kBinThreads, 0, s>>>(
+            A, ws.counts, ws.recs, ws.masks, ws.words, ws.parts, order);
         MG_LAUNCHED("bin_count_rec_kernel");
     }
     {
@@ -2368,7 +2451,7 @@ int32_t mg_bin_lists_capped(int64_t N, const float *uv, const float *rxy, const 
     }
     return emit_and_sort(ws, N, conic, depth, W, H, tile, tiles_x, tiles_x * tiles_y,
                          N > 0 ? capacity : 0, status, gauss_ids, tile_offsets,
-                         static_cast<char *>(workspace) + ws.bytes, s);
+                         static_cast<char *>(workspace) + ws.bytes, s, order);
 }
 
 }  // extern "C"

@@ -498,7 +498,31 @@ struct PreFwdArgs {
     int32_t aa;
     float *op_eff;
     int32_t act;   // kActLogScale | kActLogitOpac (effective-opacity kernel only)
+    // Optional: per block of kPreThreads Gaussians, an estimate of the
+    // binning's work over tiles of `tile` pixels (see block_work_of).
+    int32_t *block_work;
+    int32_t tile;
 };
+
+// The binning's count and write passes take a workgroup per block of 256
+// Gaussians, and a block's time grows with the tiles its rectangles cover: a
+// wave walks each rectangle over 32 tiles, which near the camera can span
+// thousands. Each visible Gaussian counts the tiles of its clamped
+// rectangle (as the binning forms it, rounded the same way for tiles of a
+// power of two), or 4 for a rectangle the count pass tests lane-parallel.
+__device__ __forceinline__ int block_work_of(bool ok, float u, float v, float rx, float ry,
+                                             int tile, int W, int H) {
+    if (!ok) return 0;
+    const int tx = (W + tile - 1) / tile, ty = (H + tile - 1) / tile;
+    const float it = 1.0f / (float)tile;
+    const int x0 = min(max((int)floorf((u - rx) * it), 0), tx - 1);
+    const int x1 = min(max((int)floorf((u + rx) * it), 0), tx - 1);
+    const int y0 = min(max((int)floorf((v - ry) * it), 0), ty - 1);
+    const int y1 = min(max((int)floorf((v + ry) * it), 0), ty - 1);
+    // Capped so that a block's sum stays well inside int32.
+    const int64_t area = (int64_t)(x1 - x0 + 1) * (y1 - y0 + 1);
+    return area > 32 ? (int)min(area, (int64_t)1 << 22) : 4;
+}
 
 template <bool MIP>
 __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFwdArgs A) {
@@ -516,6 +540,7 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFw
 
     // ------------------------------------------ projection: lane = Gaussian
     bool ok = false;
+    int bwork = 0;
     float mx = 0.f, my = 0.f, mz = 0.f;
     if (in) {
         mx = A.means[3 * g]; my = A.means[3 * g + 1]; mz = A.means[3 * g + 2];
@@ -565,6 +590,18 @@ __global__ __launch_bounds__(kPreThreads) void preprocess_fwd_kernel(const PreFw
         A.valid[g] = ok ? 1 : 0;
         if (A.valid_mask) A.valid_mask[g] = ok ? 1 : 0;
         if (MIP) A.op_eff[g] = A.aa ? op * mip2_coef(P) : op;
+        if (A.block_work) bwork = block_work_of(ok, u, v, rx, ry, A.tile, C.W, C.H);
+    }
+    if (A.block_work) {   // workgroup-uniform
+        __shared__ int32_t s_work[kPreThreads / 64];
+        for (int o = 32; o >= 1; o >>= 1) bwork += __shfl_xor(bwork, o, 64);
+        if (lane == 0) s_work[wave] = bwork;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int sum = 0;
+            for (int w = 0; w < kPreThreads / 64; ++w) sum += s_work[w];
+            A.block_work[gridDim.x - 1 - blockIdx.x] = sum;
+        }
     }
 
     if (A.sh == nullptr) return;   // explicit-colour callers: no SH, no colour
@@ -1313,7 +1350,8 @@ static int32_t preprocess_fwd(int64_t N, const float *means, const float *quats,
                               const float *filter_3d, int32_t antialias, int32_t activations,
                               float *uv, float *conic, float *depth, float *rxy,
                               int32_t *valid, uint8_t *valid_mask, float *color,
-                              float *opacity_eff, mg_stream_t stream, const char *who) {
+                              float *opacity_eff, mg_stream_t stream, const char *who,
+                              int32_t tile = 0, int32_t *block_work = nullptr) {
     PreFwdArgs A{};
     int32_t rc = make_cam(A.C, viewmat, fx, fy, cx, cy, W, H, near_plane, far_plane, blur,
                           max_radius, cam_center, sh_degree, who);
@@ -1336,6 +1374,10 @@ static int32_t preprocess_fwd(int64_t N, const float *means, const float *quats,
     A.valid_mask = valid_mask;
     A.filt = filter_3d; A.aa = antialias; A.op_eff = opacity_eff; A.act = activations;
     A.vec4 = sh && sh_degree == 3 && (!sh_fused || ((uintptr_t)sh & 15) == 0);
+    MG_REQUIRE(block_work == nullptr || tile >= 1, "%s: block_work needs a tile size, got %d",
+               who, tile);
+    A.block_work = block_work;
+    A.tile = tile;
     const int64_t blocks = ceil_div(N, kPreThreads);
     TimedScope ts("preprocess_forward", as_stream(stream));
     if (mip)
@@ -1488,12 +1530,13 @@ int32_t mg_preprocess_forward_mip(int64_t N, const float *means, const float *qu
                                   int32_t activations, float *uv, float *conic, float *depth,
                                   float *rxy,
                                   int32_t *valid, uint8_t *valid_mask, float *color,
-                                  float *opacity_eff, mg_stream_t stream) {
+                                  float *opacity_eff, int32_t tile, int32_t *block_work,
+                                  mg_stream_t stream) {
     return preprocess_fwd(N, means, quats, scales, sh, sh_rest, sh_fused, opacities, viewmat,
                           fx, fy, cx, cy, W, H, near_plane, far_plane, blur, max_radius,
                           cam_center, sh_degree, true, filter_3d, antialias, activations, uv,
                           conic, depth, rxy, valid, valid_mask, color, opacity_eff, stream,
-                          "mg_preprocess_forward_mip");
+                          "mg_preprocess_forward_mip", tile, block_work);
 }
 
 int32_t mg_preprocess_backward(int64_t N, const float *means, const float *quats,

@@ -30,6 +30,7 @@ import torch
 
 from conftest import rel_l2
 from oracle import adam_ref, binning_ref, raster_ref, render_ref
+from test_gpu_lists_capped import _host_block_work
 from test_gpu_raster import gpu_backward, gpu_forward
 
 pytestmark = pytest.mark.gpu
@@ -80,11 +81,15 @@ def _binning_bit_exact(uv, rxy, conic, op, valid, depth, W, H, label):
     # The same lists sized by a capacity instead of the host read (exact, and
     # with the 25% headroom ListCapacity keeps): past 4096 tiles the radix
     # passes and the tile ranges then take the kept count from the device.
+    # The second build also orders the binning's blocks heaviest first, from
+    # the projection's work estimate (recomputed here), as render does.
     total = int(rids.size)
-    for cap in (total, total + total // 4):
+    bw = torch.from_numpy(_host_block_work(cpu[0], cpu[1], cpu[4], W, H, 16)).to(
+        device=uv.device, dtype=torch.int32)
+    for cap, work in ((total, None), (total + total // 4, bw)):
         cids, coffs, _, status = backend._bin_capped(uv.detach(), rxy, depth, valid,
                                                       conic.detach(), op.detach(), W, H, 16,
-                                                      cap)
+                                                      cap, block_work=work)
         assert status.tolist() == [total, 0], (status.tolist(), total, cap)
         assert np.array_equal(_np(coffs), roffs), f"capacity {cap}: tile offsets differ"
         assert np.array_equal(_np(cids)[:total], rids), f"capacity {cap}: gauss_ids differ"

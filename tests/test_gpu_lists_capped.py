@@ -21,13 +21,14 @@ from test_gpu_binning import gpu_preprocess, ref_scene
 pytestmark = pytest.mark.gpu
 
 
-def _both(s, dev, tile, ellipse, capacity_of):
+def _both(s, dev, tile, ellipse, capacity_of, block_work=None, proj=None):
     """Two-call lists, then capacity-bounded lists at capacity_of(total)
-    into a sentinel-filled ids buffer."""
+    into a sentinel-filled ids buffer (with a block order from
+    ``block_work`` if given)."""
     from metal_gauss_amd import _lib, backend
 
-    uv, conic, depth, rxy, valid, _ = gpu_preprocess(s, dev)
-    op = s["op"].to(dev)
+    uv, conic, depth, rxy, valid, _ = gpu_preprocess(s, dev) if proj is None else proj
+    op = s["op"].to(dev) if proj is None else proj[5]
     args = (uv, rxy, depth, valid, conic if ellipse else None, op if ellipse else None,
             s["W"], s["H"], tile)
     ids, offs, tx = backend._bin(*args)
@@ -46,7 +47,8 @@ def _both(s, dev, tile, ellipse, capacity_of):
         N, uv.data_ptr(), rxy.data_ptr(), conic.data_ptr() if ellipse else None,
         op.data_ptr() if ellipse else None, valid.data_ptr(), depth.data_ptr(), s["W"], s["H"],
         tile, tx, n_tiles // tx, cap, got_ids.data_ptr() if cap else None, got_offs.data_ptr(),
-        status.data_ptr(), host.data_ptr(), 99, ws.data_ptr(), ws.numel(), _lib.stream(uv)))
+        status.data_ptr(), host.data_ptr(), 99, ws.data_ptr(), ws.numel(),
+        None if block_work is None else block_work.data_ptr(), _lib.stream(uv)))
     torch.cuda.synchronize()
     st = status.cpu().numpy()
     assert host.tolist() == [int(st[0]), int(st[1]), 99], "host slot differs from the device words"
@@ -87,6 +89,102 @@ def test_capped_lists_equal_the_two_call_lists(dev, case, cap):
     else:
         assert status[1] == 1
         assert (got_offs == 0).all(), "an overflowed build must leave every list empty"
+
+
+def _mip_projection(s, dev, tile):
+    """The mip projection with its per-block binning work estimate:
+    (uv, conic, depth, rxy, valid, opacity_eff), block_work."""
+    from metal_gauss_amd.backend import _PreprocessMip, _camera
+
+    W, H, f = s["W"], s["H"], s["f"]
+    K = torch.tensor([[f, 0, W / 2], [0, f, H / 2], [0, 0, 1.0]])
+    fx, fy, cx, cy, vm_h, cc = _camera(K, torch.eye(4))
+    n = s["means"].shape[0]
+    bw = torch.full(((n + 255) // 256,), -7, dtype=torch.int32, device=dev)
+    with torch.no_grad():
+        uv, conic, depth, rxy, valid, _, op = _PreprocessMip.apply(
+            s["means"].to(dev), s["quats"].to(dev), s["scales"].to(dev), s["op"].to(dev),
+            s["sh"].to(dev), None, None, False, vm_h, fx, fy, cx, cy, W, H, 0.01, 100.0, 0.3,
+            float(max(W, H)), cc, 3, None, 0, None, None, None, (tile, bw))
+    return (uv, conic, depth, rxy, valid, op), bw
+
+
+def _host_block_work(uv, rxy, valid, W, H, tile):
+    """Per 256 Gaussians: the tiles of each visible Gaussian's clamped
+    rectangle (floor((u -+ rx) / tile), exact in float32 for a tile of a power
+    of two), capped at 2^22, or 4 for a rectangle of at most 32 tiles."""
+    assert tile & (tile - 1) == 0
+    tx, ty = -(-W // tile), -(-H // tile)
+    it = np.float32(1.0) / np.float32(tile)
+    u, v = uv[:, 0], uv[:, 1]
+    rx, ry = rxy[:, 0], rxy[:, 1]
+    with np.errstate(invalid="ignore", over="ignore"):
+        cl = lambda a, hi: np.clip(np.nan_to_num(np.floor(a), nan=0.0, posinf=hi,
+                                                 neginf=0.0), 0, hi).astype(np.int64)
+        x0, x1 = cl((u - rx) * it, tx - 1), cl((u + rx) * it, tx - 1)
+        y0, y1 = cl((v - ry) * it, ty - 1), cl((v + ry) * it, ty - 1)
+    area = (x1 - x0 + 1) * (y1 - y0 + 1)
+    w = np.where(area > 32, np.minimum(area, 1 << 22), 4)
+    w = np.where(valid != 0, w, 0)
+    pad = (-w.size) % 256
+    return np.concatenate([w, np.zeros(pad, np.int64)]).reshape(-1, 256).sum(1)
+
+
+@pytest.mark.parametrize("case", [
+    # (N, W, H, tile): the counting sort's tile count, then the radix route
+    # at 8192 and 2^15 tiles (the sizes render orders blocks at).
+    (20000, 240, 320, 16), (6000, 2048, 1024, 16), (6000, 2048, 2048, 8)])
+def test_block_order_changes_no_list(dev, case):
+    """mg_bin_lists_capped with a block order: the projection's estimate
+    (equal to its host recomputation, so heavy blocks go first), or any
+    contents at all (random words, negatives, all equal), gives exactly
+    the lists without one."""
+    n, W, H, tile = case
+    s = ref_scene(N=n, W=W, H=H, seed=7)
+    if W >= 2048:
+        s["f"] = 900.0 * W / 2048
+    proj, bw = _mip_projection(s, dev, tile)
+    torch.cuda.synchronize()
+    cpu = [t.cpu().numpy() for t in proj]
+    want = _host_block_work(cpu[0], cpu[3], cpu[4], W, H, tile)
+    assert np.array_equal(bw.cpu().numpy(), want), "block work differs from the host's"
+    assert want.sum() > 0
+    base = _both(s, dev, tile, True, CAPS["roomy"], None, proj)
+    g = torch.Generator().manual_seed(3)
+    nb = bw.numel()
+    for work in (bw, torch.randint(-2 ** 31, 2 ** 31 - 1, (nb,), generator=g,
+                                   dtype=torch.int64).to(torch.int32).to(dev),
+                 torch.full((nb,), -5, dtype=torch.int32, device=dev),
+                 torch.arange(nb, dtype=torch.int32, device=dev) * 997):
+        got = _both(s, dev, tile, True, CAPS["roomy"], work, proj)
+        total = base[2]
+        assert got[2] == total and np.array_equal(got[6], base[6])
+        assert np.array_equal(got[5], base[5]), "a block order changed the tile offsets"
+        assert np.array_equal(got[4][:total], base[4][:total]), "a block order changed the ids"
+        assert np.array_equal(got[4][:total], base[0])
+
+
+def test_render_with_block_order_equals_render(dev):
+    """render past 4096 tiles with capacity lists (the blocks ordered by the
+    projection's estimate) gives the image of the sync-sized lists, bit for
+    bit, and the same intersection total."""
+    from metal_gauss_amd import backend, render
+
+    Wb, Hb = 1920, 1080
+    assert -(-Wb // 16) * -(-Hb // 16) > backend._BLOCK_ORDER_TILES
+    s = scene(n=20000, seed=5, sh=True)
+    p = _leaves(s, dev)
+    with torch.no_grad():
+        kw = dict(sh_degree=3, sh_rest=p["sh_rest"], background=(0.1, 0.2, 0.3),
+                  activations=True)
+        args = (p["means"], p["quats"], p["log_scales"], p["logits"], p["sh_dc"],
+                intrinsics(Wb, Hb), torch.eye(4), Wb, Hb)
+        rgb0, a0, info0 = render(*args, **kw)
+        total = info0["isect_total"]
+        assert total > 0
+        rgb, a, info = render(*args, list_capacity=total + 100, **kw)
+        assert info["lists_status"].tolist() == [total, 0]
+        assert torch.equal(rgb, rgb0) and torch.equal(a, a0)
 
 
 def test_capped_lists_of_no_gaussians(dev):
