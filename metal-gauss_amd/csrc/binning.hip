@@ -1685,6 +1685,48 @@ constexpr int kTdKeyBits = 20;   // key bits exchanged beside a 12-bit list inde
 constexpr uint32_t kTdKeyMask = (1u << kTdKeyBits) - 1u;
 static_assert(kTdCap <= (1 << (32 - kTdKeyBits)), "a list index fits beside the key bits");
 
+// The depth sort's tile order past kCsBuckets tiles (the radix route, which
+// has no column scan to read the list lengths from): one workgroup counting-
+// sorts the tiles over the 256 list-length bins of len_bin from the list
+// offsets, longest first (tiles of one bin in no fixed order). Every tile
+// lands in order once, whatever the offsets hold.
+constexpr int kLenOrderThreads = 1024;
+
+__global__ __launch_bounds__(kLenOrderThreads) void tile_len_order_kernel(
+    const int32_t *__restrict__ offsets, int nb, int32_t *__restrict__ order) {
+    __shared__ uint32_t s_cnt[256];
+    __shared__ uint32_t s_wave[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    auto bin_of = [&](int tt) {
+        return len_bin((uint32_t)max(offsets[tt + 1] - offsets[tt], 0));
+    };
+    if (tid < 256) s_cnt[tid] = 0;
+    __syncthreads();
+    for (int tt = tid; tt < nb; tt += kLenOrderThreads) atomicAdd(&s_cnt[bin_of(tt)], 1u);
+    __syncthreads();
+    // Exclusive starts, longest bin first: thread i < 256 (waves 0-3) scans
+    // bin 255 - i.
+    uint32_t c = 0, incl = 0;
+    if (tid < 256) {   // wave-uniform
+        c = s_cnt[255 - tid];
+        incl = c;
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t u = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += u;
+        }
+        if (lane == 63) s_wave[wave] = incl;
+    }
+    __syncthreads();
+    if (tid < 256) {
+        uint32_t before = incl - c;
+        for (int w = 0; w < wave; ++w) before += s_wave[w];
+        s_cnt[255 - tid] = before;
+    }
+    __syncthreads();
+    for (int tt = tid; tt < nb; tt += kLenOrderThreads)
+        order[atomicAdd(&s_cnt[bin_of(tt)], 1u)] = tt;
+}
+
 struct TdArgs {
     const int32_t *offsets;
     uint2 *pairs;                     // {id, depth bits}, grouped by tile (clobbered)
@@ -2217,6 +2259,15 @@ static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
             tile_ranges_u32_kernel<<<(unsigned)ceil_div(n + 1, 256 * kRangePer), 256, 0, s>>>(
                 res_tiles, n, n_tiles, tile_offsets, status);
             MG_LAUNCHED("tile_ranges_u32_kernel");
+        }
+        // The depth sort's longest-first order, in the keys region (free once
+        // the tile ranges are read from whichever buffer holds the sorted
+        // keys) when it holds a word per tile.
+        if (n_tiles <= T) {
+            order = reinterpret_cast<int32_t *>(tk_a);
+            TimedScope ts("depth_order", s);
+            tile_len_order_kernel<<<1, kLenOrderThreads, 0, s>>>(tile_offsets, n_tiles, order);
+            MG_LAUNCHED("tile_len_order_kernel");
         }
     }
     TdArgs D{tile_offsets, sorted, scratch, gauss_ids, order};
