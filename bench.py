@@ -994,7 +994,7 @@ def pmc_summary(fetch_dir, write_dir, copy_mib):
 COUNTER_REGEX = ("raster_bwd|raster_fwd|tile_order|adam_multi|preprocess_fwd|preprocess_bwd|"
                  "scan_|bin_write|bin_count|bin_offsets|count_hist|count_colscan|count_scatter|"
                  "tile_depth_sort|radix_|tile_ranges|ssim_fused|photometric_loss|stream_copy|"
-                 "copyBuffer")
+                 "copyBuffer|block_order|tile_len_order")
 
 
 def _kernel_base(name):
