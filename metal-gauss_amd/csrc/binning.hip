@@ -648,30 +648,74 @@ __device__ __forceinline__ uint32_t wave_small_claims(const BinRec &r, int ar, b
     return w_msk[lane];
 }
 
-// The count and write passes' workgroup order, from a per-block work
-// estimate (the tiles a block's rectangles cover, which the projection can
-// emit): heaviest block first, so that the few blocks whose wave walks span
-// thousands of tiles start at once instead of trailing the launch. One
-// workgroup counting-sorts the blocks over kBlkBins bins: exact below 256,
-// then 32 bins per octave. Every block lands in order exactly once, whatever
-// the estimates hold (a negative one counts as 0): they only reorder the
-// blocks, and both passes index their outputs by block, not by workgroup.
-constexpr int kBlkOrderThreads = 1024, kBlkBins = 1024, kBlkPer = 16;
+// Longest-processing-time-first orders, by one 1024-thread workgroup: a
+// counting sort of the items over kBins bins of their estimated work,
+// heaviest bin first (items of one bin in no fixed order). The bins are
+// exact below 256, then 2^kOctBits an octave (to 2^31). Finer bins cost a
+// longer scan; coarse ones crowd the items into a few bins, whose LDS
+// atomics (one wave's lanes on one bin are served one after another) then
+// dominate: the tile order past 4096 tiles took 12.1 us at config 5 with 32
+// bins an octave and 7.5 with 128, the block order 10.8 with 32 and 12.2
+// with 128.
+constexpr int kOrdThreads = 1024;
 
-__device__ __forceinline__ int block_bin(int32_t w) {
+template <int kOctBits>
+__device__ __forceinline__ int fine_bin(int32_t w) {
     const uint32_t L = (uint32_t)max(w, 0);
     if (L < 256u) return (int)L;
     const int e = 31 - __builtin_clz(L);
-    return min(kBlkBins - 1, 256 + 32 * (e - 8) + (int)((L >> (e - 5)) & 31u));
+    return 256 + (1 << kOctBits) * (e - 8) + (int)((L >> (e - kOctBits)) & ((1u << kOctBits) - 1u));
+}
+template <int kOctBits>
+constexpr int fine_bins() { return 256 + (1 << kOctBits) * 24; }
+
+// s_cnt's kBins counts become exclusive starts, the highest bin first:
+// thread j owns bins kBins - 1 - kPer * j - k, k < kPer.
+template <int kBins>
+__device__ __forceinline__ void desc_bin_starts(uint32_t *s_cnt, uint32_t *s_wave) {
+    constexpr int kPer = kBins / kOrdThreads;
+    static_assert(kPer * kOrdThreads == kBins, "whole bins per thread");
+    const int j = threadIdx.x, lane = j & 63, wave = j >> 6;
+    uint32_t c[kPer], sum = 0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        c[k] = s_cnt[kBins - 1 - kPer * j - k];
+        sum += c[k];
+    }
+    uint32_t incl = sum;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t u = (uint32_t)__shfl_up((int)incl, o, 64);
+        if (lane >= o) incl += u;
+    }
+    if (lane == 63) s_wave[wave] = incl;
+    __syncthreads();
+    uint32_t run = incl - sum;
+    for (int v = 0; v < wave; ++v) run += s_wave[v];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        s_cnt[kBins - 1 - kPer * j - k] = run;
+        run += c[k];
+    }
+    __syncthreads();
 }
 
-__global__ __launch_bounds__(kBlkOrderThreads) void block_order_kernel(
+// The count and write passes' workgroup order, from a per-block work
+// estimate (the tiles a block's rectangles cover, which the projection can
+// emit): heaviest block first, so that the few blocks whose wave walks span
+// thousands of tiles start at once instead of trailing the launch. Every
+// block lands in order exactly once, whatever the estimates hold (a negative
+// one counts as 0): they only reorder the blocks, and both passes index
+// their outputs by block, not by workgroup.
+constexpr int kBlkPer = 16, kBlkOctBits = 5, kBlkBins = 1024;
+static_assert(fine_bins<kBlkOctBits>() <= kBlkBins, "block bins");
+
+__global__ __launch_bounds__(kOrdThreads) void block_order_kernel(
     const int32_t *__restrict__ block_work, int64_t nparts, int32_t *__restrict__ order) {
     __shared__ uint32_t s_cnt[kBlkBins];
-    __shared__ uint32_t s_wave[kBlkOrderThreads / 64];
-    const int j = threadIdx.x, lane = j & 63, wave = j >> 6;
-    constexpr int64_t kBatch = (int64_t)kBlkOrderThreads * kBlkPer;
-    s_cnt[j] = 0;   // nparts >= 1
+    __shared__ uint32_t s_wave[kOrdThreads / 64];
+    const int j = threadIdx.x;
+    constexpr int64_t kBatch = (int64_t)kOrdThreads * kBlkPer;
+    for (int k = j; k < kBlkBins; k += kOrdThreads) s_cnt[k] = 0;   // nparts >= 1
     __syncthreads();
     // Each batch's loads are issued together, then binned.
     for (int64_t b0 = 0; b0 < nparts; b0 += kBatch) {
@@ -680,42 +724,29 @@ __global__ __launch_bounds__(kBlkOrderThreads) void block_order_kernel(
         for (int r = 0; r < kBlkPer; ++r) {
             // Every load in range and its value always used (negative past
             // nparts), so no branch separates the batch's loads.
-            const int64_t i = b0 + j + (int64_t)kBlkOrderThreads * r;
-            bin[r] = block_bin(block_work[min(i, nparts - 1)]) - (i < nparts ? 0 : 4096);
+            const int64_t i = b0 + j + (int64_t)kOrdThreads * r;
+            bin[r] = fine_bin<kBlkOctBits>(block_work[min(i, nparts - 1)]) -
+                     (i < nparts ? 0 : 2 * kBlkBins);
         }
 #pragma unroll
         for (int r = 0; r < kBlkPer; ++r)
             if (bin[r] >= 0) atomicAdd(&s_cnt[bin[r]], 1u);
     }
     __syncthreads();
-    // Exclusive scan over the bins from the heaviest down: thread j owns bin
-    // kBlkBins - 1 - j.
-    const uint32_t c = s_cnt[kBlkBins - 1 - j];
-    uint32_t incl = c;
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t u = (uint32_t)__shfl_up((int)incl, o, 64);
-        if (lane >= o) incl += u;
-    }
-    if (lane == 63) s_wave[wave] = incl;
-    __syncthreads();
-    uint32_t before = 0;
-    for (int v = 0; v < wave; ++v) before += s_wave[v];
-    s_cnt[kBlkBins - 1 - j] = before + incl - c;
-    __syncthreads();
+    desc_bin_starts<kBlkBins>(s_cnt, s_wave);
     for (int64_t b0 = 0; b0 < nparts; b0 += kBatch) {
         int bin[kBlkPer];
 #pragma unroll
         for (int r = 0; r < kBlkPer; ++r) {
-            // Every load in range and its value always used (negative past
-            // nparts), so no branch separates the batch's loads.
-            const int64_t i = b0 + j + (int64_t)kBlkOrderThreads * r;
-            bin[r] = block_bin(block_work[min(i, nparts - 1)]) - (i < nparts ? 0 : 4096);
+            const int64_t i = b0 + j + (int64_t)kOrdThreads * r;
+            bin[r] = fine_bin<kBlkOctBits>(block_work[min(i, nparts - 1)]) -
+                     (i < nparts ? 0 : 2 * kBlkBins);
         }
 #pragma unroll
         for (int r = 0; r < kBlkPer; ++r) {
             if (bin[r] >= 0)
                 order[atomicAdd(&s_cnt[bin[r]], 1u)] =
-                    (int32_t)(b0 + j + (int64_t)kBlkOrderThreads * r);
+                    (int32_t)(b0 + j + (int64_t)kOrdThreads * r);
         }
     }
 }
@@ -1686,45 +1717,47 @@ constexpr uint32_t kTdKeyMask = (1u << kTdKeyBits) - 1u;
 static_assert(kTdCap <= (1 << (32 - kTdKeyBits)), "a list index fits beside the key bits");
 
 // The depth sort's tile order past kCsBuckets tiles (the radix route, which
-// has no column scan to read the list lengths from): one workgroup counting-
-// sorts the tiles over the 256 list-length bins of len_bin from the list
-// offsets, longest first (tiles of one bin in no fixed order). Every tile
+// has no column scan to read the list lengths from): the tiles longest list
+// first, by the order workgroup above, from the list offsets. Every tile
 // lands in order once, whatever the offsets hold.
-constexpr int kLenOrderThreads = 1024;
+constexpr int kLenPer = 8, kLenOctBits = 7, kLenBins = 4096;
+static_assert(fine_bins<kLenOctBits>() <= kLenBins, "list-length bins");
 
-__global__ __launch_bounds__(kLenOrderThreads) void tile_len_order_kernel(
+__global__ __launch_bounds__(kOrdThreads) void tile_len_order_kernel(
     const int32_t *__restrict__ offsets, int nb, int32_t *__restrict__ order) {
-    __shared__ uint32_t s_cnt[256];
-    __shared__ uint32_t s_wave[4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    auto bin_of = [&](int tt) {
-        return len_bin((uint32_t)max(offsets[tt + 1] - offsets[tt], 0));
-    };
-    if (tid < 256) s_cnt[tid] = 0;
+    __shared__ uint32_t s_cnt[kLenBins];
+    __shared__ uint32_t s_wave[kOrdThreads / 64];
+    const int j = threadIdx.x;
+    constexpr int kBatch = kOrdThreads * kLenPer;
+    for (int k = j; k < kLenBins; k += kOrdThreads) s_cnt[k] = 0;
     __syncthreads();
-    for (int tt = tid; tt < nb; tt += kLenOrderThreads) atomicAdd(&s_cnt[bin_of(tt)], 1u);
-    __syncthreads();
-    // Exclusive starts, longest bin first: thread i < 256 (waves 0-3) scans
-    // bin 255 - i.
-    uint32_t c = 0, incl = 0;
-    if (tid < 256) {   // wave-uniform
-        c = s_cnt[255 - tid];
-        incl = c;
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t u = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += u;
+    // A tile's bin from its list length; its loads are issued with the
+    // batch's (in range, values always used), and past nb it is negative.
+    auto bins = [&](int b0, int (&bin)[kLenPer]) {
+#pragma unroll
+        for (int r = 0; r < kLenPer; ++r) {
+            const int tt = b0 + j + kOrdThreads * r;
+            const int tc = min(tt, nb - 1);
+            bin[r] = fine_bin<kLenOctBits>(offsets[tc + 1] - offsets[tc]) -
+                     (tt < nb ? 0 : 2 * kLenBins);
         }
-        if (lane == 63) s_wave[wave] = incl;
+    };
+    for (int b0 = 0; b0 < nb; b0 += kBatch) {
+        int bin[kLenPer];
+        bins(b0, bin);
+#pragma unroll
+        for (int r = 0; r < kLenPer; ++r)
+            if (bin[r] >= 0) atomicAdd(&s_cnt[bin[r]], 1u);
     }
     __syncthreads();
-    if (tid < 256) {
-        uint32_t before = incl - c;
-        for (int w = 0; w < wave; ++w) before += s_wave[w];
-        s_cnt[255 - tid] = before;
+    desc_bin_starts<kLenBins>(s_cnt, s_wave);
+    for (int b0 = 0; b0 < nb; b0 += kBatch) {
+        int bin[kLenPer];
+        bins(b0, bin);
+#pragma unroll
+        for (int r = 0; r < kLenPer; ++r)
+            if (bin[r] >= 0) order[atomicAdd(&s_cnt[bin[r]], 1u)] = b0 + j + kOrdThreads * r;
     }
-    __syncthreads();
-    for (int tt = tid; tt < nb; tt += kLenOrderThreads)
-        order[atomicAdd(&s_cnt[bin_of(tt)], 1u)] = tt;
 }
 
 struct TdArgs {
@@ -2266,7 +2299,7 @@ static int32_t emit_and_sort(const BeginWs &ws, int64_t N, const float *conic,
         if (n_tiles <= T) {
             order = reinterpret_cast<int32_t *>(tk_a);
             TimedScope ts("depth_order", s);
-            tile_len_order_kernel<<<1, kLenOrderThreads, 0, s>>>(tile_offsets, n_tiles, order);
+            tile_len_order_kernel<<<1, kOrdThreads, 0, s>>>(tile_offsets, n_tiles, order);
             MG_LAUNCHED("tile_len_order_kernel");
         }
     }
@@ -2486,7 +2519,7 @@ int32_t mg_bin_lists_capped(int64_t N, const float *uv, const float *rxy, const 
     if (N > 0) {
         TimedScope ts("bin_count", s);
         if (order) {
-            block_order_kernel<<<1, kBlkOrderThreads, 0, s>>>(block_work, nparts, ws.order);
+            block_order_kernel<<<1, kOrdThreads, 0, s>>>(block_work, nparts, ws.order);
             MG_LAUNCHED("block_order_kernel");
         }
         bin_count_rec_kernel<<<(unsigned)nparts, kBinThreads, 0, s>>>(
