@@ -942,13 +942,13 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
     # take their blocks of 256 Gaussians heaviest first, from a per-block
     # work estimate the projection kernel writes (the mip projection only).
     block_work = None
-    if list_capacity is not None:
-        tx, ty = _tile_grid(W, H, tile)
-        if tx * ty > _BLOCK_ORDER_TILES and means.shape[0] > 0:
-            block_work = (tile, torch.empty((means.shape[0] + 255) // 256, dtype=torch.int32,
-                                            device=means.device))
     if (filter_3d is not None or antialias or activations or optimizer is not None
             or reg is not None):
+        if list_capacity is not None and means.shape[0] > 0:
+            tx, ty = _tile_grid(W, H, tile)
+            if tx * ty > _BLOCK_ORDER_TILES:
+                block_work = (tile, torch.empty((means.shape[0] + 255) // 256,
+                                                dtype=torch.int32, device=means.device))
         # Both filters (and the activations) in the projection kernel; the
         # compensated opacity is binned too, which gives a tighter, still
         # exact, ellipse bound (metal_backend.py:506-511).
@@ -966,13 +966,11 @@ def render(means, quats, scales, opacities, sh, K, viewmat, W, H,
                 fx, fy, cx, cy, W, H, near, far, 0.3, max_radius, cam_center, sh_degree,
                 valid_b, act, optimizer, reg, lists, block_work)
     elif explicit_colors:
-        block_work = None
         uv, conic, depth, rxy, valid_i = _PreprocessMetal.apply(
             means, quats, scales, None, None, opacities.detach(), vm_h, fx, fy, cx, cy, W, H,
             near, far, 0.3, max_radius, cam_center, sh_degree, valid_b)
         colors = colors.contiguous()
     else:
-        block_work = None
         sh_in, rest_in = _sh_inputs(sh, sh_rest)
         uv, conic, depth, rxy, valid_i, colors = _PreprocessMetal.apply(
             means, quats, scales, sh_in, rest_in, opacities.detach(), vm_h, fx, fy, cx, cy,
