@@ -1691,9 +1691,10 @@ static int32_t tile_count_sort(const uint32_t *tiles, const V *ids, int64_t n, i
 // One workgroup per tile sorts the tile's list [offsets[t], offsets[t+1]) of
 // {id, depth bits} pairs stably by the depth's float bits (positive depths
 // order as their bits), on only the bits in which the list's keys differ:
-// LSD passes of 8 bits. The list arrives in ascending id, so ties keep id
-// order. The ids are written to gauss_ids.
-//   * Up to kTdCap entries whose keys differ in at most kTdKeyBits + 8 bits:
+// LSD passes of 8 bits (9 for keys spanning 25 bits or more). The list
+// arrives in ascending id, so ties keep id order. The ids are written to
+// gauss_ids.
+//   * Up to kTdCap entries whose keys span at most kTdKeyBits + 9 bits:
 //     the keys live in registers, each wave holding one contiguous quarter
 //     (rounded up to 64 entries); each pass ranks every wave's quarter
 //     against a wave-private LDS histogram, joins the waves through a digit
@@ -1768,15 +1769,21 @@ struct TdArgs {
     const int32_t *order;             // workgroup -> tile, longest list first (or NULL)
 };
 
+// Digits of the short-list passes: 8 bits, or 9 when the keys span 25 to
+// kTdKeyBits + 9 bits, so that 25-27 bits take three passes instead of four
+// (config 5's lists, whose depths run from the camera's near Gaussians to
+// its far ones, span 25-27 bits; config 4's at most 24).
+constexpr int kTdDigits = 512;
+
 struct TdShared {
     // The exchange buffer and the per-digit lane masks are never live at
-    // once, so they share storage (22 KB in all; 110 VGPRs hold the
+    // once, so they share storage (26 KB in all; 110 VGPRs hold the
     // workgroup to four per CU).
     union {
         uint32_t xk[kTdCap];   // exchange: list index << kTdKeyBits | key bits left
-        unsigned long long mask[kTdWaves][256];   // per wave: lanes of a round per digit
+        unsigned long long mask[kTdWaves][kTdDigits];   // per wave: lanes of a round per digit
     } u;
-    uint32_t wh[kTdWaves][256];               // per wave: digit counts, then slots
+    uint32_t wh[kTdWaves][kTdDigits];         // per wave: digit counts, then slots
     uint32_t run[256], tot[256];
     uint32_t red[2 * kTdWaves];
 };
@@ -1849,36 +1856,48 @@ __device__ __forceinline__ void td_rank(const uint32_t (&d)[kTdPer], uint32_t va
 // After td_rank: wh[w][dg] becomes the slot of wave w's first entry of digit
 // dg: the digit's start plus the entries of that digit in earlier waves. The
 // digit starts are an exclusive scan of the digit totals, or with base
-// (chunked lists) base[dg], the running start carried from earlier chunks.
-// tot (may be null) gets the digit totals. One digit per thread.
+// (chunked lists, 8-bit digits) base[dg], the running start carried from
+// earlier chunks. tot (may be null) gets the digit totals. kPerT digits per
+// thread, consecutive (256 or 512 digits).
+template <int kPerT>
 __device__ __forceinline__ void td_slots(TdShared &S, uint32_t *tot, const uint32_t *base) {
+    static_assert(kPerT * kTdThreads <= kTdDigits, "digits fit the shared arrays");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    uint32_t cnt = 0, c[kTdWaves];
+    uint32_t c[kPerT][kTdWaves], cnt[kPerT], sum = 0;
 #pragma unroll
-    for (int w = 0; w < kTdWaves; ++w) {
-        c[w] = S.wh[w][tid];
-        cnt += c[w];
+    for (int p = 0; p < kPerT; ++p) {
+        cnt[p] = 0;
+#pragma unroll
+        for (int w = 0; w < kTdWaves; ++w) {
+            c[p][w] = S.wh[w][kPerT * tid + p];
+            cnt[p] += c[p][w];
+        }
+        sum += cnt[p];
     }
     uint32_t start;
     if (base) {
-        start = base[tid];
+        start = base[kPerT * tid];
     } else {
-        uint32_t incl = cnt;
+        uint32_t incl = sum;
         for (int o = 1; o < 64; o <<= 1) {
             const uint32_t u = __shfl_up(incl, o, 64);
             if (lane >= o) incl += u;
         }
         if (lane == 63) S.red[wave] = incl;
         __syncthreads();
-        start = incl - cnt;
+        start = incl - sum;
         for (int w = 0; w < wave; ++w) start += S.red[w];
     }
 #pragma unroll
-    for (int w = 0; w < kTdWaves; ++w) {
-        S.wh[w][tid] = start;
-        start += c[w];
+    for (int p = 0; p < kPerT; ++p) {
+        if (base && p > 0) start = base[kPerT * tid + p];
+#pragma unroll
+        for (int w = 0; w < kTdWaves; ++w) {
+            S.wh[w][kPerT * tid + p] = start;
+            start += c[p][w];
+        }
+        if (tot) tot[kPerT * tid + p] = cnt[p];
     }
-    if (tot) tot[tid] = cnt;
 }
 
 // Entries per wave part for a list (or chunk) of len: a quarter, rounded up
@@ -1894,12 +1913,12 @@ __device__ __forceinline__ void td_clear_masks(TdShared &S) {
     lds_reads_done();
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 4; ++j) S.u.mask[wave][lane + 64 * j] = 0ull;
+    for (int j = 0; j < kTdDigits / 64; ++j) S.u.mask[wave][lane + 64 * j] = 0ull;
 }
 
 // Sorts the len (2..kTdCap) entries at in by key, stably, in registers and
 // LDS (see above), and writes their ids in sorted order to out. Returns
-// false, having written nothing, when the keys span more than kTdKeyBits + 8
+// false, having written nothing, when the keys span more than kTdKeyBits + 9
 // bits. Workgroup-uniform. masks_clear: the lane masks are known zero (at
 // the start of a workgroup, each wave having cleared its own), so the first
 // pass need not clear them behind a barrier.
@@ -1924,30 +1943,33 @@ __device__ __forceinline__ bool td_fast(TdShared &S, const uint2 *in, int len, i
     td_minmax(kmin, kmax, S.red);
     const uint32_t span = kmax - kmin;
     const int bits = span == 0u ? 0 : 32 - __builtin_clz(span);
-    if (bits > kTdKeyBits + 8) return false;   // workgroup-uniform
+    const int db = bits > 24 ? 9 : 8;   // digit bits; workgroup-uniform
+    if (bits > kTdKeyBits + db) return false;   // workgroup-uniform
     // First pass: k is the key less kmin; later passes: k is the exchanged
     // word, the entry's list index over its key bits left.
 #pragma unroll
     for (int r = 0; r < kTdPer; ++r) k[r] = ((valid >> r) & 1u) ? k[r] - kmin : 0u;
-    for (int shift = 0; shift < bits; shift += 8) {
+    const uint32_t dmask = (1u << db) - 1u;
+    for (int shift = 0; shift < bits; shift += db) {
         if (shift > 0 || !masks_clear) td_clear_masks(S);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) S.wh[wave][lane + 64 * j] = 0;
+        for (int j = 0; j < kTdDigits / 64; ++j) S.wh[wave][lane + 64 * j] = 0;
         __syncthreads();
         uint32_t d[kTdPer];
 #pragma unroll
-        for (int r = 0; r < kTdPer; ++r) d[r] = k[r] & 255u;
+        for (int r = 0; r < kTdPer; ++r) d[r] = k[r] & dmask;
         td_rank(d, valid, rounds, rank, S.wh[wave], S.u.mask[wave]);
         __syncthreads();
-        td_slots(S, nullptr, nullptr);
+        if (db == 9) td_slots<2>(S, nullptr, nullptr);
+        else td_slots<1>(S, nullptr, nullptr);
         __syncthreads();
-        const bool last = shift + 8 >= bits;
+        const bool last = shift + db >= bits;
 #pragma unroll
         for (int r = 0; r < kTdPer; ++r) {
             if ((valid >> r) & 1u) {
                 const uint32_t pos = S.wh[wave][d[r]] + rank[r];
                 const uint32_t idx = shift == 0 ? (uint32_t)(pb + 64 * r) : k[r] >> kTdKeyBits;
-                const uint32_t rest = (shift == 0 ? k[r] : k[r] & kTdKeyMask) >> 8;
+                const uint32_t rest = (shift == 0 ? k[r] : k[r] & kTdKeyMask) >> db;
                 // After the last pass only the index is needed.
                 S.u.xk[pos] = last ? idx : (idx << kTdKeyBits) | rest;
             }
@@ -2065,7 +2087,7 @@ __device__ __forceinline__ uint2 *td_lsd_passes(TdShared &S, uint2 *pin, uint2 *
             __syncthreads();
             td_rank(d, valid, rounds, rank, S.wh[wave], S.u.mask[wave]);
             __syncthreads();
-            td_slots(S, S.tot, S.run);
+            td_slots<1>(S, S.tot, S.run);
             __syncthreads();
 #pragma unroll
             for (int r = 0; r < kTdPer; ++r) {
@@ -2102,7 +2124,7 @@ __device__ __forceinline__ void td_write_ids(const uint2 *in, int64_t len, int32
 }
 
 // Lists the fast path does not take: longer than kTdCap, or keys spanning
-// more than kTdKeyBits + 8 bits. One LSD pass on the top 8 of the key bits
+// more than kTdKeyBits + 9 bits. One LSD pass on the top 8 of the key bits
 // (through global memory, into pairs_b) groups the list into up to 256
 // buckets of consecutive key ranges, stably; runs of whole buckets of up to
 // kTdCap entries are then sorted by the fast path, each its own segment of
@@ -2174,7 +2196,7 @@ tile_depth_sort_kernel(const TdArgs A) {
     {
         const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) S.u.mask[wave][lane + 64 * j] = 0ull;
+        for (int j = 0; j < kTdDigits / 64; ++j) S.u.mask[wave][lane + 64 * j] = 0ull;
     }
     if (len <= kTdCap && td_fast(S, in, (int)len, A.ids + s0, true)) return;
     td_long(S, A, s0, len);
