@@ -1777,7 +1777,7 @@ constexpr int kTdDigits = 512;
 
 struct TdShared {
     // The exchange buffer and the per-digit lane masks are never live at
-    // once, so they share storage (26 KB in all; 110 VGPRs hold the
+    // once, so they share storage (27.7 KB in all; 128 VGPRs hold the
     // workgroup to four per CU).
     union {
         uint32_t xk[kTdCap];   // exchange: list index << kTdKeyBits | key bits left
