@@ -1691,7 +1691,7 @@ static int32_t tile_count_sort(const uint32_t *tiles, const V *ids, int64_t n, i
 // One workgroup per tile sorts the tile's list [offsets[t], offsets[t+1]) of
 // {id, depth bits} pairs stably by the depth's float bits (positive depths
 // order as their bits), on only the bits in which the list's keys differ:
-// LSD passes of 8 bits (9 for keys spanning 25 bits or more). The list
+// LSD passes of 8 bits (9 where that takes fewer passes). The list
 // arrives in ascending id, so ties keep id order. The ids are written to
 // gauss_ids.
 //   * Up to kTdCap entries whose keys span at most kTdKeyBits + 9 bits:
@@ -1769,10 +1769,10 @@ struct TdArgs {
     const int32_t *order;             // workgroup -> tile, longest list first (or NULL)
 };
 
-// Digits of the short-list passes: 8 bits, or 9 when the keys span 25 to
-// kTdKeyBits + 9 bits, so that 25-27 bits take three passes instead of four
-// (config 5's lists, whose depths run from the camera's near Gaussians to
-// its far ones, span 25-27 bits; config 4's at most 24).
+// Digits of the short-list passes: 8 bits, or 9 where that saves a pass,
+// so that 25-27 bits take three passes instead of four (config 5's lists,
+// whose depths run from the camera's near Gaussians to its far ones, span
+// 25-27 bits; config 4's at most 24), and up to kTdKeyBits + 9 bits.
 constexpr int kTdDigits = 512;
 
 struct TdShared {
@@ -1943,7 +1943,9 @@ __device__ __forceinline__ bool td_fast(TdShared &S, const uint2 *in, int len, i
     td_minmax(kmin, kmax, S.red);
     const uint32_t span = kmax - kmin;
     const int bits = span == 0u ? 0 : 32 - __builtin_clz(span);
-    const int db = bits > 24 ? 9 : 8;   // digit bits; workgroup-uniform
+    // Digit bits (workgroup-uniform): 9 where that takes fewer passes (9,
+    // 17-18 and 25-27 bits) or the keys need it (29 bits), else 8.
+    const int db = ((bits + 8) / 9 < (bits + 7) / 8 || bits > kTdKeyBits + 8) ? 9 : 8;
     if (bits > kTdKeyBits + db) return false;   // workgroup-uniform
     // First pass: k is the key less kmin; later passes: k is the exchanged
     // word, the entry's list index over its key bits left.

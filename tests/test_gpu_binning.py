@@ -229,6 +229,35 @@ def test_depth_windows_of_every_pass_count_bit_exact(dev, spread):
     assert np.array_equal(gpu[1], ref[1]), "tile offsets differ"
 
 
+@pytest.mark.parametrize("bits", [8, 9, 12, 17, 18, 24, 25, 27, 28, 29, 30])
+def test_depth_key_spans_of_every_digit_plan_bit_exact(dev, bits):
+    """Depth keys spanning exactly `bits` bits (positive floats drawn as
+    bit patterns, a tenth of them repeated for ties): the depth sort takes
+    8-bit passes, or 9-bit ones where they save a pass (9, 17-18, 25-27
+    bits) or are needed (29); 30 bits take the long-list path. The lists
+    must equal the oracle's."""
+    from metal_gauss_amd.backend import _bin
+
+    N, W, H, tile = 3000, 64, 64, 16
+    rng = np.random.default_rng(bits)
+    f32 = np.float32
+    uv = rng.uniform(0, W, (N, 2)).astype(f32)
+    rxy = np.full((N, 2), 6.0, f32)
+    valid = np.ones(N, np.int32)
+    kb = (0x00800000 + rng.integers(0, 1 << bits, N)).astype(np.uint32)
+    kb[0], kb[1] = 0x00800000, 0x00800000 + (1 << bits) - 1   # the full span
+    rep = rng.random(N) < 0.1
+    kb[rep] = kb[rng.integers(0, N, int(rep.sum()))]
+    depth = kb.view(f32)
+    zeros3, zeros1 = np.zeros((N, 3), f32), np.zeros(N, f32)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    gids, offs, _ = _bin(t(uv), t(rxy), t(depth), t(valid), None, None, W, H, tile)
+    rids, roffs, _, _ = binning_ref.build_tile_lists(uv, rxy, zeros3, zeros1, valid, depth, W,
+                                                     H, tile, ellipse=False)
+    assert np.array_equal(offs.cpu().numpy(), roffs), "tile offsets differ"
+    assert np.array_equal(gids.cpu().numpy(), rids), "gauss_ids differ"
+
+
 @pytest.mark.parametrize("crowd", [False, True])
 def test_depth_ties_and_long_tile_lists_bit_exact(dev, crowd):
     """Exact depth ties (Gaussians copied onto others, as MCMC's relocation
